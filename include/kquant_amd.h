@@ -1,0 +1,99 @@
+/*
+ * kquant_amd — C ABI of the MI355X (gfx950) block-scaled quantization hot path.
+ *
+ * Every entry point takes raw device pointers, int64 sizes and a HIP stream
+ * (passed as void*, a hipStream_t; NULL = the legacy default stream), launches
+ * asynchronously on that stream, allocates nothing, and returns KQ_OK (0) or a
+ * negative status.  kq_last_error() returns the calling thread's last message.
+ * Callers own every buffer (inputs, outputs and workspaces).
+ *
+ * Formats (the compressed-tensors "mxfp4-pack-quantized" and vLLM MXFP8
+ * layouts that kquant uses):
+ *   - blocks are 32 consecutive elements along K (the last, contiguous axis);
+ *   - E8M0 scale: uint8 [rows, K/32], value 2^(byte-127);
+ *   - MXFP4: uint8 [rows, K/2], two E2M1 codes per byte, low nibble = even K;
+ *   - MXFP8: uint8 (float8_e4m3fn bits) [rows, K].
+ */
+#ifndef KQUANT_AMD_H
+#define KQUANT_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  KQ_OK = 0,
+  KQ_ERR_INVALID = -1,  /* bad argument: shape, alignment, enum value   */
+  KQ_ERR_HIP = -2,      /* a HIP runtime call failed (launch, query)    */
+  KQ_ERR_LIMIT = -3     /* a size exceeds what the kernel supports       */
+};
+
+/* element formats */
+enum { KQ_FMT_MXFP8_E4M3 = 0, KQ_FMT_MXFP4_E2M1 = 1 };
+/* dense element types */
+enum { KQ_DT_BF16 = 0, KQ_DT_F16 = 1, KQ_DT_F32 = 2 };
+/* flags */
+enum {
+  /* use the bit-level software rounding instead of the gfx950 convert
+     instructions (both are tested to agree byte for byte) */
+  KQ_FLAG_SOFTWARE_CVT = 1u
+};
+/* byte tables of kq_decode_bytes */
+enum { KQ_TABLE_E8M0 = 0, KQ_TABLE_E2M1 = 1, KQ_TABLE_E4M3 = 2 };
+/* expert activations */
+enum { KQ_ACT_SITU = 0, KQ_ACT_SWIGLU = 1 };
+
+/* ABI version (major << 16 | minor) and the last error of this thread. */
+int kq_version(void);
+const char* kq_last_error(void);
+
+/* ---------------------------------------------------------------- codec -- */
+
+/* Quantize a dense [rows, k] matrix (row stride ld_in elements) to MX.
+ *
+ * MXFP8 replaces kquant/mxfp8.py:11-51 (mxfp8_quantize_cpu):
+ *   e = clamp(ceil(log2(max(amax,1e-30)/448)), -127, 128), byte = e + 127,
+ *   q = float8_e4m3fn(clamp(x / 2^e, +-448))   (round to nearest even).
+ * MXFP4 is the same rule with (E2M1, 6.0); kquant has no MXFP4 quantizer,
+ * its output layout is kquant/io/mxfp4.py:1-8 / pack_codes (:32-38).
+ * out_q: uint8 [rows, k] (MXFP8) or [rows, k/2] (MXFP4), contiguous.
+ * out_scale: uint8 [rows, k/32], contiguous.  k % 32 == 0.           */
+int kq_mx_quantize(int fmt, int in_dtype, const void* in, int64_t ld_in,
+                   int64_t rows, int64_t k, void* out_q, uint8_t* out_scale,
+                   uint32_t flags, void* stream);
+
+/* Dequantize MX codes + E8M0 scales to a dense [rows, k] matrix.
+ * MXFP4 replaces kquant/io/mxfp4.py:52-64 (dequant: E2M1[code]*2^(s-127),
+ * fp32), MXFP8 replaces kquant/mxfp8.py:54-84 (mxfp8_dequantize_cpu).
+ * out_dtype KQ_DT_F32 is the reference's result; KQ_DT_BF16 / KQ_DT_F16 are
+ * that fp32 value rounded to nearest even (scripts/closure_exl3_layer.py:157).
+ * Scale byte 255 gives +inf scale (0 * inf = NaN) as exp2(128) does.   */
+int kq_mx_dequant(int fmt, const void* q, const uint8_t* scale, int64_t rows,
+                  int64_t k, int out_dtype, void* out, uint32_t flags,
+                  void* stream);
+
+/* Nibble codes <-> packed bytes, kquant/io/mxfp4.py:19-38 (unpack_codes,
+ * pack_codes): byte = lo | hi << 4 (mod 256), lo = the even index; codes are
+ * OR-ed as whole bytes exactly as the reference does.  n_codes is even. */
+int kq_unpack_codes(const uint8_t* packed, int64_t n_packed, uint8_t* codes,
+                    void* stream);
+int kq_pack_codes(const uint8_t* codes, int64_t n_codes, uint8_t* packed,
+                  void* stream);
+
+/* Decode bytes through a format table into a dense array:
+ *   KQ_TABLE_E8M0  2^(b-127)        kquant/io/mxfp4.py:41-43 (scale_factors)
+ *   KQ_TABLE_E2M1  E2M1_LUT[c]      kquant/io/mxfp4.py:46-49 (code_values);
+ *                                   codes >= 16 give NaN (the reference's
+ *                                   gather raises IndexError instead)
+ *   KQ_TABLE_E4M3  float8_e4m3fn    kquant/sqg_e4m3.py:150-151, 336-353
+ *                                   (codebook widening, .view(e4m3).to(dtype)) */
+int kq_decode_bytes(int table, const uint8_t* in, int64_t n, int out_dtype, void* out,
+                    void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* KQUANT_AMD_H */

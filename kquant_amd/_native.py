@@ -1,0 +1,136 @@
+"""ctypes binding of ``libkquant_amd.so`` (the C ABI in include/kquant_amd.h).
+
+The product path always runs the HIP kernels.  There is no CPU fallback: when
+the library is missing or no GPU is visible the calls raise RuntimeError.
+CPU tensors handed to the public functions are copied to the current GPU,
+processed there, and the results copied back, so callers that keep weights
+on the host (as kquant's CPU helpers do) still run the GPU path.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from collections.abc import Iterable
+
+import torch
+
+from ._build import LIB_PATH
+
+# enums of include/kquant_amd.h
+KQ_OK = 0
+FMT_MXFP8_E4M3 = 0
+FMT_MXFP4_E2M1 = 1
+DT_BF16 = 0
+DT_F16 = 1
+DT_F32 = 2
+FLAG_SOFTWARE_CVT = 1
+TABLE_E8M0 = 0
+TABLE_E2M1 = 1
+TABLE_E4M3 = 2
+ACT_SITU = 0
+ACT_SWIGLU = 1
+
+DTYPE_CODES = {torch.bfloat16: DT_BF16, torch.float16: DT_F16, torch.float32: DT_F32}
+
+_VP = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_INT = ctypes.c_int
+_U32 = ctypes.c_uint32
+_F32 = ctypes.c_float
+_F64 = ctypes.c_double
+
+# name -> argtypes (every entry point returns int)
+SIGNATURES: dict[str, list] = {
+    "kq_mx_quantize": [_INT, _INT, _VP, _I64, _I64, _I64, _VP, _VP, _U32, _VP],
+    "kq_mx_dequant": [_INT, _VP, _VP, _I64, _I64, _INT, _VP, _U32, _VP],
+    "kq_unpack_codes": [_VP, _I64, _VP, _VP],
+    "kq_pack_codes": [_VP, _I64, _VP, _VP],
+    "kq_decode_bytes": [_INT, _VP, _I64, _INT, _VP, _VP],
+}
+
+_lib: ctypes.CDLL | None = None
+
+
+def library() -> ctypes.CDLL:
+    """Load the native library once; raise if it has not been built."""
+
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"kquant_amd native library not found at {LIB_PATH}; "
+                "build it with `python -c 'import __graft_entry__ as g; g.build()'`"
+            )
+        lib = ctypes.CDLL(str(LIB_PATH))
+        lib.kq_version.restype = ctypes.c_int
+        lib.kq_version.argtypes = []
+        lib.kq_last_error.restype = ctypes.c_char_p
+        lib.kq_last_error.argtypes = []
+        for name, argtypes in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = ctypes.c_int
+            fn.argtypes = argtypes
+        _lib = lib
+    return _lib
+
+
+def call(name: str, *args) -> None:
+    """Call a C entry point and turn a non-zero status into RuntimeError."""
+
+    lib = library()
+    rc = getattr(lib, name)(*args)
+    if rc != KQ_OK:
+        message = lib.kq_last_error().decode(errors="replace")
+        raise RuntimeError(f"{name} failed ({rc}): {message}")
+
+
+def ptr(t: torch.Tensor | None) -> ctypes.c_void_p:
+    return ctypes.c_void_p(0 if t is None else t.data_ptr())
+
+
+def stream(device: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def require_gpu() -> torch.device:
+    if not torch.cuda.is_available():
+        raise RuntimeError(
+            "kquant_amd runs its kernels on an MI355X GPU and no GPU is visible"
+        )
+    return torch.device("cuda", torch.cuda.current_device())
+
+
+def to_gpu(tensors: Iterable[torch.Tensor | None]) -> tuple[list, torch.device, torch.device | None]:
+    """Move tensors to one GPU; return (tensors, gpu, host device or None).
+
+    The GPU is the device of the first GPU tensor, else the current device.
+    ``host`` is the original device when the inputs came from the CPU, so the
+    caller can return results where the reference would have produced them.
+    """
+
+    tensors = list(tensors)
+    gpu = None
+    for t in tensors:
+        if t is not None and t.is_cuda:
+            gpu = t.device
+            break
+    host = None
+    if gpu is None:
+        gpu = require_gpu()
+        for t in tensors:
+            if t is not None:
+                host = t.device
+                break
+    else:
+        library()
+    moved = [None if t is None else t.to(gpu) for t in tensors]
+    return moved, gpu, host
+
+
+def aligned(t: torch.Tensor, align: int = 16) -> torch.Tensor:
+    """Contiguous tensor whose data pointer is ``align``-byte aligned."""
+
+    t = t.contiguous()
+    if t.data_ptr() % align:
+        t = t.clone()
+    return t

@@ -1,0 +1,125 @@
+"""Seeded synthetic inputs of the benchmark configurations.
+
+The reference publishes no dataset for this path; each generator follows the
+recipe of one benchmark configuration (BASELINE.json ``configs``) with a
+seeded CPU ``torch.Generator`` so every run sees the same bytes.
+
+  cfg1  MXFP4 expert weight [7168, 2048] bf16, N(0, 0.02), 0.1 % outliers x20
+  cfg2  MXFP8 linear W [12288, 7168] bf16 N(0, 0.015); X [4096, 7168] bf16
+        N(0, 1) times a per-channel lognormal(0, 0.5) factor
+  cfg3  MoE prefill: 384 experts, hidden 7168, intermediate 2048, 8192 tokens,
+        top-8 routing from softmax(randn + log Zipf(1.1) popularity)
+  cfg4  Hessian rows: Student-t(4) activations, bf16
+  cfg5  MoE decode: 1 / 4 / 16 tokens, 8 random distinct experts per token
+"""
+
+from __future__ import annotations
+
+import hashlib
+import math
+
+import torch
+
+HIDDEN = 7168
+INTER = 2048
+EXPERTS = 384
+TOPK = 8
+
+
+def sha256(t: torch.Tensor) -> str:
+    t = t.detach().contiguous().cpu()
+    return hashlib.sha256(t.view(torch.uint8).numpy().tobytes()).hexdigest()
+
+
+def cfg1_weight(rows: int = 7168, cols: int = 2048, seed: int = 0) -> torch.Tensor:
+    g = torch.Generator().manual_seed(seed)
+    w = torch.randn(rows, cols, generator=g) * 0.02
+    mask = torch.rand(rows, cols, generator=g) < 1e-3
+    w[mask] *= 20.0
+    return w.to(torch.bfloat16)
+
+
+def cfg2_weight(rows: int = 12288, cols: int = HIDDEN, seed: int = 0) -> torch.Tensor:
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(rows, cols, generator=g) * 0.015).to(torch.bfloat16)
+
+
+def cfg2_activations(tokens: int = 4096, cols: int = HIDDEN, seed: int = 1) -> torch.Tensor:
+    g = torch.Generator().manual_seed(seed)
+    channel = torch.exp(0.5 * torch.randn(cols, generator=g))
+    return (torch.randn(tokens, cols, generator=g) * channel).to(torch.bfloat16)
+
+
+def student_t4(rows: int, cols: int, seed: int = 0, dtype=torch.bfloat16) -> torch.Tensor:
+    """X = Z0 / sqrt((Z1^2 + ... + Z4^2) / 4): Student-t with 4 d.o.f."""
+    g = torch.Generator().manual_seed(seed)
+    z0 = torch.randn(rows, cols, generator=g)
+    chi = torch.zeros(rows, cols)
+    for _ in range(4):
+        chi += torch.randn(rows, cols, generator=g).square()
+    return (z0 / torch.sqrt(chi / 4.0)).to(dtype)
+
+
+def zipf_routing(
+    tokens: int,
+    experts: int = EXPERTS,
+    topk: int = TOPK,
+    exponent: float = 1.1,
+    seed: int = 0,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Top-k routing with Zipf expert popularity.
+
+    p_k ~ k^-exponent over a seeded permutation of expert ids; logits =
+    randn + ln p; top-k of softmax; weights = renormalized top-k probs.
+    Returns (ids int32 [tokens, topk], weights float32 [tokens, topk]).
+    """
+    g = torch.Generator().manual_seed(seed)
+    perm = torch.randperm(experts, generator=g)
+    rank = torch.empty(experts, dtype=torch.float64)
+    rank[perm] = torch.arange(1, experts + 1, dtype=torch.float64)
+    logp = (-exponent * torch.log(rank)).float()
+    logits = torch.randn(tokens, experts, generator=g) + logp
+    probs = torch.softmax(logits, dim=-1)
+    top, ids = torch.topk(probs, topk, dim=-1)
+    weights = top / top.sum(dim=-1, keepdim=True)
+    return ids.to(torch.int32), weights.float()
+
+
+def random_routing(tokens: int, experts: int = EXPERTS, topk: int = TOPK, seed: int = 0):
+    """Decode routing: per token randperm(experts)[:topk], softmax(randn(topk)) weights."""
+    g = torch.Generator().manual_seed(seed)
+    ids = torch.stack([torch.randperm(experts, generator=g)[:topk] for _ in range(tokens)])
+    weights = torch.softmax(torch.randn(tokens, topk, generator=g), dim=-1)
+    return ids.to(torch.int32), weights.float()
+
+
+def expert_weights_bf16(
+    experts: int, hidden: int = HIDDEN, inter: int = INTER, seed: int = 0, std: float = 0.02
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Dense bf16 expert weights: w13 [E, 2*inter, hidden] (gate rows first)
+    and w2 [E, hidden, inter]."""
+    g = torch.Generator().manual_seed(seed)
+    w13 = (torch.randn(experts, 2 * inter, hidden, generator=g) * std).to(torch.bfloat16)
+    w2 = (torch.randn(experts, hidden, inter, generator=g) * std).to(torch.bfloat16)
+    return w13, w2
+
+
+def bytes_per_expert(hidden: int = HIDDEN, inter: int = INTER) -> int:
+    """MXFP4 bytes (codes + E8M0 scales) of one expert's w13 + w2."""
+    w13 = 2 * inter * hidden // 2 + 2 * inter * hidden // 32
+    w2 = hidden * inter // 2 + hidden * inter // 32
+    return w13 + w2
+
+
+def moe_flops(pairs: int, hidden: int = HIDDEN, inter: int = INTER) -> float:
+    """2 * pairs * (2*inter*hidden + hidden*inter): gate/up and down GEMMs."""
+    return 2.0 * pairs * (2 * inter * hidden + hidden * inter)
+
+
+def syrk_flops(rows: int, k: int) -> float:
+    """Useful SYRK flops N*K*(K+1) (upper triangle incl. diagonal, x2 flops/MAC)."""
+    return float(rows) * k * (k + 1)
+
+
+def log2_ceil(x: float) -> int:
+    return int(math.ceil(math.log2(x)))

@@ -1,0 +1,226 @@
+"""TEST INFRASTRUCTURE ONLY — the CPU oracle of the kquant hot path.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
+import this package, and only as the checker (or as the timed CPU baseline).
+The kquant_amd product path never imports, links or calls anything here.
+
+Contents, each following the cited reference code:
+  mx_quantize / mx_dequant / pack_codes / unpack_codes
+      C restatement in mx_oracle.c (kquant/mxfp8.py:34-50, 79-84;
+      kquant/io/mxfp4.py:19-64), loaded through ctypes.
+  weighted_covariance / accumulate_hessian / finalize_damping / covariance_comparison
+      numpy restatements of kquant/candidate_hessian.py:70-112, 219-258,
+      kquant/capture.py:713-730, kquant/exl3_encoder_backend.py:1613-1625.
+  situ / swiglu / reference_rank
+      numpy restatements of kquant/tp_simulator.py:83-94 and
+      scripts/closure_exl3_layer.py:557-598.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import numpy as np
+
+_DIR = Path(__file__).resolve().parent
+_LIB_PATH = _DIR / "libmx_oracle.so"
+_lib = None
+
+E2M1_LUT = np.array(
+    [0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0, -0.0, -0.5, -1.0, -1.5, -2.0, -3.0, -4.0, -6.0],
+    dtype=np.float32,
+)
+
+
+def _load():
+    global _lib
+    if _lib is None:
+        if not _LIB_PATH.exists():
+            raise RuntimeError(f"oracle library missing: {_LIB_PATH} (run __graft_entry__.build())")
+        lib = ctypes.CDLL(str(_LIB_PATH))
+        vp, i64, i32, u32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_uint32
+        lib.mxo_quantize.argtypes = [i32, i32, vp, i64, i64, i64, vp, vp]
+        lib.mxo_quantize.restype = None
+        lib.mxo_dequant.argtypes = [i32, vp, vp, i64, i64, vp]
+        lib.mxo_dequant.restype = None
+        lib.mxo_unpack_codes.argtypes = [vp, i64, vp]
+        lib.mxo_unpack_codes.restype = None
+        lib.mxo_pack_codes.argtypes = [vp, i64, vp]
+        lib.mxo_pack_codes.restype = None
+        lib.mxo_f32_to_e4m3.argtypes = [ctypes.c_float]
+        lib.mxo_f32_to_e4m3.restype = u32
+        lib.mxo_f32_to_e2m1.argtypes = [ctypes.c_float]
+        lib.mxo_f32_to_e2m1.restype = u32
+        lib.mxo_cast_e4m3.argtypes = [vp, i64, vp]
+        lib.mxo_cast_e4m3.restype = None
+        lib.mxo_cast_e2m1.argtypes = [vp, i64, vp]
+        lib.mxo_cast_e2m1.restype = None
+        lib.mxo_e4m3_value.argtypes = [u32]
+        lib.mxo_e4m3_value.restype = ctypes.c_float
+        _lib = lib
+    return _lib
+
+
+def _ptr(a: np.ndarray) -> ctypes.c_void_p:
+    return ctypes.c_void_p(a.ctypes.data)
+
+
+_DT = {"bf16": 0, "f16": 1, "f32": 2}
+
+
+def mx_quantize(fmt: str, x: np.ndarray, dtype: str) -> tuple[np.ndarray, np.ndarray]:
+    """MX quantize of a [rows, k] array.
+
+    fmt: "mxfp8" or "mxfp4".  dtype: "bf16" (x holds uint16 bf16 bit patterns),
+    "f16" (float16) or "f32" (float32).  Returns (codes, scales) as uint8:
+    codes [rows, k] for MXFP8, [rows, k/2] packed for MXFP4.
+    """
+    lib = _load()
+    if dtype == "bf16":
+        x = np.ascontiguousarray(x, dtype=np.uint16)
+    elif dtype == "f16":
+        x = np.ascontiguousarray(x, dtype=np.float16)
+    else:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+    rows, k = x.shape
+    f = 0 if fmt == "mxfp8" else 1
+    q = np.zeros((rows, k if f == 0 else k // 2), dtype=np.uint8)
+    s = np.zeros((rows, k // 32), dtype=np.uint8)
+    lib.mxo_quantize(f, _DT[dtype], _ptr(x), k, rows, k, _ptr(q), _ptr(s))
+    return q, s
+
+
+def mx_dequant(fmt: str, q: np.ndarray, s: np.ndarray) -> np.ndarray:
+    """fp32 [rows, k] = value(code) * 2^(s-127) (scale byte 255 -> inf)."""
+    lib = _load()
+    q = np.ascontiguousarray(q, dtype=np.uint8)
+    s = np.ascontiguousarray(s, dtype=np.uint8)
+    rows = q.shape[0]
+    k = s.shape[1] * 32
+    out = np.zeros((rows, k), dtype=np.float32)
+    lib.mxo_dequant(0 if fmt == "mxfp8" else 1, _ptr(q), _ptr(s), rows, k, _ptr(out))
+    return out
+
+
+def unpack_codes(packed: np.ndarray) -> np.ndarray:
+    lib = _load()
+    packed = np.ascontiguousarray(packed, dtype=np.uint8)
+    codes = np.zeros(packed.shape[:-1] + (packed.shape[-1] * 2,), dtype=np.uint8)
+    lib.mxo_unpack_codes(_ptr(packed), packed.size, _ptr(codes))
+    return codes
+
+
+def pack_codes(codes: np.ndarray) -> np.ndarray:
+    lib = _load()
+    codes = np.ascontiguousarray(codes, dtype=np.uint8)
+    packed = np.zeros(codes.shape[:-1] + (codes.shape[-1] // 2,), dtype=np.uint8)
+    lib.mxo_pack_codes(_ptr(codes), codes.size, _ptr(packed))
+    return packed
+
+
+def f32_to_e4m3(values: np.ndarray) -> np.ndarray:
+    """torch's float32 -> float8_e4m3fn cast (ties to even, >464 -> NaN)."""
+    lib = _load()
+    flat = np.ascontiguousarray(values, dtype=np.float32).ravel()
+    out = np.zeros(flat.size, dtype=np.uint8)
+    lib.mxo_cast_e4m3(_ptr(flat), flat.size, _ptr(out))
+    return out.reshape(np.shape(values))
+
+
+def f32_to_e2m1(values: np.ndarray) -> np.ndarray:
+    """Nearest E2M1 code, ties to the even code, sign kept (no clamping)."""
+    lib = _load()
+    flat = np.ascontiguousarray(values, dtype=np.float32).ravel()
+    out = np.zeros(flat.size, dtype=np.uint8)
+    lib.mxo_cast_e2m1(_ptr(flat), flat.size, _ptr(out))
+    return out.reshape(np.shape(values))
+
+
+def e4m3_values(codes: np.ndarray) -> np.ndarray:
+    lib = _load()
+    table = np.array([lib.mxo_e4m3_value(c) for c in range(256)], dtype=np.float32)
+    return table[np.asarray(codes, dtype=np.uint8)]
+
+
+def bf16_bits_to_f32(bits: np.ndarray) -> np.ndarray:
+    return (np.asarray(bits, dtype=np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    """Round fp32 to bf16 (nearest even), returned as uint16 bit patterns."""
+    b = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    nan = np.isnan(np.asarray(x, dtype=np.float32))
+    r = ((b + 0x7FFF + ((b >> 16) & 1)) >> 16).astype(np.uint16)
+    r[nan] = 0x7FC0
+    return r
+
+
+# --------------------------------------------------------------- SQG-E4M3 --
+# kquant/sqg_e4m3.py:197-302.  Integer/E4M3 table constructions used by the
+# QSRT trellis labels; pinned by the SHA-256 known answers of
+# tests/test_sqg_e4m3.py:32-69.
+
+TRANSITIONS = 1 << 16
+
+
+def finite_e4m3_rank_lut(values: np.ndarray) -> np.ndarray:
+    """kquant/sqg_e4m3.py:197-214: RNE to E4M3, canonical zero, monotone."""
+    if values.ndim != 1 or values.size != TRANSITIONS:
+        raise ValueError("SQG rank-law values must contain exactly 65,536 entries")
+    raw = f32_to_e4m3(values.astype(np.float32))
+    raw[(raw & 0x7F) == 0] = 0
+    decoded = e4m3_values(raw)
+    if not np.all(np.isfinite(decoded)):
+        raise RuntimeError("SQG rank law rounded to a non-finite E4M3 value")
+    if not np.all(decoded[1:] >= decoded[:-1]):
+        raise RuntimeError("SQG rank law is not monotone after E4M3 rounding")
+    return raw
+
+
+def sqg_cheb_normal_rank_e4m3_bytes() -> np.ndarray:
+    """kquant/sqg_e4m3.py:218-230: 1.5 * ndtri((rank + 0.5) / 65536) in f64."""
+    from scipy.special import ndtri
+
+    probability = (np.arange(TRANSITIONS, dtype=np.float64) + 0.5) / TRANSITIONS
+    return finite_e4m3_rank_lut(1.5 * ndtri(probability))
+
+
+def sqg_xor_cheb_t12_rank_lut_bytes() -> np.ndarray:
+    """kquant/sqg_e4m3.py:233-257: modal byte per 16 ranks, ties -> lower byte."""
+    exact = sqg_cheb_normal_rank_e4m3_bytes().reshape(1 << 12, 16)
+    out = np.empty(1 << 12, dtype=np.uint8)
+    for i, block in enumerate(exact):
+        labels, counts = np.unique(block, return_counts=True)
+        out[i] = labels[counts == counts.max()].min()
+    return out
+
+
+def _reverse_low_bits(values: np.ndarray, bits: int) -> np.ndarray:
+    result = np.zeros_like(values)
+    for index in range(bits):
+        result |= ((values >> index) & 1) << (bits - 1 - index)
+    return result
+
+
+def sqg_xor_rank_permutation(bits: int) -> np.ndarray:
+    """kquant/sqg_e4m3.py:261-285 (carry-mixed SQG rank of every codeword)."""
+    if bits not in (2, 3, 4):
+        raise ValueError("SQG supports integer K2, K3, or K4")
+    width = 16 - bits
+    history_mask = (1 << width) - 1
+    codeword = np.arange(TRANSITIONS, dtype=np.int64)
+    history = codeword >> bits
+    branch = codeword & ((1 << bits) - 1)
+    mixed = history ^ (history >> 11)
+    mixed ^= (mixed << 11) & history_mask
+    product = (0x3FA7D929 * mixed + 0xC928FD8E) & 0xFFFFFFFF
+    phase = product & history_mask
+    syndrome = product >> (32 - bits)
+    stratum = _reverse_low_bits(branch, bits) ^ syndrome
+    return (stratum << width) | phase
+
+
+def sqg_xor_cheb_t12_bytes(bits: int) -> np.ndarray:
+    """kquant/sqg_e4m3.py:288-302: labels = T12[rank >> 4]."""
+    return sqg_xor_cheb_t12_rank_lut_bytes()[sqg_xor_rank_permutation(bits) >> 4]

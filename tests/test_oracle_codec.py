@@ -1,0 +1,222 @@
+"""Pins of the CPU codec oracle (no GPU).
+
+The oracle is checked against the reference's own known answers
+(tests/test_mxfp4.py, tests/test_sqg_e4m3.py), against torch's CPU
+float8_e4m3fn cast and log2/exp2 (the library routines the reference's
+formula runs on), and against properties the formats fix (nearest value with
+ties to even, minimal block exponent, idempotence).
+"""
+
+from __future__ import annotations
+
+import hashlib
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from tests import codec_cases as cases
+
+E2M1 = oracle.E2M1_LUT
+
+
+# ------------------------------------------------ reference known answers --
+
+def test_nibble_order_low_first():
+    # tests/test_mxfp4.py:13-16
+    assert oracle.unpack_codes(np.array([[0x21]], dtype=np.uint8)).tolist() == [[1, 2]]
+
+
+def test_pack_unpack_roundtrip():
+    # tests/test_mxfp4.py:7-10 (same seeded codes)
+    g = torch.Generator().manual_seed(0)
+    codes = torch.randint(0, 16, (7, 64), dtype=torch.uint8, generator=g).numpy()
+    assert np.array_equal(oracle.unpack_codes(oracle.pack_codes(codes)), codes)
+
+
+def test_dequant_values():
+    # tests/test_mxfp4.py:19-29: code 7 / 15 at scale byte 128 -> +-12
+    codes = np.zeros((1, 32), dtype=np.uint8)
+    codes[0, 0], codes[0, 1] = 7, 15
+    w = oracle.mx_dequant("mxfp4", oracle.pack_codes(codes), np.full((1, 1), 128, np.uint8))
+    assert w[0, 0] == 12.0 and w[0, 1] == -12.0 and w[0, 2] == 0.0
+
+
+def test_dequant_blocked_matches_dequant():
+    # tests/test_mxfp4.py:32-40
+    g = torch.Generator().manual_seed(1)
+    codes = torch.randint(0, 16, (3, 5, 96), dtype=torch.uint8, generator=g).numpy()
+    scale = torch.randint(100, 140, (3, 5, 3), dtype=torch.uint8, generator=g).numpy()
+    packed = oracle.pack_codes(codes)
+    w = oracle.mx_dequant("mxfp4", packed.reshape(15, 48), scale.reshape(15, 3))
+    vals = E2M1[codes].reshape(15, 3, 32)
+    s = np.ldexp(np.float32(1), scale.reshape(15, 3).astype(np.int32) - 127).astype(np.float32)
+    assert np.array_equal(w, (vals * s[..., None]).reshape(15, 96))
+
+
+@pytest.mark.parametrize(
+    "key,expected",
+    [
+        ("t12", "cca11fe5744c9c93a34f4217f342fbc0f74ecc8a007c076582424a505fc9da5e"),
+        (2, "62027916386245a84c86156a0a08b6cf07e41548871af0e56fb40780558f6293"),
+        (3, "afe7b3633e7d243b00b379b18ec4dca573722b3727cafef47fcb6470d7e7e6c9"),
+        (4, "5a9620f0c4d8f0a60d0b6fbea921dcecbd193e6febf31043aaa6403c20389c2f"),
+    ],
+)
+def test_sqg_t12_sha256_known_answers(key, expected):
+    # tests/test_sqg_e4m3.py:32-63: 65,536 f64 quantiles rounded to E4M3
+    table = (
+        oracle.sqg_xor_cheb_t12_rank_lut_bytes()
+        if key == "t12"
+        else oracle.sqg_xor_cheb_t12_bytes(key)
+    )
+    assert hashlib.sha256(table.tobytes()).hexdigest() == expected
+
+
+@pytest.mark.parametrize("bits", (2, 3, 4))
+def test_sqg_rank_permutation_is_bijective(bits):
+    # tests/test_sqg_e4m3.py:42-55
+    ranks = oracle.sqg_xor_rank_permutation(bits)
+    assert np.array_equal(np.sort(ranks), np.arange(1 << 16))
+    width = 16 - bits
+    strata = (ranks >> width).reshape(1 << width, 1 << bits)
+    assert np.array_equal(np.sort(strata, axis=1), np.broadcast_to(np.arange(1 << bits), strata.shape))
+
+
+# ---------------------------------------------- E4M3 / E2M1 rounding pins --
+
+def _torch_e4m3(x: np.ndarray) -> np.ndarray:
+    return torch.from_numpy(np.ascontiguousarray(x, dtype=np.float32)).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+
+
+def test_e4m3_cast_matches_torch_on_all_scaled_bf16():
+    vals = oracle.bf16_bits_to_f32(cases.finite_bf16_patterns())
+    vals = vals[np.abs(vals) <= 464.0]
+    assert np.array_equal(oracle.f32_to_e4m3(vals), _torch_e4m3(vals))
+
+
+def test_e4m3_cast_matches_torch_on_random_f32_and_ties():
+    rng = np.random.default_rng(0)
+    r = (rng.standard_normal(200_000) * np.exp2(rng.integers(-14, 9, 200_000))).astype(np.float32)
+    grid = oracle.e4m3_values(np.arange(0, 0x7F, dtype=np.uint8)).astype(np.float64)
+    mids = ((grid[1:] + grid[:-1]) / 2).astype(np.float32)  # exact ties
+    edges = np.array([448.0, 463.99, 464.0, 2.0 ** -10, 3 * 2.0 ** -11, 0.0, -0.0, 1e-30], np.float32)
+    x = np.concatenate([r, mids, -mids, edges, -edges])
+    assert np.array_equal(oracle.f32_to_e4m3(x), _torch_e4m3(x))
+
+
+def test_e2m1_rounding_ties_and_identity():
+    ties = {0.25: 0, 0.75: 2, 1.25: 2, 1.75: 4, 2.5: 4, 3.5: 6, 5.0: 6}
+    for v, code in ties.items():
+        assert oracle.f32_to_e2m1(np.array([v], np.float32))[0] == code
+        assert oracle.f32_to_e2m1(np.array([-v], np.float32))[0] == code | 8
+    for c in range(16):
+        assert oracle.f32_to_e2m1(np.array([E2M1[c]], np.float32))[0] == c
+    assert oracle.f32_to_e2m1(np.array([-0.1], np.float32))[0] == 8  # sign kept
+
+
+def test_e2m1_rounding_is_nearest():
+    x = np.random.default_rng(1).uniform(-6, 6, 100_000).astype(np.float32)
+    codes = oracle.f32_to_e2m1(x)
+    err = np.abs(x.astype(np.float64) - E2M1[codes])
+    best = np.min(np.abs(x[:, None].astype(np.float64) - E2M1[None, :8].astype(np.float64)
+                         * np.sign(x)[:, None]), axis=1)
+    assert np.allclose(err, best, rtol=0, atol=0)
+
+
+# --------------------------------------------------- block quantizer pins --
+
+def _torch_mxfp8_reference(bits: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """kquant/mxfp8.py:34-50 on torch's CPU ops (log2, ceil, exp2, div, cast)."""
+    values = torch.from_numpy(oracle.bf16_bits_to_f32(bits).copy())
+    rows, k = values.shape
+    blocks = values.view(rows, k // 32, 32)
+    amax = blocks.abs().amax(dim=-1)
+    exponent = torch.ceil(torch.log2(amax.clamp(min=1e-30) / 448.0)).clamp(min=-127, max=128)
+    scale = (exponent + 127.0).to(torch.uint8)
+    q = blocks.div(torch.exp2(exponent).unsqueeze(-1)).clamp(-448.0, 448.0).view(rows, k)
+    return q.to(torch.float8_e4m3fn).view(torch.uint8).numpy(), scale.numpy()
+
+
+@pytest.mark.parametrize("source", ["exhaustive", "random", "cfg1"])
+def test_mxfp8_quantize_matches_torch_reference_formula(source):
+    if source == "exhaustive":
+        bits = cases.exhaustive_scale_blocks(448.0, 8, 12)
+    elif source == "random":
+        bits = cases.random_blocks_bf16(20_000)
+    else:
+        from kquant_amd import workloads
+
+        bits = workloads.cfg1_weight(512, 2048).view(torch.int16).numpy().view(np.uint16)
+    bits = bits.reshape(-1, 256) if bits.size % 256 == 0 else bits.reshape(-1, 32)
+    q, s = oracle.mx_quantize("mxfp8", bits, "bf16")
+    rq, rs = _torch_mxfp8_reference(bits)
+    assert np.array_equal(s, rs)
+    assert np.array_equal(q, rq)
+
+
+def test_exact_exponent_rule_equals_log2_rule_for_all_bf16():
+    """ceil(log2(q)) == exponent(q) + (q not a power of two) for every bf16 amax."""
+    amax = np.abs(oracle.bf16_bits_to_f32(cases.finite_bf16_patterns()))
+    for qmax in (448.0, 6.0):
+        q = (np.maximum(amax, np.float32(1e-30)) / np.float32(qmax)).astype(np.float32)
+        via_log = torch.ceil(torch.log2(torch.from_numpy(q))).numpy().astype(np.int64)
+        b = q.view(np.uint32)
+        exact = ((b >> 23) & 0xFF).astype(np.int64) - 127 + ((b & 0x7FFFFF) != 0)
+        assert np.array_equal(via_log, exact)
+
+
+def test_mxfp4_block_exponent_is_minimal_and_codes_nearest():
+    bits = np.concatenate([cases.exhaustive_scale_blocks(6.0, 2, 4), cases.random_blocks_bf16(5000)])
+    q, s = oracle.mx_quantize("mxfp4", bits, "bf16")
+    x = oracle.bf16_bits_to_f32(bits).astype(np.float64)
+    e = s[:, 0].astype(np.int64) - 127
+    amax = np.maximum(np.abs(x).max(axis=1), 1e-30)
+    q32 = (amax.astype(np.float32) / np.float32(6.0)).astype(np.float64)
+    # 2^e >= fl(amax/6) and 2^(e-1) < fl(amax/6)
+    assert np.all(np.ldexp(1.0, e) >= q32) and np.all(np.ldexp(1.0, e - 1) < q32)
+    codes = oracle.unpack_codes(q)
+    y = np.clip(x / np.ldexp(1.0, e)[:, None], -6, 6)
+    vals = E2M1[codes].astype(np.float64)
+    cand = np.abs(y[..., None] - np.concatenate([E2M1[:8], -E2M1[:8]]).astype(np.float64))
+    assert np.allclose(np.abs(y - vals), cand.min(axis=-1), rtol=0, atol=0)
+    # sign is kept, including values that round to zero
+    assert np.all(((codes & 8) != 0) == np.signbit(x))
+
+
+def test_mx_quantize_idempotent_after_dequant():
+    rng = np.random.default_rng(3)
+    for fmt in ("mxfp8", "mxfp4"):
+        if fmt == "mxfp4":
+            codes = rng.integers(0, 16, (64, 256), dtype=np.uint8)
+            codes[:, ::32] = 7  # block max 6.0: the scale is reproduced exactly
+            q = oracle.pack_codes(codes)
+        else:
+            q = rng.integers(0, 0x7F, (64, 256), dtype=np.uint8) | (rng.integers(0, 2, (64, 256), dtype=np.uint8) << 7)
+            q[:, ::32] = 0x7E  # block max 448
+        s = rng.integers(90, 160, (64, 8), dtype=np.uint8)
+        w = oracle.mx_dequant(fmt, q, s)
+        bits = oracle.f32_to_bf16_bits(w)
+        assert np.array_equal(oracle.bf16_bits_to_f32(bits), w)  # exact in bf16
+        q2, s2 = oracle.mx_quantize(fmt, bits, "bf16")
+        assert np.array_equal(s2, s)
+        assert np.array_equal(oracle.mx_dequant(fmt, q2, s2), w)
+
+
+def test_zero_block_scale_byte_is_19():
+    # ceil(log2(1e-30 / 448)) = -108 -> byte 19 (kquant/mxfp8.py:41-44)
+    q, s = oracle.mx_quantize("mxfp8", np.zeros((1, 32), np.uint16), "bf16")
+    assert s[0, 0] == 19 and not q.any()
+
+
+def test_fp16_and_fp32_inputs_match_torch_formula():
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal((64, 512)) * np.exp2(rng.integers(-6, 6, (64, 1)))).astype(np.float32)
+    for dt, arr in (("f32", x), ("f16", x.astype(np.float16))):
+        q, s = oracle.mx_quantize("mxfp8", arr, dt)
+        t = torch.from_numpy(arr.astype(np.float32)).view(64, 16, 32)
+        e = torch.ceil(torch.log2(t.abs().amax(-1).clamp(min=1e-30) / 448.0)).clamp(-127, 128)
+        rq = t.div(torch.exp2(e).unsqueeze(-1)).clamp(-448, 448).view(64, 512).to(torch.float8_e4m3fn)
+        assert np.array_equal(s, (e + 127).to(torch.uint8).numpy())
+        assert np.array_equal(q, rq.view(torch.uint8).numpy())
