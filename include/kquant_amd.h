@@ -41,6 +41,8 @@ enum {
      instructions (both are tested to agree byte for byte) */
   KQ_FLAG_SOFTWARE_CVT = 1u
 };
+/* kq_syrk_accumulate flags */
+enum { KQ_SYRK_OVERWRITE = 1u };
 /* byte tables of kq_decode_bytes */
 enum { KQ_TABLE_E8M0 = 0, KQ_TABLE_E2M1 = 1, KQ_TABLE_E4M3 = 2 };
 /* expert activations */
@@ -92,6 +94,44 @@ int kq_pack_codes(const uint8_t* codes, int64_t n_codes, uint8_t* packed,
  *                                   (codebook widening, .view(e4m3).to(dtype)) */
 int kq_decode_bytes(int table, const uint8_t* in, int64_t n, int out_dtype, void* out,
                     void* stream);
+
+/* -------------------------------------------------------------- Hessian -- */
+
+/* acc += X^T diag(w) X for X [n, k] (row stride ld elements, k % 8 == 0,
+ * 16-byte aligned rows), w fp32 [n] or NULL (all ones).  Replaces the chunked
+ * fp32 addmm_ of kquant/candidate_hessian.py:98-105 and
+ * kquant/capture.py:713-730 (accumulator.addmm_(x.T, x * w[:, None])).
+ * Only 128x128 tiles with tile_row <= tile_col of acc [k, k] (row stride
+ * ld_acc) are written; kq_syrk_finalize reads exactly those.  With
+ * KQ_SYRK_OVERWRITE the tiles are written instead of accumulated (acc need
+ * not be initialised).  bf16 rows use bf16 MFMA with exact products; fp16 /
+ * fp32 rows and weights use a two-term bf16 split (16 significant bits). */
+int kq_syrk_accumulate(int in_dtype, const void* x, int64_t ld, int64_t n, int64_t k,
+                       const float* weights, float* acc, int64_t ld_acc, uint32_t flags,
+                       void* stream);
+
+/* out [k, k] = symmetric(acc) / denominator, then
+ * diag(out) += damp * mean(diag(out)).  Mirrors the upper tiles written by
+ * kq_syrk_accumulate and averages (H + H^T)/2 inside diagonal tiles
+ * (kquant/candidate_hessian.py:106-107, kquant/capture.py:861-862); damping
+ * is kquant/exl3_encoder_backend.py:1613-1625 (sigma_reg * mean(diag)).
+ * acc and out must not alias. */
+int kq_syrk_finalize(const float* acc, int64_t ld_acc, int64_t k, double denominator,
+                     float damp, float* out, int64_t ld_out, void* stream);
+
+/* out [k,k] = ((X + X^T) / 2) with X = torch.lerp(A, B, alpha); A = a, or
+ * a_scale * I when a is NULL.  kquant/candidate_hessian.py:115-138
+ * (shrink_covariance) and :204-209 (identity target of
+ * adaptive_identity_shrinkage).  Contiguous fp32 inputs; out aliases none. */
+int kq_sym_lerp(const float* a, float a_scale, const float* b, int64_t k, float alpha,
+                float* out, void* stream);
+
+/* Deterministic f64 trace and sum of squares of a contiguous fp32 [k,k]
+ * matrix (kquant/candidate_hessian.py:185-191: trace(local64),
+ * local64.square()).  workspace: 2 * KQ_COV_STATS_PARTS doubles; out: 2
+ * doubles {trace, sum of squares}, both device memory. */
+#define KQ_COV_STATS_PARTS 256
+int kq_cov_stats(const float* h, int64_t k, double* workspace, double* out, void* stream);
 
 #ifdef __cplusplus
 }

@@ -27,6 +27,7 @@ FLAG_SOFTWARE_CVT = 1
 TABLE_E8M0 = 0
 TABLE_E2M1 = 1
 TABLE_E4M3 = 2
+SYRK_OVERWRITE = 1
 ACT_SITU = 0
 ACT_SWIGLU = 1
 
@@ -46,7 +47,12 @@ SIGNATURES: dict[str, list] = {
     "kq_unpack_codes": [_VP, _I64, _VP, _VP],
     "kq_pack_codes": [_VP, _I64, _VP, _VP],
     "kq_decode_bytes": [_INT, _VP, _I64, _INT, _VP, _VP],
+    "kq_syrk_accumulate": [_INT, _VP, _I64, _I64, _I64, _VP, _VP, _I64, _U32, _VP],
+    "kq_syrk_finalize": [_VP, _I64, _I64, _F64, _F32, _VP, _I64, _VP],
+    "kq_sym_lerp": [_VP, _F32, _VP, _I64, _F32, _VP, _VP],
+    "kq_cov_stats": [_VP, _I64, _VP, _VP, _VP],
 }
+COV_STATS_PARTS = 256
 
 _lib: ctypes.CDLL | None = None
 

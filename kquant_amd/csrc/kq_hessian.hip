@@ -1,0 +1,426 @@
+// Calibration Hessian: H += X^T diag(w) X over token rows, fp32 accumulate.
+//
+// kquant accumulates H with chunked fp32 addmm_ (kquant/candidate_hessian.py:
+// 98-105, kquant/capture.py:713-730).  Here bf16 activations go straight into
+// bf16 MFMA (v_mfma_f32_32x32x16_bf16): bf16 x bf16 products are exact in
+// fp32, so only the summation order differs from the reference.  fp16 / fp32
+// rows and row weights are split into a bf16 high part and a bf16 residual
+// (x*w = hi + lo to 16 significant bits), costing one more MFMA per step.
+//
+// Tiling: the K x K output is cut into 128 x 128 tiles and only tiles with
+// row-tile <= col-tile are computed (the other half is the mirror image).
+// A 256-thread workgroup owns one tile and streams every token row through
+// it in steps of 64 tokens.  Each thread loads an 8-token x 8-feature block
+// (eight 16-byte row loads), transposes it in registers with v_perm so that
+// each feature's 8 tokens are contiguous, and stores it into an LDS slab laid
+// out [feature][token] -- the MFMA operand order (8 consecutive reduction
+// elements per lane).  LDS is double buffered: the global loads of step s+1
+// are in flight while step s runs on the matrix cores.
+#include "kq_common.h"
+#include "kq_internal.h"
+
+namespace kq {
+
+namespace syrk {
+constexpr int TILE = 128;          // output tile edge
+constexpr int BK = 64;             // tokens per pipeline step
+constexpr int ROW_BYTES = BK * 2 + 16;  // LDS row (one feature): 64 bf16 + pad
+constexpr int SLAB_BYTES = TILE * ROW_BYTES;  // 18 KiB
+}  // namespace syrk
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// 8x8 transpose of 16-bit elements held as 8 rows of 4 dwords.
+// in[t] = elements (t, 0..7) packed two per dword; out[f] = (0..7, f).
+__device__ __forceinline__ void transpose8x8_b16(const u32x4_t in[8], u32x4_t out[8]) {
+#pragma unroll
+  for (int f = 0; f < 8; ++f) {
+    const uint32_t sel = (f & 1) ? 0x07060302u : 0x05040100u;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      out[f][e] = __builtin_amdgcn_perm(in[2 * e + 1][f >> 1], in[2 * e][f >> 1], sel);
+  }
+}
+
+// Split fp32 values into bf16 hi (round to nearest) and bf16 lo = fp32 residual.
+__device__ __forceinline__ void split_bf16(float v, uint32_t& hi, uint32_t& lo) {
+  __bf16 h = (__bf16)v;
+  float r = v - (float)h;
+  hi = __builtin_bit_cast(uint16_t, h);
+  lo = __builtin_bit_cast(uint16_t, (__bf16)r);
+}
+
+// IN: 0 bf16, 1 f16, 2 f32.  SPLIT: operands carry a bf16 residual part
+// (needed for weights or non-bf16 inputs).
+template <int IN, bool SPLIT, bool WEIGHTED>
+__global__ __launch_bounds__(256, 1) void syrk_upper_kernel(
+    const void* __restrict__ x, int64_t ld, int64_t n, int64_t k,
+    const float* __restrict__ w, float* __restrict__ acc, int64_t ld_acc, int ntiles,
+    int overwrite) {
+  using namespace syrk;
+  // ---- tile coordinates: linear index -> (ti <= tj) over the upper triangle
+  int rem = blockIdx.x, ti = 0;
+  while (rem >= ntiles - ti) { rem -= ntiles - ti; ++ti; }
+  const int tj = ti + rem;
+  const bool diag = ti == tj;
+  const int64_t row0 = (int64_t)ti * TILE, col0 = (int64_t)tj * TILE;
+
+  // LDS: [buffer][slab] with slabs A(hi) B(hi) [A(lo) B(lo)]
+  constexpr int NSLAB = SPLIT ? 4 : 2;
+  extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  // loader role: 256 threads cover 2 slabs x (16 feature groups x 8 token groups)
+  const int slab = tid >> 7;              // 0: rows of A (ti), 1: rows of B (tj)
+  const int fg = tid & 15;                // feature group (8 features)
+  const int tg = (tid >> 4) & 7;          // token group (8 tokens)
+  const int64_t feat0 = (slab == 0 ? row0 : col0) + fg * 8;
+  const bool feat_ok = feat0 < k;         // k % 8 == 0: whole groups in or out
+
+  u32x4_t regs[8];
+  u32x4_t regs_lo[8];
+
+  auto load_step = [&](int64_t t0) {
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const int64_t tok = t0 + tg * 8 + t;
+      u32x4_t v = {0u, 0u, 0u, 0u};
+      u32x4_t vlo = {0u, 0u, 0u, 0u};
+      if (feat_ok && tok < n) {
+        float wt = 1.0f;
+        if (WEIGHTED) wt = (slab == 1) ? w[tok] : 1.0f;
+        if (IN == 0 && !SPLIT) {
+          v = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(x) + tok * ld + feat0);
+        } else {
+          float f[8];
+          if (IN == 2) {
+            const float4_t* p = reinterpret_cast<const float4_t*>(static_cast<const float*>(x) + tok * ld + feat0);
+            float4_t a = p[0], b = p[1];
+            f[0] = a[0]; f[1] = a[1]; f[2] = a[2]; f[3] = a[3];
+            f[4] = b[0]; f[5] = b[1]; f[6] = b[2]; f[7] = b[3];
+          } else {
+            u32x4_t r = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(x) + tok * ld + feat0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              f[2 * i] = IN == 0 ? bf16_bits_to_f32(r[i] & 0xffffu) : f16_bits_to_f32(r[i] & 0xffffu);
+              f[2 * i + 1] = IN == 0 ? bf16_bits_to_f32(r[i] >> 16) : f16_bits_to_f32(r[i] >> 16);
+            }
+          }
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            uint32_t h0, l0, h1, l1;
+            split_bf16(f[2 * i] * wt, h0, l0);
+            split_bf16(f[2 * i + 1] * wt, h1, l1);
+            v[i] = h0 | (h1 << 16);
+            vlo[i] = l0 | (l1 << 16);
+          }
+        }
+      }
+      regs[t] = v;
+      if (SPLIT) regs_lo[t] = vlo;
+    }
+  };
+
+  auto store_step = [&](int buf) {
+    unsigned char* base = lds + (size_t)buf * NSLAB * SLAB_BYTES;
+    u32x4_t tr[8];
+    transpose8x8_b16(regs, tr);
+#pragma unroll
+    for (int f = 0; f < 8; ++f)
+      *reinterpret_cast<u32x4_t*>(base + slab * SLAB_BYTES + (fg * 8 + f) * ROW_BYTES + tg * 16) = tr[f];
+    if (SPLIT) {
+      transpose8x8_b16(regs_lo, tr);
+#pragma unroll
+      for (int f = 0; f < 8; ++f)
+        *reinterpret_cast<u32x4_t*>(base + (2 + slab) * SLAB_BYTES + (fg * 8 + f) * ROW_BYTES + tg * 16) = tr[f];
+    }
+  };
+
+  // wave tile: 64 x 64 at (wm, wn) inside the 128 x 128 tile, 2 x 2 MFMA 32x32
+  const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+  float16_t accv[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) accv[i][j][r] = 0.0f;
+
+  const int arow = lane & 31;          // operand row inside a 32-block
+  const int koff = (lane >> 5) * 16;   // byte offset of this lane's 8 tokens
+
+  const int64_t steps = (n + BK - 1) / BK;
+  if (steps > 0) {
+    load_step(0);
+    store_step(0);
+  }
+  __syncthreads();
+  for (int64_t s = 0; s < steps; ++s) {
+    const int buf = (int)(s & 1);
+    if (s + 1 < steps) load_step((s + 1) * BK);
+    const unsigned char* base = lds + (size_t)buf * NSLAB * SLAB_BYTES;
+#pragma unroll
+    for (int kk = 0; kk < BK / 16; ++kk) {
+      bf16x8_t a[2], b[2], alo[2], blo[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        a[i] = *reinterpret_cast<const bf16x8_t*>(base + 0 * SLAB_BYTES + (wm + i * 32 + arow) * ROW_BYTES + kk * 32 + koff);
+        b[i] = *reinterpret_cast<const bf16x8_t*>(base + 1 * SLAB_BYTES + (wn + i * 32 + arow) * ROW_BYTES + kk * 32 + koff);
+        if (SPLIT) {
+          alo[i] = *reinterpret_cast<const bf16x8_t*>(base + 2 * SLAB_BYTES + (wm + i * 32 + arow) * ROW_BYTES + kk * 32 + koff);
+          blo[i] = *reinterpret_cast<const bf16x8_t*>(base + 3 * SLAB_BYTES + (wn + i * 32 + arow) * ROW_BYTES + kk * 32 + koff);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          accv[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], accv[i][j], 0, 0, 0);
+          if (SPLIT) {
+            // (a_hi + a_lo)(b_hi + b_lo) ~ a_hi b_hi + a_hi b_lo + a_lo b_hi
+            accv[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], blo[j], accv[i][j], 0, 0, 0);
+            accv[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(alo[i], b[j], accv[i][j], 0, 0, 0);
+          }
+        }
+    }
+    if (s + 1 < steps) {
+      store_step(buf ^ 1);
+    }
+    __syncthreads();
+  }
+
+  // ---- epilogue: C[32x32] lane layout: col = lane % 32,
+  //      row = 8 * (r / 4) + 4 * (lane / 32) + r % 4
+  const int ccol = lane & 31, crow = (lane >> 5) * 4;
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t gr = row0 + wm + i * 32 + 8 * (r >> 2) + crow + (r & 3);
+        const int64_t gc = col0 + wn + j * 32 + ccol;
+        if (gr < k && gc < k) {
+          float* p = acc + gr * ld_acc + gc;
+          *p = overwrite ? accv[i][j][r] : *p + accv[i][j][r];
+        }
+      }
+  (void)diag;
+}
+
+// out = sym(acc) * inv_denom : upper tiles are read for every (i, j) as
+// acc[min][max]; one thread per output element, rows of 256 columns.
+__global__ __launch_bounds__(256) void syrk_finalize_kernel(
+    const float* __restrict__ acc, int64_t ld_acc, int64_t k, float inv_denom,
+    float* __restrict__ out, int64_t ld_out) {
+  const int64_t i = blockIdx.y;
+  const int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (j >= k) return;
+  // computed region: tile(i) <= tile(j); inside a diagonal tile both halves exist
+  const int64_t ti = i / syrk::TILE, tj = j / syrk::TILE;
+  const float v = ti <= tj ? acc[i * ld_acc + j] : acc[j * ld_acc + i];
+  out[i * ld_out + j] = v * inv_denom;
+}
+
+// Symmetrize the diagonal tiles ((H + H^T) / 2 inside each diagonal tile, the
+// off-diagonal tiles are exact mirrors already) and add damp * mean(diag).
+// One workgroup: reduce the diagonal, then update it.
+__global__ __launch_bounds__(1024) void syrk_damp_kernel(float* __restrict__ out, int64_t ld_out,
+                                                         int64_t k, float damp) {
+  __shared__ float partial[1024];
+  float s = 0.0f;
+  for (int64_t i = threadIdx.x; i < k; i += 1024) s += out[i * ld_out + i];
+  partial[threadIdx.x] = s;
+  __syncthreads();
+  for (int w = 512; w > 0; w >>= 1) {
+    if ((int)threadIdx.x < w) partial[threadIdx.x] += partial[threadIdx.x + w];
+    __syncthreads();
+  }
+  const float add = damp * (partial[0] / (float)k);
+  for (int64_t i = threadIdx.x; i < k; i += 1024) out[i * ld_out + i] += add;
+}
+
+// Inside diagonal tiles the two halves are computed by different lanes with
+// different summation orders; average them like kquant's (H + H^T) / 2.
+__global__ __launch_bounds__(256) void syrk_sym_diag_kernel(float* __restrict__ out, int64_t ld_out,
+                                                            int64_t k) {
+  const int64_t t = blockIdx.y;  // diagonal tile
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t r = e / syrk::TILE, c = e % syrk::TILE;
+  if (r >= syrk::TILE || c <= r) return;
+  const int64_t i = t * syrk::TILE + r, j = t * syrk::TILE + c;
+  if (i >= k || j >= k) return;
+  const float a = out[i * ld_out + j], b = out[j * ld_out + i];
+  const float m = (a + b) * 0.5f;
+  out[i * ld_out + j] = m;
+  out[j * ld_out + i] = m;
+}
+
+// out = sym(lerp(A, B, alpha)) with A = a, or a_scale * I when a is null.
+// torch.lerp: start + w*(end-start) for w < 0.5, else end - (end-start)*(1-w).
+__device__ __forceinline__ float lerp_torch(float s, float e, float w) {
+  return w < 0.5f ? s + w * (e - s) : e - (e - s) * (1.0f - w);
+}
+__global__ __launch_bounds__(256) void sym_lerp_kernel(const float* __restrict__ a, float a_scale,
+                                                       const float* __restrict__ b, int64_t k,
+                                                       float alpha, float* __restrict__ out) {
+  const int64_t i = blockIdx.y;
+  const int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (j >= k) return;
+  const float aij = a ? a[i * k + j] : (i == j ? a_scale : 0.0f);
+  const float aji = a ? a[j * k + i] : (i == j ? a_scale : 0.0f);
+  const float x = lerp_torch(aij, b[i * k + j], alpha);
+  const float y = lerp_torch(aji, b[j * k + i], alpha);
+  out[i * k + j] = (x + y) * 0.5f;
+}
+
+// Partial f64 sums of the diagonal and of all squares, one per workgroup.
+__global__ __launch_bounds__(256) void cov_stats_partial_kernel(const float* __restrict__ h,
+                                                                int64_t k, double* __restrict__ ws) {
+  __shared__ double s_tr[256], s_sq[256];
+  double tr = 0.0, sq = 0.0;
+  const int64_t total = k * k;
+  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
+    const double v = (double)h[e];
+    sq += v * v;
+    if (e / k == e % k) tr += v;
+  }
+  s_tr[threadIdx.x] = tr;
+  s_sq[threadIdx.x] = sq;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if ((int)threadIdx.x < w) {
+      s_tr[threadIdx.x] += s_tr[threadIdx.x + w];
+      s_sq[threadIdx.x] += s_sq[threadIdx.x + w];
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    ws[2 * blockIdx.x] = s_tr[0];
+    ws[2 * blockIdx.x + 1] = s_sq[0];
+  }
+}
+
+__global__ __launch_bounds__(256) void cov_stats_final_kernel(const double* __restrict__ ws, int nparts,
+                                                              double* __restrict__ out) {
+  __shared__ double s_tr[256], s_sq[256];
+  double tr = 0.0, sq = 0.0;
+  for (int p = threadIdx.x; p < nparts; p += 256) {
+    tr += ws[2 * p];
+    sq += ws[2 * p + 1];
+  }
+  s_tr[threadIdx.x] = tr;
+  s_sq[threadIdx.x] = sq;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if ((int)threadIdx.x < w) {
+      s_tr[threadIdx.x] += s_tr[threadIdx.x + w];
+      s_sq[threadIdx.x] += s_sq[threadIdx.x + w];
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    out[0] = s_tr[0];
+    out[1] = s_sq[0];
+  }
+}
+
+}  // namespace kq
+
+using namespace kq;
+
+extern "C" int kq_sym_lerp(const float* a, float a_scale, const float* b, int64_t k, float alpha,
+                           float* out, void* stream) {
+  if (k <= 0 || b == nullptr || out == nullptr)
+    return kq_fail(KQ_ERR_INVALID, "kq_sym_lerp: bad arguments (k=%lld)", (long long)k);
+  if (out == b || (a != nullptr && out == a))
+    return kq_fail(KQ_ERR_INVALID, "kq_sym_lerp: out must not alias the inputs");
+  sym_lerp_kernel<<<dim3((unsigned)((k + 255) / 256), (unsigned)k), 256, 0, (hipStream_t)stream>>>(
+      a, a_scale, b, k, alpha, out);
+  return kq_check_launch(hipGetLastError(), "kq_sym_lerp");
+}
+
+extern "C" int kq_cov_stats(const float* h, int64_t k, double* workspace, double* out,
+                            void* stream) {
+  if (k <= 0) return kq_fail(KQ_ERR_INVALID, "kq_cov_stats: k must be positive");
+  hipStream_t st = (hipStream_t)stream;
+  cov_stats_partial_kernel<<<KQ_COV_STATS_PARTS, 256, 0, st>>>(h, k, workspace);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return kq_check_launch(e, "kq_cov_stats");
+  cov_stats_final_kernel<<<1, 256, 0, st>>>(workspace, KQ_COV_STATS_PARTS, out);
+  return kq_check_launch(hipGetLastError(), "kq_cov_stats");
+}
+
+template <int IN, bool SPLIT, bool WEIGHTED>
+static hipError_t launch_syrk(const void* x, int64_t ld, int64_t n, int64_t k, const float* w,
+                              float* acc, int64_t ld_acc, int overwrite, hipStream_t st) {
+  const int nt = (int)((k + syrk::TILE - 1) / syrk::TILE);
+  const int ntiles = nt * (nt + 1) / 2;
+  const int nslab = SPLIT ? 4 : 2;
+  const size_t lds = (size_t)2 * nslab * syrk::SLAB_BYTES;
+  auto kern = syrk_upper_kernel<IN, SPLIT, WEIGHTED>;
+  hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (e != hipSuccess) return e;
+  kern<<<dim3(ntiles), dim3(256), lds, st>>>(x, ld, n, k, w, acc, ld_acc, nt, overwrite);
+  return hipGetLastError();
+}
+
+extern "C" int kq_syrk_accumulate(int in_dtype, const void* x, int64_t ld, int64_t n, int64_t k,
+                                  const float* weights, float* acc, int64_t ld_acc, uint32_t flags,
+                                  void* stream) {
+  if (in_dtype < KQ_DT_BF16 || in_dtype > KQ_DT_F32)
+    return kq_fail(KQ_ERR_INVALID, "kq_syrk_accumulate: unknown input dtype %d", in_dtype);
+  if (n < 0 || k <= 0 || k % 8 != 0 || ld < k || ld % 8 != 0 || ld_acc < k)
+    return kq_fail(KQ_ERR_INVALID,
+                   "kq_syrk_accumulate: need k > 0, k %% 8 == 0, ld >= k, ld %% 8 == 0, ld_acc >= k "
+                   "(n=%lld k=%lld ld=%lld ld_acc=%lld)",
+                   (long long)n, (long long)k, (long long)ld, (long long)ld_acc);
+  if (kq_misaligned(x, 16))
+    return kq_fail(KQ_ERR_INVALID, "kq_syrk_accumulate: rows must be 16-byte aligned");
+  if (k > (int64_t)1 << 20)
+    return kq_fail(KQ_ERR_LIMIT, "kq_syrk_accumulate: k=%lld exceeds 2^20", (long long)k);
+  const int overwrite = (flags & KQ_SYRK_OVERWRITE) ? 1 : 0;
+  hipStream_t st = (hipStream_t)stream;
+  hipError_t e;
+  const bool weighted = weights != nullptr;
+  if (in_dtype == KQ_DT_BF16) {
+    e = weighted ? launch_syrk<0, true, true>(x, ld, n, k, weights, acc, ld_acc, overwrite, st)
+                 : launch_syrk<0, false, false>(x, ld, n, k, weights, acc, ld_acc, overwrite, st);
+  } else if (in_dtype == KQ_DT_F16) {
+    e = weighted ? launch_syrk<1, true, true>(x, ld, n, k, weights, acc, ld_acc, overwrite, st)
+                 : launch_syrk<1, true, false>(x, ld, n, k, weights, acc, ld_acc, overwrite, st);
+  } else {
+    e = weighted ? launch_syrk<2, true, true>(x, ld, n, k, weights, acc, ld_acc, overwrite, st)
+                 : launch_syrk<2, true, false>(x, ld, n, k, weights, acc, ld_acc, overwrite, st);
+  }
+  return kq_check_launch(e, "kq_syrk_accumulate");
+}
+
+extern "C" int kq_syrk_finalize(const float* acc, int64_t ld_acc, int64_t k, double denominator,
+                                float damp, float* out, int64_t ld_out, void* stream) {
+  if (k <= 0 || ld_acc < k || ld_out < k)
+    return kq_fail(KQ_ERR_INVALID, "kq_syrk_finalize: bad sizes (k=%lld)", (long long)k);
+  if (!(denominator > 0.0))
+    return kq_fail(KQ_ERR_INVALID, "kq_syrk_finalize: denominator must be positive");
+  if (acc == out && ld_acc != ld_out)
+    return kq_fail(KQ_ERR_INVALID, "kq_syrk_finalize: in-place needs ld_acc == ld_out");
+  if (acc == out)
+    return kq_fail(KQ_ERR_INVALID, "kq_syrk_finalize: acc and out must not alias");
+  hipStream_t st = (hipStream_t)stream;
+  const float inv = (float)(1.0 / denominator);
+  syrk_finalize_kernel<<<dim3((unsigned)((k + 255) / 256), (unsigned)k), 256, 0, st>>>(
+      acc, ld_acc, k, inv, out, ld_out);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return kq_check_launch(e, "kq_syrk_finalize");
+  const unsigned nt = (unsigned)((k + syrk::TILE - 1) / syrk::TILE);
+  syrk_sym_diag_kernel<<<dim3((syrk::TILE * syrk::TILE + 255) / 256, nt), 256, 0, st>>>(out, ld_out, k);
+  e = hipGetLastError();
+  if (e != hipSuccess) return kq_check_launch(e, "kq_syrk_finalize");
+  if (damp != 0.0f) {
+    syrk_damp_kernel<<<1, 1024, 0, st>>>(out, ld_out, k, damp);
+    e = hipGetLastError();
+  }
+  return kq_check_launch(e, "kq_syrk_finalize");
+}

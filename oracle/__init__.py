@@ -224,3 +224,71 @@ def sqg_xor_rank_permutation(bits: int) -> np.ndarray:
 def sqg_xor_cheb_t12_bytes(bits: int) -> np.ndarray:
     """kquant/sqg_e4m3.py:288-302: labels = T12[rank >> 4]."""
     return sqg_xor_cheb_t12_rank_lut_bytes()[sqg_xor_rank_permutation(bits) >> 4]
+
+
+# ---------------------------------------------------------------- Hessian --
+
+def weighted_covariance(rows: np.ndarray, weights: np.ndarray, chunk_rows: int = 256):
+    """kquant/candidate_hessian.py:70-112 in numpy float32.
+
+    accumulator.addmm_(values.T, values * w[:, None]) per chunk of rows, then
+    / float(sum(w) in f64), then (H + H^T) * 0.5.  Returns (H f32, denom).
+    """
+    rows = np.asarray(rows)
+    weights = np.asarray(weights, dtype=np.float32)
+    if rows.ndim != 2 or weights.ndim != 1 or rows.shape[0] != weights.shape[0]:
+        raise ValueError("invalid covariance sample shapes")
+    if not rows.shape[0] or not rows.shape[1]:
+        raise ValueError("covariance samples must be nonempty")
+    k = rows.shape[1]
+    acc = np.zeros((k, k), dtype=np.float32)
+    denom = float(weights.astype(np.float64).sum())
+    if not np.isfinite(denom) or denom <= 0:
+        raise ValueError("covariance weights must have a positive finite sum")
+    for b in range(0, rows.shape[0], chunk_rows):
+        v = rows[b : b + chunk_rows].astype(np.float32)
+        w = weights[b : b + chunk_rows]
+        acc += v.T @ (v * w[:, None])
+    cov = acc / np.float32(denom)
+    return ((cov + cov.T) * np.float32(0.5)).astype(np.float32), denom
+
+
+def accumulate_hessian(rows: np.ndarray, weights: np.ndarray, chunk_rows: int = 1024):
+    """kquant/capture.py:713-730: unnormalized fp32 accumulator and the f64
+    sum of the weights, chunked addmm_."""
+    rows = np.asarray(rows)
+    weights = np.asarray(weights, dtype=np.float32)
+    k = rows.shape[1]
+    acc = np.zeros((k, k), dtype=np.float32)
+    denom = 0.0
+    for b in range(0, rows.shape[0], max(chunk_rows, 1)):
+        v = rows[b : b + chunk_rows].astype(np.float32)
+        w = weights[b : b + chunk_rows]
+        acc += v.T @ (v * w[:, None])
+        denom += float(w.astype(np.float64).sum())
+    return acc, denom
+
+
+def damp_diagonal(h: np.ndarray, sigma_reg: float) -> np.ndarray:
+    """kquant/exl3_encoder_backend.py:1620-1625: H.diag += sigma * mean(diag)."""
+    h = np.array(h, dtype=np.float32, copy=True)
+    diag_mean = np.float32(np.diag(h).astype(np.float32).mean(dtype=np.float32))
+    idx = np.arange(h.shape[0])
+    h[idx, idx] += np.float32(sigma_reg) * diag_mean
+    return h
+
+
+def covariance_comparison(reference: np.ndarray, candidate: np.ndarray) -> dict:
+    """kquant/candidate_hessian.py:219-258 (relative Frobenius in f64 etc.)."""
+    ref = np.asarray(reference, dtype=np.float32).astype(np.float64)
+    cand = np.asarray(candidate, dtype=np.float32).astype(np.float64)
+    ref_norm = np.linalg.norm(ref)
+    rd, cd = np.diag(ref), np.diag(cand)
+    dd = np.linalg.norm(rd) * np.linalg.norm(cd)
+    tr = np.trace(ref)
+    return {
+        "relative_frobenius_difference": float(np.linalg.norm(cand - ref) / ref_norm) if ref_norm > 0 else float("inf"),
+        "trace_ratio": float(np.trace(cand) / tr) if tr != 0 else float("inf"),
+        "diagonal_cosine_similarity": float(rd @ cd / dd) if dd > 0 else 0.0,
+        "candidate_symmetry_max_abs": float(np.abs(cand - cand.T).max()),
+    }

@@ -1,0 +1,146 @@
+"""GPU parity of the Hessian (SYRK) kernels.
+
+Bar: covariance_comparison relative Frobenius difference <= 1e-5 against the
+chunked fp32 oracle (kquant/candidate_hessian.py:98-107) and against exact
+float64 sums.  At the benchmark size (65,536 x 7,168) the full oracle is too
+slow on a CPU; there the check uses exact float64 dot products of 4,096
+sampled entries, the exact trace and the symmetry of the result.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from kquant_amd import _native as N
+from kquant_amd import candidate_hessian as ch
+from kquant_amd import workloads
+from tests.test_oracle_hessian import KATS, _expected
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+
+
+def _rel_fro(ref: np.ndarray, got: np.ndarray) -> float:
+    return oracle.covariance_comparison(ref, got)["relative_frobenius_difference"]
+
+
+@pytest.mark.parametrize("case", range(len(KATS)))
+def test_reference_known_answers_on_gpu(gpu, case):
+    rows, weights, expected = KATS[case]
+    h, denom = ch.weighted_covariance(
+        torch.tensor(rows, dtype=torch.float32), torch.tensor(weights), device=torch.device("cpu")
+    )
+    assert h.device.type == "cpu"
+    torch.testing.assert_close(h, torch.from_numpy(_expected(rows, weights, expected)))
+    torch.testing.assert_close(h, h.T)
+    assert denom == pytest.approx(float(sum(weights)))
+
+
+@pytest.mark.parametrize("n,k", [(4096, 640), (1000, 256), (63, 128), (4097, 136), (257, 8)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_unweighted_matches_oracle(gpu, n, k, dtype):
+    print(f"case syrk n={n} k={k} {dtype}", flush=True)
+    x = workloads.student_t4(n, k, seed=n + k, dtype=dtype)
+    ones = torch.ones(n)
+    h, denom = ch.weighted_covariance(x, ones, device=gpu, return_cpu=True)
+    ref, rden = oracle.weighted_covariance(x.float().numpy(), ones.numpy(), 256)
+    assert denom == rden
+    assert _rel_fro(ref, h.numpy()) <= TOL
+    x64 = x.double().numpy()
+    assert _rel_fro(x64.T @ x64 / n, h.numpy()) <= TOL
+    assert torch.equal(h, h.T)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_weighted_matches_oracle(gpu, dtype):
+    n, k = 3000, 384
+    x = workloads.student_t4(n, k, seed=11, dtype=dtype)
+    w = torch.rand(n, generator=torch.Generator().manual_seed(2)) * 2.0
+    w[::7] = 0.0
+    h, denom = ch.weighted_covariance(x, w, device=gpu)
+    ref, _ = oracle.weighted_covariance(x.float().numpy(), w.numpy(), 256)
+    assert _rel_fro(ref, h.numpy()) <= TOL
+    acc, d2 = ch.accumulate_hessian(x, w, device=gpu)
+    racc, rd2 = oracle.accumulate_hessian(x.float().numpy(), w.numpy(), 1024)
+    assert _rel_fro(racc, acc.cpu().numpy()) <= TOL
+    assert d2 == pytest.approx(rd2)
+
+
+def test_damped_hessian(gpu):
+    n, k = 2048, 512
+    x = workloads.student_t4(n, k, seed=5)
+    h, denom = ch.damped_hessian(x, damp=0.01)
+    ref, _ = oracle.weighted_covariance(x.float().numpy(), np.ones(n, np.float32), 256)
+    ref = oracle.damp_diagonal(ref, 0.01)
+    assert denom == n
+    assert _rel_fro(ref, h.cpu().numpy()) <= TOL
+    d = torch.diagonal(h).cpu().double()
+    assert torch.allclose(d, torch.from_numpy(np.diag(ref)).double(), rtol=1e-5, atol=0)
+
+
+def test_cfg4_full_size_sampled_entries(gpu):
+    """65,536 Student-t(4) bf16 rows at K = 7,168 (benchmark configuration)."""
+    n, k = 65536, 7168
+    g = torch.Generator(device=gpu).manual_seed(0)
+    z0 = torch.randn(n, k, generator=g, device=gpu)
+    chi = torch.zeros(n, k, device=gpu)
+    for _ in range(4):
+        chi += torch.randn(n, k, generator=g, device=gpu).square()
+    x = (z0 / torch.sqrt(chi / 4.0)).to(torch.bfloat16)
+    del z0, chi
+    h, denom = ch.damped_hessian(x, damp=0.0)
+    torch.cuda.synchronize()
+    assert torch.equal(h, h.T)
+    # checker: exact float64 dot products of sampled entries (torch on the GPU)
+    rng = np.random.default_rng(0)
+    i = torch.from_numpy(rng.integers(0, k, 4096)).to(gpu)
+    j = torch.from_numpy(rng.integers(0, k, 4096)).to(gpu)
+    j[:512] = i[:512]  # include diagonal entries
+    exact = torch.zeros(4096, dtype=torch.float64, device=gpu)
+    for c in range(0, 4096, 512):
+        exact[c:c + 512] = (x[:, i[c:c + 512]].double() * x[:, j[c:c + 512]].double()).sum(0) / n
+    got = h[i, j].double()
+    rel = float(torch.linalg.vector_norm(got - exact) / torch.linalg.vector_norm(exact))
+    print(f"cfg4 sampled-entry relative error {rel:.3e}", flush=True)
+    assert rel <= TOL
+    trace_exact = float(x.float().square().sum(dtype=torch.float64)) / n
+    assert abs(float(torch.trace(h.double())) - trace_exact) / trace_exact <= 1e-6
+
+
+def test_repeat_runs_are_bitwise_identical(gpu):
+    x = workloads.student_t4(4096, 512, seed=9).to(gpu)
+    a, _ = ch.damped_hessian(x, damp=0.0)
+    b, _ = ch.damped_hessian(x, damp=0.0)
+    assert torch.equal(a, b)
+
+
+def test_shrinkage_matches_reference_formulas(gpu):
+    # tests/test_candidate_hessian.py:73-110 on GPU tensors
+    rows = torch.tensor([[1.0, 0.0], [0.0, 2.0], [1.0, 2.0], [-1.0, 1.0]])
+    weights = torch.ones(4)
+    local, _ = ch.weighted_covariance(rows, weights, device=gpu, return_cpu=False)
+    actual, evidence = ch.adaptive_identity_shrinkage(local, weights, max_local_alpha=0.6)
+    assert evidence["effective_sample_size"] == pytest.approx(4.0)
+    assert 0.0 <= evidence["local_alpha"] <= 0.6
+    assert evidence["identity_scale"] == pytest.approx(float(torch.trace(local) / 2))
+    torch.testing.assert_close(torch.trace(actual), torch.trace(local))
+    torch.testing.assert_close(actual, actual.T)
+
+    rows = torch.tensor([[3.0, 0.0], [0.0, 1.0], [2.0, -1.0], [-2.0, 1.0]])
+    weights = torch.tensor([1.0, 2.0, 1.0, 0.5])
+    local, _ = ch.weighted_covariance(rows, weights, device=gpu, return_cpu=False)
+    actual, evidence = ch.adaptive_identity_shrinkage(local, weights)
+    identity_scale = float(torch.trace(local) / local.shape[0])
+    expected = torch.lerp(torch.eye(2, device=gpu) * identity_scale, local, evidence["local_alpha"])
+    torch.testing.assert_close(actual, expected)
+
+    g, l = torch.eye(3), torch.diag(torch.tensor([2.0, 3.0, 4.0]))
+    torch.testing.assert_close(ch.shrink_covariance(g, l, 0), g)
+    torch.testing.assert_close(ch.shrink_covariance(g, l, 1), l)
+    torch.testing.assert_close(ch.shrink_covariance(g, l, 0.25), 0.75 * g + 0.25 * l)
+    diagnostics = ch.covariance_comparison(g, l)
+    assert diagnostics["trace_ratio"] == 3.0
