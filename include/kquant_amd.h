@@ -95,6 +95,20 @@ int kq_pack_codes(const uint8_t* codes, int64_t n_codes, uint8_t* packed,
 int kq_decode_bytes(int table, const uint8_t* in, int64_t n, int out_dtype, void* out,
                     void* stream);
 
+/* --------------------------------------------------------- dense linear -- */
+
+/* C [m, n] = A [m, k] (bf16, row stride lda) x dequant(W)^T, W [n, k] in
+ * w_fmt (MXFP8: E4M3 bytes [n, k]; MXFP4: packed [n, k/2]) with E8M0 scales
+ * [n, k/32]; fp32 accumulation, C in bf16 or fp32 (row stride ldc).
+ * Replaces the dequantize-then-matmul of kquant's expert/linear oracles
+ * (kquant/pack/qsrt_validation.py:249-258, scripts/closure_mxfp8_mlp.py:
+ * 146-160: fp32 matmul over dequantized weights) and the external
+ * mxfp8_linear.mm call site (scripts/closure_mxfp8_mlp.py:172-177).
+ * k % 64 == 0; a, w_q 16-byte aligned. */
+int kq_mx_linear(int w_fmt, const void* a, int64_t lda, const void* w_q,
+                 const uint8_t* w_scale, int64_t m, int64_t n, int64_t k,
+                 int out_dtype, void* c, int64_t ldc, void* stream);
+
 /* -------------------------------------------------------------- Hessian -- */
 
 /* acc += X^T diag(w) X for X [n, k] (row stride ld elements, k % 8 == 0,

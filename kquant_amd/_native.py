@@ -51,6 +51,7 @@ SIGNATURES: dict[str, list] = {
     "kq_syrk_finalize": [_VP, _I64, _I64, _F64, _F32, _VP, _I64, _VP],
     "kq_sym_lerp": [_VP, _F32, _VP, _I64, _F32, _VP, _VP],
     "kq_cov_stats": [_VP, _I64, _VP, _VP, _VP],
+    "kq_mx_linear": [_INT, _VP, _I64, _VP, _VP, _I64, _I64, _I64, _INT, _VP, _I64, _VP],
 }
 COV_STATS_PARTS = 256
 

@@ -292,3 +292,75 @@ def covariance_comparison(reference: np.ndarray, candidate: np.ndarray) -> dict:
         "diagonal_cosine_similarity": float(rd @ cd / dd) if dd > 0 else 0.0,
         "candidate_symmetry_max_abs": float(np.abs(cand - cand.T).max()),
     }
+
+
+# -------------------------------------------------------------- MoE expert --
+
+def _sigmoid(x: np.ndarray) -> np.ndarray:
+    return 1.0 / (1.0 + np.exp(-x))
+
+
+def situ(gate: np.ndarray, up: np.ndarray, beta: float = 4.0, linear_beta: float = 25.0) -> np.ndarray:
+    """kquant/tp_simulator.py:83-94 in float32 (before the output cast)."""
+    g = gate.astype(np.float32)
+    u = up.astype(np.float32)
+    gate_value = np.float32(beta) * np.tanh(g / np.float32(beta)) * _sigmoid(g)
+    up_value = np.float32(linear_beta) * np.tanh(u / np.float32(linear_beta))
+    return (gate_value * up_value).astype(np.float32)
+
+
+def swiglu(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
+    """silu(gate) * up in float32."""
+    g = gate.astype(np.float32)
+    return (g * _sigmoid(g) * up.astype(np.float32)).astype(np.float32)
+
+
+def round_bf16(x: np.ndarray) -> np.ndarray:
+    return bf16_bits_to_f32(f32_to_bf16_bits(x))
+
+
+def moe_forward(
+    x: np.ndarray,
+    route_ids: np.ndarray,
+    route_weights: np.ndarray,
+    w13: callable,
+    w2: callable,
+    activation: str = "situ",
+    tokens: np.ndarray | None = None,
+    intermediate_bf16: bool = True,
+) -> np.ndarray:
+    """Routed MoE forward of scripts/closure_exl3_layer.py:557-598 (tp=1).
+
+    x: float32 [T, H] (bf16 values); route_ids int [T, k]; route_weights f32
+    [T, k]; w13(e) -> float32 [2I, H] (gate rows first), w2(e) -> float32
+    [H, I], both dequantized weights.  For every expert: gate/up fp32 GEMMs,
+    activation in fp32, the activated intermediate rounded to bf16 (the
+    down-projection operand, as F.linear in bf16 makes it), down GEMM in
+    fp32, contribution = route_weight * partial, summed per token in fp32.
+    ``tokens`` restricts the output to a subset of token rows (the result
+    has one row per listed token).
+    """
+    act = situ if activation == "situ" else swiglu
+    T = x.shape[0]
+    rows = np.arange(T) if tokens is None else np.asarray(tokens)
+    pos = {int(t): i for i, t in enumerate(rows)}
+    sub_ids = route_ids[rows]
+    out = None
+    for e in np.unique(sub_ids):
+        sel_t, sel_s = np.nonzero(sub_ids == e)
+        tok = rows[sel_t]
+        w13e = w13(int(e))
+        w2e = w2(int(e))
+        inter = w13e.shape[0] // 2
+        xe = x[tok].astype(np.float32)
+        gate = xe @ w13e[:inter].T
+        up = xe @ w13e[inter:].T
+        a = act(gate, up)
+        if intermediate_bf16:
+            a = round_bf16(a)
+        partial = a @ w2e.T
+        if out is None:
+            out = np.zeros((rows.size, w2e.shape[0]), dtype=np.float32)
+        contrib = route_weights[tok, sel_s][:, None].astype(np.float32) * partial
+        np.add.at(out, np.array([pos[int(t)] for t in tok]), contrib)
+    return out

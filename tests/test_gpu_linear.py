@@ -1,0 +1,97 @@
+"""GPU parity of the dequant-fused MX linear kernel (kq_mx_linear).
+
+Oracle: fp32 matmul of the bf16 activations and the reference-dequantized
+weights (scripts/closure_mxfp8_mlp.py:146-160).  Bars:
+  fp32 output: max |C - R| / max |R| <= 2e-3 (observed ~1e-6: products are
+      exact, only the summation order differs);
+  bf16 output: the rounding of the output alone reaches 2^-8 of an element,
+      so C is compared with the oracle rounded to bf16 (as the reference's
+      closure does, scripts/closure_mxfp8_mlp.py:184-186): every element
+      within one bf16 ulp (+ 1e-5 max|R| for cancellation) of it, >= 99%
+      bitwise equal, and
+      |C - R| <= 2^-8 |R| + 1e-5 max|R| elementwise.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from kquant_amd import linear, workloads
+from kquant_amd import mxfp4 as kq_mxfp4
+from kquant_amd import mxfp8
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+
+
+def _max_rel(ref: np.ndarray, got: np.ndarray) -> float:
+    return float(np.abs(got.astype(np.float64) - ref).max() / np.abs(ref).max())
+
+
+def check_bf16_output(ref: np.ndarray, got: np.ndarray) -> None:
+    """got: bf16 kernel output as float; ref: fp32/f64 oracle."""
+    ref = np.asarray(ref, dtype=np.float64)
+    r16 = oracle.round_bf16(ref.astype(np.float32)).astype(np.float64)
+    slack = 1e-5 * np.abs(ref).max()  # fp32 summation-order slack (cancellation)
+    ulp = np.abs(r16) * 2.0 ** -7 + slack
+    assert np.all(np.abs(got - r16) <= ulp), "an element is more than one bf16 ulp off"
+    assert np.mean(got == r16) >= 0.99
+    bound = np.abs(ref) * 2.0 ** -8 + 1e-5 * np.abs(ref).max()
+    assert np.all(np.abs(got - ref) <= bound)
+
+
+def _quantized(fmt, w):
+    if fmt == "mxfp8":
+        q, s = mxfp8.mxfp8_quantize(w)
+        return q, s, oracle.mx_dequant("mxfp8", q.view(torch.uint8).cpu().numpy(), s.cpu().numpy())
+    q, s = kq_mxfp4.mxfp4_quantize(w)
+    return q, s, oracle.mx_dequant("mxfp4", q.cpu().numpy(), s.cpu().numpy())
+
+
+@pytest.mark.parametrize("fmt", ["mxfp8", "mxfp4"])
+@pytest.mark.parametrize("m,n,k", [(256, 256, 1024), (300, 257, 192), (1, 100, 64), (17, 512, 2048), (513, 1000, 448)])
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+def test_linear_matches_fp32_oracle(gpu, fmt, m, n, k, out_dtype):
+    print(f"case linear {fmt} m={m} n={n} k={k} {out_dtype}", flush=True)
+    g = torch.Generator().manual_seed(m * 7 + n)
+    w = (torch.randn(n, k, generator=g) * 0.02).to(torch.bfloat16).to(gpu)
+    x = (torch.randn(m, k, generator=g) * torch.exp(0.5 * torch.randn(k, generator=g))).to(torch.bfloat16)
+    q, s, wd = _quantized(fmt, w)
+    fn = linear.mxfp8_linear if fmt == "mxfp8" else linear.mxfp4_linear
+    c = fn(x.to(gpu), q, s, out_dtype=out_dtype).float().cpu().numpy()
+    ref = x.float().numpy().astype(np.float64) @ wd.astype(np.float64).T
+    if out_dtype == torch.float32:
+        assert _max_rel(ref, c) <= TOL
+        assert _max_rel(ref, c) <= 1e-5
+    else:
+        check_bf16_output(ref, c)
+
+
+def test_cfg2_full_size(gpu):
+    """X [4096, 7168] x MXFP8 W [12288, 7168] (benchmark configuration 2);
+    the oracle is evaluated on 256 sampled rows of X."""
+    w = workloads.cfg2_weight().to(gpu)
+    x = workloads.cfg2_activations()
+    q, s = mxfp8.mxfp8_quantize(w)
+    c = linear.mxfp8_linear(x.to(gpu), q, s)
+    rows = np.random.default_rng(0).choice(4096, 256, replace=False)
+    wd = oracle.mx_dequant("mxfp8", q.view(torch.uint8).cpu().numpy(), s.cpu().numpy())
+    ref = x[rows].float().numpy() @ wd.T
+    got = c[torch.from_numpy(rows).to(gpu)].float().cpu().numpy()
+    check_bf16_output(ref, got)
+    c32 = linear.mxfp8_linear(x[rows].to(gpu), q, s, out_dtype=torch.float32).cpu().numpy()
+    rel = _max_rel(ref.astype(np.float64), c32)
+    print(f"cfg2 fp32-output max-rel {rel:.3e}", flush=True)
+    assert rel <= TOL
+
+
+def test_linear_rejects_bad_shapes(gpu):
+    x = torch.zeros(4, 96, dtype=torch.bfloat16, device=gpu)
+    q = torch.zeros(8, 96, dtype=torch.uint8, device=gpu)
+    s = torch.zeros(8, 3, dtype=torch.uint8, device=gpu)
+    with pytest.raises(ValueError, match="multiple of 64"):
+        linear.mxfp8_linear(x, q, s)
