@@ -95,6 +95,35 @@ int kq_pack_codes(const uint8_t* codes, int64_t n_codes, uint8_t* packed,
 int kq_decode_bytes(int table, const uint8_t* in, int64_t n, int out_dtype, void* out,
                     void* stream);
 
+/* ----------------------------------------------------------- MoE experts -- */
+
+/* Workspace bytes kq_moe_forward needs for these sizes (-1 on bad sizes). */
+int64_t kq_moe_workspace_size(int64_t tokens, int topk, int experts, int64_t hidden,
+                              int64_t inter);
+
+/* Routed MoE expert forward with MXFP4 expert weights (W4A16):
+ *   for every pair (t, s) with e = route_ids[t, s] in [0, experts):
+ *     g = x_t W13_e[0:I]^T, u = x_t W13_e[I:2I]^T        (fp32 accumulate)
+ *     a = bf16(act(g, u))          SiTU(beta, linear_beta) or SwiGLU
+ *     out_t += route_weights[t, s] * (a W2_e^T)          (fp32)
+ * which is scripts/closure_exl3_layer.py:557-598 (_reference_rank, tp = 1)
+ * with kquant/tp_simulator.py:83-94 (situ) and gate-first w13
+ * (closure_exl3_layer.py:420-423); ids outside [0, experts) contribute 0.
+ * x bf16 [tokens, hidden] (row stride ldx); route_ids int32 and
+ * route_weights fp32 [tokens, topk]; w13_q uint8 [experts, 2I, hidden/2],
+ * w13_scale [experts, 2I, hidden/32], w2_q [experts, hidden, I/2],
+ * w2_scale [experts, hidden, I/32]; out [tokens, hidden] bf16 or fp32.
+ * hidden % 512 == 0, I % 512 == 0, topk <= 64, experts <= 4096.
+ * workspace: >= kq_moe_workspace_size bytes, 256-byte aligned, caller owned;
+ * results are bitwise reproducible (no floating-point atomics). */
+int kq_moe_forward(int activation, float act_beta, float act_linear_beta,
+                   const void* x, int64_t ldx, int64_t tokens, int64_t hidden,
+                   const int32_t* route_ids, const float* route_weights, int topk,
+                   int experts, int64_t inter, const uint8_t* w13_q,
+                   const uint8_t* w13_scale, const uint8_t* w2_q, const uint8_t* w2_scale,
+                   int out_dtype, void* out, void* workspace, int64_t workspace_bytes,
+                   uint32_t flags, void* stream);
+
 /* --------------------------------------------------------- dense linear -- */
 
 /* C [m, n] = A [m, k] (bf16, row stride lda) x dequant(W)^T, W [n, k] in

@@ -52,6 +52,8 @@ SIGNATURES: dict[str, list] = {
     "kq_sym_lerp": [_VP, _F32, _VP, _I64, _F32, _VP, _VP],
     "kq_cov_stats": [_VP, _I64, _VP, _VP, _VP],
     "kq_mx_linear": [_INT, _VP, _I64, _VP, _VP, _I64, _I64, _I64, _INT, _VP, _I64, _VP],
+    "kq_moe_forward": [_INT, _F32, _F32, _VP, _I64, _I64, _I64, _VP, _VP, _INT, _INT, _I64,
+                       _VP, _VP, _VP, _VP, _INT, _VP, _VP, _I64, _U32, _VP],
 }
 COV_STATS_PARTS = 256
 
@@ -73,6 +75,8 @@ def library() -> ctypes.CDLL:
         lib.kq_version.argtypes = []
         lib.kq_last_error.restype = ctypes.c_char_p
         lib.kq_last_error.argtypes = []
+        lib.kq_moe_workspace_size.restype = ctypes.c_int64
+        lib.kq_moe_workspace_size.argtypes = [_I64, _INT, _INT, _I64, _I64]
         for name, argtypes in SIGNATURES.items():
             fn = getattr(lib, name)
             fn.restype = ctypes.c_int

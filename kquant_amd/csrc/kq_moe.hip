@@ -1,0 +1,588 @@
+// Routed MoE expert forward with MXFP4 weights (W4A16).
+//
+// Semantics: scripts/closure_exl3_layer.py:557-598 (_reference_rank, tp = 1):
+// for every (token, slot) pair routed to expert e,
+//   gate = x W1_e^T, up = x W3_e^T (w13 rows [0, I) gate, [I, 2I) up),
+//   a = act(gate, up) (SiTU kquant/tp_simulator.py:83-94, or SwiGLU), bf16,
+//   partial = a W2_e^T, contribution = route_weight * partial (fp32),
+//   out[token] = sum over its slots (fp32).
+//
+// Pipeline (all on one stream, all buffers in the caller's workspace):
+//   1. route_hist / route_scan / route_scatter: deterministic counting sort of
+//      the T*topk pairs by expert (stable in pair order), the list of experts
+//      with 1..16 pairs ("small") and the (expert, row-tile) list of the others.
+//   2. gate/up: small experts on a GEMV-shaped MFMA kernel (16 token slots,
+//      weights streamed once with 16-byte loads, K split over 4 waves);
+//      large experts on a 256x256-tile grouped GEMM (gathered token rows,
+//      packed weights in LDS).  Both fuse the activation and write bf16
+//      intermediates in expert-sorted order.
+//   3. down: same two shapes over W2; the epilogue scales by the route weight
+//      and writes one fp32 row per pair.
+//   4. combine: out[t] = sum of the topk pair rows in slot order.
+// No atomics touch floating-point data, so results are bitwise reproducible.
+#include "kq_gemm.h"
+#include "kq_internal.h"
+
+namespace kq {
+namespace moe {
+
+constexpr int SMALL_MAX = 16;        // pairs per expert handled by the GEMV path
+constexpr int PREP = 256;            // pairs per prep block
+constexpr int MAX_EXPERTS = 4096;
+constexpr int BM = 256, BN = 256, BK = 64, THREADS = 512;  // large tiles
+constexpr int A_ROW = BK * 2 + 16;
+constexpr int B_ROW = 36;            // 32 packed bytes + pad
+constexpr int A_BYTES = BM * A_ROW;
+constexpr int B_BYTES = BN * B_ROW;
+constexpr int S_BYTES = BN * 2;
+constexpr int STAGE = A_BYTES + B_BYTES + S_BYTES;
+constexpr int SMALL_CH = 64;         // output rows (channels) per GEMV workgroup
+
+struct Layout {
+  size_t counts, offsets, block_counts, sorted, small_list, large_tiles, meta, act, y, total;
+  int64_t pairs, nblk, max_small, max_large;
+};
+
+static inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+static Layout make_layout(int64_t tokens, int topk, int experts, int64_t hidden, int64_t inter) {
+  Layout L;
+  L.pairs = tokens * topk;
+  L.nblk = (L.pairs + PREP - 1) / PREP;
+  L.max_small = L.pairs < experts ? L.pairs : experts;
+  L.max_large = L.pairs / (SMALL_MAX + 1) + L.pairs / BM + 1;
+  size_t o = 0;
+  L.counts = o;       o = align256(o + sizeof(int) * experts);
+  L.offsets = o;      o = align256(o + sizeof(int) * (experts + 1));
+  L.block_counts = o; o = align256(o + sizeof(int) * (size_t)L.nblk * experts);
+  L.sorted = o;       o = align256(o + sizeof(int) * (size_t)L.pairs);
+  L.small_list = o;   o = align256(o + sizeof(int) * experts);
+  L.large_tiles = o;  o = align256(o + sizeof(int) * 2 * (size_t)L.max_large);
+  L.meta = o;         o = align256(o + sizeof(int) * 4);
+  L.act = o;          o = align256(o + 2 * (size_t)L.pairs * inter);
+  L.y = o;            o = align256(o + 4 * (size_t)L.pairs * hidden);
+  L.total = o;
+  return L;
+}
+
+// ------------------------------------------------------------ activations --
+struct ActParams {
+  int kind;       // KQ_ACT_SITU or KQ_ACT_SWIGLU
+  float beta;     // SiTU gate beta
+  float lbeta;    // SiTU linear beta
+};
+
+__device__ __forceinline__ float sigmoidf_(float v) { return 1.0f / (1.0f + expf(-v)); }
+
+__device__ __forceinline__ float activate(const ActParams& p, float g, float u) {
+  if (p.kind == KQ_ACT_SWIGLU) return g * sigmoidf_(g) * u;
+  const float gv = p.beta * tanhf(g / p.beta) * sigmoidf_(g);
+  const float uv = p.lbeta * tanhf(u / p.lbeta);
+  return gv * uv;
+}
+
+// ------------------------------------------------------------ routing prep --
+__global__ __launch_bounds__(PREP) void route_hist_kernel(const int* __restrict__ ids, int64_t pairs,
+                                                          int experts, int* __restrict__ block_counts) {
+  __shared__ int cnt[MAX_EXPERTS];
+  for (int e = threadIdx.x; e < experts; e += PREP) cnt[e] = 0;
+  __syncthreads();
+  const int64_t p = (int64_t)blockIdx.x * PREP + threadIdx.x;
+  if (p < pairs) {
+    const int e = ids[p];
+    if (e >= 0 && e < experts) atomicAdd(&cnt[e], 1);
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < experts; e += PREP)
+    block_counts[(int64_t)blockIdx.x * experts + e] = cnt[e];
+}
+
+// Exclusive scan of v[0..n) (n <= 4 * 1024) in place in LDS by 1024 threads;
+// returns the total.
+__device__ int block_exclusive_scan(int* v, int n, int* scratch /*[1024]*/) {
+  const int t = threadIdx.x;
+  int local[4];
+  int sum = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int idx = t * 4 + i;
+    local[i] = idx < n ? v[idx] : 0;
+    sum += local[i];
+  }
+  scratch[t] = sum;
+  __syncthreads();
+  for (int off = 1; off < 1024; off <<= 1) {
+    const int add = t >= off ? scratch[t - off] : 0;
+    __syncthreads();
+    scratch[t] += add;
+    __syncthreads();
+  }
+  int run = scratch[t] - sum;  // exclusive prefix of this thread's chunk
+  const int total = scratch[1023];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int idx = t * 4 + i;
+    if (idx < n) v[idx] = run;
+    run += local[i];
+  }
+  __syncthreads();
+  return total;
+}
+
+__global__ __launch_bounds__(1024) void route_scan_kernel(
+    int* __restrict__ block_counts, int nblk, int experts, int* __restrict__ counts,
+    int* __restrict__ offsets, int* __restrict__ small_list, int* __restrict__ large_tiles,
+    int* __restrict__ meta, int max_large) {
+  __shared__ int s_cnt[MAX_EXPERTS];
+  __shared__ int s_small[MAX_EXPERTS];
+  __shared__ int s_tiles[MAX_EXPERTS];
+  __shared__ int scratch[1024];
+  for (int e = threadIdx.x; e < experts; e += 1024) {
+    int s = 0;
+    for (int b = 0; b < nblk; ++b) {
+      const int c = block_counts[(int64_t)b * experts + e];
+      block_counts[(int64_t)b * experts + e] = s;
+      s += c;
+    }
+    counts[e] = s;
+    s_cnt[e] = s;
+    s_small[e] = (s >= 1 && s <= SMALL_MAX) ? 1 : 0;
+    s_tiles[e] = s > SMALL_MAX ? (s + BM - 1) / BM : 0;
+  }
+  __syncthreads();
+  const int npairs = block_exclusive_scan(s_cnt, experts, scratch);
+  const int nsmall = block_exclusive_scan(s_small, experts, scratch);
+  const int ntiles = block_exclusive_scan(s_tiles, experts, scratch);
+  for (int e = threadIdx.x; e < experts; e += 1024) {
+    offsets[e] = s_cnt[e];
+    const int n = counts[e];
+    if (n >= 1 && n <= SMALL_MAX) small_list[s_small[e]] = e;
+    if (n > SMALL_MAX) {
+      const int nt = (n + BM - 1) / BM;
+      for (int t = 0; t < nt; ++t) {
+        const int slot = s_tiles[e] + t;
+        if (slot < max_large) {
+          large_tiles[2 * slot] = e;
+          large_tiles[2 * slot + 1] = t * BM;
+        }
+      }
+    }
+  }
+  if (threadIdx.x == 0) {
+    offsets[experts] = npairs;
+    meta[0] = nsmall;
+    meta[1] = ntiles < max_large ? ntiles : max_large;
+    meta[2] = npairs;
+  }
+}
+
+__global__ __launch_bounds__(PREP) void route_scatter_kernel(
+    const int* __restrict__ ids, int64_t pairs, int experts, const int* __restrict__ offsets,
+    const int* __restrict__ block_counts, int* __restrict__ sorted) {
+  __shared__ int ex[PREP];
+  const int64_t p = (int64_t)blockIdx.x * PREP + threadIdx.x;
+  int e = p < pairs ? ids[p] : -1;
+  if (e < 0 || e >= experts) e = -1;
+  ex[threadIdx.x] = e;
+  __syncthreads();
+  if (e >= 0) {
+    int rank = 0;
+    for (int j = 0; j < (int)threadIdx.x; ++j) rank += ex[j] == e ? 1 : 0;
+    sorted[offsets[e] + block_counts[(int64_t)blockIdx.x * experts + e] + rank] = (int)p;
+  }
+}
+
+using gemm::bf16x8_t;
+using gemm::u32x2_t;
+using gemm::u32x4_t;
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+// ------------------------------------------------- GEMV-shaped small path --
+// One workgroup: one expert with n <= 16 pairs, SMALL_CH output rows (per
+// projection), 4 waves splitting K.  MFMA 16x16x32: token slot = A row, weight
+// row = B column.  Each lane streams one 16-byte (32-element, one E8M0 block)
+// piece of a weight row per 128-k step and feeds it to four MFMAs; the
+// k-order inside the step is permuted identically for A and B (a dot product
+// is invariant under a common permutation of k), so every weight byte is
+// loaded exactly once with a full-width load.
+//
+// GATEUP: rows of w13 (gate c, up I + c), output act -> bf16 intermediates.
+// !GATEUP: rows of w2, output route_weight * partial -> fp32 pair rows.
+template <bool GATEUP>
+__global__ __launch_bounds__(256) void moe_small_kernel(
+    const uint16_t* __restrict__ a, int64_t lda, int topk, const int* __restrict__ offsets,
+    const int* __restrict__ sorted, const int* __restrict__ small_list,
+    const int* __restrict__ meta, const uint8_t* __restrict__ wq, const uint8_t* __restrict__ ws,
+    int64_t rows_per_expert, int64_t K, int64_t inter, ActParams act, const float* __restrict__ route_w,
+    uint16_t* __restrict__ act_out, float* __restrict__ y_out, int64_t hidden) {
+  const int si = blockIdx.x;
+  if (si >= meta[0]) return;
+  const int e = small_list[si];
+  const int beg = offsets[e];
+  const int n = offsets[e + 1] - beg;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int m = lane & 15, g = lane >> 4;
+  const int64_t c0 = (int64_t)blockIdx.y * SMALL_CH;
+
+  // A row of this lane's token slot
+  const uint16_t* arow = nullptr;
+  if (m < n) {
+    const int pair = sorted[beg + m];
+    arow = GATEUP ? a + (int64_t)(pair / topk) * lda : a + (int64_t)(beg + m) * lda;
+  }
+  const int64_t kw = K / 2, ks = K / 32;
+  const uint8_t* wbase = wq + (int64_t)e * rows_per_expert * kw;
+  const uint8_t* sbase = ws + (int64_t)e * rows_per_expert * ks;
+  constexpr int NB = GATEUP ? 8 : 4;  // 16-row MFMA column blocks per wave
+  f32x4_t acc[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) acc[b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  const int64_t kper = K / 4;                       // k range of this wave
+  const int64_t kb0 = (wave * kper) / 32;           // first 32-block of the wave
+  const int steps = (int)(kper / 128);
+  for (int s = 0; s < steps; ++s) {
+    const int64_t kb = kb0 + 4 * s + g;             // this lane's 32-element block
+    u32x4_t wv[NB];
+    uint32_t sv[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      // GATEUP: blocks 0..3 gate rows c0 + 16b + m, blocks 4..7 up rows I + ...
+      const int64_t r = GATEUP ? (b < 4 ? c0 + 16 * b + m : inter + c0 + 16 * (b - 4) + m)
+                               : c0 + 16 * b + m;
+      wv[b] = *reinterpret_cast<const u32x4_t*>(wbase + r * kw + kb * 16);
+      sv[b] = sbase[r * ks + kb];
+    }
+    bf16x8_t av[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (arow) av[q] = *reinterpret_cast<const bf16x8_t*>(arow + kb * 32 + 8 * q);
+      else av[q] = __builtin_bit_cast(bf16x8_t, u32x4_t{0u, 0u, 0u, 0u});
+    }
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const bf16x8_t wb = gemm::dequant8<1>(u32x2_t{wv[b][q], 0u}, sv[b]);
+        acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[q], wb, acc[b], 0, 0, 0);
+      }
+    }
+  }
+
+  // reduce the 4 waves' partial sums through LDS
+  __shared__ f32x4_t red[4][NB][64];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) red[wave][b][lane] = acc[b];
+  __syncthreads();
+  if (wave != 0) return;
+#pragma unroll
+  for (int b = 0; b < NB; ++b) acc[b] = red[0][b][lane] + red[1][b][lane] + red[2][b][lane] + red[3][b][lane];
+
+  // D layout (16x16): lane holds rows (token slots) 4*(lane/16) + j, column lane % 16
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int slot = 4 * g + j;
+    if (slot >= n) continue;
+    if (GATEUP) {
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const float v = activate(act, acc[b][j], acc[b + 4][j]);
+        const int64_t ch = c0 + 16 * b + m;
+        reinterpret_cast<__bf16*>(act_out)[(int64_t)(beg + slot) * inter + ch] = (__bf16)v;
+      }
+    } else {
+      const int pair = sorted[beg + slot];
+      const float rw = route_w[pair];
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const int64_t h = c0 + 16 * b + m;
+        y_out[(int64_t)pair * hidden + h] = rw * acc[b][j];
+      }
+    }
+  }
+}
+
+// ------------------------------------------------ grouped GEMM large path --
+// Tile (expert, 256 sorted pair rows) x 256 weight rows, 8 waves of 64 x 128,
+// K step 64.  GATEUP: the 256 weight rows are 128 gate rows c0.. and the 128
+// matching up rows, so each wave holds gate (blocks 0,1) and up (blocks 2,3)
+// of the same channels and applies the activation in registers.
+template <bool GATEUP>
+__global__ __launch_bounds__(512, 1) void moe_large_kernel(
+    const uint16_t* __restrict__ a, int64_t lda, int topk, const int* __restrict__ offsets,
+    const int* __restrict__ sorted, const int* __restrict__ tiles, const int* __restrict__ meta,
+    const uint8_t* __restrict__ wq, const uint8_t* __restrict__ ws, int64_t rows_per_expert,
+    int64_t K, int64_t inter, ActParams act, const float* __restrict__ route_w,
+    uint16_t* __restrict__ act_out, float* __restrict__ y_out, int64_t hidden) {
+  const int ti = blockIdx.x;
+  if (ti >= meta[1]) return;
+  const int e = tiles[2 * ti], m0 = tiles[2 * ti + 1];
+  const int beg = offsets[e];
+  const int n = offsets[e + 1] - beg;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+  int* rowsrc = reinterpret_cast<int*>(lds + 2 * STAGE);  // A source row per tile row (-1: none)
+  if (tid < BM) {
+    const int slot = m0 + tid;
+    int src = -1;
+    if (slot < n) src = GATEUP ? sorted[beg + slot] / topk : beg + slot;
+    rowsrc[tid] = src;
+  }
+  __syncthreads();
+
+  const int64_t kw = K / 2, ks = K / 32;
+  const uint8_t* wbase = wq + (int64_t)e * rows_per_expert * kw;
+  const uint8_t* sbase = ws + (int64_t)e * rows_per_expert * ks;
+  const int64_t c0 = (int64_t)blockIdx.y * (GATEUP ? BN / 2 : BN);
+  auto wrow = [&](int r) -> int64_t {  // weight row of LDS B row r
+    if (GATEUP) return r < BN / 2 ? c0 + r : inter + c0 + (r - BN / 2);
+    return c0 + r;
+  };
+  const int64_t nrows = GATEUP ? 2 * inter : hidden;  // weight rows per expert
+
+  u32x4_t ra[4], rb;
+  uint32_t rs = 0;
+  auto load = [&](int64_t k0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int ch = tid + THREADS * i;
+      const int row = ch >> 3, col = (ch & 7) * 8;
+      const int src = rowsrc[row];
+      ra[i] = src >= 0 ? *reinterpret_cast<const u32x4_t*>(a + (int64_t)src * lda + k0 + col)
+                       : u32x4_t{0u, 0u, 0u, 0u};
+    }
+    {
+      const int row = tid >> 1, col = (tid & 1) * 16;
+      const int64_t r = wrow(row);
+      rb = r < nrows ? *reinterpret_cast<const u32x4_t*>(wbase + r * kw + k0 / 2 + col)
+                     : u32x4_t{0u, 0u, 0u, 0u};
+    }
+    if (tid < BN) {
+      const int64_t r = wrow(tid);
+      rs = r < nrows ? *reinterpret_cast<const uint16_t*>(sbase + r * ks + k0 / 32) : 0u;
+    }
+  };
+  auto store = [&](int buf) {
+    unsigned char* base = lds + buf * STAGE;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int ch = tid + THREADS * i;
+      const int row = ch >> 3, col = (ch & 7) * 16;
+      *reinterpret_cast<u32x4_t*>(base + row * A_ROW + col) = ra[i];
+    }
+    {
+      const int row = tid >> 1, col = (tid & 1) * 16;
+#pragma unroll
+      for (int d = 0; d < 4; ++d)
+        *reinterpret_cast<uint32_t*>(base + A_BYTES + row * B_ROW + col + 4 * d) = rb[d];
+    }
+    if (tid < BN) *reinterpret_cast<uint16_t*>(base + A_BYTES + B_BYTES + tid * 2) = (uint16_t)rs;
+  };
+
+  const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+  float16_t acc[2][4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+  const int frow = lane & 31, fk = lane >> 5;
+  // B row of MFMA column block j for this wave
+  auto brow = [&](int j) -> int {
+    if (GATEUP) return (j < 2 ? 0 : BN / 2) + wn + (j & 1) * 32 + frow;
+    return 2 * wn + j * 32 + frow;
+  };
+
+  const int steps = (int)(K / BK);
+  load(0);
+  store(0);
+  __syncthreads();
+  for (int s = 0; s < steps; ++s) {
+    const int buf = s & 1;
+    if (s + 1 < steps) load((int64_t)(s + 1) * BK);
+    const unsigned char* base = lds + buf * STAGE;
+    const unsigned char* bb = base + A_BYTES;
+    const unsigned char* sb = bb + B_BYTES;
+#pragma unroll
+    for (int kk = 0; kk < BK / 16; ++kk) {
+      bf16x8_t fa[2], fb[4];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        fa[i] = *reinterpret_cast<const bf16x8_t*>(base + (wm + i * 32 + frow) * A_ROW + kk * 32 + fk * 16);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int r = brow(j);
+        u32x2_t w;
+        w[0] = *reinterpret_cast<const uint32_t*>(bb + r * B_ROW + kk * 8 + fk * 4);
+        w[1] = 0u;
+        fb[j] = gemm::dequant8<1>(w, sb[r * 2 + (kk >> 1)]);
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+    }
+    if (s + 1 < steps) store(buf ^ 1);
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = wm + i * 32 + 8 * (r >> 2) + 4 * fk + (r & 3);
+      const int slot = m0 + row;
+      if (slot >= n) continue;
+      if (GATEUP) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const float v = activate(act, acc[i][j][r], acc[i][j + 2][r]);
+          const int64_t ch = c0 + wn + j * 32 + frow;
+          if (ch < inter)
+            reinterpret_cast<__bf16*>(act_out)[(int64_t)(beg + slot) * inter + ch] = (__bf16)v;
+        }
+      } else {
+        const int pair = sorted[beg + slot];
+        const float rw = route_w[pair];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int64_t h = c0 + 2 * wn + j * 32 + frow;
+          if (h < hidden) y_out[(int64_t)pair * hidden + h] = rw * acc[i][j][r];
+        }
+      }
+    }
+}
+
+// ---------------------------------------------------------------- combine --
+template <int OUT>
+__global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restrict__ y,
+                                                          const int* __restrict__ ids, int topk,
+                                                          int experts, int64_t hidden,
+                                                          void* __restrict__ out) {
+  const int64_t t = blockIdx.y;
+  const int64_t h4 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (h4 >= hidden) return;
+  f32x4_t s = {0.f, 0.f, 0.f, 0.f};
+  for (int k = 0; k < topk; ++k) {
+    const int e = ids[t * topk + k];
+    if (e < 0 || e >= experts) continue;
+    s += *reinterpret_cast<const f32x4_t*>(y + (t * topk + k) * hidden + h4);
+  }
+  if (OUT == 2) {
+    *reinterpret_cast<f32x4_t*>(static_cast<float*>(out) + t * hidden + h4) = s;
+  } else {
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    u32x2 o = {f32x2_to_bf16x2_bits(s[0], s[1]), f32x2_to_bf16x2_bits(s[2], s[3])};
+    *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(out) + t * hidden + h4) = o;
+  }
+}
+
+}  // namespace moe
+}  // namespace kq
+
+using namespace kq;
+using namespace kq::moe;
+
+extern "C" int64_t kq_moe_workspace_size(int64_t tokens, int topk, int experts, int64_t hidden,
+                                         int64_t inter) {
+  if (tokens < 0 || topk <= 0 || experts <= 0 || hidden <= 0 || inter <= 0) return -1;
+  return (int64_t)make_layout(tokens, topk, experts, hidden, inter).total;
+}
+
+extern "C" int kq_moe_forward(int activation, float act_beta, float act_linear_beta,
+                              const void* x, int64_t ldx, int64_t tokens, int64_t hidden,
+                              const int32_t* route_ids, const float* route_weights, int topk,
+                              int experts, int64_t inter, const uint8_t* w13_q,
+                              const uint8_t* w13_scale, const uint8_t* w2_q,
+                              const uint8_t* w2_scale, int out_dtype, void* out,
+                              void* workspace, int64_t workspace_bytes, uint32_t flags,
+                              void* stream) {
+  (void)flags;
+  if (activation != KQ_ACT_SITU && activation != KQ_ACT_SWIGLU)
+    return kq_fail(KQ_ERR_INVALID, "kq_moe_forward: unknown activation %d", activation);
+  if (out_dtype != KQ_DT_BF16 && out_dtype != KQ_DT_F32)
+    return kq_fail(KQ_ERR_INVALID, "kq_moe_forward: output dtype must be bf16 or f32");
+  if (tokens < 0 || topk <= 0 || topk > 64 || experts <= 0 || experts > MAX_EXPERTS)
+    return kq_fail(KQ_ERR_INVALID, "kq_moe_forward: need tokens >= 0, 1 <= topk <= 64, 1 <= experts <= %d",
+                   MAX_EXPERTS);
+  if (hidden <= 0 || inter <= 0 || hidden % 512 != 0 || inter % 512 != 0)
+    return kq_fail(KQ_ERR_INVALID,
+                   "kq_moe_forward: hidden and intermediate sizes must be multiples of 512 "
+                   "(hidden=%lld inter=%lld)", (long long)hidden, (long long)inter);
+  if (ldx < hidden || ldx % 8 != 0)
+    return kq_fail(KQ_ERR_INVALID, "kq_moe_forward: ldx must be >= hidden and a multiple of 8");
+  if (kq_misaligned(x, 16) || kq_misaligned(w13_q, 16) || kq_misaligned(w2_q, 16) ||
+      kq_misaligned(w13_scale, 2) || kq_misaligned(w2_scale, 2) || kq_misaligned(workspace, 256) ||
+      kq_misaligned(out, 16))
+    return kq_fail(KQ_ERR_INVALID, "kq_moe_forward: misaligned buffer");
+  if (tokens * topk > INT32_MAX / 2)
+    return kq_fail(KQ_ERR_LIMIT, "kq_moe_forward: too many routed pairs");
+  const Layout L = make_layout(tokens, topk, experts, hidden, inter);
+  if (workspace_bytes < (int64_t)L.total)
+    return kq_fail(KQ_ERR_INVALID, "kq_moe_forward: workspace of %lld bytes < required %lld",
+                   (long long)workspace_bytes, (long long)L.total);
+  if (tokens == 0) return KQ_OK;
+  hipStream_t st = (hipStream_t)stream;
+  unsigned char* w = (unsigned char*)workspace;
+  int* counts = (int*)(w + L.counts);
+  int* offsets = (int*)(w + L.offsets);
+  int* block_counts = (int*)(w + L.block_counts);
+  int* sorted = (int*)(w + L.sorted);
+  int* small_list = (int*)(w + L.small_list);
+  int* large_tiles = (int*)(w + L.large_tiles);
+  int* meta = (int*)(w + L.meta);
+  uint16_t* act = (uint16_t*)(w + L.act);
+  float* y = (float*)(w + L.y);
+  const ActParams ap{activation, act_beta, act_linear_beta};
+  hipError_t e;
+
+  route_hist_kernel<<<(unsigned)L.nblk, PREP, 0, st>>>(route_ids, L.pairs, experts, block_counts);
+  if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_moe_forward/hist");
+  route_scan_kernel<<<1, 1024, 0, st>>>(block_counts, (int)L.nblk, experts, counts, offsets,
+                                        small_list, large_tiles, meta, (int)L.max_large);
+  if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_moe_forward/scan");
+  route_scatter_kernel<<<(unsigned)L.nblk, PREP, 0, st>>>(route_ids, L.pairs, experts, offsets,
+                                                          block_counts, sorted);
+  if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_moe_forward/scatter");
+
+  const uint16_t* xb = (const uint16_t*)x;
+  // gate/up
+  moe_small_kernel<true><<<dim3((unsigned)L.max_small, (unsigned)(inter / SMALL_CH)), 256, 0, st>>>(
+      xb, ldx, topk, offsets, sorted, small_list, meta, w13_q, w13_scale, 2 * inter, hidden, inter,
+      ap, route_weights, act, y, hidden);
+  if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_moe_forward/gateup_small");
+  const size_t lds = 2 * (size_t)STAGE + BM * sizeof(int);
+  const bool any_large = L.pairs > SMALL_MAX;
+  if (any_large) {
+    e = hipFuncSetAttribute((const void*)moe_large_kernel<true>,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e == hipSuccess)
+      e = hipFuncSetAttribute((const void*)moe_large_kernel<false>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return kq_check_launch(e, "kq_moe_forward/attr");
+    moe_large_kernel<true><<<dim3((unsigned)L.max_large, (unsigned)(inter / (BN / 2))), THREADS, lds, st>>>(
+        xb, ldx, topk, offsets, sorted, large_tiles, meta, w13_q, w13_scale, 2 * inter, hidden,
+        inter, ap, route_weights, act, y, hidden);
+    if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_moe_forward/gateup_large");
+  }
+  // down
+  moe_small_kernel<false><<<dim3((unsigned)L.max_small, (unsigned)(hidden / SMALL_CH)), 256, 0, st>>>(
+      act, inter, topk, offsets, sorted, small_list, meta, w2_q, w2_scale, hidden, inter, inter, ap,
+      route_weights, act, y, hidden);
+  if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_moe_forward/down_small");
+  if (any_large) {
+    moe_large_kernel<false><<<dim3((unsigned)L.max_large, (unsigned)((hidden + BN - 1) / BN)), THREADS, lds, st>>>(
+        act, inter, topk, offsets, sorted, large_tiles, meta, w2_q, w2_scale, hidden, inter, inter,
+        ap, route_weights, act, y, hidden);
+    if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_moe_forward/down_large");
+  }
+  // combine
+  const dim3 cgrid((unsigned)((hidden / 4 + 255) / 256), (unsigned)tokens);
+  if (out_dtype == KQ_DT_F32)
+    moe_combine_kernel<2><<<cgrid, 256, 0, st>>>(y, route_ids, topk, experts, hidden, out);
+  else
+    moe_combine_kernel<0><<<cgrid, 256, 0, st>>>(y, route_ids, topk, experts, hidden, out);
+  return kq_check_launch(hipGetLastError(), "kq_moe_forward/combine");
+}

@@ -123,3 +123,35 @@ def syrk_flops(rows: int, k: int) -> float:
 
 def log2_ceil(x: float) -> int:
     return int(math.ceil(math.log2(x)))
+
+
+def quantized_experts(
+    needed,
+    experts: int = EXPERTS,
+    hidden: int = HIDDEN,
+    inter: int = INTER,
+    seed: int = 0,
+    std: float = 0.02,
+    device: torch.device | str = "cuda",
+):
+    """MXFP4 expert weights produced by the MXFP4 quantizer from N(0, std).
+
+    Returns (w13_packed [E, 2I, H/2], w13_scale [E, 2I, H/32], w2_packed
+    [E, H, I/2], w2_scale [E, H, I/32]) on ``device``.  Only the experts in
+    ``needed`` are generated (each from its own seeded generator, so a
+    subset reproduces the same bytes); the others are zero.
+    """
+    from .mxfp4 import mxfp4_quantize
+
+    device = torch.device(device)
+    w13q = torch.zeros(experts, 2 * inter, hidden // 2, dtype=torch.uint8, device=device)
+    w13s = torch.zeros(experts, 2 * inter, hidden // 32, dtype=torch.uint8, device=device)
+    w2q = torch.zeros(experts, hidden, inter // 2, dtype=torch.uint8, device=device)
+    w2s = torch.zeros(experts, hidden, inter // 32, dtype=torch.uint8, device=device)
+    for e in sorted({int(v) for v in needed}):
+        g = torch.Generator(device=device).manual_seed(seed * 100003 + e)
+        w13 = (torch.randn(2 * inter, hidden, generator=g, device=device) * std).to(torch.bfloat16)
+        w2 = (torch.randn(hidden, inter, generator=g, device=device) * std).to(torch.bfloat16)
+        w13q[e], w13s[e] = mxfp4_quantize(w13)
+        w2q[e], w2s[e] = mxfp4_quantize(w2)
+    return w13q, w13s, w2q, w2s
