@@ -18,6 +18,9 @@ from ._build import LIB_PATH
 
 # enums of include/kquant_amd.h
 KQ_OK = 0
+KQ_ERR_INVALID = -1
+KQ_ERR_HIP = -2
+KQ_ERR_LIMIT = -3
 FMT_MXFP8_E4M3 = 0
 FMT_MXFP4_E2M1 = 1
 DT_BF16 = 0
