@@ -157,13 +157,13 @@ def main() -> int:
     if not args.quick and want("moe_prefill"):
         ids, rw = workloads.zipf_routing(8192)
         active = torch.unique(ids).tolist()
-        weights = workloads.quantized_experts(active, device=dev)
+        weights = moe.prepare_expert_weights(*workloads.quantized_experts(active, device=dev))
         x3 = (torch.randn(8192, workloads.HIDDEN, generator=torch.Generator().manual_seed(6))
               .to(torch.bfloat16).to(dev))
         ids_d, rw_d = ids.to(dev), rw.to(dev)
 
         def moe_step():
-            moe.grouped_expert_forward(x3, ids_d, rw_d, *weights)
+            moe.grouped_expert_forward(x3, ids_d, rw_d, weights)
 
         t_moe = _time_loop(torch, moe_step, max(3, args.steps // 10), 2)
         flops = workloads.moe_flops(ids.numel())
@@ -187,12 +187,12 @@ def main() -> int:
         for tokens in (1, 4, 16):
             ids, rw = workloads.random_routing(tokens, seed=tokens)
             active = torch.unique(ids).tolist()
-            weights = workloads.quantized_experts(active, device=dev)
+            weights = moe.prepare_expert_weights(*workloads.quantized_experts(active, device=dev))
             x5 = torch.randn(tokens, workloads.HIDDEN, generator=torch.Generator().manual_seed(5)).to(torch.bfloat16).to(dev)
             ids_d, rw_d = ids.to(dev), rw.to(dev)
 
             def dec_step():
-                moe.grouped_expert_forward(x5, ids_d, rw_d, *weights)
+                moe.grouped_expert_forward(x5, ids_d, rw_d, weights)
 
             t = _time_loop(torch, dec_step, max(10, args.steps), 5)
             nbytes = len(active) * workloads.bytes_per_expert() + tokens * workloads.HIDDEN * 2

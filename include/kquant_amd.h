@@ -77,6 +77,28 @@ int kq_mx_dequant(int fmt, const void* q, const uint8_t* scale, int64_t rows,
                   int64_t k, int out_dtype, void* out, uint32_t flags,
                   void* stream);
 
+/* Split a bf16/f16 [rows, k] matrix into two MXFP8 parts: hi = the MXFP8
+ * quantization of x (the kq_mx_quantize rule and bytes), lo = the MXFP8
+ * quantization of the fp32 residual x - dequant(hi).  dequant(hi) +
+ * dequant(lo) reproduces bf16 inputs (all but ~3e-5 of N(0,1) elements
+ * exactly, the rest within 2^-22 of their block maximum), which lets a
+ * GEMM run bf16 activations on the block-scaled fp8 MFMA.  No kquant
+ * counterpart: it is the operand format of kq_moe_forward's GEMV path.
+ * out_hi / out_lo: uint8 [rows, k]; scale_hi / scale_lo: uint8 [rows, k/32]. */
+int kq_mx_split_quantize(int in_dtype, const void* in, int64_t ld_in, int64_t rows, int64_t k,
+                         uint8_t* out_hi, uint8_t* out_lo, uint8_t* scale_hi, uint8_t* scale_lo,
+                         void* stream);
+
+/* Repack `mats` MXFP4 matrices (packed [rows, k/2] + E8M0 [rows, k/32] each,
+ * stacked) into the MFMA-tiled layout kq_moe_forward reads: per matrix,
+ * 1 KiB tiles [rows/16][k/128] with tile byte 16*l + j = packed[16 rg + l%16]
+ * [64 c + 16 (l/16) + j], and 64-byte scale tiles with byte l =
+ * scale[16 rg + l%16][4 c + l/16].  A one-time weight preparation (the role
+ * of the external kernel's prepare_weights in scripts/closure_exl3_layer.py:
+ * 412-443); same bytes, permuted.  rows % 16 == 0, k % 128 == 0. */
+int kq_mx_tile_weights(const uint8_t* q, const uint8_t* scale, int64_t mats, int64_t rows,
+                       int64_t k, uint8_t* q_tiled, uint8_t* scale_tiled, void* stream);
+
 /* Nibble codes <-> packed bytes, kquant/io/mxfp4.py:19-38 (unpack_codes,
  * pack_codes): byte = lo | hi << 4 (mod 256), lo = the even index; codes are
  * OR-ed as whole bytes exactly as the reference does.  n_codes is even. */
@@ -110,17 +132,18 @@ int64_t kq_moe_workspace_size(int64_t tokens, int topk, int experts, int64_t hid
  * with kquant/tp_simulator.py:83-94 (situ) and gate-first w13
  * (closure_exl3_layer.py:420-423); ids outside [0, experts) contribute 0.
  * x bf16 [tokens, hidden] (row stride ldx); route_ids int32 and
- * route_weights fp32 [tokens, topk]; w13_q uint8 [experts, 2I, hidden/2],
- * w13_scale [experts, 2I, hidden/32], w2_q [experts, hidden, I/2],
- * w2_scale [experts, hidden, I/32]; out [tokens, hidden] bf16 or fp32.
+ * route_weights fp32 [tokens, topk]; the weights in the kq_mx_tile_weights
+ * layout: w13_t / w13_st = tiles of the [experts, 2I, hidden] MXFP4 w13
+ * (gate rows first), w2_t / w2_st = tiles of [experts, hidden, I];
+ * out [tokens, hidden] bf16 or fp32.
  * hidden % 512 == 0, I % 512 == 0, topk <= 64, experts <= 4096.
  * workspace: >= kq_moe_workspace_size bytes, 256-byte aligned, caller owned;
  * results are bitwise reproducible (no floating-point atomics). */
 int kq_moe_forward(int activation, float act_beta, float act_linear_beta,
                    const void* x, int64_t ldx, int64_t tokens, int64_t hidden,
                    const int32_t* route_ids, const float* route_weights, int topk,
-                   int experts, int64_t inter, const uint8_t* w13_q,
-                   const uint8_t* w13_scale, const uint8_t* w2_q, const uint8_t* w2_scale,
+                   int experts, int64_t inter, const uint8_t* w13_t,
+                   const uint8_t* w13_st, const uint8_t* w2_t, const uint8_t* w2_st,
                    int out_dtype, void* out, void* workspace, int64_t workspace_bytes,
                    uint32_t flags, void* stream);
 

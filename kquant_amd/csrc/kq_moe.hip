@@ -36,10 +36,10 @@ constexpr int A_BYTES = BM * A_ROW;
 constexpr int B_BYTES = BN * B_ROW;
 constexpr int S_BYTES = BN * 2;
 constexpr int STAGE = A_BYTES + B_BYTES + S_BYTES;
-constexpr int SMALL_CH = 64;         // output rows (channels) per GEMV workgroup
 
 struct Layout {
-  size_t counts, offsets, block_counts, sorted, small_list, large_tiles, meta, act, y, total;
+  size_t counts, offsets, block_counts, sorted, small_list, large_tiles, meta, act, y;
+  size_t xs_hi, xs_lo, xs_shi, xs_slo, as_hi, as_lo, as_shi, as_slo, total;
   int64_t pairs, nblk, max_small, max_large;
 };
 
@@ -61,6 +61,15 @@ static Layout make_layout(int64_t tokens, int topk, int experts, int64_t hidden,
   L.meta = o;         o = align256(o + sizeof(int) * 4);
   L.act = o;          o = align256(o + 2 * (size_t)L.pairs * inter);
   L.y = o;            o = align256(o + 4 * (size_t)L.pairs * hidden);
+  // MXFP8 hi/lo split of the tokens and of the intermediates (small path)
+  L.xs_hi = o;        o = align256(o + (size_t)tokens * hidden);
+  L.xs_lo = o;        o = align256(o + (size_t)tokens * hidden);
+  L.xs_shi = o;       o = align256(o + (size_t)tokens * hidden / 32);
+  L.xs_slo = o;       o = align256(o + (size_t)tokens * hidden / 32);
+  L.as_hi = o;        o = align256(o + (size_t)L.pairs * inter);
+  L.as_lo = o;        o = align256(o + (size_t)L.pairs * inter);
+  L.as_shi = o;       o = align256(o + (size_t)L.pairs * inter / 32);
+  L.as_slo = o;       o = align256(o + (size_t)L.pairs * inter / 32);
   L.total = o;
   return L;
 }
@@ -168,6 +177,7 @@ __global__ __launch_bounds__(1024) void route_scan_kernel(
       }
     }
   }
+  for (int i = nsmall + (int)threadIdx.x; i < experts; i += 1024) small_list[i] = -1;
   if (threadIdx.x == 0) {
     offsets[experts] = npairs;
     meta[0] = nsmall;
@@ -192,91 +202,236 @@ __global__ __launch_bounds__(PREP) void route_scatter_kernel(
   }
 }
 
+// Whole routing prep in one workgroup for up to PREP_ONE pairs: histogram,
+// scans and the stable scatter (rank = earlier pairs with the same expert).
+constexpr int PREP_ONE = 1024;
+__global__ __launch_bounds__(1024) void route_prep_one_kernel(
+    const int* __restrict__ ids, int pairs, int experts, int* __restrict__ counts,
+    int* __restrict__ offsets, int* __restrict__ sorted, int* __restrict__ small_list,
+    int* __restrict__ large_tiles, int* __restrict__ meta, int max_large) {
+  __shared__ int s_cnt[MAX_EXPERTS];
+  __shared__ int s_small[MAX_EXPERTS];
+  __shared__ int s_tiles[MAX_EXPERTS];
+  __shared__ int s_ids[PREP_ONE];
+  __shared__ int scratch[1024];
+  const int t = threadIdx.x;
+  for (int e = t; e < experts; e += 1024) s_cnt[e] = 0;
+  int my = -1;
+  if (t < pairs) {
+    my = ids[t];
+    if (my < 0 || my >= experts) my = -1;
+  }
+  s_ids[t] = my;
+  __syncthreads();
+  if (my >= 0) atomicAdd(&s_cnt[my], 1);
+  __syncthreads();
+  for (int e = t; e < experts; e += 1024) {
+    const int c = s_cnt[e];
+    counts[e] = c;
+    s_small[e] = (c >= 1 && c <= SMALL_MAX) ? 1 : 0;
+    s_tiles[e] = c > SMALL_MAX ? (c + BM - 1) / BM : 0;
+  }
+  __syncthreads();
+  const int npairs = block_exclusive_scan(s_cnt, experts, scratch);
+  const int nsmall = block_exclusive_scan(s_small, experts, scratch);
+  const int ntiles = block_exclusive_scan(s_tiles, experts, scratch);
+  for (int e = t; e < experts; e += 1024) {
+    offsets[e] = s_cnt[e];
+    const int c = counts[e];
+    if (c >= 1 && c <= SMALL_MAX) small_list[s_small[e]] = e;
+    if (c > SMALL_MAX) {
+      const int nt = (c + BM - 1) / BM;
+      for (int k = 0; k < nt; ++k) {
+        const int slot = s_tiles[e] + k;
+        if (slot < max_large) {
+          large_tiles[2 * slot] = e;
+          large_tiles[2 * slot + 1] = k * BM;
+        }
+      }
+    }
+  }
+  if (my >= 0) {
+    int rank = 0;
+    for (int j = 0; j < t; ++j) rank += s_ids[j] == my ? 1 : 0;
+    sorted[s_cnt[my] + rank] = t;
+  }
+  for (int i = nsmall + t; i < experts; i += 1024) small_list[i] = -1;
+  if (t == 0) {
+    offsets[experts] = npairs;
+    meta[0] = nsmall;
+    meta[1] = ntiles < max_large ? ntiles : max_large;
+    meta[2] = npairs;
+  }
+}
+
 using gemm::bf16x8_t;
 using gemm::u32x2_t;
 using gemm::u32x4_t;
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 // ------------------------------------------------- GEMV-shaped small path --
-// One workgroup: one expert with n <= 16 pairs, SMALL_CH output rows (per
-// projection), 4 waves splitting K.  MFMA 16x16x32: token slot = A row, weight
-// row = B column.  Each lane streams one 16-byte (32-element, one E8M0 block)
-// piece of a weight row per 128-k step and feeds it to four MFMAs; the
-// k-order inside the step is permuted identically for A and B (a dot product
-// is invariant under a common permutation of k), so every weight byte is
-// loaded exactly once with a full-width load.
+// One workgroup: one expert with n <= 16 pairs and CH output rows per
+// projection; WAVES waves split K.  The packed MXFP4 weights go straight into
+// the block-scaled MFMA v_mfma_scale_f32_16x16x128_f8f6f4 (B = E2M1, its E8M0
+// scale per 32-element block) with no dequantization: lane (n, g) of a
+// 16x16x128 step holds the 16 packed bytes of weight row n, k-block g, which
+// is exactly the checkpoint layout, so every weight byte is read once with a
+// 16-byte load.  The A operand is the activation split into two MXFP8 parts
+// (hi + residual lo, kq_mx_split_quantize), two MFMAs per step, which
+// reproduces the bf16 activation.  A lane (m, g) holds A bytes
+// k = 16g + i (i < 16) and 64 + 16g + (i - 16) of its token row and supplies
+// the E8M0 scale of block g.  Loads run two 128-k steps ahead of the MFMAs.
 //
 // GATEUP: rows of w13 (gate c, up I + c), output act -> bf16 intermediates.
 // !GATEUP: rows of w2, output route_weight * partial -> fp32 pair rows.
-template <bool GATEUP>
-__global__ __launch_bounds__(256) void moe_small_kernel(
-    const uint16_t* __restrict__ a, int64_t lda, int topk, const int* __restrict__ offsets,
-    const int* __restrict__ sorted, const int* __restrict__ small_list,
-    const int* __restrict__ meta, const uint8_t* __restrict__ wq, const uint8_t* __restrict__ ws,
-    int64_t rows_per_expert, int64_t K, int64_t inter, ActParams act, const float* __restrict__ route_w,
-    uint16_t* __restrict__ act_out, float* __restrict__ y_out, int64_t hidden) {
-  const int si = blockIdx.x;
-  if (si >= meta[0]) return;
-  const int e = small_list[si];
-  const int beg = offsets[e];
-  const int n = offsets[e + 1] - beg;
+typedef int i32x8_t __attribute__((ext_vector_type(8)));
+
+template <bool GATEUP, int CH, int WAVES, int STEPS>
+__global__ __launch_bounds__(WAVES * 64) void moe_small_kernel(
+    const uint8_t* __restrict__ ahi, const uint8_t* __restrict__ alo,
+    const uint8_t* __restrict__ ashi, const uint8_t* __restrict__ aslo, int topk,
+    const int* __restrict__ offsets, const int* __restrict__ sorted,
+    const int* __restrict__ small_list, const uint8_t* __restrict__ wt,
+    const uint8_t* __restrict__ wst, int64_t rows_per_expert, int64_t K, int64_t inter,
+    ActParams act, const float* __restrict__ route_w, uint16_t* __restrict__ act_out,
+    float* __restrict__ y_out, int64_t hidden) {
+  constexpr int NBP = CH / 16;                    // 16-row blocks per projection
+  constexpr int NB = GATEUP ? 2 * NBP : NBP;      // blocks per wave
+  const int e = small_list[blockIdx.x];           // -1 past the last small expert
+  if (e < 0) return;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int m = lane & 15, g = lane >> 4;
-  const int64_t c0 = (int64_t)blockIdx.y * SMALL_CH;
+  const int64_t c0 = (int64_t)blockIdx.y * CH;
 
-  // A row of this lane's token slot
-  const uint16_t* arow = nullptr;
-  if (m < n) {
-    const int pair = sorted[beg + m];
-    arow = GATEUP ? a + (int64_t)(pair / topk) * lda : a + (int64_t)(beg + m) * lda;
+  // weight tiles (kq_mx_tile_weights layout): [expert][row group][chunk][1 KiB]
+  const int64_t nchunk = K / 128;
+  const int64_t rgs = rows_per_expert / 16;
+  const int64_t kper = K / WAVES;                 // k range of this wave
+  const int64_t c_first = (wave * kper) / 128;    // first 128-k chunk of the wave
+  const int steps = (int)(kper / 128);
+  const uint8_t* wtile[NB];
+  const uint8_t* stile[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    const int64_t rg = GATEUP ? (b < NBP ? c0 / 16 + b : inter / 16 + c0 / 16 + (b - NBP)) : c0 / 16 + b;
+    const int64_t t0 = ((int64_t)e * rgs + rg) * nchunk + c_first;
+    wtile[b] = wt + t0 * 1024 + 16 * lane;
+    stile[b] = wst + t0 * 64 + lane;
   }
-  const int64_t kw = K / 2, ks = K / 32;
-  const uint8_t* wbase = wq + (int64_t)e * rows_per_expert * kw;
-  const uint8_t* sbase = ws + (int64_t)e * rows_per_expert * ks;
-  constexpr int NB = GATEUP ? 8 : 4;  // 16-row MFMA column blocks per wave
+  struct WBuf {
+    u32x4_t w[NB];
+    uint32_t ws[NB];
+  };
+  struct ABuf {
+    u32x4_t h0, h1, l0, l1;
+    uint32_t sh, sl;
+  };
+  auto load_w = [&](int s, WBuf& B) {
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      B.w[b] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(wtile[b] + (int64_t)s * 1024));
+      B.ws[b] = stile[b][(int64_t)s * 64];
+    }
+  };
+  // Issue the first weight loads before the dependent token-index loads.
+  WBuf w0, w1, w2;
+  if constexpr (STEPS > 0) {
+    load_w(0, w0);
+    if (STEPS > 1) load_w(1, w1);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  const int beg = offsets[e];
+  const int n = offsets[e + 1] - beg;
+  // A row of this lane's token slot.  Slots past n re-read slot 0 (always
+  // valid, n >= 1): MFMA output row m depends only on A row m and rows >= n
+  // are never stored, so the duplicate needs no masking, and the loads stay
+  // unconditional so the compiler keeps them in flight across steps.
+  const int mslot = m < n ? m : 0;
+  const int apair = sorted[beg + mslot];
+  const int64_t arow = GATEUP ? (int64_t)(apair / topk) : (int64_t)(beg + mslot);
+  const uint8_t* ah = ahi + arow * K;
+  const uint8_t* al = alo + arow * K;
+  const uint8_t* ash = ashi + arow * (K / 32);
+  const uint8_t* asl = aslo + arow * (K / 32);
+  auto load_a = [&](int s, ABuf& B) {
+    const int64_t c = c_first + s;                // 128-k chunk
+    B.h0 = *reinterpret_cast<const u32x4_t*>(ah + 128 * c + 16 * g);
+    B.h1 = *reinterpret_cast<const u32x4_t*>(ah + 128 * c + 64 + 16 * g);
+    B.l0 = *reinterpret_cast<const u32x4_t*>(al + 128 * c + 16 * g);
+    B.l1 = *reinterpret_cast<const u32x4_t*>(al + 128 * c + 64 + 16 * g);
+    B.sh = ash[4 * c + g];
+    B.sl = asl[4 * c + g];
+  };
   f32x4_t acc[NB];
 #pragma unroll
   for (int b = 0; b < NB; ++b) acc[b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
-  const int64_t kper = K / 4;                       // k range of this wave
-  const int64_t kb0 = (wave * kper) / 32;           // first 32-block of the wave
-  const int steps = (int)(kper / 128);
-  for (int s = 0; s < steps; ++s) {
-    const int64_t kb = kb0 + 4 * s + g;             // this lane's 32-element block
-    u32x4_t wv[NB];
-    uint32_t sv[NB];
+  auto compute = [&](const WBuf& W, const ABuf& A) {
+    const i32x8_t ah8 = __builtin_bit_cast(i32x8_t, (u32x4_t[2]){A.h0, A.h1});
+    const i32x8_t al8 = __builtin_bit_cast(i32x8_t, (u32x4_t[2]){A.l0, A.l1});
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
-      // GATEUP: blocks 0..3 gate rows c0 + 16b + m, blocks 4..7 up rows I + ...
-      const int64_t r = GATEUP ? (b < 4 ? c0 + 16 * b + m : inter + c0 + 16 * (b - 4) + m)
-                               : c0 + 16 * b + m;
-      wv[b] = *reinterpret_cast<const u32x4_t*>(wbase + r * kw + kb * 16);
-      sv[b] = sbase[r * ks + kb];
+      const i32x8_t w8 = i32x8_t{(int)W.w[b][0], (int)W.w[b][1], (int)W.w[b][2], (int)W.w[b][3], 0, 0, 0, 0};
+      acc[b] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ah8, w8, acc[b], 0, 4, 0, (int)A.sh, 0, (int)W.ws[b]);
+      acc[b] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(al8, w8, acc[b], 0, 4, 0, (int)A.sl, 0, (int)W.ws[b]);
     }
-    bf16x8_t av[4];
+  };
+  ABuf a0, a1, a2;
+  if constexpr (STEPS > 0) {
+    // Straight-line pipeline for a compile-time step count: three buffers,
+    // loads issued two steps ahead; with no loop the compiler counts the
+    // outstanding loads exactly and never waits for a prefetch early.
+    load_a(0, a0);
+    if (STEPS > 1) load_a(1, a1);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      if (arow) av[q] = *reinterpret_cast<const bf16x8_t*>(arow + kb * 32 + 8 * q);
-      else av[q] = __builtin_bit_cast(bf16x8_t, u32x4_t{0u, 0u, 0u, 0u});
-    }
-#pragma unroll
-    for (int b = 0; b < NB; ++b) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const bf16x8_t wb = gemm::dequant8<1>(u32x2_t{wv[b][q], 0u}, sv[b]);
-        acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[q], wb, acc[b], 0, 0, 0);
+    for (int s = 0; s < STEPS; ++s) {
+      if (s + 2 < STEPS) {
+        if ((s + 2) % 3 == 0) { load_w(s + 2, w0); load_a(s + 2, a0); }
+        else if ((s + 2) % 3 == 1) { load_w(s + 2, w1); load_a(s + 2, a1); }
+        else { load_w(s + 2, w2); load_a(s + 2, a2); }
       }
+      __builtin_amdgcn_sched_barrier(0);
+      if (s % 3 == 0) compute(w0, a0);
+      else if (s % 3 == 1) compute(w1, a1);
+      else compute(w2, a2);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  } else {
+    // Runtime step count: two alternating buffers; loads are never
+    // predicated (past the last step they re-read it, in bounds).
+    const int last = steps - 1;
+    load_w(0, w0);
+    load_a(0, a0);
+    for (int s = 0; s < steps; s += 2) {
+      const int s1 = s + 1 < last ? s + 1 : last, s2 = s + 2 < last ? s + 2 : last;
+      load_w(s1, w1);
+      load_a(s1, a1);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(w0, a0);
+      __builtin_amdgcn_sched_barrier(0);
+      load_w(s2, w0);
+      load_a(s2, a0);
+      __builtin_amdgcn_sched_barrier(0);
+      if (s + 1 < steps) compute(w1, a1);
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 
-  // reduce the 4 waves' partial sums through LDS
-  __shared__ f32x4_t red[4][NB][64];
+  // reduce the waves' partial sums through LDS; wave w finishes block w
+  __shared__ f32x4_t red[WAVES][NB][64];
 #pragma unroll
   for (int b = 0; b < NB; ++b) red[wave][b][lane] = acc[b];
   __syncthreads();
-  if (wave != 0) return;
+  if (wave >= NBP) return;
+  const int b = wave;
+  f32x4_t x0 = red[0][b][lane], x1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int b = 0; b < NB; ++b) acc[b] = red[0][b][lane] + red[1][b][lane] + red[2][b][lane] + red[3][b][lane];
+  for (int w = 1; w < WAVES; ++w) x0 += red[w][b][lane];
+  if (GATEUP) {
+    x1 = red[0][b + NBP][lane];
+#pragma unroll
+    for (int w = 1; w < WAVES; ++w) x1 += red[w][b + NBP][lane];
+  }
 
   // D layout (16x16): lane holds rows (token slots) 4*(lane/16) + j, column lane % 16
 #pragma unroll
@@ -284,20 +439,13 @@ __global__ __launch_bounds__(256) void moe_small_kernel(
     const int slot = 4 * g + j;
     if (slot >= n) continue;
     if (GATEUP) {
-#pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        const float v = activate(act, acc[b][j], acc[b + 4][j]);
-        const int64_t ch = c0 + 16 * b + m;
-        reinterpret_cast<__bf16*>(act_out)[(int64_t)(beg + slot) * inter + ch] = (__bf16)v;
-      }
+      const float v = activate(act, x0[j], x1[j]);
+      const int64_t ch = c0 + 16 * b + m;
+      reinterpret_cast<__bf16*>(act_out)[(int64_t)(beg + slot) * inter + ch] = (__bf16)v;
     } else {
       const int pair = sorted[beg + slot];
-      const float rw = route_w[pair];
-#pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        const int64_t h = c0 + 16 * b + m;
-        y_out[(int64_t)pair * hidden + h] = rw * acc[b][j];
-      }
+      const int64_t h = c0 + 16 * b + m;
+      y_out[(int64_t)pair * hidden + h] = route_w[pair] * x0[j];
     }
   }
 }
@@ -311,7 +459,7 @@ template <bool GATEUP>
 __global__ __launch_bounds__(512, 1) void moe_large_kernel(
     const uint16_t* __restrict__ a, int64_t lda, int topk, const int* __restrict__ offsets,
     const int* __restrict__ sorted, const int* __restrict__ tiles, const int* __restrict__ meta,
-    const uint8_t* __restrict__ wq, const uint8_t* __restrict__ ws, int64_t rows_per_expert,
+    const uint8_t* __restrict__ wt, const uint8_t* __restrict__ wst, int64_t rows_per_expert,
     int64_t K, int64_t inter, ActParams act, const float* __restrict__ route_w,
     uint16_t* __restrict__ act_out, float* __restrict__ y_out, int64_t hidden) {
   const int ti = blockIdx.x;
@@ -330,15 +478,14 @@ __global__ __launch_bounds__(512, 1) void moe_large_kernel(
   }
   __syncthreads();
 
-  const int64_t kw = K / 2, ks = K / 32;
-  const uint8_t* wbase = wq + (int64_t)e * rows_per_expert * kw;
-  const uint8_t* sbase = ws + (int64_t)e * rows_per_expert * ks;
+  // weights in the kq_mx_tile_weights layout: [expert][row group][chunk][1 KiB]
+  const int64_t nchunk = K / 128, rgs = rows_per_expert / 16;
   const int64_t c0 = (int64_t)blockIdx.y * (GATEUP ? BN / 2 : BN);
-  auto wrow = [&](int r) -> int64_t {  // weight row of LDS B row r
-    if (GATEUP) return r < BN / 2 ? c0 + r : inter + c0 + (r - BN / 2);
-    return c0 + r;
-  };
   const int64_t nrows = GATEUP ? 2 * inter : hidden;  // weight rows per expert
+  auto grow_group = [&](int lrg) -> int64_t {  // global row group of local group lrg (16 per tile)
+    if (GATEUP) return lrg < 8 ? c0 / 16 + lrg : inter / 16 + c0 / 16 + (lrg - 8);
+    return c0 / 16 + lrg;
+  };
 
   u32x4_t ra[4], rb;
   uint32_t rs = 0;
@@ -351,15 +498,23 @@ __global__ __launch_bounds__(512, 1) void moe_large_kernel(
       ra[i] = src >= 0 ? *reinterpret_cast<const u32x4_t*>(a + (int64_t)src * lda + k0 + col)
                        : u32x4_t{0u, 0u, 0u, 0u};
     }
+    const int64_t chunk = k0 / 128;
+    const int h = (int)((k0 / 64) & 1);  // which half of the 128-k tile this step reads
     {
-      const int row = tid >> 1, col = (tid & 1) * 16;
-      const int64_t r = wrow(row);
-      rb = r < nrows ? *reinterpret_cast<const u32x4_t*>(wbase + r * kw + k0 / 2 + col)
-                     : u32x4_t{0u, 0u, 0u, 0u};
+      // 16 local row groups x 32 lanes x 16 B: one contiguous 512 B half tile each
+      const int lrg = tid >> 5, l = h * 32 + (tid & 31);
+      const int64_t rg = grow_group(lrg);
+      rb = 16 * rg < nrows
+               ? *reinterpret_cast<const u32x4_t*>(wt + (((int64_t)e * rgs + rg) * nchunk + chunk) * 1024 + 16 * l)
+               : u32x4_t{0u, 0u, 0u, 0u};
     }
     if (tid < BN) {
-      const int64_t r = wrow(tid);
-      rs = r < nrows ? *reinterpret_cast<const uint16_t*>(sbase + r * ks + k0 / 32) : 0u;
+      // two scale bytes per thread: tile lanes l, l + 1 (rows 2q, 2q + 1 of the group)
+      const int lrg = tid >> 4, q = tid & 15, l = h * 32 + 2 * q;
+      const int64_t rg = grow_group(lrg);
+      rs = 16 * rg < nrows
+               ? *reinterpret_cast<const uint16_t*>(wst + (((int64_t)e * rgs + rg) * nchunk + chunk) * 64 + l)
+               : 0u;
     }
   };
   auto store = [&](int buf) {
@@ -371,12 +526,19 @@ __global__ __launch_bounds__(512, 1) void moe_large_kernel(
       *reinterpret_cast<u32x4_t*>(base + row * A_ROW + col) = ra[i];
     }
     {
-      const int row = tid >> 1, col = (tid & 1) * 16;
+      const int lrg = tid >> 5, l = tid & 31;  // lane within the half tile
+      const int row = 16 * lrg + (l & 15), col = 16 * (l >> 4);
 #pragma unroll
       for (int d = 0; d < 4; ++d)
         *reinterpret_cast<uint32_t*>(base + A_BYTES + row * B_ROW + col + 4 * d) = rb[d];
     }
-    if (tid < BN) *reinterpret_cast<uint16_t*>(base + A_BYTES + B_BYTES + tid * 2) = (uint16_t)rs;
+    if (tid < BN) {
+      const int lrg = tid >> 4, q = tid & 15;
+      const int j = q >> 3;                   // scale block within this step
+      unsigned char* sb = base + A_BYTES + B_BYTES;
+      sb[(16 * lrg + ((2 * q) & 15)) * 2 + j] = (unsigned char)(rs & 0xffu);
+      sb[(16 * lrg + ((2 * q + 1) & 15)) * 2 + j] = (unsigned char)(rs >> 8);
+    }
   };
 
   const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
@@ -485,6 +647,27 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restric
 using namespace kq;
 using namespace kq::moe;
 
+// Pick the small-path instantiation for a reduction length K: 8 waves with a
+// compile-time step count when K is a multiple of 1024 (K/1024 steps of 128
+// per wave, 1..8), else 4 waves with a runtime loop (K % 512 == 0).
+template <bool GATEUP, int CH, typename... Args>
+static hipError_t launch_small(dim3 grid, int64_t K, hipStream_t st, Args... args) {
+  const int64_t steps8 = K % 1024 == 0 ? K / 1024 : 0;
+  switch (steps8) {
+#define KQ_SMALL_CASE(S) \
+    case S: moe_small_kernel<GATEUP, CH, 8, S><<<grid, 512, 0, st>>>(args...); break;
+    KQ_SMALL_CASE(1) KQ_SMALL_CASE(2) KQ_SMALL_CASE(3) KQ_SMALL_CASE(4)
+    KQ_SMALL_CASE(5) KQ_SMALL_CASE(6) KQ_SMALL_CASE(7) KQ_SMALL_CASE(8)
+#undef KQ_SMALL_CASE
+    default:
+      if (steps8 > 0)
+        moe_small_kernel<GATEUP, CH, 8, 0><<<grid, 512, 0, st>>>(args...);
+      else
+        moe_small_kernel<GATEUP, CH, 4, 0><<<grid, 256, 0, st>>>(args...);
+  }
+  return hipGetLastError();
+}
+
 extern "C" int64_t kq_moe_workspace_size(int64_t tokens, int topk, int experts, int64_t hidden,
                                          int64_t inter) {
   if (tokens < 0 || topk <= 0 || experts <= 0 || hidden <= 0 || inter <= 0) return -1;
@@ -494,9 +677,9 @@ extern "C" int64_t kq_moe_workspace_size(int64_t tokens, int topk, int experts, 
 extern "C" int kq_moe_forward(int activation, float act_beta, float act_linear_beta,
                               const void* x, int64_t ldx, int64_t tokens, int64_t hidden,
                               const int32_t* route_ids, const float* route_weights, int topk,
-                              int experts, int64_t inter, const uint8_t* w13_q,
-                              const uint8_t* w13_scale, const uint8_t* w2_q,
-                              const uint8_t* w2_scale, int out_dtype, void* out,
+                              int experts, int64_t inter, const uint8_t* w13_t,
+                              const uint8_t* w13_st, const uint8_t* w2_t,
+                              const uint8_t* w2_st, int out_dtype, void* out,
                               void* workspace, int64_t workspace_bytes, uint32_t flags,
                               void* stream) {
   (void)flags;
@@ -513,8 +696,8 @@ extern "C" int kq_moe_forward(int activation, float act_beta, float act_linear_b
                    "(hidden=%lld inter=%lld)", (long long)hidden, (long long)inter);
   if (ldx < hidden || ldx % 8 != 0)
     return kq_fail(KQ_ERR_INVALID, "kq_moe_forward: ldx must be >= hidden and a multiple of 8");
-  if (kq_misaligned(x, 16) || kq_misaligned(w13_q, 16) || kq_misaligned(w2_q, 16) ||
-      kq_misaligned(w13_scale, 2) || kq_misaligned(w2_scale, 2) || kq_misaligned(workspace, 256) ||
+  if (kq_misaligned(x, 16) || kq_misaligned(w13_t, 16) || kq_misaligned(w2_t, 16) ||
+      kq_misaligned(w13_st, 2) || kq_misaligned(w2_st, 2) || kq_misaligned(workspace, 256) ||
       kq_misaligned(out, 16))
     return kq_fail(KQ_ERR_INVALID, "kq_moe_forward: misaligned buffer");
   if (tokens * topk > INT32_MAX / 2)
@@ -538,21 +721,42 @@ extern "C" int kq_moe_forward(int activation, float act_beta, float act_linear_b
   const ActParams ap{activation, act_beta, act_linear_beta};
   hipError_t e;
 
-  route_hist_kernel<<<(unsigned)L.nblk, PREP, 0, st>>>(route_ids, L.pairs, experts, block_counts);
-  if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_moe_forward/hist");
-  route_scan_kernel<<<1, 1024, 0, st>>>(block_counts, (int)L.nblk, experts, counts, offsets,
-                                        small_list, large_tiles, meta, (int)L.max_large);
-  if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_moe_forward/scan");
-  route_scatter_kernel<<<(unsigned)L.nblk, PREP, 0, st>>>(route_ids, L.pairs, experts, offsets,
-                                                          block_counts, sorted);
-  if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_moe_forward/scatter");
+  if (L.pairs <= PREP_ONE) {
+    route_prep_one_kernel<<<1, 1024, 0, st>>>(route_ids, (int)L.pairs, experts, counts, offsets,
+                                               sorted, small_list, large_tiles, meta, (int)L.max_large);
+    if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_moe_forward/prep");
+  } else {
+    route_hist_kernel<<<(unsigned)L.nblk, PREP, 0, st>>>(route_ids, L.pairs, experts, block_counts);
+    if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_moe_forward/hist");
+    route_scan_kernel<<<1, 1024, 0, st>>>(block_counts, (int)L.nblk, experts, counts, offsets,
+                                          small_list, large_tiles, meta, (int)L.max_large);
+    if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_moe_forward/scan");
+    route_scatter_kernel<<<(unsigned)L.nblk, PREP, 0, st>>>(route_ids, L.pairs, experts, offsets,
+                                                            block_counts, sorted);
+    if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_moe_forward/scatter");
+  }
 
   const uint16_t* xb = (const uint16_t*)x;
   // gate/up
-  moe_small_kernel<true><<<dim3((unsigned)L.max_small, (unsigned)(inter / SMALL_CH)), 256, 0, st>>>(
-      xb, ldx, topk, offsets, sorted, small_list, meta, w13_q, w13_scale, 2 * inter, hidden, inter,
-      ap, route_weights, act, y, hidden);
-  if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_moe_forward/gateup_small");
+  uint8_t* xs_hi = w + L.xs_hi;
+  uint8_t* xs_lo = w + L.xs_lo;
+  uint8_t* xs_shi = w + L.xs_shi;
+  uint8_t* xs_slo = w + L.xs_slo;
+  uint8_t* as_hi = w + L.as_hi;
+  uint8_t* as_lo = w + L.as_lo;
+  uint8_t* as_shi = w + L.as_shi;
+  uint8_t* as_slo = w + L.as_slo;
+  {
+    const int rc = kq_mx_split_quantize(KQ_DT_BF16, x, ldx, tokens, hidden, xs_hi, xs_lo, xs_shi,
+                                        xs_slo, stream);
+    if (rc != KQ_OK) return rc;
+    const dim3 grid((unsigned)L.max_small, (unsigned)(inter / 32));
+    e = launch_small<true, 32>(grid, hidden, st, (const uint8_t*)xs_hi, (const uint8_t*)xs_lo,
+                               (const uint8_t*)xs_shi, (const uint8_t*)xs_slo, topk, offsets, sorted,
+                               small_list, w13_t, w13_st, 2 * inter, hidden, inter, ap,
+                               route_weights, act, y, hidden);
+    if (e != hipSuccess) return kq_check_launch(e, "kq_moe_forward/gateup_small");
+  }
   const size_t lds = 2 * (size_t)STAGE + BM * sizeof(int);
   const bool any_large = L.pairs > SMALL_MAX;
   if (any_large) {
@@ -563,18 +767,25 @@ extern "C" int kq_moe_forward(int activation, float act_beta, float act_linear_b
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return kq_check_launch(e, "kq_moe_forward/attr");
     moe_large_kernel<true><<<dim3((unsigned)L.max_large, (unsigned)(inter / (BN / 2))), THREADS, lds, st>>>(
-        xb, ldx, topk, offsets, sorted, large_tiles, meta, w13_q, w13_scale, 2 * inter, hidden,
+        xb, ldx, topk, offsets, sorted, large_tiles, meta, w13_t, w13_st, 2 * inter, hidden,
         inter, ap, route_weights, act, y, hidden);
     if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_moe_forward/gateup_large");
   }
   // down
-  moe_small_kernel<false><<<dim3((unsigned)L.max_small, (unsigned)(hidden / SMALL_CH)), 256, 0, st>>>(
-      act, inter, topk, offsets, sorted, small_list, meta, w2_q, w2_scale, hidden, inter, inter, ap,
-      route_weights, act, y, hidden);
-  if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_moe_forward/down_small");
+  {
+    const int rc = kq_mx_split_quantize(KQ_DT_BF16, act, inter, L.pairs, inter, as_hi, as_lo, as_shi,
+                                        as_slo, stream);
+    if (rc != KQ_OK) return rc;
+    const dim3 grid((unsigned)L.max_small, (unsigned)(hidden / 64));
+    e = launch_small<false, 64>(grid, inter, st, (const uint8_t*)as_hi, (const uint8_t*)as_lo,
+                                (const uint8_t*)as_shi, (const uint8_t*)as_slo, topk, offsets, sorted,
+                                small_list, w2_t, w2_st, hidden, inter, inter, ap,
+                                route_weights, act, y, hidden);
+    if (e != hipSuccess) return kq_check_launch(e, "kq_moe_forward/down_small");
+  }
   if (any_large) {
     moe_large_kernel<false><<<dim3((unsigned)L.max_large, (unsigned)((hidden + BN - 1) / BN)), THREADS, lds, st>>>(
-        act, inter, topk, offsets, sorted, large_tiles, meta, w2_q, w2_scale, hidden, inter, inter,
+        act, inter, topk, offsets, sorted, large_tiles, meta, w2_t, w2_st, hidden, inter, inter,
         ap, route_weights, act, y, hidden);
     if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_moe_forward/down_large");
   }

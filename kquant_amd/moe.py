@@ -16,6 +16,8 @@ Layouts (compressed-tensors MXFP4, kquant/io/mxfp4.py:1-8):
 
 from __future__ import annotations
 
+from dataclasses import dataclass
+
 import torch
 
 from . import _native as N
@@ -31,6 +33,67 @@ def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     return buf
 
 
+@dataclass(frozen=True)
+class MXFP4Experts:
+    """Expert weights prepared for ``grouped_expert_forward``: the MXFP4 bytes
+    of w13 and w2 repacked once into the MFMA-tiled layout
+    (``kq_mx_tile_weights``: 1 KiB tiles of 16 rows x 128 columns, one E8M0
+    byte per row and 32-column block alongside).  Same bytes, permuted; the
+    role of the external kernel's ``prepare_weights`` step
+    (scripts/closure_exl3_layer.py:412-443)."""
+
+    w13_tiles: torch.Tensor
+    w13_scale_tiles: torch.Tensor
+    w2_tiles: torch.Tensor
+    w2_scale_tiles: torch.Tensor
+    experts: int
+    hidden: int
+    inter: int
+
+
+def _tile(q: torch.Tensor, s: torch.Tensor, rows: int, k: int) -> tuple[torch.Tensor, torch.Tensor]:
+    experts = q.shape[0]
+    qt = torch.empty(experts, rows // 16, k // 128, 1024, dtype=torch.uint8, device=q.device)
+    st = torch.empty(experts, rows // 16, k // 128, 64, dtype=torch.uint8, device=q.device)
+    N.call("kq_mx_tile_weights", N.ptr(q), N.ptr(s), experts, rows, k, N.ptr(qt), N.ptr(st),
+           N.stream(q.device))
+    return qt, st
+
+
+def prepare_expert_weights(
+    w13_packed: torch.Tensor,
+    w13_scale: torch.Tensor,
+    w2_packed: torch.Tensor,
+    w2_scale: torch.Tensor,
+) -> MXFP4Experts:
+    """Validate checkpoint-layout MXFP4 expert weights and repack them once
+    for ``grouped_expert_forward`` (on the GPU; CPU inputs are moved)."""
+
+    for t in (w13_packed, w13_scale, w2_packed, w2_scale):
+        if t.dtype != torch.uint8:
+            raise TypeError(f"expected uint8 packed weights and scales, got {t.dtype}")
+    if w13_packed.ndim != 3 or w2_packed.ndim != 3:
+        raise ValueError("expert weights must be stacked [experts, rows, packed columns]")
+    experts = w13_packed.shape[0]
+    inter = w13_packed.shape[1] // 2
+    hidden = w13_packed.shape[2] * 2
+    if w13_packed.shape != (experts, 2 * inter, hidden // 2):
+        raise ValueError(f"w13_packed shape {tuple(w13_packed.shape)} != {(experts, 2 * inter, hidden // 2)}")
+    if w13_scale.shape != (experts, 2 * inter, hidden // 32):
+        raise ValueError("w13_scale shape does not match w13_packed")
+    if w2_packed.shape != (experts, hidden, inter // 2):
+        raise ValueError(f"w2_packed shape {tuple(w2_packed.shape)} != {(experts, hidden, inter // 2)}")
+    if w2_scale.shape != (experts, hidden, inter // 32):
+        raise ValueError("w2_scale shape does not match w2_packed")
+    if hidden % 512 or inter % 512:
+        raise ValueError("hidden and intermediate sizes must be multiples of 512")
+    (w13q, w13s, w2q, w2s), gpu, _ = N.to_gpu([w13_packed, w13_scale, w2_packed, w2_scale])
+    w13q, w13s, w2q, w2s = (N.aligned(t) for t in (w13q, w13s, w2q, w2s))
+    w13t, w13st = _tile(w13q, w13s, 2 * inter, hidden)
+    w2t, w2st = _tile(w2q, w2s, hidden, inter)
+    return MXFP4Experts(w13t, w13st, w2t, w2st, experts, hidden, inter)
+
+
 def situ(gate: torch.Tensor, up: torch.Tensor, *, beta: float = 4.0,
          linear_beta: float = 25.0) -> torch.Tensor:
     """kquant/tp_simulator.py:83-94 (host-side helper, computed with torch)."""
@@ -43,10 +106,10 @@ def grouped_expert_forward(
     x: torch.Tensor,
     route_ids: torch.Tensor,
     route_weights: torch.Tensor,
-    w13_packed: torch.Tensor,
-    w13_scale: torch.Tensor,
-    w2_packed: torch.Tensor,
-    w2_scale: torch.Tensor,
+    w13_packed: torch.Tensor | MXFP4Experts,
+    w13_scale: torch.Tensor | None = None,
+    w2_packed: torch.Tensor | None = None,
+    w2_scale: torch.Tensor | None = None,
     *,
     activation: str = "situ",
     beta: float = 4.0,
@@ -54,7 +117,12 @@ def grouped_expert_forward(
     out_dtype: torch.dtype = torch.float32,
 ) -> torch.Tensor:
     """Route-weighted expert outputs ``[T, H]`` (fp32 by default, as the
-    reference's accumulator is)."""
+    reference's accumulator is).
+
+    The weights are either an ``MXFP4Experts`` from
+    ``prepare_expert_weights`` (serving: prepare once per layer) or the four
+    checkpoint-layout tensors, which are then prepared on every call.
+    """
 
     if activation not in ("situ", "swiglu"):
         raise ValueError(f"unsupported activation {activation!r}")
@@ -62,38 +130,33 @@ def grouped_expert_forward(
         raise TypeError("out_dtype must be float32 or bfloat16")
     if x.ndim != 2:
         raise ValueError("x must be [tokens, hidden]")
-    tokens, hidden = x.shape
-    if route_ids.shape != route_weights.shape or route_ids.ndim != 2 or route_ids.shape[0] != tokens:
+    if route_ids.shape != route_weights.shape or route_ids.ndim != 2 or route_ids.shape[0] != x.shape[0]:
         raise ValueError("route_ids and route_weights must both be [tokens, topk]")
-    for t in (w13_packed, w13_scale, w2_packed, w2_scale):
-        if t.dtype != torch.uint8:
-            raise TypeError(f"expected uint8 packed weights and scales, got {t.dtype}")
-    experts = w13_packed.shape[0]
-    inter = w13_packed.shape[1] // 2
-    if w13_packed.shape != (experts, 2 * inter, hidden // 2):
-        raise ValueError(f"w13_packed shape {tuple(w13_packed.shape)} != {(experts, 2 * inter, hidden // 2)}")
-    if w13_scale.shape != (experts, 2 * inter, hidden // 32):
-        raise ValueError("w13_scale shape does not match w13_packed")
-    if w2_packed.shape != (experts, hidden, inter // 2):
-        raise ValueError(f"w2_packed shape {tuple(w2_packed.shape)} != {(experts, hidden, inter // 2)}")
-    if w2_scale.shape != (experts, hidden, inter // 32):
-        raise ValueError("w2_scale shape does not match w2_packed")
+    if isinstance(w13_packed, MXFP4Experts):
+        prepared = w13_packed
+    else:
+        if w13_scale is None or w2_packed is None or w2_scale is None:
+            raise ValueError("pass MXFP4Experts or all four packed weight tensors")
+        prepared = prepare_expert_weights(w13_packed, w13_scale, w2_packed, w2_scale)
+    tokens, hidden = x.shape
+    if hidden != prepared.hidden:
+        raise ValueError(f"x hidden size {hidden} != expert hidden size {prepared.hidden}")
     topk = route_ids.shape[1]
     xb = x if x.dtype == torch.bfloat16 else x.to(torch.bfloat16)
     ids = route_ids.to(torch.int32)
     rw = route_weights.to(torch.float32)
-    (xb, ids, rw, w13q, w13s, w2q, w2s), gpu, host = N.to_gpu(
-        [xb, ids, rw, w13_packed, w13_scale, w2_packed, w2_scale])
-    xb, ids, rw = N.aligned(xb), N.aligned(ids), N.aligned(rw)
-    w13q, w13s, w2q, w2s = (N.aligned(t) for t in (w13q, w13s, w2q, w2s))
+    gpu = prepared.w13_tiles.device
+    host = None if xb.is_cuda else xb.device
+    xb, ids, rw = (N.aligned(t.to(gpu)) for t in (xb, ids, rw))
     out = torch.empty(tokens, hidden, dtype=out_dtype, device=gpu)
     lib = N.library()
-    nbytes = int(lib.kq_moe_workspace_size(tokens, topk, experts, hidden, inter))
+    nbytes = int(lib.kq_moe_workspace_size(tokens, topk, prepared.experts, hidden, prepared.inter))
     if nbytes < 0:
         raise ValueError("invalid MoE sizes")
     ws = _workspace(gpu, nbytes)
     N.call("kq_moe_forward", N.ACT_SITU if activation == "situ" else N.ACT_SWIGLU,
            float(beta), float(linear_beta), N.ptr(xb), hidden, tokens, hidden, N.ptr(ids),
-           N.ptr(rw), topk, experts, inter, N.ptr(w13q), N.ptr(w13s), N.ptr(w2q), N.ptr(w2s),
+           N.ptr(rw), topk, prepared.experts, prepared.inter, N.ptr(prepared.w13_tiles),
+           N.ptr(prepared.w13_scale_tiles), N.ptr(prepared.w2_tiles), N.ptr(prepared.w2_scale_tiles),
            N.DTYPE_CODES[out_dtype], N.ptr(out), N.ptr(ws), ws.numel(), 0, N.stream(gpu))
     return out if host is None else out.to(host)

@@ -364,3 +364,15 @@ def moe_forward(
         contrib = route_weights[tok, sel_s][:, None].astype(np.float32) * partial
         np.add.at(out, np.array([pos[int(t)] for t in tok]), contrib)
     return out
+
+
+def mx_tile(packed: np.ndarray, scale: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """MFMA-tiled MXFP4 layout of one matrix (see kq_mx_tile_weights):
+    tiles [rows/16, k/128, 64 lanes, 16 B] and scales [rows/16, k/128, 64]."""
+    rows, kh = packed.shape
+    k = kh * 2
+    p = packed.reshape(rows // 16, 16, k // 128, 4, 16)        # rg, m, c, g, j
+    q_t = p.transpose(0, 2, 3, 1, 4).reshape(rows // 16, k // 128, 64, 16)  # lane = g*16 + m
+    s = scale.reshape(rows // 16, 16, k // 128, 4)               # rg, m, c, g
+    s_t = s.transpose(0, 2, 3, 1).reshape(rows // 16, k // 128, 64)
+    return np.ascontiguousarray(q_t), np.ascontiguousarray(s_t)

@@ -95,6 +95,18 @@ def test_decode_real_shapes(gpu, tokens):
     assert rel <= TOL
 
 
+def test_tile_layout_matches_oracle(gpu):
+    w13q, w13s, w2q, w2s = workloads.quantized_experts([0, 2], 3, 512, 1024, seed=8, device=gpu)
+    prep = moe.prepare_expert_weights(w13q, w13s, w2q, w2s)
+    for e in (0, 2):
+        qt, st = oracle.mx_tile(w13q[e].cpu().numpy(), w13s[e].cpu().numpy())
+        assert np.array_equal(prep.w13_tiles[e].cpu().numpy().reshape(qt.shape), qt)
+        assert np.array_equal(prep.w13_scale_tiles[e].cpu().numpy().reshape(st.shape), st)
+        qt, st = oracle.mx_tile(w2q[e].cpu().numpy(), w2s[e].cpu().numpy())
+        assert np.array_equal(prep.w2_tiles[e].cpu().numpy().reshape(qt.shape), qt)
+        assert np.array_equal(prep.w2_scale_tiles[e].cpu().numpy().reshape(st.shape), st)
+
+
 def test_prefill_zipf_full_size_sampled_tokens(gpu):
     """Configuration 3: 8192 tokens, Zipf(1.1) top-8 over 384 experts."""
     ids, w = workloads.zipf_routing(8192)
@@ -102,8 +114,9 @@ def test_prefill_zipf_full_size_sampled_tokens(gpu):
     assert counts.max() > 16 and (counts[counts > 0] <= 16).any()  # both kernel paths
     x = torch.randn(8192, 7168, generator=torch.Generator().manual_seed(6)).to(torch.bfloat16)
     weights = workloads.quantized_experts(torch.unique(ids).tolist(), device=gpu)
-    out = moe.grouped_expert_forward(x.to(gpu), ids.to(gpu), w.to(gpu), *weights)
-    out2 = moe.grouped_expert_forward(x.to(gpu), ids.to(gpu), w.to(gpu), *weights)
+    prep = moe.prepare_expert_weights(*weights)
+    out = moe.grouped_expert_forward(x.to(gpu), ids.to(gpu), w.to(gpu), prep)
+    out2 = moe.grouped_expert_forward(x.to(gpu), ids.to(gpu), w.to(gpu), prep)
     assert torch.equal(out, out2)  # bitwise reproducible
     check = np.array([0, 4097, 8191])
     ref = _oracle(x, ids, w, weights, "situ", tokens=check)
