@@ -199,6 +199,70 @@ int kq_sym_lerp(const float* a, float a_scale, const float* b, int64_t k, float 
 #define KQ_COV_STATS_PARTS 256
 int kq_cov_stats(const float* h, int64_t k, double* workspace, double* out, void* stream);
 
+/* ---------------------------------------------------- scale-plane codecs --
+ * Lossless codings of a uint8 E8M0 scale plane [rows, cols], cols <= 255,
+ * rows contiguous.  Variable-length outputs are produced in two calls: a
+ * measuring call whose int64 offsets array ends in the total (read it after
+ * the stream synchronises, size the output), then an emitting call. */
+
+/* X4T fixed stream and per-tile exception offsets of `mats` stacked planes
+ * [mats * rows, cols], rows % 16 == 0, rows * cols < 2^24.
+ * kquant/x4t.py:90-130 (pack_x4t_scale_components: per-row adjacent base,
+ * lowest base on ties, selector bit = value is base + 1) and :201-234
+ * (x4t_scale_storage_bytes / x4t_scale_exception_count).
+ * fixed: mats * rows/16 tiles of 16 * (1 + ceil(cols/8)) bytes.
+ * tile_offsets: tiles + 1 int64; on completion entry t is the first
+ * exception of tile t and entry `tiles` the total.  Matrix m's exceptions
+ * are entries [tile_offsets[m * rows/16], tile_offsets[(m+1) * rows/16]). */
+int kq_x4t_analyze(const uint8_t* scale, int64_t mats, int64_t rows, int64_t cols,
+                   uint8_t* fixed, int64_t* tile_offsets, void* stream);
+
+/* X4T exception words (matrix-local position | value << 24, row-major) at
+ * the offsets kq_x4t_analyze produced.  kquant/x4t.py:117-126. */
+int kq_x4t_emit_exceptions(const uint8_t* scale, int64_t mats, int64_t rows, int64_t cols,
+                           const uint8_t* fixed, const int64_t* tile_offsets,
+                           uint32_t* exceptions, void* stream);
+
+/* X4T decode (kquant/x4t.py:477-524, _decode_scale_components) into
+ * out [mats * rows, cols].  exception_offsets: mats + 1 int64 giving each
+ * matrix's exception range (NULL when mats == 1: all n_exceptions).  With
+ * status non-NULL (mats == 1 only) the plane is also validated into
+ * status[4] uint32: {selector padding bits set, index of the first exception
+ * with a bad or non-increasing position (0xffffffff if none), index of the
+ * first exception naming its row's pair (0xffffffff if none), stream not
+ * canonical}.  The first failure in that order is the reference's error. */
+int kq_x4t_decode(const uint8_t* fixed, const uint32_t* exceptions, int64_t n_exceptions,
+                  const int64_t* exception_offsets, int64_t mats, int64_t rows, int64_t cols,
+                  uint8_t* out, uint32_t* status, void* stream);
+
+/* KQSC row-palette payload, version 1 (kquant/mxfp4_scale_codec.py:27-85,
+ * pack_scale_plane) or 2 (:205-292, pack_scale_plane_compact), tile_rows in
+ * 1..255.  row_meta: rows uint32 scratch; tile_offsets: tiles + 1 int64 with
+ * tiles = ceil(rows / tile_rows), entry `tiles` = total body bytes.  The
+ * payload is 16 + 4 * (tiles + 1) + total bytes; the total must be < 2^32. */
+int kq_kqsc_measure(int version, const uint8_t* scale, int64_t rows, int64_t cols, int tile_rows,
+                    uint32_t* row_meta, int64_t* tile_offsets, void* stream);
+int kq_kqsc_emit(int version, const uint8_t* scale, int64_t rows, int64_t cols, int tile_rows,
+                 const uint32_t* row_meta, const int64_t* tile_offsets, uint8_t* payload,
+                 void* stream);
+
+/* KQSC tile decode and validation (kquant/mxfp4_scale_codec.py:88-161,
+ * unpack_scale_plane; :295-424, unpack_scale_plane_compact) of a device
+ * payload whose header and offset table the caller has parsed and checked.
+ * status: one uint64, ~0 when valid, else (tile << 20) | key of the first
+ * failure in the reference's order (key < 8: tile-level check; key >= 8:
+ * 8 + row * 1024 + sub, sub 0 palette escape, 1 adjacent range, 2 selector
+ * padding, 3 + 2e bad position / 4 + 2e redundant value of exception e). */
+int kq_kqsc_decode(int version, const uint8_t* payload, int64_t payload_bytes, int64_t rows,
+                   int64_t cols, int tile_rows, uint8_t* out, uint64_t* status, void* stream);
+
+/* Structural counts of a version-2 payload (kquant/mxfp4_scale_codec.py:427-499,
+ * compact_scale_plane_stats): tile_stats [tiles, 3] uint32 {palette escapes,
+ * count escapes, exceptions}; status as for kq_kqsc_decode with key 0..4 =
+ * explicit bits short / padded, count codes short / padded, accounting. */
+int kq_kqsc_stats(const uint8_t* payload, int64_t payload_bytes, int64_t rows, int64_t cols,
+                  int tile_rows, uint32_t* tile_stats, uint64_t* status, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

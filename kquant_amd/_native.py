@@ -59,6 +59,13 @@ SIGNATURES: dict[str, list] = {
     "kq_mx_linear": [_INT, _VP, _I64, _VP, _VP, _I64, _I64, _I64, _INT, _VP, _I64, _VP],
     "kq_moe_forward": [_INT, _F32, _F32, _VP, _I64, _I64, _I64, _VP, _VP, _INT, _INT, _I64,
                        _VP, _VP, _VP, _VP, _INT, _VP, _VP, _I64, _U32, _VP],
+    "kq_x4t_analyze": [_VP, _I64, _I64, _I64, _VP, _VP, _VP],
+    "kq_x4t_emit_exceptions": [_VP, _I64, _I64, _I64, _VP, _VP, _VP, _VP],
+    "kq_x4t_decode": [_VP, _VP, _I64, _VP, _I64, _I64, _I64, _VP, _VP, _VP],
+    "kq_kqsc_measure": [_INT, _VP, _I64, _I64, _INT, _VP, _VP, _VP],
+    "kq_kqsc_emit": [_INT, _VP, _I64, _I64, _INT, _VP, _VP, _VP, _VP],
+    "kq_kqsc_decode": [_INT, _VP, _I64, _I64, _I64, _INT, _VP, _VP, _VP],
+    "kq_kqsc_stats": [_VP, _I64, _I64, _I64, _INT, _VP, _VP, _VP],
 }
 COV_STATS_PARTS = 256
 
