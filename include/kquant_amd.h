@@ -58,7 +58,10 @@ const char* kq_last_error(void);
  *
  * MXFP8 replaces kquant/mxfp8.py:11-51 (mxfp8_quantize_cpu):
  *   e = clamp(ceil(log2(max(amax,1e-30)/448)), -127, 128), byte = e + 127,
- *   q = float8_e4m3fn(clamp(x / 2^e, +-448))   (round to nearest even).
+ *   q = float8_e4m3fn(clamp(x / 2^e, +-448))   (round to nearest even),
+ * with the quotient and its log2 each rounded to fp32 as the reference's
+ * float32 torch ops do (this decides e only for fp32 inputs whose amax lies a
+ * few ulps above 448 * 2^k).
  * MXFP4 is the same rule with (E2M1, 6.0); kquant has no MXFP4 quantizer,
  * its output layout is kquant/io/mxfp4.py:1-8 / pack_codes (:32-38).
  * out_q: uint8 [rows, k] (MXFP8) or [rows, k/2] (MXFP4), contiguous.
@@ -262,6 +265,43 @@ int kq_kqsc_decode(int version, const uint8_t* payload, int64_t payload_bytes, i
  * explicit bits short / padded, count codes short / padded, accounting. */
 int kq_kqsc_stats(const uint8_t* payload, int64_t payload_bytes, int64_t rows, int64_t cols,
                   int tile_rows, uint32_t* tile_stats, uint64_t* status, void* stream);
+
+/* ------------------------------------------------------------ SQG tables --
+ * Tables of kquant/sqg_e4m3.py, 65,536 entries (T12: 4,096), device memory. */
+enum { KQ_SQG_RANK_XOR = 0, KQ_SQG_RANK_MIX = 1, KQ_SQG_RANK_K2_OCTILE = 2 };
+
+/* int64 ranks [65536] of every L16 codeword.  KQ_SQG_RANK_XOR:
+ * sqg_xor_rank_permutation(bits) (kquant/sqg_e4m3.py:261-285);
+ * KQ_SQG_RANK_MIX: sqg_rank_permutation(bits) (:408-438);
+ * KQ_SQG_RANK_K2_OCTILE: sqg_k2_eight_stratum_rank_permutation(history_bit)
+ * (:356-389, bits ignored). */
+int kq_sqg_rank_permutation(int kind, int bits, int history_bit, int64_t* ranks, void* stream);
+
+/* u8 [65536] canonical E4M3 of 1.5 * ndtri((rank + 0.5) / 65536)
+ * (sqg_cheb_normal_rank_e4m3_bytes, kquant/sqg_e4m3.py:218-230). */
+int kq_sqg_normal_rank_law(uint8_t* law, void* stream);
+
+/* u8 [65536] canonical E4M3 (single zero byte) of fp32 values [65536]
+ * (_finite_e4m3_rank_lut, kquant/sqg_e4m3.py:197-208). */
+int kq_sqg_finite_rank_lut(const float* values, uint8_t* law, void* stream);
+
+/* status (one uint32, device): bit 0 a NaN byte, bit 1 a decrease between
+ * neighbouring entries (kquant/sqg_e4m3.py:209-213). */
+int kq_sqg_check_rank_law(const uint8_t* law, uint32_t* status, void* stream);
+
+/* u8 [4096] modal byte of each 16 consecutive ranks, ties to the lower byte
+ * (sqg_xor_cheb_t12_rank_lut_bytes, kquant/sqg_e4m3.py:233-257). */
+int kq_sqg_modal_compress(const uint8_t* law, uint8_t* t12, void* stream);
+
+/* out[i] = lut[ranks[i] >> shift] for i < n (the label maps of
+ * kquant/sqg_e4m3.py:176-179, :289-291, :392-405).  status bit 0: a NaN label
+ * was read; bit 1: a rank outside the table (its output byte is 0). */
+int kq_sqg_gather(const uint8_t* lut, int64_t lut_len, int shift, const int64_t* ranks, int64_t n,
+                  uint8_t* out, uint32_t* status, void* stream);
+
+/* u8 [65536] R44 research labels sqg_e4m3_bytes(bits, "normal")
+ * (kquant/sqg_e4m3.py:75-127); status bit 0: a non-finite value. */
+int kq_sqg_r44_bytes(int bits, uint8_t* out, uint32_t* status, void* stream);
 
 #ifdef __cplusplus
 }

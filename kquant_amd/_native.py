@@ -66,7 +66,17 @@ SIGNATURES: dict[str, list] = {
     "kq_kqsc_emit": [_INT, _VP, _I64, _I64, _INT, _VP, _VP, _VP, _VP],
     "kq_kqsc_decode": [_INT, _VP, _I64, _I64, _I64, _INT, _VP, _VP, _VP],
     "kq_kqsc_stats": [_VP, _I64, _I64, _I64, _INT, _VP, _VP, _VP],
+    "kq_sqg_rank_permutation": [_INT, _INT, _INT, _VP, _VP],
+    "kq_sqg_normal_rank_law": [_VP, _VP],
+    "kq_sqg_finite_rank_lut": [_VP, _VP, _VP],
+    "kq_sqg_check_rank_law": [_VP, _VP, _VP],
+    "kq_sqg_modal_compress": [_VP, _VP, _VP],
+    "kq_sqg_gather": [_VP, _I64, _INT, _VP, _I64, _VP, _VP, _VP],
+    "kq_sqg_r44_bytes": [_INT, _VP, _VP, _VP],
 }
+SQG_RANK_XOR = 0
+SQG_RANK_MIX = 1
+SQG_RANK_K2_OCTILE = 2
 COV_STATS_PARTS = 256
 
 _lib: ctypes.CDLL | None = None

@@ -58,7 +58,7 @@ __global__ __launch_bounds__(256) void mx_quantize_kernel(
   amax = quad_max(amax);
 
   const float qmax = FMT == 0 ? 448.0f : 6.0f;
-  const int e = mx_block_exponent(amax, qmax);
+  const int e = IN == 2 ? mx_block_exponent_f32_log2(amax, qmax) : mx_block_exponent(amax, qmax);
   const uint32_t sbyte = (uint32_t)(e + 127);
   if (part == 0) out_scale[blk] = (uint8_t)sbyte;
 

@@ -69,6 +69,22 @@ __device__ __forceinline__ int mx_block_exponent(float amax, float qmax) {
   return e;
 }
 
+// The same exponent for fp32 inputs, whose quotients can sit a few ulps above
+// a power of two: kquant/mxfp8.py:41-43 takes torch.log2 in float32, which
+// rounds k + log2(1 + f) down to k when log2(1 + f) is below half an ulp of
+// k, so the reference keeps exponent k there and clamps the block's top
+// values to qmax.  log2 is evaluated in double and rounded once to float; a
+// double result within an ulp of the true value rounds like the correctly
+// rounded one, because log2(1 + m 2^-23) is never near an f32 midpoint of k.
+__device__ __forceinline__ int mx_block_exponent_f32_log2(float amax, float qmax) {
+  const float q = __fdiv_rn(fmaxf(amax, 1e-30f), qmax);
+  if (__float_as_uint(q) >= 0x7f800000u) return 128;  // amax = +inf
+  int e = (int)ceilf((float)log2((double)q));
+  e = e < -127 ? -127 : e;
+  e = e > 128 ? 128 : e;
+  return e;
+}
+
 // 2^-e as an exact fp32 multiplier; e = 128 (only for an infinite amax)
 // gives 0 so x * 0 reproduces x / exp2(128) = x / inf (0, or NaN for inf).
 __device__ __forceinline__ float mx_inv_scale(int e) {

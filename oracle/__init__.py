@@ -226,6 +226,57 @@ def sqg_xor_cheb_t12_bytes(bits: int) -> np.ndarray:
     return sqg_xor_cheb_t12_rank_lut_bytes()[sqg_xor_rank_permutation(bits) >> 4]
 
 
+def _mix_width(values, width, ma, mb, sa, sb, sc):
+    """kquant/sqg_e4m3.py:38-60: xorshift / odd multiply mixer modulo 2^width."""
+    mask = (1 << width) - 1
+    r = values & mask
+    for m, s in ((ma | 1, sa), (mb | 1, sb)):
+        r ^= r >> min(max(s, 1), width - 1)
+        r = (r * m) & mask
+    r ^= r >> min(max(sc, 1), width - 1)
+    return r & mask
+
+
+def sqg_rank_permutation(bits: int) -> np.ndarray:
+    """kquant/sqg_e4m3.py:408-438 (and :96-115): mix-width SQG rank."""
+    width = 16 - bits
+    t = np.arange(TRANSITIONS, dtype=np.int64)
+    history, branch = t >> bits, t & ((1 << bits) - 1)
+    phase = _mix_width(history, width, 0x65AF, 0x16BF, 6, 4, 5)
+    syndrome = _mix_width(history ^ 0x5105, width, 0x8693, 0x2A21, 2, 4, 4) & ((1 << bits) - 1)
+    stratum = (7 * (_reverse_low_bits(branch, bits) ^ syndrome)) & ((1 << bits) - 1)
+    return (stratum << width) | phase
+
+
+def sqg_k2_eight_stratum_rank_permutation(history_bit: int = 2) -> np.ndarray:
+    """kquant/sqg_e4m3.py:356-389: K3 ranks of the codeword with bits 2, h swapped."""
+    t = np.arange(TRANSITIONS, dtype=np.int64)
+    swap = ((t >> 2) ^ (t >> history_bit)) & 1
+    return sqg_rank_permutation(3)[t ^ (swap << 2) ^ (swap << history_bit)]
+
+
+def sqg_r44_bytes(bits: int) -> np.ndarray:
+    """kquant/sqg_e4m3.py:84-127: R44 compander of the clipped mix-rank probability.
+
+    numpy float64 element-wise arithmetic rounds each product and sum
+    separately, as the reference's tensor operations do.
+    """
+    p_coef = (1.25667142, 2.87422731, -9.02398882, 5.36810336, -0.46703015)
+    q_coef = (1.0, 2.07630930, -8.08332684, 6.32135736, -1.31208298)
+    rank = sqg_rank_permutation(bits)
+    prob = np.clip((rank.astype(np.float64) + 0.5) / TRANSITIONS, 1 / 2048, 1 - 1 / 2048)
+    a = 2.0 * prob - 1.0
+    x = a * a
+    num = np.full_like(x, p_coef[-1])
+    den = np.full_like(x, q_coef[-1])
+    for c in reversed(p_coef[:-1]):
+        num = num * x + c
+    for c in reversed(q_coef[:-1]):
+        den = den * x + c
+    values = (1.5 * (a * num / den)).astype(np.float32)
+    return f32_to_e4m3(values)
+
+
 # ---------------------------------------------------------------- Hessian --
 
 def weighted_covariance(rows: np.ndarray, weights: np.ndarray, chunk_rows: int = 256):
