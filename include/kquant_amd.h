@@ -266,6 +266,52 @@ int kq_kqsc_decode(int version, const uint8_t* payload, int64_t payload_bytes, i
 int kq_kqsc_stats(const uint8_t* payload, int64_t payload_bytes, int64_t rows, int64_t cols,
                   int tile_rows, uint32_t* tile_stats, uint64_t* status, void* stream);
 
+/* Workspace bytes of kq_mx_linear_f32 (m * 3k bf16), -1 on bad sizes. */
+int64_t kq_mx_linear_f32_workspace_size(int64_t m, int64_t k);
+
+/* C [m, n] fp32 = A [m, k] fp32 x dequant(W [n, k])^T at fp32-GEMM accuracy:
+ * A is split exactly into three bf16 terms (a = a0 + a1 + a2) written to the
+ * workspace as [m, 3k], and one launch of the kq_mx_linear kernel accumulates
+ * all three products in fp32 (weight column k' % k for A column k').
+ * Replaces the fp32 F.linear over dequantized official weights of
+ * kquant/pack/qsrt_validation.py:240-258 (official_expert_output) and the
+ * fp32 closure oracles.  k % 64 == 0, lda % 4 == 0; a, w_q, workspace
+ * 16-byte aligned. */
+int kq_mx_linear_f32(int w_fmt, const float* a, int64_t lda, const void* w_q,
+                     const uint8_t* w_scale, int64_t m, int64_t n, int64_t k, float* c,
+                     int64_t ldc, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------- expert MLP helpers --
+ * out[r, c] = act(gate[r, c], up[r, c]) computed in fp32 (SiTU with beta /
+ * linear_beta, kquant/tp_simulator.py:83-94, or SwiGLU), rounded to
+ * out_dtype.  gate and up share the row stride ld_in. */
+int kq_expert_activation(int activation, float beta, float linear_beta, int in_dtype,
+                         const void* gate, const void* up, int64_t ld_in, int64_t rows,
+                         int64_t cols, int out_dtype, void* out, int64_t ld_out, void* stream);
+
+/* out[i] = (sum over p of partials[p * stride + i]) in fp32, summed in order
+ * p = 0..parts-1, rounded to out_dtype (kquant/tp_simulator.py:72-80,
+ * reduce_partials). */
+int kq_reduce_partials(const float* partials, int64_t parts, int64_t stride, int64_t n,
+                       int out_dtype, void* out, void* stream);
+
+/* Deterministic f64 sums behind comparison_metrics
+ * (kquant/tp_simulator.py:137-160): out[5] = {sum (a - r)^2, max |a - r|,
+ * sum r^2, sum a^2, sum r*a} with a - r formed in fp32.  workspace: 256 * 5
+ * doubles.  relative_l2 = sqrt(out[0]) / max(sqrt(out[2]), FLT_MIN),
+ * cosine = out[4] / (max(sqrt(out[2]), eps) * max(sqrt(out[3]), eps)). */
+int kq_comparison_sums(int ref_dtype, const void* reference, int act_dtype, const void* actual,
+                       int64_t n, double* workspace, double* out, void* stream);
+
+/* K3 router (kquant/tp_simulator.py:114-134, kimi_topk): scores =
+ * sigmoid(logits) in fp32, top-k of scores + bias[e] in descending order
+ * (ties to the lower expert id), weights = chosen scores / their sum *
+ * routed_scaling_factor.  logits [tokens, experts] (row stride ld),
+ * weights fp32 / ids int32 [tokens, topk].  experts <= 1024, topk <= 64. */
+int kq_kimi_topk(int logit_dtype, const void* logits, int64_t ld, const float* bias,
+                 int64_t tokens, int experts, int topk, float routed_scaling_factor,
+                 float* weights, int32_t* ids, void* stream);
+
 /* ------------------------------------------------------------ SQG tables --
  * Tables of kquant/sqg_e4m3.py, 65,536 entries (T12: 4,096), device memory. */
 enum { KQ_SQG_RANK_XOR = 0, KQ_SQG_RANK_MIX = 1, KQ_SQG_RANK_K2_OCTILE = 2 };

@@ -73,6 +73,12 @@ SIGNATURES: dict[str, list] = {
     "kq_sqg_modal_compress": [_VP, _VP, _VP],
     "kq_sqg_gather": [_VP, _I64, _INT, _VP, _I64, _VP, _VP, _VP],
     "kq_sqg_r44_bytes": [_INT, _VP, _VP, _VP],
+    "kq_mx_linear_f32": [_INT, _VP, _I64, _VP, _VP, _I64, _I64, _I64, _VP, _I64, _VP, _I64, _VP],
+    "kq_expert_activation": [_INT, _F32, _F32, _INT, _VP, _VP, _I64, _I64, _I64, _INT, _VP, _I64,
+                             _VP],
+    "kq_reduce_partials": [_VP, _I64, _I64, _I64, _INT, _VP, _VP],
+    "kq_comparison_sums": [_INT, _VP, _INT, _VP, _I64, _VP, _VP, _VP],
+    "kq_kimi_topk": [_INT, _VP, _I64, _VP, _I64, _INT, _INT, _F32, _VP, _VP, _VP],
 }
 SQG_RANK_XOR = 0
 SQG_RANK_MIX = 1
@@ -99,6 +105,8 @@ def library() -> ctypes.CDLL:
         lib.kq_last_error.argtypes = []
         lib.kq_moe_workspace_size.restype = ctypes.c_int64
         lib.kq_moe_workspace_size.argtypes = [_I64, _INT, _INT, _I64, _I64]
+        lib.kq_mx_linear_f32_workspace_size.restype = ctypes.c_int64
+        lib.kq_mx_linear_f32_workspace_size.argtypes = [_I64, _I64]
         for name, argtypes in SIGNATURES.items():
             fn = getattr(lib, name)
             fn.restype = ctypes.c_int

@@ -22,6 +22,7 @@
 // No atomics touch floating-point data, so results are bitwise reproducible.
 #include "kq_gemm.h"
 #include "kq_internal.h"
+#include "kq_act.h"
 
 namespace kq {
 namespace moe {
@@ -75,21 +76,6 @@ static Layout make_layout(int64_t tokens, int topk, int experts, int64_t hidden,
 }
 
 // ------------------------------------------------------------ activations --
-struct ActParams {
-  int kind;       // KQ_ACT_SITU or KQ_ACT_SWIGLU
-  float beta;     // SiTU gate beta
-  float lbeta;    // SiTU linear beta
-};
-
-__device__ __forceinline__ float sigmoidf_(float v) { return 1.0f / (1.0f + expf(-v)); }
-
-__device__ __forceinline__ float activate(const ActParams& p, float g, float u) {
-  if (p.kind == KQ_ACT_SWIGLU) return g * sigmoidf_(g) * u;
-  const float gv = p.beta * tanhf(g / p.beta) * sigmoidf_(g);
-  const float uv = p.lbeta * tanhf(u / p.lbeta);
-  return gv * uv;
-}
-
 // ------------------------------------------------------------ routing prep --
 __global__ __launch_bounds__(PREP) void route_hist_kernel(const int* __restrict__ ids, int64_t pairs,
                                                           int experts, int* __restrict__ block_counts) {

@@ -21,6 +21,10 @@ from dataclasses import dataclass
 import torch
 
 from . import _native as N
+from .io.mxfp4 import dequant
+from .linear import mxfp4_linear
+from .source_weights import PackedMXFP4Matrix
+from .tp_simulator import situ, swiglu
 
 _WORKSPACES: dict[torch.device, torch.Tensor] = {}
 
@@ -94,12 +98,70 @@ def prepare_expert_weights(
     return MXFP4Experts(w13t, w13st, w2t, w2st, experts, hidden, inter)
 
 
-def situ(gate: torch.Tensor, up: torch.Tensor, *, beta: float = 4.0,
-         linear_beta: float = 25.0) -> torch.Tensor:
-    """kquant/tp_simulator.py:83-94 (host-side helper, computed with torch)."""
-    gate_value = beta * torch.tanh(gate.float() / beta) * torch.sigmoid(gate.float())
-    up_value = linear_beta * torch.tanh(up.float() / linear_beta)
-    return (gate_value * up_value).to(gate.dtype)
+def expert_output(
+    inputs: torch.Tensor,
+    w1: tuple[torch.Tensor, torch.Tensor],
+    w3: tuple[torch.Tensor, torch.Tensor],
+    w2: tuple[torch.Tensor, torch.Tensor],
+    *,
+    activation: str = "situ",
+    beta: float = 4.0,
+    linear_beta: float = 25.0,
+) -> torch.Tensor:
+    """One expert's MLP over its MXFP4 matrices, in fp32.
+
+    kquant/pack/qsrt_validation.py:240-258 (``official_expert_output``):
+    gate = x W1^T, up = x W3^T, middle = situ(gate, up), out = middle W2^T,
+    every product an fp32 ``F.linear`` over the dequantized official
+    matrix.  Here each matrix stays packed (``(packed, scale)`` or a
+    ``PackedMXFP4Matrix``) and the products run in ``kq_mx_linear_f32``
+    (fp32 activations split exactly into bf16 terms, fp32 accumulation);
+    the activation runs in ``kq_expert_activation``.  Output fp32 [rows, H].
+    """
+
+    if activation not in ("situ", "swiglu"):
+        raise ValueError(f"unsupported activation {activation!r}")
+    if inputs.ndim != 2:
+        raise ValueError("expert inputs must be two-dimensional")
+    (p1, s1), (p3, s3), (p2, s2) = (_pair(w) for w in (w1, w3, w2))
+    x = inputs.float()
+    gate = mxfp4_linear(x, p1, s1, out_dtype=torch.float32)
+    up = mxfp4_linear(x, p3, s3, out_dtype=torch.float32)
+    if activation == "situ":
+        middle = situ(gate, up, beta=beta, linear_beta=linear_beta)
+    else:
+        middle = swiglu(gate, up)
+    return mxfp4_linear(middle, p2, s2, out_dtype=torch.float32)
+
+
+def _pair(w) -> tuple[torch.Tensor, torch.Tensor]:
+    if isinstance(w, PackedMXFP4Matrix):
+        return w.packed, w.scale
+    packed, scale = w
+    return packed, scale
+
+
+def reconstruct_source(
+    raw: dict[str, dict[str, torch.Tensor]],
+    device: torch.device | str,
+    *,
+    scale_byte_max: int | None = None,
+) -> dict[str, torch.Tensor]:
+    """bf16 expert matrices from their MXFP4 parts, optionally clamping the
+    E8M0 bytes to ``scale_byte_max`` first
+    (scripts/closure_exl3_layer.py:143-161, ``_reconstruct_source``).
+    ``raw[matrix]`` holds ``"packed"`` and ``"scale"``."""
+
+    result = {}
+    for matrix, value in raw.items():
+        scale = value["scale"].view(torch.uint8)
+        if scale_byte_max is not None:
+            scale = scale.clamp(max=scale_byte_max)
+        result[matrix] = dequant(value["packed"], scale, dtype=torch.bfloat16).to(device=device)
+    return result
+
+
+_reconstruct_source = reconstruct_source
 
 
 def grouped_expert_forward(

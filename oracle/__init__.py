@@ -14,6 +14,12 @@ Contents, each following the cited reference code:
   situ / swiglu / reference_rank
       numpy restatements of kquant/tp_simulator.py:83-94 and
       scripts/closure_exl3_layer.py:557-598.
+  reduce_partials / kimi_topk / comparison_metrics / expert_output
+      kquant/tp_simulator.py:72-80, 114-160; kquant/pack/qsrt_validation.py:240-258.
+  sqg_* tables
+      kquant/sqg_e4m3.py:38-60, 84-127, 197-302, 356-438.
+  scale_plane (submodule): X4T and KQSC scale-plane codecs
+      kquant/x4t.py, kquant/mxfp4_scale_codec.py.
 """
 
 from __future__ import annotations
@@ -364,6 +370,53 @@ def swiglu(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
     """silu(gate) * up in float32."""
     g = gate.astype(np.float32)
     return (g * _sigmoid(g) * up.astype(np.float32)).astype(np.float32)
+
+
+def reduce_partials(partials: list[np.ndarray]) -> np.ndarray:
+    """kquant/tp_simulator.py:72-80: fp32 sum of rank partials in rank order."""
+    acc = np.zeros_like(np.asarray(partials[0], dtype=np.float32))
+    for p in partials:
+        acc = (acc + np.asarray(p, dtype=np.float32)).astype(np.float32)
+    return acc
+
+
+def kimi_topk(logits: np.ndarray, bias: np.ndarray, topk: int, scale: float = 1.0):
+    """kquant/tp_simulator.py:114-134 in float64 arithmetic on fp32 inputs:
+    sigmoid scores, top-k of score + bias (descending, lower id on ties),
+    weights = chosen scores / their sum * scale.  Returns (weights, ids, keys)."""
+    scores = 1.0 / (1.0 + np.exp(-logits.astype(np.float64)))
+    keys = scores + bias.astype(np.float64)[None, :]
+    order = np.lexsort((np.broadcast_to(np.arange(keys.shape[1]), keys.shape), -keys), axis=1)
+    ids = order[:, :topk]
+    chosen = np.take_along_axis(scores, ids, axis=1)
+    weights = chosen / chosen.sum(axis=1, keepdims=True) * scale
+    return weights, ids.astype(np.int32), np.take_along_axis(keys, order, axis=1)
+
+
+def comparison_metrics(reference: np.ndarray, actual: np.ndarray) -> dict[str, float]:
+    """kquant/tp_simulator.py:137-160 in float64 (diff formed in float32)."""
+    r = reference.astype(np.float32).ravel()
+    a = actual.astype(np.float32).ravel()
+    d = (a - r).astype(np.float64)
+    r64, a64 = r.astype(np.float64), a.astype(np.float64)
+    rn = np.sqrt(np.sum(r64 * r64))
+    cos = np.sum(r64 * a64) / np.sqrt(max(np.sum(r64 * r64) * np.sum(a64 * a64), 1e-16))
+    return {
+        "relative_l2": float(np.sqrt(np.sum(d * d)) / max(rn, np.finfo(np.float32).tiny)),
+        "max_abs": float(np.max(np.abs(d))) if d.size else 0.0,
+        "cosine": float(cos),
+    }
+
+
+def expert_output(x: np.ndarray, w1: np.ndarray, w3: np.ndarray, w2: np.ndarray,
+                  activation: str = "situ") -> np.ndarray:
+    """kquant/pack/qsrt_validation.py:240-258 (official_expert_output) with
+    dense dequantized matrices [out, in]: float64 products, fp32 activation."""
+    x64 = x.astype(np.float64)
+    gate = (x64 @ w1.astype(np.float64).T).astype(np.float32)
+    up = (x64 @ w3.astype(np.float64).T).astype(np.float32)
+    mid = situ(gate, up) if activation == "situ" else swiglu(gate, up)
+    return mid.astype(np.float64) @ w2.astype(np.float64).T
 
 
 def round_bf16(x: np.ndarray) -> np.ndarray:

@@ -31,7 +31,8 @@ def test_library_exports_every_declared_symbol():
 def test_python_binding_covers_every_entry_point():
     lib = _native.library()
     assert lib.kq_version() >> 16 == 1
-    bound = set(_native.SIGNATURES) | {"kq_version", "kq_last_error", "kq_moe_workspace_size"}
+    bound = set(_native.SIGNATURES) | {"kq_version", "kq_last_error", "kq_moe_workspace_size",
+                                        "kq_mx_linear_f32_workspace_size"}
     assert set(declared_symbols()) <= bound
 
 
