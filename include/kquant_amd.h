@@ -42,7 +42,7 @@ enum {
   KQ_FLAG_SOFTWARE_CVT = 1u
 };
 /* kq_syrk_accumulate flags */
-enum { KQ_SYRK_OVERWRITE = 1u };
+enum { KQ_SYRK_OVERWRITE = 1u, KQ_SYRK_SQUARE_WEIGHTS = 2u, KQ_SUM_SQUARE_F64 = 4u };
 /* byte tables of kq_decode_bytes */
 enum { KQ_TABLE_E8M0 = 0, KQ_TABLE_E2M1 = 1, KQ_TABLE_E4M3 = 2 };
 /* expert activations */
@@ -187,6 +187,51 @@ int kq_syrk_accumulate(int in_dtype, const void* x, int64_t ld, int64_t n, int64
  * acc and out must not alias. */
 int kq_syrk_finalize(const float* acc, int64_t ld_acc, int64_t k, double denominator,
                      float damp, float* out, int64_t ld_out, void* stream);
+
+/* Routing sort on its own: the pairs p = t * topk + s of route_ids
+ * [tokens, topk] grouped by expert, stable in pair order (ids outside
+ * [0, experts) dropped), as the per-expert row selection of
+ * kquant/qsrt_candidates.py:264-289 orders them.  Outputs: offsets int64
+ * [experts + 1]; rows int32 [pairs] (token t of each sorted pair);
+ * optional sorted_pairs int32 [pairs]; optional sorted_weights fp32 [pairs] =
+ * pair_weights[pair].  Entries past offsets[experts] are unspecified.
+ * workspace: kq_route_sort_workspace_size bytes, 256-byte aligned. */
+int64_t kq_route_sort_workspace_size(int64_t tokens, int topk, int experts);
+int kq_route_sort(const int32_t* route_ids, int64_t tokens, int topk, int experts,
+                  const float* pair_weights, int64_t* offsets, int32_t* rows, int32_t* sorted_pairs,
+                  float* sorted_weights, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Per-group (per-expert) weighted X^T X in one launch: group g owns row-list
+ * positions [offsets[g], offsets[g+1]) (offsets: device int64 [groups + 1]);
+ * position p is row row_index[p] of x (row p itself when row_index is NULL)
+ * with weight weights[p] (squared in fp32 with KQ_SYRK_SQUARE_WEIGHTS, the
+ * gate^2 weighting of kquant/qsrt_candidates.py:562; 1 when weights is
+ * NULL).  acc: [groups, k, k] fp32, upper tiles overwritten (finish with
+ * kq_syrk_finalize_grouped).  The batched form of the per-expert
+ * weighted_covariance calls of build_expert_hessians
+ * (kquant/qsrt_candidates.py:534-618). */
+int kq_syrk_grouped(int in_dtype, const void* x, int64_t ld, const int64_t* offsets, int groups,
+                    const int32_t* row_index, const float* weights, int64_t k, float* acc,
+                    uint32_t flags, void* stream);
+
+/* out[g] = f64 sum of the group's weights (fp32 squares with
+ * KQ_SYRK_SQUARE_WEIGHTS, f64 squares with KQ_SUM_SQUARE_F64; the row count
+ * when weights is NULL): the denominators float(w.double().sum()) of
+ * kquant/candidate_hessian.py:95 and the Kish sums of :141-153. */
+int kq_segment_weight_sums(const float* weights, const int64_t* offsets, int groups, uint32_t flags,
+                           double* out, void* stream);
+
+/* out[g] = sym(acc[g]) / denominators[g] (device f64 [groups]); a group with
+ * denominator <= 0 gives zeros.  acc, out: [groups, k, k]; no aliasing. */
+int kq_syrk_finalize_grouped(const float* acc, int64_t k, int groups, const double* denominators,
+                             float* out, void* stream);
+
+/* Sums of covariance_comparison (kquant/candidate_hessian.py:219-258) for
+ * fp32 [k, k] reference R and candidate C, in f64: out[8] = {sum (C-R)^2,
+ * sum R^2, trace R, trace C, sum diag(R)^2, sum diag(C)^2, diag(R).diag(C),
+ * max |C - C^T|}.  workspace: 256 * 8 doubles.  Deterministic. */
+int kq_covariance_comparison_sums(const float* reference, const float* candidate, int64_t k,
+                                  double* workspace, double* out, void* stream);
 
 /* out [k,k] = ((X + X^T) / 2) with X = torch.lerp(A, B, alpha); A = a, or
  * a_scale * I when a is NULL.  kquant/candidate_hessian.py:115-138

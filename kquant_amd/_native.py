@@ -31,6 +31,8 @@ TABLE_E8M0 = 0
 TABLE_E2M1 = 1
 TABLE_E4M3 = 2
 SYRK_OVERWRITE = 1
+SYRK_SQUARE_WEIGHTS = 2
+SUM_SQUARE_F64 = 4
 ACT_SITU = 0
 ACT_SWIGLU = 1
 
@@ -79,6 +81,11 @@ SIGNATURES: dict[str, list] = {
     "kq_reduce_partials": [_VP, _I64, _I64, _I64, _INT, _VP, _VP],
     "kq_comparison_sums": [_INT, _VP, _INT, _VP, _I64, _VP, _VP, _VP],
     "kq_kimi_topk": [_INT, _VP, _I64, _VP, _I64, _INT, _INT, _F32, _VP, _VP, _VP],
+    "kq_syrk_grouped": [_INT, _VP, _I64, _VP, _INT, _VP, _VP, _I64, _VP, _U32, _VP],
+    "kq_segment_weight_sums": [_VP, _VP, _INT, _U32, _VP, _VP],
+    "kq_syrk_finalize_grouped": [_VP, _I64, _INT, _VP, _VP, _VP],
+    "kq_route_sort": [_VP, _I64, _INT, _INT, _VP, _VP, _VP, _VP, _VP, _VP, _I64, _VP],
+    "kq_covariance_comparison_sums": [_VP, _VP, _I64, _VP, _VP, _VP],
 }
 SQG_RANK_XOR = 0
 SQG_RANK_MIX = 1
@@ -107,6 +114,8 @@ def library() -> ctypes.CDLL:
         lib.kq_moe_workspace_size.argtypes = [_I64, _INT, _INT, _I64, _I64]
         lib.kq_mx_linear_f32_workspace_size.restype = ctypes.c_int64
         lib.kq_mx_linear_f32_workspace_size.argtypes = [_I64, _I64]
+        lib.kq_route_sort_workspace_size.restype = ctypes.c_int64
+        lib.kq_route_sort_workspace_size.argtypes = [_I64, _INT, _INT]
         for name, argtypes in SIGNATURES.items():
             fn = getattr(lib, name)
             fn.restype = ctypes.c_int

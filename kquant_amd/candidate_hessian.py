@@ -185,19 +185,33 @@ def shrink_covariance(
     return out if host is None else out.to(host)
 
 
+def _weight_sums(w: torch.Tensor, offsets: torch.Tensor, groups: int, flags: int) -> torch.Tensor:
+    out = torch.empty(groups, dtype=torch.float64, device=w.device if w is not None else offsets.device)
+    N.call("kq_segment_weight_sums", N.ptr(w), N.ptr(offsets), groups, flags, N.ptr(out),
+           N.stream(out.device))
+    return out
+
+
+def _single_group(n: int, gpu: torch.device) -> torch.Tensor:
+    return torch.tensor([0, n], dtype=torch.int64, device=gpu)
+
+
 def weighted_effective_sample_size(weights: torch.Tensor) -> float:
-    """Kish effective sample size (kquant/candidate_hessian.py:141-153)."""
+    """Kish effective sample size (kquant/candidate_hessian.py:141-153):
+    (sum w)^2 / sum w^2 with both sums in f64 (``kq_segment_weight_sums``)."""
 
     if weights.ndim != 1 or not weights.numel():
         raise ValueError("weights must be a nonempty vector")
-    if not torch.all(torch.isfinite(weights)) or torch.any(weights < 0):
+    (w,), gpu, _ = N.to_gpu([weights])
+    if not torch.all(torch.isfinite(w)) or torch.any(w < 0):
         raise ValueError("weights must be finite and nonnegative")
-    weights64 = weights.double()
-    total = weights64.sum()
-    squared_total = weights64.square().sum()
+    w = N.aligned(w.float(), 4)
+    offsets = _single_group(w.numel(), gpu)
+    total = float(_weight_sums(w, offsets, 1, 0).item())
+    squared_total = float(_weight_sums(w, offsets, 1, N.SUM_SQUARE_F64).item())
     if total <= 0 or squared_total <= 0:
         raise ValueError("weights must have positive effective support")
-    return float(total.square() / squared_total)
+    return total * total / squared_total
 
 
 def adaptive_identity_shrinkage(
@@ -259,36 +273,197 @@ def adaptive_identity_shrinkage(
 def covariance_comparison(reference: torch.Tensor, candidate: torch.Tensor) -> dict[str, float]:
     """Compact scale/shape diagnostics (kquant/candidate_hessian.py:219-258).
 
-    This is the parity metric itself (relative Frobenius difference in f64);
-    it is evaluated with torch on the tensors' device.
+    This is the parity metric itself: the relative Frobenius difference, trace
+    ratio and diagonal cosine from f64 sums (``kq_covariance_comparison_sums``),
+    and the candidate's largest asymmetry.
     """
 
     if reference.ndim != 2 or reference.shape[0] != reference.shape[1]:
         raise ValueError("reference covariance must be square")
     if candidate.shape != reference.shape:
         raise ValueError("candidate covariance shape differs")
-    reference = reference.float()
-    candidate = candidate.float().to(reference.device)
-    if not torch.all(torch.isfinite(reference)) or not torch.all(torch.isfinite(candidate)):
+    (r, c), gpu, _ = N.to_gpu([reference, candidate])
+    r, c = r.float().contiguous(), c.float().contiguous()
+    if not torch.all(torch.isfinite(r)) or not torch.all(torch.isfinite(c)):
         raise ValueError("covariances must be finite")
-    reference_norm = torch.linalg.vector_norm(reference.double())
-    reference_diagonal = torch.diagonal(reference).double()
-    candidate_diagonal = torch.diagonal(candidate).double()
-    diagonal_denominator = torch.linalg.vector_norm(reference_diagonal) * torch.linalg.vector_norm(
-        candidate_diagonal
-    )
-    trace = torch.trace(reference.double())
+    k = r.shape[0]
+    ws = torch.empty(256 * 8, dtype=torch.float64, device=gpu)
+    out = torch.empty(8, dtype=torch.float64, device=gpu)
+    N.call("kq_covariance_comparison_sums", N.ptr(r), N.ptr(c), k, N.ptr(ws), N.ptr(out),
+           N.stream(gpu))
+    s_dd, s_rr, tr_r, tr_c, d_rr, d_cc, d_rc, asym = (float(v) for v in out.cpu().tolist())
+    reference_norm = math.sqrt(s_rr)
+    diagonal_denominator = math.sqrt(d_rr) * math.sqrt(d_cc)
     return {
-        "relative_frobenius_difference": float(
-            torch.linalg.vector_norm((candidate - reference).double()) / reference_norm
-        )
+        "relative_frobenius_difference": math.sqrt(s_dd) / reference_norm
         if reference_norm > 0
         else math.inf,
-        "trace_ratio": float(torch.trace(candidate.double()) / trace) if trace != 0 else math.inf,
-        "diagonal_cosine_similarity": float(
-            torch.dot(reference_diagonal, candidate_diagonal) / diagonal_denominator
-        )
+        "trace_ratio": tr_c / tr_r if tr_r != 0 else math.inf,
+        "diagonal_cosine_similarity": d_rc / diagonal_denominator
         if diagonal_denominator > 0
         else 0.0,
-        "candidate_symmetry_max_abs": float((candidate - candidate.T).abs().max()),
+        "candidate_symmetry_max_abs": float(torch.tensor(asym, dtype=torch.float32)),
     }
+
+
+# -------------------------------------------------------- per-expert Hessians --
+
+def _grouped(x: torch.Tensor, k: int, offsets: torch.Tensor, groups: int, index, weights,
+             flags: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """Finalized [groups, k, k] covariances and f64 denominators [groups]."""
+    gpu = x.device
+    kp = x.shape[1]
+    acc = torch.empty(groups, kp, kp, dtype=torch.float32, device=gpu)
+    N.call("kq_syrk_grouped", N.DTYPE_CODES[x.dtype], N.ptr(x), kp, N.ptr(offsets), groups, N.ptr(index),
+           N.ptr(weights), kp, N.ptr(acc), flags, N.stream(gpu))
+    sq = N.SYRK_SQUARE_WEIGHTS if flags & N.SYRK_SQUARE_WEIGHTS else 0
+    denominators = _weight_sums(weights, offsets, groups, sq)
+    out = torch.empty_like(acc)
+    N.call("kq_syrk_finalize_grouped", N.ptr(acc), kp, groups, N.ptr(denominators), N.ptr(out),
+           N.stream(gpu))
+    del acc
+    if kp != k:
+        out = out[:, :k, :k].contiguous()
+    return out, denominators
+
+
+def expert_hessians(
+    inputs: torch.Tensor,
+    route_ids: torch.Tensor,
+    gates: torch.Tensor,
+    experts: int,
+    *,
+    gate_square: bool = True,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Every expert's gate^2-weighted covariance of the token rows routed to it.
+
+    ``inputs`` [T, K]; ``route_ids`` / ``gates`` [T, topk].  Expert e gets
+    sum(g^2 x x^T) / sum(g^2) over its routed rows in token order, exactly the
+    ``weighted_covariance(rows_e, gates_e.square())`` that
+    ``build_expert_hessians`` (kquant/qsrt_candidates.py:534-586) forms per
+    expert, for all experts in one routing sort and one grouped SYRK launch.
+    Returns (H [E, K, K] fp32, denominators [E] f64, row counts [E] int64);
+    experts without rows get zeros and denominator 0.
+    """
+
+    if inputs.ndim != 2 or route_ids.ndim != 2 or route_ids.shape != gates.shape:
+        raise ValueError("inputs must be [T, K] and route_ids / gates [T, topk]")
+    if route_ids.shape[0] != inputs.shape[0]:
+        raise ValueError("route_ids rows must match inputs")
+    (x, ids, g), gpu, _ = N.to_gpu([inputs, route_ids, gates])
+    x, k = _prepare_rows(x, gpu)
+    tokens, topk = map(int, ids.shape)
+    ids = N.aligned(ids.to(torch.int32), 4)
+    g = N.aligned(g.float(), 4)
+    lib = N.library()
+    ws = torch.empty(max(int(lib.kq_route_sort_workspace_size(tokens, topk, experts)), 256),
+                     dtype=torch.uint8, device=gpu)
+    offsets = torch.empty(experts + 1, dtype=torch.int64, device=gpu)
+    rows = torch.empty(max(tokens * topk, 1), dtype=torch.int32, device=gpu)
+    sorted_w = torch.empty(max(tokens * topk, 1), dtype=torch.float32, device=gpu)
+    N.call("kq_route_sort", N.ptr(ids), tokens, topk, experts, N.ptr(g), N.ptr(offsets), N.ptr(rows),
+           None, N.ptr(sorted_w), N.ptr(ws), ws.numel(), N.stream(gpu))
+    flags = N.SYRK_SQUARE_WEIGHTS if gate_square else 0
+    h, denominators = _grouped(x, k, offsets, experts, rows, sorted_w, flags)
+    return h, denominators, offsets[1:] - offsets[:-1]
+
+
+def expert_hessians_from_rows(
+    rows: torch.Tensor,
+    offsets: torch.Tensor,
+    weights: torch.Tensor | None = None,
+    *,
+    square_weights: bool = False,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-group covariances of rows already grouped by expert.
+
+    ``rows`` [P, K] with group g at rows [offsets[g], offsets[g+1]) (the
+    per-expert post-SiTU rows of the H2 fit, kquant/qsrt_candidates.py:
+    577-583), optional row ``weights`` [P] (squared first when
+    ``square_weights``).  Returns (H [G, K, K], denominators [G] f64).
+    """
+
+    if rows.ndim != 2 or offsets.ndim != 1 or offsets.numel() < 2:
+        raise ValueError("rows must be [P, K] and offsets [G + 1]")
+    host_offsets = offsets.detach().to("cpu", torch.int64)
+    if (int(host_offsets[0]) != 0 or bool((host_offsets[1:] < host_offsets[:-1]).any())
+            or int(host_offsets[-1]) > rows.shape[0]):
+        raise ValueError("offsets must rise from 0 to at most the number of rows")
+    if weights is not None and (weights.ndim != 1 or weights.shape[0] < int(host_offsets[-1])):
+        raise ValueError("weights must cover every grouped row")
+    (x, o, w), gpu, _ = N.to_gpu([rows, offsets, weights])
+    x, k = _prepare_rows(x, gpu)
+    o = N.aligned(o.to(torch.int64), 8)
+    if w is not None:
+        w = N.aligned(w.float(), 4)
+    flags = N.SYRK_SQUARE_WEIGHTS if square_weights else 0
+    return _grouped(x, k, o, int(o.numel()) - 1, None, w, flags)
+
+
+def build_expert_hessians(
+    inputs: torch.Tensor,
+    gates: torch.Tensor,
+    source_middle: torch.Tensor,
+    *,
+    global_h13: torch.Tensor,
+    global_h2: torch.Tensor,
+    device: torch.device,
+    h13_alpha: float = 0.0,
+    h2_alpha: float | None = None,
+    chunk_rows: int = 256,
+    max_local_alpha: float = 0.75,
+) -> tuple[torch.Tensor, torch.Tensor, dict[str, float | str]]:
+    """H13 and support-aware post-SiTU H2 of one expert
+    (kquant/qsrt_candidates.py:534-618; defaults are the reference's PHASE1
+    constants kquant/qsrt.py:204-209: h13_alpha 0, H2 weighted OAS toward the
+    scaled identity capped at 0.75).  Weights are gates^2."""
+
+    if inputs.ndim != 2 or inputs.shape[0] != gates.shape[0]:
+        raise ValueError("invalid expert input covariance samples")
+    if source_middle.ndim != 2 or source_middle.shape[0] != inputs.shape[0]:
+        raise ValueError("source middle rows do not match expert inputs")
+    if global_h2.shape != (source_middle.shape[1], source_middle.shape[1]):
+        raise ValueError("global H2 dimension does not match source middle rows")
+    (g,), gpu, _ = N.to_gpu([gates])
+    g = N.aligned(g.float().contiguous(), 4)
+    offsets = _single_group(int(g.numel()), gpu)
+    h13_weight = float(_weight_sums(g, offsets, 1, N.SYRK_SQUARE_WEIGHTS).item())
+    global_h13 = global_h13.to(device=device, dtype=torch.float32)
+    if h13_alpha == 0.0:
+        h13 = global_h13
+    else:
+        local_h13, _ = expert_hessians_from_rows(inputs, offsets, g, square_weights=True)
+        h13 = shrink_covariance(global_h13, local_h13[0], h13_alpha).to(device)
+    local_h2, h2_den = expert_hessians_from_rows(source_middle, offsets, g, square_weights=True)
+    h2_weight = float(h2_den[0].item())
+    if not math.isclose(h13_weight, h2_weight, rel_tol=1e-9, abs_tol=1e-12):
+        raise ValueError("H13 and H2 expert covariance weights differ")
+    local_h2 = local_h2[0]
+    if h2_alpha is None:
+        square = (g * g).contiguous()
+        h2, shrinkage = adaptive_identity_shrinkage(local_h2, square, max_local_alpha=max_local_alpha)
+        evidence: dict[str, float | str] = {
+            "h2_shrinkage_policy": "weighted_oas_scaled_identity",
+            "h2_local_alpha": shrinkage["local_alpha"],
+            "h2_local_alpha_cap": shrinkage["max_local_alpha"],
+            "h2_effective_sample_size": shrinkage["effective_sample_size"],
+            "h2_oas_shrinkage": shrinkage["oas_shrinkage"],
+            "h2_identity_scale": shrinkage["identity_scale"],
+        }
+    else:
+        dimension = local_h2.shape[0]
+        ws = torch.empty(2 * N.COV_STATS_PARTS, dtype=torch.float64, device=gpu)
+        stats = torch.empty(2, dtype=torch.float64, device=gpu)
+        N.call("kq_cov_stats", N.ptr(local_h2), dimension, N.ptr(ws), N.ptr(stats), N.stream(gpu))
+        identity_scale = float(torch.tensor(float(stats[0].item()), dtype=torch.float32)) / dimension
+        h2 = torch.empty_like(local_h2)
+        N.call("kq_sym_lerp", None, float(torch.tensor(identity_scale, dtype=torch.float32)),
+               N.ptr(local_h2), dimension, float(h2_alpha), N.ptr(h2), N.stream(gpu))
+        evidence = {
+            "h2_shrinkage_policy": "fixed_alpha_scaled_identity",
+            "h2_local_alpha": float(h2_alpha),
+            "h2_local_alpha_cap": float(h2_alpha),
+            "h2_identity_scale": identity_scale,
+        }
+    return h13, h2.to(device), {"gate_square_sum": h13_weight, "h13_local_alpha": float(h13_alpha),
+                                **evidence}

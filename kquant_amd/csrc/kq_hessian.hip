@@ -52,13 +52,24 @@ __device__ __forceinline__ void split_bf16(float v, uint32_t& hi, uint32_t& lo) 
 }
 
 // IN: 0 bf16, 1 f16, 2 f32.  SPLIT: operands carry a bf16 residual part
-// (needed for weights or non-bf16 inputs).
-template <int IN, bool SPLIT, bool WEIGHTED>
+// (needed for weights or non-bf16 inputs).  GROUPED: blockIdx.y is a group
+// (an expert) whose rows are list positions [offsets[g], offsets[g+1]), row
+// index[p] of x (or p itself without an index), weight w[p] (squared when
+// square_w), and whose k x k result sits at acc + g * acc_stride.
+template <int IN, bool SPLIT, bool WEIGHTED, bool GROUPED>
 __global__ __launch_bounds__(256, 1) void syrk_upper_kernel(
     const void* __restrict__ x, int64_t ld, int64_t n, int64_t k,
     const float* __restrict__ w, float* __restrict__ acc, int64_t ld_acc, int ntiles,
-    int overwrite) {
+    int overwrite, const int64_t* __restrict__ offsets, const int32_t* __restrict__ index,
+    int64_t acc_stride, int square_w) {
   using namespace syrk;
+  int64_t list0 = 0;
+  if (GROUPED) {
+    const int64_t g = blockIdx.y;
+    list0 = offsets[g];
+    n = offsets[g + 1] - list0;
+    acc += g * acc_stride;
+  }
   // ---- tile coordinates: linear index -> (ti <= tj) over the upper triangle
   int rem = blockIdx.x, ti = 0;
   while (rem >= ntiles - ti) { rem -= ntiles - ti; ++ti; }
@@ -85,12 +96,16 @@ __global__ __launch_bounds__(256, 1) void syrk_upper_kernel(
   auto load_step = [&](int64_t t0) {
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
-      const int64_t tok = t0 + tg * 8 + t;
+      const int64_t pos = t0 + tg * 8 + t;
       u32x4_t v = {0u, 0u, 0u, 0u};
       u32x4_t vlo = {0u, 0u, 0u, 0u};
-      if (feat_ok && tok < n) {
+      if (feat_ok && pos < n) {
+        const int64_t tok = !GROUPED ? pos : (index ? (int64_t)index[list0 + pos] : list0 + pos);
         float wt = 1.0f;
-        if (WEIGHTED) wt = (slab == 1) ? w[tok] : 1.0f;
+        if (WEIGHTED && slab == 1) {
+          wt = w[GROUPED ? list0 + pos : pos];
+          if (GROUPED && square_w) wt *= wt;
+        }
         if (IN == 0 && !SPLIT) {
           v = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(x) + tok * ld + feat0);
         } else {
@@ -327,6 +342,110 @@ __global__ __launch_bounds__(256) void cov_stats_final_kernel(const double* __re
   }
 }
 
+// Grouped finalize: out[g] = sym(acc[g]) / denominators[g] (zeros when the
+// group has no weight), blockIdx.z = group.
+__global__ __launch_bounds__(256) void syrk_finalize_grouped_kernel(
+    const float* __restrict__ acc, int64_t k, const double* __restrict__ denominators,
+    float* __restrict__ out) {
+  const int64_t g = blockIdx.z, i = blockIdx.y;
+  const int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (j >= k) return;
+  const double d = denominators[g];
+  const float inv = d > 0.0 ? (float)(1.0 / d) : 0.0f;
+  const float* a = acc + g * k * k;
+  const int64_t ti = i / syrk::TILE, tj = j / syrk::TILE;
+  const float v = ti <= tj ? a[i * k + j] : a[j * k + i];
+  out[g * k * k + i * k + j] = v * inv;
+}
+
+__global__ __launch_bounds__(256) void syrk_sym_diag_grouped_kernel(float* __restrict__ out, int64_t k) {
+  const int64_t g = blockIdx.z, t = blockIdx.y;
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t r = e / syrk::TILE, c = e % syrk::TILE;
+  if (r >= syrk::TILE || c <= r) return;
+  const int64_t i = t * syrk::TILE + r, j = t * syrk::TILE + c;
+  if (i >= k || j >= k) return;
+  float* o = out + g * k * k;
+  const float m = (o[i * k + j] + o[j * k + i]) * 0.5f;
+  o[i * k + j] = m;
+  o[j * k + i] = m;
+}
+
+// Per-group f64 sums of the row weights (of their fp32 squares with
+// square_w; of 1 per row without weights): one workgroup per group, a fixed
+// reduction tree, so the result is deterministic.
+__global__ __launch_bounds__(256) void segment_weight_sum_kernel(const float* __restrict__ w,
+                                                                 const int64_t* __restrict__ offsets,
+                                                                 int square_w, double* __restrict__ out) {
+  __shared__ double part[256];
+  const int64_t g = blockIdx.x;
+  const int64_t p0 = offsets[g], p1 = offsets[g + 1];
+  double s = 0.0;
+  for (int64_t p = p0 + threadIdx.x; p < p1; p += 256) {
+    float v = w ? w[p] : 1.0f;
+    if (square_w == 1) v = v * v;  // fp32 square, then f64 sum
+    const double d = (double)v;
+    s += square_w == 2 ? d * d : d;  // f64 square
+  }
+  part[threadIdx.x] = s;
+  __syncthreads();
+  for (int h = 128; h > 0; h >>= 1) {
+    if ((int)threadIdx.x < h) part[threadIdx.x] += part[threadIdx.x + h];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) out[g] = part[0];
+}
+
+// Sums behind covariance_comparison (kquant/candidate_hessian.py:219-258), in
+// f64 over fp32 [k, k] matrices R (reference) and C (candidate): per block
+// {sum (C-R)^2 with C-R formed in fp32, sum R^2, tr R, tr C, sum diag R^2,
+// sum diag C^2, sum diag R*C, max |C - C^T|}.
+constexpr int CMP_PARTS = 256;
+constexpr int CMP_FIELDS = 8;
+__global__ __launch_bounds__(256) void cov_compare_partial_kernel(const float* __restrict__ r,
+                                                                  const float* __restrict__ c, int64_t k,
+                                                                  double* __restrict__ ws) {
+  __shared__ double red[CMP_FIELDS][256];
+  double f[CMP_FIELDS] = {0, 0, 0, 0, 0, 0, 0, 0};
+  const int64_t total = k * k;
+  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)CMP_PARTS * 256) {
+    const int64_t i = e / k, j = e - i * k;
+    const float rv = r[e], cv = c[e];
+    const double d = (double)(cv - rv);
+    f[0] += d * d;
+    f[1] += (double)rv * rv;
+    if (i == j) {
+      f[2] += rv;
+      f[3] += cv;
+      f[4] += (double)rv * rv;
+      f[5] += (double)cv * cv;
+      f[6] += (double)rv * cv;
+    }
+    f[7] = fmax(f[7], (double)fabsf(cv - c[j * k + i]));
+  }
+  const int t = threadIdx.x;
+  for (int q = 0; q < CMP_FIELDS; ++q) red[q][t] = f[q];
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if (t < w) {
+      for (int q = 0; q < 7; ++q) red[q][t] += red[q][t + w];
+      red[7][t] = fmax(red[7][t], red[7][t + w]);
+    }
+    __syncthreads();
+  }
+  if (t < CMP_FIELDS) ws[blockIdx.x * CMP_FIELDS + t] = red[t][0];
+}
+
+__global__ void cov_compare_final_kernel(const double* __restrict__ ws, double* __restrict__ out) {
+  if (threadIdx.x != 0) return;
+  double f[CMP_FIELDS] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int b = 0; b < CMP_PARTS; ++b) {
+    for (int q = 0; q < 7; ++q) f[q] += ws[b * CMP_FIELDS + q];
+    f[7] = fmax(f[7], ws[b * CMP_FIELDS + 7]);
+  }
+  for (int q = 0; q < CMP_FIELDS; ++q) out[q] = f[q];
+}
+
 }  // namespace kq
 
 using namespace kq;
@@ -353,17 +472,20 @@ extern "C" int kq_cov_stats(const float* h, int64_t k, double* workspace, double
   return kq_check_launch(hipGetLastError(), "kq_cov_stats");
 }
 
-template <int IN, bool SPLIT, bool WEIGHTED>
+template <int IN, bool SPLIT, bool WEIGHTED, bool GROUPED>
 static hipError_t launch_syrk(const void* x, int64_t ld, int64_t n, int64_t k, const float* w,
-                              float* acc, int64_t ld_acc, int overwrite, hipStream_t st) {
+                              float* acc, int64_t ld_acc, int overwrite, hipStream_t st,
+                              const int64_t* offsets = nullptr, const int32_t* index = nullptr,
+                              int groups = 1, int square_w = 0) {
   const int nt = (int)((k + syrk::TILE - 1) / syrk::TILE);
   const int ntiles = nt * (nt + 1) / 2;
   const int nslab = SPLIT ? 4 : 2;
   const size_t lds = (size_t)2 * nslab * syrk::SLAB_BYTES;
-  auto kern = syrk_upper_kernel<IN, SPLIT, WEIGHTED>;
+  auto kern = syrk_upper_kernel<IN, SPLIT, WEIGHTED, GROUPED>;
   hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return e;
-  kern<<<dim3(ntiles), dim3(256), lds, st>>>(x, ld, n, k, w, acc, ld_acc, nt, overwrite);
+  kern<<<dim3(ntiles, groups), dim3(256), lds, st>>>(x, ld, n, k, w, acc, ld_acc, nt, overwrite, offsets,
+                                                     index, k * ld_acc, square_w);
   return hipGetLastError();
 }
 
@@ -386,14 +508,14 @@ extern "C" int kq_syrk_accumulate(int in_dtype, const void* x, int64_t ld, int64
   hipError_t e;
   const bool weighted = weights != nullptr;
   if (in_dtype == KQ_DT_BF16) {
-    e = weighted ? launch_syrk<0, true, true>(x, ld, n, k, weights, acc, ld_acc, overwrite, st)
-                 : launch_syrk<0, false, false>(x, ld, n, k, weights, acc, ld_acc, overwrite, st);
+    e = weighted ? launch_syrk<0, true, true, false>(x, ld, n, k, weights, acc, ld_acc, overwrite, st)
+                 : launch_syrk<0, false, false, false>(x, ld, n, k, weights, acc, ld_acc, overwrite, st);
   } else if (in_dtype == KQ_DT_F16) {
-    e = weighted ? launch_syrk<1, true, true>(x, ld, n, k, weights, acc, ld_acc, overwrite, st)
-                 : launch_syrk<1, true, false>(x, ld, n, k, weights, acc, ld_acc, overwrite, st);
+    e = weighted ? launch_syrk<1, true, true, false>(x, ld, n, k, weights, acc, ld_acc, overwrite, st)
+                 : launch_syrk<1, true, false, false>(x, ld, n, k, weights, acc, ld_acc, overwrite, st);
   } else {
-    e = weighted ? launch_syrk<2, true, true>(x, ld, n, k, weights, acc, ld_acc, overwrite, st)
-                 : launch_syrk<2, true, false>(x, ld, n, k, weights, acc, ld_acc, overwrite, st);
+    e = weighted ? launch_syrk<2, true, true, false>(x, ld, n, k, weights, acc, ld_acc, overwrite, st)
+                 : launch_syrk<2, true, false, false>(x, ld, n, k, weights, acc, ld_acc, overwrite, st);
   }
   return kq_check_launch(e, "kq_syrk_accumulate");
 }
@@ -423,4 +545,69 @@ extern "C" int kq_syrk_finalize(const float* acc, int64_t ld_acc, int64_t k, dou
     e = hipGetLastError();
   }
   return kq_check_launch(e, "kq_syrk_finalize");
+}
+
+extern "C" int kq_syrk_grouped(int in_dtype, const void* x, int64_t ld, const int64_t* offsets,
+                               int groups, const int32_t* row_index, const float* weights, int64_t k,
+                               float* acc, uint32_t flags, void* stream) {
+  if (in_dtype < KQ_DT_BF16 || in_dtype > KQ_DT_F32)
+    return kq_fail(KQ_ERR_INVALID, "kq_syrk_grouped: unknown input dtype %d", in_dtype);
+  if (groups < 1 || groups > 65535 || k <= 0 || k % 8 != 0 || ld < k || ld % 8 != 0 || !offsets)
+    return kq_fail(KQ_ERR_INVALID,
+                   "kq_syrk_grouped: need 1 <= groups <= 65535, k %% 8 == 0, ld >= k, ld %% 8 == 0 "
+                   "(groups=%d k=%lld ld=%lld)", groups, (long long)k, (long long)ld);
+  if (kq_misaligned(x, 16) || kq_misaligned(offsets, 8) || kq_misaligned(row_index, 4))
+    return kq_fail(KQ_ERR_INVALID, "kq_syrk_grouped: misaligned rows, offsets or index");
+  if (k > 16384) return kq_fail(KQ_ERR_LIMIT, "kq_syrk_grouped: k=%lld exceeds 16384", (long long)k);
+  const int sq = (flags & KQ_SYRK_SQUARE_WEIGHTS) ? 1 : 0;
+  hipStream_t st = (hipStream_t)stream;
+  hipError_t e;
+  const bool weighted = weights != nullptr;
+  if (in_dtype == KQ_DT_BF16)
+    e = weighted ? launch_syrk<0, true, true, true>(x, ld, 0, k, weights, acc, k, 1, st, offsets, row_index, groups, sq)
+                 : launch_syrk<0, false, false, true>(x, ld, 0, k, weights, acc, k, 1, st, offsets, row_index, groups, sq);
+  else if (in_dtype == KQ_DT_F16)
+    e = weighted ? launch_syrk<1, true, true, true>(x, ld, 0, k, weights, acc, k, 1, st, offsets, row_index, groups, sq)
+                 : launch_syrk<1, true, false, true>(x, ld, 0, k, weights, acc, k, 1, st, offsets, row_index, groups, sq);
+  else
+    e = weighted ? launch_syrk<2, true, true, true>(x, ld, 0, k, weights, acc, k, 1, st, offsets, row_index, groups, sq)
+                 : launch_syrk<2, true, false, true>(x, ld, 0, k, weights, acc, k, 1, st, offsets, row_index, groups, sq);
+  return kq_check_launch(e, "kq_syrk_grouped");
+}
+
+extern "C" int kq_segment_weight_sums(const float* weights, const int64_t* offsets, int groups,
+                                      uint32_t flags, double* out, void* stream) {
+  if (groups < 1 || !offsets || !out || kq_misaligned(offsets, 8) || kq_misaligned(out, 8))
+    return kq_fail(KQ_ERR_INVALID, "kq_segment_weight_sums: bad arguments");
+  const int mode = (flags & KQ_SUM_SQUARE_F64) ? 2 : (flags & KQ_SYRK_SQUARE_WEIGHTS) ? 1 : 0;
+  segment_weight_sum_kernel<<<groups, 256, 0, (hipStream_t)stream>>>(weights, offsets, mode, out);
+  return kq_check_launch(hipGetLastError(), "kq_segment_weight_sums");
+}
+
+extern "C" int kq_syrk_finalize_grouped(const float* acc, int64_t k, int groups,
+                                        const double* denominators, float* out, void* stream) {
+  if (k <= 0 || groups < 1 || groups > 65535 || !denominators)
+    return kq_fail(KQ_ERR_INVALID, "kq_syrk_finalize_grouped: bad sizes (k=%lld groups=%d)",
+                   (long long)k, groups);
+  if (acc == out) return kq_fail(KQ_ERR_INVALID, "kq_syrk_finalize_grouped: acc and out must not alias");
+  if (k > 65535) return kq_fail(KQ_ERR_LIMIT, "kq_syrk_finalize_grouped: k too large");
+  hipStream_t st = (hipStream_t)stream;
+  syrk_finalize_grouped_kernel<<<dim3((unsigned)((k + 255) / 256), (unsigned)k, (unsigned)groups), 256, 0,
+                                 st>>>(acc, k, denominators, out);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return kq_check_launch(e, "kq_syrk_finalize_grouped");
+  const unsigned nt = (unsigned)((k + syrk::TILE - 1) / syrk::TILE);
+  syrk_sym_diag_grouped_kernel<<<dim3((syrk::TILE * syrk::TILE + 255) / 256, nt, (unsigned)groups), 256, 0,
+                                 st>>>(out, k);
+  return kq_check_launch(hipGetLastError(), "kq_syrk_finalize_grouped");
+}
+
+extern "C" int kq_covariance_comparison_sums(const float* reference, const float* candidate, int64_t k,
+                                             double* workspace, double* out, void* stream) {
+  if (k <= 0 || !reference || !candidate || kq_misaligned(workspace, 8) || kq_misaligned(out, 8))
+    return kq_fail(KQ_ERR_INVALID, "kq_covariance_comparison_sums: bad arguments");
+  hipStream_t st = (hipStream_t)stream;
+  cov_compare_partial_kernel<<<CMP_PARTS, 256, 0, st>>>(reference, candidate, k, workspace);
+  cov_compare_final_kernel<<<1, 64, 0, st>>>(workspace, out);
+  return kq_check_launch(hipGetLastError(), "kq_covariance_comparison_sums");
 }

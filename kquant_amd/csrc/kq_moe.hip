@@ -627,6 +627,23 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restric
   }
 }
 
+// Expert-sorted pair list -> int64 offsets, token rows and gathered weights.
+__global__ __launch_bounds__(256) void route_rows_kernel(const int* __restrict__ offsets32, int experts,
+                                                         const int* __restrict__ sorted, int topk,
+                                                         const float* __restrict__ pair_w,
+                                                         int64_t* __restrict__ offsets, int32_t* __restrict__ rows,
+                                                         int32_t* __restrict__ pairs_out,
+                                                         float* __restrict__ w_out) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i <= experts) offsets[i] = offsets32[i];
+  const int total = offsets32[experts];
+  if (i >= total) return;
+  const int pair = sorted[i];
+  rows[i] = pair / topk;
+  if (pairs_out) pairs_out[i] = pair;
+  if (w_out) w_out[i] = pair_w[pair];
+}
+
 }  // namespace moe
 }  // namespace kq
 
@@ -782,4 +799,74 @@ extern "C" int kq_moe_forward(int activation, float act_beta, float act_linear_b
   else
     moe_combine_kernel<0><<<cgrid, 256, 0, st>>>(y, route_ids, topk, experts, hidden, out);
   return kq_check_launch(hipGetLastError(), "kq_moe_forward/combine");
+}
+
+// Routing sort alone (for per-expert calibration statistics): the pairs
+// (t, s) of route_ids [tokens, topk] grouped by expert, stable in pair order.
+static size_t route_sort_layout(int64_t pairs, int experts, size_t* parts) {
+  const int64_t nblk = (pairs + PREP - 1) / PREP;
+  const int64_t max_large = pairs / (SMALL_MAX + 1) + pairs / BM + 1;
+  size_t o = 0;
+  parts[0] = o; o = align256(o + sizeof(int) * experts);                 // counts
+  parts[1] = o; o = align256(o + sizeof(int) * (experts + 1));           // offsets32
+  parts[2] = o; o = align256(o + sizeof(int) * (size_t)nblk * experts);  // block counts
+  parts[3] = o; o = align256(o + sizeof(int) * (size_t)pairs);           // sorted pairs
+  parts[4] = o; o = align256(o + sizeof(int) * experts);                 // small list
+  parts[5] = o; o = align256(o + sizeof(int) * 2 * (size_t)max_large);   // large tiles
+  parts[6] = o; o = align256(o + sizeof(int) * 4);                       // meta
+  return o;
+}
+
+extern "C" int64_t kq_route_sort_workspace_size(int64_t tokens, int topk, int experts) {
+  if (tokens < 0 || topk <= 0 || experts <= 0) return -1;
+  size_t parts[7];
+  return (int64_t)route_sort_layout(tokens * topk, experts, parts);
+}
+
+extern "C" int kq_route_sort(const int32_t* route_ids, int64_t tokens, int topk, int experts,
+                             const float* pair_weights, int64_t* offsets, int32_t* rows,
+                             int32_t* sorted_pairs, float* sorted_weights, void* workspace,
+                             int64_t workspace_bytes, void* stream) {
+  if (tokens < 0 || topk <= 0 || topk > 64 || experts <= 0 || experts > MAX_EXPERTS)
+    return kq_fail(KQ_ERR_INVALID, "kq_route_sort: need 1 <= topk <= 64, 1 <= experts <= %d",
+                   MAX_EXPERTS);
+  if (tokens * topk > INT32_MAX / 2) return kq_fail(KQ_ERR_LIMIT, "kq_route_sort: too many pairs");
+  if (sorted_weights && !pair_weights)
+    return kq_fail(KQ_ERR_INVALID, "kq_route_sort: sorted_weights needs pair_weights");
+  size_t parts[7];
+  const int64_t pairs = tokens * topk;
+  const size_t need = route_sort_layout(pairs, experts, parts);
+  if (workspace_bytes < (int64_t)need || kq_misaligned(workspace, 256))
+    return kq_fail(KQ_ERR_INVALID, "kq_route_sort: workspace needs %lld bytes, 256-byte aligned",
+                   (long long)need);
+  if (kq_misaligned(offsets, 8)) return kq_fail(KQ_ERR_INVALID, "kq_route_sort: misaligned offsets");
+  hipStream_t st = (hipStream_t)stream;
+  unsigned char* w = (unsigned char*)workspace;
+  int* counts = (int*)(w + parts[0]);
+  int* off32 = (int*)(w + parts[1]);
+  int* block_counts = (int*)(w + parts[2]);
+  int* sorted = (int*)(w + parts[3]);
+  int* small_list = (int*)(w + parts[4]);
+  int* large_tiles = (int*)(w + parts[5]);
+  int* meta = (int*)(w + parts[6]);
+  const int64_t nblk = (pairs + PREP - 1) / PREP;
+  const int max_large = (int)(pairs / (SMALL_MAX + 1) + pairs / BM + 1);
+  hipError_t e;
+  if (pairs <= PREP_ONE) {
+    route_prep_one_kernel<<<1, 1024, 0, st>>>(route_ids, (int)pairs, experts, counts, off32, sorted,
+                                               small_list, large_tiles, meta, max_large);
+  } else {
+    route_hist_kernel<<<(unsigned)nblk, PREP, 0, st>>>(route_ids, pairs, experts, block_counts);
+    if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_route_sort");
+    route_scan_kernel<<<1, 1024, 0, st>>>(block_counts, (int)nblk, experts, counts, off32, small_list,
+                                          large_tiles, meta, max_large);
+    if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_route_sort");
+    route_scatter_kernel<<<(unsigned)nblk, PREP, 0, st>>>(route_ids, pairs, experts, off32,
+                                                          block_counts, sorted);
+  }
+  if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_route_sort");
+  const int64_t n = pairs > experts + 1 ? pairs : experts + 1;
+  route_rows_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(off32, experts, sorted, topk, pair_weights,
+                                                                 offsets, rows, sorted_pairs, sorted_weights);
+  return kq_check_launch(hipGetLastError(), "kq_route_sort");
 }

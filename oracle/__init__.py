@@ -337,17 +337,19 @@ def damp_diagonal(h: np.ndarray, sigma_reg: float) -> np.ndarray:
 
 def covariance_comparison(reference: np.ndarray, candidate: np.ndarray) -> dict:
     """kquant/candidate_hessian.py:219-258 (relative Frobenius in f64 etc.)."""
-    ref = np.asarray(reference, dtype=np.float32).astype(np.float64)
-    cand = np.asarray(candidate, dtype=np.float32).astype(np.float64)
+    ref32 = np.asarray(reference, dtype=np.float32)
+    cand32 = np.asarray(candidate, dtype=np.float32)
+    ref, cand = ref32.astype(np.float64), cand32.astype(np.float64)
     ref_norm = np.linalg.norm(ref)
     rd, cd = np.diag(ref), np.diag(cand)
     dd = np.linalg.norm(rd) * np.linalg.norm(cd)
     tr = np.trace(ref)
+    diff = (cand32 - ref32).astype(np.float64)  # (candidate - reference).double(): fp32 difference
     return {
-        "relative_frobenius_difference": float(np.linalg.norm(cand - ref) / ref_norm) if ref_norm > 0 else float("inf"),
+        "relative_frobenius_difference": float(np.linalg.norm(diff) / ref_norm) if ref_norm > 0 else float("inf"),
         "trace_ratio": float(np.trace(cand) / tr) if tr != 0 else float("inf"),
         "diagonal_cosine_similarity": float(rd @ cd / dd) if dd > 0 else 0.0,
-        "candidate_symmetry_max_abs": float(np.abs(cand - cand.T).max()),
+        "candidate_symmetry_max_abs": float(np.abs(cand32 - cand32.T).max()),
     }
 
 

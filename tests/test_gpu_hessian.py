@@ -144,3 +144,115 @@ def test_shrinkage_matches_reference_formulas(gpu):
     torch.testing.assert_close(ch.shrink_covariance(g, l, 0.25), 0.75 * g + 0.25 * l)
     diagnostics = ch.covariance_comparison(g, l)
     assert diagnostics["trace_ratio"] == 3.0
+
+
+def test_weighted_effective_sample_size_tracks_weight_concentration(gpu):
+    # tests/test_candidate_hessian.py:65-70
+    assert ch.weighted_effective_sample_size(torch.ones(8)) == pytest.approx(8.0)
+    concentrated = ch.weighted_effective_sample_size(torch.tensor([10.0, 1.0, 1.0, 1.0]))
+    assert 1.0 < concentrated < 4.0
+    assert concentrated == pytest.approx(13.0 ** 2 / 103.0, rel=1e-12)
+
+
+def _routing(tokens, topk, experts, seed):
+    g = np.random.default_rng(seed)
+    p = np.arange(1, experts + 1, dtype=np.float64) ** -1.1
+    p /= p.sum()
+    ids = np.stack([g.choice(experts, size=topk, replace=False, p=p) for _ in range(tokens)])
+    ids = ids.astype(np.int32)
+    ids[g.random(ids.shape) < 0.02] = -1          # dropped slots
+    ids[ids == experts - 1] = experts + 3         # expert E-1 never receives rows
+    gates = g.random(ids.shape).astype(np.float32)
+    return ids, gates
+
+
+@pytest.mark.parametrize("k", [256, 200])
+def test_expert_hessians_match_per_expert_oracle(gpu, k):
+    """All experts in one routing sort + one grouped SYRK launch vs the oracle's
+    weighted_covariance of each expert's rows (token order, weight g^2)."""
+    tokens, topk, experts = 1500, 4, 12
+    x = workloads.student_t4(tokens, k, seed=5)
+    ids, gates = _routing(tokens, topk, experts, 6)
+    h, den, counts = ch.expert_hessians(x.to(gpu), torch.from_numpy(ids), torch.from_numpy(gates), experts)
+    assert h.shape == (experts, k, k) and den.dtype == torch.float64
+    xf = x.float().numpy()
+    for e in range(experts):
+        mask = ids == e
+        rows = np.nonzero(mask.any(axis=1))[0]
+        assert int(counts[e]) == len(rows)
+        if not len(rows):
+            assert float(den[e]) == 0.0 and not torch.any(h[e] != 0)
+            continue
+        w = (gates * mask).sum(axis=1)[rows]
+        w2 = (w * w).astype(np.float32)
+        ref, denom = oracle.weighted_covariance(xf[rows], w2)
+        assert float(den[e]) == pytest.approx(denom, rel=1e-12)
+        got = h[e].cpu().numpy()
+        rel = np.linalg.norm(got - ref) / np.linalg.norm(ref)
+        assert rel <= 1e-5, (e, rel)
+        assert np.array_equal(got, got.T)
+
+
+def test_expert_hessians_from_rows_cfg4_expert_shape(gpu):
+    """Pre-grouped rows at the expert-down width K = 2048 (config 4 ii), unit
+    and fp32-squared weights, group sizes 0 .. 700."""
+    k = 2048
+    sizes = [0, 1, 7, 64, 700, 130]
+    n = sum(sizes)
+    x = workloads.student_t4(n, k, seed=8)
+    offsets = torch.tensor(np.concatenate([[0], np.cumsum(sizes)]), dtype=torch.int64)
+    w = torch.rand(n, generator=torch.Generator().manual_seed(2))
+    for weights, square in ((None, False), (w, True)):
+        h, den = ch.expert_hessians_from_rows(x.to(gpu), offsets, weights, square_weights=square)
+        for gi, (a, b) in enumerate(zip(offsets[:-1].tolist(), offsets[1:].tolist())):
+            if a == b:
+                assert float(den[gi]) == 0.0
+                continue
+            ww = np.ones(b - a, np.float32) if weights is None else (w[a:b].numpy() ** 2).astype(np.float32)
+            ref, denom = oracle.weighted_covariance(x[a:b].float().numpy(), ww)
+            rel = np.linalg.norm(h[gi].cpu().numpy() - ref) / np.linalg.norm(ref)
+            assert float(den[gi]) == pytest.approx(denom, rel=1e-12)
+            assert rel <= 1e-5, (gi, rel)
+
+
+def test_build_expert_hessians_composes_reference_steps(gpu):
+    """kquant/qsrt_candidates.py:534-618 on one expert, both H2 policies and a
+    nonzero H13 alpha, against the tested primitives composed as the reference does."""
+    g = torch.Generator().manual_seed(12)
+    n, hdim, idim = 300, 512, 256
+    inputs = torch.randn(n, hdim, generator=g)
+    middle = torch.randn(n, idim, generator=g) * 0.3
+    gates = torch.rand(n, generator=g)
+    global_h13 = torch.eye(hdim) * 0.5
+    global_h2 = torch.eye(idim)
+    w = gates.float().square()
+    for h13_alpha, h2_alpha in ((0.0, None), (0.3, 0.5)):
+        h13, h2, ev = ch.build_expert_hessians(inputs.to(gpu), gates.to(gpu), middle.to(gpu),
+                                               global_h13=global_h13, global_h2=global_h2, device=gpu,
+                                               h13_alpha=h13_alpha, h2_alpha=h2_alpha)
+        assert ev["gate_square_sum"] == pytest.approx(float(w.double().sum()), rel=1e-12)
+        local_h2, _ = ch.weighted_covariance(middle, w, device=gpu, return_cpu=False)
+        if h2_alpha is None:
+            want_h2, sh = ch.adaptive_identity_shrinkage(local_h2, w, max_local_alpha=0.75)
+            assert ev["h2_local_alpha"] == pytest.approx(sh["local_alpha"], rel=1e-6)
+        else:
+            scale = float(torch.trace(local_h2) / idim)
+            want_h2 = ch.shrink_covariance(torch.eye(idim, device=gpu) * scale, local_h2, h2_alpha)
+        assert ch.covariance_comparison(want_h2, h2)["relative_frobenius_difference"] <= 1e-5
+        if h13_alpha == 0.0:
+            assert torch.equal(h13.cpu(), global_h13)
+        else:
+            local_h13, _ = ch.weighted_covariance(inputs, w, device=gpu, return_cpu=False)
+            want = ch.shrink_covariance(global_h13.to(gpu), local_h13, h13_alpha)
+            assert ch.covariance_comparison(want, h13)["relative_frobenius_difference"] <= 1e-5
+
+
+def test_covariance_comparison_matches_oracle(gpu):
+    g = torch.Generator().manual_seed(13)
+    a = torch.randn(300, 300, generator=g)
+    r = a @ a.T / 300
+    c = r + 1e-4 * torch.randn(300, 300, generator=g)
+    got = ch.covariance_comparison(r.to(gpu), c.to(gpu))
+    want = oracle.covariance_comparison(r.numpy(), c.numpy())
+    for key, value in want.items():
+        assert got[key] == pytest.approx(value, rel=1e-9, abs=1e-12), key

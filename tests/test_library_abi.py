@@ -32,7 +32,8 @@ def test_python_binding_covers_every_entry_point():
     lib = _native.library()
     assert lib.kq_version() >> 16 == 1
     bound = set(_native.SIGNATURES) | {"kq_version", "kq_last_error", "kq_moe_workspace_size",
-                                        "kq_mx_linear_f32_workspace_size"}
+                                        "kq_mx_linear_f32_workspace_size",
+                                        "kq_route_sort_workspace_size"}
     assert set(declared_symbols()) <= bound
 
 

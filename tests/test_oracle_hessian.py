@@ -109,8 +109,3 @@ def test_shrink_covariance_rejects_invalid_alpha():
         ch.shrink_covariance(torch.eye(2), torch.eye(2), 1.1)
 
 
-def test_weighted_effective_sample_size_tracks_weight_concentration():
-    # tests/test_candidate_hessian.py:65-70 (pure host arithmetic)
-    assert ch.weighted_effective_sample_size(torch.ones(8)) == pytest.approx(8.0)
-    concentrated = ch.weighted_effective_sample_size(torch.tensor([10.0, 1.0, 1.0, 1.0]))
-    assert 1.0 < concentrated < 4.0
