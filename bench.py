@@ -251,6 +251,107 @@ def main() -> int:
         }
         del x4, acc
 
+    # --------------------------- config 4 (ii) per-expert Hessians, K=2048 --
+    if not args.quick and want("hessian_experts"):
+        ids, rw = workloads.zipf_routing(65536)
+        experts = workloads.EXPERTS
+        counts = torch.bincount(ids[ids >= 0].flatten().long(), minlength=experts)
+        offsets = torch.zeros(experts + 1, dtype=torch.int64)
+        offsets[1:] = torch.cumsum(counts, 0)
+        pairs = int(offsets[-1])
+        k2 = workloads.INTER
+        g = torch.Generator(device=dev).manual_seed(1)
+        rows = torch.empty(pairs, k2, dtype=torch.bfloat16, device=dev)
+        for c0 in range(0, pairs, 65536):  # Student-t(4) rows, generated in slabs
+            n = min(65536, pairs - c0)
+            z = torch.randn(n, k2, generator=g, device=dev)
+            chi = sum(torch.randn(n, k2, generator=g, device=dev).square() for _ in range(4))
+            rows[c0:c0 + n] = (z / torch.sqrt(chi / 4)).to(torch.bfloat16)
+        gates = torch.rand(pairs, generator=g, device=dev)
+        offsets_d = offsets.to(dev)
+        hacc = torch.empty(experts, k2, k2, dtype=torch.float32, device=dev)
+
+        def he_step():
+            N.call("kq_syrk_grouped", N.DT_BF16, N.ptr(rows), k2, N.ptr(offsets_d), experts, None,
+                   N.ptr(gates), k2, N.ptr(hacc), N.SYRK_SQUARE_WEIGHTS, stream)
+
+        the = _time_loop(torch, he_step, 3, 1)
+        flops = float((counts.double() * k2 * (k2 + 1)).sum())
+        hbytes = pairs * k2 * 2 + pairs * 4 + experts * k2 * k2 * 4
+        result["cfg4_hessian_experts_k2048"] = {
+            "workload": "cfg4 (ii): gate^2-weighted X^T X of each expert's routed rows, 65536 tokens "
+                        "top-8 Zipf(1.1) over 384 experts (524288 rows of 2048 bf16), one grouped launch",
+            "ms": round(the * 1e3, 3),
+            "tflops": round(flops / the / 1e12, 1),
+            "gbs": round(hbytes / the / 1e9, 1),
+            "roofline": _roofline("hbm", hbytes / the / 1e9),
+            "active_experts": int((counts > 0).sum()),
+        }
+        del rows, hacc
+
+    # ------------------------------------- scale-plane codecs and SQG tables --
+    if not args.quick and want("scale_planes"):
+        from kquant_amd import sqg_e4m3
+        w1 = workloads.cfg1_weight().to(dev)
+        _, plane = kq_mxfp4.mxfp4_quantize(w1)          # [7168, 64] E8M0 plane
+        prows, pcols = plane.shape
+        tiles = prows // 16
+        fixed = torch.empty(tiles * 16 * (1 + pcols // 8), dtype=torch.uint8, device=dev)
+        toff = torch.empty(tiles + 1, dtype=torch.int64, device=dev)
+        N.call("kq_x4t_analyze", N.ptr(plane), 1, prows, pcols, N.ptr(fixed), N.ptr(toff), stream)
+        n_exc = int(toff[-1].item())
+        exc = torch.empty(max(n_exc, 1), dtype=torch.uint32, device=dev)
+        out_plane = torch.empty_like(plane)
+
+        def x4t_pack():
+            N.call("kq_x4t_analyze", N.ptr(plane), 1, prows, pcols, N.ptr(fixed), N.ptr(toff), stream)
+            N.call("kq_x4t_emit_exceptions", N.ptr(plane), 1, prows, pcols, N.ptr(fixed), N.ptr(toff),
+                   N.ptr(exc), stream)
+
+        def x4t_decode():
+            N.call("kq_x4t_decode", N.ptr(fixed), N.ptr(exc), n_exc, None, 1, prows, pcols,
+                   N.ptr(out_plane), None, stream)
+
+        t_xp = _time_loop(torch, x4t_pack, 50, 5)
+        t_xd = _time_loop(torch, x4t_decode, 50, 5)
+        meta = torch.empty(prows, dtype=torch.int32, device=dev)
+        koff = torch.empty(prows // 16 + 1, dtype=torch.int64, device=dev)
+        N.call("kq_kqsc_measure", 2, N.ptr(plane), prows, pcols, 16, N.ptr(meta), N.ptr(koff), stream)
+        payload = torch.empty(16 + 4 * (prows // 16 + 1) + int(koff[-1].item()), dtype=torch.uint8,
+                              device=dev)
+        kstatus = torch.empty(1, dtype=torch.int64, device=dev)
+
+        def kqsc_pack():
+            N.call("kq_kqsc_measure", 2, N.ptr(plane), prows, pcols, 16, N.ptr(meta), N.ptr(koff), stream)
+            N.call("kq_kqsc_emit", 2, N.ptr(plane), prows, pcols, 16, N.ptr(meta), N.ptr(koff),
+                   N.ptr(payload), stream)
+
+        def kqsc_decode():
+            N.call("kq_kqsc_decode", 2, N.ptr(payload), payload.numel(), prows, pcols, 16,
+                   N.ptr(out_plane), N.ptr(kstatus), stream)
+
+        t_kp = _time_loop(torch, kqsc_pack, 50, 5)
+        t_kd = _time_loop(torch, kqsc_decode, 50, 5)
+        t0 = time.perf_counter()
+        sqg_e4m3._normal_law.cache_clear()
+        sqg_e4m3._t12.cache_clear()
+        sqg_e4m3._xor_t12_labels.cache_clear()
+        sqg_e4m3._rank.cache_clear()
+        labels = sqg_e4m3.sqg_xor_cheb_t12_bytes(3, device=dev)
+        torch.cuda.synchronize()
+        t_sqg = time.perf_counter() - t0
+        result["scale_planes_cfg1"] = {
+            "workload": "E8M0 plane [7168x64] of the cfg1 MXFP4 weight",
+            "x4t_exceptions": n_exc,
+            "x4t_pack_us": round(t_xp * 1e6, 2),
+            "x4t_predecode_us": round(t_xd * 1e6, 2),
+            "kqsc_v2_bytes": int(payload.numel()),
+            "kqsc_v2_pack_us": round(t_kp * 1e6, 2),
+            "kqsc_v2_decode_us": round(t_kd * 1e6, 2),
+            "sqg_k3_t12_labels_build_ms": round(t_sqg * 1e3, 3),
+            "sqg_labels": int(labels.numel()),
+        }
+
     # ------------------------------------------------- CPU baseline --
     cpu = None
     if not args.no_cpu_baseline and want("cpu"):
