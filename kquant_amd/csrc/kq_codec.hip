@@ -12,34 +12,46 @@ namespace kq {
 // IN: 0 bf16, 1 f16, 2 f32.  FMT: 0 MXFP8-E4M3, 1 MXFP4-E2M1.
 // HW: use the gfx950 scaled convert instructions (round to nearest even,
 // saturating), otherwise the bit-level software rounding.
-template <int IN, int FMT, bool HW>
-__global__ __launch_bounds__(256) void mx_quantize_kernel(
-    const void* __restrict__ in, int64_t ld_in, int64_t nblk, int64_t total_blocks,
-    uint8_t* __restrict__ out_q, uint8_t* __restrict__ out_scale) {
-  const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int64_t blk = g >> 2;
-  const int part = (int)(g & 3);
-  if (blk >= total_blocks) return;  // whole quads leave together
-  const int64_t row = blk / nblk;
-  const int64_t kb = blk - row * nblk;
-  const int64_t col = kb * 32 + part * 8;
+typedef uint32_t u32x4_q __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_q __attribute__((ext_vector_type(2)));
 
+// One lane's 16-byte (16-bit inputs) or 32-byte (fp32) share of a block.
+template <int IN>
+struct QChunk {
+  u32x4_q d[IN == 2 ? 2 : 1];
+};
+
+template <int IN>
+__device__ __forceinline__ QChunk<IN> load_qchunk(const void* __restrict__ in, int64_t elem) {
+  QChunk<IN> c;
+  if (IN == 2) {
+    const u32x4_q* p = reinterpret_cast<const u32x4_q*>(static_cast<const float*>(in) + elem);
+    c.d[0] = __builtin_nontemporal_load(p);
+    c.d[1] = __builtin_nontemporal_load(p + 1);
+  } else {
+    c.d[0] = __builtin_nontemporal_load(
+        reinterpret_cast<const u32x4_q*>(static_cast<const uint16_t*>(in) + elem));
+  }
+  return c;
+}
+
+// Quantize one lane's 8 elements of block `blk` (part = lane within the quad
+// that owns the block) and store its codes, and the block's scale from part 0.
+template <int IN, int FMT, bool HW>
+__device__ __forceinline__ void quantize_qchunk(const QChunk<IN>& ch, int64_t blk, int part,
+                                                uint8_t* __restrict__ out_q,
+                                                uint8_t* __restrict__ out_scale) {
   // 8 elements of this lane as fp32 and, for 16-bit inputs, their raw pairs.
   float x[8];
   uint32_t raw[4];
   if (IN == 2) {
-    const float4_t* p = reinterpret_cast<const float4_t*>(
-        static_cast<const float*>(in) + row * ld_in + col);
-    float4_t a = __builtin_nontemporal_load(p);
-    float4_t b = __builtin_nontemporal_load(p + 1);
-    x[0] = a[0]; x[1] = a[1]; x[2] = a[2]; x[3] = a[3];
-    x[4] = b[0]; x[5] = b[1]; x[6] = b[2]; x[7] = b[3];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      x[i] = __uint_as_float(ch.d[0][i]);
+      x[4 + i] = __uint_as_float(ch.d[1][i]);
+    }
   } else {
-    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-    const u32x4* p = reinterpret_cast<const u32x4*>(
-        static_cast<const uint16_t*>(in) + row * ld_in + col);
-    u32x4 v = __builtin_nontemporal_load(p);
-    raw[0] = v[0]; raw[1] = v[1]; raw[2] = v[2]; raw[3] = v[3];
+    raw[0] = ch.d[0][0]; raw[1] = ch.d[0][1]; raw[2] = ch.d[0][2]; raw[3] = ch.d[0][3];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       if (IN == 0) {
@@ -104,7 +116,7 @@ __global__ __launch_bounds__(256) void mx_quantize_kernel(
     }
     typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
     u32x2 o = {w0, w1};
-    *reinterpret_cast<u32x2*>(out_q + row * (nblk * 32) + col) = o;
+    __builtin_nontemporal_store(o, reinterpret_cast<u32x2*>(out_q + blk * 32 + part * 8));
   } else {
     uint32_t w = 0;
     if (hw) {
@@ -134,7 +146,47 @@ __global__ __launch_bounds__(256) void mx_quantize_kernel(
         w |= f32_to_e2m1_rne(y) << (4 * i);
       }
     }
-    *reinterpret_cast<uint32_t*>(out_q + row * (nblk * 16) + kb * 16 + part * 4) = w;
+    __builtin_nontemporal_store(w, reinterpret_cast<uint32_t*>(out_q + blk * 16 + part * 4));
+  }
+}
+
+
+// Each thread handles ITERS chunks 256 apart (a wave covers 16 consecutive
+// blocks per step, so every load and store of a wave is one contiguous
+// range); all loads are issued before the first block is converted.  With
+// contiguous rows the input offset is the chunk index times 8 elements, so
+// no division by the row length is needed.
+#ifndef KQ_QUANT_ITERS
+#define KQ_QUANT_ITERS 2
+#endif
+constexpr int QUANT_ITERS = KQ_QUANT_ITERS;
+
+template <int IN, int FMT, bool HW, bool CONTIG>
+__global__ __launch_bounds__(256) void mx_quantize_kernel(
+    const void* __restrict__ in, int64_t ld_in, int64_t nblk, int64_t total_blocks,
+    uint8_t* __restrict__ out_q, uint8_t* __restrict__ out_scale) {
+  const int64_t c0 = (int64_t)blockIdx.x * (256 * QUANT_ITERS) + threadIdx.x;
+  QChunk<IN> v[QUANT_ITERS];
+#pragma unroll
+  for (int it = 0; it < QUANT_ITERS; ++it) {
+    const int64_t c = c0 + it * 256;
+    const int64_t blk = c >> 2;
+    if (blk < total_blocks) {  // whole quads are in or out together
+      int64_t elem;
+      if (CONTIG) {
+        elem = c * 8;
+      } else {
+        const int64_t row = blk / nblk;
+        elem = row * ld_in + (blk - row * nblk) * 32 + (c & 3) * 8;
+      }
+      v[it] = load_qchunk<IN>(in, elem);
+    }
+  }
+#pragma unroll
+  for (int it = 0; it < QUANT_ITERS; ++it) {
+    const int64_t c = c0 + it * 256;
+    const int64_t blk = c >> 2;
+    if (blk < total_blocks) quantize_qchunk<IN, FMT, HW>(v[it], blk, (int)(c & 3), out_q, out_scale);
   }
 }
 
@@ -384,12 +436,18 @@ extern "C" int kq_decode_bytes(int table, const uint8_t* in, int64_t n, int out_
 template <int IN, int FMT>
 static hipError_t launch_quantize(bool hw, const void* in, int64_t ld, int64_t nblk,
                                   int64_t total, void* oq, uint8_t* os, hipStream_t st) {
-  const int64_t threads = total * 4;
-  const dim3 grid((unsigned)((threads + 255) / 256));
-  if (hw)
-    mx_quantize_kernel<IN, FMT, true><<<grid, 256, 0, st>>>(in, ld, nblk, total, (uint8_t*)oq, os);
+  const int64_t chunks = total * 4;
+  const dim3 grid((unsigned)((chunks + 256 * QUANT_ITERS - 1) / (256 * QUANT_ITERS)));
+  const bool contig = ld == nblk * 32;
+  uint8_t* q = (uint8_t*)oq;
+  if (hw && contig)
+    mx_quantize_kernel<IN, FMT, true, true><<<grid, 256, 0, st>>>(in, ld, nblk, total, q, os);
+  else if (hw)
+    mx_quantize_kernel<IN, FMT, true, false><<<grid, 256, 0, st>>>(in, ld, nblk, total, q, os);
+  else if (contig)
+    mx_quantize_kernel<IN, FMT, false, true><<<grid, 256, 0, st>>>(in, ld, nblk, total, q, os);
   else
-    mx_quantize_kernel<IN, FMT, false><<<grid, 256, 0, st>>>(in, ld, nblk, total, (uint8_t*)oq, os);
+    mx_quantize_kernel<IN, FMT, false, false><<<grid, 256, 0, st>>>(in, ld, nblk, total, q, os);
   return hipGetLastError();
 }
 
