@@ -225,6 +225,206 @@ __global__ __launch_bounds__(256, 1) void syrk_upper_kernel(
   (void)diag;
 }
 
+// ---------------------------------------------------------------------------
+// bf16 SYRK on 256 x 256 upper tiles.  X stays in LDS in its natural
+// [token][feature] layout (16-byte row loads go straight in, no register
+// transpose) and the MFMA operands, which need 8 consecutive tokens per lane,
+// are read with the transposing ds_read_b64_tr_b16: in a 16-lane group, lane
+// s points at token s/4 and features 4(s%4)..+3 of one 16-feature strip, and
+// lane i receives the 4 tokens of feature i.  Two such reads give the 8
+// tokens of a 32x32x16 bf16 MFMA operand.  8 waves of 64 x 128 (2 x 4 MFMA
+// blocks), double-buffered LDS stages of BK tokens.  WEIGHTED: the B side is
+// w * x split into bf16 hi + lo (two more slabs, BK = 32), A stays exact, so
+// each product is a_hi * (b_hi + b_lo) (two MFMAs).  Diagonal tiles of an
+// unweighted call read B from the A slab.
+namespace syrk2 {
+constexpr int TILE = 256;
+constexpr int THREADS = 512;
+constexpr int ROW_BYTES = TILE * 2 + 64;  // one token row of 256 features + pad
+template <bool W> constexpr int bk() { return W ? 32 : 64; }
+template <bool W> constexpr int slab_bytes() { return bk<W>() * ROW_BYTES; }
+template <bool W> constexpr int nslab() { return W ? 3 : 2; }
+template <bool W> constexpr int stage_bytes() { return nslab<W>() * slab_bytes<W>(); }
+}  // namespace syrk2
+
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
+
+__device__ __forceinline__ s16x4_t lds_read_tr16(const unsigned char* base, int byte_off) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_s16x4_t*)((__attribute__((address_space(3))) unsigned char*)base + byte_off));
+}
+
+template <bool WEIGHTED, bool GROUPED>
+__global__ __launch_bounds__(512, 1) void syrk256_kernel(
+    const uint16_t* __restrict__ x, int64_t ld, int64_t n, int64_t k, const float* __restrict__ w,
+    float* __restrict__ acc, int64_t ld_acc, int ntiles, int overwrite,
+    const int64_t* __restrict__ offsets, const int32_t* __restrict__ index, int64_t acc_stride,
+    int square_w) {
+  using namespace syrk2;
+  constexpr int BK = bk<WEIGHTED>();
+  constexpr int SLAB = slab_bytes<WEIGHTED>();
+  constexpr int STAGE = stage_bytes<WEIGHTED>();
+  constexpr int CPT = BK * 32 / THREADS;  // 16-byte chunks per thread per slab
+  extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+
+  int64_t list0 = 0;
+  if (GROUPED) {
+    const int64_t g = blockIdx.y;
+    list0 = offsets[g];
+    n = offsets[g + 1] - list0;
+    acc += g * acc_stride;
+  }
+  int rem = blockIdx.x, ti = 0;
+  while (rem >= ntiles - ti) { rem -= ntiles - ti; ++ti; }
+  const int tj = ti + rem;
+  const bool share_b = !WEIGHTED && ti == tj;
+  const int64_t row0 = (int64_t)ti * TILE, col0 = (int64_t)tj * TILE;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+  // ---- global -> registers: chunk c = tid + THREADS * i: token c / 32, features 8 (c % 32)
+  u32x4_t ra[CPT], rb[CPT], rbl[CPT];
+  auto load = [&](int64_t t0) {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int c = tid + THREADS * i;
+      const int64_t pos = t0 + (c >> 5);
+      const int fc = (c & 31) * 8;
+      u32x4_t va = {0u, 0u, 0u, 0u}, vb = {0u, 0u, 0u, 0u}, vl = {0u, 0u, 0u, 0u};
+      if (pos < n) {
+        const int64_t tok = !GROUPED ? pos : (index ? (int64_t)index[list0 + pos] : list0 + pos);
+        const uint16_t* rowp = x + tok * ld;
+        if (row0 + fc < k) va = *reinterpret_cast<const u32x4_t*>(rowp + row0 + fc);
+        if (!share_b && col0 + fc < k) {
+          const u32x4_t raw = *reinterpret_cast<const u32x4_t*>(rowp + col0 + fc);
+          if (WEIGHTED) {
+            float wt = w[GROUPED ? list0 + pos : pos];
+            if (GROUPED && square_w) wt *= wt;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              uint32_t h0, l0, h1, l1;
+              split_bf16(bf16_bits_to_f32(raw[e] & 0xffffu) * wt, h0, l0);
+              split_bf16(bf16_bits_to_f32(raw[e] >> 16) * wt, h1, l1);
+              vb[e] = h0 | (h1 << 16);
+              vl[e] = l0 | (l1 << 16);
+            }
+          } else {
+            vb = raw;
+          }
+        }
+      }
+      ra[i] = va;
+      rb[i] = vb;
+      if (WEIGHTED) rbl[i] = vl;
+    }
+  };
+  auto store = [&](int buf) {
+    unsigned char* base = lds + buf * STAGE;
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int c = tid + THREADS * i;
+      const int off = (c >> 5) * ROW_BYTES + (c & 31) * 16;
+      *reinterpret_cast<u32x4_t*>(base + off) = ra[i];
+      if (!share_b) *reinterpret_cast<u32x4_t*>(base + SLAB + off) = rb[i];
+      if (WEIGHTED) *reinterpret_cast<u32x4_t*>(base + 2 * SLAB + off) = rbl[i];
+    }
+  };
+
+  const int wm = (wave >> 1) * 64, wn = (wave & 1) * 128;
+  float16_t accv[2][4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) accv[i][j][r] = 0.0f;
+
+  // transposed-read address of this lane inside a 32-feature x 16-token block:
+  // 16-lane group g covers features 16 (g % 2) + [0, 16) and tokens 8 (g / 2) + [0, 8)
+  const int g16 = lane >> 4, s16 = lane & 15;
+  const int lane_off = (8 * (g16 >> 1) + (s16 >> 2)) * ROW_BYTES + (16 * (g16 & 1) + 4 * (s16 & 3)) * 2;
+
+  const int64_t steps = (n + BK - 1) / BK;
+  if (steps > 0) {
+    load(0);
+    store(0);
+  }
+  __syncthreads();
+  for (int64_t s = 0; s < steps; ++s) {
+    const int buf = (int)(s & 1);
+    if (s + 1 < steps) load((s + 1) * BK);
+    const unsigned char* a_base = lds + buf * STAGE;
+    const unsigned char* b_base = share_b ? a_base : a_base + SLAB;
+#pragma unroll
+    for (int kk = 0; kk < BK / 16; ++kk) {
+      const int koff = kk * 16 * ROW_BYTES + lane_off;
+      bf16x8_t fa[2], fb[4], fbl[4];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int o = koff + (wm + i * 32) * 2;
+        const s16x4_t lo = lds_read_tr16(a_base, o);
+        const s16x4_t hi = lds_read_tr16(a_base, o + 4 * ROW_BYTES);
+        fa[i] = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int o = koff + (wn + j * 32) * 2;
+        const s16x4_t lo = lds_read_tr16(b_base, o);
+        const s16x4_t hi = lds_read_tr16(b_base, o + 4 * ROW_BYTES);
+        fb[j] = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        if (WEIGHTED) {
+          const s16x4_t l2 = lds_read_tr16(a_base + 2 * SLAB, o);
+          const s16x4_t h2 = lds_read_tr16(a_base + 2 * SLAB, o + 4 * ROW_BYTES);
+          fbl[j] = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(l2, h2, 0, 1, 2, 3, 4, 5, 6, 7));
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          accv[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], accv[i][j], 0, 0, 0);
+          if (WEIGHTED)
+            accv[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fbl[j], accv[i][j], 0, 0, 0);
+        }
+    }
+    if (s + 1 < steps) store(buf ^ 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue: C[32x32] lane layout col = lane % 32, row = 8 (r/4) + 4 (lane/32) + r%4
+  const int ccol = lane & 31, crow = (lane >> 5) * 4;
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t gr = row0 + wm + i * 32 + 8 * (r >> 2) + crow + (r & 3);
+        const int64_t gc = col0 + wn + j * 32 + ccol;
+        if (gr < k && gc < k) {
+          float* p = acc + gr * ld_acc + gc;
+          *p = overwrite ? accv[i][j][r] : *p + accv[i][j][r];
+        }
+      }
+}
+
+template <bool WEIGHTED, bool GROUPED>
+static hipError_t launch_syrk256(const void* x, int64_t ld, int64_t n, int64_t k, const float* w,
+                                 float* acc, int64_t ld_acc, int overwrite, hipStream_t st,
+                                 const int64_t* offsets = nullptr, const int32_t* index = nullptr,
+                                 int groups = 1, int square_w = 0) {
+  const int nt = (int)((k + syrk2::TILE - 1) / syrk2::TILE);
+  const int ntiles = nt * (nt + 1) / 2;
+  const size_t lds = 2 * (size_t)syrk2::stage_bytes<WEIGHTED>();
+  auto kern = syrk256_kernel<WEIGHTED, GROUPED>;
+  hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (e != hipSuccess) return e;
+  kern<<<dim3(ntiles, groups), dim3(syrk2::THREADS), lds, st>>>(
+      (const uint16_t*)x, ld, n, k, w, acc, ld_acc, nt, overwrite, offsets, index, k * ld_acc, square_w);
+  return hipGetLastError();
+}
+
 // out = sym(acc) * inv_denom : upper tiles are read for every (i, j) as
 // acc[min][max]; one thread per output element, rows of 256 columns.
 __global__ __launch_bounds__(256) void syrk_finalize_kernel(
@@ -508,8 +708,8 @@ extern "C" int kq_syrk_accumulate(int in_dtype, const void* x, int64_t ld, int64
   hipError_t e;
   const bool weighted = weights != nullptr;
   if (in_dtype == KQ_DT_BF16) {
-    e = weighted ? launch_syrk<0, true, true, false>(x, ld, n, k, weights, acc, ld_acc, overwrite, st)
-                 : launch_syrk<0, false, false, false>(x, ld, n, k, weights, acc, ld_acc, overwrite, st);
+    e = weighted ? launch_syrk256<true, false>(x, ld, n, k, weights, acc, ld_acc, overwrite, st)
+                 : launch_syrk256<false, false>(x, ld, n, k, weights, acc, ld_acc, overwrite, st);
   } else if (in_dtype == KQ_DT_F16) {
     e = weighted ? launch_syrk<1, true, true, false>(x, ld, n, k, weights, acc, ld_acc, overwrite, st)
                  : launch_syrk<1, true, false, false>(x, ld, n, k, weights, acc, ld_acc, overwrite, st);
@@ -564,8 +764,8 @@ extern "C" int kq_syrk_grouped(int in_dtype, const void* x, int64_t ld, const in
   hipError_t e;
   const bool weighted = weights != nullptr;
   if (in_dtype == KQ_DT_BF16)
-    e = weighted ? launch_syrk<0, true, true, true>(x, ld, 0, k, weights, acc, k, 1, st, offsets, row_index, groups, sq)
-                 : launch_syrk<0, false, false, true>(x, ld, 0, k, weights, acc, k, 1, st, offsets, row_index, groups, sq);
+    e = weighted ? launch_syrk256<true, true>(x, ld, 0, k, weights, acc, k, 1, st, offsets, row_index, groups, sq)
+                 : launch_syrk256<false, true>(x, ld, 0, k, weights, acc, k, 1, st, offsets, row_index, groups, sq);
   else if (in_dtype == KQ_DT_F16)
     e = weighted ? launch_syrk<1, true, true, true>(x, ld, 0, k, weights, acc, k, 1, st, offsets, row_index, groups, sq)
                  : launch_syrk<1, true, false, true>(x, ld, 0, k, weights, acc, k, 1, st, offsets, row_index, groups, sq);
