@@ -16,6 +16,8 @@
 // out [feature][token] -- the MFMA operand order (8 consecutive reduction
 // elements per lane).  LDS is double buffered: the global loads of step s+1
 // are in flight while step s runs on the matrix cores.
+#include <type_traits>
+
 #include "kq_common.h"
 #include "kq_internal.h"
 
@@ -240,8 +242,14 @@ __global__ __launch_bounds__(256, 1) void syrk_upper_kernel(
 namespace syrk2 {
 constexpr int TILE = 256;
 constexpr int THREADS = 512;
-constexpr int ROW_BYTES = TILE * 2 + 64;  // one token row of 256 features + pad
-template <bool W> constexpr int bk() { return W ? 32 : 64; }
+#ifndef KQ_SYRK_PAD
+#define KQ_SYRK_PAD 64
+#endif
+#ifndef KQ_SYRK_BK
+#define KQ_SYRK_BK 32
+#endif
+constexpr int ROW_BYTES = TILE * 2 + KQ_SYRK_PAD;  // one token row of 256 features + pad
+template <bool W> constexpr int bk() { return W ? 32 : KQ_SYRK_BK; }
 template <bool W> constexpr int slab_bytes() { return bk<W>() * ROW_BYTES; }
 template <bool W> constexpr int nslab() { return W ? 3 : 2; }
 template <bool W> constexpr int stage_bytes() { return nslab<W>() * slab_bytes<W>(); }
@@ -253,6 +261,46 @@ typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
 __device__ __forceinline__ s16x4_t lds_read_tr16(const unsigned char* base, int byte_off) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
       (lds_s16x4_t*)((__attribute__((address_space(3))) unsigned char*)base + byte_off));
+}
+
+// Upper tile (ti <= tj) of an nt x nt tile grid for workgroup b.  Ungrouped
+// launches are XCD-aware: workgroups are dispatched to the 8 XCDs round-robin
+// (b % 8), so XCD x is given the contiguous run [x * per, (x + 1) * per) of a
+// blocked order of the triangle (4 x 4 tile blocks, block rows then block
+// columns), and the ~32 tiles an XCD runs at once share a few row and column
+// slabs in its L2.  Returns false for the spare blocks of the last run.
+constexpr int SYRK_XCDS = 8;
+constexpr int SYRK_BLOCK = 4;
+__device__ __forceinline__ bool upper_tile_for_block(int b, int nt, bool grouped, int& ti, int& tj) {
+  const int total = nt * (nt + 1) / 2;
+  int t = b;
+  if (!grouped) {
+    const int per = (total + SYRK_XCDS - 1) / SYRK_XCDS;
+    t = (b % SYRK_XCDS) * per + b / SYRK_XCDS;
+    if (t >= total) return false;
+  }
+  const int nb = (nt + SYRK_BLOCK - 1) / SYRK_BLOCK;
+  for (int R = 0; R < nb; ++R) {
+    const int r0 = R * SYRK_BLOCK, r1 = min(r0 + SYRK_BLOCK, nt);
+    for (int C = R; C < nb; ++C) {
+      const int c0 = C * SYRK_BLOCK, c1 = min(c0 + SYRK_BLOCK, nt);
+      int cnt = 0;  // tiles (i, j) of this block with i <= j
+      for (int i = r0; i < r1; ++i) cnt += max(0, c1 - max(c0, i));
+      if (t < cnt) {
+        for (int i = r0; i < r1; ++i) {
+          const int jlo = max(c0, i), row = max(0, c1 - jlo);
+          if (t < row) {
+            ti = i;
+            tj = jlo + t;
+            return true;
+          }
+          t -= row;
+        }
+      }
+      t -= cnt;
+    }
+  }
+  return false;
 }
 
 template <bool WEIGHTED, bool GROUPED>
@@ -275,9 +323,8 @@ __global__ __launch_bounds__(512, 1) void syrk256_kernel(
     n = offsets[g + 1] - list0;
     acc += g * acc_stride;
   }
-  int rem = blockIdx.x, ti = 0;
-  while (rem >= ntiles - ti) { rem -= ntiles - ti; ++ti; }
-  const int tj = ti + rem;
+  int ti, tj;
+  if (!upper_tile_for_block(blockIdx.x, ntiles, GROUPED, ti, tj)) return;  // spare block
   const bool share_b = !WEIGHTED && ti == tj;
   const int64_t row0 = (int64_t)ti * TILE, col0 = (int64_t)tj * TILE;
 
@@ -409,6 +456,191 @@ __global__ __launch_bounds__(512, 1) void syrk256_kernel(
       }
 }
 
+// ---------------------------------------------------------------------------
+// Unweighted bf16 SYRK with direct-to-LDS loads.  Same tiles, waves and
+// transposed operand reads as syrk256_kernel, but X rows go from HBM into LDS
+// by buffer_load_dwordx4 ... lds (no register staging), through a ring of
+// four stages of 32 tokens, issued three steps ahead of their use, so the
+// memory latency is covered by three steps of MFMA work.  A wave's load
+// writes 1 KiB of LDS contiguously (two token rows), so rows are not padded:
+// 16-byte chunk c of token row r is stored at slot c ^ 4 (r % 4), which puts
+// the four rows of each transposed read on distinct LDS banks.  Tokens past n
+// get an out-of-range buffer offset and read as zeros; features past k only
+// reach output rows and columns past k, which are not stored.  The stages are
+// distinct LDS arrays and the loop is unrolled over them, so the compiler can
+// see which stage each read touches and keeps the explicit partial waits.
+namespace syrk3 {
+constexpr int TILE = 256;
+constexpr int BK = 32;
+constexpr int ROW = TILE * 2;      // bytes per token row
+constexpr int SLAB = BK * ROW;     // 16 KiB
+}  // namespace syrk3
+
+__shared__ __attribute__((aligned(16))) unsigned char syrk3_lds[4 * 2 * syrk3::SLAB];
+
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
+// Buffer resource over [base, base + nbytes): raw addressing, range-checked
+// (out-of-range offsets read as zero); dword 3 is the gfx9 default format.
+__device__ __forceinline__ i32x4_t make_rsrc(const void* base, uint32_t nbytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  i32x4_t r;
+  r[0] = (int)(uint32_t)a;
+  r[1] = (int)(uint32_t)(a >> 32) & 0xffff;
+  r[2] = (int)nbytes;
+  r[3] = 0x00020000;
+  return r;
+}
+
+// s_waitcnt immediate (gfx9 encoding) for vmcnt(N), other counters untouched.
+constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+// 16 bytes per lane from rsrc + voffset straight into LDS at m0 + 16 * lane.
+// Issued as assembly so the compiler neither inserts a full vmcnt wait before
+// later LDS reads nor moves LDS accesses across it; the kernel waits itself.
+__device__ __forceinline__ void load_to_lds16(i32x4_t rsrc, uint32_t voffset, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(lds_addr), "v"(voffset), "s"(rsrc)
+               : "memory", "m0");
+}
+
+__device__ __forceinline__ uint32_t lds_offset_of(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) unsigned char*)p;
+}
+
+__global__ __launch_bounds__(512, 1) void syrk256_dma_kernel(
+    const uint16_t* __restrict__ x, int64_t ld, int64_t n, int64_t k, float* __restrict__ acc,
+    int64_t ld_acc, int nt, int overwrite, uint32_t nbytes) {
+  using namespace syrk3;
+  int ti, tj;
+  if (!upper_tile_for_block(blockIdx.x, nt, false, ti, tj)) return;  // spare block
+  const bool share_b = ti == tj;
+  const int64_t row0 = (int64_t)ti * TILE, col0 = (int64_t)tj * TILE;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const i32x4_t rsrc = make_rsrc(x, nbytes);
+  const uint32_t lds0 = lds_offset_of(syrk3_lds);
+
+  // Loads: wave w, part q in {0, 1}: token rows 2 (2w + q) + lane / 32 of a
+  // stage, this lane's 16-byte slot lane % 32 holds global chunk slot ^ 4 (row % 4).
+  int drow[2], dchunk[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    drow[q] = 2 * (2 * wave + q) + (lane >> 5);
+    dchunk[q] = (lane & 31) ^ (4 * (drow[q] & 3));
+  }
+  // stage s lives at [2 SLAB s, 2 SLAB s + SLAB) (A) and the next SLAB bytes (B)
+  auto issue = [&](int stage, int64_t t0) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int64_t tok = t0 + drow[q];
+      const bool ok = tok < n;
+      const uint32_t base = ok ? (uint32_t)(tok * ld * 2) : nbytes;  // nbytes: first offset past the range
+      const uint32_t dst = lds0 + (uint32_t)(2 * SLAB * stage + (2 * wave + q) * 1024);
+      load_to_lds16(rsrc, ok ? base + (uint32_t)((row0 + dchunk[q] * 8) * 2) : base, dst);
+      if (!share_b)
+        load_to_lds16(rsrc, ok ? base + (uint32_t)((col0 + dchunk[q] * 8) * 2) : base, dst + SLAB);
+    }
+  };
+
+  const int wm = (wave >> 1) * 64, wn = (wave & 1) * 128;
+  float16_t accv[2][4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) accv[i][j][r] = 0.0f;
+
+  // Transposed reads: 16-lane group g covers features 16 (g % 2) of a 32-feature
+  // block and tokens 8 (g / 2) + [0, 8); lane s16 reads token s16 / 4 (+4 for
+  // the second half) and features 4 (s16 % 4) .. +3.
+  const int g16 = lane >> 4, s16 = lane & 15;
+  const int trow = 8 * (g16 >> 1) + (s16 >> 2);
+  const int xorv = 4 * (s16 >> 2);
+  int offa[2], offb[4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int f = wm + i * 32 + 16 * (g16 & 1) + 4 * (s16 & 3);
+    offa[i] = trow * ROW + (((f >> 3) ^ xorv) << 4) + (f & 7) * 2;
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int f = wn + j * 32 + 16 * (g16 & 1) + 4 * (s16 & 3);
+    offb[j] = trow * ROW + (((f >> 3) ^ xorv) << 4) + (f & 7) * 2;
+  }
+
+  // Step s on stage s % 4: wait for this step's loads (two later steps may
+  // still be in flight), barrier (every wave's loads have landed; every wave
+  // is done with the stage the next loads overwrite), issue the loads of step
+  // s + 3, compute.  Steps past the end load zeros, which keeps the per-step
+  // count of outstanding loads fixed.
+  const int64_t steps = (n + BK - 1) / BK;
+  issue(0, 0);
+  issue(1, BK);
+  issue(2, 2 * BK);
+  for (int64_t s = 0; s < steps; ++s) {
+    const int stage = (int)(s & 3);
+    if (share_b) __builtin_amdgcn_s_waitcnt(waitcnt_vm(4));
+    else __builtin_amdgcn_s_waitcnt(waitcnt_vm(8));
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    issue((stage + 3) & 3, (s + 3) * BK);
+    const unsigned char* a_base = syrk3_lds + 2 * SLAB * stage;
+    const unsigned char* b_base = share_b ? a_base : a_base + SLAB;
+#pragma unroll
+    for (int kk = 0; kk < BK / 16; ++kk) {
+      bf16x8_t fa[2], fb[4];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int o = offa[i] + kk * 16 * ROW;
+        const s16x4_t lo = lds_read_tr16(a_base, o);
+        const s16x4_t hi = lds_read_tr16(a_base, o + 4 * ROW);
+        fa[i] = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int o = offb[j] + kk * 16 * ROW;
+        const s16x4_t lo = lds_read_tr16(b_base, o);
+        const s16x4_t hi = lds_read_tr16(b_base, o + 4 * ROW);
+        fb[j] = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          accv[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], accv[i][j], 0, 0, 0);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));  // no load may land after the workgroup ends
+
+  const int ccol = lane & 31, crow = (lane >> 5) * 4;
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t gr = row0 + wm + i * 32 + 8 * (r >> 2) + crow + (r & 3);
+        const int64_t gc = col0 + wn + j * 32 + ccol;
+        if (gr < k && gc < k) {
+          float* p = acc + gr * ld_acc + gc;
+          *p = overwrite ? accv[i][j][r] : *p + accv[i][j][r];
+        }
+      }
+}
+
+static hipError_t launch_syrk256_dma(const void* x, int64_t ld, int64_t n, int64_t k, float* acc,
+                                     int64_t ld_acc, int overwrite, hipStream_t st) {
+  const int nt = (int)((k + syrk3::TILE - 1) / syrk3::TILE);
+  const int ntiles = nt * (nt + 1) / 2;
+  const int blocks = SYRK_XCDS * ((ntiles + SYRK_XCDS - 1) / SYRK_XCDS);
+  syrk256_dma_kernel<<<dim3(blocks), dim3(512), 0, st>>>((const uint16_t*)x, ld, n, k, acc, ld_acc, nt,
+                                                          overwrite, (uint32_t)(n * ld * 2));
+  return hipGetLastError();
+}
+
 template <bool WEIGHTED, bool GROUPED>
 static hipError_t launch_syrk256(const void* x, int64_t ld, int64_t n, int64_t k, const float* w,
                                  float* acc, int64_t ld_acc, int overwrite, hipStream_t st,
@@ -416,11 +648,12 @@ static hipError_t launch_syrk256(const void* x, int64_t ld, int64_t n, int64_t k
                                  int groups = 1, int square_w = 0) {
   const int nt = (int)((k + syrk2::TILE - 1) / syrk2::TILE);
   const int ntiles = nt * (nt + 1) / 2;
+  const int blocks = GROUPED ? ntiles : SYRK_XCDS * ((ntiles + SYRK_XCDS - 1) / SYRK_XCDS);
   const size_t lds = 2 * (size_t)syrk2::stage_bytes<WEIGHTED>();
   auto kern = syrk256_kernel<WEIGHTED, GROUPED>;
   hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return e;
-  kern<<<dim3(ntiles, groups), dim3(syrk2::THREADS), lds, st>>>(
+  kern<<<dim3(blocks, groups), dim3(syrk2::THREADS), lds, st>>>(
       (const uint16_t*)x, ld, n, k, w, acc, ld_acc, nt, overwrite, offsets, index, k * ld_acc, square_w);
   return hipGetLastError();
 }
@@ -708,8 +941,12 @@ extern "C" int kq_syrk_accumulate(int in_dtype, const void* x, int64_t ld, int64
   hipError_t e;
   const bool weighted = weights != nullptr;
   if (in_dtype == KQ_DT_BF16) {
-    e = weighted ? launch_syrk256<true, false>(x, ld, n, k, weights, acc, ld_acc, overwrite, st)
-                 : launch_syrk256<false, false>(x, ld, n, k, weights, acc, ld_acc, overwrite, st);
+    if (weighted)
+      e = launch_syrk256<true, false>(x, ld, n, k, weights, acc, ld_acc, overwrite, st);
+    else if (n * ld * 2 < ((int64_t)1 << 32) - 4096)  // the buffer descriptor's 32-bit range
+      e = launch_syrk256_dma(x, ld, n, k, acc, ld_acc, overwrite, st);
+    else
+      e = launch_syrk256<false, false>(x, ld, n, k, weights, acc, ld_acc, overwrite, st);
   } else if (in_dtype == KQ_DT_F16) {
     e = weighted ? launch_syrk<1, true, true, false>(x, ld, n, k, weights, acc, ld_acc, overwrite, st)
                  : launch_syrk<1, true, false, false>(x, ld, n, k, weights, acc, ld_acc, overwrite, st);
