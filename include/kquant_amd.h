@@ -41,6 +41,11 @@ enum {
      instructions (both are tested to agree byte for byte) */
   KQ_FLAG_SOFTWARE_CVT = 1u
 };
+/* kq_moe_forward flags: run the grouped GEMMs on the register-staged kernel
+   (the path taken when x or the intermediate exceed a 4 GiB buffer range)
+   instead of the direct-to-LDS one; both meet the same error bound, and
+   differ only by fp32 rounding (they sum each MFMA's k in another order) */
+enum { KQ_MOE_REGISTER_STAGED = 1u };
 /* kq_syrk_accumulate flags */
 enum { KQ_SYRK_OVERWRITE = 1u, KQ_SYRK_SQUARE_WEIGHTS = 2u, KQ_SUM_SQUARE_F64 = 4u };
 /* byte tables of kq_decode_bytes */
@@ -141,6 +146,7 @@ int64_t kq_moe_workspace_size(int64_t tokens, int topk, int experts, int64_t hid
  * out [tokens, hidden] bf16 or fp32.
  * hidden % 512 == 0, I % 512 == 0, topk <= 64, experts <= 4096.
  * workspace: >= kq_moe_workspace_size bytes, 256-byte aligned, caller owned;
+ * flags: 0 or KQ_MOE_REGISTER_STAGED.
  * results are bitwise reproducible (no floating-point atomics). */
 int kq_moe_forward(int activation, float act_beta, float act_linear_beta,
                    const void* x, int64_t ldx, int64_t tokens, int64_t hidden,

@@ -33,6 +33,7 @@ TABLE_E4M3 = 2
 SYRK_OVERWRITE = 1
 SYRK_SQUARE_WEIGHTS = 2
 SUM_SQUARE_F64 = 4
+MOE_REGISTER_STAGED = 1
 ACT_SITU = 0
 ACT_SWIGLU = 1
 

@@ -18,6 +18,7 @@
 // are in flight while step s runs on the matrix cores.
 #include <type_traits>
 
+#include "kq_dma.h"
 #include "kq_common.h"
 #include "kq_internal.h"
 
@@ -466,9 +467,7 @@ __global__ __launch_bounds__(512, 1) void syrk256_kernel(
 // 16-byte chunk c of token row r is stored at slot c ^ 4 (r % 4), which puts
 // the four rows of each transposed read on distinct LDS banks.  Tokens past n
 // get an out-of-range buffer offset and read as zeros; features past k only
-// reach output rows and columns past k, which are not stored.  The stages are
-// distinct LDS arrays and the loop is unrolled over them, so the compiler can
-// see which stage each read touches and keeps the explicit partial waits.
+// reach output rows and columns past k, which are not stored.
 namespace syrk3 {
 constexpr int TILE = 256;
 constexpr int BK = 32;
@@ -478,36 +477,11 @@ constexpr int SLAB = BK * ROW;     // 16 KiB
 
 __shared__ __attribute__((aligned(16))) unsigned char syrk3_lds[4 * 2 * syrk3::SLAB];
 
-typedef int i32x4_t __attribute__((ext_vector_type(4)));
-
-// Buffer resource over [base, base + nbytes): raw addressing, range-checked
-// (out-of-range offsets read as zero); dword 3 is the gfx9 default format.
-__device__ __forceinline__ i32x4_t make_rsrc(const void* base, uint32_t nbytes) {
-  const uint64_t a = reinterpret_cast<uint64_t>(base);
-  i32x4_t r;
-  r[0] = (int)(uint32_t)a;
-  r[1] = (int)(uint32_t)(a >> 32) & 0xffff;
-  r[2] = (int)nbytes;
-  r[3] = 0x00020000;
-  return r;
-}
-
-// s_waitcnt immediate (gfx9 encoding) for vmcnt(N), other counters untouched.
-constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
-
-// 16 bytes per lane from rsrc + voffset straight into LDS at m0 + 16 * lane.
-// Issued as assembly so the compiler neither inserts a full vmcnt wait before
-// later LDS reads nor moves LDS accesses across it; the kernel waits itself.
-__device__ __forceinline__ void load_to_lds16(i32x4_t rsrc, uint32_t voffset, uint32_t lds_addr) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-               :
-               : "s"(lds_addr), "v"(voffset), "s"(rsrc)
-               : "memory", "m0");
-}
-
-__device__ __forceinline__ uint32_t lds_offset_of(const void* p) {
-  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) unsigned char*)p;
-}
+using dma::i32x4_t;
+using dma::load_to_lds16;
+using dma::lds_offset_of;
+using dma::make_rsrc;
+using dma::waitcnt_vm;
 
 __global__ __launch_bounds__(512, 1) void syrk256_dma_kernel(
     const uint16_t* __restrict__ x, int64_t ld, int64_t n, int64_t k, float* __restrict__ acc,

@@ -20,6 +20,7 @@
 //      and writes one fp32 row per pair.
 //   4. combine: out[t] = sum of the topk pair rows in slot order.
 // No atomics touch floating-point data, so results are bitwise reproducible.
+#include "kq_dma.h"
 #include "kq_gemm.h"
 #include "kq_internal.h"
 #include "kq_act.h"
@@ -603,6 +604,235 @@ __global__ __launch_bounds__(512, 1) void moe_large_kernel(
     }
 }
 
+// ------------------------------------- grouped GEMM, direct-to-LDS loads --
+// Same tiles, waves, fragments and epilogues as moe_large_kernel, reorganised
+// around direct HBM -> LDS loads:
+//  * persistent: one workgroup per CU walks the (row tile, column tile) list,
+//    tile T = row_tile * col_tiles + col_tile.  Worker w (workgroups are
+//    numbered so the G/8 workers of one XCD are consecutive) takes tiles w,
+//    w + G, ...; the 32 workgroups of one XCD therefore work on neighbouring
+//    tiles of the same rows at the same time, and the gathered activation rows
+//    of a row tile are fetched into that XCD's L2 once.
+//  * loads go through a ring of three LDS stages (K step 64) issued two steps
+//    ahead, continuing across tile boundaries: the first two stages of a
+//    workgroup's next tile are in flight while it finishes and stores the
+//    current one.
+//  * activation rows: 128 bytes of a row per stage, 16-byte chunk c of tile
+//    row r stored at slot c ^ ((r / 2) % 8), so the 16 lanes of an MFMA
+//    fragment read hit 16 distinct bank groups.  Rows past the expert's count
+//    read as zero without touching memory (out-of-range buffer offset).
+//  * k order: within each 32-element scale block, lane half f of MFMA kk takes
+//    k = 16 f + 8 kk + [0, 8) (the same for activations and weights), so one
+//    8-byte LDS read gives a lane the packed weights of both MFMAs of a block.
+//  * waves whose 64 rows are all past the expert's count skip their MFMAs.
+namespace dma_gemm {
+constexpr int NSTAGE = 3;
+constexpr int DA_BYTES = BM * BK * 2;        // 32 KiB, unpadded 128-byte rows
+constexpr int DB_BYTES = BN * BK / 2;        // 8 KiB: 16 row groups x 512 B half tiles
+constexpr int DS_BYTES = BN * BK / 32;       // 512 B: 16 row groups x 32 B
+constexpr int DSTAGE = DA_BYTES + DB_BYTES + DS_BYTES;
+constexpr int LOADS_PER_STAGE = 6;          // per wave: 4 activation, 1 weight, 1 scale
+}  // namespace dma_gemm
+
+__shared__ __attribute__((aligned(16))) unsigned char moe_dma_lds[dma_gemm::NSTAGE * dma_gemm::DSTAGE];
+
+template <bool GATEUP>
+__global__ __launch_bounds__(512, 1) void moe_large_dma_kernel(
+    const uint16_t* __restrict__ a, int64_t lda, uint32_t a_bytes, int topk,
+    const int* __restrict__ offsets, const int* __restrict__ sorted, const int* __restrict__ tiles,
+    const int* __restrict__ meta, const uint8_t* __restrict__ wt, const uint8_t* __restrict__ wst,
+    int64_t rows_per_expert, int64_t K, int64_t inter, int col_tiles, ActParams act,
+    const float* __restrict__ route_w, uint16_t* __restrict__ act_out, float* __restrict__ y_out,
+    int64_t hidden) {
+  using namespace dma_gemm;
+  using dma::i32x4_t;
+  const int G = gridDim.x;
+  const int worker = (int)(blockIdx.x % 8) * (G / 8) + (int)(blockIdx.x / 8);
+  const int total = meta[1] * col_tiles;
+  if (worker >= total) return;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t nchunk = K / 128, rgs = rows_per_expert / 16;
+  const int64_t nrows = GATEUP ? 2 * inter : hidden;  // weight rows per expert
+  const uint32_t b_bytes = (uint32_t)(rgs * nchunk * 1024), s_bytes = (uint32_t)(rgs * nchunk * 64);
+  const int steps = (int)(K / BK);
+  const uint32_t lds0 = dma::lds_offset_of(moe_dma_lds);
+  const i32x4_t a_rsrc = dma::make_rsrc(a, a_bytes);
+
+  // global row group of local group lrg (16 per tile) for column tile c0
+  auto grow_group = [&](int64_t c0, int lrg) -> int64_t {
+    if (GATEUP) return lrg < 8 ? c0 / 16 + lrg : inter / 16 + c0 / 16 + (lrg - 8);
+    return c0 / 16 + lrg;
+  };
+
+  // ---- load side: tile lt, step ls; per-lane byte offsets (invalid -> past the range)
+  int lt = worker, ls = 0;
+  uint32_t a_off[4], b_off = 0, s_off = 0;
+  i32x4_t b_rsrc = dma::make_rsrc(wt, 0), s_rsrc = dma::make_rsrc(wst, 0);
+  auto set_load_tile = [&]() {
+    if (lt >= total) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) a_off[q] = a_bytes;
+      b_off = b_bytes;
+      s_off = s_bytes;
+      return;
+    }
+    const int mt = lt / col_tiles, nt = lt - mt * col_tiles;
+    const int e = tiles[2 * mt], m0 = tiles[2 * mt + 1];
+    const int beg = offsets[e], n = offsets[e + 1] - beg;
+    const int64_t c0 = (int64_t)nt * (GATEUP ? BN / 2 : BN);
+    // all four row lookups are issued before the first is used (one wait)
+    int src[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int slot = m0 + 8 * (8 * q + wave) + (lane >> 3);
+      src[q] = GATEUP ? sorted[beg + (slot < n ? slot : n - 1)] : beg + slot;
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int row = 8 * (8 * q + wave) + (lane >> 3);
+      const int c = (lane & 7) ^ ((row >> 1) & 7);
+      const int64_t r = GATEUP ? src[q] / topk : src[q];
+      a_off[q] = m0 + row < n ? (uint32_t)(r * lda * 2 + c * 16) : a_bytes;
+    }
+    b_rsrc = dma::make_rsrc(wt + (int64_t)e * rgs * nchunk * 1024, b_bytes);
+    s_rsrc = dma::make_rsrc(wst + (int64_t)e * rgs * nchunk * 64, s_bytes);
+    {
+      const int64_t rg = grow_group(c0, 2 * wave + (lane >> 5));
+      b_off = 16 * rg < nrows ? (uint32_t)(rg * nchunk * 1024 + (lane & 31) * 16) : b_bytes;
+    }
+    {
+      const int64_t rg = grow_group(c0, 2 * wave + ((lane >> 1) & 1));
+      s_off = 16 * rg < nrows ? (uint32_t)(rg * nchunk * 64 + (lane & 1) * 16) : s_bytes;
+    }
+  };
+  auto issue = [&](int slot) {
+    const uint32_t base = lds0 + (uint32_t)(slot * DSTAGE);
+    const uint32_t k0 = (uint32_t)(ls * BK);
+    const uint32_t chunk = k0 / 128, h = (k0 / 64) & 1;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t off = a_off[q] >= a_bytes ? a_bytes : a_off[q] + 2 * k0;
+      dma::load_to_lds16(a_rsrc, off, base + (uint32_t)((8 * q + wave) * 1024));
+    }
+    dma::load_to_lds16(b_rsrc, b_off >= b_bytes ? b_bytes : b_off + chunk * 1024 + h * 512,
+                       base + (uint32_t)(DA_BYTES + wave * 1024));
+    if (lane < 4)
+      dma::load_to_lds16(s_rsrc, s_off >= s_bytes ? s_bytes : s_off + chunk * 64 + h * 32,
+                         base + (uint32_t)(DA_BYTES + DB_BYTES + wave * 64));
+  };
+  auto advance = [&]() {
+    if (++ls == steps) {
+      ls = 0;
+      lt += G;
+      set_load_tile();
+    }
+  };
+
+  // ---- compute side: per-lane LDS read offsets (fixed for the whole kernel)
+  const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+  const int frow = lane & 31, fk = lane >> 5;
+  int arow[2], axor[2], boff[4], soff[4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int row = wm + i * 32 + frow;
+    arow[i] = row * (BK * 2);
+    axor[i] = (2 * fk) ^ ((row >> 1) & 7);
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int r = GATEUP ? (j < 2 ? 0 : BN / 2) + wn + (j & 1) * 32 + frow : 2 * wn + j * 32 + frow;
+    boff[j] = DA_BYTES + (r >> 4) * 512 + (r & 15) * 16 + 8 * fk;
+    soff[j] = DA_BYTES + DB_BYTES + (r >> 4) * 32 + (r & 15);
+  }
+
+  set_load_tile();
+  issue(0);
+  advance();
+  issue(1);
+  advance();
+  int cslot = 0;
+  for (int t = worker; t < total; t += G) {
+    const int mt = t / col_tiles, nt = t - mt * col_tiles;
+    const int e = tiles[2 * mt], m0 = tiles[2 * mt + 1];
+    const int beg = offsets[e], n = offsets[e + 1] - beg;
+    const int64_t c0 = (int64_t)nt * (GATEUP ? BN / 2 : BN);
+    const bool active = m0 + wm < n;
+
+    float16_t acc[2][4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    for (int s = 0; s < steps; ++s) {
+      // this step's loads landed (the next step's may be in flight); every
+      // wave is done with the slot the next issue overwrites
+      dma::wait_and_barrier<LOADS_PER_STAGE>();
+      issue(cslot == 0 ? 2 : cslot - 1);
+      advance();
+      if (active) {
+        const unsigned char* st = moe_dma_lds + cslot * DSTAGE;
+#pragma unroll
+        for (int jb = 0; jb < 2; ++jb) {
+          u32x2_t raw[4];
+          uint32_t sc[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            raw[j] = *reinterpret_cast<const u32x2_t*>(st + boff[j] + jb * 256);
+            sc[j] = st[soff[j] + jb * 16];
+          }
+#pragma unroll
+          for (int kk = 0; kk < 2; ++kk) {
+            bf16x8_t fa[2], fb[4];
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+              fa[i] = *reinterpret_cast<const bf16x8_t*>(st + arow[i] + 16 * ((4 * jb + kk) ^ axor[i]));
+#pragma unroll
+            for (int j = 0; j < 4; ++j) fb[j] = gemm::dequant8<1>(u32x2_t{raw[j][kk], 0u}, sc[j]);
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+              for (int j = 0; j < 4; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+          }
+        }
+      }
+      cslot = cslot == 2 ? 0 : cslot + 1;
+    }
+
+    if (active) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = wm + i * 32 + 8 * (r >> 2) + 4 * fk + (r & 3);
+          const int slot = m0 + row;
+          if (slot >= n) continue;
+          if (GATEUP) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+              const float v = activate(act, acc[i][j][r], acc[i][j + 2][r]);
+              const int64_t ch = c0 + wn + j * 32 + frow;
+              reinterpret_cast<__bf16*>(act_out)[(int64_t)(beg + slot) * inter + ch] = (__bf16)v;
+            }
+          } else {
+            const int pair = sorted[beg + slot];
+            const float rw = route_w[pair];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const int64_t h = c0 + 2 * wn + j * 32 + frow;
+              y_out[(int64_t)pair * hidden + h] = rw * acc[i][j][r];
+            }
+          }
+        }
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(dma::waitcnt_vm(0));  // no load may land after the workgroup ends
+}
+
 // ---------------------------------------------------------------- combine --
 template <int OUT>
 __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restrict__ y,
@@ -685,7 +915,8 @@ extern "C" int kq_moe_forward(int activation, float act_beta, float act_linear_b
                               const uint8_t* w2_st, int out_dtype, void* out,
                               void* workspace, int64_t workspace_bytes, uint32_t flags,
                               void* stream) {
-  (void)flags;
+  if (flags & ~(uint32_t)KQ_MOE_REGISTER_STAGED)
+    return kq_fail(KQ_ERR_INVALID, "kq_moe_forward: unknown flags 0x%x", flags);
   if (activation != KQ_ACT_SITU && activation != KQ_ACT_SWIGLU)
     return kq_fail(KQ_ERR_INVALID, "kq_moe_forward: unknown activation %d", activation);
   if (out_dtype != KQ_DT_BF16 && out_dtype != KQ_DT_F32)
@@ -762,7 +993,24 @@ extern "C" int kq_moe_forward(int activation, float act_beta, float act_linear_b
   }
   const size_t lds = 2 * (size_t)STAGE + BM * sizeof(int);
   const bool any_large = L.pairs > SMALL_MAX;
-  if (any_large) {
+  // direct-to-LDS path unless a buffer exceeds one 32-bit buffer range
+  const uint64_t x_bytes = (uint64_t)tokens * ldx * 2, act_bytes = (uint64_t)L.pairs * inter * 2;
+  const bool dma_path = !(flags & KQ_MOE_REGISTER_STAGED) && x_bytes <= dma::MAX_RANGE &&
+                        act_bytes <= dma::MAX_RANGE &&
+                        (uint64_t)(2 * inter) * hidden / 2 <= dma::MAX_RANGE;
+  int grid_dma = 0;
+  if (any_large && dma_path) {
+    int dev = 0, cus = 0;
+    if ((e = hipGetDevice(&dev)) == hipSuccess)
+      e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return kq_check_launch(e, "kq_moe_forward/device");
+    grid_dma = cus / 8 * 8 > 0 ? cus / 8 * 8 : 8;
+    const int col_tiles = (int)(inter / (BN / 2));
+    moe_large_dma_kernel<true><<<grid_dma, THREADS, 0, st>>>(
+        xb, ldx, (uint32_t)x_bytes, topk, offsets, sorted, large_tiles, meta, w13_t, w13_st,
+        2 * inter, hidden, inter, col_tiles, ap, route_weights, act, y, hidden);
+    if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_moe_forward/gateup_large");
+  } else if (any_large) {
     e = hipFuncSetAttribute((const void*)moe_large_kernel<true>,
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e == hipSuccess)
@@ -786,7 +1034,13 @@ extern "C" int kq_moe_forward(int activation, float act_beta, float act_linear_b
                                 route_weights, act, y, hidden);
     if (e != hipSuccess) return kq_check_launch(e, "kq_moe_forward/down_small");
   }
-  if (any_large) {
+  if (any_large && dma_path) {
+    const int col_tiles = (int)(hidden / BN);
+    moe_large_dma_kernel<false><<<grid_dma, THREADS, 0, st>>>(
+        act, inter, (uint32_t)act_bytes, topk, offsets, sorted, large_tiles, meta, w2_t, w2_st,
+        hidden, inter, inter, col_tiles, ap, route_weights, act, y, hidden);
+    if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_moe_forward/down_large");
+  } else if (any_large) {
     moe_large_kernel<false><<<dim3((unsigned)L.max_large, (unsigned)((hidden + BN - 1) / BN)), THREADS, lds, st>>>(
         act, inter, topk, offsets, sorted, large_tiles, meta, w2_t, w2_st, hidden, inter, inter,
         ap, route_weights, act, y, hidden);

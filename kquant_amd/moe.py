@@ -177,6 +177,7 @@ def grouped_expert_forward(
     beta: float = 4.0,
     linear_beta: float = 25.0,
     out_dtype: torch.dtype = torch.float32,
+    register_staged: bool = False,
 ) -> torch.Tensor:
     """Route-weighted expert outputs ``[T, H]`` (fp32 by default, as the
     reference's accumulator is).
@@ -184,6 +185,9 @@ def grouped_expert_forward(
     The weights are either an ``MXFP4Experts`` from
     ``prepare_expert_weights`` (serving: prepare once per layer) or the four
     checkpoint-layout tensors, which are then prepared on every call.
+    ``register_staged`` runs the grouped GEMMs on the register-staged kernel
+    (taken anyway when a buffer exceeds 4 GiB) instead of the direct-to-LDS
+    one; both meet the same error bound and differ only by fp32 rounding.
     """
 
     if activation not in ("situ", "swiglu"):
@@ -220,5 +224,6 @@ def grouped_expert_forward(
            float(beta), float(linear_beta), N.ptr(xb), hidden, tokens, hidden, N.ptr(ids),
            N.ptr(rw), topk, prepared.experts, prepared.inter, N.ptr(prepared.w13_tiles),
            N.ptr(prepared.w13_scale_tiles), N.ptr(prepared.w2_tiles), N.ptr(prepared.w2_scale_tiles),
-           N.DTYPE_CODES[out_dtype], N.ptr(out), N.ptr(ws), ws.numel(), 0, N.stream(gpu))
+           N.DTYPE_CODES[out_dtype], N.ptr(out), N.ptr(ws), ws.numel(),
+           N.MOE_REGISTER_STAGED if register_staged else 0, N.stream(gpu))
     return out if host is None else out.to(host)
