@@ -85,18 +85,6 @@ int kq_mx_dequant(int fmt, const void* q, const uint8_t* scale, int64_t rows,
                   int64_t k, int out_dtype, void* out, uint32_t flags,
                   void* stream);
 
-/* Split a bf16/f16 [rows, k] matrix into two MXFP8 parts: hi = the MXFP8
- * quantization of x (the kq_mx_quantize rule and bytes), lo = the MXFP8
- * quantization of the fp32 residual x - dequant(hi).  dequant(hi) +
- * dequant(lo) reproduces bf16 inputs (all but ~3e-5 of N(0,1) elements
- * exactly, the rest within 2^-22 of their block maximum), which lets a
- * GEMM run bf16 activations on the block-scaled fp8 MFMA.  No kquant
- * counterpart: it is the operand format of kq_moe_forward's GEMV path.
- * out_hi / out_lo: uint8 [rows, k]; scale_hi / scale_lo: uint8 [rows, k/32]. */
-int kq_mx_split_quantize(int in_dtype, const void* in, int64_t ld_in, int64_t rows, int64_t k,
-                         uint8_t* out_hi, uint8_t* out_lo, uint8_t* scale_hi, uint8_t* scale_lo,
-                         void* stream);
-
 /* Repack `mats` MXFP4 matrices (packed [rows, k/2] + E8M0 [rows, k/32] each,
  * stacked) into the MFMA-tiled layout kq_moe_forward reads: per matrix,
  * 1 KiB tiles [rows/16][k/128] with tile byte 16*l + j = packed[16 rg + l%16]

@@ -50,7 +50,6 @@ _F64 = ctypes.c_double
 SIGNATURES: dict[str, list] = {
     "kq_mx_quantize": [_INT, _INT, _VP, _I64, _I64, _I64, _VP, _VP, _U32, _VP],
     "kq_mx_dequant": [_INT, _VP, _VP, _I64, _I64, _INT, _VP, _U32, _VP],
-    "kq_mx_split_quantize": [_INT, _VP, _I64, _I64, _I64, _VP, _VP, _VP, _VP, _VP],
     "kq_mx_tile_weights": [_VP, _VP, _I64, _I64, _I64, _VP, _VP, _VP],
     "kq_unpack_codes": [_VP, _I64, _VP, _VP],
     "kq_pack_codes": [_VP, _I64, _VP, _VP],

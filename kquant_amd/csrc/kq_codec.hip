@@ -190,68 +190,6 @@ __global__ __launch_bounds__(256) void mx_quantize_kernel(
   }
 }
 
-// ------------------------------------------------------ split quantize --
-// x = dequant(hi) + dequant(lo) + err: hi is the MXFP8 quantization of x (the
-// same rule and bytes as mx_quantize_kernel), lo the MXFP8 quantization of the
-// fp32 residual x - dequant(hi) with its own block scale.  For bf16 inputs the
-// two E4M3 parts carry all 8 significant bits in almost every element (the
-// residual after hi has at most 4-5 significant bits), so a GEMM over hi and
-// lo on the block-scaled fp8 MFMA reproduces a bf16-operand GEMM.
-template <int IN>
-__global__ __launch_bounds__(256) void mx_split_quantize_kernel(
-    const uint16_t* __restrict__ in, int64_t ld_in, int64_t nblk, int64_t total_blocks,
-    uint8_t* __restrict__ out_hi, uint8_t* __restrict__ out_lo, uint8_t* __restrict__ s_hi,
-    uint8_t* __restrict__ s_lo) {
-  const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int64_t blk = g >> 2;
-  const int part = (int)(g & 3);
-  if (blk >= total_blocks) return;
-  const int64_t row = blk / nblk;
-  const int64_t kb = blk - row * nblk;
-  const int64_t col = kb * 32 + part * 8;
-  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-  const u32x4 v = *reinterpret_cast<const u32x4*>(in + row * ld_in + col);
-  float x[8];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    x[2 * i] = IN == 0 ? bf16_bits_to_f32(v[i] & 0xffffu) : f16_bits_to_f32(v[i] & 0xffffu);
-    x[2 * i + 1] = IN == 0 ? bf16_bits_to_f32(v[i] >> 16) : f16_bits_to_f32(v[i] >> 16);
-  }
-  float amax = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(x[i]));
-  amax = quad_max(amax);
-  const int e_hi = mx_block_exponent(amax, 448.0f);
-  const float inv_hi = mx_inv_scale(e_hi);
-  const float sc_hi = e8m0_to_f32((uint32_t)(e_hi + 127));  // 2^e_hi
-  uint32_t hi[8];
-  float r[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    hi[i] = f32_to_e4m3_rne(__builtin_amdgcn_fmed3f(x[i] * inv_hi, -448.0f, 448.0f));
-    r[i] = x[i] - e4m3_to_f32(hi[i]) * sc_hi;
-  }
-  float rmax = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) rmax = fmaxf(rmax, fabsf(r[i]));
-  rmax = quad_max(rmax);
-  const int e_lo = mx_block_exponent(rmax, 448.0f);
-  const float inv_lo = mx_inv_scale(e_lo);
-  uint32_t lo[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) lo[i] = f32_to_e4m3_rne(__builtin_amdgcn_fmed3f(r[i] * inv_lo, -448.0f, 448.0f));
-  if (part == 0) {
-    s_hi[blk] = (uint8_t)(e_hi + 127);
-    s_lo[blk] = (uint8_t)(e_lo + 127);
-  }
-  const int64_t o = row * (nblk * 32) + col;
-  *reinterpret_cast<u32x2*>(out_hi + o) =
-      u32x2{hi[0] | (hi[1] << 8) | (hi[2] << 16) | (hi[3] << 24), hi[4] | (hi[5] << 8) | (hi[6] << 16) | (hi[7] << 24)};
-  *reinterpret_cast<u32x2*>(out_lo + o) =
-      u32x2{lo[0] | (lo[1] << 8) | (lo[2] << 16) | (lo[3] << 24), lo[4] | (lo[5] << 8) | (lo[6] << 16) | (lo[7] << 24)};
-}
-
 // ------------------------------------------------------------ dequantize --
 // OUT: 0 bf16, 1 f16, 2 f32.  Each lane expands 8 codes of one block.
 template <int FMT, int OUT, bool HW>
@@ -528,30 +466,6 @@ extern "C" int kq_mx_dequant(int fmt, const void* q, const uint8_t* scale, int64
                                   : launch_dequant<1, 2>(hw, qb, scale, total, out, st);
   }
   return kq_check_launch(err, "kq_mx_dequant");
-}
-
-extern "C" int kq_mx_split_quantize(int in_dtype, const void* in, int64_t ld_in, int64_t rows,
-                                    int64_t k, uint8_t* out_hi, uint8_t* out_lo, uint8_t* scale_hi,
-                                    uint8_t* scale_lo, void* stream) {
-  if (in_dtype != KQ_DT_BF16 && in_dtype != KQ_DT_F16)
-    return kq_fail(KQ_ERR_INVALID, "kq_mx_split_quantize: input must be bf16 or f16");
-  if (rows < 0 || k < 0 || k % 32 != 0 || ld_in < k || ld_in % 8 != 0)
-    return kq_fail(KQ_ERR_INVALID, "kq_mx_split_quantize: need k %% 32 == 0, ld_in >= k, ld_in %% 8 == 0");
-  if (kq_misaligned(in, 16) || kq_misaligned(out_hi, 8) || kq_misaligned(out_lo, 8))
-    return kq_fail(KQ_ERR_INVALID, "kq_mx_split_quantize: misaligned buffers");
-  if (rows == 0 || k == 0) return KQ_OK;
-  const int64_t nblk = k / 32, total = rows * nblk;
-  if (total * 4 / 256 + 1 > (int64_t)0x7fffffff)
-    return kq_fail(KQ_ERR_LIMIT, "kq_mx_split_quantize: too many blocks");
-  const dim3 grid((unsigned)((total * 4 + 255) / 256));
-  hipStream_t st = (hipStream_t)stream;
-  if (in_dtype == KQ_DT_BF16)
-    mx_split_quantize_kernel<0><<<grid, 256, 0, st>>>((const uint16_t*)in, ld_in, nblk, total, out_hi,
-                                                      out_lo, scale_hi, scale_lo);
-  else
-    mx_split_quantize_kernel<1><<<grid, 256, 0, st>>>((const uint16_t*)in, ld_in, nblk, total, out_hi,
-                                                      out_lo, scale_hi, scale_lo);
-  return kq_check_launch(hipGetLastError(), "kq_mx_split_quantize");
 }
 
 extern "C" int kq_mx_tile_weights(const uint8_t* q, const uint8_t* scale, int64_t mats,

@@ -12,9 +12,9 @@
 //      the T*topk pairs by expert (stable in pair order), the list of experts
 //      with 1..16 pairs ("small") and the (expert, row-tile) list of the others.
 //   2. gate/up: small experts on a GEMV-shaped MFMA kernel (16 token slots,
-//      weights streamed once with 16-byte loads, K split over 4 waves);
-//      large experts on a 256x256-tile grouped GEMM (gathered token rows,
-//      packed weights in LDS).  Both fuse the activation and write bf16
+//      weights streamed once with 16-byte loads, K split over 8 waves);
+//      large experts on a persistent 256x256-tile grouped GEMM (gathered
+//      token rows and packed weights loaded straight into LDS).  Both fuse the activation and write bf16
 //      intermediates in expert-sorted order.
 //   3. down: same two shapes over W2; the epilogue scales by the route weight
 //      and writes one fp32 row per pair.
@@ -40,8 +40,7 @@ constexpr int S_BYTES = BN * 2;
 constexpr int STAGE = A_BYTES + B_BYTES + S_BYTES;
 
 struct Layout {
-  size_t counts, offsets, block_counts, sorted, small_list, large_tiles, meta, act, y;
-  size_t xs_hi, xs_lo, xs_shi, xs_slo, as_hi, as_lo, as_shi, as_slo, total;
+  size_t counts, offsets, block_counts, sorted, small_list, large_tiles, meta, act, y, total;
   int64_t pairs, nblk, max_small, max_large;
 };
 
@@ -63,15 +62,6 @@ static Layout make_layout(int64_t tokens, int topk, int experts, int64_t hidden,
   L.meta = o;         o = align256(o + sizeof(int) * 4);
   L.act = o;          o = align256(o + 2 * (size_t)L.pairs * inter);
   L.y = o;            o = align256(o + 4 * (size_t)L.pairs * hidden);
-  // MXFP8 hi/lo split of the tokens and of the intermediates (small path)
-  L.xs_hi = o;        o = align256(o + (size_t)tokens * hidden);
-  L.xs_lo = o;        o = align256(o + (size_t)tokens * hidden);
-  L.xs_shi = o;       o = align256(o + (size_t)tokens * hidden / 32);
-  L.xs_slo = o;       o = align256(o + (size_t)tokens * hidden / 32);
-  L.as_hi = o;        o = align256(o + (size_t)L.pairs * inter);
-  L.as_lo = o;        o = align256(o + (size_t)L.pairs * inter);
-  L.as_shi = o;       o = align256(o + (size_t)L.pairs * inter / 32);
-  L.as_slo = o;       o = align256(o + (size_t)L.pairs * inter / 32);
   L.total = o;
   return L;
 }
@@ -134,11 +124,19 @@ __global__ __launch_bounds__(1024) void route_scan_kernel(
   __shared__ int s_tiles[MAX_EXPERTS];
   __shared__ int scratch[1024];
   for (int e = threadIdx.x; e < experts; e += 1024) {
+    // column scan of this expert's per-block counts, 16 independent loads at
+    // a time so their latencies overlap
     int s = 0;
-    for (int b = 0; b < nblk; ++b) {
-      const int c = block_counts[(int64_t)b * experts + e];
-      block_counts[(int64_t)b * experts + e] = s;
-      s += c;
+    for (int b0 = 0; b0 < nblk; b0 += 16) {
+      int c[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        c[i] = b0 + i < nblk ? block_counts[(int64_t)(b0 + i) * experts + e] : 0;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        if (b0 + i < nblk) block_counts[(int64_t)(b0 + i) * experts + e] = s;
+        s += c[i];
+      }
     }
     counts[e] = s;
     s_cnt[e] = s;
@@ -258,25 +256,22 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 // ------------------------------------------------- GEMV-shaped small path --
 // One workgroup: one expert with n <= 16 pairs and CH output rows per
-// projection; WAVES waves split K.  The packed MXFP4 weights go straight into
-// the block-scaled MFMA v_mfma_scale_f32_16x16x128_f8f6f4 (B = E2M1, its E8M0
-// scale per 32-element block) with no dequantization: lane (n, g) of a
-// 16x16x128 step holds the 16 packed bytes of weight row n, k-block g, which
-// is exactly the checkpoint layout, so every weight byte is read once with a
-// 16-byte load.  The A operand is the activation split into two MXFP8 parts
-// (hi + residual lo, kq_mx_split_quantize), two MFMAs per step, which
-// reproduces the bf16 activation.  A lane (m, g) holds A bytes
-// k = 16g + i (i < 16) and 64 + 16g + (i - 16) of its token row and supplies
-// the E8M0 scale of block g.  Loads run two 128-k steps ahead of the MFMAs.
+// projection; WAVES waves split K.  Weights stream from the
+// kq_mx_tile_weights layout with one 16-byte non-temporal load per lane per
+// 1 KiB tile: lane (r, g) of a tile holds weight row r, k 32 g .. 32 g + 31 of
+// the 128-k chunk, and its own E8M0 byte.  They are expanded to bf16 in
+// registers (gfx950 scaled converts; E2M1 x 2^s is exact in bf16) and fed to
+// v_mfma_f32_16x16x32_bf16 with the bf16 activation rows read as they are, so
+// every product is exact and the accumulation is fp32.  MFMA t (0..3) of a
+// chunk takes k = 32 g + 8 t + [0, 8) from lane half-group g of both
+// operands, which puts each lane's 16 weight bytes and its 64 activation bytes
+// in one contiguous piece.  Loads run two 128-k steps ahead of the MFMAs.
 //
 // GATEUP: rows of w13 (gate c, up I + c), output act -> bf16 intermediates.
 // !GATEUP: rows of w2, output route_weight * partial -> fp32 pair rows.
-typedef int i32x8_t __attribute__((ext_vector_type(8)));
-
 template <bool GATEUP, int CH, int WAVES, int STEPS>
 __global__ __launch_bounds__(WAVES * 64) void moe_small_kernel(
-    const uint8_t* __restrict__ ahi, const uint8_t* __restrict__ alo,
-    const uint8_t* __restrict__ ashi, const uint8_t* __restrict__ aslo, int topk,
+    const uint16_t* __restrict__ a, int64_t lda, int topk,
     const int* __restrict__ offsets, const int* __restrict__ sorted,
     const int* __restrict__ small_list, const uint8_t* __restrict__ wt,
     const uint8_t* __restrict__ wst, int64_t rows_per_expert, int64_t K, int64_t inter,
@@ -310,8 +305,7 @@ __global__ __launch_bounds__(WAVES * 64) void moe_small_kernel(
     uint32_t ws[NB];
   };
   struct ABuf {
-    u32x4_t h0, h1, l0, l1;
-    uint32_t sh, sl;
+    u32x4_t v[4];
   };
   auto load_w = [&](int s, WBuf& B) {
 #pragma unroll
@@ -337,30 +331,24 @@ __global__ __launch_bounds__(WAVES * 64) void moe_small_kernel(
   const int mslot = m < n ? m : 0;
   const int apair = sorted[beg + mslot];
   const int64_t arow = GATEUP ? (int64_t)(apair / topk) : (int64_t)(beg + mslot);
-  const uint8_t* ah = ahi + arow * K;
-  const uint8_t* al = alo + arow * K;
-  const uint8_t* ash = ashi + arow * (K / 32);
-  const uint8_t* asl = aslo + arow * (K / 32);
+  const uint16_t* ap = a + arow * lda + 32 * g;
   auto load_a = [&](int s, ABuf& B) {
     const int64_t c = c_first + s;                // 128-k chunk
-    B.h0 = *reinterpret_cast<const u32x4_t*>(ah + 128 * c + 16 * g);
-    B.h1 = *reinterpret_cast<const u32x4_t*>(ah + 128 * c + 64 + 16 * g);
-    B.l0 = *reinterpret_cast<const u32x4_t*>(al + 128 * c + 16 * g);
-    B.l1 = *reinterpret_cast<const u32x4_t*>(al + 128 * c + 64 + 16 * g);
-    B.sh = ash[4 * c + g];
-    B.sl = asl[4 * c + g];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) B.v[t] = *reinterpret_cast<const u32x4_t*>(ap + 128 * c + 8 * t);
   };
   f32x4_t acc[NB];
 #pragma unroll
   for (int b = 0; b < NB; ++b) acc[b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   auto compute = [&](const WBuf& W, const ABuf& A) {
-    const i32x8_t ah8 = __builtin_bit_cast(i32x8_t, (u32x4_t[2]){A.h0, A.h1});
-    const i32x8_t al8 = __builtin_bit_cast(i32x8_t, (u32x4_t[2]){A.l0, A.l1});
 #pragma unroll
-    for (int b = 0; b < NB; ++b) {
-      const i32x8_t w8 = i32x8_t{(int)W.w[b][0], (int)W.w[b][1], (int)W.w[b][2], (int)W.w[b][3], 0, 0, 0, 0};
-      acc[b] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ah8, w8, acc[b], 0, 4, 0, (int)A.sh, 0, (int)W.ws[b]);
-      acc[b] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(al8, w8, acc[b], 0, 4, 0, (int)A.sl, 0, (int)W.ws[b]);
+    for (int t = 0; t < 4; ++t) {
+      const bf16x8_t fa = __builtin_bit_cast(bf16x8_t, A.v[t]);
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const bf16x8_t fb = gemm::dequant8<1>(u32x2_t{W.w[b][t], 0u}, W.ws[b]);
+        acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa, fb, acc[b], 0, 0, 0);
+      }
     }
   };
   ABuf a0, a1, a2;
@@ -972,23 +960,10 @@ extern "C" int kq_moe_forward(int activation, float act_beta, float act_linear_b
 
   const uint16_t* xb = (const uint16_t*)x;
   // gate/up
-  uint8_t* xs_hi = w + L.xs_hi;
-  uint8_t* xs_lo = w + L.xs_lo;
-  uint8_t* xs_shi = w + L.xs_shi;
-  uint8_t* xs_slo = w + L.xs_slo;
-  uint8_t* as_hi = w + L.as_hi;
-  uint8_t* as_lo = w + L.as_lo;
-  uint8_t* as_shi = w + L.as_shi;
-  uint8_t* as_slo = w + L.as_slo;
   {
-    const int rc = kq_mx_split_quantize(KQ_DT_BF16, x, ldx, tokens, hidden, xs_hi, xs_lo, xs_shi,
-                                        xs_slo, stream);
-    if (rc != KQ_OK) return rc;
     const dim3 grid((unsigned)L.max_small, (unsigned)(inter / 32));
-    e = launch_small<true, 32>(grid, hidden, st, (const uint8_t*)xs_hi, (const uint8_t*)xs_lo,
-                               (const uint8_t*)xs_shi, (const uint8_t*)xs_slo, topk, offsets, sorted,
-                               small_list, w13_t, w13_st, 2 * inter, hidden, inter, ap,
-                               route_weights, act, y, hidden);
+    e = launch_small<true, 32>(grid, hidden, st, xb, ldx, topk, offsets, sorted, small_list, w13_t,
+                               w13_st, 2 * inter, hidden, inter, ap, route_weights, act, y, hidden);
     if (e != hipSuccess) return kq_check_launch(e, "kq_moe_forward/gateup_small");
   }
   const size_t lds = 2 * (size_t)STAGE + BM * sizeof(int);
@@ -1024,14 +999,10 @@ extern "C" int kq_moe_forward(int activation, float act_beta, float act_linear_b
   }
   // down
   {
-    const int rc = kq_mx_split_quantize(KQ_DT_BF16, act, inter, L.pairs, inter, as_hi, as_lo, as_shi,
-                                        as_slo, stream);
-    if (rc != KQ_OK) return rc;
     const dim3 grid((unsigned)L.max_small, (unsigned)(hidden / 64));
-    e = launch_small<false, 64>(grid, inter, st, (const uint8_t*)as_hi, (const uint8_t*)as_lo,
-                                (const uint8_t*)as_shi, (const uint8_t*)as_slo, topk, offsets, sorted,
-                                small_list, w2_t, w2_st, hidden, inter, inter, ap,
-                                route_weights, act, y, hidden);
+    e = launch_small<false, 64>(grid, inter, st, (const uint16_t*)act, inter, topk, offsets, sorted,
+                                small_list, w2_t, w2_st, hidden, inter, inter, ap, route_weights, act,
+                                y, hidden);
     if (e != hipSuccess) return kq_check_launch(e, "kq_moe_forward/down_small");
   }
   if (any_large && dma_path) {

@@ -172,29 +172,3 @@ def test_repeat_runs_are_identical(gpu):
     a = _quantize("mxfp4", w)
     b = _quantize("mxfp4", w)
     assert np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1])
-
-
-def test_split_quantize_hi_is_mxfp8_and_reconstructs(gpu):
-    """kq_mx_split_quantize: hi == MXFP8 quantize bytes; hi + lo reproduces bf16."""
-    w = workloads.cfg2_activations(256, 7168)
-    bits = w.view(torch.int16).numpy().view(np.uint16)
-    x = w.to(gpu)
-    rows, k = x.shape
-    hi = torch.empty(rows, k, dtype=torch.uint8, device=gpu)
-    lo = torch.empty_like(hi)
-    shi = torch.empty(rows, k // 32, dtype=torch.uint8, device=gpu)
-    slo = torch.empty_like(shi)
-    N.call("kq_mx_split_quantize", N.DT_BF16, N.ptr(x), k, rows, k, N.ptr(hi), N.ptr(lo), N.ptr(shi),
-           N.ptr(slo), N.stream(gpu))
-    torch.cuda.synchronize()
-    rq, rs = oracle.mx_quantize("mxfp8", bits, "bf16")
-    assert np.array_equal(hi.cpu().numpy(), rq) and np.array_equal(shi.cpu().numpy(), rs)
-    xf = oracle.bf16_bits_to_f32(bits)
-    d_hi = oracle.mx_dequant("mxfp8", rq, rs)
-    # lo is the MXFP8 rule applied to the fp32 residual
-    rl, rsl = oracle.mx_quantize("mxfp8", (xf - d_hi).astype(np.float32), "f32")
-    assert np.array_equal(lo.cpu().numpy(), rl) and np.array_equal(slo.cpu().numpy(), rsl)
-    recon = d_hi + oracle.mx_dequant("mxfp8", rl, rsl)
-    blockmax = np.abs(xf.reshape(rows, -1, 32)).max(-1, keepdims=True)
-    assert (np.abs(recon - xf).reshape(rows, -1, 32) / blockmax).max() < 2.0 ** -20
-    assert np.mean(recon == xf) > 0.999
