@@ -14,8 +14,8 @@
 //   2. gate/up: small experts on a GEMV-shaped MFMA kernel (16 token slots,
 //      weights streamed once with 16-byte loads, K split over 8 waves);
 //      large experts on a persistent 256x256-tile grouped GEMM (gathered
-//      token rows and packed weights loaded straight into LDS).  Both fuse the activation and write bf16
-//      intermediates in expert-sorted order.
+//      token rows and packed weights loaded straight into LDS).  Both fuse
+//      the activation and write bf16 intermediates in expert-sorted order.
 //   3. down: same two shapes over W2; the epilogue scales by the route weight
 //      and writes one fp32 row per pair.
 //   4. combine: out[t] = sum of the topk pair rows in slot order.
@@ -255,42 +255,47 @@ using gemm::u32x4_t;
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 // ------------------------------------------------- GEMV-shaped small path --
-// One workgroup: one expert with n <= 16 pairs and CH output rows per
-// projection; WAVES waves split K.  Weights stream from the
-// kq_mx_tile_weights layout with one 16-byte non-temporal load per lane per
-// 1 KiB tile: lane (r, g) of a tile holds weight row r, k 32 g .. 32 g + 31 of
-// the 128-k chunk, and its own E8M0 byte.  They are expanded to bf16 in
+// One workgroup: one expert with n <= 16 pairs.  Its S * RW waves form RW row
+// groups of S waves; the S waves of a group split K, and each holds NBP
+// 16-row blocks per projection (GATEUP: gate rows c and up rows I + c), so a
+// workgroup covers CH = RW * 16 * NBP output channels.  Weights stream from
+// the kq_mx_tile_weights layout with one 16-byte non-temporal load per lane
+// per 1 KiB tile: lane (r, g) of a tile holds weight row r, k 32 g .. 32 g + 31
+// of the 128-k chunk, and its own E8M0 byte.  They are expanded to bf16 in
 // registers (gfx950 scaled converts; E2M1 x 2^s is exact in bf16) and fed to
 // v_mfma_f32_16x16x32_bf16 with the bf16 activation rows read as they are, so
 // every product is exact and the accumulation is fp32.  MFMA t (0..3) of a
 // chunk takes k = 32 g + 8 t + [0, 8) from lane half-group g of both
 // operands, which puts each lane's 16 weight bytes and its 64 activation bytes
-// in one contiguous piece.  Loads run two 128-k steps ahead of the MFMAs.
+// in one contiguous piece.  Loads run P 128-k steps ahead of the MFMAs through
+// a ring of P + 1 register buffers (straight-line code for a compile-time
+// step count, so the compiler counts the outstanding loads exactly).
 //
-// GATEUP: rows of w13 (gate c, up I + c), output act -> bf16 intermediates.
+// GATEUP: rows of w13, output act -> bf16 intermediates.
 // !GATEUP: rows of w2, output route_weight * partial -> fp32 pair rows.
-template <bool GATEUP, int CH, int WAVES, int STEPS>
-__global__ __launch_bounds__(WAVES * 64) void moe_small_kernel(
+template <bool GATEUP, int NBP, int S, int RW, int P, int STEPS>
+__global__ __launch_bounds__(S * RW * 64) void moe_small_kernel(
     const uint16_t* __restrict__ a, int64_t lda, int topk,
     const int* __restrict__ offsets, const int* __restrict__ sorted,
     const int* __restrict__ small_list, const uint8_t* __restrict__ wt,
     const uint8_t* __restrict__ wst, int64_t rows_per_expert, int64_t K, int64_t inter,
     ActParams act, const float* __restrict__ route_w, uint16_t* __restrict__ act_out,
     float* __restrict__ y_out, int64_t hidden) {
-  constexpr int NBP = CH / 16;                    // 16-row blocks per projection
-  constexpr int NB = GATEUP ? 2 * NBP : NBP;      // blocks per wave
+  constexpr int NB = GATEUP ? 2 * NBP : NBP;      // 16-row blocks per wave
+  constexpr int CH = RW * 16 * NBP;               // channels per workgroup
+  constexpr int NBUF = P + 1;
   const int e = small_list[blockIdx.x];           // -1 past the last small expert
   if (e < 0) return;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int kpart = wave % S, rgw = wave / S;
   const int m = lane & 15, g = lane >> 4;
-  const int64_t c0 = (int64_t)blockIdx.y * CH;
+  const int64_t c0 = (int64_t)blockIdx.y * CH + rgw * 16 * NBP;  // first channel of this wave
 
   // weight tiles (kq_mx_tile_weights layout): [expert][row group][chunk][1 KiB]
   const int64_t nchunk = K / 128;
   const int64_t rgs = rows_per_expert / 16;
-  const int64_t kper = K / WAVES;                 // k range of this wave
-  const int64_t c_first = (wave * kper) / 128;    // first 128-k chunk of the wave
-  const int steps = (int)(kper / 128);
+  const int64_t c_first = kpart * nchunk / S;     // this wave's 128-k chunks
+  const int steps = (int)((kpart + 1) * nchunk / S - c_first);
   const uint8_t* wtile[NB];
   const uint8_t* stile[NB];
 #pragma unroll
@@ -315,10 +320,11 @@ __global__ __launch_bounds__(WAVES * 64) void moe_small_kernel(
     }
   };
   // Issue the first weight loads before the dependent token-index loads.
-  WBuf w0, w1, w2;
+  WBuf wb[NBUF];
+  ABuf ab[NBUF];
   if constexpr (STEPS > 0) {
-    load_w(0, w0);
-    if (STEPS > 1) load_w(1, w1);
+#pragma unroll
+    for (int s = 0; s < P && s < STEPS; ++s) load_w(s, wb[s]);
   }
   __builtin_amdgcn_sched_barrier(0);
 
@@ -351,76 +357,76 @@ __global__ __launch_bounds__(WAVES * 64) void moe_small_kernel(
       }
     }
   };
-  ABuf a0, a1, a2;
   if constexpr (STEPS > 0) {
-    // Straight-line pipeline for a compile-time step count: three buffers,
-    // loads issued two steps ahead; with no loop the compiler counts the
-    // outstanding loads exactly and never waits for a prefetch early.
-    load_a(0, a0);
-    if (STEPS > 1) load_a(1, a1);
+#pragma unroll
+    for (int s = 0; s < P && s < STEPS; ++s) load_a(s, ab[s]);
 #pragma unroll
     for (int s = 0; s < STEPS; ++s) {
-      if (s + 2 < STEPS) {
-        if ((s + 2) % 3 == 0) { load_w(s + 2, w0); load_a(s + 2, a0); }
-        else if ((s + 2) % 3 == 1) { load_w(s + 2, w1); load_a(s + 2, a1); }
-        else { load_w(s + 2, w2); load_a(s + 2, a2); }
+      if (s + P < STEPS) {
+        load_w(s + P, wb[(s + P) % NBUF]);
+        load_a(s + P, ab[(s + P) % NBUF]);
       }
       __builtin_amdgcn_sched_barrier(0);
-      if (s % 3 == 0) compute(w0, a0);
-      else if (s % 3 == 1) compute(w1, a1);
-      else compute(w2, a2);
+      compute(wb[s % NBUF], ab[s % NBUF]);
       __builtin_amdgcn_sched_barrier(0);
     }
   } else {
     // Runtime step count: two alternating buffers; loads are never
     // predicated (past the last step they re-read it, in bounds).
     const int last = steps - 1;
-    load_w(0, w0);
-    load_a(0, a0);
+    load_w(0, wb[0]);
+    load_a(0, ab[0]);
     for (int s = 0; s < steps; s += 2) {
       const int s1 = s + 1 < last ? s + 1 : last, s2 = s + 2 < last ? s + 2 : last;
-      load_w(s1, w1);
-      load_a(s1, a1);
+      load_w(s1, wb[1]);
+      load_a(s1, ab[1]);
       __builtin_amdgcn_sched_barrier(0);
-      compute(w0, a0);
+      compute(wb[0], ab[0]);
       __builtin_amdgcn_sched_barrier(0);
-      load_w(s2, w0);
-      load_a(s2, a0);
+      load_w(s2, wb[0]);
+      load_a(s2, ab[0]);
       __builtin_amdgcn_sched_barrier(0);
-      if (s + 1 < steps) compute(w1, a1);
+      if (s + 1 < steps) compute(wb[1], ab[1]);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
 
-  // reduce the waves' partial sums through LDS; wave w finishes block w
-  __shared__ f32x4_t red[WAVES][NB][64];
-#pragma unroll
-  for (int b = 0; b < NB; ++b) red[wave][b][lane] = acc[b];
-  __syncthreads();
-  if (wave >= NBP) return;
-  const int b = wave;
-  f32x4_t x0 = red[0][b][lane], x1 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int w = 1; w < WAVES; ++w) x0 += red[w][b][lane];
-  if (GATEUP) {
-    x1 = red[0][b + NBP][lane];
-#pragma unroll
-    for (int w = 1; w < WAVES; ++w) x1 += red[w][b + NBP][lane];
-  }
-
   // D layout (16x16): lane holds rows (token slots) 4*(lane/16) + j, column lane % 16
+  auto store = [&](int u, f32x4_t x0, f32x4_t x1) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int slot = 4 * g + j;
-    if (slot >= n) continue;
-    if (GATEUP) {
-      const float v = activate(act, x0[j], x1[j]);
-      const int64_t ch = c0 + 16 * b + m;
-      reinterpret_cast<__bf16*>(act_out)[(int64_t)(beg + slot) * inter + ch] = (__bf16)v;
-    } else {
-      const int pair = sorted[beg + slot];
-      const int64_t h = c0 + 16 * b + m;
-      y_out[(int64_t)pair * hidden + h] = route_w[pair] * x0[j];
+    for (int j = 0; j < 4; ++j) {
+      const int slot = 4 * g + j;
+      if (slot >= n) continue;
+      const int64_t ch = c0 + 16 * u + m;
+      if (GATEUP) {
+        const float v = activate(act, x0[j], x1[j]);
+        reinterpret_cast<__bf16*>(act_out)[(int64_t)(beg + slot) * inter + ch] = (__bf16)v;
+      } else {
+        const int pair = sorted[beg + slot];
+        y_out[(int64_t)pair * hidden + ch] = route_w[pair] * x0[j];
+      }
+    }
+  };
+  if constexpr (S == 1) {
+#pragma unroll
+    for (int u = 0; u < NBP; ++u) store(u, acc[u], GATEUP ? acc[u + NBP] : acc[u]);
+  } else {
+    // sum the S partial products of each block through LDS (in k order);
+    // wave kpart of a row group finishes blocks kpart, kpart + S, ...
+    __shared__ f32x4_t red[S * RW][NB][64];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) red[wave][b][lane] = acc[b];
+    __syncthreads();
+    for (int u = kpart; u < NBP; u += S) {
+      f32x4_t x0 = red[rgw * S][u][lane], x1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int p = 1; p < S; ++p) x0 += red[rgw * S + p][u][lane];
+      if (GATEUP) {
+        x1 = red[rgw * S][u + NBP][lane];
+#pragma unroll
+        for (int p = 1; p < S; ++p) x1 += red[rgw * S + p][u + NBP][lane];
+      }
+      store(u, x0, x1);
     }
   }
 }
@@ -871,20 +877,39 @@ using namespace kq::moe;
 // Pick the small-path instantiation for a reduction length K: 8 waves with a
 // compile-time step count when K is a multiple of 1024 (K/1024 steps of 128
 // per wave, 1..8), else 4 waves with a runtime loop (K % 512 == 0).
-template <bool GATEUP, int CH, typename... Args>
-static hipError_t launch_small(dim3 grid, int64_t K, hipStream_t st, Args... args) {
-  const int64_t steps8 = K % 1024 == 0 ? K / 1024 : 0;
-  switch (steps8) {
-#define KQ_SMALL_CASE(S) \
-    case S: moe_small_kernel<GATEUP, CH, 8, S><<<grid, 512, 0, st>>>(args...); break;
-    KQ_SMALL_CASE(1) KQ_SMALL_CASE(2) KQ_SMALL_CASE(3) KQ_SMALL_CASE(4)
-    KQ_SMALL_CASE(5) KQ_SMALL_CASE(6) KQ_SMALL_CASE(7) KQ_SMALL_CASE(8)
+// GEMV launch shapes (channels per workgroup = RW * 16 * NBP), measured on
+// the decode batches of 1, 4 and 16 tokens (hidden 7168, intermediate 2048):
+// K split over 4 waves for gate/up (14 steps of 128 each) and over 2 for down
+// (8 steps) streams better than shorter per-wave runs; prefetch depth 2-3 and
+// one or two row groups per workgroup are within 1 % of each other.
+#ifndef KQ_GU_NBP
+#define KQ_GU_NBP 2
+#define KQ_GU_S 4
+#define KQ_GU_RW 1
+#define KQ_GU_P 2
+#endif
+#ifndef KQ_DN_NBP
+#define KQ_DN_NBP 4
+#define KQ_DN_S 2
+#define KQ_DN_RW 1
+#define KQ_DN_P 2
+#endif
+
+template <bool GATEUP, int NBP, int S, int RW, int P, typename... Args>
+static hipError_t launch_small(int64_t experts_max, int64_t channels, int64_t K, hipStream_t st,
+                               Args... args) {
+  constexpr int CH = RW * 16 * NBP;
+  const dim3 grid((unsigned)experts_max, (unsigned)(channels / CH));
+  const int64_t nchunk = K / 128;
+  const int64_t steps = nchunk % S == 0 ? nchunk / S : 0;
+  switch (steps) {
+#define KQ_SMALL_CASE(N) \
+    case N: moe_small_kernel<GATEUP, NBP, S, RW, P, N><<<grid, S * RW * 64, 0, st>>>(args...); break;
+    KQ_SMALL_CASE(2) KQ_SMALL_CASE(4) KQ_SMALL_CASE(7) KQ_SMALL_CASE(8) KQ_SMALL_CASE(14)
+    KQ_SMALL_CASE(16) KQ_SMALL_CASE(28)
 #undef KQ_SMALL_CASE
     default:
-      if (steps8 > 0)
-        moe_small_kernel<GATEUP, CH, 8, 0><<<grid, 512, 0, st>>>(args...);
-      else
-        moe_small_kernel<GATEUP, CH, 4, 0><<<grid, 256, 0, st>>>(args...);
+      moe_small_kernel<GATEUP, NBP, S, RW, P, 0><<<grid, S * RW * 64, 0, st>>>(args...);
   }
   return hipGetLastError();
 }
@@ -961,9 +986,9 @@ extern "C" int kq_moe_forward(int activation, float act_beta, float act_linear_b
   const uint16_t* xb = (const uint16_t*)x;
   // gate/up
   {
-    const dim3 grid((unsigned)L.max_small, (unsigned)(inter / 32));
-    e = launch_small<true, 32>(grid, hidden, st, xb, ldx, topk, offsets, sorted, small_list, w13_t,
-                               w13_st, 2 * inter, hidden, inter, ap, route_weights, act, y, hidden);
+    e = launch_small<true, KQ_GU_NBP, KQ_GU_S, KQ_GU_RW, KQ_GU_P>(
+        L.max_small, inter, hidden, st, xb, ldx, topk, offsets, sorted, small_list, w13_t, w13_st,
+        2 * inter, hidden, inter, ap, route_weights, act, y, hidden);
     if (e != hipSuccess) return kq_check_launch(e, "kq_moe_forward/gateup_small");
   }
   const size_t lds = 2 * (size_t)STAGE + BM * sizeof(int);
@@ -999,10 +1024,9 @@ extern "C" int kq_moe_forward(int activation, float act_beta, float act_linear_b
   }
   // down
   {
-    const dim3 grid((unsigned)L.max_small, (unsigned)(hidden / 64));
-    e = launch_small<false, 64>(grid, inter, st, (const uint16_t*)act, inter, topk, offsets, sorted,
-                                small_list, w2_t, w2_st, hidden, inter, inter, ap, route_weights, act,
-                                y, hidden);
+    e = launch_small<false, KQ_DN_NBP, KQ_DN_S, KQ_DN_RW, KQ_DN_P>(
+        L.max_small, hidden, inter, st, (const uint16_t*)act, inter, topk, offsets, sorted, small_list,
+        w2_t, w2_st, hidden, inter, inter, ap, route_weights, act, y, hidden);
     if (e != hipSuccess) return kq_check_launch(e, "kq_moe_forward/down_small");
   }
   if (any_large && dma_path) {
