@@ -29,6 +29,7 @@ namespace kq {
 namespace moe {
 
 constexpr int SMALL_MAX = 16;        // pairs per expert handled by the GEMV path
+constexpr int DECODE_MAX_PAIRS = 256;  // at most this many pairs: decode routing, all GEMV
 constexpr int PREP = 256;            // pairs per prep block
 constexpr int MAX_EXPERTS = 4096;
 constexpr int BM = 256, BN = 256, BK = 64, THREADS = 512;  // large tiles
@@ -41,7 +42,7 @@ constexpr int STAGE = A_BYTES + B_BYTES + S_BYTES;
 
 struct Layout {
   size_t counts, offsets, block_counts, sorted, small_list, large_tiles, meta, act, y, total;
-  int64_t pairs, nblk, max_small, max_large;
+  int64_t pairs, nblk, max_small, max_large, max_list;
 };
 
 static inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -52,12 +53,16 @@ static Layout make_layout(int64_t tokens, int topk, int experts, int64_t hidden,
   L.nblk = (L.pairs + PREP - 1) / PREP;
   L.max_small = L.pairs < experts ? L.pairs : experts;
   L.max_large = L.pairs / (SMALL_MAX + 1) + L.pairs / BM + 1;
+  // GEMV list entries: one per small expert, or (decode) one per 16 pairs of
+  // every routed expert, at most experts + pairs / 16
+  L.max_list = L.pairs <= DECODE_MAX_PAIRS ? L.max_small + L.pairs / SMALL_MAX + 1 : L.max_small;
+  const int64_t list_cap = L.max_list > experts ? L.max_list : experts;
   size_t o = 0;
   L.counts = o;       o = align256(o + sizeof(int) * experts);
   L.offsets = o;      o = align256(o + sizeof(int) * (experts + 1));
   L.block_counts = o; o = align256(o + sizeof(int) * (size_t)L.nblk * experts);
   L.sorted = o;       o = align256(o + sizeof(int) * (size_t)L.pairs);
-  L.small_list = o;   o = align256(o + sizeof(int) * experts);
+  L.small_list = o;   o = align256(o + sizeof(int) * 3 * (size_t)list_cap);
   L.large_tiles = o;  o = align256(o + sizeof(int) * 2 * (size_t)L.max_large);
   L.meta = o;         o = align256(o + sizeof(int) * 4);
   L.act = o;          o = align256(o + 2 * (size_t)L.pairs * inter);
@@ -150,7 +155,11 @@ __global__ __launch_bounds__(1024) void route_scan_kernel(
   for (int e = threadIdx.x; e < experts; e += 1024) {
     offsets[e] = s_cnt[e];
     const int n = counts[e];
-    if (n >= 1 && n <= SMALL_MAX) small_list[s_small[e]] = e;
+    if (n >= 1 && n <= SMALL_MAX) {
+      small_list[3 * s_small[e]] = e;
+      small_list[3 * s_small[e] + 1] = s_cnt[e];
+      small_list[3 * s_small[e] + 2] = n;
+    }
     if (n > SMALL_MAX) {
       const int nt = (n + BM - 1) / BM;
       for (int t = 0; t < nt; ++t) {
@@ -162,7 +171,7 @@ __global__ __launch_bounds__(1024) void route_scan_kernel(
       }
     }
   }
-  for (int i = nsmall + (int)threadIdx.x; i < experts; i += 1024) small_list[i] = -1;
+  for (int i = nsmall + (int)threadIdx.x; i < experts; i += 1024) small_list[3 * i] = -1;
   if (threadIdx.x == 0) {
     offsets[experts] = npairs;
     meta[0] = nsmall;
@@ -223,7 +232,11 @@ __global__ __launch_bounds__(1024) void route_prep_one_kernel(
   for (int e = t; e < experts; e += 1024) {
     offsets[e] = s_cnt[e];
     const int c = counts[e];
-    if (c >= 1 && c <= SMALL_MAX) small_list[s_small[e]] = e;
+    if (c >= 1 && c <= SMALL_MAX) {
+      small_list[3 * s_small[e]] = e;
+      small_list[3 * s_small[e] + 1] = s_cnt[e];
+      small_list[3 * s_small[e] + 2] = c;
+    }
     if (c > SMALL_MAX) {
       const int nt = (c + BM - 1) / BM;
       for (int k = 0; k < nt; ++k) {
@@ -240,12 +253,60 @@ __global__ __launch_bounds__(1024) void route_prep_one_kernel(
     for (int j = 0; j < t; ++j) rank += s_ids[j] == my ? 1 : 0;
     sorted[s_cnt[my] + rank] = t;
   }
-  for (int i = nsmall + t; i < experts; i += 1024) small_list[i] = -1;
+  for (int i = nsmall + t; i < experts; i += 1024) small_list[3 * i] = -1;
   if (t == 0) {
     offsets[experts] = npairs;
     meta[0] = nsmall;
     meta[1] = ntiles < max_large ? ntiles : max_large;
     meta[2] = npairs;
+  }
+}
+
+// Routing for a few pairs (decode): one workgroup, one pair per thread, no
+// per-expert work.  The pairs are sorted stably by expert, and every routed
+// expert, whatever its count, is listed in ascending expert order as entries
+// (expert, first sorted position, count <= 16), one per 16 of its pairs.
+__global__ __launch_bounds__(DECODE_MAX_PAIRS) void route_decode_kernel(
+    const int* __restrict__ ids, int pairs, int experts, int* __restrict__ sorted,
+    int* __restrict__ small_list, int max_list, int* __restrict__ meta) {
+  __shared__ int s_id[DECODE_MAX_PAIRS];
+  __shared__ int s_first[DECODE_MAX_PAIRS];  // expert at its first pair, else -1
+  __shared__ int s_nent[DECODE_MAX_PAIRS];   // list entries of that expert
+  const int t = threadIdx.x;
+  int my = t < pairs ? ids[t] : -1;
+  if (my < 0 || my >= experts) my = -1;
+  s_id[t] = my;
+  __syncthreads();
+  int rank = 0, below = 0, cnt = 0;
+  for (int j = 0; j < pairs; ++j) {
+    const int v = s_id[j];
+    rank += (j < t && v == my) ? 1 : 0;
+    below += (v >= 0 && v < my) ? 1 : 0;
+    cnt += v == my ? 1 : 0;
+  }
+  const bool first = my >= 0 && rank == 0;
+  const int nent = (cnt + SMALL_MAX - 1) / SMALL_MAX;
+  s_first[t] = first ? my : -1;
+  s_nent[t] = first ? nent : 0;
+  __syncthreads();
+  int e0 = 0, nlist = 0;
+  for (int j = 0; j < pairs; ++j) {
+    const int v = s_first[j], ne = s_nent[j];
+    nlist += ne;
+    e0 += (v >= 0 && v < my) ? ne : 0;
+  }
+  if (my >= 0) sorted[below + rank] = t;
+  if (first) {
+    for (int q = 0; q < nent; ++q) {
+      small_list[3 * (e0 + q)] = my;
+      small_list[3 * (e0 + q) + 1] = below + SMALL_MAX * q;
+      small_list[3 * (e0 + q) + 2] = cnt - SMALL_MAX * q < SMALL_MAX ? cnt - SMALL_MAX * q : SMALL_MAX;
+    }
+  }
+  for (int i = nlist + t; i < max_list; i += DECODE_MAX_PAIRS) small_list[3 * i] = -1;
+  if (t == 0) {
+    meta[0] = nlist;
+    meta[1] = 0;
   }
 }
 
@@ -255,7 +316,8 @@ using gemm::u32x4_t;
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 // ------------------------------------------------- GEMV-shaped small path --
-// One workgroup: one expert with n <= 16 pairs.  Its S * RW waves form RW row
+// One workgroup: up to 16 pairs of one expert (a list entry (expert, first
+// sorted position, count)).  Its S * RW waves form RW row
 // groups of S waves; the S waves of a group split K, and each holds NBP
 // 16-row blocks per projection (GATEUP: gate rows c and up rows I + c), so a
 // workgroup covers CH = RW * 16 * NBP output channels.  Weights stream from
@@ -275,8 +337,7 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 // !GATEUP: rows of w2, output route_weight * partial -> fp32 pair rows.
 template <bool GATEUP, int NBP, int S, int RW, int P, int STEPS>
 __global__ __launch_bounds__(S * RW * 64) void moe_small_kernel(
-    const uint16_t* __restrict__ a, int64_t lda, int topk,
-    const int* __restrict__ offsets, const int* __restrict__ sorted,
+    const uint16_t* __restrict__ a, int64_t lda, int topk, const int* __restrict__ sorted,
     const int* __restrict__ small_list, const uint8_t* __restrict__ wt,
     const uint8_t* __restrict__ wst, int64_t rows_per_expert, int64_t K, int64_t inter,
     ActParams act, const float* __restrict__ route_w, uint16_t* __restrict__ act_out,
@@ -284,8 +345,10 @@ __global__ __launch_bounds__(S * RW * 64) void moe_small_kernel(
   constexpr int NB = GATEUP ? 2 * NBP : NBP;      // 16-row blocks per wave
   constexpr int CH = RW * 16 * NBP;               // channels per workgroup
   constexpr int NBUF = P + 1;
-  const int e = small_list[blockIdx.x];           // -1 past the last small expert
+  const int e = small_list[3 * blockIdx.x];       // -1 past the last entry
   if (e < 0) return;
+  const int beg = small_list[3 * blockIdx.x + 1];
+  const int n = small_list[3 * blockIdx.x + 2];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int kpart = wave % S, rgw = wave / S;
   const int m = lane & 15, g = lane >> 4;
@@ -328,8 +391,6 @@ __global__ __launch_bounds__(S * RW * 64) void moe_small_kernel(
   }
   __builtin_amdgcn_sched_barrier(0);
 
-  const int beg = offsets[e];
-  const int n = offsets[e + 1] - beg;
   // A row of this lane's token slot.  Slots past n re-read slot 0 (always
   // valid, n >= 1): MFMA output row m depends only on A row m and rows >= n
   // are never stored, so the duplicate needs no masking, and the loads stay
@@ -429,6 +490,7 @@ __global__ __launch_bounds__(S * RW * 64) void moe_small_kernel(
       store(u, x0, x1);
     }
   }
+
 }
 
 // ------------------------------------------------ grouped GEMM large path --
@@ -967,8 +1029,15 @@ extern "C" int kq_moe_forward(int activation, float act_beta, float act_linear_b
   float* y = (float*)(w + L.y);
   const ActParams ap{activation, act_beta, act_linear_beta};
   hipError_t e;
+  // Decode: few pairs.  Every routed expert takes the GEMV path (in entries
+  // of up to 16 pairs) and the grouped GEMM is not launched.
+  const bool decode = L.pairs <= DECODE_MAX_PAIRS;
 
-  if (L.pairs <= PREP_ONE) {
+  if (decode) {
+    route_decode_kernel<<<1, DECODE_MAX_PAIRS, 0, st>>>(route_ids, (int)L.pairs, experts, sorted,
+                                                         small_list, (int)L.max_list, meta);
+    if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_moe_forward/route");
+  } else if (L.pairs <= PREP_ONE) {
     route_prep_one_kernel<<<1, 1024, 0, st>>>(route_ids, (int)L.pairs, experts, counts, offsets,
                                                sorted, small_list, large_tiles, meta, (int)L.max_large);
     if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_moe_forward/prep");
@@ -987,12 +1056,12 @@ extern "C" int kq_moe_forward(int activation, float act_beta, float act_linear_b
   // gate/up
   {
     e = launch_small<true, KQ_GU_NBP, KQ_GU_S, KQ_GU_RW, KQ_GU_P>(
-        L.max_small, inter, hidden, st, xb, ldx, topk, offsets, sorted, small_list, w13_t, w13_st,
-        2 * inter, hidden, inter, ap, route_weights, act, y, hidden);
+        L.max_list, inter, hidden, st, xb, ldx, topk, (const int*)sorted, (const int*)small_list,
+        w13_t, w13_st, 2 * inter, hidden, inter, ap, route_weights, act, y, hidden);
     if (e != hipSuccess) return kq_check_launch(e, "kq_moe_forward/gateup_small");
   }
   const size_t lds = 2 * (size_t)STAGE + BM * sizeof(int);
-  const bool any_large = L.pairs > SMALL_MAX;
+  const bool any_large = !decode && L.pairs > SMALL_MAX;
   // direct-to-LDS path unless a buffer exceeds one 32-bit buffer range
   const uint64_t x_bytes = (uint64_t)tokens * ldx * 2, act_bytes = (uint64_t)L.pairs * inter * 2;
   const bool dma_path = !(flags & KQ_MOE_REGISTER_STAGED) && x_bytes <= dma::MAX_RANGE &&
@@ -1025,8 +1094,8 @@ extern "C" int kq_moe_forward(int activation, float act_beta, float act_linear_b
   // down
   {
     e = launch_small<false, KQ_DN_NBP, KQ_DN_S, KQ_DN_RW, KQ_DN_P>(
-        L.max_small, hidden, inter, st, (const uint16_t*)act, inter, topk, offsets, sorted, small_list,
-        w2_t, w2_st, hidden, inter, inter, ap, route_weights, act, y, hidden);
+        L.max_list, hidden, inter, st, (const uint16_t*)act, inter, topk, (const int*)sorted,
+        (const int*)small_list, w2_t, w2_st, hidden, inter, inter, ap, route_weights, act, y, hidden);
     if (e != hipSuccess) return kq_check_launch(e, "kq_moe_forward/down_small");
   }
   if (any_large && dma_path) {
@@ -1060,7 +1129,7 @@ static size_t route_sort_layout(int64_t pairs, int experts, size_t* parts) {
   parts[1] = o; o = align256(o + sizeof(int) * (experts + 1));           // offsets32
   parts[2] = o; o = align256(o + sizeof(int) * (size_t)nblk * experts);  // block counts
   parts[3] = o; o = align256(o + sizeof(int) * (size_t)pairs);           // sorted pairs
-  parts[4] = o; o = align256(o + sizeof(int) * experts);                 // small list
+  parts[4] = o; o = align256(o + sizeof(int) * 3 * experts);             // small list
   parts[5] = o; o = align256(o + sizeof(int) * 2 * (size_t)max_large);   // large tiles
   parts[6] = o; o = align256(o + sizeof(int) * 4);                       // meta
   return o;

@@ -48,11 +48,15 @@ def _max_rel(ref, got):
 
 
 @pytest.mark.parametrize("act", ["situ", "swiglu"])
-def test_small_config_both_paths(gpu, act):
-    T, k, E, H, I = 40, 4, 8, 512, 1024
+@pytest.mark.parametrize("T", [40, 80])
+def test_small_config_both_paths(gpu, act, T):
+    """T=40 (160 pairs): decode routing, every expert on the GEMV kernel, the
+    experts with more than 16 pairs split into entries of at most 16.  T=80
+    (320 pairs): every expert has 29..80 pairs, all on the grouped GEMM."""
+    k, E, H, I = 4, 8, 512, 1024
     g = torch.Generator().manual_seed(1)
     x = torch.randn(T, H, generator=g).to(torch.bfloat16)
-    # expert 0 gets every token (40 pairs: grouped GEMM path), the rest <= 16
+    # expert 0 gets every token, the others <= 16 pairs each
     ids = torch.stack([torch.cat([torch.tensor([0]), 1 + torch.randperm(E - 1, generator=g)[: k - 1]])
                        for _ in range(T)]).to(torch.int32)
     w = torch.softmax(torch.randn(T, k, generator=g), -1)
@@ -78,6 +82,17 @@ def test_invalid_ids_contribute_nothing(gpu):
     valid = (ids >= 0) & (ids < E)
     ref = _oracle(x, torch.where(valid, ids, torch.zeros_like(ids)), w * valid, weights, "situ")
     assert _max_rel(ref, out.cpu().numpy()) <= TOL
+
+
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
+def test_no_valid_pair_gives_zeros(gpu, out_dtype):
+    T, k, E, H, I = 5, 2, 4, 512, 512
+    ids = torch.tensor([[-1, 4], [7, -2], [4, 4], [-1, -1], [100, 5]], dtype=torch.int32)
+    w = torch.rand(T, k)
+    weights = workloads.quantized_experts(range(E), E, H, I, seed=4, device=gpu)
+    x = torch.randn(T, H).to(torch.bfloat16)
+    out = moe.grouped_expert_forward(x.to(gpu), ids.to(gpu), w.to(gpu), *weights, out_dtype=out_dtype)
+    assert out.dtype == out_dtype and torch.count_nonzero(out) == 0
 
 
 @pytest.mark.parametrize("tokens", [1, 4, 16])
