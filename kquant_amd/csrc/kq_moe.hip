@@ -269,20 +269,29 @@ __global__ __launch_bounds__(1024) void route_prep_one_kernel(
 __global__ __launch_bounds__(DECODE_MAX_PAIRS) void route_decode_kernel(
     const int* __restrict__ ids, int pairs, int experts, int* __restrict__ sorted,
     int* __restrict__ small_list, int max_list, int* __restrict__ meta) {
-  __shared__ int s_id[DECODE_MAX_PAIRS];
-  __shared__ int s_first[DECODE_MAX_PAIRS];  // expert at its first pair, else -1
-  __shared__ int s_nent[DECODE_MAX_PAIRS];   // list entries of that expert
+  // ids past `pairs` are -1 and the loops run over whole groups of four
+  // (one 16-byte LDS read each), so no read waits on the previous one
+  __shared__ __attribute__((aligned(16))) int s_id[DECODE_MAX_PAIRS];
+  __shared__ __attribute__((aligned(16))) int s_first[DECODE_MAX_PAIRS];  // expert at its first pair, else -1
+  __shared__ __attribute__((aligned(16))) int s_nent[DECODE_MAX_PAIRS];   // list entries of that expert
+  typedef int i32x4 __attribute__((ext_vector_type(4)));
   const int t = threadIdx.x;
+  const int pairs4 = (pairs + 3) & ~3;
   int my = t < pairs ? ids[t] : -1;
   if (my < 0 || my >= experts) my = -1;
   s_id[t] = my;
   __syncthreads();
   int rank = 0, below = 0, cnt = 0;
-  for (int j = 0; j < pairs; ++j) {
-    const int v = s_id[j];
-    rank += (j < t && v == my) ? 1 : 0;
-    below += (v >= 0 && v < my) ? 1 : 0;
-    cnt += v == my ? 1 : 0;
+#pragma unroll 4
+  for (int j4 = 0; j4 < pairs4; j4 += 4) {
+    const i32x4 v4 = *reinterpret_cast<const i32x4*>(s_id + j4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int v = v4[i];
+      rank += (j4 + i < t && v == my) ? 1 : 0;
+      below += (v >= 0 && v < my) ? 1 : 0;
+      cnt += v == my ? 1 : 0;
+    }
   }
   const bool first = my >= 0 && rank == 0;
   const int nent = (cnt + SMALL_MAX - 1) / SMALL_MAX;
@@ -290,10 +299,15 @@ __global__ __launch_bounds__(DECODE_MAX_PAIRS) void route_decode_kernel(
   s_nent[t] = first ? nent : 0;
   __syncthreads();
   int e0 = 0, nlist = 0;
-  for (int j = 0; j < pairs; ++j) {
-    const int v = s_first[j], ne = s_nent[j];
-    nlist += ne;
-    e0 += (v >= 0 && v < my) ? ne : 0;
+#pragma unroll 4
+  for (int j4 = 0; j4 < pairs4; j4 += 4) {
+    const i32x4 v4 = *reinterpret_cast<const i32x4*>(s_first + j4);
+    const i32x4 n4 = *reinterpret_cast<const i32x4*>(s_nent + j4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      nlist += n4[i];
+      e0 += (v4[i] >= 0 && v4[i] < my) ? n4[i] : 0;
+    }
   }
   if (my >= 0) sorted[below + rank] = t;
   if (first) {
