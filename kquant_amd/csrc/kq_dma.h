@@ -45,6 +45,14 @@ __device__ __forceinline__ void load_to_lds16(i32x4_t rsrc, uint32_t voffset, ui
                : "memory", "m0");
 }
 
+// 4 bytes per lane from rsrc + voffset (4-byte aligned) into LDS at m0 + 4 * lane.
+__device__ __forceinline__ void load_to_lds4(i32x4_t rsrc, uint32_t voffset, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds"
+               :
+               : "s"(lds_addr), "v"(voffset), "s"(rsrc)
+               : "memory", "m0");
+}
+
 // LDS byte address of a __shared__ object.
 __device__ __forceinline__ uint32_t lds_offset_of(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) unsigned char*)p;

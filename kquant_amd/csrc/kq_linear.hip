@@ -9,6 +9,7 @@
 // Workgroup tile 256 x 256, 8 waves of 64 x 128 (2 x 4 MFMA 32x32 blocks),
 // K step 64, LDS double buffered.  Weights are staged in LDS still packed
 // (E4M3: 64 B per row and step, E2M1: 32 B) and expanded to bf16 per fragment.
+#include "kq_dma.h"
 #include "kq_gemm.h"
 #include "kq_internal.h"
 
@@ -167,6 +168,207 @@ __global__ __launch_bounds__(512, 1) void mx_linear_kernel(
       }
 }
 
+// ------------------------------------------------ direct-to-LDS variant --
+// Same tile (256 x 256, 8 waves of 64 x 128, K step 64) and result as
+// mx_linear_kernel, with every operand moved HBM -> LDS by
+// buffer_load ... lds through a ring of three stages issued two steps ahead,
+// continuing across tile boundaries: the kernel is persistent (one workgroup
+// per CU, tiles t = worker, worker + G, ... with N fastest, workers of one XCD
+// numbered consecutively so they share A rows in its L2).
+//  * k order: in a 64-k step, lane half f of MFMA q (0..3) takes
+//    k = 32 f + 8 q + [0, 8) on both operands, so a lane's weights for the
+//    step are one 16-byte chunk (E2M1) or two (E4M3) of its row, read with
+//    128-bit LDS reads, under the one scale byte of block f.
+//  * A rows: 128 B per stage, 16-byte chunk c of row r at slot c ^ ((r/2)%8).
+//    Weight rows: 32 B (E2M1) / 64 B (E4M3) per stage, chunk c of row r at
+//    slot c ^ ((r/8)%2) / c ^ ((r/4)%4).  Either way the 16 lanes of a read
+//    hit 16 distinct bank groups.
+//  * scales: one aligned dword per weight row per stage (four blocks, two of
+//    them this step's) by 4-byte direct loads; needs KB % 128 == 0.
+//  * rows past M or N read as zero (out-of-range offsets) and are not stored.
+namespace lin3 {
+constexpr int NSTAGE = 3;
+constexpr int A_BYTES = lin::BM * lin::BK * 2;                      // 32 KiB
+template <int FMT> constexpr int w_row() { return FMT == 0 ? 64 : 32; }  // bytes per row per stage
+template <int FMT> constexpr int b_bytes() { return lin::BN * w_row<FMT>(); }
+constexpr int S_BYTES = lin::BN * 4;
+template <int FMT> constexpr int stage() { return A_BYTES + b_bytes<FMT>() + S_BYTES; }
+template <int FMT> constexpr int loads() { return 4 + (FMT == 0 ? 2 : 1) + 1; }  // per wave per stage
+}  // namespace lin3
+
+__shared__ __attribute__((aligned(16))) unsigned char lin3_lds[lin3::NSTAGE * lin3::stage<0>()];
+
+template <int FMT, int OUT>
+__global__ __launch_bounds__(512, 1) void mx_linear_dma_kernel(
+    const uint16_t* __restrict__ a, int64_t lda, uint32_t a_bytes, const uint8_t* __restrict__ wq,
+    const uint8_t* __restrict__ ws, uint32_t w_bytes, uint32_t s_bytes, void* __restrict__ c,
+    int64_t ldc, int M, int N, int K, int KB) {
+  using namespace lin3;
+  using dma::i32x4_t;
+  constexpr int WROW = w_row<FMT>(), STAGE = stage<FMT>(), LOADS = loads<FMT>();
+  constexpr int BM = lin::BM, BN = lin::BN, BK = lin::BK;
+  const int mtiles = (M + BM - 1) / BM, ntiles = (N + BN - 1) / BN, total = mtiles * ntiles;
+  const int G = gridDim.x;
+  const int worker = (int)(blockIdx.x % 8) * (G / 8) + (int)(blockIdx.x / 8);
+  if (worker >= total) return;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t kw = FMT == 0 ? KB : KB / 2;  // packed bytes per weight row
+  const int64_t ks = KB / 32;                 // scale bytes per weight row
+  const int steps = K / BK;
+  const uint32_t lds0 = dma::lds_offset_of(lin3_lds);
+  const i32x4_t a_rsrc = dma::make_rsrc(a, a_bytes);
+  const i32x4_t w_rsrc = dma::make_rsrc(wq, w_bytes);
+  const i32x4_t s_rsrc = dma::make_rsrc(ws, s_bytes);
+
+  // ---- load side (tile lt, step ls); per-lane row offsets, invalid -> past the range
+  int lt = worker, ls = 0;
+  uint32_t a_off[4], w_off[2], s_off;
+  auto set_load_tile = [&]() {
+    const bool live = lt < total;
+    const int mt = live ? lt / ntiles : 0, nt = live ? lt - mt * ntiles : 0;
+    const int m0 = mt * BM, n0 = nt * BN;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int row = 8 * (8 * q + wave) + (lane >> 3);
+      const int ch = (lane & 7) ^ ((row >> 1) & 7);
+      a_off[q] = live && m0 + row < M ? (uint32_t)((int64_t)(m0 + row) * lda * 2 + ch * 16) : a_bytes;
+    }
+#pragma unroll
+    for (int q = 0; q < (FMT == 0 ? 2 : 1); ++q) {
+      // E4M3: 16 rows x 4 chunks per instruction; E2M1: 32 rows x 2 chunks
+      const int row = FMT == 0 ? 16 * (8 * q + wave) + (lane >> 2) : 32 * wave + (lane >> 1);
+      const int ch = FMT == 0 ? (lane & 3) ^ ((row >> 2) & 3) : (lane & 1) ^ ((row >> 3) & 1);
+      w_off[q] = live && n0 + row < N ? (uint32_t)((int64_t)(n0 + row) * kw + ch * 16) : w_bytes;
+    }
+    {
+      const int row = 32 * wave + (lane & 31);
+      s_off = live && n0 + row < N ? (uint32_t)((int64_t)(n0 + row) * ks) : s_bytes;
+    }
+  };
+  auto issue = [&](int slot) {
+    const uint32_t base = lds0 + (uint32_t)(slot * STAGE);
+    const int k0 = ls * BK, kb0 = k0 % KB;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      dma::load_to_lds16(a_rsrc, a_off[q] >= a_bytes ? a_bytes : a_off[q] + 2 * (uint32_t)k0,
+                         base + (uint32_t)((8 * q + wave) * 1024));
+    const uint32_t wk = FMT == 0 ? (uint32_t)kb0 : (uint32_t)kb0 / 2;
+#pragma unroll
+    for (int q = 0; q < (FMT == 0 ? 2 : 1); ++q)
+      dma::load_to_lds16(w_rsrc, w_off[q] >= w_bytes ? w_bytes : w_off[q] + wk,
+                         base + (uint32_t)(A_BYTES + (8 * q + wave) * 1024));
+    if (lane < 32)
+      dma::load_to_lds4(s_rsrc, s_off >= s_bytes ? s_bytes : s_off + (uint32_t)((kb0 / 32) & ~3),
+                        base + (uint32_t)(A_BYTES + b_bytes<FMT>() + wave * 128));
+  };
+  auto advance = [&]() {
+    if (++ls == steps) {
+      ls = 0;
+      lt += G;
+      set_load_tile();
+    }
+  };
+
+  // ---- compute side: per-lane LDS offsets
+  const int wm = (wave >> 1) * 64, wn = (wave & 1) * 128;
+  const int frow = lane & 31, f = lane >> 5;
+  int arow[2], axor[2], woff[4][FMT == 0 ? 2 : 1], soff[4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int row = wm + i * 32 + frow;
+    arow[i] = row * (BK * 2);
+    axor[i] = (4 * f) ^ ((row >> 1) & 7);
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int row = wn + j * 32 + frow;
+    if (FMT == 0) {
+      woff[j][0] = A_BYTES + row * WROW + 16 * ((2 * f) ^ ((row >> 2) & 3));
+      woff[j][FMT == 0 ? 1 : 0] = A_BYTES + row * WROW + 16 * ((2 * f + 1) ^ ((row >> 2) & 3));
+    } else {
+      woff[j][0] = A_BYTES + row * WROW + 16 * (f ^ ((row >> 3) & 1));
+    }
+    soff[j] = A_BYTES + b_bytes<FMT>() + row * 4 + f;
+  }
+
+  set_load_tile();
+  issue(0);
+  advance();
+  issue(1);
+  advance();
+  int cslot = 0;
+  for (int t = worker; t < total; t += G) {
+    const int mt = t / ntiles, nt = t - mt * ntiles;
+    const int m0 = mt * BM, n0 = nt * BN;
+    const bool active = m0 + wm < M && n0 + wn < N;
+    float16_t acc[2][4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    for (int s = 0; s < steps; ++s) {
+      const int kb0 = (s * BK) % KB;
+      dma::wait_and_barrier<LOADS>();
+      issue(cslot == 0 ? 2 : cslot - 1);
+      advance();
+      if (active) {
+        const unsigned char* st = lin3_lds + cslot * STAGE;
+        const int sbyte = (kb0 / 32) & 3;  // 0 or 2: this step's blocks in the scale dword
+        u32x4_t wv[4][FMT == 0 ? 2 : 1];
+        uint32_t sc[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+#pragma unroll
+          for (int h = 0; h < (FMT == 0 ? 2 : 1); ++h)
+            wv[j][h] = *reinterpret_cast<const u32x4_t*>(st + woff[j][h]);
+          sc[j] = st[soff[j] + sbyte];
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          bf16x8_t fa[2], fb[4];
+#pragma unroll
+          for (int i = 0; i < 2; ++i)
+            fa[i] = *reinterpret_cast<const bf16x8_t*>(st + arow[i] + 16 * (q ^ axor[i]));
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            u32x2_t w;
+            if (FMT == 0) w = u32x2_t{wv[j][q >> 1][2 * (q & 1)], wv[j][q >> 1][2 * (q & 1) + 1]};
+            else w = u32x2_t{wv[j][0][q], 0u};
+            fb[j] = gemm::dequant8<FMT>(w, sc[j]);
+          }
+#pragma unroll
+          for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+        }
+      }
+      cslot = cslot == 2 ? 0 : cslot + 1;
+    }
+
+    if (active) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int gm = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * f + (r & 3);
+            const int gn = n0 + wn + j * 32 + frow;
+            if (gm < M && gn < N) {
+              if (OUT == 2) static_cast<float*>(c)[(int64_t)gm * ldc + gn] = acc[i][j][r];
+              else static_cast<__bf16*>(c)[(int64_t)gm * ldc + gn] = (__bf16)acc[i][j][r];
+            }
+          }
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(dma::waitcnt_vm(0));  // no load may land after the workgroup ends
+}
+
 // Exact three-term bf16 split of fp32 A: a = a0 + a1 + a2 (each step keeps
 // the next 8 significant bits and leaves an exactly representable residual),
 // written as row [a0 | a1 | a2] of a [rows, 3k] bf16 matrix.  Four columns
@@ -205,9 +407,44 @@ __global__ __launch_bounds__(256) void split3_bf16_kernel(const float* __restric
 
 using namespace kq;
 
+// Direct-to-LDS path: needs 4-byte aligned scale rows (KB % 128 == 0, scale
+// pointer 4-byte aligned); operands larger than one 32-bit buffer range are
+// cut into row chunks of M and N.
+template <int FMT, int OUT>
+static hipError_t launch_linear_dma(const uint16_t* a, int64_t lda, const uint8_t* wq,
+                                    const uint8_t* ws, void* c, int64_t ldc, int M, int N, int K,
+                                    int KB, hipStream_t st) {
+  int dev = 0, cus = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e != hipSuccess) return e;
+  const int64_t kw = FMT == 0 ? KB : KB / 2, ks = KB / 32;
+  const int64_t m_chunk = (int64_t)(dma::MAX_RANGE / (uint64_t)(lda * 2)) / lin::BM * lin::BM;
+  const int64_t n_chunk = (int64_t)(dma::MAX_RANGE / (uint64_t)kw) / lin::BN * lin::BN;
+  for (int64_t m0 = 0; m0 < M; m0 += m_chunk) {
+    const int mc = (int)(M - m0 < m_chunk ? M - m0 : m_chunk);
+    for (int64_t n0 = 0; n0 < N; n0 += n_chunk) {
+      const int nc = (int)(N - n0 < n_chunk ? N - n0 : n_chunk);
+      const int tiles = ((mc + lin::BM - 1) / lin::BM) * ((nc + lin::BN - 1) / lin::BN);
+      int grid = cus / 8 * 8 > 0 ? cus / 8 * 8 : 8;
+      if (grid > (tiles + 7) / 8 * 8) grid = (tiles + 7) / 8 * 8;
+      void* cp = OUT == 2 ? (void*)(static_cast<float*>(c) + m0 * ldc + n0)
+                          : (void*)(static_cast<uint16_t*>(c) + m0 * ldc + n0);
+      mx_linear_dma_kernel<FMT, OUT><<<grid, lin::THREADS, 0, st>>>(
+          a + m0 * lda, lda, (uint32_t)(mc * lda * 2), wq + n0 * kw, ws + n0 * ks,
+          (uint32_t)(nc * kw), (uint32_t)(nc * ks), cp, ldc, mc, nc, K, KB);
+      if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+  }
+  return hipSuccess;
+}
+
 template <int FMT, int OUT>
 static hipError_t launch_linear(const uint16_t* a, int64_t lda, const uint8_t* wq, const uint8_t* ws,
                                 void* c, int64_t ldc, int M, int N, int K, int KB, hipStream_t st) {
+  if (KB % 128 == 0 && !kq_misaligned(ws, 4) && (uint64_t)lda * 2 * lin::BM <= dma::MAX_RANGE &&
+      (uint64_t)(FMT == 0 ? KB : KB / 2) * lin::BN <= dma::MAX_RANGE)
+    return launch_linear_dma<FMT, OUT>(a, lda, wq, ws, c, ldc, M, N, K, KB, st);
   const size_t lds = 2 * (size_t)lin::stage_bytes<FMT>();
   auto kern = mx_linear_kernel<FMT, OUT>;
   hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);

@@ -71,6 +71,39 @@ def test_linear_matches_fp32_oracle(gpu, fmt, m, n, k, out_dtype):
         check_bf16_output(ref, c)
 
 
+@pytest.mark.parametrize("fmt", ["mxfp8", "mxfp4"])
+def test_linear_many_tiles_per_workgroup(gpu, fmt):
+    """17 x 17 tiles of 256 (more than one per workgroup of the persistent
+    grid) with ragged last rows and columns."""
+    m, n, k = 4200, 4200, 256
+    g = torch.Generator().manual_seed(3)
+    w = (torch.randn(n, k, generator=g) * 0.02).to(torch.bfloat16).to(gpu)
+    x = torch.randn(m, k, generator=g).to(torch.bfloat16)
+    q, s, wd = _quantized(fmt, w)
+    fn = linear.mxfp8_linear if fmt == "mxfp8" else linear.mxfp4_linear
+    c = fn(x.to(gpu), q, s, out_dtype=torch.float32).cpu().numpy()
+    ref = x.float().numpy() @ wd.T.astype(np.float32)
+    assert _max_rel(ref.astype(np.float64), c) <= 1e-5
+
+
+@pytest.mark.parametrize("fmt", ["mxfp8", "mxfp4"])
+@pytest.mark.parametrize("k", [384, 192])
+def test_linear_fp32_source(gpu, fmt, k):
+    """fp32 activations: the exact three-term bf16 split (A has 3k columns,
+    column j multiplies weight column j % k); k = 384 takes the direct-to-LDS
+    kernel, k = 192 the register-staged one."""
+    m, n = 300, 520
+    g = torch.Generator().manual_seed(k)
+    w = (torch.randn(n, k, generator=g) * 0.02).to(torch.bfloat16).to(gpu)
+    x = torch.randn(m, k, generator=g) * torch.exp(torch.randn(k, generator=g))
+    q, s, wd = _quantized(fmt, w)
+    fn = linear.mxfp8_linear if fmt == "mxfp8" else linear.mxfp4_linear
+    c = fn(x.to(gpu), q, s).cpu().numpy()
+    assert c.dtype == np.float32
+    ref = x.double().numpy() @ wd.astype(np.float64).T
+    assert _max_rel(ref, c) <= 1e-5
+
+
 def test_cfg2_full_size(gpu):
     """X [4096, 7168] x MXFP8 W [12288, 7168] (benchmark configuration 2);
     the oracle is evaluated on 256 sampled rows of X."""
