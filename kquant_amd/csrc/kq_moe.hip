@@ -691,9 +691,11 @@ __global__ __launch_bounds__(512, 1) void moe_large_kernel(
 //    row r stored at slot c ^ ((r / 2) % 8), so the 16 lanes of an MFMA
 //    fragment read hit 16 distinct bank groups.  Rows past the expert's count
 //    read as zero without touching memory (out-of-range buffer offset).
-//  * k order: within each 32-element scale block, lane half f of MFMA kk takes
-//    k = 16 f + 8 kk + [0, 8) (the same for activations and weights), so one
-//    8-byte LDS read gives a lane the packed weights of both MFMAs of a block.
+//  * k order: in a 64-k step, lane half f of MFMA q (0..3) takes
+//    k = 32 f + 8 q + [0, 8) on both operands, so a lane's weights for the
+//    step are the one 16-byte tile unit (row, block f) -- one 128-bit LDS
+//    read, the 16 lanes of a row group reading 256 contiguous bytes -- under
+//    the one scale byte of block f.
 //  * waves whose 64 rows are all past the expert's count skip their MFMAs.
 namespace dma_gemm {
 constexpr int NSTAGE = 3;
@@ -807,13 +809,13 @@ __global__ __launch_bounds__(512, 1) void moe_large_dma_kernel(
   for (int i = 0; i < 2; ++i) {
     const int row = wm + i * 32 + frow;
     arow[i] = row * (BK * 2);
-    axor[i] = (2 * fk) ^ ((row >> 1) & 7);
+    axor[i] = (4 * fk) ^ ((row >> 1) & 7);
   }
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int r = GATEUP ? (j < 2 ? 0 : BN / 2) + wn + (j & 1) * 32 + frow : 2 * wn + j * 32 + frow;
-    boff[j] = DA_BYTES + (r >> 4) * 512 + (r & 15) * 16 + 8 * fk;
-    soff[j] = DA_BYTES + DB_BYTES + (r >> 4) * 32 + (r & 15);
+    boff[j] = DA_BYTES + (r >> 4) * 512 + (fk * 16 + (r & 15)) * 16;
+    soff[j] = DA_BYTES + DB_BYTES + (r >> 4) * 32 + fk * 16 + (r & 15);
   }
 
   set_load_tile();
@@ -845,29 +847,26 @@ __global__ __launch_bounds__(512, 1) void moe_large_dma_kernel(
       advance();
       if (active) {
         const unsigned char* st = moe_dma_lds + cslot * DSTAGE;
+        u32x4_t raw[4];
+        uint32_t sc[4];
 #pragma unroll
-        for (int jb = 0; jb < 2; ++jb) {
-          u32x2_t raw[4];
-          uint32_t sc[4];
+        for (int j = 0; j < 4; ++j) {
+          raw[j] = *reinterpret_cast<const u32x4_t*>(st + boff[j]);
+          sc[j] = st[soff[j]];
+        }
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            raw[j] = *reinterpret_cast<const u32x2_t*>(st + boff[j] + jb * 256);
-            sc[j] = st[soff[j] + jb * 16];
-          }
+        for (int q = 0; q < 4; ++q) {
+          bf16x8_t fa[2], fb[4];
 #pragma unroll
-          for (int kk = 0; kk < 2; ++kk) {
-            bf16x8_t fa[2], fb[4];
+          for (int i = 0; i < 2; ++i)
+            fa[i] = *reinterpret_cast<const bf16x8_t*>(st + arow[i] + 16 * (q ^ axor[i]));
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
-              fa[i] = *reinterpret_cast<const bf16x8_t*>(st + arow[i] + 16 * ((4 * jb + kk) ^ axor[i]));
+          for (int j = 0; j < 4; ++j) fb[j] = gemm::dequant8<1>(u32x2_t{raw[j][q], 0u}, sc[j]);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) fb[j] = gemm::dequant8<1>(u32x2_t{raw[j][kk], 0u}, sc[j]);
+          for (int i = 0; i < 2; ++i)
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-              for (int j = 0; j < 4; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
-          }
+            for (int j = 0; j < 4; ++j)
+              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
         }
       }
       cslot = cslot == 2 ? 0 : cslot + 1;
