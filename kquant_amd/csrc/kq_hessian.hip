@@ -54,9 +54,33 @@ __device__ __forceinline__ void split_bf16(float v, uint32_t& hi, uint32_t& lo) 
   lo = __builtin_bit_cast(uint16_t, (__bf16)r);
 }
 
+// Group of grid row r for the grouped kernels: groups in descending order of
+// their row count (ties by index), so the longest tiles start first and the
+// short ones fill in behind them (longest-processing-time-first order; the
+// result of each group does not depend on it).  Every thread ranks a few
+// groups against all others with uniform (scalar) reads of offsets; for more
+// than LPT_MAX_GROUPS groups the quadratic ranking costs more than it saves
+// and row r is group r.
+constexpr int LPT_MAX_GROUPS = 1024;
+__device__ __forceinline__ int64_t group_of_row(const int64_t* __restrict__ offsets, int groups, int r) {
+  if (groups > LPT_MAX_GROUPS) return r;
+  __shared__ int s_group;
+  for (int g = threadIdx.x; g < groups; g += blockDim.x) {
+    const int64_t ng = offsets[g + 1] - offsets[g];
+    int rank = 0;
+    for (int h = 0; h < groups; ++h) {
+      const int64_t nh = offsets[h + 1] - offsets[h];
+      rank += (nh > ng || (nh == ng && h < g)) ? 1 : 0;
+    }
+    if (rank == r) s_group = g;
+  }
+  __syncthreads();
+  return s_group;
+}
+
 // IN: 0 bf16, 1 f16, 2 f32.  SPLIT: operands carry a bf16 residual part
 // (needed for weights or non-bf16 inputs).  GROUPED: blockIdx.y is a group
-// (an expert) whose rows are list positions [offsets[g], offsets[g+1]), row
+// (an expert; grid row order from group_of_row) whose rows are list positions [offsets[g], offsets[g+1]), row
 // index[p] of x (or p itself without an index), weight w[p] (squared when
 // square_w), and whose k x k result sits at acc + g * acc_stride.
 template <int IN, bool SPLIT, bool WEIGHTED, bool GROUPED>
@@ -68,7 +92,7 @@ __global__ __launch_bounds__(256, 1) void syrk_upper_kernel(
   using namespace syrk;
   int64_t list0 = 0;
   if (GROUPED) {
-    const int64_t g = blockIdx.y;
+    const int64_t g = group_of_row(offsets, gridDim.y, blockIdx.y);
     list0 = offsets[g];
     n = offsets[g + 1] - list0;
     acc += g * acc_stride;
@@ -319,7 +343,7 @@ __global__ __launch_bounds__(512, 1) void syrk256_kernel(
 
   int64_t list0 = 0;
   if (GROUPED) {
-    const int64_t g = blockIdx.y;
+    const int64_t g = group_of_row(offsets, gridDim.y, blockIdx.y);
     list0 = offsets[g];
     n = offsets[g + 1] - list0;
     acc += g * acc_stride;
