@@ -62,6 +62,23 @@ def _time_loop(torch, fn, steps: int, warmup: int) -> float:
     return start.elapsed_time(stop) / 1e3 / steps
 
 
+def _bound(N, name: str, *args):
+    """A C entry point with its arguments converted once: for kernels of a few
+    microseconds, so the timed loop measures the GPU and not the per-call
+    Python argument conversion."""
+    import ctypes
+
+    fn = getattr(N.library(), name)
+    conv = tuple(ctypes.c_void_p(a) if a is None else a for a in args)
+
+    def run():
+        rc = fn(*conv)
+        if rc != 0:
+            raise RuntimeError(f"{name} failed ({rc}): {N.library().kq_last_error().decode()}")
+
+    return run
+
+
 def _traffic(name: str):
     path = ROOT / "profiles" / f"{name}_traffic.json"
     if path.exists():
@@ -125,9 +142,8 @@ def main() -> int:
     s8 = torch.empty(rows, cols // 32, dtype=torch.uint8, device=dev)
     quant_bytes = rows * cols * 2 + rows * cols + rows * cols // 32
 
-    def quantize_step():
-        N.call("kq_mx_quantize", N.FMT_MXFP8_E4M3, N.DT_BF16, N.ptr(w2), cols, rows, cols,
-               N.ptr(q8), N.ptr(s8), 0, stream)
+    quantize_step = _bound(N, "kq_mx_quantize", N.FMT_MXFP8_E4M3, N.DT_BF16, N.ptr(w2), cols, rows, cols,
+                           N.ptr(q8), N.ptr(s8), 0, stream)
 
     t_quant = _time_loop(torch, quantize_step, args.steps, args.warmup) if want("quantize") else float("nan")
     quant_gbs = quant_bytes / t_quant / 1e9
@@ -213,13 +229,10 @@ def main() -> int:
         d4 = torch.empty(7168, 2048, dtype=torch.bfloat16, device=dev)
         b1 = 7168 * 2048 * 2 + 7168 * 1024 + 7168 * 64
 
-        def q_step():
-            N.call("kq_mx_quantize", N.FMT_MXFP4_E2M1, N.DT_BF16, N.ptr(w1), 2048, 7168, 2048,
-                   N.ptr(q4), N.ptr(s4), 0, stream)
-
-        def d_step():
-            N.call("kq_mx_dequant", N.FMT_MXFP4_E2M1, N.ptr(q4), N.ptr(s4), 7168, 2048, N.DT_BF16,
-                   N.ptr(d4), 0, stream)
+        q_step = _bound(N, "kq_mx_quantize", N.FMT_MXFP4_E2M1, N.DT_BF16, N.ptr(w1), 2048, 7168, 2048,
+                        N.ptr(q4), N.ptr(s4), 0, stream)
+        d_step = _bound(N, "kq_mx_dequant", N.FMT_MXFP4_E2M1, N.ptr(q4), N.ptr(s4), 7168, 2048,
+                        N.DT_BF16, N.ptr(d4), 0, stream)
 
         tq = _time_loop(torch, q_step, args.steps, args.warmup)
         td = _time_loop(torch, d_step, args.steps, args.warmup)
