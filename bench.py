@@ -31,6 +31,7 @@ sys.path.insert(0, str(ROOT))
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 FP4_PEAK_TFLOPS = 10100.0
+FP8_PEAK_TFLOPS = 5000.0
 METRIC = "quantize GB/s + MXFP4 expert GEMM TFLOPS, as % of MI355X roofline (1 GPU)"
 
 
@@ -195,6 +196,23 @@ def main() -> int:
             "roofline": _roofline("mfma", tflops, "moe_prefill_cfg3"),
             "frac_of_fp4_dense_peak": round(tflops / FP4_PEAK_TFLOPS, 4),
         }
+        # Activation-quantized modes (W4A8 / W4A4, no kquant counterpart): the
+        # same forward with tokens and intermediates MX-quantized, every GEMM on
+        # the block-scaled fp8/fp4 MFMA; priced against that MFMA's peak
+        # (E4M3 x E2M1 runs at the fp8 rate, E2M1 x E2M1 at the fp4 rate).
+        for fmt, peak in (("mxfp8", FP8_PEAK_TFLOPS), ("mxfp4", FP4_PEAK_TFLOPS)):
+            def mx_step(fmt=fmt):
+                moe.grouped_expert_forward(x3, ids_d, rw_d, weights, activation_format=fmt)
+
+            t_mx = _time_loop(torch, mx_step, max(3, args.steps // 10), 2)
+            tf = flops / t_mx / 1e12
+            result[f"cfg3_moe_prefill_{'w4a8' if fmt == 'mxfp8' else 'w4a4'}"] = {
+                "workload": f"cfg3 shapes, activations {fmt.upper()}-quantized per row, block-scaled MFMA",
+                "tflops": round(tf, 1),
+                "ms": round(t_mx * 1e3, 3),
+                "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": peak, "unit": "TFLOP/s",
+                             "frac": round(tf / peak, 4), "traffic": None},
+            }
         del weights, x3
 
     # -------------------------------------------------- config 5 decode --

@@ -46,6 +46,12 @@ enum {
    instead of the direct-to-LDS one; both meet the same error bound, and
    differ only by fp32 rounding (they sum each MFMA's k in another order) */
 enum { KQ_MOE_REGISTER_STAGED = 1u };
+/* kq_moe_forward flags: activation-quantized modes (no kquant counterpart).
+   The tokens and the bf16 intermediates are MX-quantized per row with the
+   kq_mx_quantize rule (E4M3 for W4A8, E2M1 for W4A4) and every GEMM runs
+   on the block-scaled fp8/fp4 MFMA; the result equals an fp32 GEMM over the
+   dequantized operands up to summation order */
+enum { KQ_MOE_ACT_MXFP8 = 2u, KQ_MOE_ACT_MXFP4 = 4u };
 /* kq_syrk_accumulate flags */
 enum { KQ_SYRK_OVERWRITE = 1u, KQ_SYRK_SQUARE_WEIGHTS = 2u, KQ_SUM_SQUARE_F64 = 4u };
 /* byte tables of kq_decode_bytes */
@@ -134,7 +140,7 @@ int64_t kq_moe_workspace_size(int64_t tokens, int topk, int experts, int64_t hid
  * out [tokens, hidden] bf16 or fp32.
  * hidden % 512 == 0, I % 512 == 0, topk <= 64, experts <= 4096.
  * workspace: >= kq_moe_workspace_size bytes, 256-byte aligned, caller owned;
- * flags: 0 or KQ_MOE_REGISTER_STAGED.
+ * flags: 0, KQ_MOE_REGISTER_STAGED, KQ_MOE_ACT_MXFP8 or KQ_MOE_ACT_MXFP4.
  * results are bitwise reproducible (no floating-point atomics). */
 int kq_moe_forward(int activation, float act_beta, float act_linear_beta,
                    const void* x, int64_t ldx, int64_t tokens, int64_t hidden,

@@ -34,6 +34,8 @@ SYRK_OVERWRITE = 1
 SYRK_SQUARE_WEIGHTS = 2
 SUM_SQUARE_F64 = 4
 MOE_REGISTER_STAGED = 1
+MOE_ACT_MXFP8 = 2
+MOE_ACT_MXFP4 = 4
 ACT_SITU = 0
 ACT_SWIGLU = 1
 

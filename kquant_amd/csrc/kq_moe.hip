@@ -41,7 +41,8 @@ constexpr int S_BYTES = BN * 2;
 constexpr int STAGE = A_BYTES + B_BYTES + S_BYTES;
 
 struct Layout {
-  size_t counts, offsets, block_counts, sorted, small_list, large_tiles, meta, act, y, total;
+  size_t counts, offsets, block_counts, sorted, small_list, large_tiles, meta, act, y;
+  size_t xq, xs, aq, as, total;  // MX-quantized tokens / intermediates (activation-quantized modes)
   int64_t pairs, nblk, max_small, max_large, max_list;
 };
 
@@ -67,6 +68,10 @@ static Layout make_layout(int64_t tokens, int topk, int experts, int64_t hidden,
   L.meta = o;         o = align256(o + sizeof(int) * 4);
   L.act = o;          o = align256(o + 2 * (size_t)L.pairs * inter);
   L.y = o;            o = align256(o + 4 * (size_t)L.pairs * hidden);
+  L.xq = o;           o = align256(o + (size_t)tokens * hidden);
+  L.xs = o;           o = align256(o + (size_t)tokens * hidden / 32);
+  L.aq = o;           o = align256(o + (size_t)L.pairs * inter);
+  L.as = o;           o = align256(o + (size_t)L.pairs * inter / 32);
   L.total = o;
   return L;
 }
@@ -507,6 +512,172 @@ __global__ __launch_bounds__(S * RW * 64) void moe_small_kernel(
 
 }
 
+// ------------------------------------ activation-quantized GEMV (W4A8/W4A4) --
+// Same workgroup shape, weight stream and epilogues as moe_small_kernel, for
+// activations MX-quantized beforehand (AF = 0: E4M3 bytes [rows, K]; AF = 4:
+// E2M1 packed [rows, K/2]; E8M0 scales [rows, K/32]).  Both operands go into
+// v_mfma_scale_f32_16x16x128_f8f6f4 as they are: lane (m, g) of a 128-k chunk
+// supplies A = E2M1 k 32g .. 32g + 31 (16 bytes) or E4M3 k 16g .. 16g + 15 and
+// 64 + 16g .. + 15 (2 x 16 bytes) of token slot m, the weights of row m of the
+// tile and block g, and the scales of (slot m, block g) and (row m, block g).
+typedef int i32x8_t __attribute__((ext_vector_type(8)));
+
+template <bool GATEUP, int AF, int NBP, int S, int RW, int P, int STEPS>
+__global__ __launch_bounds__(S * RW * 64) void moe_small_mx_kernel(
+    const uint8_t* __restrict__ aq, const uint8_t* __restrict__ as, int topk,
+    const int* __restrict__ sorted, const int* __restrict__ small_list,
+    const uint8_t* __restrict__ wt, const uint8_t* __restrict__ wst, int64_t rows_per_expert,
+    int64_t K, int64_t inter, ActParams act, const float* __restrict__ route_w,
+    uint16_t* __restrict__ act_out, float* __restrict__ y_out, int64_t hidden) {
+  constexpr int NB = GATEUP ? 2 * NBP : NBP;
+  constexpr int CH = RW * 16 * NBP;
+  constexpr int NBUF = P + 1;
+  constexpr int ABYTES = AF == 4 ? 64 : 128;      // A bytes per row per 128-k chunk
+  const int e = small_list[3 * blockIdx.x];
+  if (e < 0) return;
+  const int beg = small_list[3 * blockIdx.x + 1];
+  const int n = small_list[3 * blockIdx.x + 2];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int kpart = wave % S, rgw = wave / S;
+  const int m = lane & 15, g = lane >> 4;
+  const int64_t c0 = (int64_t)blockIdx.y * CH + rgw * 16 * NBP;
+  const int64_t nchunk = K / 128;
+  const int64_t rgs = rows_per_expert / 16;
+  const int64_t c_first = kpart * nchunk / S;
+  const int steps = (int)((kpart + 1) * nchunk / S - c_first);
+  const uint8_t* wtile[NB];
+  const uint8_t* stile[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    const int64_t rg = GATEUP ? (b < NBP ? c0 / 16 + b : inter / 16 + c0 / 16 + (b - NBP)) : c0 / 16 + b;
+    const int64_t t0 = ((int64_t)e * rgs + rg) * nchunk + c_first;
+    wtile[b] = wt + t0 * 1024 + 16 * lane;
+    stile[b] = wst + t0 * 64 + lane;
+  }
+  struct WBuf {
+    u32x4_t w[NB];
+    uint32_t ws[NB];
+  };
+  struct ABuf {
+    u32x4_t v[AF == 4 ? 1 : 2];
+    uint32_t s;
+  };
+  auto load_w = [&](int s, WBuf& B) {
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      B.w[b] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(wtile[b] + (int64_t)s * 1024));
+      B.ws[b] = stile[b][(int64_t)s * 64];
+    }
+  };
+  WBuf wb[NBUF];
+  ABuf ab[NBUF];
+  if constexpr (STEPS > 0) {
+#pragma unroll
+    for (int s = 0; s < P && s < STEPS; ++s) load_w(s, wb[s]);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  const int mslot = m < n ? m : 0;
+  const int apair = sorted[beg + mslot];
+  const int64_t arow = GATEUP ? (int64_t)(apair / topk) : (int64_t)(beg + mslot);
+  const uint8_t* ap = aq + arow * (AF == 4 ? K / 2 : K);
+  const uint8_t* sp = as + arow * (K / 32);
+  auto load_a = [&](int s, ABuf& B) {
+    const int64_t c = c_first + s;
+    if (AF == 4) {
+      B.v[0] = *reinterpret_cast<const u32x4_t*>(ap + ABYTES * c + 16 * g);
+    } else {
+      B.v[0] = *reinterpret_cast<const u32x4_t*>(ap + ABYTES * c + 16 * g);
+      B.v[AF == 4 ? 0 : 1] = *reinterpret_cast<const u32x4_t*>(ap + ABYTES * c + 64 + 16 * g);
+    }
+    B.s = sp[4 * c + g];
+  };
+  f32x4_t acc[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) acc[b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  auto compute = [&](const WBuf& W, const ABuf& A) {
+    i32x8_t a8;
+    if (AF == 4) {
+      a8 = i32x8_t{(int)A.v[0][0], (int)A.v[0][1], (int)A.v[0][2], (int)A.v[0][3], 0, 0, 0, 0};
+    } else {
+      const int h = AF == 4 ? 0 : 1;
+      a8 = i32x8_t{(int)A.v[0][0], (int)A.v[0][1], (int)A.v[0][2], (int)A.v[0][3],
+                   (int)A.v[h][0], (int)A.v[h][1], (int)A.v[h][2], (int)A.v[h][3]};
+    }
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const i32x8_t w8 = i32x8_t{(int)W.w[b][0], (int)W.w[b][1], (int)W.w[b][2], (int)W.w[b][3], 0, 0, 0, 0};
+      acc[b] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a8, w8, acc[b], AF, 4, 0, (int)A.s, 0,
+                                                                (int)W.ws[b]);
+    }
+  };
+  if constexpr (STEPS > 0) {
+#pragma unroll
+    for (int s = 0; s < P && s < STEPS; ++s) load_a(s, ab[s]);
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s) {
+      if (s + P < STEPS) {
+        load_w(s + P, wb[(s + P) % NBUF]);
+        load_a(s + P, ab[(s + P) % NBUF]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      compute(wb[s % NBUF], ab[s % NBUF]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  } else {
+    const int last = steps - 1;
+    load_w(0, wb[0]);
+    load_a(0, ab[0]);
+    for (int s = 0; s < steps; s += 2) {
+      const int s1 = s + 1 < last ? s + 1 : last, s2 = s + 2 < last ? s + 2 : last;
+      load_w(s1, wb[1]);
+      load_a(s1, ab[1]);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(wb[0], ab[0]);
+      __builtin_amdgcn_sched_barrier(0);
+      load_w(s2, wb[0]);
+      load_a(s2, ab[0]);
+      __builtin_amdgcn_sched_barrier(0);
+      if (s + 1 < steps) compute(wb[1], ab[1]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  auto store = [&](int u, f32x4_t x0, f32x4_t x1) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int slot = 4 * g + j;
+      if (slot >= n) continue;
+      const int64_t ch = c0 + 16 * u + m;
+      if (GATEUP) {
+        const float v = activate(act, x0[j], x1[j]);
+        reinterpret_cast<__bf16*>(act_out)[(int64_t)(beg + slot) * inter + ch] = (__bf16)v;
+      } else {
+        const int pair = sorted[beg + slot];
+        y_out[(int64_t)pair * hidden + ch] = route_w[pair] * x0[j];
+      }
+    }
+  };
+  if constexpr (S == 1) {
+#pragma unroll
+    for (int u = 0; u < NBP; ++u) store(u, acc[u], GATEUP ? acc[u + NBP] : acc[u]);
+  } else {
+    __shared__ f32x4_t red[S * RW][NB][64];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) red[wave][b][lane] = acc[b];
+    __syncthreads();
+    for (int u = kpart; u < NBP; u += S) {
+      f32x4_t x0 = red[rgw * S][u][lane], x1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int p = 1; p < S; ++p) x0 += red[rgw * S + p][u][lane];
+      if (GATEUP) {
+        x1 = red[rgw * S][u + NBP][lane];
+#pragma unroll
+        for (int p = 1; p < S; ++p) x1 += red[rgw * S + p][u + NBP][lane];
+      }
+      store(u, x0, x1);
+    }
+  }
+}
+
 // ------------------------------------------------ grouped GEMM large path --
 // Tile (expert, 256 sorted pair rows) x 256 weight rows, 8 waves of 64 x 128,
 // K step 64.  GATEUP: the 256 weight rows are 128 gate rows c0.. and the 128
@@ -902,6 +1073,248 @@ __global__ __launch_bounds__(512, 1) void moe_large_dma_kernel(
   __builtin_amdgcn_s_waitcnt(dma::waitcnt_vm(0));  // no load may land after the workgroup ends
 }
 
+// ------------------------- grouped GEMM, activation-quantized (W4A8/W4A4) --
+// moe_large_dma_kernel's tiles, waves, persistent order and epilogues, with
+// MX-quantized activations (AF = 0 E4M3, 4 E2M1) and one
+// v_mfma_scale_f32_16x16x128_f8f6f4 per 16x16 block and 128-k step: a wave's
+// 64 x 128 output is 4 x 8 blocks.  Per stage (128 k) in LDS: A rows
+// (64 / 128 B, chunk c of row r at c ^ ((r/4)%4) / c ^ ((r/2)%8)), A scales
+// (one dword per row: its four blocks), the row groups' 1 KiB weight tiles
+// and their 64-byte scale tiles, all by direct loads.  Lane (m, g) of a block
+// reads A chunk g (E2M1) or chunks g and 4 + g (E4M3) of row m, the weight
+// unit (g, m) of its row group and the two scale bytes; the 16 lanes of every
+// 128-bit read cover 256 distinct bytes.
+namespace mx_gemm {
+constexpr int BKQ = 128;
+template <int AF> constexpr int a_row() { return AF == 4 ? 64 : 128; }
+template <int AF> constexpr int a_bytes() { return BM * a_row<AF>(); }
+constexpr int AS_BYTES = BM * 4;
+constexpr int W_BYTES = 16 * 1024;
+constexpr int WS_BYTES = 16 * 64;
+template <int AF> constexpr int stage() { return a_bytes<AF>() + AS_BYTES + W_BYTES + WS_BYTES; }
+template <int AF> constexpr int nstage() { return AF == 4 ? 4 : 3; }
+template <int AF> constexpr int loads() { return (AF == 4 ? 2 : 4) + 1 + 2 + 1; }  // per wave per stage
+}  // namespace mx_gemm
+
+__shared__ __attribute__((aligned(16))) unsigned char moe_mx_lds[3 * mx_gemm::stage<0>()];
+static_assert(4 * mx_gemm::stage<4>() <= 3 * mx_gemm::stage<0>(), "LDS ring size");
+
+template <bool GATEUP, int AF>
+__global__ __launch_bounds__(512, 1) void moe_large_mx_kernel(
+    const uint8_t* __restrict__ aq, const uint8_t* __restrict__ as, uint32_t aq_bytes,
+    uint32_t as_bytes, int topk, const int* __restrict__ offsets, const int* __restrict__ sorted,
+    const int* __restrict__ tiles, const int* __restrict__ meta, const uint8_t* __restrict__ wt,
+    const uint8_t* __restrict__ wst, int64_t rows_per_expert, int64_t K, int64_t inter,
+    int col_tiles, ActParams act, const float* __restrict__ route_w, uint16_t* __restrict__ act_out,
+    float* __restrict__ y_out, int64_t hidden) {
+  using namespace mx_gemm;
+  using dma::i32x4_t;
+  constexpr int AROW = a_row<AF>(), ABYTES = a_bytes<AF>(), STAGE = stage<AF>();
+  constexpr int NST = nstage<AF>(), LOADS = loads<AF>();
+  constexpr int AQ = AF == 4 ? 2 : 4;  // A direct loads per wave per stage
+  const int G = gridDim.x;
+  const int worker = (int)(blockIdx.x % 8) * (G / 8) + (int)(blockIdx.x / 8);
+  const int total = meta[1] * col_tiles;
+  if (worker >= total) return;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t nchunk = K / 128, rgs = rows_per_expert / 16;
+  const int64_t nrows = GATEUP ? 2 * inter : hidden;
+  const int64_t arow_bytes = AF == 4 ? K / 2 : K, asrow = K / 32;
+  const uint32_t b_bytes = (uint32_t)(rgs * nchunk * 1024), s_bytes = (uint32_t)(rgs * nchunk * 64);
+  const int steps = (int)(K / BKQ);
+  const uint32_t lds0 = dma::lds_offset_of(moe_mx_lds);
+  const i32x4_t a_rsrc = dma::make_rsrc(aq, aq_bytes);
+  const i32x4_t as_rsrc = dma::make_rsrc(as, as_bytes);
+  auto grow_group = [&](int64_t c0, int lrg) -> int64_t {
+    if (GATEUP) return lrg < 8 ? c0 / 16 + lrg : inter / 16 + c0 / 16 + (lrg - 8);
+    return c0 / 16 + lrg;
+  };
+
+  // ---- load side
+  int lt = worker, ls = 0;
+  uint32_t a_off[AQ], as_off, b_off[2], bs_off = 0;
+  i32x4_t b_rsrc = dma::make_rsrc(wt, 0), s_rsrc = dma::make_rsrc(wst, 0);
+  auto set_load_tile = [&]() {
+    if (lt >= total) {
+#pragma unroll
+      for (int q = 0; q < AQ; ++q) a_off[q] = aq_bytes;
+      as_off = as_bytes;
+      b_off[0] = b_off[1] = b_bytes;
+      bs_off = s_bytes;
+      return;
+    }
+    const int mt = lt / col_tiles, nt = lt - mt * col_tiles;
+    const int e = tiles[2 * mt], m0 = tiles[2 * mt + 1];
+    const int beg = offsets[e], n = offsets[e + 1] - beg;
+    const int64_t c0 = (int64_t)nt * (GATEUP ? BN / 2 : BN);
+    // rows of this lane's A loads (all lookups issued before the first use)
+    int src[AQ + 1];
+#pragma unroll
+    for (int q = 0; q < AQ; ++q) {
+      const int row = AF == 4 ? 16 * (8 * q + wave) + (lane >> 2) : 8 * (8 * q + wave) + (lane >> 3);
+      const int slot = m0 + row;
+      src[q] = GATEUP ? sorted[beg + (slot < n ? slot : n - 1)] : beg + slot;
+    }
+    {
+      const int slot = m0 + 32 * wave + (lane & 31);
+      src[AQ] = GATEUP ? sorted[beg + (slot < n ? slot : n - 1)] : beg + slot;
+    }
+#pragma unroll
+    for (int q = 0; q < AQ; ++q) {
+      const int row = AF == 4 ? 16 * (8 * q + wave) + (lane >> 2) : 8 * (8 * q + wave) + (lane >> 3);
+      const int ch = AF == 4 ? (lane & 3) ^ ((row >> 2) & 3) : (lane & 7) ^ ((row >> 1) & 7);
+      const int64_t r = GATEUP ? src[q] / topk : src[q];
+      a_off[q] = m0 + row < n ? (uint32_t)(r * arow_bytes + ch * 16) : aq_bytes;
+    }
+    {
+      const int row = 32 * wave + (lane & 31);
+      const int64_t r = GATEUP ? src[AQ] / topk : src[AQ];
+      as_off = m0 + row < n ? (uint32_t)(r * asrow) : as_bytes;
+    }
+    b_rsrc = dma::make_rsrc(wt + (int64_t)e * rgs * nchunk * 1024, b_bytes);
+    s_rsrc = dma::make_rsrc(wst + (int64_t)e * rgs * nchunk * 64, s_bytes);
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int64_t rg = grow_group(c0, 2 * wave + q);
+      b_off[q] = 16 * rg < nrows ? (uint32_t)(rg * nchunk * 1024 + lane * 16) : b_bytes;
+    }
+    {
+      const int64_t rg = grow_group(c0, 2 * wave + ((lane >> 2) & 1));
+      bs_off = 16 * rg < nrows ? (uint32_t)(rg * nchunk * 64 + (lane & 3) * 16) : s_bytes;
+    }
+  };
+  auto issue = [&](int slot) {
+    const uint32_t base = lds0 + (uint32_t)(slot * STAGE);
+    const uint32_t chunk = (uint32_t)ls;  // one 128-k chunk per step
+#pragma unroll
+    for (int q = 0; q < AQ; ++q)
+      dma::load_to_lds16(a_rsrc, a_off[q] >= aq_bytes ? aq_bytes : a_off[q] + chunk * AROW,
+                         base + (uint32_t)((8 * q + wave) * 1024));
+    if (lane < 32)
+      dma::load_to_lds4(as_rsrc, as_off >= as_bytes ? as_bytes : as_off + chunk * 4,
+                        base + (uint32_t)(ABYTES + wave * 128));
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+      dma::load_to_lds16(b_rsrc, b_off[q] >= b_bytes ? b_bytes : b_off[q] + chunk * 1024,
+                         base + (uint32_t)(ABYTES + AS_BYTES + (2 * wave + q) * 1024));
+    if (lane < 8)
+      dma::load_to_lds16(s_rsrc, bs_off >= s_bytes ? s_bytes : bs_off + chunk * 64,
+                         base + (uint32_t)(ABYTES + AS_BYTES + W_BYTES + wave * 128));
+  };
+  auto advance = [&]() {
+    if (++ls == steps) {
+      ls = 0;
+      lt += G;
+      set_load_tile();
+    }
+  };
+
+  // ---- compute side
+  const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+  const int fm = lane & 15, fg = lane >> 4;
+  int aoff[4][AF == 4 ? 1 : 2], asoff[4], boff[8], bsoff[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = wm + 16 * i + fm;
+    if (AF == 4) {
+      aoff[i][0] = r * AROW + 16 * (fg ^ ((r >> 2) & 3));
+    } else {
+      aoff[i][0] = r * AROW + 16 * (fg ^ ((r >> 1) & 7));
+      aoff[i][AF == 4 ? 0 : 1] = r * AROW + 16 * ((4 + fg) ^ ((r >> 1) & 7));
+    }
+    asoff[i] = ABYTES + r * 4 + fg;
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int rr = GATEUP ? (j < 4 ? 0 : BN / 2) + wn + 16 * (j & 3) + fm : 2 * wn + 16 * j + fm;
+    boff[j] = ABYTES + AS_BYTES + (rr >> 4) * 1024 + (fg * 16 + (rr & 15)) * 16;
+    bsoff[j] = ABYTES + AS_BYTES + W_BYTES + (rr >> 4) * 64 + fg * 16 + (rr & 15);
+  }
+
+  set_load_tile();
+#pragma unroll
+  for (int p = 0; p < NST - 1; ++p) {
+    issue(p);
+    advance();
+  }
+  int cslot = 0;
+  for (int t = worker; t < total; t += G) {
+    const int mt = t / col_tiles, nt = t - mt * col_tiles;
+    const int e = tiles[2 * mt], m0 = tiles[2 * mt + 1];
+    const int beg = offsets[e], n = offsets[e + 1] - beg;
+    const int64_t c0 = (int64_t)nt * (GATEUP ? BN / 2 : BN);
+    const bool active = m0 + wm < n;
+    f32x4_t acc[4][8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    for (int s = 0; s < steps; ++s) {
+      dma::wait_and_barrier<(NST - 2) * LOADS>();
+      issue(cslot == 0 ? NST - 1 : cslot - 1);
+      advance();
+      if (active) {
+        const unsigned char* st = moe_mx_lds + cslot * STAGE;
+        i32x8_t a8[4];
+        uint32_t sa[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const u32x4_t v0 = *reinterpret_cast<const u32x4_t*>(st + aoff[i][0]);
+          if (AF == 4) {
+            a8[i] = i32x8_t{(int)v0[0], (int)v0[1], (int)v0[2], (int)v0[3], 0, 0, 0, 0};
+          } else {
+            const u32x4_t v1 = *reinterpret_cast<const u32x4_t*>(st + aoff[i][AF == 4 ? 0 : 1]);
+            a8[i] = i32x8_t{(int)v0[0], (int)v0[1], (int)v0[2], (int)v0[3],
+                            (int)v1[0], (int)v1[1], (int)v1[2], (int)v1[3]};
+          }
+          sa[i] = st[asoff[i]];
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const u32x4_t w = *reinterpret_cast<const u32x4_t*>(st + boff[j]);
+          const i32x8_t b8 = i32x8_t{(int)w[0], (int)w[1], (int)w[2], (int)w[3], 0, 0, 0, 0};
+          const int sb = st[bsoff[j]];
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a8[i], b8, acc[i][j], AF, 4, 0,
+                                                                         (int)sa[i], 0, sb);
+        }
+      }
+      cslot = cslot == NST - 1 ? 0 : cslot + 1;
+    }
+
+    if (active) {
+      // D layout (16x16): lane holds rows 4 fg + r, column fm of its block
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int slot = m0 + wm + 16 * i + 4 * fg + r;
+          if (slot >= n) continue;
+          if (GATEUP) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const float v = activate(act, acc[i][j][r], acc[i][j + 4][r]);
+              const int64_t ch = c0 + wn + 16 * j + fm;
+              reinterpret_cast<__bf16*>(act_out)[(int64_t)(beg + slot) * inter + ch] = (__bf16)v;
+            }
+          } else {
+            const int pair = sorted[beg + slot];
+            const float rw = route_w[pair];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+              const int64_t h = c0 + 2 * wn + 16 * j + fm;
+              y_out[(int64_t)pair * hidden + h] = rw * acc[i][j][r];
+            }
+          }
+        }
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(dma::waitcnt_vm(0));  // no load may land after the workgroup ends
+}
+
 // ---------------------------------------------------------------- combine --
 template <int OUT>
 __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restrict__ y,
@@ -989,6 +1402,77 @@ static hipError_t launch_small(int64_t experts_max, int64_t channels, int64_t K,
   return hipGetLastError();
 }
 
+template <bool GATEUP, int AF, int NBP, int S, int RW, int P, typename... Args>
+static hipError_t launch_small_mx(int64_t experts_max, int64_t channels, int64_t K, hipStream_t st,
+                                  Args... args) {
+  constexpr int CH = RW * 16 * NBP;
+  const dim3 grid((unsigned)experts_max, (unsigned)(channels / CH));
+  const int64_t nchunk = K / 128;
+  const int64_t steps = nchunk % S == 0 ? nchunk / S : 0;
+  switch (steps) {
+#define KQ_SMALL_MX_CASE(N) \
+    case N: moe_small_mx_kernel<GATEUP, AF, NBP, S, RW, P, N><<<grid, S * RW * 64, 0, st>>>(args...); break;
+    KQ_SMALL_MX_CASE(2) KQ_SMALL_MX_CASE(4) KQ_SMALL_MX_CASE(7) KQ_SMALL_MX_CASE(8) KQ_SMALL_MX_CASE(14)
+    KQ_SMALL_MX_CASE(16)
+#undef KQ_SMALL_MX_CASE
+    default:
+      moe_small_mx_kernel<GATEUP, AF, NBP, S, RW, P, 0><<<grid, S * RW * 64, 0, st>>>(args...);
+  }
+  return hipGetLastError();
+}
+
+// Activation-quantized forward (W4A8 / W4A4): the same routing and combine,
+// tokens and intermediates MX-quantized (kq_mx_quantize's rule) before each
+// projection, both GEMM shapes on the block-scaled MFMA.
+template <int AF>
+static int moe_forward_mx(const Layout& L, unsigned char* w, const ActParams& ap, const void* x,
+                          int64_t ldx, int64_t tokens, int64_t hidden, const float* route_weights,
+                          int topk, int64_t inter, const uint8_t* w13_t, const uint8_t* w13_st,
+                          const uint8_t* w2_t, const uint8_t* w2_st, bool decode, int grid_dma,
+                          void* stream) {
+  hipStream_t st = (hipStream_t)stream;
+  const int fmt = AF == 4 ? KQ_FMT_MXFP4_E2M1 : KQ_FMT_MXFP8_E4M3;
+  const int* offsets = (const int*)(w + L.offsets);
+  const int* sorted = (const int*)(w + L.sorted);
+  const int* small_list = (const int*)(w + L.small_list);
+  const int* large_tiles = (const int*)(w + L.large_tiles);
+  const int* meta = (const int*)(w + L.meta);
+  uint16_t* act = (uint16_t*)(w + L.act);
+  float* y = (float*)(w + L.y);
+  uint8_t *xq = w + L.xq, *xs = w + L.xs, *aq = w + L.aq, *as = w + L.as;
+  const bool any_large = !decode && L.pairs > SMALL_MAX;
+  hipError_t e;
+  int rc = kq_mx_quantize(fmt, KQ_DT_BF16, x, ldx, tokens, hidden, xq, xs, 0, stream);
+  if (rc != KQ_OK) return rc;
+  e = launch_small_mx<true, AF, KQ_GU_NBP, KQ_GU_S, KQ_GU_RW, KQ_GU_P>(
+      L.max_list, inter, hidden, st, (const uint8_t*)xq, (const uint8_t*)xs, topk, sorted, small_list,
+      w13_t, w13_st, 2 * inter, hidden, inter, ap, route_weights, act, y, hidden);
+  if (e != hipSuccess) return kq_check_launch(e, "kq_moe_forward/gateup_small");
+  const int64_t abytes = AF == 4 ? hidden / 2 : hidden;
+  if (any_large) {
+    moe_large_mx_kernel<true, AF><<<grid_dma, THREADS, 0, st>>>(
+        xq, xs, (uint32_t)(tokens * abytes), (uint32_t)(tokens * hidden / 32), topk, offsets, sorted,
+        large_tiles, meta, w13_t, w13_st, 2 * inter, hidden, inter, (int)(inter / (BN / 2)), ap,
+        route_weights, act, y, hidden);
+    if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_moe_forward/gateup_large");
+  }
+  rc = kq_mx_quantize(fmt, KQ_DT_BF16, act, inter, L.pairs, inter, aq, as, 0, stream);
+  if (rc != KQ_OK) return rc;
+  e = launch_small_mx<false, AF, KQ_DN_NBP, KQ_DN_S, KQ_DN_RW, KQ_DN_P>(
+      L.max_list, hidden, inter, st, (const uint8_t*)aq, (const uint8_t*)as, topk, sorted, small_list,
+      w2_t, w2_st, hidden, inter, inter, ap, route_weights, act, y, hidden);
+  if (e != hipSuccess) return kq_check_launch(e, "kq_moe_forward/down_small");
+  if (any_large) {
+    const int64_t ibytes = AF == 4 ? inter / 2 : inter;
+    moe_large_mx_kernel<false, AF><<<grid_dma, THREADS, 0, st>>>(
+        aq, as, (uint32_t)(L.pairs * ibytes), (uint32_t)(L.pairs * inter / 32), topk, offsets, sorted,
+        large_tiles, meta, w2_t, w2_st, hidden, inter, inter, (int)(hidden / BN), ap, route_weights, act,
+        y, hidden);
+    if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_moe_forward/down_large");
+  }
+  return KQ_OK;
+}
+
 extern "C" int64_t kq_moe_workspace_size(int64_t tokens, int topk, int experts, int64_t hidden,
                                          int64_t inter) {
   if (tokens < 0 || topk <= 0 || experts <= 0 || hidden <= 0 || inter <= 0) return -1;
@@ -1003,8 +1487,13 @@ extern "C" int kq_moe_forward(int activation, float act_beta, float act_linear_b
                               const uint8_t* w2_st, int out_dtype, void* out,
                               void* workspace, int64_t workspace_bytes, uint32_t flags,
                               void* stream) {
-  if (flags & ~(uint32_t)KQ_MOE_REGISTER_STAGED)
+  if (flags & ~(uint32_t)(KQ_MOE_REGISTER_STAGED | KQ_MOE_ACT_MXFP8 | KQ_MOE_ACT_MXFP4))
     return kq_fail(KQ_ERR_INVALID, "kq_moe_forward: unknown flags 0x%x", flags);
+  const int act_fmt = (flags & KQ_MOE_ACT_MXFP4) ? 4 : (flags & KQ_MOE_ACT_MXFP8) ? 0 : -1;
+  if ((flags & KQ_MOE_ACT_MXFP4) && (flags & KQ_MOE_ACT_MXFP8))
+    return kq_fail(KQ_ERR_INVALID, "kq_moe_forward: KQ_MOE_ACT_MXFP8 and KQ_MOE_ACT_MXFP4 exclude each other");
+  if (act_fmt >= 0 && (flags & KQ_MOE_REGISTER_STAGED))
+    return kq_fail(KQ_ERR_INVALID, "kq_moe_forward: the activation-quantized modes have no register-staged kernel");
   if (activation != KQ_ACT_SITU && activation != KQ_ACT_SWIGLU)
     return kq_fail(KQ_ERR_INVALID, "kq_moe_forward: unknown activation %d", activation);
   if (out_dtype != KQ_DT_BF16 && out_dtype != KQ_DT_F32)
@@ -1065,6 +1554,36 @@ extern "C" int kq_moe_forward(int activation, float act_beta, float act_linear_b
     if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_moe_forward/scatter");
   }
 
+  auto combine = [&]() -> int {
+    const dim3 cgrid((unsigned)((hidden / 4 + 255) / 256), (unsigned)tokens);
+    if (out_dtype == KQ_DT_F32)
+      moe_combine_kernel<2><<<cgrid, 256, 0, st>>>(y, route_ids, topk, experts, hidden, out);
+    else
+      moe_combine_kernel<0><<<cgrid, 256, 0, st>>>(y, route_ids, topk, experts, hidden, out);
+    return kq_check_launch(hipGetLastError(), "kq_moe_forward/combine");
+  };
+
+  if (act_fmt >= 0) {
+    if ((uint64_t)tokens * hidden > dma::MAX_RANGE || (uint64_t)L.pairs * inter > dma::MAX_RANGE ||
+        (uint64_t)(2 * inter) * hidden / 2 > dma::MAX_RANGE)
+      return kq_fail(KQ_ERR_LIMIT, "kq_moe_forward: activation-quantized operands exceed 4 GiB");
+    int grid_mx = 8;
+    if (!decode && L.pairs > SMALL_MAX) {
+      int dev = 0, cus = 0;
+      if ((e = hipGetDevice(&dev)) == hipSuccess)
+        e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+      if (e != hipSuccess) return kq_check_launch(e, "kq_moe_forward/device");
+      grid_mx = cus / 8 * 8 > 0 ? cus / 8 * 8 : 8;
+    }
+    const int rc = act_fmt == 4
+        ? moe_forward_mx<4>(L, w, ap, x, ldx, tokens, hidden, route_weights, topk, inter, w13_t, w13_st,
+                            w2_t, w2_st, decode, grid_mx, stream)
+        : moe_forward_mx<0>(L, w, ap, x, ldx, tokens, hidden, route_weights, topk, inter, w13_t, w13_st,
+                            w2_t, w2_st, decode, grid_mx, stream);
+    if (rc != KQ_OK) return rc;
+    return combine();
+  }
+
   const uint16_t* xb = (const uint16_t*)x;
   // gate/up
   {
@@ -1123,13 +1642,7 @@ extern "C" int kq_moe_forward(int activation, float act_beta, float act_linear_b
         ap, route_weights, act, y, hidden);
     if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_moe_forward/down_large");
   }
-  // combine
-  const dim3 cgrid((unsigned)((hidden / 4 + 255) / 256), (unsigned)tokens);
-  if (out_dtype == KQ_DT_F32)
-    moe_combine_kernel<2><<<cgrid, 256, 0, st>>>(y, route_ids, topk, experts, hidden, out);
-  else
-    moe_combine_kernel<0><<<cgrid, 256, 0, st>>>(y, route_ids, topk, experts, hidden, out);
-  return kq_check_launch(hipGetLastError(), "kq_moe_forward/combine");
+  return combine();
 }
 
 // Routing sort alone (for per-expert calibration statistics): the pairs

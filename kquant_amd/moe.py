@@ -121,6 +121,11 @@ def expert_output(
 
     if activation not in ("situ", "swiglu"):
         raise ValueError(f"unsupported activation {activation!r}")
+    act_flags = {"bf16": 0, "mxfp8": N.MOE_ACT_MXFP8, "mxfp4": N.MOE_ACT_MXFP4}
+    if activation_format not in act_flags:
+        raise ValueError(f"activation_format must be bf16, mxfp8 or mxfp4, got {activation_format!r}")
+    if register_staged and activation_format != "bf16":
+        raise ValueError("register_staged applies to the bf16-activation mode only")
     if inputs.ndim != 2:
         raise ValueError("expert inputs must be two-dimensional")
     (p1, s1), (p3, s3), (p2, s2) = (_pair(w) for w in (w1, w3, w2))
@@ -178,6 +183,7 @@ def grouped_expert_forward(
     linear_beta: float = 25.0,
     out_dtype: torch.dtype = torch.float32,
     register_staged: bool = False,
+    activation_format: str = "bf16",
 ) -> torch.Tensor:
     """Route-weighted expert outputs ``[T, H]`` (fp32 by default, as the
     reference's accumulator is).
@@ -188,10 +194,22 @@ def grouped_expert_forward(
     ``register_staged`` runs the grouped GEMMs on the register-staged kernel
     (taken anyway when a buffer exceeds 4 GiB) instead of the direct-to-LDS
     one; both meet the same error bound and differ only by fp32 rounding.
+
+    ``activation_format`` "mxfp8" / "mxfp4" selects the activation-quantized
+    modes (W4A8 / W4A4, no kquant counterpart): the tokens and the bf16
+    intermediates are MX-quantized per row (the ``mxfp8_quantize`` /
+    ``mxfp4_quantize`` rule) and every GEMM runs on the block-scaled fp8/fp4
+    MFMA.  The result is an fp32 GEMM over the dequantized operands up to
+    summation order; it is not the bf16-activation result.
     """
 
     if activation not in ("situ", "swiglu"):
         raise ValueError(f"unsupported activation {activation!r}")
+    act_flags = {"bf16": 0, "mxfp8": N.MOE_ACT_MXFP8, "mxfp4": N.MOE_ACT_MXFP4}
+    if activation_format not in act_flags:
+        raise ValueError(f"activation_format must be bf16, mxfp8 or mxfp4, got {activation_format!r}")
+    if register_staged and activation_format != "bf16":
+        raise ValueError("register_staged applies to the bf16-activation mode only")
     if out_dtype not in (torch.float32, torch.bfloat16):
         raise TypeError("out_dtype must be float32 or bfloat16")
     if x.ndim != 2:
@@ -225,5 +243,5 @@ def grouped_expert_forward(
            N.ptr(rw), topk, prepared.experts, prepared.inter, N.ptr(prepared.w13_tiles),
            N.ptr(prepared.w13_scale_tiles), N.ptr(prepared.w2_tiles), N.ptr(prepared.w2_scale_tiles),
            N.DTYPE_CODES[out_dtype], N.ptr(out), N.ptr(ws), ws.numel(),
-           N.MOE_REGISTER_STAGED if register_staged else 0, N.stream(gpu))
+           (N.MOE_REGISTER_STAGED if register_staged else 0) | act_flags[activation_format], N.stream(gpu))
     return out if host is None else out.to(host)

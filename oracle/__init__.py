@@ -425,6 +425,13 @@ def round_bf16(x: np.ndarray) -> np.ndarray:
     return bf16_bits_to_f32(f32_to_bf16_bits(x))
 
 
+def mx_roundtrip_rows(fmt: str, x: np.ndarray) -> np.ndarray:
+    """dequant(quant(x)) row by row for a float32 array holding bf16 values
+    (the operand an activation-quantized GEMM multiplies)."""
+    q, sc = mx_quantize(fmt, f32_to_bf16_bits(np.asarray(x, np.float32)), "bf16")
+    return mx_dequant(fmt, q, sc)
+
+
 def moe_forward(
     x: np.ndarray,
     route_ids: np.ndarray,
@@ -434,6 +441,7 @@ def moe_forward(
     activation: str = "situ",
     tokens: np.ndarray | None = None,
     intermediate_bf16: bool = True,
+    act_format: str | None = None,
 ) -> np.ndarray:
     """Routed MoE forward of scripts/closure_exl3_layer.py:557-598 (tp=1).
 
@@ -445,9 +453,17 @@ def moe_forward(
     fp32, contribution = route_weight * partial, summed per token in fp32.
     ``tokens`` restricts the output to a subset of token rows (the result
     has one row per listed token).
+
+    ``act_format`` "mxfp8" / "mxfp4" restates the activation-quantized mode
+    (no kquant counterpart): every token row and every bf16 intermediate row
+    is MX-quantized along its length with the rule of ``mx_quantize`` and
+    dequantized before its GEMM, so the GEMMs see exactly the operands the
+    block-scaled MFMA multiplies.
     """
     act = situ if activation == "situ" else swiglu
     T = x.shape[0]
+    if act_format is not None:
+        x = mx_roundtrip_rows(act_format, x)
     rows = np.arange(T) if tokens is None else np.asarray(tokens)
     pos = {int(t): i for i, t in enumerate(rows)}
     sub_ids = route_ids[rows]
@@ -464,6 +480,8 @@ def moe_forward(
         a = act(gate, up)
         if intermediate_bf16:
             a = round_bf16(a)
+        if act_format is not None:
+            a = mx_roundtrip_rows(act_format, a)
         partial = a @ w2e.T
         if out is None:
             out = np.zeros((rows.size, w2e.shape[0]), dtype=np.float32)

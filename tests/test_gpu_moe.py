@@ -173,3 +173,83 @@ def test_many_tiles_per_workgroup(gpu, register_staged):
     # another fp32 summation order can move a gate/up value across a bf16
     # rounding boundary of the intermediate, which the down GEMM carries on
     assert _max_rel(out.cpu().numpy().astype(np.float64), other.cpu().numpy()) <= 2e-4
+
+
+# Bars of the activation-quantized modes against the oracle on the same
+# quantized operands (element error / max |ref|):
+#  * W4A4: the E2M1 x E2M1 MFMA sums exactly in fp32, so the GEMMs differ
+#    from the oracle only by summation order; 99.9 % of elements within 1e-5.
+#    The rest come from an intermediate moved across a bf16 rounding boundary
+#    and so across an MX step (a few per million elements), which changes
+#    that pair's row by up to one step: all within 0.05.
+#  * W4A8: the E4M3 x E2M1 MFMA does not sum at full fp32 precision (its
+#    products span ~2^17 within one instruction): ~1 % of the bf16
+#    intermediates differ from an fp32 or fp64 GEMM on the same operands by
+#    one ulp, and E4M3's finer steps turn more of those into requantized
+#    elements; 99 % within 1e-3 (observed 99.9 %), all within 2e-2
+#    (observed max 3e-3).
+_MX_BARS = {"mxfp4": (1e-5, 0.999, 0.05), "mxfp8": (1e-3, 0.99, 2e-2)}
+
+
+def _check_operand_exact(ref: np.ndarray, got: np.ndarray, fmt: str) -> float:
+    tight, frac, worst = _MX_BARS[fmt]
+    rel = np.abs(got.astype(np.float64) - ref) / np.abs(ref).max()
+    assert np.mean(rel <= tight) >= frac, f"only {np.mean(rel <= tight):.5f} of elements within {tight}"
+    assert rel.max() <= worst
+    return float(np.median(rel))
+
+
+@pytest.mark.parametrize("fmt", ["mxfp8", "mxfp4"])
+@pytest.mark.parametrize("T", [6, 600])
+def test_activation_quantized_matches_operand_oracle(gpu, fmt, T):
+    """W4A8 / W4A4 modes.  T=6 (24 pairs): decode routing, every expert on the
+    GEMV kernel.  T=600 (2400 pairs): expert 0 with every token on the grouped
+    GEMM (3 row tiles, the last ragged), experts with <= 16 pairs on the
+    GEMV kernel, the rest on the grouped GEMM."""
+    k, E, H, I = 4, 12, 512, 1024
+    g = torch.Generator().manual_seed(21 + T)
+    x = (torch.randn(T, H, generator=g) * torch.exp(0.5 * torch.randn(H, generator=g))).to(torch.bfloat16)
+    p = torch.tensor([0.02] * (E - 1))
+    p[-1] = 0.0005
+    ids = torch.stack([torch.cat([torch.tensor([0]), 1 + torch.multinomial(p, k - 1, generator=g)]) for _ in range(T)])
+    ids = ids.to(torch.int32)
+    w = torch.softmax(torch.randn(T, k, generator=g), -1)
+    weights = workloads.quantized_experts(range(E), E, H, I, seed=22, device=gpu)
+    out = moe.grouped_expert_forward(x.to(gpu), ids.to(gpu), w.to(gpu), *weights, activation_format=fmt)
+    ref = _oracle_mx(x, ids, w, weights, fmt)
+    med = _check_operand_exact(ref, out.cpu().numpy(), fmt)
+    print(f"moe {fmt} T={T} median rel {med:.2e}", flush=True)
+    again = moe.grouped_expert_forward(x.to(gpu), ids.to(gpu), w.to(gpu), *weights, activation_format=fmt)
+    assert torch.equal(out, again)
+
+
+def _oracle_mx(x, ids, w, weights, fmt, tokens=None):
+    w13q, w13s, w2q, w2s = weights
+    cache = {}
+
+    def w13(e):
+        if ("a", e) not in cache:
+            cache[("a", e)] = _deq(w13q[e], w13s[e])
+        return cache[("a", e)]
+
+    def w2(e):
+        if ("b", e) not in cache:
+            cache[("b", e)] = _deq(w2q[e], w2s[e])
+        return cache[("b", e)]
+
+    return oracle.moe_forward(x.float().cpu().numpy(), ids.cpu().numpy(), w.cpu().numpy(), w13, w2,
+                              "situ", tokens=tokens, act_format=fmt)
+
+
+@pytest.mark.parametrize("fmt", ["mxfp8", "mxfp4"])
+def test_activation_quantized_cfg3_full_size_sampled_tokens(gpu, fmt):
+    """Configuration 3 shapes in the W4A8 / W4A4 modes, oracle on sampled tokens."""
+    ids, w = workloads.zipf_routing(8192)
+    x = torch.randn(8192, 7168, generator=torch.Generator().manual_seed(6)).to(torch.bfloat16)
+    weights = workloads.quantized_experts(torch.unique(ids).tolist(), device=gpu)
+    prep = moe.prepare_expert_weights(*weights)
+    out = moe.grouped_expert_forward(x.to(gpu), ids.to(gpu), w.to(gpu), prep, activation_format=fmt)
+    check = np.array([0, 1, 4097, 8191])
+    ref = _oracle_mx(x, ids, w, weights, fmt, tokens=check)
+    med = _check_operand_exact(ref, out[torch.from_numpy(check)].cpu().numpy(), fmt)
+    print(f"moe cfg3 {fmt} median rel {med:.2e}", flush=True)
