@@ -1077,16 +1077,16 @@ __global__ __launch_bounds__(512, 1) void moe_large_dma_kernel(
 // moe_large_dma_kernel's tiles, waves, persistent order and epilogues, with
 // MX-quantized activations (AF = 0 E4M3, 4 E2M1) and one
 // v_mfma_scale_f32_16x16x128_f8f6f4 per 16x16 block and 128-k step: a wave's
-// 64 x 128 output is 4 x 8 blocks.  Per stage (128 k) in LDS: A rows
-// (64 / 128 B, chunk c of row r at c ^ ((r/4)%4) / c ^ ((r/2)%8)), A scales
-// (one dword per row: its four blocks), the row groups' 1 KiB weight tiles
-// and their 64-byte scale tiles, all by direct loads.  Lane (m, g) of a block
-// reads A chunk g (E2M1) or chunks g and 4 + g (E4M3) of row m, the weight
-// unit (g, m) of its row group and the two scale bytes; the 16 lanes of every
-// 128-bit read cover 256 distinct bytes.
+// 64 x 128 output is 4 x 8 blocks.  Per stage (128 k) in LDS: A in the weight
+// tiles' order -- per 16-row group, [16-byte chunk][row][16 B] (4 chunks of
+// E2M1, 8 of E4M3) --, A scales (one dword per row: its four blocks), the row
+// groups' 1 KiB weight tiles and their 64-byte scale tiles, all by direct
+// loads.  Lane (m, g) of a block reads A chunk g (E2M1) or chunks g and 4 + g
+// (E4M3) of row m, the weight unit (g, m) of its row group and the two scale
+// bytes; the 16 lanes of every 128-bit read cover 256 contiguous bytes.
 namespace mx_gemm {
 constexpr int BKQ = 128;
-template <int AF> constexpr int a_row() { return AF == 4 ? 64 : 128; }
+template <int AF> constexpr int a_row() { return AF == 4 ? 64 : 128; }   // A bytes per row per stage
 template <int AF> constexpr int a_bytes() { return BM * a_row<AF>(); }
 constexpr int AS_BYTES = BM * 4;
 constexpr int W_BYTES = 16 * 1024;
@@ -1149,10 +1149,14 @@ __global__ __launch_bounds__(512, 1) void moe_large_mx_kernel(
     const int beg = offsets[e], n = offsets[e + 1] - beg;
     const int64_t c0 = (int64_t)nt * (GATEUP ? BN / 2 : BN);
     // rows of this lane's A loads (all lookups issued before the first use)
+    // A load q of wave w: 1 KiB = 16 rows x 4 chunks, row group (8q + w) (E2M1)
+    // or (8q + w) / 2 with chunks 4 ((8q + w) % 2) .. + 3 (E4M3); lane l:
+    // row 16 rg + l % 16, chunk l / 16 (+ 4 for the second half)
     int src[AQ + 1];
 #pragma unroll
     for (int q = 0; q < AQ; ++q) {
-      const int row = AF == 4 ? 16 * (8 * q + wave) + (lane >> 2) : 8 * (8 * q + wave) + (lane >> 3);
+      const int t = 8 * q + wave;
+      const int row = 16 * (AF == 4 ? t : t >> 1) + (lane & 15);
       const int slot = m0 + row;
       src[q] = GATEUP ? sorted[beg + (slot < n ? slot : n - 1)] : beg + slot;
     }
@@ -1162,8 +1166,9 @@ __global__ __launch_bounds__(512, 1) void moe_large_mx_kernel(
     }
 #pragma unroll
     for (int q = 0; q < AQ; ++q) {
-      const int row = AF == 4 ? 16 * (8 * q + wave) + (lane >> 2) : 8 * (8 * q + wave) + (lane >> 3);
-      const int ch = AF == 4 ? (lane & 3) ^ ((row >> 2) & 3) : (lane & 7) ^ ((row >> 1) & 7);
+      const int t = 8 * q + wave;
+      const int row = 16 * (AF == 4 ? t : t >> 1) + (lane & 15);
+      const int ch = (lane >> 4) + (AF == 4 ? 0 : 4 * (t & 1));
       const int64_t r = GATEUP ? src[q] / topk : src[q];
       a_off[q] = m0 + row < n ? (uint32_t)(r * arow_bytes + ch * 16) : aq_bytes;
     }
@@ -1217,12 +1222,9 @@ __global__ __launch_bounds__(512, 1) void moe_large_mx_kernel(
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int r = wm + 16 * i + fm;
-    if (AF == 4) {
-      aoff[i][0] = r * AROW + 16 * (fg ^ ((r >> 2) & 3));
-    } else {
-      aoff[i][0] = r * AROW + 16 * (fg ^ ((r >> 1) & 7));
-      aoff[i][AF == 4 ? 0 : 1] = r * AROW + 16 * ((4 + fg) ^ ((r >> 1) & 7));
-    }
+    const int rgb = (r >> 4) * 16 * AROW;  // this row group's A block
+    aoff[i][0] = rgb + (fg * 16 + fm) * 16;
+    if (AF != 4) aoff[i][AF == 4 ? 0 : 1] = rgb + ((4 + fg) * 16 + fm) * 16;
     asoff[i] = ABYTES + r * 4 + fg;
   }
 #pragma unroll
@@ -1271,15 +1273,23 @@ __global__ __launch_bounds__(512, 1) void moe_large_mx_kernel(
           }
           sa[i] = st[asoff[i]];
         }
+        // all of the step's weight reads are issued before the first MFMA, so
+        // their LDS latency is paid once per step, not once per column block
+        u32x4_t wv[8];
+        int sb[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          const u32x4_t w = *reinterpret_cast<const u32x4_t*>(st + boff[j]);
-          const i32x8_t b8 = i32x8_t{(int)w[0], (int)w[1], (int)w[2], (int)w[3], 0, 0, 0, 0};
-          const int sb = st[bsoff[j]];
+          wv[j] = *reinterpret_cast<const u32x4_t*>(st + boff[j]);
+          sb[j] = st[bsoff[j]];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const i32x8_t b8 = i32x8_t{(int)wv[j][0], (int)wv[j][1], (int)wv[j][2], (int)wv[j][3], 0, 0, 0, 0};
 #pragma unroll
           for (int i = 0; i < 4; ++i)
             acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a8[i], b8, acc[i][j], AF, 4, 0,
-                                                                         (int)sa[i], 0, sb);
+                                                                         (int)sa[i], 0, sb[j]);
         }
       }
       cslot = cslot == NST - 1 ? 0 : cslot + 1;
