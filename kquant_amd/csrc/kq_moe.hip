@@ -845,6 +845,26 @@ __global__ __launch_bounds__(512, 1) void moe_large_kernel(
     }
 }
 
+// Tile t of the grouped GEMMs -> (row-tile index mt, column tile nt).  The
+// row tiles of one expert are consecutive in the tile list, so its tiles
+// occupy the range [first * col_tiles, (first + cnt) * col_tiles); inside it
+// they are taken in blocks of nblk column tiles x all cnt row tiles, so the
+// ~32 workgroups of an XCD that run neighbouring tiles together share a few
+// activation row tiles and a few weight tiles in its L2 (instead of one row
+// tile against all of the expert's weight tiles).  A permutation within each
+// expert's range: results do not depend on it.
+__device__ __forceinline__ void grouped_tile(int t, int col_tiles, int nblk, const int* __restrict__ tiles,
+                                             const int* __restrict__ offsets, int& mt, int& nt) {
+  const int mt0 = t / col_tiles;
+  const int e = tiles[2 * mt0], m0 = tiles[2 * mt0 + 1];
+  const int first = mt0 - m0 / BM;
+  const int cnt = (offsets[e + 1] - offsets[e] + BM - 1) / BM;
+  const int u = t - first * col_tiles;
+  const int nb = u / (cnt * nblk), rem = u - nb * cnt * nblk;
+  mt = first + rem / nblk;
+  nt = nb * nblk + rem % nblk;
+}
+
 // ------------------------------------- grouped GEMM, direct-to-LDS loads --
 // Same tiles, waves, fragments and epilogues as moe_large_kernel, reorganised
 // around direct HBM -> LDS loads:
@@ -900,6 +920,7 @@ __global__ __launch_bounds__(512, 1) void moe_large_dma_kernel(
   const uint32_t b_bytes = (uint32_t)(rgs * nchunk * 1024), s_bytes = (uint32_t)(rgs * nchunk * 64);
   const int steps = (int)(K / BK);
   const uint32_t lds0 = dma::lds_offset_of(moe_dma_lds);
+  const int nblk = col_tiles % 8 == 0 ? 8 : col_tiles % 4 == 0 ? 4 : 1;
   const i32x4_t a_rsrc = dma::make_rsrc(a, a_bytes);
 
   // global row group of local group lrg (16 per tile) for column tile c0
@@ -920,7 +941,8 @@ __global__ __launch_bounds__(512, 1) void moe_large_dma_kernel(
       s_off = s_bytes;
       return;
     }
-    const int mt = lt / col_tiles, nt = lt - mt * col_tiles;
+    int mt, nt;
+    grouped_tile(lt, col_tiles, nblk, tiles, offsets, mt, nt);
     const int e = tiles[2 * mt], m0 = tiles[2 * mt + 1];
     const int beg = offsets[e], n = offsets[e + 1] - beg;
     const int64_t c0 = (int64_t)nt * (GATEUP ? BN / 2 : BN);
@@ -996,7 +1018,8 @@ __global__ __launch_bounds__(512, 1) void moe_large_dma_kernel(
   advance();
   int cslot = 0;
   for (int t = worker; t < total; t += G) {
-    const int mt = t / col_tiles, nt = t - mt * col_tiles;
+    int mt, nt;
+    grouped_tile(t, col_tiles, nblk, tiles, offsets, mt, nt);
     const int e = tiles[2 * mt], m0 = tiles[2 * mt + 1];
     const int beg = offsets[e], n = offsets[e + 1] - beg;
     const int64_t c0 = (int64_t)nt * (GATEUP ? BN / 2 : BN);
@@ -1124,6 +1147,7 @@ __global__ __launch_bounds__(512, 1) void moe_large_mx_kernel(
   const uint32_t b_bytes = (uint32_t)(rgs * nchunk * 1024), s_bytes = (uint32_t)(rgs * nchunk * 64);
   const int steps = (int)(K / BKQ);
   const uint32_t lds0 = dma::lds_offset_of(moe_mx_lds);
+  const int nblk = col_tiles % 8 == 0 ? 8 : col_tiles % 4 == 0 ? 4 : 1;
   const i32x4_t a_rsrc = dma::make_rsrc(aq, aq_bytes);
   const i32x4_t as_rsrc = dma::make_rsrc(as, as_bytes);
   auto grow_group = [&](int64_t c0, int lrg) -> int64_t {
@@ -1144,7 +1168,8 @@ __global__ __launch_bounds__(512, 1) void moe_large_mx_kernel(
       bs_off = s_bytes;
       return;
     }
-    const int mt = lt / col_tiles, nt = lt - mt * col_tiles;
+    int mt, nt;
+    grouped_tile(lt, col_tiles, nblk, tiles, offsets, mt, nt);
     const int e = tiles[2 * mt], m0 = tiles[2 * mt + 1];
     const int beg = offsets[e], n = offsets[e + 1] - beg;
     const int64_t c0 = (int64_t)nt * (GATEUP ? BN / 2 : BN);
@@ -1242,7 +1267,8 @@ __global__ __launch_bounds__(512, 1) void moe_large_mx_kernel(
   }
   int cslot = 0;
   for (int t = worker; t < total; t += G) {
-    const int mt = t / col_tiles, nt = t - mt * col_tiles;
+    int mt, nt;
+    grouped_tile(t, col_tiles, nblk, tiles, offsets, mt, nt);
     const int e = tiles[2 * mt], m0 = tiles[2 * mt + 1];
     const int beg = offsets[e], n = offsets[e + 1] - beg;
     const int64_t c0 = (int64_t)nt * (GATEUP ? BN / 2 : BN);
