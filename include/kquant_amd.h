@@ -97,7 +97,8 @@ int kq_mx_dequant(int fmt, const void* q, const uint8_t* scale, int64_t rows,
  * [64 c + 16 (l/16) + j], and 64-byte scale tiles with byte l =
  * scale[16 rg + l%16][4 c + l/16].  A one-time weight preparation (the role
  * of the external kernel's prepare_weights in scripts/closure_exl3_layer.py:
- * 412-443); same bytes, permuted.  rows % 16 == 0, k % 128 == 0. */
+ * 412-443); same bytes, permuted.  rows % 16 == 0, k % 128 == 0.  scale and
+ * scale_tiled may both be NULL (packed bytes only, for X4T-coded scales). */
 int kq_mx_tile_weights(const uint8_t* q, const uint8_t* scale, int64_t mats, int64_t rows,
                        int64_t k, uint8_t* q_tiled, uint8_t* scale_tiled, void* stream);
 
@@ -149,6 +150,39 @@ int kq_moe_forward(int activation, float act_beta, float act_linear_beta,
                    const uint8_t* w13_st, const uint8_t* w2_t, const uint8_t* w2_st,
                    int out_dtype, void* out, void* workspace, int64_t workspace_bytes,
                    uint32_t flags, void* stream);
+
+/* Workspace bytes kq_moe_forward_x4t needs (-1 on bad sizes): the
+ * kq_moe_forward workspace plus one w13 and one w2 scale slot per routed
+ * expert, min(tokens * topk, experts) of each. */
+int64_t kq_moe_x4t_workspace_size(int64_t tokens, int topk, int experts, int64_t hidden,
+                                  int64_t inter);
+
+/* kq_moe_forward with the expert scales kept X4T-compressed in device memory
+ * (kquant/x4t.py's per-expert w1 / w3 / w2 scale planes: fixed streams of
+ * `experts` stacked matrices, their exception streams, and per-16-row-tile
+ * exception indexes from kq_x4t_tile_index).  The X4T runtime refinement of
+ * docs/qsrt-technical-brief.md:446-474: after routing, one launch expands
+ * only the routed experts' scales - w1 and w3 into the gate and up rows of
+ * the gate-first w13 - into workspace slots in the kq_mx_tile_weights scale
+ * layout, and the GEMMs read them there; no allocation, host work or
+ * exception search per call.  w13_t / w2_t as for kq_moe_forward.  w1 / w3
+ * planes are [inter, hidden / 32], w2 planes [hidden, inter / 32]; hidden
+ * and inter at most 8160.  The components must be a valid X4T encoding (as
+ * kq_x4t_decode accepts): the expansion does not validate them; with tile
+ * indexes that kq_x4t_tile_index made from the same exception streams it
+ * accesses no memory outside the buffers described here, whatever they hold.  Same
+ * flags and same results, bit for bit, as kq_moe_forward over the decoded
+ * scales.  workspace: >= kq_moe_x4t_workspace_size bytes. */
+int kq_moe_forward_x4t(int activation, float act_beta, float act_linear_beta,
+                       const void* x, int64_t ldx, int64_t tokens, int64_t hidden,
+                       const int32_t* route_ids, const float* route_weights, int topk,
+                       int experts, int64_t inter, const uint8_t* w13_t, const uint8_t* w2_t,
+                       const uint8_t* w1_fixed, const uint32_t* w1_exceptions,
+                       const uint32_t* w1_tile_index, const uint8_t* w3_fixed,
+                       const uint32_t* w3_exceptions, const uint32_t* w3_tile_index,
+                       const uint8_t* w2_fixed, const uint32_t* w2_exceptions,
+                       const uint32_t* w2_tile_index, int out_dtype, void* out,
+                       void* workspace, int64_t workspace_bytes, uint32_t flags, void* stream);
 
 /* --------------------------------------------------------- dense linear -- */
 
@@ -282,6 +316,18 @@ int kq_x4t_emit_exceptions(const uint8_t* scale, int64_t mats, int64_t rows, int
 int kq_x4t_decode(const uint8_t* fixed, const uint32_t* exceptions, int64_t n_exceptions,
                   const int64_t* exception_offsets, int64_t mats, int64_t rows, int64_t cols,
                   uint8_t* out, uint32_t* status, void* stream);
+
+/* Per-tile exception index of `mats` stacked X4T matrices [rows, cols]:
+ * index[m * rows/16 + t] = the first entry of matrix m's exception range
+ * (exception_offsets[m] .. exception_offsets[m + 1], or all n_exceptions when
+ * exception_offsets is NULL and mats == 1) whose position lies at or past
+ * tile t's first position; index[mats * rows/16] = n_exceptions.  The same
+ * numbers kq_x4t_analyze's tile_offsets hold, recovered from the streams
+ * alone (kquant/x4t.py's container keeps only per-matrix offsets,
+ * x4t.py:594-602).  One-time preparation for kq_moe_forward_x4t. */
+int kq_x4t_tile_index(const uint32_t* exceptions, int64_t n_exceptions,
+                      const int64_t* exception_offsets, int64_t mats, int64_t rows, int64_t cols,
+                      uint32_t* index, void* stream);
 
 /* KQSC row-palette payload, version 1 (kquant/mxfp4_scale_codec.py:27-85,
  * pack_scale_plane) or 2 (:205-292, pack_scale_plane_compact), tile_rows in

@@ -66,6 +66,10 @@ SIGNATURES: dict[str, list] = {
     "kq_x4t_analyze": [_VP, _I64, _I64, _I64, _VP, _VP, _VP],
     "kq_x4t_emit_exceptions": [_VP, _I64, _I64, _I64, _VP, _VP, _VP, _VP],
     "kq_x4t_decode": [_VP, _VP, _I64, _VP, _I64, _I64, _I64, _VP, _VP, _VP],
+    "kq_x4t_tile_index": [_VP, _I64, _VP, _I64, _I64, _I64, _VP, _VP],
+    "kq_moe_forward_x4t": [_INT, _F32, _F32, _VP, _I64, _I64, _I64, _VP, _VP, _INT, _INT, _I64,
+                           _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _INT, _VP, _VP,
+                           _I64, _U32, _VP],
     "kq_kqsc_measure": [_INT, _VP, _I64, _I64, _INT, _VP, _VP, _VP],
     "kq_kqsc_emit": [_INT, _VP, _I64, _I64, _INT, _VP, _VP, _VP, _VP],
     "kq_kqsc_decode": [_INT, _VP, _I64, _I64, _I64, _INT, _VP, _VP, _VP],
@@ -114,6 +118,8 @@ def library() -> ctypes.CDLL:
         lib.kq_last_error.argtypes = []
         lib.kq_moe_workspace_size.restype = ctypes.c_int64
         lib.kq_moe_workspace_size.argtypes = [_I64, _INT, _INT, _I64, _I64]
+        lib.kq_moe_x4t_workspace_size.restype = ctypes.c_int64
+        lib.kq_moe_x4t_workspace_size.argtypes = [_I64, _INT, _INT, _I64, _I64]
         lib.kq_mx_linear_f32_workspace_size.restype = ctypes.c_int64
         lib.kq_mx_linear_f32_workspace_size.argtypes = [_I64, _I64]
         lib.kq_route_sort_workspace_size.restype = ctypes.c_int64

@@ -337,7 +337,7 @@ __global__ __launch_bounds__(256) void mx_tile_kernel(const uint8_t* __restrict_
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
   *reinterpret_cast<u32x4*>(qt + 16 * t) =
       *reinterpret_cast<const u32x4*>(q + row * (k / 2) + 64 * c + 16 * g);
-  st[t] = s[row * (k / 32) + 4 * c + g];
+  if (st) st[t] = s[row * (k / 32) + 4 * c + g];
 }
 
 }  // namespace kq
@@ -477,13 +477,16 @@ extern "C" int kq_mx_tile_weights(const uint8_t* q, const uint8_t* scale, int64_
                    (long long)rows, (long long)k);
   if (kq_misaligned(q, 16) || kq_misaligned(q_tiled, 16))
     return kq_fail(KQ_ERR_INVALID, "kq_mx_tile_weights: packed buffers must be 16-byte aligned");
+  if (!scale != !scale_tiled)
+    return kq_fail(KQ_ERR_INVALID, "kq_mx_tile_weights: scale and scale_tiled must both be given or both NULL");
   const int64_t per = rows / 16 * (k / 128) * 64;  // lane slots per matrix
   if (per == 0 || mats == 0) return KQ_OK;
   hipStream_t st = (hipStream_t)stream;
   const unsigned grid = (unsigned)((per + 255) / 256);
   for (int64_t m = 0; m < mats; ++m) {
-    mx_tile_kernel<<<grid, 256, 0, st>>>(q + m * rows * (k / 2), scale + m * rows * (k / 32), rows, k,
-                                         q_tiled + m * per * 16, scale_tiled + m * per);
+    mx_tile_kernel<<<grid, 256, 0, st>>>(q + m * rows * (k / 2), scale ? scale + m * rows * (k / 32) : nullptr,
+                                         rows, k, q_tiled + m * per * 16,
+                                         scale_tiled ? scale_tiled + m * per : nullptr);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return kq_check_launch(e, "kq_mx_tile_weights");
   }

@@ -42,15 +42,19 @@ constexpr int STAGE = A_BYTES + B_BYTES + S_BYTES;
 
 struct Layout {
   size_t counts, offsets, block_counts, sorted, small_list, large_tiles, meta, act, y;
-  size_t xq, xs, aq, as, total;  // MX-quantized tokens / intermediates (activation-quantized modes)
-  int64_t pairs, nblk, max_small, max_large, max_list;
+  size_t xq, xs, aq, as;  // MX-quantized tokens / intermediates (activation-quantized modes)
+  size_t rank_of, routed, s13, s2;  // routed-expert ranks and expanded scale slots (X4T scales)
+  size_t total;
+  int64_t pairs, nblk, max_small, max_large, max_list, max_routed;
 };
 
 static inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
-static Layout make_layout(int64_t tokens, int topk, int experts, int64_t hidden, int64_t inter) {
+static Layout make_layout(int64_t tokens, int topk, int experts, int64_t hidden, int64_t inter,
+                          bool x4t = false) {
   Layout L;
   L.pairs = tokens * topk;
+  L.max_routed = L.pairs < experts ? L.pairs : experts;
   L.nblk = (L.pairs + PREP - 1) / PREP;
   L.max_small = L.pairs < experts ? L.pairs : experts;
   L.max_large = L.pairs / (SMALL_MAX + 1) + L.pairs / BM + 1;
@@ -72,6 +76,13 @@ static Layout make_layout(int64_t tokens, int topk, int experts, int64_t hidden,
   L.xs = o;           o = align256(o + (size_t)tokens * hidden / 32);
   L.aq = o;           o = align256(o + (size_t)L.pairs * inter);
   L.as = o;           o = align256(o + (size_t)L.pairs * inter / 32);
+  L.rank_of = L.routed = L.s13 = L.s2 = o;
+  if (x4t) {  // one scale slot per routed expert: w13 [2I, H/32] and w2 [H, I/32] scale tiles
+    L.rank_of = o;    o = align256(o + sizeof(int) * experts);
+    L.routed = o;     o = align256(o + sizeof(int) * (size_t)L.max_routed);
+    L.s13 = o;        o = align256(o + (size_t)L.max_routed * 2 * inter * (hidden / 32));
+    L.s2 = o;         o = align256(o + (size_t)L.max_routed * hidden * (inter / 32));
+  }
   L.total = o;
   return L;
 }
@@ -125,10 +136,42 @@ __device__ int block_exclusive_scan(int* v, int n, int* scratch /*[1024]*/) {
   return total;
 }
 
+// Ranks of the routed experts (count > 0) in ascending expert order, for the
+// per-call expansion of compressed scales: rank_of[e] for every routed e,
+// routed[r] = the expert of rank r, -1 for r in [routed experts, max_routed).
+// Called by all 1024 threads after counts[0, experts) are written; tmp is an
+// LDS array of `experts` ints that is overwritten and then rebuilt.
+__device__ void routed_ranks(const int* counts, int experts, int* rank_of, int* routed, int max_routed,
+                             int* tmp, int* scratch) {
+  int keep[4];
+  for (int i = 0; i < 4; ++i) {
+    const int e = threadIdx.x + 1024 * i;
+    keep[i] = e < experts ? tmp[e] : 0;
+    if (e < experts) tmp[e] = counts[e] > 0 ? 1 : 0;
+  }
+  __syncthreads();
+  const int nrouted = block_exclusive_scan(tmp, experts, scratch);
+  for (int i = 0; i < 4; ++i) {
+    const int e = threadIdx.x + 1024 * i;
+    if (e < experts && counts[e] > 0) {
+      rank_of[e] = tmp[e];
+      if (tmp[e] < max_routed) routed[tmp[e]] = e;
+    }
+  }
+  for (int r = nrouted + (int)threadIdx.x; r < max_routed; r += 1024) routed[r] = -1;
+  __syncthreads();
+  for (int i = 0; i < 4; ++i) {
+    const int e = threadIdx.x + 1024 * i;
+    if (e < experts) tmp[e] = keep[i];
+  }
+  __syncthreads();
+}
+
 __global__ __launch_bounds__(1024) void route_scan_kernel(
     int* __restrict__ block_counts, int nblk, int experts, int* __restrict__ counts,
     int* __restrict__ offsets, int* __restrict__ small_list, int* __restrict__ large_tiles,
-    int* __restrict__ meta, int max_large) {
+    int* __restrict__ meta, int max_large, int* __restrict__ rank_of, int* __restrict__ routed,
+    int max_routed) {
   __shared__ int s_cnt[MAX_EXPERTS];
   __shared__ int s_small[MAX_EXPERTS];
   __shared__ int s_tiles[MAX_EXPERTS];
@@ -154,6 +197,7 @@ __global__ __launch_bounds__(1024) void route_scan_kernel(
     s_tiles[e] = s > SMALL_MAX ? (s + BM - 1) / BM : 0;
   }
   __syncthreads();
+  if (rank_of) routed_ranks(counts, experts, rank_of, routed, max_routed, s_small, scratch);
   const int npairs = block_exclusive_scan(s_cnt, experts, scratch);
   const int nsmall = block_exclusive_scan(s_small, experts, scratch);
   const int ntiles = block_exclusive_scan(s_tiles, experts, scratch);
@@ -207,7 +251,8 @@ constexpr int PREP_ONE = 1024;
 __global__ __launch_bounds__(1024) void route_prep_one_kernel(
     const int* __restrict__ ids, int pairs, int experts, int* __restrict__ counts,
     int* __restrict__ offsets, int* __restrict__ sorted, int* __restrict__ small_list,
-    int* __restrict__ large_tiles, int* __restrict__ meta, int max_large) {
+    int* __restrict__ large_tiles, int* __restrict__ meta, int max_large, int* __restrict__ rank_of,
+    int* __restrict__ routed, int max_routed) {
   __shared__ int s_cnt[MAX_EXPERTS];
   __shared__ int s_small[MAX_EXPERTS];
   __shared__ int s_tiles[MAX_EXPERTS];
@@ -231,6 +276,7 @@ __global__ __launch_bounds__(1024) void route_prep_one_kernel(
     s_tiles[e] = c > SMALL_MAX ? (c + BM - 1) / BM : 0;
   }
   __syncthreads();
+  if (rank_of) routed_ranks(counts, experts, rank_of, routed, max_routed, s_small, scratch);
   const int npairs = block_exclusive_scan(s_cnt, experts, scratch);
   const int nsmall = block_exclusive_scan(s_small, experts, scratch);
   const int ntiles = block_exclusive_scan(s_tiles, experts, scratch);
@@ -273,7 +319,8 @@ __global__ __launch_bounds__(1024) void route_prep_one_kernel(
 // (expert, first sorted position, count <= 16), one per 16 of its pairs.
 __global__ __launch_bounds__(DECODE_MAX_PAIRS) void route_decode_kernel(
     const int* __restrict__ ids, int pairs, int experts, int* __restrict__ sorted,
-    int* __restrict__ small_list, int max_list, int* __restrict__ meta) {
+    int* __restrict__ small_list, int max_list, int* __restrict__ meta, int* __restrict__ rank_of,
+    int* __restrict__ routed, int max_routed) {
   // ids past `pairs` are -1 and the loops run over whole groups of four
   // (one 16-byte LDS read each), so no read waits on the previous one
   __shared__ __attribute__((aligned(16))) int s_id[DECODE_MAX_PAIRS];
@@ -303,7 +350,7 @@ __global__ __launch_bounds__(DECODE_MAX_PAIRS) void route_decode_kernel(
   s_first[t] = first ? my : -1;
   s_nent[t] = first ? nent : 0;
   __syncthreads();
-  int e0 = 0, nlist = 0;
+  int e0 = 0, nlist = 0, r0 = 0, nrouted = 0;
 #pragma unroll 4
   for (int j4 = 0; j4 < pairs4; j4 += 4) {
     const i32x4 v4 = *reinterpret_cast<const i32x4*>(s_first + j4);
@@ -312,7 +359,16 @@ __global__ __launch_bounds__(DECODE_MAX_PAIRS) void route_decode_kernel(
     for (int i = 0; i < 4; ++i) {
       nlist += n4[i];
       e0 += (v4[i] >= 0 && v4[i] < my) ? n4[i] : 0;
+      r0 += (v4[i] >= 0 && v4[i] < my) ? 1 : 0;
+      nrouted += v4[i] >= 0 ? 1 : 0;
     }
+  }
+  if (rank_of) {  // routed-expert ranks (see routed_ranks)
+    if (first) {
+      rank_of[my] = r0;
+      if (r0 < max_routed) routed[r0] = my;
+    }
+    for (int r = nrouted + t; r < max_routed; r += DECODE_MAX_PAIRS) routed[r] = -1;
   }
   if (my >= 0) sorted[below + rank] = t;
   if (first) {
@@ -358,8 +414,8 @@ template <bool GATEUP, int NBP, int S, int RW, int P, int STEPS>
 __global__ __launch_bounds__(S * RW * 64) void moe_small_kernel(
     const uint16_t* __restrict__ a, int64_t lda, int topk, const int* __restrict__ sorted,
     const int* __restrict__ small_list, const uint8_t* __restrict__ wt,
-    const uint8_t* __restrict__ wst, int64_t rows_per_expert, int64_t K, int64_t inter,
-    ActParams act, const float* __restrict__ route_w, uint16_t* __restrict__ act_out,
+    const uint8_t* __restrict__ wst, const int* __restrict__ sslot, int64_t rows_per_expert, int64_t K,
+    int64_t inter, ActParams act, const float* __restrict__ route_w, uint16_t* __restrict__ act_out,
     float* __restrict__ y_out, int64_t hidden) {
   constexpr int NB = GATEUP ? 2 * NBP : NBP;      // 16-row blocks per wave
   constexpr int CH = RW * 16 * NBP;               // channels per workgroup
@@ -368,6 +424,7 @@ __global__ __launch_bounds__(S * RW * 64) void moe_small_kernel(
   if (e < 0) return;
   const int beg = small_list[3 * blockIdx.x + 1];
   const int n = small_list[3 * blockIdx.x + 2];
+  const int se = sslot ? sslot[e] : e;            // scale slot of the expert
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int kpart = wave % S, rgw = wave / S;
   const int m = lane & 15, g = lane >> 4;
@@ -385,7 +442,7 @@ __global__ __launch_bounds__(S * RW * 64) void moe_small_kernel(
     const int64_t rg = GATEUP ? (b < NBP ? c0 / 16 + b : inter / 16 + c0 / 16 + (b - NBP)) : c0 / 16 + b;
     const int64_t t0 = ((int64_t)e * rgs + rg) * nchunk + c_first;
     wtile[b] = wt + t0 * 1024 + 16 * lane;
-    stile[b] = wst + t0 * 64 + lane;
+    stile[b] = wst + (((int64_t)se * rgs + rg) * nchunk + c_first) * 64 + lane;
   }
   struct WBuf {
     u32x4_t w[NB];
@@ -526,8 +583,8 @@ template <bool GATEUP, int AF, int NBP, int S, int RW, int P, int STEPS>
 __global__ __launch_bounds__(S * RW * 64) void moe_small_mx_kernel(
     const uint8_t* __restrict__ aq, const uint8_t* __restrict__ as, int topk,
     const int* __restrict__ sorted, const int* __restrict__ small_list,
-    const uint8_t* __restrict__ wt, const uint8_t* __restrict__ wst, int64_t rows_per_expert,
-    int64_t K, int64_t inter, ActParams act, const float* __restrict__ route_w,
+    const uint8_t* __restrict__ wt, const uint8_t* __restrict__ wst, const int* __restrict__ sslot,
+    int64_t rows_per_expert, int64_t K, int64_t inter, ActParams act, const float* __restrict__ route_w,
     uint16_t* __restrict__ act_out, float* __restrict__ y_out, int64_t hidden) {
   constexpr int NB = GATEUP ? 2 * NBP : NBP;
   constexpr int CH = RW * 16 * NBP;
@@ -537,6 +594,7 @@ __global__ __launch_bounds__(S * RW * 64) void moe_small_mx_kernel(
   if (e < 0) return;
   const int beg = small_list[3 * blockIdx.x + 1];
   const int n = small_list[3 * blockIdx.x + 2];
+  const int se = sslot ? sslot[e] : e;            // scale slot of the expert
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int kpart = wave % S, rgw = wave / S;
   const int m = lane & 15, g = lane >> 4;
@@ -552,7 +610,7 @@ __global__ __launch_bounds__(S * RW * 64) void moe_small_mx_kernel(
     const int64_t rg = GATEUP ? (b < NBP ? c0 / 16 + b : inter / 16 + c0 / 16 + (b - NBP)) : c0 / 16 + b;
     const int64_t t0 = ((int64_t)e * rgs + rg) * nchunk + c_first;
     wtile[b] = wt + t0 * 1024 + 16 * lane;
-    stile[b] = wst + t0 * 64 + lane;
+    stile[b] = wst + (((int64_t)se * rgs + rg) * nchunk + c_first) * 64 + lane;
   }
   struct WBuf {
     u32x4_t w[NB];
@@ -687,12 +745,13 @@ template <bool GATEUP>
 __global__ __launch_bounds__(512, 1) void moe_large_kernel(
     const uint16_t* __restrict__ a, int64_t lda, int topk, const int* __restrict__ offsets,
     const int* __restrict__ sorted, const int* __restrict__ tiles, const int* __restrict__ meta,
-    const uint8_t* __restrict__ wt, const uint8_t* __restrict__ wst, int64_t rows_per_expert,
-    int64_t K, int64_t inter, ActParams act, const float* __restrict__ route_w,
+    const uint8_t* __restrict__ wt, const uint8_t* __restrict__ wst, const int* __restrict__ sslot,
+    int64_t rows_per_expert, int64_t K, int64_t inter, ActParams act, const float* __restrict__ route_w,
     uint16_t* __restrict__ act_out, float* __restrict__ y_out, int64_t hidden) {
   const int ti = blockIdx.x;
   if (ti >= meta[1]) return;
   const int e = tiles[2 * ti], m0 = tiles[2 * ti + 1];
+  const int se = sslot ? sslot[e] : e;  // scale slot of the expert
   const int beg = offsets[e];
   const int n = offsets[e + 1] - beg;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -741,7 +800,7 @@ __global__ __launch_bounds__(512, 1) void moe_large_kernel(
       const int lrg = tid >> 4, q = tid & 15, l = h * 32 + 2 * q;
       const int64_t rg = grow_group(lrg);
       rs = 16 * rg < nrows
-               ? *reinterpret_cast<const uint16_t*>(wst + (((int64_t)e * rgs + rg) * nchunk + chunk) * 64 + l)
+               ? *reinterpret_cast<const uint16_t*>(wst + (((int64_t)se * rgs + rg) * nchunk + chunk) * 64 + l)
                : 0u;
     }
   };
@@ -904,9 +963,9 @@ __global__ __launch_bounds__(512, 1) void moe_large_dma_kernel(
     const uint16_t* __restrict__ a, int64_t lda, uint32_t a_bytes, int topk,
     const int* __restrict__ offsets, const int* __restrict__ sorted, const int* __restrict__ tiles,
     const int* __restrict__ meta, const uint8_t* __restrict__ wt, const uint8_t* __restrict__ wst,
-    int64_t rows_per_expert, int64_t K, int64_t inter, int col_tiles, ActParams act,
-    const float* __restrict__ route_w, uint16_t* __restrict__ act_out, float* __restrict__ y_out,
-    int64_t hidden) {
+    const int* __restrict__ sslot, int64_t rows_per_expert, int64_t K, int64_t inter, int col_tiles,
+    ActParams act, const float* __restrict__ route_w, uint16_t* __restrict__ act_out,
+    float* __restrict__ y_out, int64_t hidden) {
   using namespace dma_gemm;
   using dma::i32x4_t;
   const int G = gridDim.x;
@@ -961,7 +1020,7 @@ __global__ __launch_bounds__(512, 1) void moe_large_dma_kernel(
       a_off[q] = m0 + row < n ? (uint32_t)(r * lda * 2 + c * 16) : a_bytes;
     }
     b_rsrc = dma::make_rsrc(wt + (int64_t)e * rgs * nchunk * 1024, b_bytes);
-    s_rsrc = dma::make_rsrc(wst + (int64_t)e * rgs * nchunk * 64, s_bytes);
+    s_rsrc = dma::make_rsrc(wst + (int64_t)(sslot ? sslot[e] : e) * rgs * nchunk * 64, s_bytes);
     {
       const int64_t rg = grow_group(c0, 2 * wave + (lane >> 5));
       b_off = 16 * rg < nrows ? (uint32_t)(rg * nchunk * 1024 + (lane & 31) * 16) : b_bytes;
@@ -1127,9 +1186,9 @@ __global__ __launch_bounds__(512, 1) void moe_large_mx_kernel(
     const uint8_t* __restrict__ aq, const uint8_t* __restrict__ as, uint32_t aq_bytes,
     uint32_t as_bytes, int topk, const int* __restrict__ offsets, const int* __restrict__ sorted,
     const int* __restrict__ tiles, const int* __restrict__ meta, const uint8_t* __restrict__ wt,
-    const uint8_t* __restrict__ wst, int64_t rows_per_expert, int64_t K, int64_t inter,
-    int col_tiles, ActParams act, const float* __restrict__ route_w, uint16_t* __restrict__ act_out,
-    float* __restrict__ y_out, int64_t hidden) {
+    const uint8_t* __restrict__ wst, const int* __restrict__ sslot, int64_t rows_per_expert, int64_t K,
+    int64_t inter, int col_tiles, ActParams act, const float* __restrict__ route_w,
+    uint16_t* __restrict__ act_out, float* __restrict__ y_out, int64_t hidden) {
   using namespace mx_gemm;
   using dma::i32x4_t;
   constexpr int AROW = a_row<AF>(), ABYTES = a_bytes<AF>(), STAGE = stage<AF>();
@@ -1203,7 +1262,7 @@ __global__ __launch_bounds__(512, 1) void moe_large_mx_kernel(
       as_off = m0 + row < n ? (uint32_t)(r * asrow) : as_bytes;
     }
     b_rsrc = dma::make_rsrc(wt + (int64_t)e * rgs * nchunk * 1024, b_bytes);
-    s_rsrc = dma::make_rsrc(wst + (int64_t)e * rgs * nchunk * 64, s_bytes);
+    s_rsrc = dma::make_rsrc(wst + (int64_t)(sslot ? sslot[e] : e) * rgs * nchunk * 64, s_bytes);
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
       const int64_t rg = grow_group(c0, 2 * wave + q);
@@ -1464,8 +1523,8 @@ template <int AF>
 static int moe_forward_mx(const Layout& L, unsigned char* w, const ActParams& ap, const void* x,
                           int64_t ldx, int64_t tokens, int64_t hidden, const float* route_weights,
                           int topk, int64_t inter, const uint8_t* w13_t, const uint8_t* w13_st,
-                          const uint8_t* w2_t, const uint8_t* w2_st, bool decode, int grid_dma,
-                          void* stream) {
+                          const uint8_t* w2_t, const uint8_t* w2_st, const int* sslot, bool decode,
+                          int grid_dma, void* stream) {
   hipStream_t st = (hipStream_t)stream;
   const int fmt = AF == 4 ? KQ_FMT_MXFP4_E2M1 : KQ_FMT_MXFP8_E4M3;
   const int* offsets = (const int*)(w + L.offsets);
@@ -1482,13 +1541,13 @@ static int moe_forward_mx(const Layout& L, unsigned char* w, const ActParams& ap
   if (rc != KQ_OK) return rc;
   e = launch_small_mx<true, AF, KQ_GU_NBP, KQ_GU_S, KQ_GU_RW, KQ_GU_P>(
       L.max_list, inter, hidden, st, (const uint8_t*)xq, (const uint8_t*)xs, topk, sorted, small_list,
-      w13_t, w13_st, 2 * inter, hidden, inter, ap, route_weights, act, y, hidden);
+      w13_t, w13_st, sslot, 2 * inter, hidden, inter, ap, route_weights, act, y, hidden);
   if (e != hipSuccess) return kq_check_launch(e, "kq_moe_forward/gateup_small");
   const int64_t abytes = AF == 4 ? hidden / 2 : hidden;
   if (any_large) {
     moe_large_mx_kernel<true, AF><<<grid_dma, THREADS, 0, st>>>(
         xq, xs, (uint32_t)(tokens * abytes), (uint32_t)(tokens * hidden / 32), topk, offsets, sorted,
-        large_tiles, meta, w13_t, w13_st, 2 * inter, hidden, inter, (int)(inter / (BN / 2)), ap,
+        large_tiles, meta, w13_t, w13_st, sslot, 2 * inter, hidden, inter, (int)(inter / (BN / 2)), ap,
         route_weights, act, y, hidden);
     if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_moe_forward/gateup_large");
   }
@@ -1496,13 +1555,13 @@ static int moe_forward_mx(const Layout& L, unsigned char* w, const ActParams& ap
   if (rc != KQ_OK) return rc;
   e = launch_small_mx<false, AF, KQ_DN_NBP, KQ_DN_S, KQ_DN_RW, KQ_DN_P>(
       L.max_list, hidden, inter, st, (const uint8_t*)aq, (const uint8_t*)as, topk, sorted, small_list,
-      w2_t, w2_st, hidden, inter, inter, ap, route_weights, act, y, hidden);
+      w2_t, w2_st, sslot, hidden, inter, inter, ap, route_weights, act, y, hidden);
   if (e != hipSuccess) return kq_check_launch(e, "kq_moe_forward/down_small");
   if (any_large) {
     const int64_t ibytes = AF == 4 ? inter / 2 : inter;
     moe_large_mx_kernel<false, AF><<<grid_dma, THREADS, 0, st>>>(
         aq, as, (uint32_t)(L.pairs * ibytes), (uint32_t)(L.pairs * inter / 32), topk, offsets, sorted,
-        large_tiles, meta, w2_t, w2_st, hidden, inter, inter, (int)(hidden / BN), ap, route_weights, act,
+        large_tiles, meta, w2_t, w2_st, sslot, hidden, inter, inter, (int)(hidden / BN), ap, route_weights, act,
         y, hidden);
     if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_moe_forward/down_large");
   }
@@ -1515,43 +1574,46 @@ extern "C" int64_t kq_moe_workspace_size(int64_t tokens, int topk, int experts, 
   return (int64_t)make_layout(tokens, topk, experts, hidden, inter).total;
 }
 
-extern "C" int kq_moe_forward(int activation, float act_beta, float act_linear_beta,
-                              const void* x, int64_t ldx, int64_t tokens, int64_t hidden,
-                              const int32_t* route_ids, const float* route_weights, int topk,
-                              int experts, int64_t inter, const uint8_t* w13_t,
-                              const uint8_t* w13_st, const uint8_t* w2_t,
-                              const uint8_t* w2_st, int out_dtype, void* out,
-                              void* workspace, int64_t workspace_bytes, uint32_t flags,
-                              void* stream) {
+// The forward behind both entry points.  With xa non-null the scales come
+// from X4T planes: the routing also ranks the routed experts, one launch
+// expands their scales into workspace slots (xa's output fields are filled
+// here) and the GEMMs read each expert's scales from its slot.
+static int moe_forward_impl(const char* fn, int activation, float act_beta, float act_linear_beta,
+                            const void* x, int64_t ldx, int64_t tokens, int64_t hidden,
+                            const int32_t* route_ids, const float* route_weights, int topk, int experts,
+                            int64_t inter, const uint8_t* w13_t, const uint8_t* w13_st,
+                            const uint8_t* w2_t, const uint8_t* w2_st, X4TExpandArgs* xa, int out_dtype,
+                            void* out, void* workspace, int64_t workspace_bytes, uint32_t flags,
+                            void* stream) {
   if (flags & ~(uint32_t)(KQ_MOE_REGISTER_STAGED | KQ_MOE_ACT_MXFP8 | KQ_MOE_ACT_MXFP4))
-    return kq_fail(KQ_ERR_INVALID, "kq_moe_forward: unknown flags 0x%x", flags);
+    return kq_fail(KQ_ERR_INVALID, "%s: unknown flags 0x%x", fn, flags);
   const int act_fmt = (flags & KQ_MOE_ACT_MXFP4) ? 4 : (flags & KQ_MOE_ACT_MXFP8) ? 0 : -1;
   if ((flags & KQ_MOE_ACT_MXFP4) && (flags & KQ_MOE_ACT_MXFP8))
-    return kq_fail(KQ_ERR_INVALID, "kq_moe_forward: KQ_MOE_ACT_MXFP8 and KQ_MOE_ACT_MXFP4 exclude each other");
+    return kq_fail(KQ_ERR_INVALID, "%s: KQ_MOE_ACT_MXFP8 and KQ_MOE_ACT_MXFP4 exclude each other", fn);
   if (act_fmt >= 0 && (flags & KQ_MOE_REGISTER_STAGED))
-    return kq_fail(KQ_ERR_INVALID, "kq_moe_forward: the activation-quantized modes have no register-staged kernel");
+    return kq_fail(KQ_ERR_INVALID, "%s: the activation-quantized modes have no register-staged kernel", fn);
   if (activation != KQ_ACT_SITU && activation != KQ_ACT_SWIGLU)
-    return kq_fail(KQ_ERR_INVALID, "kq_moe_forward: unknown activation %d", activation);
+    return kq_fail(KQ_ERR_INVALID, "%s: unknown activation %d", fn, activation);
   if (out_dtype != KQ_DT_BF16 && out_dtype != KQ_DT_F32)
-    return kq_fail(KQ_ERR_INVALID, "kq_moe_forward: output dtype must be bf16 or f32");
+    return kq_fail(KQ_ERR_INVALID, "%s: output dtype must be bf16 or f32", fn);
   if (tokens < 0 || topk <= 0 || topk > 64 || experts <= 0 || experts > MAX_EXPERTS)
-    return kq_fail(KQ_ERR_INVALID, "kq_moe_forward: need tokens >= 0, 1 <= topk <= 64, 1 <= experts <= %d",
+    return kq_fail(KQ_ERR_INVALID, "%s: need tokens >= 0, 1 <= topk <= 64, 1 <= experts <= %d", fn,
                    MAX_EXPERTS);
   if (hidden <= 0 || inter <= 0 || hidden % 512 != 0 || inter % 512 != 0)
     return kq_fail(KQ_ERR_INVALID,
-                   "kq_moe_forward: hidden and intermediate sizes must be multiples of 512 "
-                   "(hidden=%lld inter=%lld)", (long long)hidden, (long long)inter);
+                   "%s: hidden and intermediate sizes must be multiples of 512 "
+                   "(hidden=%lld inter=%lld)", fn, (long long)hidden, (long long)inter);
   if (ldx < hidden || ldx % 8 != 0)
-    return kq_fail(KQ_ERR_INVALID, "kq_moe_forward: ldx must be >= hidden and a multiple of 8");
+    return kq_fail(KQ_ERR_INVALID, "%s: ldx must be >= hidden and a multiple of 8", fn);
   if (kq_misaligned(x, 16) || kq_misaligned(w13_t, 16) || kq_misaligned(w2_t, 16) ||
       kq_misaligned(w13_st, 2) || kq_misaligned(w2_st, 2) || kq_misaligned(workspace, 256) ||
       kq_misaligned(out, 16))
-    return kq_fail(KQ_ERR_INVALID, "kq_moe_forward: misaligned buffer");
+    return kq_fail(KQ_ERR_INVALID, "%s: misaligned buffer", fn);
   if (tokens * topk > INT32_MAX / 2)
-    return kq_fail(KQ_ERR_LIMIT, "kq_moe_forward: too many routed pairs");
-  const Layout L = make_layout(tokens, topk, experts, hidden, inter);
+    return kq_fail(KQ_ERR_LIMIT, "%s: too many routed pairs", fn);
+  const Layout L = make_layout(tokens, topk, experts, hidden, inter, xa != nullptr);
   if (workspace_bytes < (int64_t)L.total)
-    return kq_fail(KQ_ERR_INVALID, "kq_moe_forward: workspace of %lld bytes < required %lld",
+    return kq_fail(KQ_ERR_INVALID, "%s: workspace of %lld bytes < required %lld", fn,
                    (long long)workspace_bytes, (long long)L.total);
   if (tokens == 0) return KQ_OK;
   hipStream_t st = (hipStream_t)stream;
@@ -1566,6 +1628,9 @@ extern "C" int kq_moe_forward(int activation, float act_beta, float act_linear_b
   uint16_t* act = (uint16_t*)(w + L.act);
   float* y = (float*)(w + L.y);
   const ActParams ap{activation, act_beta, act_linear_beta};
+  int* rank_of = xa ? (int*)(w + L.rank_of) : nullptr;
+  int* routed = xa ? (int*)(w + L.routed) : nullptr;
+  const int max_routed = (int)L.max_routed;
   hipError_t e;
   // Decode: few pairs.  Every routed expert takes the GEMV path (in entries
   // of up to 16 pairs) and the grouped GEMM is not launched.
@@ -1573,22 +1638,35 @@ extern "C" int kq_moe_forward(int activation, float act_beta, float act_linear_b
 
   if (decode) {
     route_decode_kernel<<<1, DECODE_MAX_PAIRS, 0, st>>>(route_ids, (int)L.pairs, experts, sorted,
-                                                         small_list, (int)L.max_list, meta);
+                                                         small_list, (int)L.max_list, meta, rank_of,
+                                                         routed, max_routed);
     if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_moe_forward/route");
   } else if (L.pairs <= PREP_ONE) {
     route_prep_one_kernel<<<1, 1024, 0, st>>>(route_ids, (int)L.pairs, experts, counts, offsets,
-                                               sorted, small_list, large_tiles, meta, (int)L.max_large);
+                                               sorted, small_list, large_tiles, meta, (int)L.max_large,
+                                               rank_of, routed, max_routed);
     if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_moe_forward/prep");
   } else {
     route_hist_kernel<<<(unsigned)L.nblk, PREP, 0, st>>>(route_ids, L.pairs, experts, block_counts);
     if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_moe_forward/hist");
     route_scan_kernel<<<1, 1024, 0, st>>>(block_counts, (int)L.nblk, experts, counts, offsets,
-                                          small_list, large_tiles, meta, (int)L.max_large);
+                                          small_list, large_tiles, meta, (int)L.max_large, rank_of,
+                                          routed, max_routed);
     if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_moe_forward/scan");
     route_scatter_kernel<<<(unsigned)L.nblk, PREP, 0, st>>>(route_ids, L.pairs, experts, offsets,
                                                             block_counts, sorted);
     if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_moe_forward/scatter");
   }
+
+  if (xa) {
+    xa->p[0].out = xa->p[1].out = w + L.s13;
+    xa->p[2].out = w + L.s2;
+    if ((e = x4t_expand_routed(*xa, routed, max_routed, st)) != hipSuccess)
+      return kq_check_launch(e, "kq_moe_forward_x4t/expand");
+    w13_st = w + L.s13;
+    w2_st = w + L.s2;
+  }
+  const int* sslot = rank_of;
 
   auto combine = [&]() -> int {
     const dim3 cgrid((unsigned)((hidden / 4 + 255) / 256), (unsigned)tokens);
@@ -1602,7 +1680,7 @@ extern "C" int kq_moe_forward(int activation, float act_beta, float act_linear_b
   if (act_fmt >= 0) {
     if ((uint64_t)tokens * hidden > dma::MAX_RANGE || (uint64_t)L.pairs * inter > dma::MAX_RANGE ||
         (uint64_t)(2 * inter) * hidden / 2 > dma::MAX_RANGE)
-      return kq_fail(KQ_ERR_LIMIT, "kq_moe_forward: activation-quantized operands exceed 4 GiB");
+      return kq_fail(KQ_ERR_LIMIT, "%s: activation-quantized operands exceed 4 GiB", fn);
     int grid_mx = 8;
     if (!decode && L.pairs > SMALL_MAX) {
       int dev = 0, cus = 0;
@@ -1613,9 +1691,9 @@ extern "C" int kq_moe_forward(int activation, float act_beta, float act_linear_b
     }
     const int rc = act_fmt == 4
         ? moe_forward_mx<4>(L, w, ap, x, ldx, tokens, hidden, route_weights, topk, inter, w13_t, w13_st,
-                            w2_t, w2_st, decode, grid_mx, stream)
+                            w2_t, w2_st, sslot, decode, grid_mx, stream)
         : moe_forward_mx<0>(L, w, ap, x, ldx, tokens, hidden, route_weights, topk, inter, w13_t, w13_st,
-                            w2_t, w2_st, decode, grid_mx, stream);
+                            w2_t, w2_st, sslot, decode, grid_mx, stream);
     if (rc != KQ_OK) return rc;
     return combine();
   }
@@ -1625,7 +1703,7 @@ extern "C" int kq_moe_forward(int activation, float act_beta, float act_linear_b
   {
     e = launch_small<true, KQ_GU_NBP, KQ_GU_S, KQ_GU_RW, KQ_GU_P>(
         L.max_list, inter, hidden, st, xb, ldx, topk, (const int*)sorted, (const int*)small_list,
-        w13_t, w13_st, 2 * inter, hidden, inter, ap, route_weights, act, y, hidden);
+        w13_t, w13_st, sslot, 2 * inter, hidden, inter, ap, route_weights, act, y, hidden);
     if (e != hipSuccess) return kq_check_launch(e, "kq_moe_forward/gateup_small");
   }
   const size_t lds = 2 * (size_t)STAGE + BM * sizeof(int);
@@ -1644,7 +1722,7 @@ extern "C" int kq_moe_forward(int activation, float act_beta, float act_linear_b
     grid_dma = cus / 8 * 8 > 0 ? cus / 8 * 8 : 8;
     const int col_tiles = (int)(inter / (BN / 2));
     moe_large_dma_kernel<true><<<grid_dma, THREADS, 0, st>>>(
-        xb, ldx, (uint32_t)x_bytes, topk, offsets, sorted, large_tiles, meta, w13_t, w13_st,
+        xb, ldx, (uint32_t)x_bytes, topk, offsets, sorted, large_tiles, meta, w13_t, w13_st, sslot,
         2 * inter, hidden, inter, col_tiles, ap, route_weights, act, y, hidden);
     if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_moe_forward/gateup_large");
   } else if (any_large) {
@@ -1655,7 +1733,7 @@ extern "C" int kq_moe_forward(int activation, float act_beta, float act_linear_b
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return kq_check_launch(e, "kq_moe_forward/attr");
     moe_large_kernel<true><<<dim3((unsigned)L.max_large, (unsigned)(inter / (BN / 2))), THREADS, lds, st>>>(
-        xb, ldx, topk, offsets, sorted, large_tiles, meta, w13_t, w13_st, 2 * inter, hidden,
+        xb, ldx, topk, offsets, sorted, large_tiles, meta, w13_t, w13_st, sslot, 2 * inter, hidden,
         inter, ap, route_weights, act, y, hidden);
     if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_moe_forward/gateup_large");
   }
@@ -1663,22 +1741,83 @@ extern "C" int kq_moe_forward(int activation, float act_beta, float act_linear_b
   {
     e = launch_small<false, KQ_DN_NBP, KQ_DN_S, KQ_DN_RW, KQ_DN_P>(
         L.max_list, hidden, inter, st, (const uint16_t*)act, inter, topk, (const int*)sorted,
-        (const int*)small_list, w2_t, w2_st, hidden, inter, inter, ap, route_weights, act, y, hidden);
+        (const int*)small_list, w2_t, w2_st, sslot, hidden, inter, inter, ap, route_weights, act, y,
+        hidden);
     if (e != hipSuccess) return kq_check_launch(e, "kq_moe_forward/down_small");
   }
   if (any_large && dma_path) {
     const int col_tiles = (int)(hidden / BN);
     moe_large_dma_kernel<false><<<grid_dma, THREADS, 0, st>>>(
-        act, inter, (uint32_t)act_bytes, topk, offsets, sorted, large_tiles, meta, w2_t, w2_st,
+        act, inter, (uint32_t)act_bytes, topk, offsets, sorted, large_tiles, meta, w2_t, w2_st, sslot,
         hidden, inter, inter, col_tiles, ap, route_weights, act, y, hidden);
     if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_moe_forward/down_large");
   } else if (any_large) {
     moe_large_kernel<false><<<dim3((unsigned)L.max_large, (unsigned)((hidden + BN - 1) / BN)), THREADS, lds, st>>>(
-        act, inter, topk, offsets, sorted, large_tiles, meta, w2_t, w2_st, hidden, inter, inter,
+        act, inter, topk, offsets, sorted, large_tiles, meta, w2_t, w2_st, sslot, hidden, inter, inter,
         ap, route_weights, act, y, hidden);
     if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_moe_forward/down_large");
   }
   return combine();
+}
+
+extern "C" int kq_moe_forward(int activation, float act_beta, float act_linear_beta,
+                              const void* x, int64_t ldx, int64_t tokens, int64_t hidden,
+                              const int32_t* route_ids, const float* route_weights, int topk,
+                              int experts, int64_t inter, const uint8_t* w13_t,
+                              const uint8_t* w13_st, const uint8_t* w2_t,
+                              const uint8_t* w2_st, int out_dtype, void* out,
+                              void* workspace, int64_t workspace_bytes, uint32_t flags,
+                              void* stream) {
+  if (!w13_st || !w2_st) return kq_fail(KQ_ERR_INVALID, "kq_moe_forward: null scale tiles");
+  return moe_forward_impl("kq_moe_forward", activation, act_beta, act_linear_beta, x, ldx, tokens, hidden,
+                          route_ids, route_weights, topk, experts, inter, w13_t, w13_st, w2_t, w2_st,
+                          nullptr, out_dtype, out, workspace, workspace_bytes, flags, stream);
+}
+
+extern "C" int64_t kq_moe_x4t_workspace_size(int64_t tokens, int topk, int experts, int64_t hidden,
+                                             int64_t inter) {
+  if (tokens < 0 || topk <= 0 || experts <= 0 || hidden <= 0 || inter <= 0) return -1;
+  return (int64_t)make_layout(tokens, topk, experts, hidden, inter, true).total;
+}
+
+extern "C" int kq_moe_forward_x4t(int activation, float act_beta, float act_linear_beta,
+                                  const void* x, int64_t ldx, int64_t tokens, int64_t hidden,
+                                  const int32_t* route_ids, const float* route_weights, int topk,
+                                  int experts, int64_t inter, const uint8_t* w13_t, const uint8_t* w2_t,
+                                  const uint8_t* w1_fixed, const uint32_t* w1_exceptions,
+                                  const uint32_t* w1_tile_index, const uint8_t* w3_fixed,
+                                  const uint32_t* w3_exceptions, const uint32_t* w3_tile_index,
+                                  const uint8_t* w2_fixed, const uint32_t* w2_exceptions,
+                                  const uint32_t* w2_tile_index, int out_dtype, void* out,
+                                  void* workspace, int64_t workspace_bytes, uint32_t flags,
+                                  void* stream) {
+  const char* fn = "kq_moe_forward_x4t";
+  if (hidden <= 0 || inter <= 0 || hidden % 512 != 0 || inter % 512 != 0)
+    return kq_fail(KQ_ERR_INVALID, "%s: hidden and intermediate sizes must be multiples of 512", fn);
+  // X4T planes: w1 / w3 [inter, hidden / 32], w2 [hidden, inter / 32]; at most
+  // 255 columns and 2^24 positions per matrix
+  if (hidden / 32 > 255 || inter / 32 > 255 || inter * (hidden / 32) > (1 << 24) - 1 ||
+      hidden * (inter / 32) > (1 << 24) - 1)
+    return kq_fail(KQ_ERR_LIMIT, "%s: scale planes beyond the X4T geometry (hidden=%lld inter=%lld)", fn,
+                   (long long)hidden, (long long)inter);
+  const void* planes[9] = {w1_fixed, w1_exceptions, w1_tile_index, w3_fixed, w3_exceptions,
+                           w3_tile_index, w2_fixed, w2_exceptions, w2_tile_index};
+  for (int i = 0; i < 9; ++i) {
+    if (!planes[i]) return kq_fail(KQ_ERR_INVALID, "%s: null X4T component", fn);
+    if (i % 3 != 0 && kq_misaligned(planes[i], 4))
+      return kq_fail(KQ_ERR_INVALID, "%s: misaligned X4T exceptions or tile index", fn);
+  }
+  X4TExpandArgs xa{};
+  xa.n = 3;
+  xa.p[0] = X4TPlane{w1_fixed, w1_exceptions, w1_tile_index, nullptr, inter / 16, 2 * inter / 16, 0,
+                     (int)(hidden / 32)};
+  xa.p[1] = X4TPlane{w3_fixed, w3_exceptions, w3_tile_index, nullptr, inter / 16, 2 * inter / 16,
+                     inter / 16, (int)(hidden / 32)};
+  xa.p[2] = X4TPlane{w2_fixed, w2_exceptions, w2_tile_index, nullptr, hidden / 16, hidden / 16, 0,
+                     (int)(inter / 32)};
+  return moe_forward_impl(fn, activation, act_beta, act_linear_beta, x, ldx, tokens, hidden, route_ids,
+                          route_weights, topk, experts, inter, w13_t, nullptr, w2_t, nullptr, &xa,
+                          out_dtype, out, workspace, workspace_bytes, flags, stream);
 }
 
 // Routing sort alone (for per-expert calibration statistics): the pairs
@@ -1734,12 +1873,12 @@ extern "C" int kq_route_sort(const int32_t* route_ids, int64_t tokens, int topk,
   hipError_t e;
   if (pairs <= PREP_ONE) {
     route_prep_one_kernel<<<1, 1024, 0, st>>>(route_ids, (int)pairs, experts, counts, off32, sorted,
-                                               small_list, large_tiles, meta, max_large);
+                                               small_list, large_tiles, meta, max_large, nullptr, nullptr, 0);
   } else {
     route_hist_kernel<<<(unsigned)nblk, PREP, 0, st>>>(route_ids, pairs, experts, block_counts);
     if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_route_sort");
     route_scan_kernel<<<1, 1024, 0, st>>>(block_counts, (int)nblk, experts, counts, off32, small_list,
-                                          large_tiles, meta, max_large);
+                                          large_tiles, meta, max_large, nullptr, nullptr, 0);
     if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_route_sort");
     route_scatter_kernel<<<(unsigned)nblk, PREP, 0, st>>>(route_ids, pairs, experts, off32,
                                                           block_counts, sorted);

@@ -278,6 +278,87 @@ __global__ __launch_bounds__(SP_THREADS) void x4t_decode_kernel(
   for (int p = threadIdx.x; p < span; p += SP_THREADS) o[p] = buf[p];
 }
 
+// Per-tile exception index of X4T matrices: index[m * tiles + t] = first
+// exception of matrix m at or after tile t's first position (a lower bound
+// over the matrix's sorted exception range), index[mats * tiles] = n_exc.
+// Built once per weight set, it lets a runtime expansion find a tile's
+// exceptions without any search.
+__global__ __launch_bounds__(256) void x4t_tile_index_kernel(
+    const uint32_t* __restrict__ exc, int64_t n_exc, const int64_t* __restrict__ exc_offsets,
+    int64_t mats, int64_t tiles_per_mat, int cols, uint32_t* __restrict__ index) {
+  const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x, total = mats * tiles_per_mat;
+  if (g > total) return;
+  if (g == total) {
+    index[total] = (uint32_t)n_exc;
+    return;
+  }
+  const int64_t m = g / tiles_per_mat, t = g - m * tiles_per_mat;
+  int64_t lo = 0, hi = n_exc;
+  if (exc_offsets) {
+    lo = min(max(exc_offsets[m], (int64_t)0), n_exc);
+    hi = min(max(exc_offsets[m + 1], lo), n_exc);
+  }
+  const uint32_t key = (uint32_t)(t * X4T_ROWS * cols);
+  while (lo < hi) {
+    const int64_t mid = lo + (hi - lo) / 2;
+    if ((exc[mid] & X4T_POS_MASK) < key) lo = mid + 1;
+    else hi = mid;
+  }
+  index[g] = (uint32_t)lo;
+}
+
+// Runtime expansion of routed experts' X4T scales (one launch, no search, no
+// allocation).  Block (r, y): y runs over the 16-row tiles of every plane in
+// turn; the block decodes that tile of matrix routed[r] (nothing when -1) -
+// base + selector bit, then the tile's exceptions from the precomputed index -
+// into LDS and writes it to slot r of the plane's output in the
+// kq_mx_tile_weights scale layout: 64-byte tiles [row group][cols / 4] with
+// byte l = scale[16 rg + l % 16][4 c + l / 16].
+__global__ __launch_bounds__(SP_THREADS) void x4t_expand_tiled_kernel(X4TExpandArgs a,
+                                                                       const int* __restrict__ routed) {
+  const int e = routed[blockIdx.x];
+  if (e < 0) return;
+  int64_t t = blockIdx.y;
+  int pi = 0;
+  if (t >= a.p[0].tiles) {
+    t -= a.p[0].tiles;
+    pi = 1;
+    if (a.n > 2 && t >= a.p[1].tiles) {
+      t -= a.p[1].tiles;
+      pi = 2;
+    }
+  }
+  const X4TPlane P = pi == 0 ? a.p[0] : pi == 1 ? a.p[1] : a.p[2];
+  __shared__ uint8_t buf[X4T_ROWS * 256];
+  const int cols = P.cols, sb = (cols + 7) >> 3, span = X4T_ROWS * cols;
+  const int64_t ti = (int64_t)e * P.tiles + t;
+  const uint8_t* f = P.fixed + ti * (X4T_ROWS * (1 + sb));
+  for (int p = threadIdx.x; p < span; p += SP_THREADS) {
+    const int i = p / cols, c = p - i * cols;
+    buf[p] = (uint8_t)(f[i] + ((f[X4T_ROWS + i * sb + (c >> 3)] >> (c & 7)) & 1));
+  }
+  __syncthreads();
+  const uint32_t lo = P.tile_index[ti], hi = P.tile_index[ti + 1];
+  const uint32_t pos0 = (uint32_t)(t * span);
+  for (uint32_t k = lo + threadIdx.x; k < hi; k += SP_THREADS) {
+    const uint32_t w = P.exceptions[k];
+    const uint32_t off = (w & X4T_POS_MASK) - pos0;  // wraps past span when outside the tile
+    if (off < (uint32_t)span) buf[off] = (uint8_t)(w >> 24);
+  }
+  __syncthreads();
+  // dword j of the tile row group: chunk j / 16, lanes 4 (j % 16) .. + 3 =
+  // rows 4 (j % 4) .. + 3 of column 4 (j / 16) + (j % 16) / 4
+  const int nchunk = cols >> 2;
+  uint32_t* dst = reinterpret_cast<uint32_t*>(
+      P.out + (((int64_t)blockIdx.x * P.out_rgs + P.out_rg0 + t) * nchunk) * 64);
+  for (int j = threadIdx.x; j < nchunk * 16; j += SP_THREADS) {
+    const int c = 4 * (j >> 4) + ((j & 15) >> 2);
+    const uint8_t* src = buf + 4 * (j & 3) * cols + c;
+    dst[j] = (uint32_t)src[0] | (uint32_t)src[cols] << 8 | (uint32_t)src[2 * cols] << 16 |
+             (uint32_t)src[3 * cols] << 24;
+  }
+}
+
 // status: {selector padding, first bad position index, first redundant value
 // index, non-canonical}.
 __global__ void x4t_status_init_kernel(uint32_t* status) {
@@ -898,6 +979,32 @@ static int kqsc_geometry(const char* who, int version, int64_t rows, int64_t col
   if (*tiles > 0x7fffffff) return kq_fail(KQ_ERR_LIMIT, "%s: too many tiles", who);
   return KQ_OK;
 }
+
+extern "C" int kq_x4t_tile_index(const uint32_t* exceptions, int64_t n_exceptions,
+                                 const int64_t* exception_offsets, int64_t mats, int64_t rows,
+                                 int64_t cols, uint32_t* index, void* stream) {
+  if (int rc = x4t_geometry("kq_x4t_tile_index", mats, rows, cols)) return rc;
+  if (n_exceptions < 0 || n_exceptions > 0xffffffffLL)
+    return kq_fail(KQ_ERR_INVALID, "kq_x4t_tile_index: bad exception count %lld", (long long)n_exceptions);
+  if (mats > 1 && !exception_offsets)
+    return kq_fail(KQ_ERR_INVALID, "kq_x4t_tile_index: several matrices need exception_offsets");
+  if (kq_misaligned(exceptions, 4) || kq_misaligned(exception_offsets, 8) || kq_misaligned(index, 4))
+    return kq_fail(KQ_ERR_INVALID, "kq_x4t_tile_index: misaligned buffers");
+  const int64_t total = mats * (rows / X4T_ROWS) + 1;
+  x4t_tile_index_kernel<<<(unsigned)((total + 255) / 256), 256, 0, (hipStream_t)stream>>>(
+      exceptions, n_exceptions, exception_offsets, mats, rows / X4T_ROWS, (int)cols, index);
+  return kq_check_launch(hipGetLastError(), "kq_x4t_tile_index");
+}
+
+namespace kq {
+hipError_t x4t_expand_routed(const X4TExpandArgs& args, const int* routed, int max_routed, hipStream_t st) {
+  int64_t tiles = 0;
+  for (int i = 0; i < args.n; ++i) tiles += args.p[i].tiles;
+  if (max_routed <= 0 || tiles == 0) return hipSuccess;
+  x4t_expand_tiled_kernel<<<dim3((unsigned)max_routed, (unsigned)tiles), SP_THREADS, 0, st>>>(args, routed);
+  return hipGetLastError();
+}
+}  // namespace kq
 
 extern "C" int kq_kqsc_measure(int version, const uint8_t* scale, int64_t rows, int64_t cols,
                                int tile_rows, uint32_t* row_meta, int64_t* tile_offsets,

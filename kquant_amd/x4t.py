@@ -225,3 +225,37 @@ def decode_x4t_scale_components_batched(
     N.call("kq_x4t_decode", N.ptr(f), N.ptr(e), int(exceptions.numel()), N.ptr(o), mats, rows,
            columns, N.ptr(out), None, N.stream(gpu))
     return out if host is None else out.to(host)
+
+
+def x4t_tile_index(
+    exceptions: torch.Tensor,
+    offsets: torch.Tensor,
+    *,
+    rows: int,
+    columns: int,
+) -> torch.Tensor:
+    """Per-16-row-tile exception index of ``mats`` stacked planes, on the GPU.
+
+    ``exceptions`` uint32 and ``offsets`` int64 [mats + 1] as
+    ``pack_x4t_scale_components_batched`` returns them (or as kquant's X4T
+    container stores a matrix kind: one exception stream and per-expert
+    offsets).  Returns uint32 [mats * rows / 16 + 1]: entry m * rows/16 + t
+    is the first exception of matrix m at or past tile t, the last entry the
+    total.  The one-time index ``grouped_expert_forward`` needs to expand
+    routed experts' scales without searching.
+    """
+
+    if exceptions.dtype != torch.uint32 or exceptions.ndim != 1:
+        raise ValueError("X4T exception tensor must be one-dimensional uint32")
+    if offsets.dtype != torch.int64 or offsets.ndim != 1 or offsets.numel() < 2:
+        raise ValueError("X4T exception offsets must be int64 [mats + 1]")
+    if rows <= 0 or rows % X4T_TILE_ROWS or not 1 <= columns <= 255 or rows * columns > X4T_POSITION_MASK:
+        raise ValueError("X4T plane geometry is invalid")
+    mats = int(offsets.numel()) - 1
+    (e, o), gpu, _ = N.to_gpu([exceptions, offsets])
+    o = N.aligned(o.contiguous(), 8)
+    e = N.aligned(e.contiguous(), 4) if e.numel() else torch.zeros(1, dtype=torch.uint32, device=gpu)
+    index = torch.empty(mats * (rows // X4T_TILE_ROWS) + 1, dtype=torch.uint32, device=gpu)
+    N.call("kq_x4t_tile_index", N.ptr(e), int(exceptions.numel()), N.ptr(o), mats, rows, columns,
+           N.ptr(index), N.stream(gpu))
+    return index

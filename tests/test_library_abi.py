@@ -32,7 +32,7 @@ def test_python_binding_covers_every_entry_point():
     lib = _native.library()
     assert lib.kq_version() >> 16 == 1
     bound = set(_native.SIGNATURES) | {"kq_version", "kq_last_error", "kq_moe_workspace_size",
-                                        "kq_mx_linear_f32_workspace_size",
+                                        "kq_moe_x4t_workspace_size", "kq_mx_linear_f32_workspace_size",
                                         "kq_route_sort_workspace_size"}
     assert set(declared_symbols()) <= bound
 
@@ -43,3 +43,23 @@ def test_argument_errors_need_no_gpu():
     assert rc == _native.KQ_ERR_INVALID
     assert b"k % 32" in lib.kq_last_error()
     assert lib.kq_moe_workspace_size(8, 8, 384, 7168, 2048) > 8 * 8 * 7168 * 4
+
+
+def test_x4t_moe_argument_errors_need_no_gpu():
+    lib = _native.library()
+    base = lib.kq_moe_workspace_size(4, 8, 384, 7168, 2048)
+    # one w13 and one w2 scale slot per routed expert (min(32 pairs, 384))
+    slots = 32 * (2 * 2048 * 7168 // 32 + 7168 * 2048 // 32)
+    assert lib.kq_moe_x4t_workspace_size(4, 8, 384, 7168, 2048) >= base + slots
+    assert lib.kq_moe_x4t_workspace_size(4, 0, 384, 7168, 2048) == -1
+    fake = ctypes.c_void_p(256)  # never dereferenced: validation fails first
+    planes = [fake] * 9
+    rc = lib.kq_moe_forward_x4t(_native.ACT_SITU, 4.0, 25.0, fake, 8192, 1, 8192, fake, fake, 8, 384,
+                                2048, fake, fake, *planes, _native.DT_F32, fake, fake, 1 << 30, 0, None)
+    assert rc == _native.KQ_ERR_LIMIT and b"X4T geometry" in lib.kq_last_error()
+    planes[4] = None
+    rc = lib.kq_moe_forward_x4t(_native.ACT_SITU, 4.0, 25.0, fake, 7168, 1, 7168, fake, fake, 8, 384,
+                                2048, fake, fake, *planes, _native.DT_F32, fake, fake, 1 << 30, 0, None)
+    assert rc == _native.KQ_ERR_INVALID and b"null X4T component" in lib.kq_last_error()
+    rc = lib.kq_x4t_tile_index(fake, 0, None, 1, 32, 300, fake, None)
+    assert rc != 0
