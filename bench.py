@@ -174,7 +174,10 @@ def main() -> int:
     if not args.quick and want("moe_prefill"):
         ids, rw = workloads.zipf_routing(8192)
         active = torch.unique(ids).tolist()
-        weights = moe.prepare_expert_weights(*workloads.quantized_experts(active, device=dev))
+        raw = workloads.quantized_experts(active, device=dev)
+        weights = moe.prepare_expert_weights(*raw)
+        x4t_scales = moe.prepare_expert_weights(*raw, scale_format="x4t")
+        del raw
         x3 = (torch.randn(8192, workloads.HIDDEN, generator=torch.Generator().manual_seed(6))
               .to(torch.bfloat16).to(dev))
         ids_d, rw_d = ids.to(dev), rw.to(dev)
@@ -196,6 +199,16 @@ def main() -> int:
             "roofline": _roofline("mfma", tflops, "moe_prefill_cfg3"),
             "frac_of_fp4_dense_peak": round(tflops / FP4_PEAK_TFLOPS, 4),
         }
+
+        # the same forward with X4T-coded expert scales (grouped-GEMM experts'
+        # scales expanded per call, the GEMV experts' decoded in the GEMV)
+        def moe_x4t_step():
+            moe.grouped_expert_forward(x3, ids_d, rw_d, x4t_scales)
+
+        t_x4t = _time_loop(torch, moe_x4t_step, max(3, args.steps // 10), 2)
+        moe_result["x4t_scales_ms"] = round(t_x4t * 1e3, 3)
+        moe_result["x4t_added_us"] = round((t_x4t - t_moe) * 1e6, 1)
+        del x4t_scales
         # Activation-quantized modes (W4A8 / W4A4, no kquant counterpart): the
         # same forward with tokens and intermediates MX-quantized, every GEMM on
         # the block-scaled fp8/fp4 MFMA; priced against that MFMA's peak
@@ -221,22 +234,32 @@ def main() -> int:
         for tokens in (1, 4, 16):
             ids, rw = workloads.random_routing(tokens, seed=tokens)
             active = torch.unique(ids).tolist()
-            weights = moe.prepare_expert_weights(*workloads.quantized_experts(active, device=dev))
+            raw = workloads.quantized_experts(active, device=dev)
+            weights = moe.prepare_expert_weights(*raw)
+            # the same experts with X4T-coded scales, expanded per call
+            weights_x4t = moe.prepare_expert_weights(*raw, scale_format="x4t")
+            del raw
             x5 = torch.randn(tokens, workloads.HIDDEN, generator=torch.Generator().manual_seed(5)).to(torch.bfloat16).to(dev)
             ids_d, rw_d = ids.to(dev), rw.to(dev)
 
             def dec_step():
                 moe.grouped_expert_forward(x5, ids_d, rw_d, weights)
 
+            def dec_x4t_step():
+                moe.grouped_expert_forward(x5, ids_d, rw_d, weights_x4t)
+
             t = _time_loop(torch, dec_step, max(10, args.steps), 5)
+            t_x = _time_loop(torch, dec_x4t_step, max(10, args.steps), 5)
             nbytes = len(active) * workloads.bytes_per_expert() + tokens * workloads.HIDDEN * 2
             dec[f"batch{tokens}"] = {
                 "us": round(t * 1e6, 1),
                 "distinct_experts": len(active),
                 "gbs": round(nbytes / t / 1e9, 1),
                 "hbm_frac": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4),
+                "x4t_scales_us": round(t_x * 1e6, 1),
+                "x4t_added_us": round((t_x - t) * 1e6, 1),
             }
-            del weights
+            del weights, weights_x4t
         result["cfg5_moe_decode"] = dec
 
     # ------------------------------------------------- config 1 codec --

@@ -152,8 +152,8 @@ int kq_moe_forward(int activation, float act_beta, float act_linear_beta,
                    uint32_t flags, void* stream);
 
 /* Workspace bytes kq_moe_forward_x4t needs (-1 on bad sizes): the
- * kq_moe_forward workspace plus one w13 and one w2 scale slot per routed
- * expert, min(tokens * topk, experts) of each. */
+ * kq_moe_forward workspace plus, above 256 routed pairs, one w13 and one w2
+ * scale slot per possible grouped-GEMM expert, min(pairs / 17, experts). */
 int64_t kq_moe_x4t_workspace_size(int64_t tokens, int topk, int experts, int64_t hidden,
                                   int64_t inter);
 
@@ -161,11 +161,13 @@ int64_t kq_moe_x4t_workspace_size(int64_t tokens, int topk, int experts, int64_t
  * (kquant/x4t.py's per-expert w1 / w3 / w2 scale planes: fixed streams of
  * `experts` stacked matrices, their exception streams, and per-16-row-tile
  * exception indexes from kq_x4t_tile_index).  The X4T runtime refinement of
- * docs/qsrt-technical-brief.md:446-474: after routing, one launch expands
- * only the routed experts' scales - w1 and w3 into the gate and up rows of
- * the gate-first w13 - into workspace slots in the kq_mx_tile_weights scale
- * layout, and the GEMMs read them there; no allocation, host work or
- * exception search per call.  w13_t / w2_t as for kq_moe_forward.  w1 / w3
+ * docs/qsrt-technical-brief.md:446-474, with no allocation, host work or
+ * exception search per call: each GEMV workgroup (experts with <= 16 pairs,
+ * every expert when decoding) decodes the scales of its own rows - w1 and w3
+ * into the gate and up rows of the gate-first w13 - into LDS before its K
+ * loop; for the experts on the grouped GEMM one launch after routing expands
+ * their scales into workspace slots in the kq_mx_tile_weights scale layout.
+ * w13_t / w2_t as for kq_moe_forward.  w1 / w3
  * planes are [inter, hidden / 32], w2 planes [hidden, inter / 32]; hidden
  * and inter at most 8160.  The components must be a valid X4T encoding (as
  * kq_x4t_decode accepts): the expansion does not validate them; with tile

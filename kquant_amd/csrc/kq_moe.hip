@@ -54,7 +54,9 @@ static Layout make_layout(int64_t tokens, int topk, int experts, int64_t hidden,
                           bool x4t = false) {
   Layout L;
   L.pairs = tokens * topk;
-  L.max_routed = L.pairs < experts ? L.pairs : experts;
+  // experts on the grouped GEMM (more than SMALL_MAX pairs; none when decoding)
+  L.max_routed = L.pairs <= DECODE_MAX_PAIRS ? 0
+               : L.pairs / (SMALL_MAX + 1) < experts ? L.pairs / (SMALL_MAX + 1) : experts;
   L.nblk = (L.pairs + PREP - 1) / PREP;
   L.max_small = L.pairs < experts ? L.pairs : experts;
   L.max_large = L.pairs / (SMALL_MAX + 1) + L.pairs / BM + 1;
@@ -77,7 +79,7 @@ static Layout make_layout(int64_t tokens, int topk, int experts, int64_t hidden,
   L.aq = o;           o = align256(o + (size_t)L.pairs * inter);
   L.as = o;           o = align256(o + (size_t)L.pairs * inter / 32);
   L.rank_of = L.routed = L.s13 = L.s2 = o;
-  if (x4t) {  // one scale slot per routed expert: w13 [2I, H/32] and w2 [H, I/32] scale tiles
+  if (x4t) {  // a scale slot per grouped-GEMM expert: w13 [2I, H/32] and w2 [H, I/32] scale tiles
     L.rank_of = o;    o = align256(o + sizeof(int) * experts);
     L.routed = o;     o = align256(o + sizeof(int) * (size_t)L.max_routed);
     L.s13 = o;        o = align256(o + (size_t)L.max_routed * 2 * inter * (hidden / 32));
@@ -136,9 +138,10 @@ __device__ int block_exclusive_scan(int* v, int n, int* scratch /*[1024]*/) {
   return total;
 }
 
-// Ranks of the routed experts (count > 0) in ascending expert order, for the
-// per-call expansion of compressed scales: rank_of[e] for every routed e,
-// routed[r] = the expert of rank r, -1 for r in [routed experts, max_routed).
+// Ranks of the grouped-GEMM experts (count > SMALL_MAX) in ascending expert
+// order, for the per-call expansion of compressed scales: rank_of[e] for each
+// such e, routed[r] = the expert of rank r, -1 for r in [their number,
+// max_routed).
 // Called by all 1024 threads after counts[0, experts) are written; tmp is an
 // LDS array of `experts` ints that is overwritten and then rebuilt.
 __device__ void routed_ranks(const int* counts, int experts, int* rank_of, int* routed, int max_routed,
@@ -147,13 +150,13 @@ __device__ void routed_ranks(const int* counts, int experts, int* rank_of, int* 
   for (int i = 0; i < 4; ++i) {
     const int e = threadIdx.x + 1024 * i;
     keep[i] = e < experts ? tmp[e] : 0;
-    if (e < experts) tmp[e] = counts[e] > 0 ? 1 : 0;
+    if (e < experts) tmp[e] = counts[e] > SMALL_MAX ? 1 : 0;
   }
   __syncthreads();
   const int nrouted = block_exclusive_scan(tmp, experts, scratch);
   for (int i = 0; i < 4; ++i) {
     const int e = threadIdx.x + 1024 * i;
-    if (e < experts && counts[e] > 0) {
+    if (e < experts && counts[e] > SMALL_MAX) {
       rank_of[e] = tmp[e];
       if (tmp[e] < max_routed) routed[tmp[e]] = e;
     }
@@ -319,8 +322,7 @@ __global__ __launch_bounds__(1024) void route_prep_one_kernel(
 // (expert, first sorted position, count <= 16), one per 16 of its pairs.
 __global__ __launch_bounds__(DECODE_MAX_PAIRS) void route_decode_kernel(
     const int* __restrict__ ids, int pairs, int experts, int* __restrict__ sorted,
-    int* __restrict__ small_list, int max_list, int* __restrict__ meta, int* __restrict__ rank_of,
-    int* __restrict__ routed, int max_routed) {
+    int* __restrict__ small_list, int max_list, int* __restrict__ meta) {
   // ids past `pairs` are -1 and the loops run over whole groups of four
   // (one 16-byte LDS read each), so no read waits on the previous one
   __shared__ __attribute__((aligned(16))) int s_id[DECODE_MAX_PAIRS];
@@ -350,7 +352,7 @@ __global__ __launch_bounds__(DECODE_MAX_PAIRS) void route_decode_kernel(
   s_first[t] = first ? my : -1;
   s_nent[t] = first ? nent : 0;
   __syncthreads();
-  int e0 = 0, nlist = 0, r0 = 0, nrouted = 0;
+  int e0 = 0, nlist = 0;
 #pragma unroll 4
   for (int j4 = 0; j4 < pairs4; j4 += 4) {
     const i32x4 v4 = *reinterpret_cast<const i32x4*>(s_first + j4);
@@ -359,16 +361,7 @@ __global__ __launch_bounds__(DECODE_MAX_PAIRS) void route_decode_kernel(
     for (int i = 0; i < 4; ++i) {
       nlist += n4[i];
       e0 += (v4[i] >= 0 && v4[i] < my) ? n4[i] : 0;
-      r0 += (v4[i] >= 0 && v4[i] < my) ? 1 : 0;
-      nrouted += v4[i] >= 0 ? 1 : 0;
     }
-  }
-  if (rank_of) {  // routed-expert ranks (see routed_ranks)
-    if (first) {
-      rank_of[my] = r0;
-      if (r0 < max_routed) routed[r0] = my;
-    }
-    for (int r = nrouted + t; r < max_routed; r += DECODE_MAX_PAIRS) routed[r] = -1;
   }
   if (my >= 0) sorted[below + rank] = t;
   if (first) {
@@ -390,6 +383,150 @@ using gemm::u32x2_t;
 using gemm::u32x4_t;
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
+// ------------------------------------------- fused X4T scales (GEMV path) --
+// With X4T-coded scales the GEMV workgroup decodes the scales of its own row
+// blocks into LDS before its K loop: no separate launch and no dense scale
+// traffic.  Planes: w1 and w3 (gate and up rows) for gate/up, w2 for down.
+struct X4TGemv {
+  const uint8_t* fixed[2];    // [experts][tiles][16 (1 + ceil(cols / 8))]
+  const uint32_t* exc[2];     // matrix-local position | value << 24
+  const uint32_t* idx[2];     // [experts * tiles + 1] first exception per tile
+  int64_t tiles;              // 16-row tiles per matrix
+  int cols;                   // scale columns, K / 32 (<= 255)
+};
+
+// Registers carried from the prologue's loads to its LDS work.
+struct X4TPending {
+  u32x4_t piece[2];
+  uint32_t xr;
+};
+
+// LDS use of the fused decode for nrb row blocks: decoded scale tiles
+// [nrb][nchunk][64], the staged fixed tiles, the exception ranges.
+static inline size_t x4t_gemv_lds(int nrb, int64_t nchunk, int cols) {
+  return (size_t)nrb * nchunk * 64 + (size_t)nrb * 16 * (1 + (cols + 7) / 8) + 8 * (size_t)nrb;
+}
+
+// Row block q of the workgroup (q = row group of waves * NB + block b): its
+// plane (1 = up rows of w13) and its tile in that plane.
+template <bool GATEUP, int NB, int NBP>
+__device__ __forceinline__ int64_t x4t_rb_tile(int q, int64_t tile0, bool& up) {
+  const int b = q % NB;
+  up = GATEUP && b >= NBP;
+  return tile0 + (q / NB) * NBP + (up ? b - NBP : b);
+}
+
+// LDS barrier without waiting for outstanding global loads: this wave's LDS
+// accesses complete, then s_barrier; compiler memory clobbers on both sides.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0); vmcnt, expcnt untouched
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// First half: the loads of the row blocks' fixed tiles and exception ranges
+// (issued before the weight prefetch, so waiting for them leaves it in flight).
+template <bool GATEUP, int NB, int NBP, int NRB, int T>
+__device__ __forceinline__ void x4t_issue(const X4TGemv& xg, int e, int64_t tile0, X4TPending& pd) {
+  const int tp = 1 + ((xg.cols + 7) >> 3);
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int i = threadIdx.x + u * T;
+    if (i < NRB * tp) {
+      const int q = i / tp, pc = i - q * tp;
+      bool up;
+      const int64_t t = x4t_rb_tile<GATEUP, NB, NBP>(q, tile0, up);
+      const uint8_t* f = up ? xg.fixed[1] : xg.fixed[0];
+      pd.piece[u] = *reinterpret_cast<const u32x4_t*>(f + ((int64_t)e * xg.tiles + t) * (16 * tp) + 16 * pc);
+    }
+  }
+  if (threadIdx.x < 2 * NRB) {
+    bool up;
+    const int64_t t = x4t_rb_tile<GATEUP, NB, NBP>((int)threadIdx.x >> 1, tile0, up);
+    const uint32_t* ix = up ? xg.idx[1] : xg.idx[0];
+    pd.xr = ix[(int64_t)e * xg.tiles + t + (threadIdx.x & 1)];
+  }
+}
+
+// Second half: decode into sl[(q * nchunk + chunk) * 64 + l] (the scale-tile
+// layout: byte l = scale[16 tile + l % 16][4 chunk + l / 16]) and patch the
+// exceptions; ends with a barrier after which every wave may read sl.
+template <bool GATEUP, int NB, int NBP, int NRB, int T>
+__device__ __forceinline__ void x4t_finish(const X4TGemv& xg, int e, int64_t tile0, int nchunk,
+                                           const X4TPending& pd, uint8_t* lds) {
+  constexpr int U = 4;
+  const int tid = threadIdx.x;
+  const int cols = xg.cols, sb = (cols + 7) >> 3, tp = 1 + sb, span = 16 * cols;
+  uint8_t* sl = lds;
+  uint8_t* fl = lds + (size_t)NRB * nchunk * 64;
+  uint32_t* xl = reinterpret_cast<uint32_t*>(fl + NRB * 16 * tp);
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+    if (tid + u * T < NRB * tp) *reinterpret_cast<u32x4_t*>(fl + 16 * (tid + u * T)) = pd.piece[u];
+  if (tid < 2 * NRB) xl[tid] = pd.xr;
+  lds_barrier();
+  int lo[NRB], pre[NRB + 1];
+  pre[0] = 0;
+#pragma unroll
+  for (int q = 0; q < NRB; ++q) {
+    lo[q] = (int)xl[2 * q];
+    const int hi = (int)xl[2 * q + 1];
+    pre[q + 1] = pre[q] + (hi > lo[q] ? hi - lo[q] : 0);
+  }
+  const int total = pre[NRB];
+  uint32_t wv[U];
+  int qv[U];
+  auto fetch = [&](int base) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int k = base + tid + u * T;
+      qv[u] = -1;
+      int src = 0;
+#pragma unroll
+      for (int q = 0; q < NRB; ++q)
+        if (k >= pre[q] && k < pre[q + 1]) {
+          qv[u] = q;
+          src = lo[q] + (k - pre[q]);
+        }
+      if (qv[u] >= 0) {
+        const bool up = GATEUP && (qv[u] % NB) >= NBP;
+        wv[u] = (up ? xg.exc[1] : xg.exc[0])[src];
+      }
+    }
+  };
+  fetch(0);
+#pragma unroll
+  for (int q = 0; q < NRB; ++q) {
+    const uint8_t* f = fl + q * 16 * tp;
+    for (int j = tid; j < nchunk * 16; j += T) {
+      const int w = j & 15, r0 = 4 * (w & 3), c = 4 * (j >> 4) + (w >> 2);
+      const uint32_t base4 = *reinterpret_cast<const uint32_t*>(f + r0);
+      const uint8_t* sel = f + 16 + r0 * sb + (c >> 3);
+      uint32_t v = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        v |= (((base4 >> (8 * i)) + ((sel[i * sb] >> (c & 7)) & 1)) & 0xffu) << (8 * i);
+      *reinterpret_cast<uint32_t*>(sl + (q * nchunk + (j >> 4)) * 64 + 4 * w) = v;
+    }
+  }
+  lds_barrier();
+  for (int base = 0; base < total; base += U * T) {
+    if (base > 0) fetch(base);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (qv[u] < 0) continue;
+      bool up;
+      const int64_t t = x4t_rb_tile<GATEUP, NB, NBP>(qv[u], tile0, up);
+      const uint32_t off = (wv[u] & 0xffffffu) - (uint32_t)(t * span);  // wraps past the tile when outside
+      if (off >= (uint32_t)span) continue;
+      const int r = (int)off / cols, c = (int)off - r * cols;
+      sl[(qv[u] * nchunk + (c >> 2)) * 64 + (c & 3) * 16 + r] = (uint8_t)(wv[u] >> 24);
+    }
+  }
+  lds_barrier();
+}
+
 // ------------------------------------------------- GEMV-shaped small path --
 // One workgroup: up to 16 pairs of one expert (a list entry (expert, first
 // sorted position, count)).  Its S * RW waves form RW row
@@ -410,18 +547,24 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 //
 // GATEUP: rows of w13, output act -> bf16 intermediates.
 // !GATEUP: rows of w2, output route_weight * partial -> fp32 pair rows.
-template <bool GATEUP, int NBP, int S, int RW, int P, int STEPS>
+template <bool GATEUP, bool X4T, int NBP, int S, int RW, int P, int STEPS>
 __global__ __launch_bounds__(S * RW * 64) void moe_small_kernel(
     const uint16_t* __restrict__ a, int64_t lda, int topk, const int* __restrict__ sorted,
     const int* __restrict__ small_list, const uint8_t* __restrict__ wt,
-    const uint8_t* __restrict__ wst, const int* __restrict__ sslot, int64_t rows_per_expert, int64_t K,
-    int64_t inter, ActParams act, const float* __restrict__ route_w, uint16_t* __restrict__ act_out,
-    float* __restrict__ y_out, int64_t hidden) {
+    const uint8_t* __restrict__ wst, const int* __restrict__ sslot, X4TGemv xg, int64_t rows_per_expert,
+    int64_t K, int64_t inter, ActParams act, const float* __restrict__ route_w,
+    uint16_t* __restrict__ act_out, float* __restrict__ y_out, int64_t hidden) {
   constexpr int NB = GATEUP ? 2 * NBP : NBP;      // 16-row blocks per wave
   constexpr int CH = RW * 16 * NBP;               // channels per workgroup
   constexpr int NBUF = P + 1;
+  constexpr int T = S * RW * 64, NRB = RW * NB;
+  static_assert(NB * 33 <= 128 * S, "fixed tiles of the row blocks: at most two 16-byte loads per thread");
+  extern __shared__ __attribute__((aligned(16))) unsigned char x4t_lds[];
   const int e = small_list[3 * blockIdx.x];       // -1 past the last entry
   if (e < 0) return;
+  X4TPending pd;
+  const int64_t tile0 = (int64_t)blockIdx.y * RW * NBP;  // first tile of this workgroup's row blocks
+  if constexpr (X4T) x4t_issue<GATEUP, NB, NBP, NRB, T>(xg, e, tile0, pd);
   const int beg = small_list[3 * blockIdx.x + 1];
   const int n = small_list[3 * blockIdx.x + 2];
   const int se = sslot ? sslot[e] : e;            // scale slot of the expert
@@ -455,7 +598,7 @@ __global__ __launch_bounds__(S * RW * 64) void moe_small_kernel(
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
       B.w[b] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(wtile[b] + (int64_t)s * 1024));
-      B.ws[b] = stile[b][(int64_t)s * 64];
+      if constexpr (!X4T) B.ws[b] = stile[b][(int64_t)s * 64];
     }
   };
   // Issue the first weight loads before the dependent token-index loads.
@@ -483,13 +626,18 @@ __global__ __launch_bounds__(S * RW * 64) void moe_small_kernel(
   f32x4_t acc[NB];
 #pragma unroll
   for (int b = 0; b < NB; ++b) acc[b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  auto compute = [&](const WBuf& W, const ABuf& A) {
+  // X4T: this wave's decoded scale bytes, sl[((rgw * NB + b) * nchunk + c_first + s) * 64 + lane]
+  const uint8_t* xs = x4t_lds + ((int64_t)rgw * NB * nchunk + c_first) * 64 + lane;
+  auto compute = [&](const WBuf& W, const ABuf& A, int s) {
+    uint32_t ws[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) ws[b] = X4T ? (uint32_t)xs[((int64_t)b * nchunk + s) * 64] : W.ws[b];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       const bf16x8_t fa = __builtin_bit_cast(bf16x8_t, A.v[t]);
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
-        const bf16x8_t fb = gemm::dequant8<1>(u32x2_t{W.w[b][t], 0u}, W.ws[b]);
+        const bf16x8_t fb = gemm::dequant8<1>(u32x2_t{W.w[b][t], 0u}, ws[b]);
         acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa, fb, acc[b], 0, 0, 0);
       }
     }
@@ -497,6 +645,7 @@ __global__ __launch_bounds__(S * RW * 64) void moe_small_kernel(
   if constexpr (STEPS > 0) {
 #pragma unroll
     for (int s = 0; s < P && s < STEPS; ++s) load_a(s, ab[s]);
+    if constexpr (X4T) x4t_finish<GATEUP, NB, NBP, NRB, T>(xg, e, tile0, (int)nchunk, pd, x4t_lds);
 #pragma unroll
     for (int s = 0; s < STEPS; ++s) {
       if (s + P < STEPS) {
@@ -504,7 +653,7 @@ __global__ __launch_bounds__(S * RW * 64) void moe_small_kernel(
         load_a(s + P, ab[(s + P) % NBUF]);
       }
       __builtin_amdgcn_sched_barrier(0);
-      compute(wb[s % NBUF], ab[s % NBUF]);
+      compute(wb[s % NBUF], ab[s % NBUF], s);
       __builtin_amdgcn_sched_barrier(0);
     }
   } else {
@@ -513,17 +662,18 @@ __global__ __launch_bounds__(S * RW * 64) void moe_small_kernel(
     const int last = steps - 1;
     load_w(0, wb[0]);
     load_a(0, ab[0]);
+    if constexpr (X4T) x4t_finish<GATEUP, NB, NBP, NRB, T>(xg, e, tile0, (int)nchunk, pd, x4t_lds);
     for (int s = 0; s < steps; s += 2) {
       const int s1 = s + 1 < last ? s + 1 : last, s2 = s + 2 < last ? s + 2 : last;
       load_w(s1, wb[1]);
       load_a(s1, ab[1]);
       __builtin_amdgcn_sched_barrier(0);
-      compute(wb[0], ab[0]);
+      compute(wb[0], ab[0], s);
       __builtin_amdgcn_sched_barrier(0);
       load_w(s2, wb[0]);
       load_a(s2, ab[0]);
       __builtin_amdgcn_sched_barrier(0);
-      if (s + 1 < steps) compute(wb[1], ab[1]);
+      if (s + 1 < steps) compute(wb[1], ab[1], s + 1);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
@@ -579,19 +729,26 @@ __global__ __launch_bounds__(S * RW * 64) void moe_small_kernel(
 // tile and block g, and the scales of (slot m, block g) and (row m, block g).
 typedef int i32x8_t __attribute__((ext_vector_type(8)));
 
-template <bool GATEUP, int AF, int NBP, int S, int RW, int P, int STEPS>
+template <bool GATEUP, bool X4T, int AF, int NBP, int S, int RW, int P, int STEPS>
 __global__ __launch_bounds__(S * RW * 64) void moe_small_mx_kernel(
     const uint8_t* __restrict__ aq, const uint8_t* __restrict__ as, int topk,
     const int* __restrict__ sorted, const int* __restrict__ small_list,
     const uint8_t* __restrict__ wt, const uint8_t* __restrict__ wst, const int* __restrict__ sslot,
-    int64_t rows_per_expert, int64_t K, int64_t inter, ActParams act, const float* __restrict__ route_w,
-    uint16_t* __restrict__ act_out, float* __restrict__ y_out, int64_t hidden) {
+    X4TGemv xg, int64_t rows_per_expert, int64_t K, int64_t inter, ActParams act,
+    const float* __restrict__ route_w, uint16_t* __restrict__ act_out, float* __restrict__ y_out,
+    int64_t hidden) {
   constexpr int NB = GATEUP ? 2 * NBP : NBP;
   constexpr int CH = RW * 16 * NBP;
   constexpr int NBUF = P + 1;
   constexpr int ABYTES = AF == 4 ? 64 : 128;      // A bytes per row per 128-k chunk
+  constexpr int T = S * RW * 64, NRB = RW * NB;
+  static_assert(NB * 33 <= 128 * S, "fixed tiles of the row blocks: at most two 16-byte loads per thread");
+  extern __shared__ __attribute__((aligned(16))) unsigned char x4t_lds[];
   const int e = small_list[3 * blockIdx.x];
   if (e < 0) return;
+  X4TPending pd;
+  const int64_t tile0 = (int64_t)blockIdx.y * RW * NBP;
+  if constexpr (X4T) x4t_issue<GATEUP, NB, NBP, NRB, T>(xg, e, tile0, pd);
   const int beg = small_list[3 * blockIdx.x + 1];
   const int n = small_list[3 * blockIdx.x + 2];
   const int se = sslot ? sslot[e] : e;            // scale slot of the expert
@@ -624,7 +781,7 @@ __global__ __launch_bounds__(S * RW * 64) void moe_small_mx_kernel(
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
       B.w[b] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(wtile[b] + (int64_t)s * 1024));
-      B.ws[b] = stile[b][(int64_t)s * 64];
+      if constexpr (!X4T) B.ws[b] = stile[b][(int64_t)s * 64];
     }
   };
   WBuf wb[NBUF];
@@ -652,7 +809,8 @@ __global__ __launch_bounds__(S * RW * 64) void moe_small_mx_kernel(
   f32x4_t acc[NB];
 #pragma unroll
   for (int b = 0; b < NB; ++b) acc[b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  auto compute = [&](const WBuf& W, const ABuf& A) {
+  const uint8_t* xs = x4t_lds + ((int64_t)rgw * NB * nchunk + c_first) * 64 + lane;
+  auto compute = [&](const WBuf& W, const ABuf& A, int s) {
     i32x8_t a8;
     if (AF == 4) {
       a8 = i32x8_t{(int)A.v[0][0], (int)A.v[0][1], (int)A.v[0][2], (int)A.v[0][3], 0, 0, 0, 0};
@@ -664,13 +822,14 @@ __global__ __launch_bounds__(S * RW * 64) void moe_small_mx_kernel(
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
       const i32x8_t w8 = i32x8_t{(int)W.w[b][0], (int)W.w[b][1], (int)W.w[b][2], (int)W.w[b][3], 0, 0, 0, 0};
-      acc[b] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a8, w8, acc[b], AF, 4, 0, (int)A.s, 0,
-                                                                (int)W.ws[b]);
+      const int wsb = X4T ? (int)xs[((int64_t)b * nchunk + s) * 64] : (int)W.ws[b];
+      acc[b] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a8, w8, acc[b], AF, 4, 0, (int)A.s, 0, wsb);
     }
   };
   if constexpr (STEPS > 0) {
 #pragma unroll
     for (int s = 0; s < P && s < STEPS; ++s) load_a(s, ab[s]);
+    if constexpr (X4T) x4t_finish<GATEUP, NB, NBP, NRB, T>(xg, e, tile0, (int)nchunk, pd, x4t_lds);
 #pragma unroll
     for (int s = 0; s < STEPS; ++s) {
       if (s + P < STEPS) {
@@ -678,24 +837,25 @@ __global__ __launch_bounds__(S * RW * 64) void moe_small_mx_kernel(
         load_a(s + P, ab[(s + P) % NBUF]);
       }
       __builtin_amdgcn_sched_barrier(0);
-      compute(wb[s % NBUF], ab[s % NBUF]);
+      compute(wb[s % NBUF], ab[s % NBUF], s);
       __builtin_amdgcn_sched_barrier(0);
     }
   } else {
     const int last = steps - 1;
     load_w(0, wb[0]);
     load_a(0, ab[0]);
+    if constexpr (X4T) x4t_finish<GATEUP, NB, NBP, NRB, T>(xg, e, tile0, (int)nchunk, pd, x4t_lds);
     for (int s = 0; s < steps; s += 2) {
       const int s1 = s + 1 < last ? s + 1 : last, s2 = s + 2 < last ? s + 2 : last;
       load_w(s1, wb[1]);
       load_a(s1, ab[1]);
       __builtin_amdgcn_sched_barrier(0);
-      compute(wb[0], ab[0]);
+      compute(wb[0], ab[0], s);
       __builtin_amdgcn_sched_barrier(0);
       load_w(s2, wb[0]);
       load_a(s2, ab[0]);
       __builtin_amdgcn_sched_barrier(0);
-      if (s + 1 < steps) compute(wb[1], ab[1]);
+      if (s + 1 < steps) compute(wb[1], ab[1], s + 1);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
@@ -1478,42 +1638,72 @@ using namespace kq::moe;
 #define KQ_DN_P 2
 #endif
 
+// x4t: the instantiation decoding X4T scales in its prologue, with that
+// decode's dynamic LDS.
 template <bool GATEUP, int NBP, int S, int RW, int P, typename... Args>
-static hipError_t launch_small(int64_t experts_max, int64_t channels, int64_t K, hipStream_t st,
-                               Args... args) {
-  constexpr int CH = RW * 16 * NBP;
+static hipError_t launch_small(bool x4t, int64_t experts_max, int64_t channels, int64_t K, int cols,
+                               hipStream_t st, Args... args) {
+  constexpr int CH = RW * 16 * NBP, NB = GATEUP ? 2 * NBP : NBP;
   const dim3 grid((unsigned)experts_max, (unsigned)(channels / CH));
   const int64_t nchunk = K / 128;
   const int64_t steps = nchunk % S == 0 ? nchunk / S : 0;
+  const size_t shm = x4t ? x4t_gemv_lds(RW * NB, nchunk, cols) : 0;
   switch (steps) {
-#define KQ_SMALL_CASE(N) \
-    case N: moe_small_kernel<GATEUP, NBP, S, RW, P, N><<<grid, S * RW * 64, 0, st>>>(args...); break;
+#define KQ_SMALL_CASE(N)                                                                        \
+    case N:                                                                                     \
+      if (x4t) moe_small_kernel<GATEUP, true, NBP, S, RW, P, N><<<grid, S * RW * 64, shm, st>>>(args...); \
+      else moe_small_kernel<GATEUP, false, NBP, S, RW, P, N><<<grid, S * RW * 64, 0, st>>>(args...);       \
+      break;
     KQ_SMALL_CASE(2) KQ_SMALL_CASE(4) KQ_SMALL_CASE(7) KQ_SMALL_CASE(8) KQ_SMALL_CASE(14)
     KQ_SMALL_CASE(16) KQ_SMALL_CASE(28)
 #undef KQ_SMALL_CASE
     default:
-      moe_small_kernel<GATEUP, NBP, S, RW, P, 0><<<grid, S * RW * 64, 0, st>>>(args...);
+      if (x4t) moe_small_kernel<GATEUP, true, NBP, S, RW, P, 0><<<grid, S * RW * 64, shm, st>>>(args...);
+      else moe_small_kernel<GATEUP, false, NBP, S, RW, P, 0><<<grid, S * RW * 64, 0, st>>>(args...);
   }
   return hipGetLastError();
 }
 
 template <bool GATEUP, int AF, int NBP, int S, int RW, int P, typename... Args>
-static hipError_t launch_small_mx(int64_t experts_max, int64_t channels, int64_t K, hipStream_t st,
-                                  Args... args) {
-  constexpr int CH = RW * 16 * NBP;
+static hipError_t launch_small_mx(bool x4t, int64_t experts_max, int64_t channels, int64_t K, int cols,
+                                  hipStream_t st, Args... args) {
+  constexpr int CH = RW * 16 * NBP, NB = GATEUP ? 2 * NBP : NBP;
   const dim3 grid((unsigned)experts_max, (unsigned)(channels / CH));
   const int64_t nchunk = K / 128;
   const int64_t steps = nchunk % S == 0 ? nchunk / S : 0;
+  const size_t shm = x4t ? x4t_gemv_lds(RW * NB, nchunk, cols) : 0;
   switch (steps) {
-#define KQ_SMALL_MX_CASE(N) \
-    case N: moe_small_mx_kernel<GATEUP, AF, NBP, S, RW, P, N><<<grid, S * RW * 64, 0, st>>>(args...); break;
+#define KQ_SMALL_MX_CASE(N)                                                                                \
+    case N:                                                                                                \
+      if (x4t) moe_small_mx_kernel<GATEUP, true, AF, NBP, S, RW, P, N><<<grid, S * RW * 64, shm, st>>>(args...); \
+      else moe_small_mx_kernel<GATEUP, false, AF, NBP, S, RW, P, N><<<grid, S * RW * 64, 0, st>>>(args...);       \
+      break;
     KQ_SMALL_MX_CASE(2) KQ_SMALL_MX_CASE(4) KQ_SMALL_MX_CASE(7) KQ_SMALL_MX_CASE(8) KQ_SMALL_MX_CASE(14)
     KQ_SMALL_MX_CASE(16)
 #undef KQ_SMALL_MX_CASE
     default:
-      moe_small_mx_kernel<GATEUP, AF, NBP, S, RW, P, 0><<<grid, S * RW * 64, 0, st>>>(args...);
+      if (x4t) moe_small_mx_kernel<GATEUP, true, AF, NBP, S, RW, P, 0><<<grid, S * RW * 64, shm, st>>>(args...);
+      else moe_small_mx_kernel<GATEUP, false, AF, NBP, S, RW, P, 0><<<grid, S * RW * 64, 0, st>>>(args...);
   }
   return hipGetLastError();
+}
+
+// The GEMV kernels' X4T planes from the expansion's plane descriptors:
+// w1 / w3 for gate/up, w2 for down (or nothing without X4T scales).
+static X4TGemv x4t_gemv(const X4TExpandArgs* xa, bool gateup) {
+  X4TGemv g{};
+  if (!xa) return g;
+  const X4TPlane& p0 = gateup ? xa->p[0] : xa->p[2];
+  const X4TPlane& p1 = gateup ? xa->p[1] : xa->p[2];
+  g.fixed[0] = p0.fixed;
+  g.fixed[1] = p1.fixed;
+  g.exc[0] = p0.exceptions;
+  g.exc[1] = p1.exceptions;
+  g.idx[0] = p0.tile_index;
+  g.idx[1] = p1.tile_index;
+  g.tiles = p0.tiles;
+  g.cols = p0.cols;
+  return g;
 }
 
 // Activation-quantized forward (W4A8 / W4A4): the same routing and combine,
@@ -1523,8 +1713,8 @@ template <int AF>
 static int moe_forward_mx(const Layout& L, unsigned char* w, const ActParams& ap, const void* x,
                           int64_t ldx, int64_t tokens, int64_t hidden, const float* route_weights,
                           int topk, int64_t inter, const uint8_t* w13_t, const uint8_t* w13_st,
-                          const uint8_t* w2_t, const uint8_t* w2_st, const int* sslot, bool decode,
-                          int grid_dma, void* stream) {
+                          const uint8_t* w2_t, const uint8_t* w2_st, const int* sslot,
+                          const X4TExpandArgs* xa, bool decode, int grid_dma, void* stream) {
   hipStream_t st = (hipStream_t)stream;
   const int fmt = AF == 4 ? KQ_FMT_MXFP4_E2M1 : KQ_FMT_MXFP8_E4M3;
   const int* offsets = (const int*)(w + L.offsets);
@@ -1539,9 +1729,11 @@ static int moe_forward_mx(const Layout& L, unsigned char* w, const ActParams& ap
   hipError_t e;
   int rc = kq_mx_quantize(fmt, KQ_DT_BF16, x, ldx, tokens, hidden, xq, xs, 0, stream);
   if (rc != KQ_OK) return rc;
+  const int* gslot = xa ? nullptr : sslot;  // the GEMVs decode X4T scales themselves
   e = launch_small_mx<true, AF, KQ_GU_NBP, KQ_GU_S, KQ_GU_RW, KQ_GU_P>(
-      L.max_list, inter, hidden, st, (const uint8_t*)xq, (const uint8_t*)xs, topk, sorted, small_list,
-      w13_t, w13_st, sslot, 2 * inter, hidden, inter, ap, route_weights, act, y, hidden);
+      xa != nullptr, L.max_list, inter, hidden, (int)(hidden / 32), st, (const uint8_t*)xq,
+      (const uint8_t*)xs, topk, sorted, small_list, w13_t, w13_st, gslot, x4t_gemv(xa, true), 2 * inter,
+      hidden, inter, ap, route_weights, act, y, hidden);
   if (e != hipSuccess) return kq_check_launch(e, "kq_moe_forward/gateup_small");
   const int64_t abytes = AF == 4 ? hidden / 2 : hidden;
   if (any_large) {
@@ -1554,8 +1746,9 @@ static int moe_forward_mx(const Layout& L, unsigned char* w, const ActParams& ap
   rc = kq_mx_quantize(fmt, KQ_DT_BF16, act, inter, L.pairs, inter, aq, as, 0, stream);
   if (rc != KQ_OK) return rc;
   e = launch_small_mx<false, AF, KQ_DN_NBP, KQ_DN_S, KQ_DN_RW, KQ_DN_P>(
-      L.max_list, hidden, inter, st, (const uint8_t*)aq, (const uint8_t*)as, topk, sorted, small_list,
-      w2_t, w2_st, sslot, hidden, inter, inter, ap, route_weights, act, y, hidden);
+      xa != nullptr, L.max_list, hidden, inter, (int)(inter / 32), st, (const uint8_t*)aq,
+      (const uint8_t*)as, topk, sorted, small_list, w2_t, w2_st, gslot, x4t_gemv(xa, false), hidden, inter,
+      inter, ap, route_weights, act, y, hidden);
   if (e != hipSuccess) return kq_check_launch(e, "kq_moe_forward/down_small");
   if (any_large) {
     const int64_t ibytes = AF == 4 ? inter / 2 : inter;
@@ -1638,8 +1831,7 @@ static int moe_forward_impl(const char* fn, int activation, float act_beta, floa
 
   if (decode) {
     route_decode_kernel<<<1, DECODE_MAX_PAIRS, 0, st>>>(route_ids, (int)L.pairs, experts, sorted,
-                                                         small_list, (int)L.max_list, meta, rank_of,
-                                                         routed, max_routed);
+                                                         small_list, (int)L.max_list, meta);
     if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_moe_forward/route");
   } else if (L.pairs <= PREP_ONE) {
     route_prep_one_kernel<<<1, 1024, 0, st>>>(route_ids, (int)L.pairs, experts, counts, offsets,
@@ -1666,7 +1858,8 @@ static int moe_forward_impl(const char* fn, int activation, float act_beta, floa
     w13_st = w + L.s13;
     w2_st = w + L.s2;
   }
-  const int* sslot = rank_of;
+  const int* sslot = rank_of;                // grouped-GEMM experts' scale slots
+  const int* gslot = nullptr;                // the GEMVs read dense scales or decode X4T ones
 
   auto combine = [&]() -> int {
     const dim3 cgrid((unsigned)((hidden / 4 + 255) / 256), (unsigned)tokens);
@@ -1691,9 +1884,9 @@ static int moe_forward_impl(const char* fn, int activation, float act_beta, floa
     }
     const int rc = act_fmt == 4
         ? moe_forward_mx<4>(L, w, ap, x, ldx, tokens, hidden, route_weights, topk, inter, w13_t, w13_st,
-                            w2_t, w2_st, sslot, decode, grid_mx, stream)
+                            w2_t, w2_st, sslot, xa, decode, grid_mx, stream)
         : moe_forward_mx<0>(L, w, ap, x, ldx, tokens, hidden, route_weights, topk, inter, w13_t, w13_st,
-                            w2_t, w2_st, sslot, decode, grid_mx, stream);
+                            w2_t, w2_st, sslot, xa, decode, grid_mx, stream);
     if (rc != KQ_OK) return rc;
     return combine();
   }
@@ -1702,8 +1895,9 @@ static int moe_forward_impl(const char* fn, int activation, float act_beta, floa
   // gate/up
   {
     e = launch_small<true, KQ_GU_NBP, KQ_GU_S, KQ_GU_RW, KQ_GU_P>(
-        L.max_list, inter, hidden, st, xb, ldx, topk, (const int*)sorted, (const int*)small_list,
-        w13_t, w13_st, sslot, 2 * inter, hidden, inter, ap, route_weights, act, y, hidden);
+        xa != nullptr, L.max_list, inter, hidden, (int)(hidden / 32), st, xb, ldx, topk, (const int*)sorted,
+        (const int*)small_list, w13_t, w13_st, gslot, x4t_gemv(xa, true), 2 * inter, hidden, inter, ap,
+        route_weights, act, y, hidden);
     if (e != hipSuccess) return kq_check_launch(e, "kq_moe_forward/gateup_small");
   }
   const size_t lds = 2 * (size_t)STAGE + BM * sizeof(int);
@@ -1740,9 +1934,9 @@ static int moe_forward_impl(const char* fn, int activation, float act_beta, floa
   // down
   {
     e = launch_small<false, KQ_DN_NBP, KQ_DN_S, KQ_DN_RW, KQ_DN_P>(
-        L.max_list, hidden, inter, st, (const uint16_t*)act, inter, topk, (const int*)sorted,
-        (const int*)small_list, w2_t, w2_st, sslot, hidden, inter, inter, ap, route_weights, act, y,
-        hidden);
+        xa != nullptr, L.max_list, hidden, inter, (int)(inter / 32), st, (const uint16_t*)act, inter, topk,
+        (const int*)sorted, (const int*)small_list, w2_t, w2_st, gslot, x4t_gemv(xa, false), hidden, inter,
+        inter, ap, route_weights, act, y, hidden);
     if (e != hipSuccess) return kq_check_launch(e, "kq_moe_forward/down_small");
   }
   if (any_large && dma_path) {

@@ -308,55 +308,91 @@ __global__ __launch_bounds__(256) void x4t_tile_index_kernel(
 }
 
 // Runtime expansion of routed experts' X4T scales (one launch, no search, no
-// allocation).  Block (r, y): y runs over the 16-row tiles of every plane in
-// turn; the block decodes that tile of matrix routed[r] (nothing when -1) -
-// base + selector bit, then the tile's exceptions from the precomputed index -
-// into LDS and writes it to slot r of the plane's output in the
-// kq_mx_tile_weights scale layout: 64-byte tiles [row group][cols / 4] with
-// byte l = scale[16 rg + l % 16][4 c + l / 16].
+// allocation).  Block (r, y) takes X4T_EXPAND_TILES consecutive 16-row tiles
+// of one plane (y runs over every plane's tile groups in turn) of matrix
+// routed[r] (nothing when -1): their fixed bytes (contiguous) are staged in
+// LDS with 16-byte loads, decoded - base + selector bit - straight into the
+// kq_mx_tile_weights scale layout in LDS (64-byte tiles [row group][cols / 4],
+// byte l = scale[16 rg + l % 16][4 c + l / 16]), patched with the group's
+// exceptions (one contiguous range of the sorted stream, from the precomputed
+// tile index) and copied to slot r of the plane's output with 16-byte stores.
+constexpr int X4T_EXPAND_TILES = 8;
+constexpr int X4T_MAX_PIECES = X4T_EXPAND_TILES * 33;  // 16-byte pieces of 8 fixed tiles, cols <= 255
+
 __global__ __launch_bounds__(SP_THREADS) void x4t_expand_tiled_kernel(X4TExpandArgs a,
                                                                        const int* __restrict__ routed) {
+  constexpr int G = X4T_EXPAND_TILES, U = 4;
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
   const int e = routed[blockIdx.x];
   if (e < 0) return;
-  int64_t t = blockIdx.y;
+  int64_t grp = blockIdx.y;
   int pi = 0;
-  if (t >= a.p[0].tiles) {
-    t -= a.p[0].tiles;
+  if (grp >= a.p[0].tiles / G) {
+    grp -= a.p[0].tiles / G;
     pi = 1;
-    if (a.n > 2 && t >= a.p[1].tiles) {
-      t -= a.p[1].tiles;
+    if (a.n > 2 && grp >= a.p[1].tiles / G) {
+      grp -= a.p[1].tiles / G;
       pi = 2;
     }
   }
   const X4TPlane P = pi == 0 ? a.p[0] : pi == 1 ? a.p[1] : a.p[2];
-  __shared__ uint8_t buf[X4T_ROWS * 256];
-  const int cols = P.cols, sb = (cols + 7) >> 3, span = X4T_ROWS * cols;
-  const int64_t ti = (int64_t)e * P.tiles + t;
-  const uint8_t* f = P.fixed + ti * (X4T_ROWS * (1 + sb));
-  for (int p = threadIdx.x; p < span; p += SP_THREADS) {
-    const int i = p / cols, c = p - i * cols;
-    buf[p] = (uint8_t)(f[i] + ((f[X4T_ROWS + i * sb + (c >> 3)] >> (c & 7)) & 1));
+  __shared__ __attribute__((aligned(16))) uint8_t buf[G * X4T_ROWS * 256];
+  __shared__ __attribute__((aligned(16))) uint8_t fl[X4T_MAX_PIECES * 16];
+  const int tid = threadIdx.x;
+  const int cols = P.cols, sb = (cols + 7) >> 3, tp = 1 + sb, span = X4T_ROWS * cols, nchunk = cols >> 2;
+  const int64_t t0 = grp * G, ti0 = (int64_t)e * P.tiles + t0;
+  const uint8_t* fsrc = P.fixed + ti0 * (16 * tp);
+  u32x4 pc[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+    if (tid + u * SP_THREADS < G * tp) pc[u] = *reinterpret_cast<const u32x4*>(fsrc + 16 * (tid + u * SP_THREADS));
+  const uint32_t lo = P.tile_index[ti0], hi = P.tile_index[ti0 + G];
+  const int total = hi > lo ? (int)(hi - lo) : 0;
+  uint32_t wv[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+    if (tid + u * SP_THREADS < total) wv[u] = P.exceptions[lo + tid + u * SP_THREADS];
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+    if (tid + u * SP_THREADS < G * tp) *reinterpret_cast<u32x4*>(fl + 16 * (tid + u * SP_THREADS)) = pc[u];
+  __syncthreads();
+  // dword j of a tile: chunk j / 16, bytes l = 4 (j % 16) .. + 3, i.e. rows
+  // 4 (j % 4) .. + 3 of column 4 (j / 16) + (j % 16) / 4
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const uint8_t* f = fl + g * 16 * tp;
+    for (int j = tid; j < nchunk * 16; j += SP_THREADS) {
+      const int w = j & 15, r0 = 4 * (w & 3), c = 4 * (j >> 4) + (w >> 2);
+      const uint32_t base4 = *reinterpret_cast<const uint32_t*>(f + r0);
+      const uint8_t* sel = f + X4T_ROWS + r0 * sb + (c >> 3);
+      uint32_t v = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        v |= (((base4 >> (8 * i)) + ((sel[i * sb] >> (c & 7)) & 1)) & 0xffu) << (8 * i);
+      *reinterpret_cast<uint32_t*>(buf + (g * nchunk + (j >> 4)) * 64 + 4 * w) = v;
+    }
   }
   __syncthreads();
-  const uint32_t lo = P.tile_index[ti], hi = P.tile_index[ti + 1];
-  const uint32_t pos0 = (uint32_t)(t * span);
-  for (uint32_t k = lo + threadIdx.x; k < hi; k += SP_THREADS) {
-    const uint32_t w = P.exceptions[k];
-    const uint32_t off = (w & X4T_POS_MASK) - pos0;  // wraps past span when outside the tile
-    if (off < (uint32_t)span) buf[off] = (uint8_t)(w >> 24);
+  const uint32_t pos0 = (uint32_t)(t0 * span);
+  for (int base = 0; base < total; base += U * SP_THREADS) {
+    if (base > 0) {
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (base + tid + u * SP_THREADS < total) wv[u] = P.exceptions[lo + base + tid + u * SP_THREADS];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (base + tid + u * SP_THREADS >= total) continue;
+      const uint32_t off = (wv[u] & X4T_POS_MASK) - pos0;  // wraps past the group when outside it
+      if (off >= (uint32_t)(G * span)) continue;
+      const int g = (int)off / span, rem = (int)off - g * span;
+      const int r = rem / cols, c = rem - r * cols;
+      buf[(g * nchunk + (c >> 2)) * 64 + (c & 3) * 16 + r] = (uint8_t)(wv[u] >> 24);
+    }
   }
   __syncthreads();
-  // dword j of the tile row group: chunk j / 16, lanes 4 (j % 16) .. + 3 =
-  // rows 4 (j % 4) .. + 3 of column 4 (j / 16) + (j % 16) / 4
-  const int nchunk = cols >> 2;
-  uint32_t* dst = reinterpret_cast<uint32_t*>(
-      P.out + (((int64_t)blockIdx.x * P.out_rgs + P.out_rg0 + t) * nchunk) * 64);
-  for (int j = threadIdx.x; j < nchunk * 16; j += SP_THREADS) {
-    const int c = 4 * (j >> 4) + ((j & 15) >> 2);
-    const uint8_t* src = buf + 4 * (j & 3) * cols + c;
-    dst[j] = (uint32_t)src[0] | (uint32_t)src[cols] << 8 | (uint32_t)src[2 * cols] << 16 |
-             (uint32_t)src[3 * cols] << 24;
-  }
+  u32x4* dst = reinterpret_cast<u32x4*>(P.out + (((int64_t)blockIdx.x * P.out_rgs + P.out_rg0 + t0) * nchunk) * 64);
+  for (int i = tid; i < G * span / 16; i += SP_THREADS) dst[i] = reinterpret_cast<const u32x4*>(buf)[i];
 }
 
 // status: {selector padding, first bad position index, first redundant value
@@ -998,10 +1034,14 @@ extern "C" int kq_x4t_tile_index(const uint32_t* exceptions, int64_t n_exception
 
 namespace kq {
 hipError_t x4t_expand_routed(const X4TExpandArgs& args, const int* routed, int max_routed, hipStream_t st) {
-  int64_t tiles = 0;
-  for (int i = 0; i < args.n; ++i) tiles += args.p[i].tiles;
-  if (max_routed <= 0 || tiles == 0) return hipSuccess;
-  x4t_expand_tiled_kernel<<<dim3((unsigned)max_routed, (unsigned)tiles), SP_THREADS, 0, st>>>(args, routed);
+  int64_t groups = 0;
+  for (int i = 0; i < args.n; ++i) {
+    if (args.p[i].tiles % X4T_EXPAND_TILES != 0 || args.p[i].cols % 4 != 0 || args.p[i].cols > 255)
+      return hipErrorInvalidValue;
+    groups += args.p[i].tiles / X4T_EXPAND_TILES;
+  }
+  if (max_routed <= 0 || groups == 0) return hipSuccess;
+  x4t_expand_tiled_kernel<<<dim3((unsigned)max_routed, (unsigned)groups), SP_THREADS, 0, st>>>(args, routed);
   return hipGetLastError();
 }
 }  // namespace kq
