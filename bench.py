@@ -48,10 +48,17 @@ def _args():
     return p.parse_args()
 
 
-def _time_loop(torch, fn, steps: int, warmup: int) -> float:
-    """Average seconds per call with HIP events on the current stream."""
-    for _ in range(warmup):
+def _time_loop(torch, fn, steps: int, warmup: int, warm_s: float = 0.0) -> float:
+    """Average seconds per call with HIP events on the current stream, after
+    ``warmup`` calls and at least ``warm_s`` seconds of them (the clocks of a
+    long MFMA-bound kernel settle over the first ~100 ms of sustained load)."""
+    t0 = time.perf_counter()
+    done = 0
+    while done < warmup or time.perf_counter() - t0 < warm_s:
         fn()
+        done += 1
+        if warm_s and done % 4 == 0:
+            torch.cuda.synchronize()
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     stop = torch.cuda.Event(enable_timing=True)
@@ -159,7 +166,7 @@ def main() -> int:
                    x2.shape[0], rows, cols, N.DT_BF16, N.ptr(out2), rows, stream)
 
         quantize_step()
-        t_gemm = _time_loop(torch, gemm_step, max(5, args.steps // 5), 3)
+        t_gemm = _time_loop(torch, gemm_step, max(5, args.steps // 5), 3, 0.3)
         flops = 2.0 * x2.shape[0] * rows * cols
         result["cfg2_mxfp8_linear"] = {
             "workload": "X[4096x7168] bf16 @ dequant(MXFP8 W[12288x7168])^T -> bf16, fp32 accumulate",
@@ -185,7 +192,7 @@ def main() -> int:
         def moe_step():
             moe.grouped_expert_forward(x3, ids_d, rw_d, weights)
 
-        t_moe = _time_loop(torch, moe_step, max(3, args.steps // 10), 2)
+        t_moe = _time_loop(torch, moe_step, max(3, args.steps // 10), 2, 0.3)
         flops = workloads.moe_flops(ids.numel())
         tflops = flops / t_moe / 1e12
         wbytes = len(active) * workloads.bytes_per_expert()
@@ -205,7 +212,7 @@ def main() -> int:
         def moe_x4t_step():
             moe.grouped_expert_forward(x3, ids_d, rw_d, x4t_scales)
 
-        t_x4t = _time_loop(torch, moe_x4t_step, max(3, args.steps // 10), 2)
+        t_x4t = _time_loop(torch, moe_x4t_step, max(3, args.steps // 10), 2, 0.3)
         moe_result["x4t_scales_ms"] = round(t_x4t * 1e3, 3)
         moe_result["x4t_added_us"] = round((t_x4t - t_moe) * 1e6, 1)
         del x4t_scales
@@ -217,7 +224,7 @@ def main() -> int:
             def mx_step(fmt=fmt):
                 moe.grouped_expert_forward(x3, ids_d, rw_d, weights, activation_format=fmt)
 
-            t_mx = _time_loop(torch, mx_step, max(3, args.steps // 10), 2)
+            t_mx = _time_loop(torch, mx_step, max(3, args.steps // 10), 2, 0.3)
             tf = flops / t_mx / 1e12
             result[f"cfg3_moe_prefill_{'w4a8' if fmt == 'mxfp8' else 'w4a4'}"] = {
                 "workload": f"cfg3 shapes, activations {fmt.upper()}-quantized per row, block-scaled MFMA",
