@@ -54,6 +54,9 @@ enum { KQ_MOE_REGISTER_STAGED = 1u };
 enum { KQ_MOE_ACT_MXFP8 = 2u, KQ_MOE_ACT_MXFP4 = 4u };
 /* kq_syrk_accumulate flags */
 enum { KQ_SYRK_OVERWRITE = 1u, KQ_SYRK_SQUARE_WEIGHTS = 2u, KQ_SUM_SQUARE_F64 = 4u };
+/* kq_block_ldl flags: also zero the diagonal (finalize_capture_H's
+   L[dr, dr] = 0, kquant/exl3_encoder_backend.py:1649-1651) */
+enum { KQ_LDL_ZERO_DIAGONAL = 1u };
 /* byte tables of kq_decode_bytes */
 enum { KQ_TABLE_E8M0 = 0, KQ_TABLE_E2M1 = 1, KQ_TABLE_E4M3 = 2 };
 /* expert activations */
@@ -282,6 +285,55 @@ int kq_sym_lerp(const float* a, float a_scale, const float* b, int64_t k, float 
  * doubles {trace, sum of squares}, both device memory. */
 #define KQ_COV_STATS_PARTS 256
 int kq_cov_stats(const float* h, int64_t k, double* workspace, double* out, void* stream);
+
+/* ------------------------------------------------ H finalize / block LDL --
+ * The Hessian finalize of the trellis encoder
+ * (kquant/exl3_encoder_backend.py:1588-1663, finalize_capture_H, and
+ * :316-386, block_ldl), fp32 device matrices, row-major. */
+
+/* H *= 1 / count (skipped when count == 0), then
+ * diag(H) += sigma_reg * mean(diag(H)) (exl3_encoder_backend.py:1611-1628;
+ * the mean is summed in f64 and rounded to fp32).  diag_mean: one float
+ * (device) receiving the mean before damping; diag: k floats receiving the
+ * damped diagonal, or NULL.  k <= 65535. */
+int kq_h_regularize(float* h, int64_t k, int64_t ld, double count, float sigma_reg, float* diag,
+                    float* diag_mean, void* stream);
+
+/* In place X <- B S_r X S_c B over `batch` matrices [rows, cols] (row stride
+ * ld, matrix stride `stride`), B = blockdiag of the 128 x 128 Sylvester
+ * Hadamard / sqrt(128) (kquant/exl3_reference.py:195-212).  sides: 1 = left
+ * only (blockwise_preapply_had_l_, exl3_encoder_backend.py:288-299), 2 =
+ * right only (blockwise_preapply_had_r_, :302-313), 3 = both (the rotation
+ * of finalize_capture_H, :1640-1644, with H *= su^T before the right side
+ * and H *= su before the left: row_scale = col_scale = su).  row_scale /
+ * col_scale: fp32 vectors or NULL.  The transformed dimensions must be
+ * multiples of 128.  Results equal the reference's fp32 matmuls up to fp32
+ * rounding (the transform here is a fast Walsh-Hadamard, adds only). */
+int kq_blockwise_hadamard(float* x, int64_t rows, int64_t cols, int64_t ld, int64_t batch,
+                          int64_t stride, int sides, const float* row_scale, const float* col_scale,
+                          void* stream);
+
+/* Lower Cholesky factors L (A = L L^T, zeros above the diagonal) of `batch`
+ * symmetric fp32 matrices [n, n]: torch.linalg.cholesky's output
+ * (exl3_encoder_backend.py:325-330).  Only the lower triangle of A is read;
+ * a == l (same ld and stride) factors in place.  info: batch int32 (device),
+ * 0 on success, else the order of the first leading minor that is not
+ * positive definite (LAPACK's convention; the factor is then meaningless).
+ * workspace: kq_cholesky_workspace_size bytes.  n, batch <= 65535. */
+int64_t kq_cholesky_workspace_size(int64_t n, int64_t batch);
+int kq_cholesky(const float* a, int64_t lda, int64_t stride_a, float* l, int64_t ldl,
+                int64_t stride_l, int64_t n, int64_t batch, int32_t* info, void* workspace,
+                int64_t workspace_bytes, void* stream);
+
+/* The block LDL step of exl3_encoder_backend.py:356-384 in place on lower
+ * Cholesky factors: every b x b diagonal block DL_i is inverted, each block
+ * column multiplied by its block's inverse (L[:, i] = L[:, i] inv(DL_i)) and
+ * the diagonal blocks set to the identity; with KQ_LDL_ZERO_DIAGONAL the
+ * diagonal is then zeroed.  b a power of two <= 64, n % b == 0.  workspace:
+ * kq_block_ldl_workspace_size bytes. */
+int64_t kq_block_ldl_workspace_size(int64_t n, int b, int64_t batch);
+int kq_block_ldl(float* l, int64_t ld, int64_t stride, int64_t n, int b, int64_t batch,
+                 uint32_t flags, void* workspace, int64_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------- scale-plane codecs --
  * Lossless codings of a uint8 E8M0 scale plane [rows, cols], cols <= 255,

@@ -92,7 +92,12 @@ SIGNATURES: dict[str, list] = {
     "kq_syrk_finalize_grouped": [_VP, _I64, _INT, _VP, _VP, _VP],
     "kq_route_sort": [_VP, _I64, _INT, _INT, _VP, _VP, _VP, _VP, _VP, _VP, _I64, _VP],
     "kq_covariance_comparison_sums": [_VP, _VP, _I64, _VP, _VP, _VP],
+    "kq_h_regularize": [_VP, _I64, _I64, _F64, _F32, _VP, _VP, _VP],
+    "kq_blockwise_hadamard": [_VP, _I64, _I64, _I64, _I64, _I64, _INT, _VP, _VP, _VP],
+    "kq_cholesky": [_VP, _I64, _I64, _VP, _I64, _I64, _I64, _I64, _VP, _VP, _I64, _VP],
+    "kq_block_ldl": [_VP, _I64, _I64, _I64, _INT, _I64, _U32, _VP, _I64, _VP],
 }
+LDL_ZERO_DIAGONAL = 1
 SQG_RANK_XOR = 0
 SQG_RANK_MIX = 1
 SQG_RANK_K2_OCTILE = 2
@@ -122,6 +127,10 @@ def library() -> ctypes.CDLL:
         lib.kq_moe_x4t_workspace_size.argtypes = [_I64, _INT, _INT, _I64, _I64]
         lib.kq_mx_linear_f32_workspace_size.restype = ctypes.c_int64
         lib.kq_mx_linear_f32_workspace_size.argtypes = [_I64, _I64]
+        lib.kq_cholesky_workspace_size.restype = ctypes.c_int64
+        lib.kq_cholesky_workspace_size.argtypes = [_I64, _I64]
+        lib.kq_block_ldl_workspace_size.restype = ctypes.c_int64
+        lib.kq_block_ldl_workspace_size.argtypes = [_I64, _INT, _I64]
         lib.kq_route_sort_workspace_size.restype = ctypes.c_int64
         lib.kq_route_sort_workspace_size.argtypes = [_I64, _INT, _INT]
         for name, argtypes in SIGNATURES.items():

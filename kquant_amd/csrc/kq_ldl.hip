@@ -1,0 +1,438 @@
+// Hessian finalize of the trellis encoder on MI355X
+// (kquant/exl3_encoder_backend.py:316-386 block_ldl, :1588-1663
+// finalize_capture_H): diagonal regularization, sign flips with a blockwise
+// Hadamard rotation, a batched blocked Cholesky and the block LDL built on it.
+//
+//  * regularize: H *= 1/count (fp32 reciprocal, as torch divides a tensor by
+//    a host scalar), then diag += sigma * mean(diag) with the mean summed in
+//    f64; the regularized diagonal and its mean are returned.
+//  * rotation: B S_r X S_c B with B = blockdiag(Had_128 / sqrt(128)), the
+//    Sylvester Hadamard of kquant/exl3_reference.py:195-212.  B is block
+//    diagonal, so every 128x128 tile of X transforms on its own: one
+//    workgroup per tile, a fast Walsh-Hadamard transform along the rows and /
+//    or columns in LDS (adds only), then one scale (1/128 exactly for both
+//    sides, fl(1/sqrt(128)) for one).
+//  * Cholesky (lower, fp32): right-looking over 64-column panels, one launch
+//    per step and all matrices of a batch per launch.  The diagonal block is
+//    factored in LDS by one workgroup, which also inverts it; the panel below
+//    is A21 inv(L11)^T and the trailing update A22 -= L21 L21^T, both on
+//    v_mfma_f32_16x16x4f32 from LDS.  A failing pivot (<= 0 or NaN) records
+//    the leading-minor order in info (LAPACK's convention) and the
+//    factorization continues with pivot 1, so every launch still completes.
+//  * block LDL: every b x b diagonal block DL_i of L is inverted, each block
+//    column multiplied by its inverse and the diagonal blocks set to I.
+#include "kq_internal.h"
+
+namespace kq {
+namespace ldl {
+
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int NB = 64;     // Cholesky panel
+constexpr int LD = 68;     // padded LDS row: lane (i, k) of an MFMA read hits bank 4 i + k
+constexpr int HAD = 128;   // Hadamard block
+constexpr int HLD = HAD + 1;
+constexpr int MAX_B = 64;  // block LDL block size limit
+
+// ------------------------------------------------------------ regularize --
+__global__ __launch_bounds__(256) void diag_mean_kernel(const float* __restrict__ h, int64_t k, int64_t ld,
+                                                        float inv, float* __restrict__ mean_out) {
+  __shared__ double part[256];
+  double s = 0.0;
+  for (int64_t i = threadIdx.x; i < k; i += 256) s += (double)(h[i * ld + i] * inv);
+  part[threadIdx.x] = s;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if ((int)threadIdx.x < w) part[threadIdx.x] += part[threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) mean_out[0] = (float)(part[0] / (double)k);
+}
+
+__global__ __launch_bounds__(256) void regularize_kernel(float* __restrict__ h, int64_t k, int64_t ld, float inv,
+                                                         float sigma, const float* __restrict__ mean,
+                                                         float* __restrict__ diag_out) {
+  const int64_t i = blockIdx.y, j = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (j >= k) return;
+  float v = h[i * ld + j];
+  if (inv != 1.f) v *= inv;
+  if (i == j) {
+    v += sigma * mean[0];
+    if (diag_out) diag_out[i] = v;
+  }
+  h[i * ld + j] = v;
+}
+
+// --------------------------------------------------------------- rotation --
+// sides: bit 0 = left (B X: each column of a tile transformed), bit 1 = right
+// (X B: each row).  Row / column scales (or none) apply before the transforms.
+__global__ __launch_bounds__(256) void hadamard_kernel(float* __restrict__ x, int64_t rows, int64_t cols,
+                                                       int64_t ld, int64_t stride, int sides,
+                                                       const float* __restrict__ rs,
+                                                       const float* __restrict__ cs, float post) {
+  __shared__ float t[HAD][HLD];
+  float* X = x + (int64_t)blockIdx.z * stride;
+  const int64_t r0 = (int64_t)blockIdx.y * HAD, c0 = (int64_t)blockIdx.x * HAD;
+  const int tid = threadIdx.x;
+  for (int i = tid; i < HAD * HAD; i += 256) {
+    const int r = i >> 7, c = i & (HAD - 1);
+    float v = 0.f;
+    if (r0 + r < rows && c0 + c < cols) {
+      v = X[(r0 + r) * ld + c0 + c];
+      if (rs) v *= rs[r0 + r];
+      if (cs) v *= cs[c0 + c];
+    }
+    t[r][c] = v;
+  }
+  __syncthreads();
+  // 64 butterflies per line per stage: thread -> (line, pair), pair p of
+  // stage h joins elements c and c + h with c = (p / h) * 2h + p % h
+  if (sides & 2) {
+    for (int h = 1; h < HAD; h <<= 1) {
+      for (int i = tid; i < HAD * (HAD / 2); i += 256) {
+        const int r = i >> 6, p = i & 63;
+        const int c = (p / h) * 2 * h + (p % h);
+        const float a = t[r][c], b = t[r][c + h];
+        t[r][c] = a + b;
+        t[r][c + h] = a - b;
+      }
+      __syncthreads();
+    }
+  }
+  if (sides & 1) {
+    for (int h = 1; h < HAD; h <<= 1) {
+      for (int i = tid; i < HAD * (HAD / 2); i += 256) {
+        const int c = i & (HAD - 1), p = i >> 7;
+        const int r = (p / h) * 2 * h + (p % h);
+        const float a = t[r][c], b = t[r + h][c];
+        t[r][c] = a + b;
+        t[r + h][c] = a - b;
+      }
+      __syncthreads();
+    }
+  }
+  for (int i = tid; i < HAD * HAD; i += 256) {
+    const int r = i >> 7, c = i & (HAD - 1);
+    if (r0 + r < rows && c0 + c < cols) X[(r0 + r) * ld + c0 + c] = t[r][c] * post;
+  }
+}
+
+// --------------------------------------------------------------- Cholesky --
+// L = tril(A) (upper part zero); info = 0.  a and l may be the same buffer.
+__global__ __launch_bounds__(256) void chol_init_kernel(const float* a, int64_t lda, int64_t sa, float* l,
+                                                        int64_t ldl, int64_t sl, int64_t n, int* __restrict__ info) {
+  const int64_t b = blockIdx.z, i = blockIdx.y, j = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i == 0 && j == 0) info[b] = 0;
+  if (j >= n) return;
+  const float v = j <= i ? a[b * sa + i * lda + j] : 0.f;
+  l[b * sl + i * ldl + j] = v;
+}
+
+// Factor the diagonal block of panel p in LDS (padded past n with the
+// identity), write it back (zeros above its diagonal) and its inverse to winv.
+__global__ __launch_bounds__(256) void chol_diag_kernel(float* __restrict__ l, int64_t n, int64_t ldl, int64_t sl,
+                                                        int p, float* __restrict__ winv, int* __restrict__ info) {
+  __shared__ float a[NB][LD];
+  __shared__ float xi[NB][LD];
+  __shared__ int bad;
+  const int64_t b = blockIdx.x;
+  float* L = l + b * sl;
+  const int tid = threadIdx.x;
+  const int64_t c0 = (int64_t)p * NB;
+  const int nb = (int)(n - c0 < NB ? n - c0 : NB);
+  if (tid == 0) bad = 0;
+  for (int i = tid; i < NB * NB; i += 256) {
+    const int r = i / NB, c = i % NB;
+    a[r][c] = (r < nb && c < nb) ? (c <= r ? L[(c0 + r) * ldl + c0 + c] : 0.f) : (r == c ? 1.f : 0.f);
+  }
+  __syncthreads();
+  for (int c = 0; c < NB; ++c) {
+    float d = a[c][c];
+    if (!(d > 0.f)) {
+      if (tid == 0 && bad == 0) bad = (int)(c0 + c + 1);
+      d = 1.f;
+    }
+    const float s = sqrtf(d);
+    __syncthreads();
+    for (int r = c + tid; r < NB; r += 256) a[r][c] = r == c ? s : a[r][c] / s;
+    __syncthreads();
+    const int w = NB - c - 1;
+    for (int i = tid; i < w * w; i += 256) {
+      const int r = c + 1 + i / w, q = c + 1 + i % w;
+      if (q <= r) a[r][q] -= a[r][c] * a[q][c];
+    }
+    __syncthreads();
+  }
+  if (tid < NB) {  // column j of inv(L11) by forward substitution
+    const int j = tid;
+    for (int i = 0; i < j; ++i) xi[i][j] = 0.f;
+    xi[j][j] = 1.f / a[j][j];
+    for (int i = j + 1; i < NB; ++i) {
+      float acc = 0.f;
+      for (int k = j; k < i; ++k) acc += a[i][k] * xi[k][j];
+      xi[i][j] = -acc / a[i][i];
+    }
+  }
+  __syncthreads();
+  float* W = winv + b * NB * NB;
+  for (int i = tid; i < NB * NB; i += 256) {
+    const int r = i / NB, c = i % NB;
+    if (r < nb && c < nb) L[(c0 + r) * ldl + c0 + c] = c <= r ? a[r][c] : 0.f;
+    W[i] = xi[r][c];
+  }
+  if (tid == 0 && bad != 0 && info[b] == 0) info[b] = bad;
+}
+
+// acc (this wave's 32x32 of a 64x64 tile, as 2x2 16x16 blocks) += X Y^T over
+// k < NB, X and Y row-major in LDS.  v_mfma_f32_16x16x4f32: lane l gives
+// A[l % 16][l / 16] and B[l / 16][l % 16]; D block rows 4 (l / 16) + j,
+// column l % 16.
+__device__ __forceinline__ void mm_nt(const float (*X)[LD], const float (*Y)[LD], f32x4_t acc[2][2]) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int rb = 32 * (wave >> 1), cb = 32 * (wave & 1);
+  const int li = lane & 15, lk = lane >> 4;
+#pragma unroll 4
+  for (int k = 0; k < NB; k += 4) {
+    const float a0 = X[rb + li][k + lk], a1 = X[rb + 16 + li][k + lk];
+    const float b0 = Y[cb + li][k + lk], b1 = Y[cb + 16 + li][k + lk];
+    acc[0][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, b0, acc[0][0], 0, 0, 0);
+    acc[0][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, b1, acc[0][1], 0, 0, 0);
+    acc[1][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, b0, acc[1][0], 0, 0, 0);
+    acc[1][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, b1, acc[1][1], 0, 0, 0);
+  }
+}
+
+// Load rows [r0, r0 + 64) x cols [c0, c0 + 64) of M (zero past n).
+__device__ __forceinline__ void load_tile(float (*T)[LD], const float* M, int64_t ld, int64_t n, int64_t r0,
+                                          int64_t c0) {
+  for (int i = threadIdx.x; i < NB * NB; i += 256) {
+    const int r = i / NB, c = i % NB;
+    T[r][c] = (r0 + r < n && c0 + c < n) ? M[(r0 + r) * ld + c0 + c] : 0.f;
+  }
+}
+
+// Panel: L[i, p] = A[i, p] inv(L[p, p])^T for row block i = p + 1 + blockIdx.x.
+__global__ __launch_bounds__(256) void chol_panel_kernel(float* __restrict__ l, int64_t n, int64_t ldl, int64_t sl,
+                                                         int p, const float* __restrict__ winv) {
+  __shared__ float av[NB][LD];
+  __shared__ float iv[NB][LD];
+  const int64_t b = blockIdx.y;
+  float* L = l + b * sl;
+  const int64_t r0 = (int64_t)(p + 1 + blockIdx.x) * NB, c0 = (int64_t)p * NB;
+  load_tile(av, L, ldl, n, r0, c0);
+  const float* W = winv + b * NB * NB;
+  for (int i = threadIdx.x; i < NB * NB; i += 256) iv[i / NB][i % NB] = W[i];
+  __syncthreads();
+  f32x4_t acc[2][2] = {};
+  mm_nt(av, iv, acc);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+    for (int bj = 0; bj < 2; ++bj)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int64_t r = r0 + 32 * (wave >> 1) + 16 * bi + 4 * (lane >> 4) + j;
+        const int64_t c = c0 + 32 * (wave & 1) + 16 * bj + (lane & 15);
+        if (r < n && c < n) L[r * ldl + c] = acc[bi][bj][j];
+      }
+}
+
+// Trailing update: A[bi, bj] -= L[bi, p] L[bj, p]^T over the lower tiles
+// bi >= bj > p (blockIdx.x enumerates them row by row).
+__global__ __launch_bounds__(256) void chol_update_kernel(float* __restrict__ l, int64_t n, int64_t ldl, int64_t sl,
+                                                          int p) {
+  __shared__ float xi[NB][LD];
+  __shared__ float xj[NB][LD];
+  const int64_t b = blockIdx.y;
+  float* L = l + b * sl;
+  const int64_t t = blockIdx.x;
+  int64_t i = (int64_t)((sqrt(8.0 * (double)t + 1.0) - 1.0) * 0.5);
+  while ((i + 1) * (i + 2) / 2 <= t) ++i;
+  while (i * (i + 1) / 2 > t) --i;
+  const int64_t j = t - i * (i + 1) / 2;
+  const int64_t ri = (int64_t)(p + 1 + i) * NB, rj = (int64_t)(p + 1 + j) * NB, c0 = (int64_t)p * NB;
+  load_tile(xi, L, ldl, n, ri, c0);
+  load_tile(xj, L, ldl, n, rj, c0);
+  __syncthreads();
+  f32x4_t acc[2][2] = {};
+  mm_nt(xi, xj, acc);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+    for (int bj = 0; bj < 2; ++bj)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int64_t r = ri + 32 * (wave >> 1) + 16 * bi + 4 * (lane >> 4) + q;
+        const int64_t c = rj + 32 * (wave & 1) + 16 * bj + (lane & 15);
+        if (r < n && c < n) L[r * ldl + c] -= acc[bi][bj][q];
+      }
+}
+
+// -------------------------------------------------------------- block LDL --
+// inv of every b x b diagonal block (lower triangular) into winv [batch][n / b][b][b].
+__global__ __launch_bounds__(64) void ldl_inv_kernel(const float* __restrict__ l, int64_t ldl, int64_t sl,
+                                                     int64_t n, int bs, float* __restrict__ winv) {
+  __shared__ float a[MAX_B][MAX_B + 1];
+  __shared__ float xi[MAX_B][MAX_B + 1];
+  const int64_t b = blockIdx.y, blk = blockIdx.x;
+  const float* L = l + b * sl + blk * bs * ldl + blk * bs;
+  for (int i = threadIdx.x; i < bs * bs; i += 64) a[i / bs][i % bs] = L[(int64_t)(i / bs) * ldl + i % bs];
+  __syncthreads();
+  if ((int)threadIdx.x < bs) {
+    const int j = threadIdx.x;
+    for (int i = 0; i < j; ++i) xi[i][j] = 0.f;
+    xi[j][j] = 1.f / a[j][j];
+    for (int i = j + 1; i < bs; ++i) {
+      float acc = 0.f;
+      for (int k = j; k < i; ++k) acc += a[i][k] * xi[k][j];
+      xi[i][j] = -acc / a[i][i];
+    }
+  }
+  __syncthreads();
+  float* W = winv + (b * (n / bs) + blk) * bs * bs;
+  for (int i = threadIdx.x; i < bs * bs; i += 64) W[i] = xi[i / bs][i % bs];
+}
+
+// Column block cb: rows below it times inv(DL_cb); its diagonal block set to
+// I (its diagonal to 0 with zero_diag); rows above it are zero and stay so.
+template <int BS>
+__global__ __launch_bounds__(256) void ldl_apply_kernel(float* __restrict__ l, int64_t ldl, int64_t sl, int64_t n,
+                                                        const float* __restrict__ winv, int zero_diag) {
+  constexpr int bs = BS;
+  __shared__ float iv[BS * BS];
+  const int64_t b = blockIdx.z, cb = blockIdx.y;
+  const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const float* W = winv + (b * (n / bs) + cb) * bs * bs;
+  for (int i = threadIdx.x; i < bs * bs; i += 256) iv[i] = W[i];
+  __syncthreads();
+  const int64_t c0 = cb * bs;
+  if (r >= n || r < c0) return;
+  float* row = l + b * sl + r * ldl + c0;
+  if (r < c0 + bs) {
+    for (int c = 0; c < bs; ++c) row[c] = (c0 + c == r && !zero_diag) ? 1.f : 0.f;
+    return;
+  }
+  float v[BS];
+#pragma unroll
+  for (int k = 0; k < BS; ++k) v[k] = row[k];
+#pragma unroll
+  for (int c = 0; c < BS; ++c) {
+    float acc = 0.f;
+#pragma unroll
+    for (int k = c; k < BS; ++k) acc += v[k] * iv[k * BS + c];
+    row[c] = acc;
+  }
+}
+
+}  // namespace ldl
+}  // namespace kq
+
+using namespace kq::ldl;
+
+extern "C" int kq_h_regularize(float* h, int64_t k, int64_t ld, double count, float sigma_reg, float* diag,
+                               float* diag_mean, void* stream) {
+  if (k <= 0 || k > 65535 || ld < k)
+    return kq_fail(KQ_ERR_INVALID, "kq_h_regularize: need 0 < k <= 65535 and ld >= k");
+  if (!h || !diag_mean) return kq_fail(KQ_ERR_INVALID, "kq_h_regularize: null buffer");
+  if (!(count >= 0.0)) return kq_fail(KQ_ERR_INVALID, "kq_h_regularize: count must be >= 0");
+  hipStream_t st = (hipStream_t)stream;
+  const float inv = count > 0.0 ? 1.f / (float)count : 1.f;
+  diag_mean_kernel<<<1, 256, 0, st>>>(h, k, ld, inv, diag_mean);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return kq_check_launch(e, "kq_h_regularize");
+  regularize_kernel<<<dim3((unsigned)((k + 255) / 256), (unsigned)k), 256, 0, st>>>(h, k, ld, inv, sigma_reg,
+                                                                                   diag_mean, diag);
+  return kq_check_launch(hipGetLastError(), "kq_h_regularize");
+}
+
+extern "C" int kq_blockwise_hadamard(float* x, int64_t rows, int64_t cols, int64_t ld, int64_t batch,
+                                     int64_t stride, int sides, const float* row_scale, const float* col_scale,
+                                     void* stream) {
+  if (sides < 1 || sides > 3) return kq_fail(KQ_ERR_INVALID, "kq_blockwise_hadamard: sides must be 1, 2 or 3");
+  if (rows <= 0 || cols <= 0 || ld < cols || batch <= 0 || (batch > 1 && stride < rows * ld))
+    return kq_fail(KQ_ERR_INVALID, "kq_blockwise_hadamard: bad sizes");
+  if (((sides & 1) && rows % HAD) || ((sides & 2) && cols % HAD))
+    return kq_fail(KQ_ERR_INVALID, "kq_blockwise_hadamard: the transformed dimension must be a multiple of 128");
+  if (rows / HAD + 1 > 65535 || batch > 65535)
+    return kq_fail(KQ_ERR_LIMIT, "kq_blockwise_hadamard: too many blocks");
+  const float post = sides == 3 ? 1.f / 128.f : 0.08838834764831845f;  // 1/128, fl(1/sqrt(128))
+  const dim3 grid((unsigned)((cols + HAD - 1) / HAD), (unsigned)((rows + HAD - 1) / HAD), (unsigned)batch);
+  hadamard_kernel<<<grid, 256, 0, (hipStream_t)stream>>>(x, rows, cols, ld, stride, sides, row_scale, col_scale,
+                                                         post);
+  return kq_check_launch(hipGetLastError(), "kq_blockwise_hadamard");
+}
+
+extern "C" int64_t kq_cholesky_workspace_size(int64_t n, int64_t batch) {
+  if (n <= 0 || batch <= 0) return -1;
+  return batch * NB * NB * (int64_t)sizeof(float);
+}
+
+extern "C" int kq_cholesky(const float* a, int64_t lda, int64_t stride_a, float* l, int64_t ldl, int64_t stride_l,
+                           int64_t n, int64_t batch, int32_t* info, void* workspace, int64_t workspace_bytes,
+                           void* stream) {
+  if (n <= 0 || n > 65535 || batch <= 0 || batch > 65535 || lda < n || ldl < n)
+    return kq_fail(KQ_ERR_INVALID, "kq_cholesky: need 0 < n <= 65535, 0 < batch <= 65535, lda and ldl >= n");
+  if (batch > 1 && (stride_a < n * lda || stride_l < n * ldl))
+    return kq_fail(KQ_ERR_INVALID, "kq_cholesky: batch strides smaller than one matrix");
+  if (!a || !l || !info || !workspace) return kq_fail(KQ_ERR_INVALID, "kq_cholesky: null buffer");
+  if (a != l && ((a < l + stride_l * (batch - 1) + n * ldl) && (l < a + stride_a * (batch - 1) + n * lda)))
+    return kq_fail(KQ_ERR_INVALID, "kq_cholesky: a and l overlap without being the same buffer");
+  if (a == l && (lda != ldl || stride_a != stride_l))
+    return kq_fail(KQ_ERR_INVALID, "kq_cholesky: in place needs equal leading dimensions and strides");
+  if (workspace_bytes < kq_cholesky_workspace_size(n, batch))
+    return kq_fail(KQ_ERR_INVALID, "kq_cholesky: workspace too small");
+  hipStream_t st = (hipStream_t)stream;
+  float* winv = (float*)workspace;
+  chol_init_kernel<<<dim3((unsigned)((n + 255) / 256), (unsigned)n, (unsigned)batch), 256, 0, st>>>(
+      a, lda, stride_a, l, ldl, stride_l, n, info);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return kq_check_launch(e, "kq_cholesky/init");
+  const int m = (int)((n + NB - 1) / NB);
+  for (int p = 0; p < m; ++p) {
+    chol_diag_kernel<<<(unsigned)batch, 256, 0, st>>>(l, n, ldl, stride_l, p, winv, info);
+    if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_cholesky/diag");
+    const int q = m - p - 1;
+    if (q == 0) break;
+    chol_panel_kernel<<<dim3((unsigned)q, (unsigned)batch), 256, 0, st>>>(l, n, ldl, stride_l, p, winv);
+    if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_cholesky/panel");
+    chol_update_kernel<<<dim3((unsigned)((int64_t)q * (q + 1) / 2), (unsigned)batch), 256, 0, st>>>(
+        l, n, ldl, stride_l, p);
+    if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_cholesky/update");
+  }
+  return KQ_OK;
+}
+
+extern "C" int64_t kq_block_ldl_workspace_size(int64_t n, int b, int64_t batch) {
+  if (n <= 0 || b <= 0 || batch <= 0) return -1;
+  return batch * n * (int64_t)b * (int64_t)sizeof(float);
+}
+
+extern "C" int kq_block_ldl(float* l, int64_t ld, int64_t stride, int64_t n, int b, int64_t batch,
+                            uint32_t flags, void* workspace, int64_t workspace_bytes, void* stream) {
+  if (flags & ~(uint32_t)KQ_LDL_ZERO_DIAGONAL) return kq_fail(KQ_ERR_INVALID, "kq_block_ldl: unknown flags");
+  if (n <= 0 || b <= 0 || b > MAX_B || (b & (b - 1)) != 0 || n % b != 0 || ld < n || batch <= 0 ||
+      batch > 65535 || (batch > 1 && stride < n * ld))
+    return kq_fail(KQ_ERR_INVALID,
+                   "kq_block_ldl: need b a power of two <= %d, n %% b == 0, ld >= n (n=%lld b=%d)", MAX_B,
+                   (long long)n, b);
+  if (n / b > 65535) return kq_fail(KQ_ERR_LIMIT, "kq_block_ldl: too many blocks");
+  if (!l || !workspace) return kq_fail(KQ_ERR_INVALID, "kq_block_ldl: null buffer");
+  if (workspace_bytes < kq_block_ldl_workspace_size(n, b, batch))
+    return kq_fail(KQ_ERR_INVALID, "kq_block_ldl: workspace too small");
+  hipStream_t st = (hipStream_t)stream;
+  float* winv = (float*)workspace;
+  ldl_inv_kernel<<<dim3((unsigned)(n / b), (unsigned)batch), 64, 0, st>>>(l, ld, stride, n, b, winv);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return kq_check_launch(e, "kq_block_ldl/inv");
+  const dim3 grid((unsigned)((n + 255) / 256), (unsigned)(n / b), (unsigned)batch);
+  const int zd = (flags & KQ_LDL_ZERO_DIAGONAL) ? 1 : 0;
+  switch (b) {
+#define KQ_LDL_CASE(B) \
+    case B: ldl_apply_kernel<B><<<grid, 256, 0, st>>>(l, ld, stride, n, winv, zd); break;
+    KQ_LDL_CASE(1) KQ_LDL_CASE(2) KQ_LDL_CASE(4) KQ_LDL_CASE(8) KQ_LDL_CASE(16) KQ_LDL_CASE(32) KQ_LDL_CASE(64)
+#undef KQ_LDL_CASE
+  }
+  return kq_check_launch(hipGetLastError(), "kq_block_ldl/apply");
+}

@@ -20,6 +20,9 @@ Contents, each following the cited reference code:
       kquant/sqg_e4m3.py:38-60, 84-127, 197-302, 356-438.
   scale_plane (submodule): X4T and KQSC scale-plane codecs
       kquant/x4t.py, kquant/mxfp4_scale_codec.py.
+  ldl (submodule): the encoder's Hessian finalize — Hadamard rotation,
+      regularization, block LDL — kquant/exl3_encoder_backend.py:288-386,
+      1588-1663, kquant/exl3_reference.py:195-212.
 """
 
 from __future__ import annotations

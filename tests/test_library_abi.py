@@ -33,6 +33,7 @@ def test_python_binding_covers_every_entry_point():
     assert lib.kq_version() >> 16 == 1
     bound = set(_native.SIGNATURES) | {"kq_version", "kq_last_error", "kq_moe_workspace_size",
                                         "kq_moe_x4t_workspace_size", "kq_mx_linear_f32_workspace_size",
+                                        "kq_cholesky_workspace_size", "kq_block_ldl_workspace_size",
                                         "kq_route_sort_workspace_size"}
     assert set(declared_symbols()) <= bound
 
@@ -68,3 +69,20 @@ def test_x4t_moe_argument_errors_need_no_gpu():
     assert rc == _native.KQ_ERR_INVALID and b"null X4T component" in lib.kq_last_error()
     rc = lib.kq_x4t_tile_index(fake, 0, None, 1, 32, 300, fake, None)
     assert rc != 0
+
+
+def test_ldl_argument_errors_need_no_gpu():
+    lib = _native.library()
+    fake = ctypes.c_void_p(256)  # never dereferenced: validation fails first
+    assert lib.kq_cholesky_workspace_size(7168, 1) == 64 * 64 * 4
+    assert lib.kq_block_ldl_workspace_size(2048, 16, 3) == 3 * 2048 * 16 * 4
+    rc = lib.kq_cholesky(fake, 0, 0, fake, 0, 0, 0, 1, fake, fake, 1 << 20, None)
+    assert rc == _native.KQ_ERR_INVALID
+    rc = lib.kq_cholesky(fake, 64, 4096, ctypes.c_void_p(512), 64, 4096, 64, 2, fake, fake, 1 << 20, None)
+    assert rc == _native.KQ_ERR_INVALID and b"overlap" in lib.kq_last_error()
+    rc = lib.kq_block_ldl(fake, 96, 0, 96, 3, 1, 0, fake, 1 << 20, None)
+    assert rc == _native.KQ_ERR_INVALID and b"power of two" in lib.kq_last_error()
+    rc = lib.kq_blockwise_hadamard(fake, 100, 128, 128, 1, 0, 1, None, None, None)
+    assert rc == _native.KQ_ERR_INVALID and b"multiple of 128" in lib.kq_last_error()
+    rc = lib.kq_h_regularize(fake, 10, 10, -1.0, 0.025, None, fake, None)
+    assert rc == _native.KQ_ERR_INVALID
