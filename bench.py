@@ -32,6 +32,7 @@ HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 FP4_PEAK_TFLOPS = 10100.0
 FP8_PEAK_TFLOPS = 5000.0
+FP32_PEAK_TFLOPS = 157.3
 METRIC = "quantize GB/s + MXFP4 expert GEMM TFLOPS, as % of MI355X roofline (1 GPU)"
 
 
@@ -349,6 +350,63 @@ def main() -> int:
             "active_experts": int((counts > 0).sum()),
         }
         del rows, hacc
+
+    # ------------------------------- encoder H finalize (rotation, block LDL) --
+    if not args.quick and want("h_finalize"):
+        def spd(batch: int, n: int, seed: int) -> torch.Tensor:
+            gh = torch.Generator(device=dev).manual_seed(seed)
+            out = torch.empty(batch, n, n, dtype=torch.float32, device=dev)
+            for b in range(batch):
+                xs = torch.randn(2 * n, n, generator=gh, device=dev)
+                h = xs.T @ xs / (2 * n)
+                out[b] = h + 0.025 * torch.diagonal(h).mean() * torch.eye(n, device=dev)
+            return out
+
+        def chol_ws(n: int, batch: int) -> torch.Tensor:
+            return torch.empty(int(N.library().kq_cholesky_workspace_size(n, batch)), dtype=torch.uint8,
+                               device=dev)
+
+        fin = {}
+        for label, batch, n in (("h13_k7168", 1, 7168), ("h2_experts48_k2048", 48, 2048)):
+            h = spd(batch, n, 3)
+            lower = torch.empty_like(h)
+            info = torch.empty(batch, dtype=torch.int32, device=dev)
+            wsc = chol_ws(n, batch)
+            wsl = torch.empty(int(N.library().kq_block_ldl_workspace_size(n, 16, batch)), dtype=torch.uint8,
+                              device=dev)
+            su = torch.ones(n, dtype=torch.float32, device=dev)
+            mean = torch.empty(1, dtype=torch.float32, device=dev)
+
+            def rot_step():
+                for b in range(batch):
+                    N.call("kq_h_regularize", N.ptr(h[b]), n, n, 1.0, 1e-6, None, N.ptr(mean), stream)
+                N.call("kq_blockwise_hadamard", N.ptr(h), n, n, n, batch, n * n, 3, N.ptr(su), N.ptr(su), stream)
+
+            def chol_step():
+                N.call("kq_cholesky", N.ptr(h), n, n * n, N.ptr(lower), n, n * n, n, batch, N.ptr(info),
+                       N.ptr(wsc), wsc.numel(), stream)
+
+            def ldl_step():
+                N.call("kq_block_ldl", N.ptr(lower), n, n * n, n, 16, batch, N.LDL_ZERO_DIAGONAL, N.ptr(wsl),
+                       wsl.numel(), stream)
+
+            t_rot = _time_loop(torch, rot_step, 3, 1)
+            t_chol = _time_loop(torch, chol_step, 3, 1)
+            ldl_step()
+            t_ldl = _time_loop(torch, ldl_step, 3, 1)
+            t_torch = _time_loop(torch, lambda: torch.linalg.cholesky(h), 3, 1)
+            flops = batch * n ** 3 / 3.0
+            fin[label] = {
+                "matrices": batch, "n": n,
+                "regularize_rotate_ms": round(t_rot * 1e3, 3),
+                "cholesky_ms": round(t_chol * 1e3, 3),
+                "cholesky_tflops": round(flops / t_chol / 1e12, 2),
+                "cholesky_frac_of_fp32_mfma_peak": round(flops / t_chol / 1e12 / FP32_PEAK_TFLOPS, 4),
+                "block_ldl_ms": round(t_ldl * 1e3, 3),
+                "torch_linalg_cholesky_ms": round(t_torch * 1e3, 3),
+            }
+            del h, lower
+        result["h_finalize"] = fin
 
     # ------------------------------------- scale-plane codecs and SQG tables --
     if not args.quick and want("scale_planes"):

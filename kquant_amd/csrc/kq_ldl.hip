@@ -12,10 +12,11 @@
 //    workgroup per tile, a fast Walsh-Hadamard transform along the rows and /
 //    or columns in LDS (adds only), then one scale (1/128 exactly for both
 //    sides, fl(1/sqrt(128)) for one).
-//  * Cholesky (lower, fp32): right-looking over 64-column panels, one launch
-//    per step and all matrices of a batch per launch.  The diagonal block is
-//    factored in LDS by one workgroup, which also inverts it; the panel below
-//    is A21 inv(L11)^T and the trailing update A22 -= L21 L21^T, both on
+//  * Cholesky (lower, fp32): right-looking over 64-column panels, two
+//    launches per step and all matrices of a batch per launch.  A diagonal
+//    block is factored and inverted by one wave in registers, by the
+//    trailing-update workgroup that completes it; the panel below is
+//    A21 inv(L11)^T and the trailing update A22 -= L21 L21^T, both on
 //    v_mfma_f32_16x16x4f32 from LDS.  A failing pivot (<= 0 or NaN) records
 //    the leading-minor order in info (LAPACK's convention) and the
 //    factorization continues with pivot 1, so every launch still completes.
@@ -64,6 +65,40 @@ __global__ __launch_bounds__(256) void regularize_kernel(float* __restrict__ h, 
 }
 
 // --------------------------------------------------------------- rotation --
+// 128-point fast Walsh-Hadamard transform (Sylvester order, unscaled) of
+// every row (ROWS) or column of the LDS tile: two threads per line, each
+// holding 64 consecutive points in registers; stages 1..32 run in
+// registers, stage 64 pairs the two threads (lanes 2l, 2l + 1) by shuffle.
+template <bool ROWS>
+__device__ __forceinline__ void fwht_lines(float (*t)[HLD]) {
+  const int line = threadIdx.x >> 1, half = threadIdx.x & 1;
+  float v[64];
+#pragma unroll
+  for (int i = 0; i < 64; ++i) v[i] = ROWS ? t[line][64 * half + i] : t[64 * half + i][line];
+#pragma unroll
+  for (int h = 1; h < 64; h <<= 1) {
+#pragma unroll
+    for (int i = 0; i < 64; ++i) {
+      if (i & h) continue;
+      const float a = v[i], b = v[i + h];
+      v[i] = a + b;
+      v[i + h] = a - b;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 64; ++i) {
+    const float o = __shfl_xor(v[i], 1);
+    v[i] = half ? o - v[i] : v[i] + o;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 64; ++i) {
+    if (ROWS) t[line][64 * half + i] = v[i];
+    else t[64 * half + i][line] = v[i];
+  }
+  __syncthreads();
+}
+
 // sides: bit 0 = left (B X: each column of a tile transformed), bit 1 = right
 // (X B: each row).  Row / column scales (or none) apply before the transforms.
 __global__ __launch_bounds__(256) void hadamard_kernel(float* __restrict__ x, int64_t rows, int64_t cols,
@@ -85,32 +120,8 @@ __global__ __launch_bounds__(256) void hadamard_kernel(float* __restrict__ x, in
     t[r][c] = v;
   }
   __syncthreads();
-  // 64 butterflies per line per stage: thread -> (line, pair), pair p of
-  // stage h joins elements c and c + h with c = (p / h) * 2h + p % h
-  if (sides & 2) {
-    for (int h = 1; h < HAD; h <<= 1) {
-      for (int i = tid; i < HAD * (HAD / 2); i += 256) {
-        const int r = i >> 6, p = i & 63;
-        const int c = (p / h) * 2 * h + (p % h);
-        const float a = t[r][c], b = t[r][c + h];
-        t[r][c] = a + b;
-        t[r][c + h] = a - b;
-      }
-      __syncthreads();
-    }
-  }
-  if (sides & 1) {
-    for (int h = 1; h < HAD; h <<= 1) {
-      for (int i = tid; i < HAD * (HAD / 2); i += 256) {
-        const int c = i & (HAD - 1), p = i >> 7;
-        const int r = (p / h) * 2 * h + (p % h);
-        const float a = t[r][c], b = t[r + h][c];
-        t[r][c] = a + b;
-        t[r + h][c] = a - b;
-      }
-      __syncthreads();
-    }
-  }
+  if (sides & 2) fwht_lines<true>(t);
+  if (sides & 1) fwht_lines<false>(t);
   for (int i = tid; i < HAD * HAD; i += 256) {
     const int r = i >> 7, c = i & (HAD - 1);
     if (r0 + r < rows && c0 + c < cols) X[(r0 + r) * ld + c0 + c] = t[r][c] * post;
@@ -118,6 +129,52 @@ __global__ __launch_bounds__(256) void hadamard_kernel(float* __restrict__ x, in
 }
 
 // --------------------------------------------------------------- Cholesky --
+__device__ __forceinline__ float readlane_f(float v, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+// One wave factors the 64 x 64 block a (LDS; rows past the matrix padded with
+// the identity) into L, written back to a with zeros above the diagonal, and
+// writes inv(L) to xi.  Lane r holds row r in registers; column c is
+// broadcast from lane q with readlane, so each step is an FMA per row and
+// trailing column.  Entries above the diagonal take meaningless values in
+// registers and are never read.  inv(L): lane j solves column j by forward
+// substitution, the rows of L read as LDS broadcasts.  Returns (uniformly)
+// the first failing column + 1, or 0; a failing pivot is replaced by 1.
+__device__ __forceinline__ int factor64_wave(float (*a)[LD], float (*xi)[LD]) {
+  const int lane = threadIdx.x & 63;
+  float v[NB];
+#pragma unroll
+  for (int c = 0; c < NB; ++c) v[c] = a[lane][c];
+  int bad = 0;
+#pragma unroll
+  for (int c = 0; c < NB; ++c) {
+    float d = readlane_f(v[c], c);
+    if (!(d > 0.f)) {
+      if (bad == 0) bad = c + 1;
+      d = 1.f;
+    }
+    const float s = sqrtf(d);
+    v[c] = lane == c ? s : v[c] / s;
+#pragma unroll
+    for (int q = c + 1; q < NB; ++q) v[q] = fmaf(-v[c], readlane_f(v[c], q), v[q]);
+  }
+#pragma unroll
+  for (int c = 0; c < NB; ++c) a[lane][c] = c <= lane ? v[c] : 0.f;
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the rows are in LDS before the broadcast reads
+  float x[NB];
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    float acc = i == lane ? 1.f : 0.f;
+#pragma unroll
+    for (int k = 0; k < i; ++k) acc = fmaf(-a[i][k], x[k], acc);
+    x[i] = acc / a[i][i];
+  }
+#pragma unroll
+  for (int i = 0; i < NB; ++i) xi[i][lane] = x[i];
+  return bad;
+}
+
 // L = tril(A) (upper part zero); info = 0.  a and l may be the same buffer.
 __global__ __launch_bounds__(256) void chol_init_kernel(const float* a, int64_t lda, int64_t sa, float* l,
                                                         int64_t ldl, int64_t sl, int64_t n, int* __restrict__ info) {
@@ -128,59 +185,35 @@ __global__ __launch_bounds__(256) void chol_init_kernel(const float* a, int64_t 
   l[b * sl + i * ldl + j] = v;
 }
 
-// Factor the diagonal block of panel p in LDS (padded past n with the
-// identity), write it back (zeros above its diagonal) and its inverse to winv.
-__global__ __launch_bounds__(256) void chol_diag_kernel(float* __restrict__ l, int64_t n, int64_t ldl, int64_t sl,
-                                                        int p, float* __restrict__ winv, int* __restrict__ info) {
-  __shared__ float a[NB][LD];
-  __shared__ float xi[NB][LD];
-  __shared__ int bad;
-  const int64_t b = blockIdx.x;
-  float* L = l + b * sl;
-  const int tid = threadIdx.x;
-  const int64_t c0 = (int64_t)p * NB;
-  const int nb = (int)(n - c0 < NB ? n - c0 : NB);
-  if (tid == 0) bad = 0;
-  for (int i = tid; i < NB * NB; i += 256) {
+// Factor the diagonal block of panel 0 (one wave per matrix; the later
+// panels' diagonal blocks are factored by the trailing update that finishes
+// them), writing L11 back (zeros above its diagonal) and inv(L11) to winv.
+__device__ __forceinline__ void store_diag(float (*a)[LD], float (*xi)[LD], float* L, int64_t ldl, int64_t c0,
+                                           int nb, float* W, int bad, int* info) {
+  const int lane = threadIdx.x & 63;
+  for (int i = lane; i < NB * NB; i += 64) {
     const int r = i / NB, c = i % NB;
-    a[r][c] = (r < nb && c < nb) ? (c <= r ? L[(c0 + r) * ldl + c0 + c] : 0.f) : (r == c ? 1.f : 0.f);
-  }
-  __syncthreads();
-  for (int c = 0; c < NB; ++c) {
-    float d = a[c][c];
-    if (!(d > 0.f)) {
-      if (tid == 0 && bad == 0) bad = (int)(c0 + c + 1);
-      d = 1.f;
-    }
-    const float s = sqrtf(d);
-    __syncthreads();
-    for (int r = c + tid; r < NB; r += 256) a[r][c] = r == c ? s : a[r][c] / s;
-    __syncthreads();
-    const int w = NB - c - 1;
-    for (int i = tid; i < w * w; i += 256) {
-      const int r = c + 1 + i / w, q = c + 1 + i % w;
-      if (q <= r) a[r][q] -= a[r][c] * a[q][c];
-    }
-    __syncthreads();
-  }
-  if (tid < NB) {  // column j of inv(L11) by forward substitution
-    const int j = tid;
-    for (int i = 0; i < j; ++i) xi[i][j] = 0.f;
-    xi[j][j] = 1.f / a[j][j];
-    for (int i = j + 1; i < NB; ++i) {
-      float acc = 0.f;
-      for (int k = j; k < i; ++k) acc += a[i][k] * xi[k][j];
-      xi[i][j] = -acc / a[i][i];
-    }
-  }
-  __syncthreads();
-  float* W = winv + b * NB * NB;
-  for (int i = tid; i < NB * NB; i += 256) {
-    const int r = i / NB, c = i % NB;
-    if (r < nb && c < nb) L[(c0 + r) * ldl + c0 + c] = c <= r ? a[r][c] : 0.f;
+    if (r < nb && c < nb) L[(c0 + r) * ldl + c0 + c] = a[r][c];
     W[i] = xi[r][c];
   }
-  if (tid == 0 && bad != 0 && info[b] == 0) info[b] = bad;
+  if (lane == 0 && bad != 0 && *info == 0) *info = (int)(c0 + bad);
+}
+
+__global__ __launch_bounds__(64) void chol_diag_kernel(float* __restrict__ l, int64_t n, int64_t ldl, int64_t sl,
+                                                       float* __restrict__ winv, int* __restrict__ info) {
+  __shared__ float a[NB][LD];
+  __shared__ float xi[NB][LD];
+  const int64_t b = blockIdx.x;
+  float* L = l + b * sl;
+  const int nb = (int)(n < NB ? n : NB);
+  for (int i = threadIdx.x; i < NB * NB; i += 64) {
+    const int r = i / NB, c = i % NB;
+    a[r][c] = (r < nb && c < nb) ? (c <= r ? L[r * ldl + c] : 0.f) : (r == c ? 1.f : 0.f);
+  }
+  __syncthreads();
+  const int bad = factor64_wave(a, xi);
+  __syncthreads();
+  store_diag(a, xi, L, ldl, 0, nb, winv + b * NB * NB, bad, info + b);
 }
 
 // acc (this wave's 32x32 of a 64x64 tile, as 2x2 16x16 blocks) += X Y^T over
@@ -239,9 +272,10 @@ __global__ __launch_bounds__(256) void chol_panel_kernel(float* __restrict__ l, 
 }
 
 // Trailing update: A[bi, bj] -= L[bi, p] L[bj, p]^T over the lower tiles
-// bi >= bj > p (blockIdx.x enumerates them row by row).
+// bi >= bj > p (blockIdx.x enumerates them row by row).  The workgroup of
+// tile (p + 1, p + 1) then factors it as the next panel's diagonal block.
 __global__ __launch_bounds__(256) void chol_update_kernel(float* __restrict__ l, int64_t n, int64_t ldl, int64_t sl,
-                                                          int p) {
+                                                          int p, float* __restrict__ winv, int* __restrict__ info) {
   __shared__ float xi[NB][LD];
   __shared__ float xj[NB][LD];
   const int64_t b = blockIdx.y;
@@ -258,16 +292,33 @@ __global__ __launch_bounds__(256) void chol_update_kernel(float* __restrict__ l,
   f32x4_t acc[2][2] = {};
   mm_nt(xi, xj, acc);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const bool next_diag = t == 0;  // tile (p + 1, p + 1): the next panel's diagonal block
+  if (next_diag) __syncthreads();  // every wave is done reading xi / xj
 #pragma unroll
   for (int bi = 0; bi < 2; ++bi)
 #pragma unroll
     for (int bj = 0; bj < 2; ++bj)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int64_t r = ri + 32 * (wave >> 1) + 16 * bi + 4 * (lane >> 4) + q;
-        const int64_t c = rj + 32 * (wave & 1) + 16 * bj + (lane & 15);
-        if (r < n && c < n) L[r * ldl + c] -= acc[bi][bj][q];
+        const int lr = 32 * (wave >> 1) + 16 * bi + 4 * (lane >> 4) + q;
+        const int lc = 32 * (wave & 1) + 16 * bj + (lane & 15);
+        const int64_t r = ri + lr, c = rj + lc;
+        if (r < n && c < n) {
+          const float v = L[r * ldl + c] - acc[bi][bj][q];
+          if (next_diag) xi[lr][lc] = v;
+          else L[r * ldl + c] = v;
+        } else if (next_diag) {
+          xi[lr][lc] = lr == lc ? 1.f : 0.f;
+        }
       }
+  if (!next_diag) return;
+  __syncthreads();
+  if (wave == 0) {
+    const int bad = factor64_wave(xi, xj);
+    const int nb = (int)(n - ri < NB ? n - ri : NB);
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    store_diag(xi, xj, L, ldl, ri, nb, winv + b * NB * NB, bad, info + b);
+  }
 }
 
 // -------------------------------------------------------------- block LDL --
@@ -390,15 +441,14 @@ extern "C" int kq_cholesky(const float* a, int64_t lda, int64_t stride_a, float*
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return kq_check_launch(e, "kq_cholesky/init");
   const int m = (int)((n + NB - 1) / NB);
-  for (int p = 0; p < m; ++p) {
-    chol_diag_kernel<<<(unsigned)batch, 256, 0, st>>>(l, n, ldl, stride_l, p, winv, info);
-    if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_cholesky/diag");
+  chol_diag_kernel<<<(unsigned)batch, 64, 0, st>>>(l, n, ldl, stride_l, winv, info);
+  if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_cholesky/diag");
+  for (int p = 0; p + 1 < m; ++p) {
     const int q = m - p - 1;
-    if (q == 0) break;
     chol_panel_kernel<<<dim3((unsigned)q, (unsigned)batch), 256, 0, st>>>(l, n, ldl, stride_l, p, winv);
     if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_cholesky/panel");
     chol_update_kernel<<<dim3((unsigned)((int64_t)q * (q + 1) / 2), (unsigned)batch), 256, 0, st>>>(
-        l, n, ldl, stride_l, p);
+        l, n, ldl, stride_l, p, winv, info);
     if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_cholesky/update");
   }
   return KQ_OK;
