@@ -335,6 +335,51 @@ int64_t kq_block_ldl_workspace_size(int64_t n, int b, int64_t batch);
 int kq_block_ldl(float* l, int64_t ld, int64_t stride, int64_t n, int b, int64_t batch,
                  uint32_t flags, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* --------------------------------------------------------- QSRT trellis --
+ * The QSRT-E4M3 trellis bitstream and its weight decode.  A 16 x 16 tile
+ * stores 256 K-bit edges (K = 2, 3, 4): 16 spans of 16 symbols, each span K
+ * uint16 words MSB first, adjacent words exchanged (kquant/qsrt.py:811-857,
+ * pack_trellis_edges / unpack_trellis_edges).  Tiles are [tiles][256] int16
+ * symbols and [tiles][16 K] int16 words. */
+enum { KQ_QSRT_TRANSPOSED = 1u };
+
+/* Pack the low K bits of every symbol (pack_trellis_edges). */
+int kq_trellis_pack(const int16_t* symbols, int64_t tiles, int bits, int16_t* packed, void* stream);
+
+/* Unpack to the K-bit edges (states == 0, unpack_trellis_edges) or to the
+ * cyclic 16-bit states (states != 0: unpack_trellis_states,
+ * kquant/qsrt.py:860-863 with kquant/exl3_reference.py:37-61). */
+int kq_trellis_unpack(const int16_t* packed, int64_t tiles, int bits, int states, int16_t* out,
+                      void* stream);
+
+/* Decode a complete packed matrix (the payload of pack_qsrt_trellis,
+ * kquant/qsrt.py:983-1013: 128-channel records along the rate axis, record r
+ * at rate record_bits[r] (host array), tiles of a record in row-major
+ * (k_tile, n_tile) order) to its EXL-oriented weight [K, N] =
+ * [16 k_tiles, 16 n_tiles]: decode_qsrt_weight (kquant/exl3_reference.py:
+ * 149-192, 270-295) with suh [K] and svh [N] fp32 (device), or the
+ * regularized weight (decode_qsrt_regularized_weight) when both are NULL.
+ * rate_axis 0 = k, 1 = n.  labels: 3 x 65536 E4M3 bytes (device), the
+ * state labels of K2, K3 and K4 (kq_sqg_* / sqg_codebook_bytes).  out:
+ * out_dtype values with row stride ldo, [K, N] or, with KQ_QSRT_TRANSPOSED,
+ * [N, K] (the loader's dense orientation).  Both dimensions are multiples of
+ * 128, at most 1024 records.  The regularized weight is exact; the rotated
+ * one equals the reference's fp32 matmuls up to fp32 rounding. */
+int kq_qsrt_decode_weight(const int16_t* payload, int64_t payload_words, int64_t k_tiles,
+                          int64_t n_tiles, int rate_axis, const uint8_t* record_bits,
+                          const uint8_t* labels, const float* suh, const float* svh, int out_dtype,
+                          void* out, int64_t ldo, uint32_t flags, void* stream);
+
+/* The same decode from given 16-bit states [k_tiles][n_tiles][256]
+ * (decode_qsrt_regularized_weight / decode_qsrt_weight,
+ * kquant/exl3_reference.py:149-192, 270-295, which accept any states): tile
+ * rates per tile along the rate axis, tile_bits [k_tiles or n_tiles] uint8
+ * (device). */
+int kq_qsrt_decode_states(const int16_t* states, int64_t k_tiles, int64_t n_tiles, int rate_axis,
+                          const uint8_t* tile_bits, const uint8_t* labels, const float* suh,
+                          const float* svh, int out_dtype, void* out, int64_t ldo, uint32_t flags,
+                          void* stream);
+
 /* ---------------------------------------------------- scale-plane codecs --
  * Lossless codings of a uint8 E8M0 scale plane [rows, cols], cols <= 255,
  * rows contiguous.  Variable-length outputs are produced in two calls: a

@@ -96,7 +96,12 @@ SIGNATURES: dict[str, list] = {
     "kq_blockwise_hadamard": [_VP, _I64, _I64, _I64, _I64, _I64, _INT, _VP, _VP, _VP],
     "kq_cholesky": [_VP, _I64, _I64, _VP, _I64, _I64, _I64, _I64, _VP, _VP, _I64, _VP],
     "kq_block_ldl": [_VP, _I64, _I64, _I64, _INT, _I64, _U32, _VP, _I64, _VP],
+    "kq_trellis_pack": [_VP, _I64, _INT, _VP, _VP],
+    "kq_trellis_unpack": [_VP, _I64, _INT, _INT, _VP, _VP],
+    "kq_qsrt_decode_weight": [_VP, _I64, _I64, _I64, _INT, _VP, _VP, _VP, _VP, _INT, _VP, _I64, _U32, _VP],
+    "kq_qsrt_decode_states": [_VP, _I64, _I64, _INT, _VP, _VP, _VP, _VP, _INT, _VP, _I64, _U32, _VP],
 }
+QSRT_TRANSPOSED = 1
 LDL_ZERO_DIAGONAL = 1
 SQG_RANK_XOR = 0
 SQG_RANK_MIX = 1

@@ -22,17 +22,20 @@
 //    factorization continues with pivot 1, so every launch still completes.
 //  * block LDL: every b x b diagonal block DL_i of L is inverted, each block
 //    column multiplied by its inverse and the diagonal blocks set to I.
+#include "kq_hadamard.h"
 #include "kq_internal.h"
 
 namespace kq {
 namespace ldl {
 
+using kq::had::fwht_lines;
+using kq::had::HAD;
+using kq::had::HLD;
+
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int NB = 64;     // Cholesky panel
 constexpr int LD = 68;     // padded LDS row: lane (i, k) of an MFMA read hits bank 4 i + k
-constexpr int HAD = 128;   // Hadamard block
-constexpr int HLD = HAD + 1;
 constexpr int MAX_B = 64;  // block LDL block size limit
 
 // ------------------------------------------------------------ regularize --
@@ -65,40 +68,6 @@ __global__ __launch_bounds__(256) void regularize_kernel(float* __restrict__ h, 
 }
 
 // --------------------------------------------------------------- rotation --
-// 128-point fast Walsh-Hadamard transform (Sylvester order, unscaled) of
-// every row (ROWS) or column of the LDS tile: two threads per line, each
-// holding 64 consecutive points in registers; stages 1..32 run in
-// registers, stage 64 pairs the two threads (lanes 2l, 2l + 1) by shuffle.
-template <bool ROWS>
-__device__ __forceinline__ void fwht_lines(float (*t)[HLD]) {
-  const int line = threadIdx.x >> 1, half = threadIdx.x & 1;
-  float v[64];
-#pragma unroll
-  for (int i = 0; i < 64; ++i) v[i] = ROWS ? t[line][64 * half + i] : t[64 * half + i][line];
-#pragma unroll
-  for (int h = 1; h < 64; h <<= 1) {
-#pragma unroll
-    for (int i = 0; i < 64; ++i) {
-      if (i & h) continue;
-      const float a = v[i], b = v[i + h];
-      v[i] = a + b;
-      v[i + h] = a - b;
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < 64; ++i) {
-    const float o = __shfl_xor(v[i], 1);
-    v[i] = half ? o - v[i] : v[i] + o;
-  }
-  __syncthreads();
-#pragma unroll
-  for (int i = 0; i < 64; ++i) {
-    if (ROWS) t[line][64 * half + i] = v[i];
-    else t[64 * half + i][line] = v[i];
-  }
-  __syncthreads();
-}
-
 // sides: bit 0 = left (B X: each column of a tile transformed), bit 1 = right
 // (X B: each row).  Row / column scales (or none) apply before the transforms.
 __global__ __launch_bounds__(256) void hadamard_kernel(float* __restrict__ x, int64_t rows, int64_t cols,

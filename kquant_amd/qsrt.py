@@ -1,0 +1,139 @@
+"""QSRT trellis bitstream and the decode of packed QSRT matrices, on the GPU.
+
+Drop-in for the bitstream functions of ``kquant/qsrt.py`` (same names,
+arguments, dtypes and errors):
+
+  ``pack_trellis_edges(indices, bits)``      (:811-833)  -> ``kq_trellis_pack``
+  ``unpack_trellis_edges(packed, bits)``     (:836-857)  -> ``kq_trellis_unpack``
+  ``unpack_trellis_states(packed, bits)``    (:860-863)  -> ``kq_trellis_unpack``
+
+and, as the payload-level decode a serving loader needs (the role of
+``decode_qsrt_exl3_weight``, :1107-1141, minus the mode tables of the
+Kimi-K3 checkpoint schema), ``decode_qsrt_payload``: one launch from the
+packed payload of 128-channel records to the EXL-oriented weight
+(``kq_qsrt_decode_weight``).  CPU inputs run on the current GPU and come
+back on the CPU.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _native as N
+from .sqg_e4m3 import SQG_XOR_CHEB_T12, sqg_codebook_bytes
+
+TILE_CHANNELS = 16
+TILE_VALUES = TILE_CHANNELS * TILE_CHANNELS
+RECORD_CHANNELS = 128
+
+
+def _validate_k(bits: int) -> None:
+    if isinstance(bits, bool) or not isinstance(bits, int) or bits not in (2, 3, 4):
+        raise ValueError("QSRT supports K=2, K=3, or K=4")
+
+
+def _on_gpu(t: torch.Tensor) -> tuple[torch.Tensor, torch.device | None]:
+    (g,), _, host = N.to_gpu([t])
+    return g, host
+
+
+def pack_trellis_edges(indices: torch.Tensor, bits: int) -> torch.Tensor:
+    """Pack the low K bits of every index with the native word ordering."""
+
+    _validate_k(bits)
+    if indices.ndim < 1 or indices.shape[-1] != TILE_VALUES:
+        raise ValueError("indices must have a final dimension of 256")
+    if indices.dtype == torch.bool or indices.is_floating_point():
+        raise TypeError("indices must use an integer dtype")
+    g, host = _on_gpu(indices)
+    sym = N.aligned((g & 0xFFFF).to(torch.int16) if g.dtype != torch.int16 else g, 2)
+    tiles = sym.numel() // TILE_VALUES
+    out = torch.empty(*indices.shape[:-1], TILE_CHANNELS * bits, dtype=torch.int16, device=g.device)
+    N.call("kq_trellis_pack", N.ptr(sym), tiles, bits, N.ptr(out), N.stream(g.device))
+    return out if host is None else out.to(host)
+
+
+def _unpack(packed: torch.Tensor, bits: int, states: bool) -> torch.Tensor:
+    _validate_k(bits)
+    expected_words = TILE_CHANNELS * bits
+    if packed.ndim < 1 or packed.shape[-1] != expected_words:
+        raise ValueError(f"packed tiles must end in {expected_words} int16 words")
+    if packed.dtype != torch.int16:
+        raise TypeError("packed trellis words must use torch.int16")
+    g, host = _on_gpu(packed)
+    g = N.aligned(g, 2)
+    tiles = g.numel() // expected_words
+    out = torch.empty(*packed.shape[:-1], TILE_VALUES, dtype=torch.int16, device=g.device)
+    N.call("kq_trellis_unpack", N.ptr(g), tiles, bits, 1 if states else 0, N.ptr(out), N.stream(g.device))
+    return out if host is None else out.to(host)
+
+
+def unpack_trellis_edges(packed: torch.Tensor, bits: int) -> torch.Tensor:
+    """Invert :func:`pack_trellis_edges` to the stored K-bit edge symbols."""
+
+    return _unpack(packed, bits, False)
+
+
+def unpack_trellis_states(packed: torch.Tensor, bits: int) -> torch.Tensor:
+    """Unpack native edge words and reconstruct every cyclic 16-bit state."""
+
+    return _unpack(packed, bits, True)
+
+
+def rate_labels(codebook: str = SQG_XOR_CHEB_T12, *, rate_axis: str | None = None,
+                device: torch.device | str | None = None) -> torch.Tensor:
+    """The K2, K3 and K4 state labels of a codebook as one uint8 [3, 65536]
+    device table (the layout the decode kernels read)."""
+
+    gpu = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+    return torch.stack([sqg_codebook_bytes(bits, codebook, rate_axis=rate_axis, device=gpu)
+                        for bits in (2, 3, 4)]).contiguous()
+
+
+def decode_qsrt_payload(
+    payload: torch.Tensor,
+    *,
+    k_tiles: int,
+    n_tiles: int,
+    rate_axis: str,
+    record_bits,
+    suh: torch.Tensor | None = None,
+    svh: torch.Tensor | None = None,
+    codebook: str = SQG_XOR_CHEB_T12,
+    out_dtype: torch.dtype = torch.float32,
+    transposed: bool = False,
+) -> torch.Tensor:
+    """Decode a packed QSRT matrix (``pack_qsrt_trellis``'s payload,
+    kquant/qsrt.py:983-1013) to its weight: ``[K, N]`` (EXL orientation) or,
+    with ``transposed``, ``[N, K]``.  With ``suh`` / ``svh`` this is
+    ``decode_qsrt_weight`` (kquant/exl3_reference.py:270-295); without, the
+    regularized weight.  ``record_bits`` gives each 128-channel record's rate
+    along ``rate_axis``."""
+
+    if rate_axis not in ("k", "n"):
+        raise ValueError("rate_axis must be 'k' or 'n'")
+    if payload.dtype != torch.int16 or payload.ndim != 1:
+        raise TypeError("QSRT trellis payload must be a one-dimensional torch.int16 tensor")
+    if (suh is None) != (svh is None):
+        raise ValueError("pass both suh and svh, or neither")
+    bits = bytes(int(b) for b in record_bits)
+    if any(b not in (2, 3, 4) for b in bits):
+        raise ValueError("tile_bits must contain only integer K2, K3, or K4")
+    g, host = _on_gpu(payload)
+    g = N.aligned(g, 2)
+    gpu = g.device
+    k, n = k_tiles * TILE_CHANNELS, n_tiles * TILE_CHANNELS
+    labels = rate_labels(codebook, rate_axis=rate_axis, device=gpu)
+    su = sv = None
+    if suh is not None:
+        if suh.numel() != k or svh.numel() != n:
+            raise ValueError("suh and svh must match the K and N dimensions")
+        su = N.aligned(suh.to(device=gpu, dtype=torch.float32).reshape(-1), 4)
+        sv = N.aligned(svh.to(device=gpu, dtype=torch.float32).reshape(-1), 4)
+    shape = (n, k) if transposed else (k, n)
+    out = torch.empty(shape, dtype=out_dtype, device=gpu)
+    # record rates are a host array (bytes pass as a pointer to their buffer)
+    N.call("kq_qsrt_decode_weight", N.ptr(g), g.numel(), k_tiles, n_tiles, 0 if rate_axis == "k" else 1,
+           bits, N.ptr(labels), N.ptr(su), N.ptr(sv), N.DTYPE_CODES[out_dtype], N.ptr(out), shape[1],
+           N.QSRT_TRANSPOSED if transposed else 0, N.stream(gpu))
+    return out if host is None else out.to(host)
