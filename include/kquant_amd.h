@@ -380,6 +380,22 @@ int kq_qsrt_decode_states(const int16_t* states, int64_t k_tiles, int64_t n_tile
                           const float* svh, int out_dtype, void* out, int64_t ldo, uint32_t flags,
                           void* stream);
 
+/* SQG trellis quantizer: the tail-biting Viterbi search of
+ * kquant/csrc/qsrt_quantize_tiles_kernel.cuh with the SQG E4M3 labels of
+ * kquant/csrc/sqg_quantize.cu (quantize_tiles_sqg_cuda, :165-342), in the
+ * same fp16 arithmetic, decision packing and tie order, so the states and
+ * values are those of the reference kernel bit for bit.  tiles / out_tiles
+ * fp32 [n_tiles, 256]; out_states int16 [n_tiles, 256] (the cyclic 16-bit
+ * states of the path); lut: 65536 E4M3 labels in state order (device);
+ * tailbite_context 1..128.  One workgroup per tile, `workgroups` of them
+ * over the tiles; workspace: kq_sqg_quantize_workspace_size(bits,
+ * workgroups) bytes for the decisions.  Tiles whose every path cost
+ * overflows fp16 (|x| in the hundreds) are outside the reference's domain. */
+int64_t kq_sqg_quantize_workspace_size(int bits, int workgroups);
+int kq_sqg_quantize_tiles(const float* tiles, int64_t n_tiles, const uint8_t* lut, int bits,
+                          int tailbite_context, float* out_tiles, int16_t* out_states, void* workspace,
+                          int64_t workspace_bytes, int workgroups, void* stream);
+
 /* ---------------------------------------------------- scale-plane codecs --
  * Lossless codings of a uint8 E8M0 scale plane [rows, cols], cols <= 255,
  * rows contiguous.  Variable-length outputs are produced in two calls: a

@@ -18,6 +18,9 @@ Contents, each following the cited reference code:
       kquant/tp_simulator.py:72-80, 114-160; kquant/pack/qsrt_validation.py:240-258.
   sqg_* tables
       kquant/sqg_e4m3.py:38-60, 84-127, 197-302, 356-438.
+  sqg_quantize_tiles
+      C restatement in sqg_viterbi.c of the SQG trellis (Viterbi) quantizer,
+      kquant/csrc/qsrt_quantize_tiles_kernel.cuh, kquant/csrc/sqg_quantize.cu.
   scale_plane (submodule): X4T and KQSC scale-plane codecs
       kquant/x4t.py, kquant/mxfp4_scale_codec.py.
   ldl (submodule): the encoder's Hessian finalize — Hadamard rotation,
@@ -57,6 +60,10 @@ def _load():
         lib.mxo_unpack_codes.restype = None
         lib.mxo_pack_codes.argtypes = [vp, i64, vp]
         lib.mxo_pack_codes.restype = None
+        lib.sqgo_quantize_tiles.argtypes = [vp, ctypes.c_int64, vp, i32, i32, vp, vp]
+        lib.sqgo_quantize_tiles.restype = None
+        lib.sqgo_f64_to_f16.argtypes = [vp, ctypes.c_int64, vp]
+        lib.sqgo_f64_to_f16.restype = None
         lib.mxo_f32_to_e4m3.argtypes = [ctypes.c_float]
         lib.mxo_f32_to_e4m3.restype = u32
         lib.mxo_f32_to_e2m1.argtypes = [ctypes.c_float]
@@ -126,6 +133,29 @@ def pack_codes(codes: np.ndarray) -> np.ndarray:
     packed = np.zeros(codes.shape[:-1] + (codes.shape[-1] // 2,), dtype=np.uint8)
     lib.mxo_pack_codes(_ptr(codes), codes.size, _ptr(packed))
     return packed
+
+
+def sqg_quantize_tiles(tiles: np.ndarray, lut: np.ndarray, bits: int, tailbite_context: int = 128):
+    """The SQG trellis quantizer (sqg_viterbi.c; kquant/csrc/qsrt_quantize_tiles_kernel.cuh
+    with the SQG labels of kquant/csrc/sqg_quantize.cu): tiles float32 [n, 256],
+    lut uint8 [65536] E4M3 labels in state order -> (reconstructed float32
+    [n, 256], states int16 [n, 256])."""
+    lib = _load()
+    x = np.ascontiguousarray(tiles, dtype=np.float32).reshape(-1, 256)
+    lab = np.ascontiguousarray(lut, dtype=np.uint8)
+    out = np.empty_like(x)
+    states = np.empty(x.shape, dtype=np.int16)
+    lib.sqgo_quantize_tiles(_ptr(x), x.shape[0], _ptr(lab), bits, tailbite_context, _ptr(out), _ptr(states))
+    return out, states
+
+
+def f64_to_f16_bits(x: np.ndarray) -> np.ndarray:
+    """sqg_viterbi.c's fp16 rounding (nearest, ties to even), as uint16 bits."""
+    lib = _load()
+    v = np.ascontiguousarray(x, dtype=np.float64)
+    out = np.empty(v.shape, dtype=np.uint16)
+    lib.sqgo_f64_to_f16(_ptr(v), v.size, _ptr(out))
+    return out
 
 
 def f32_to_e4m3(values: np.ndarray) -> np.ndarray:

@@ -34,6 +34,7 @@ def test_python_binding_covers_every_entry_point():
     bound = set(_native.SIGNATURES) | {"kq_version", "kq_last_error", "kq_moe_workspace_size",
                                         "kq_moe_x4t_workspace_size", "kq_mx_linear_f32_workspace_size",
                                         "kq_cholesky_workspace_size", "kq_block_ldl_workspace_size",
+                                        "kq_sqg_quantize_workspace_size",
                                         "kq_route_sort_workspace_size"}
     assert set(declared_symbols()) <= bound
 
