@@ -408,6 +408,54 @@ def main() -> int:
             del h, lower
         result["h_finalize"] = fin
 
+    # ------------------------------ QSRT trellis: SQG encoder and weight decode --
+    if not args.quick and want("qsrt"):
+        from kquant_amd import qsrt as kq_qsrt
+        from kquant_amd import sqg_quantizer
+        from kquant_amd.sqg_e4m3 import sqg_xor_cheb_t12_bytes
+
+        qres = {}
+        gq = torch.Generator(device=dev).manual_seed(7)
+        n_enc = 2048
+        xt = torch.randn(n_enc, 256, generator=gq, device=dev)
+        for bits in (2, 3, 4):
+            lut = sqg_xor_cheb_t12_bytes(bits, device=dev)
+
+            def enc_step(lut=lut, bits=bits):
+                sqg_quantizer.quantize_tiles_sqg(xt, lut, bits, 128)
+
+            t_enc = _time_loop(torch, enc_step, 2, 1)
+            qres[f"sqg_encode_k{bits}"] = {
+                "tiles": n_enc,
+                "ms": round(t_enc * 1e3, 2),
+                "tiles_per_s": round(n_enc / t_enc, 1),
+                # 512 steps (256-step primer + closing pass) x 65536 edges per tile
+                "edge_evals_per_s": round(n_enc * 512 * 65536 / t_enc / 1e12, 3),
+                "unit": "edge_evals T/s",
+            }
+        # decode of one Kimi-K3 w1 matrix: EXL [K=3584, N=3072], rate axis n, P24 x 2 + P33 x 10
+        k_tiles, n_tiles = 224, 192
+        record_bits = (2, 4) * 2 + (3,) * 20
+        words = sum(8 * k_tiles * 16 * b for b in record_bits)
+        payload = torch.randint(-32768, 32768, (words,), dtype=torch.int16, generator=gq, device=dev)
+        suh = torch.ones(k_tiles * 16, device=dev)
+        svh = torch.ones(n_tiles * 16, device=dev)
+
+        def dec_qsrt():
+            kq_qsrt.decode_qsrt_payload(payload, k_tiles=k_tiles, n_tiles=n_tiles, rate_axis="n",
+                                        record_bits=record_bits, suh=suh, svh=svh, out_dtype=torch.bfloat16,
+                                        transposed=True)
+
+        t_dq = _time_loop(torch, dec_qsrt, 20, 3)
+        dbytes = words * 2 + k_tiles * n_tiles * 256 * 2
+        qres["qsrt_decode_w1_k3"] = {
+            "workload": "QSRT w1 [3072 x 3584] (R2: 2 x P24 + 10 x P33) -> bf16 [N, K], rotation included",
+            "us": round(t_dq * 1e6, 1),
+            "gbs": round(dbytes / t_dq / 1e9, 1),
+            "hbm_frac": round(dbytes / t_dq / 1e9 / HBM_PEAK_GBS, 4),
+        }
+        result["qsrt"] = qres
+
     # ------------------------------------- scale-plane codecs and SQG tables --
     if not args.quick and want("scale_planes"):
         from kquant_amd import sqg_e4m3

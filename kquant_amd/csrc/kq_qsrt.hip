@@ -117,6 +117,7 @@ __global__ __launch_bounds__(256) void decode_kernel(const int16_t* __restrict__
     const int bits = tb < 2 ? 2 : tb > 4 ? 4 : tb;  // validated by the caller; clamped to stay in the tables
     const uint8_t* lab = labels + (int64_t)(bits - 2) * 65536;
     const uint16_t* st = reinterpret_cast<const uint16_t*>(src) + (kt * n_tiles + nt) * 256;
+#pragma unroll 16
     for (int e = 0; e < 64; ++e) {
       const int i = 64 * part + e;
       const int pos = tc_position(i);
@@ -137,6 +138,7 @@ __global__ __launch_bounds__(256) void decode_kernel(const int16_t* __restrict__
     }
     __syncthreads();
     const uint8_t* lab = labels + (int64_t)(bits - 2) * 65536;
+#pragma unroll 16
     for (int e = 0; e < 64; ++e) {
       const int i = 64 * part + e;
       const int q0 = ((i + 1) * bits - 16 + nbits) % nbits;

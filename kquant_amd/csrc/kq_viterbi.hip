@@ -47,12 +47,17 @@ __device__ __forceinline__ _Float16 e4m3_to_f16(uint32_t b) {
 }
 
 // The labels of predecessor k for nodes 2p and 2p + 1, from a 16-bit
-// little-endian pair of E4M3 bytes.
+// little-endian pair of E4M3 bytes: each byte's 7 magnitude bits shifted
+// left by 7 are the fp16 pattern of its value / 2^8 (E4M3 exponent bias 7
+// against fp16's 15; E4M3 subnormals land on fp16 subnormals), the sign bit
+// moves to bit 15, and one exact packed multiply by 2^8 finishes.
 __device__ __forceinline__ h2_t pair_labels(uint32_t word16) {
-  h2_t r;
-  r[0] = e4m3_to_f16(word16 & 0xff);
-  r[1] = e4m3_to_f16((word16 >> 8) & 0xff);
-  return r;
+  const uint32_t t = (word16 & 0xffu) | ((word16 & 0xff00u) << 8);  // bytes -> [b0, 0, b1, 0]
+  const uint32_t bits = ((t & 0x007f007fu) << 7) | ((t & 0x00800080u) << 8);
+  h2_t scale;
+  scale[0] = (_Float16)256.0f;
+  scale[1] = (_Float16)256.0f;
+  return __builtin_bit_cast(h2_t, bits) * scale;
 }
 
 __device__ __forceinline__ int bitrev5(int v) { return (int)(__builtin_bitreverse32((uint32_t)v) >> 27); }
