@@ -454,6 +454,38 @@ def main() -> int:
             "gbs": round(dbytes / t_dq / 1e9, 1),
             "hbm_frac": round(dbytes / t_dq / 1e9 / HBM_PEAK_GBS, 4),
         }
+        # the fused linear on the same matrix (x @ W without materializing W)
+        # and on the TP12-local expert shapes of the same checkpoint
+        lin_cases = {
+            "k3_w1": (k_tiles, n_tiles, "n", record_bits, payload, suh, svh),
+        }
+        for name, kt_, nt_, axis, bits_ in (("tp12_w13", 224, 32, "n", (3,) * 4), ("tp12_w2", 16, 224, "k", (3, 3))):
+            w_ = sum(8 * (kt_ if axis == "n" else nt_) * 16 * b for b in bits_)
+            lin_cases[name] = (kt_, nt_, axis, bits_,
+                               torch.randint(-32768, 32768, (w_,), dtype=torch.int16, generator=gq, device=dev),
+                               torch.ones(kt_ * 16, device=dev), torch.ones(nt_ * 16, device=dev))
+        lin = {}
+        reps = 20
+        for name, (kt_, nt_, axis, bits_, p_, su_, sv_) in lin_cases.items():
+            row = {}
+            for m in (1, 4, 16):
+                xq = torch.randn(m, kt_ * 16, generator=gq, device=dev).to(torch.bfloat16)
+                outq = torch.empty(m, nt_ * 16, dtype=torch.bfloat16, device=dev)
+                run = kq_qsrt.qsrt_linear_launcher(xq, p_, outq, k_tiles=kt_, n_tiles=nt_, rate_axis=axis,
+                                                   record_bits=bits_, suh=su_, svh=sv_)
+                run()
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph):
+                    for _ in range(reps):
+                        run()
+                row[f"m{m}_us"] = round(_time_loop(torch, graph.replay, 10, 3) / reps * 1e6, 2)
+            row["weight_bytes"] = int(p_.numel() * 2)
+            lin[name] = row
+        qres["qsrt_linear"] = {
+            "workload": "x[m, K] bf16 @ QSRT W (rotated, fp32 math) -> bf16; time per call from a HIP "
+                        "graph of 20 back-to-back calls",
+            **lin,
+        }
         result["qsrt"] = qres
 
     # ------------------------------------- scale-plane codecs and SQG tables --

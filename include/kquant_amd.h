@@ -380,6 +380,27 @@ int kq_qsrt_decode_states(const int16_t* states, int64_t k_tiles, int64_t n_tile
                           const float* svh, int out_dtype, void* out, int64_t ldo, uint32_t flags,
                           void* stream);
 
+/* A linear layer on a packed QSRT matrix without materializing the weight:
+ * out[m, n] = sum_k x[m, k] W[k, n] for m < rows, W the matrix that
+ * kq_qsrt_decode_weight would produce from the same arguments (rotated with
+ * suh / svh, or regularized when both are NULL).  It replaces the serving
+ * use of the decode, which builds the dense weight and then applies it
+ * (scripts/stream_k3_pytorch.py:771-775 with decode_qsrt_exl3_weight,
+ * kquant/qsrt.py:1107-1141).  x: x_dtype values [rows, ldx >= K]; out:
+ * out_dtype values [rows, ldo >= N]; fp32 arithmetic throughout (the
+ * activation rows are rotated in fp32, the weight is never rounded to
+ * bf16), so the result is the exact product up to fp32 summation order.
+ * Meant for decode-sized batches: every 16 rows decode the weight once more.
+ * workspace: kq_qsrt_linear_workspace_size(rows, k_tiles, n_tiles) bytes
+ * (may be 0), 256-byte aligned and zeroed before its first use; each call
+ * leaves it zeroed again.  Calls sharing a workspace must not overlap. */
+int64_t kq_qsrt_linear_workspace_size(int64_t rows, int64_t k_tiles, int64_t n_tiles);
+int kq_qsrt_linear(const void* x, int x_dtype, int64_t rows, int64_t ldx, const int16_t* payload,
+                   int64_t payload_words, int64_t k_tiles, int64_t n_tiles, int rate_axis,
+                   const uint8_t* record_bits, const uint8_t* labels, const float* suh, const float* svh,
+                   int out_dtype, void* out, int64_t ldo, void* workspace, int64_t workspace_bytes,
+                   void* stream);
+
 /* SQG trellis quantizer: the tail-biting Viterbi search of
  * kquant/csrc/qsrt_quantize_tiles_kernel.cuh with the SQG E4M3 labels of
  * kquant/csrc/sqg_quantize.cu (quantize_tiles_sqg_cuda, :165-342), in the

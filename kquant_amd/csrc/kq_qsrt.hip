@@ -16,6 +16,7 @@
 // its own rate (kquant/qsrt.py:974-1018), so a 128 x 128 output block is one
 // record: one workgroup decodes its 64 tiles into LDS, transforms both sides
 // there and writes the block.
+#include "kq_dma.h"
 #include "kq_hadamard.h"
 #include "kq_internal.h"
 
@@ -167,6 +168,332 @@ __global__ __launch_bounds__(256) void decode_kernel(const int16_t* __restrict__
   }
 }
 
+
+// ---------------------------------------------------------- fused linear --
+// out[m, n] = sum_k x[m, k] W[k, n] with W the decoded weight, never written
+// to memory: the serving use of the decode (scripts/stream_k3_pytorch.py:
+// 771-775 decodes, then the expert's linear applies it).  With suh / svh,
+// W = diag(suh) B W_reg B diag(svh), so the product is computed as
+// (((x o suh) B) W_reg) B o svh: the activation rows are rotated once per
+// workgroup, the tiles feed fp32 FMAs straight from the trellis, and the
+// 128-column output block is rotated in the epilogue (B is linear, so each
+// K chunk's partial block may be rotated before the chunks are summed).
+//
+// Workgroup (n block nb, K chunk, row group): 16 waves = 8 n tiles x 2 halves
+// of every 128-row k block of the chunk (4 k tiles each).  Lane l of a wave
+// owns trellis symbols 4l .. 4l + 3 of each tile: one column
+// (l >> 3) + 8 (l & 1) and rows r0, r0 + 1, r0 + 8, r0 + 9 with
+// r0 = 2 ((l >> 1) & 3) in the tensor-core order, and their four states are
+// one window of 16 + 3K stream bits.  Stored dword d of a tile is stream
+// bits 32 d .. 32 d + 31, most significant first (the word exchange makes
+// it so), so the window comes from two dwords.  The block's 65,536-entry
+// label table of the current rate lives in LDS, and the k blocks' trellis
+// words stream through a ring of LDS stages filled by direct loads several
+// blocks ahead.  The table lookups (one random LDS byte read per weight)
+// bound the main loop.
+constexpr int LIN_THREADS = 1024;
+// 128-row k blocks a workgroup may cover: its rotated activation rows
+// (M x 128 per block, fp32) take at most 32 KB of LDS.
+constexpr int lin_max_kb(int m) { return 64 / m; }
+// k blocks of trellis words in flight per workgroup (8 KB of LDS each)
+constexpr int LIN_STAGES = 4;
+
+struct LinRecords {
+  uint8_t bits[MAX_RECORDS];
+  uint32_t prefix8[MAX_RECORDS / 8 + 1];  // sum of bits[r] over r < 8 i
+};
+
+struct LinArgs {
+  const void* x;
+  int64_t ldx, m;
+  const uint32_t* payload;
+  const uint8_t* labels;
+  const float* suh;
+  const float* svh;
+  void* out;
+  int64_t ldo;
+  float* partial;  // [chunks][m][N] when chunks > 1
+  int* counters;   // [row groups][n blocks], zero between calls
+  int k_tiles, n_tiles, rate_n, kbw, chunks, x_dtype, out_dtype;
+};
+
+// Rate of record r and the sum of the rates of records before it, from the
+// kernel-argument table through uniform dword loads (r is uniform).
+__device__ __forceinline__ int record_rate(const LinRecords& rec, int r) {
+  r = __builtin_amdgcn_readfirstlane(r);
+  const uint32_t w = reinterpret_cast<const uint32_t*>(rec.bits)[r >> 2];
+  return (int)((w >> (8 * (r & 3))) & 0xffu);
+}
+
+__device__ __forceinline__ uint32_t record_rates_before(const LinRecords& rec, int r) {
+  r = __builtin_amdgcn_readfirstlane(r);
+  const uint32_t* w = reinterpret_cast<const uint32_t*>(rec.bits) + ((r >> 3) << 1);
+  const int n = r & 7;  // records r & ~7 .. r - 1 on top of the prefix
+  const uint32_t m0 = n >= 4 ? 0xffffffffu : (1u << (8 * n)) - 1u;
+  const uint32_t m1 = n <= 4 ? 0u : (1u << (8 * (n - 4))) - 1u;
+  // rates are at most 4, so the byte sums of a multiply do not carry
+  return rec.prefix8[r >> 3] + (((w[0] & m0) * 0x01010101u) >> 24) + (((w[1] & m1) * 0x01010101u) >> 24);
+}
+
+// 128-point Sylvester transform (unnormalized) of the line held as
+// (v0, v1) = elements (lane, lane + 64) of one wave.
+__device__ __forceinline__ void fwht128(float& v0, float& v1, int lane) {
+  const float a = v0 + v1, b = v0 - v1;
+  v0 = a;
+  v1 = b;
+#pragma unroll
+  for (int s = 1; s < 64; s <<= 1) {
+    const float p0 = __shfl_xor(v0, s), p1 = __shfl_xor(v1, s);
+    const bool up = lane & s;
+    v0 = up ? p0 - v0 : v0 + p0;
+    v1 = up ? p1 - v1 : v1 + p1;
+  }
+}
+
+// E4M3 byte -> fp32 by placing its bits in an fp32 pattern (exponent bias
+// 7 instead of 127, codes with a zero exponent landing on fp32 denormals,
+// which these kernels keep) and one exact multiply by 2^120.
+__device__ __forceinline__ float e4m3_scaled(uint32_t b) {
+  return __builtin_bit_cast(float, ((b & 0x7Fu) << 20) | ((b & 0x80u) << 24)) * 0x1p120f;
+}
+
+__device__ __forceinline__ float load_x(const void* x, int dtype, int64_t i) {
+  if (dtype == KQ_DT_F32) return reinterpret_cast<const float*>(x)[i];
+  if (dtype == KQ_DT_F16) return (float)reinterpret_cast<const _Float16*>(x)[i];
+  return (float)reinterpret_cast<const __bf16*>(x)[i];
+}
+
+__device__ __forceinline__ void store_out(void* out, int dtype, int64_t i, float v) {
+  if (dtype == KQ_DT_F32) reinterpret_cast<float*>(out)[i] = v;
+  else if (dtype == KQ_DT_F16) reinterpret_cast<_Float16*>(out)[i] = (_Float16)v;
+  else reinterpret_cast<__bf16*>(out)[i] = (__bf16)v;
+}
+
+// Stage the label table of rate `bits` into LDS (direct loads; the caller
+// waits and crosses a barrier).
+__device__ __forceinline__ void stage_labels(const uint8_t* labels, int bits, uint8_t* lut, int wave, int lane) {
+  const dma::i32x4_t rs = dma::make_rsrc(labels + (int64_t)(bits - 2) * 65536, 65536);
+  const uint32_t base = dma::lds_offset_of(lut);
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const uint32_t c = (uint32_t)__builtin_amdgcn_readfirstlane((it * 16 + wave) * 1024);
+    dma::load_to_lds16(rs, c + (uint32_t)lane * 16u, base + c);
+  }
+}
+
+// One k block's 64 tiles as a stage of the LDS ring: every wave issues
+// exactly one 16-byte-per-lane direct load (waves past the block's 2 K
+// kilobytes read nothing, through an empty resource, into a scratch
+// kilobyte), so every wave has the same number of stage loads in flight.
+// Local tile u = (k tile in block) * 8 + (n tile in block) lands at dword
+// u * 8 K of the stage.  wave is the (uniform) wave index.
+__device__ __forceinline__ void stage_block(const LinArgs& a, const LinRecords& rec, int nb, int kb,
+                                            uint32_t* stage, uint32_t* spill, int wave, int lane) {
+  const int record = a.rate_n ? nb : kb;
+  const int bits = record_rate(rec, record);
+  const int64_t record_dw = (int64_t)RECORD_TILES * (a.rate_n ? a.k_tiles : a.n_tiles) * 8;
+  const int64_t rec0 = (int64_t)record_rates_before(rec, record) * record_dw;
+  const int tile_bytes = 32 * bits;
+  const bool live = wave < 2 * bits;
+  // rate n: the block is 64 consecutive tiles of its record; rate k: 8 runs
+  // of 8 tiles, one per k tile of the block, n_tiles tiles apart
+  const int64_t first_tile = a.rate_n ? (int64_t)kb * 64 : (int64_t)nb * 8;
+  const uint8_t* base = reinterpret_cast<const uint8_t*>(a.payload) + (rec0 * 4 + first_tile * tile_bytes);
+  const int byte = wave * 1024 + lane * 16;
+  const int u = byte / tile_bytes, within = byte - u * tile_bytes;
+  const int64_t rel = a.rate_n ? (int64_t)u : (int64_t)(u >> 3) * a.n_tiles + (u & 7);
+  const dma::i32x4_t rs = dma::make_rsrc(base, live ? (uint32_t)dma::MAX_RANGE : 0u);
+  const uint32_t lds = (uint32_t)__builtin_amdgcn_readfirstlane(
+      (int)(live ? dma::lds_offset_of(stage) + (uint32_t)wave * 1024u : dma::lds_offset_of(spill)));
+  dma::load_to_lds16(rs, live ? (uint32_t)(rel * tile_bytes + within) : 0u, lds);
+}
+
+template <int M, bool ROT>
+__global__ __launch_bounds__(LIN_THREADS) void linear_kernel(LinArgs a, LinRecords rec) {
+  __shared__ __attribute__((aligned(16))) uint8_t lut[65536];
+  __shared__ __attribute__((aligned(16))) uint32_t ring[LIN_STAGES][2048];
+  __shared__ __attribute__((aligned(16))) uint32_t spill[256];
+  __shared__ __attribute__((aligned(16))) float xs[M][lin_max_kb(M) * 128];
+  __shared__ float yb[2][M][128];
+  __shared__ int s_last;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int half = wave >> 3, ntl = wave & 7;
+  const int n_blocks = a.n_tiles >> 3, k_blocks = a.k_tiles >> 3;
+  const int nb = (int)(blockIdx.x % (unsigned)n_blocks), chunk = (int)(blockIdx.x / (unsigned)n_blocks);
+  const int kb0 = chunk * a.kbw;
+  const int kbn = min(a.kbw, k_blocks - kb0);
+  const int64_t m0 = (int64_t)blockIdx.y * M;
+  const int mc = (int)min((int64_t)M, a.m - m0);
+  const int64_t n_cols = (int64_t)a.n_tiles * TILE;
+
+  // labels of the first block's rate, then the first stages of the ring
+  int lut_bits = record_rate(rec, a.rate_n ? nb : kb0);
+  stage_labels(a.labels, lut_bits, lut, wave, lane);
+#pragma unroll
+  for (int j = 0; j < LIN_STAGES; ++j)
+    if (j < kbn) stage_block(a, rec, nb, kb0 + j, ring[j], spill, wave, lane);
+
+  // rotated activation rows of this chunk: lines (row m, k block kbi)
+  for (int line = wave; line < M * kbn; line += 16) {
+    const int m = line / kbn, kbi = line - m * kbn;
+    float v0 = 0.f, v1 = 0.f;
+    if (m < mc) {
+      const int64_t k = (int64_t)(kb0 + kbi) * 128 + lane;
+      const int64_t row = (m0 + m) * a.ldx;
+      v0 = load_x(a.x, a.x_dtype, row + k);
+      v1 = load_x(a.x, a.x_dtype, row + k + 64);
+      if constexpr (ROT) {
+        v0 *= a.suh[k];
+        v1 *= a.suh[k + 64];
+        fwht128(v0, v1, lane);
+      }
+    }
+    xs[m][kbi * 128 + lane] = v0;
+    xs[m][kbi * 128 + lane + 64] = v1;
+  }
+
+  const int r0 = 2 * ((lane >> 1) & 3);
+  float acc[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) acc[m] = 0.f;
+
+  for (int kbi = 0; kbi < kbn; ++kbi) {
+    const int bits = record_rate(rec, a.rate_n ? nb : kb0 + kbi);
+    // stage loads complete in order: block kbi has landed once no more than
+    // the younger stages (min(LIN_STAGES - 1, kbn - 1 - kbi)) are in flight;
+    // the barrier makes every wave's visible (and, on the first pass, the
+    // activation rows and the labels)
+    static_assert(LIN_STAGES == 4, "the waits below count up to three younger stages");
+    const int younger = min(LIN_STAGES - 1, kbn - 1 - kbi);
+    if (younger >= 3) __builtin_amdgcn_s_waitcnt(dma::waitcnt_vm(3));
+    else if (younger == 2) __builtin_amdgcn_s_waitcnt(dma::waitcnt_vm(2));
+    else if (younger == 1) __builtin_amdgcn_s_waitcnt(dma::waitcnt_vm(1));
+    else __builtin_amdgcn_s_waitcnt(dma::waitcnt_vm(0));
+    __syncthreads();
+    if (bits != lut_bits) {  // rate along k changed: restage the labels (uniform)
+      stage_labels(a.labels, bits, lut, wave, lane);
+      __builtin_amdgcn_s_waitcnt(dma::waitcnt_vm(0));
+      __syncthreads();
+      lut_bits = bits;
+    }
+    const uint32_t* stage = ring[kbi % LIN_STAGES];
+    const int sb = ((4 * lane + 1) * bits - 16 + 256 * bits) % (256 * bits);
+    const int d0 = sb >> 5, d1 = (d0 + 1) % (8 * bits), off = sb & 31, sh = 64 - (16 + 3 * bits);
+    uint32_t st[16];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t* t = stage + ((half * 4 + i) * 8 + ntl) * 8 * bits;
+      const uint64_t v = (((uint64_t)t[d0] << 32) | t[d1]) << off;
+      const uint32_t win = (uint32_t)(v >> sh);
+      st[4 * i + 0] = (win >> (3 * bits)) & 0xffffu;
+      st[4 * i + 1] = (win >> (2 * bits)) & 0xffffu;
+      st[4 * i + 2] = (win >> bits) & 0xffffu;
+      st[4 * i + 3] = win & 0xffffu;
+    }
+    float w[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) w[e] = e4m3_scaled(lut[st[e]]);
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int kk = kbi * 128 + (half * 4 + i) * 16 + r0;
+        const float2 xa = *reinterpret_cast<const float2*>(&xs[m][kk]);
+        const float2 xb = *reinterpret_cast<const float2*>(&xs[m][kk + 8]);
+        acc[m] = fmaf(xa.x, w[4 * i + 0], acc[m]);
+        acc[m] = fmaf(xa.y, w[4 * i + 1], acc[m]);
+        acc[m] = fmaf(xb.x, w[4 * i + 2], acc[m]);
+        acc[m] = fmaf(xb.y, w[4 * i + 3], acc[m]);
+      }
+    }
+    // pin the products here: sunk past the barrier below, they would keep
+    // every activation value of the block live across it
+#pragma unroll
+    for (int m = 0; m < M; ++m) asm volatile("" : "+v"(acc[m]));
+    // every wave is done with this stage: refill it with block kbi + stages
+    __syncthreads();
+    if (kbi + LIN_STAGES < kbn)
+      stage_block(a, rec, nb, kb0 + kbi + LIN_STAGES, ring[kbi % LIN_STAGES], spill, wave, lane);
+  }
+
+  // the four lanes of a column (lanes differing in bits 1 and 2) hold its rows
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    acc[m] += __shfl_xor(acc[m], 2);
+    acc[m] += __shfl_xor(acc[m], 4);
+  }
+  if ((lane & 6) == 0) {
+    const int c = ntl * 16 + (lane >> 3) + 8 * (lane & 1);
+#pragma unroll
+    for (int m = 0; m < M; ++m) yb[half][m][c] = acc[m];
+  }
+  __syncthreads();
+
+  const int64_t col0 = (int64_t)nb * 128;
+  if (wave < mc) {
+    const int m = wave;
+    float v0 = yb[0][m][lane] + yb[1][m][lane];
+    float v1 = yb[0][m][lane + 64] + yb[1][m][lane + 64];
+    if constexpr (ROT) {
+      fwht128(v0, v1, lane);
+      v0 *= (1.f / 128.f) * a.svh[col0 + lane];
+      v1 *= (1.f / 128.f) * a.svh[col0 + lane + 64];
+    }
+    if (a.chunks == 1) {
+      store_out(a.out, a.out_dtype, (m0 + m) * a.ldo + col0 + lane, v0);
+      store_out(a.out, a.out_dtype, (m0 + m) * a.ldo + col0 + lane + 64, v1);
+    } else {
+      float* p = a.partial + ((int64_t)chunk * a.m + m0 + m) * n_cols + col0;
+      __hip_atomic_store(p + lane, v0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(p + lane + 64, v1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  if (a.chunks == 1) return;
+
+  // The last chunk to finish this block sums every chunk's partial in order.
+  // Partials travel as agent-scope atomic stores and loads, which bypass the
+  // per-XCD L2s (written through / always missed), so no device-wide fence
+  // (an L2 writeback and invalidate per workgroup) is needed: every wave
+  // waits for its stores to complete before the barrier that precedes the
+  // counter increment, and the last workgroup reads after seeing the count.
+  __builtin_amdgcn_s_waitcnt(dma::waitcnt_vm(0));
+  __syncthreads();
+  int* counter = a.counters + (int64_t)blockIdx.y * n_blocks + nb;
+  if (tid == 0)
+    s_last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == a.chunks - 1;
+  __syncthreads();
+  if (!s_last) return;
+  // TPO adjacent threads per output, thread j of them summing chunks j,
+  // j + TPO, ... (loads issued together), then a fixed shuffle tree
+  constexpr int TPO = LIN_THREADS / (M * 128) > 0 ? LIN_THREADS / (M * 128) : 1;
+  for (int o0 = 0; o0 < M * 128; o0 += LIN_THREADS / TPO) {
+    const int o = o0 + tid / TPO, j = tid % TPO, m = o >> 7, c = o & 127;
+    float sum = 0.f;
+    if (m < mc) {
+      const float* p = a.partial + (m0 + m) * n_cols + col0 + c;
+      const int64_t stride = a.m * n_cols;
+      int ch = j;
+      for (; ch + 3 * TPO < a.chunks; ch += 4 * TPO) {
+        float v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          v[u] = __hip_atomic_load(p + (ch + u * TPO) * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        sum += v[0];
+        sum += v[1];
+        sum += v[2];
+        sum += v[3];
+      }
+      for (; ch < a.chunks; ch += TPO)
+        sum += __hip_atomic_load(p + ch * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+#pragma unroll
+    for (int sft = 1; sft < TPO; sft <<= 1) sum += __shfl_xor(sum, sft);
+    if (j == 0 && m < mc) store_out(a.out, a.out_dtype, (m0 + m) * a.ldo + col0 + c, sum);
+  }
+  if (tid == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 }  // namespace qsrt
 }  // namespace kq
 
@@ -271,4 +598,142 @@ extern "C" int kq_qsrt_decode_states(const int16_t* states, int64_t k_tiles, int
   if (ldo < (tr ? k_tiles * TILE : n_tiles * TILE)) return kq_fail(KQ_ERR_INVALID, "%s: ldo too small", fn);
   return launch_decode<true>(states, k_tiles, n_tiles, rate_axis, RecordRates{}, tile_bits, labels, suh, svh,
                              out_dtype, out, ldo, tr, (hipStream_t)stream, fn);
+}
+
+// ---------------------------------------------------------- fused linear --
+namespace {
+
+struct LinPlan {
+  int mt;      // rows per workgroup (1, 2, 4, 8 or 16)
+  int groups;  // row groups
+  int kbw;     // k blocks per workgroup
+  int chunks;  // workgroups along K
+  int64_t counters_bytes, partial_bytes;
+};
+
+// K chunk per workgroup: the fewest rounds of workgroups times k blocks per
+// workgroup, plus the cost of a cross-workgroup reduction when K is split
+// (ties to the larger chunk: fewer partials to sum).
+constexpr int LIN_REDUCE_KB = 4;
+hipError_t lin_plan(int64_t m, int64_t k_tiles, int64_t n_tiles, LinPlan* p) {
+  int dev = 0, cus = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e != hipSuccess) return e;
+  p->mt = m >= 16 ? 16 : m >= 8 ? 8 : m >= 4 ? 4 : m >= 2 ? 2 : 1;
+  if (p->mt < m && m < 16) p->mt *= 2;
+  p->groups = (int)((m + p->mt - 1) / p->mt);
+  const int64_t n_blocks = n_tiles / RECORD_TILES, k_blocks = k_tiles / RECORD_TILES;
+  const int64_t slots = cus > 0 ? cus : 1;  // one 16-wave workgroup per CU
+  int64_t best = -1;
+  const int max_kb = lin_max_kb(p->mt);
+  for (int kbw = 1; kbw <= max_kb; ++kbw) {
+    const int64_t chunks = (k_blocks + kbw - 1) / kbw;
+    const int64_t rounds = (n_blocks * chunks * p->groups + slots - 1) / slots;
+    // time in units of one k block per workgroup; summing partials across
+    // workgroups costs about LIN_REDUCE_KB more (store, count, reload)
+    const int64_t cost = rounds * kbw + (chunks > 1 ? LIN_REDUCE_KB : 0);
+    if (best < 0 || cost <= best) {
+      best = cost;
+      p->kbw = kbw;
+      p->chunks = (int)chunks;
+    }
+  }
+  p->counters_bytes = (p->chunks > 1 ? (int64_t)p->groups * n_blocks * 4 + 255 : 0) / 256 * 256;
+  p->partial_bytes = p->chunks > 1 ? (int64_t)p->chunks * m * n_tiles * TILE * 4 : 0;
+  return hipSuccess;
+}
+
+template <int M>
+void launch_linear_m(const LinArgs& a, const LinRecords& rec, bool rot, dim3 grid, hipStream_t st) {
+  if (rot) linear_kernel<M, true><<<grid, LIN_THREADS, 0, st>>>(a, rec);
+  else linear_kernel<M, false><<<grid, LIN_THREADS, 0, st>>>(a, rec);
+}
+
+}  // namespace
+
+extern "C" int64_t kq_qsrt_linear_workspace_size(int64_t m, int64_t k_tiles, int64_t n_tiles) {
+  if (m <= 0 || k_tiles <= 0 || n_tiles <= 0 || k_tiles % RECORD_TILES || n_tiles % RECORD_TILES) return 0;
+  LinPlan p;
+  if (lin_plan(m, k_tiles, n_tiles, &p) != hipSuccess) return -1;
+  return p.counters_bytes + p.partial_bytes;
+}
+
+extern "C" int kq_qsrt_linear(const void* x, int x_dtype, int64_t m, int64_t ldx, const int16_t* payload,
+                              int64_t payload_words, int64_t k_tiles, int64_t n_tiles, int rate_axis,
+                              const uint8_t* record_bits, const uint8_t* labels, const float* suh, const float* svh,
+                              int out_dtype, void* out, int64_t ldo, void* workspace, int64_t ws_bytes,
+                              void* stream) {
+  const char* fn = "kq_qsrt_linear";
+  if (rate_axis != 0 && rate_axis != 1) return kq_fail(KQ_ERR_INVALID, "%s: rate_axis must be 0 (k) or 1 (n)", fn);
+  if (m < 0) return kq_fail(KQ_ERR_INVALID, "%s: negative row count", fn);
+  if (k_tiles <= 0 || n_tiles <= 0 || k_tiles % RECORD_TILES || n_tiles % RECORD_TILES)
+    return kq_fail(KQ_ERR_INVALID, "%s: both dimensions must be positive multiples of 128 (%lld x %lld tiles)", fn,
+                   (long long)k_tiles, (long long)n_tiles);
+  if (x_dtype < KQ_DT_BF16 || x_dtype > KQ_DT_F32 || out_dtype < KQ_DT_BF16 || out_dtype > KQ_DT_F32)
+    return kq_fail(KQ_ERR_INVALID, "%s: bad activation or output dtype", fn);
+  if ((suh == nullptr) != (svh == nullptr)) return kq_fail(KQ_ERR_INVALID, "%s: give both suh and svh or neither", fn);
+  const int64_t rows = k_tiles * TILE, cols = n_tiles * TILE;
+  if (m == 0) return KQ_OK;
+  if (!x || !payload || !record_bits || !labels || !out) return kq_fail(KQ_ERR_INVALID, "%s: null buffer", fn);
+  if (kq_misaligned(payload, 4)) return kq_fail(KQ_ERR_INVALID, "%s: payload must be 4-byte aligned", fn);
+  if (ldx < rows || ldo < cols) return kq_fail(KQ_ERR_INVALID, "%s: ldx or ldo too small", fn);
+  const int64_t records = (rate_axis ? n_tiles : k_tiles) / RECORD_TILES;
+  if (records > MAX_RECORDS)
+    return kq_fail(KQ_ERR_LIMIT, "%s: %lld records (at most %d)", fn, (long long)records, MAX_RECORDS);
+  const int64_t per_record = (int64_t)RECORD_TILES * (rate_axis ? k_tiles : n_tiles);
+  LinRecords rec{};
+  int64_t words = 0;
+  uint32_t sum = 0;
+  for (int64_t r = 0; r < records; ++r) {
+    const int b = record_bits[r];
+    if (b < 2 || b > 4) return kq_fail(KQ_ERR_INVALID, "%s: record %lld has rate %d (K2..K4 only)", fn, (long long)r, b);
+    if (r % 8 == 0) rec.prefix8[r / 8] = sum;
+    rec.bits[r] = (uint8_t)b;
+    sum += (uint32_t)b;
+    words += per_record * TILE * b;
+  }
+  if (words != payload_words)
+    return kq_fail(KQ_ERR_INVALID, "%s: payload has %lld words, the records need %lld", fn,
+                   (long long)payload_words, (long long)words);
+  LinPlan p;
+  hipError_t e = lin_plan(m, k_tiles, n_tiles, &p);
+  if (e != hipSuccess) return kq_check_launch(e, fn);
+  const int64_t need = p.counters_bytes + p.partial_bytes;
+  if (need > 0 && (!workspace || ws_bytes < need || kq_misaligned(workspace, 256)))
+    return kq_fail(KQ_ERR_INVALID, "%s: workspace needs %lld bytes (256-byte aligned, zeroed before first use)", fn,
+                   (long long)need);
+  const int64_t n_blocks = n_tiles / RECORD_TILES;
+  if (n_blocks * p.chunks > 0x7fffffff || p.groups > 65535)
+    return kq_fail(KQ_ERR_LIMIT, "%s: too many workgroups", fn);
+  LinArgs a{};
+  a.x = x;
+  a.ldx = ldx;
+  a.m = m;
+  a.payload = reinterpret_cast<const uint32_t*>(payload);
+  a.labels = labels;
+  a.suh = suh;
+  a.svh = svh;
+  a.out = out;
+  a.ldo = ldo;
+  a.counters = need > 0 ? static_cast<int*>(workspace) : nullptr;
+  a.partial = need > 0 ? reinterpret_cast<float*>(static_cast<char*>(workspace) + p.counters_bytes) : nullptr;
+  a.k_tiles = (int)k_tiles;
+  a.n_tiles = (int)n_tiles;
+  a.rate_n = rate_axis;
+  a.kbw = p.kbw;
+  a.chunks = p.chunks;
+  a.x_dtype = x_dtype;
+  a.out_dtype = out_dtype;
+  const dim3 grid((unsigned)(n_blocks * p.chunks), (unsigned)p.groups);
+  const bool rot = suh != nullptr;
+  const hipStream_t st = (hipStream_t)stream;
+  switch (p.mt) {
+    case 1: launch_linear_m<1>(a, rec, rot, grid, st); break;
+    case 2: launch_linear_m<2>(a, rec, rot, grid, st); break;
+    case 4: launch_linear_m<4>(a, rec, rot, grid, st); break;
+    case 8: launch_linear_m<8>(a, rec, rot, grid, st); break;
+    default: launch_linear_m<16>(a, rec, rot, grid, st); break;
+  }
+  return kq_check_launch(hipGetLastError(), fn);
 }

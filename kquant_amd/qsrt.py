@@ -11,8 +11,11 @@ and, as the payload-level decode a serving loader needs (the role of
 ``decode_qsrt_exl3_weight``, :1107-1141, minus the mode tables of the
 Kimi-K3 checkpoint schema), ``decode_qsrt_payload``: one launch from the
 packed payload of 128-channel records to the EXL-oriented weight
-(``kq_qsrt_decode_weight``).  CPU inputs run on the current GPU and come
-back on the CPU.
+(``kq_qsrt_decode_weight``).  ``qsrt_linear`` applies such a matrix to
+activation rows without building the weight (``kq_qsrt_linear``): the
+serving step of scripts/stream_k3_pytorch.py:771-775, which decodes the
+dense weight and then runs the linear.  CPU inputs run on the current GPU
+and come back on the CPU.
 """
 
 from __future__ import annotations
@@ -80,14 +83,26 @@ def unpack_trellis_states(packed: torch.Tensor, bits: int) -> torch.Tensor:
     return _unpack(packed, bits, True)
 
 
+_LABELS: dict[tuple[str, str | None, torch.device], torch.Tensor] = {}
+_LINEAR_WORKSPACES: dict[torch.device, torch.Tensor] = {}
+
+
 def rate_labels(codebook: str = SQG_XOR_CHEB_T12, *, rate_axis: str | None = None,
                 device: torch.device | str | None = None) -> torch.Tensor:
     """The K2, K3 and K4 state labels of a codebook as one uint8 [3, 65536]
-    device table (the layout the decode kernels read)."""
+    device table (the layout the decode kernels read); built once per
+    codebook, rate axis and device."""
 
     gpu = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
-    return torch.stack([sqg_codebook_bytes(bits, codebook, rate_axis=rate_axis, device=gpu)
-                        for bits in (2, 3, 4)]).contiguous()
+    if gpu.index is None:
+        gpu = torch.device(gpu.type, torch.cuda.current_device())
+    key = (codebook, rate_axis, gpu)
+    table = _LABELS.get(key)
+    if table is None:
+        table = torch.stack([sqg_codebook_bytes(bits, codebook, rate_axis=rate_axis, device=gpu)
+                             for bits in (2, 3, 4)]).contiguous()
+        _LABELS[key] = table
+    return table
 
 
 def decode_qsrt_payload(
@@ -136,4 +151,131 @@ def decode_qsrt_payload(
     N.call("kq_qsrt_decode_weight", N.ptr(g), g.numel(), k_tiles, n_tiles, 0 if rate_axis == "k" else 1,
            bits, N.ptr(labels), N.ptr(su), N.ptr(sv), N.DTYPE_CODES[out_dtype], N.ptr(out), shape[1],
            N.QSRT_TRANSPOSED if transposed else 0, N.stream(gpu))
+    return out if host is None else out.to(host)
+
+
+def _check_record_bits(record_bits) -> bytes:
+    bits = bytes(int(b) for b in record_bits)
+    if any(b not in (2, 3, 4) for b in bits):
+        raise ValueError("tile_bits must contain only integer K2, K3, or K4")
+    return bits
+
+
+def qsrt_linear_launcher(
+    x: torch.Tensor,
+    payload: torch.Tensor,
+    out: torch.Tensor,
+    *,
+    k_tiles: int,
+    n_tiles: int,
+    rate_axis: str,
+    record_bits,
+    suh: torch.Tensor | None = None,
+    svh: torch.Tensor | None = None,
+    codebook: str = SQG_XOR_CHEB_T12,
+):
+    """A zero-argument callable that writes ``x @ W`` into ``out`` with fixed
+    device buffers (x [m, K] and out [m, N] on the payload's GPU, row-major):
+    every check, table and workspace is settled once, so the call is one
+    launch and may be captured in a HIP graph."""
+
+    if rate_axis not in ("k", "n"):
+        raise ValueError("rate_axis must be 'k' or 'n'")
+    if payload.dtype != torch.int16 or payload.ndim != 1 or not payload.is_cuda:
+        raise TypeError("QSRT trellis payload must be a one-dimensional torch.int16 GPU tensor")
+    if (suh is None) != (svh is None):
+        raise ValueError("pass both suh and svh, or neither")
+    if x.dtype not in N.DTYPE_CODES or out.dtype not in N.DTYPE_CODES:
+        raise TypeError("x and out must be bfloat16, float16 or float32")
+    k, n = k_tiles * TILE_CHANNELS, n_tiles * TILE_CHANNELS
+    if x.ndim != 2 or x.shape[1] != k or x.stride(1) != 1:
+        raise ValueError(f"x must be [m, {k}] with unit column stride")
+    if out.shape != (x.shape[0], n) or out.stride(1) != 1:
+        raise ValueError(f"out must be [{x.shape[0]}, {n}] with unit column stride")
+    gpu = payload.device
+    if x.device != gpu or out.device != gpu:
+        raise ValueError("x, out and the payload must be on one GPU")
+    if payload.data_ptr() % 4:
+        raise ValueError("the payload must be 4-byte aligned")
+    bits = _check_record_bits(record_bits)
+    m = x.shape[0]
+    labels = rate_labels(codebook, rate_axis=rate_axis, device=gpu)
+    su = sv = None
+    if suh is not None:
+        if suh.numel() != k or svh.numel() != n:
+            raise ValueError("suh and svh must match the K and N dimensions")
+        su = N.aligned(suh.to(device=gpu, dtype=torch.float32).reshape(-1), 4)
+        sv = N.aligned(svh.to(device=gpu, dtype=torch.float32).reshape(-1), 4)
+    need = int(N.library().kq_qsrt_linear_workspace_size(max(m, 1), k_tiles, n_tiles)) if m else 0
+    if need < 0:
+        raise RuntimeError("kq_qsrt_linear_workspace_size: no HIP device")
+    ws = torch.zeros(need, dtype=torch.uint8, device=gpu) if need else None  # counters start (and stay) at zero
+    args = (N.ptr(x), N.DTYPE_CODES[x.dtype], m, x.stride(0) if m else k, N.ptr(payload), payload.numel(),
+            k_tiles, n_tiles, 0 if rate_axis == "k" else 1, bits, N.ptr(labels), N.ptr(su), N.ptr(sv),
+            N.DTYPE_CODES[out.dtype], N.ptr(out), out.stride(0) if m else n, N.ptr(ws), need)
+    keep = (x, payload, out, labels, su, sv, ws)  # the buffers the pointers refer to
+
+    def run(_keep=keep) -> None:
+        N.call("kq_qsrt_linear", *args, N.stream(gpu))
+
+    return run
+
+
+def qsrt_linear(
+    x: torch.Tensor,
+    payload: torch.Tensor,
+    *,
+    k_tiles: int,
+    n_tiles: int,
+    rate_axis: str,
+    record_bits,
+    suh: torch.Tensor | None = None,
+    svh: torch.Tensor | None = None,
+    codebook: str = SQG_XOR_CHEB_T12,
+    out_dtype: torch.dtype | None = None,
+) -> torch.Tensor:
+    """``x @ W`` for the packed QSRT matrix W of ``decode_qsrt_payload``
+    (same arguments), computed from the trellis words directly: x [..., K]
+    (bf16, fp16 or fp32) -> [..., N] in ``out_dtype`` (default x's dtype),
+    fp32 arithmetic inside.  For the reference's dense path this is
+    ``F.linear(x, decode_qsrt_exl3_weight(...).T)`` without the bf16 weight
+    it materializes (scripts/stream_k3_pytorch.py:771-775)."""
+
+    if rate_axis not in ("k", "n"):
+        raise ValueError("rate_axis must be 'k' or 'n'")
+    if payload.dtype != torch.int16 or payload.ndim != 1:
+        raise TypeError("QSRT trellis payload must be a one-dimensional torch.int16 tensor")
+    if (suh is None) != (svh is None):
+        raise ValueError("pass both suh and svh, or neither")
+    if x.dtype not in N.DTYPE_CODES:
+        raise TypeError("x must be bfloat16, float16 or float32")
+    k, n = k_tiles * TILE_CHANNELS, n_tiles * TILE_CHANNELS
+    if x.shape[-1] != k:
+        raise ValueError(f"x has {x.shape[-1]} features, the matrix has K = {k}")
+    bits = _check_record_bits(record_bits)
+    out_dtype = x.dtype if out_dtype is None else out_dtype
+    (g, xg), gpu, host = N.to_gpu([payload, x])
+    g = N.aligned(g, 4)
+    rows = xg.reshape(-1, k)
+    rows = rows if rows.stride(-1) == 1 else rows.contiguous()
+    m = rows.shape[0]
+    labels = rate_labels(codebook, rate_axis=rate_axis, device=gpu)
+    su = sv = None
+    if suh is not None:
+        if suh.numel() != k or svh.numel() != n:
+            raise ValueError("suh and svh must match the K and N dimensions")
+        su = N.aligned(suh.to(device=gpu, dtype=torch.float32).reshape(-1), 4)
+        sv = N.aligned(svh.to(device=gpu, dtype=torch.float32).reshape(-1), 4)
+    out = torch.empty(m, n, dtype=out_dtype, device=gpu)
+    need = int(N.library().kq_qsrt_linear_workspace_size(max(m, 1), k_tiles, n_tiles)) if m else 0
+    if need < 0:
+        raise RuntimeError("kq_qsrt_linear_workspace_size: no HIP device")
+    ws = _LINEAR_WORKSPACES.get(gpu)
+    if need and (ws is None or ws.numel() < need):
+        ws = torch.zeros(need, dtype=torch.uint8, device=gpu)  # counters start (and stay) at zero
+        _LINEAR_WORKSPACES[gpu] = ws
+    N.call("kq_qsrt_linear", N.ptr(rows), N.DTYPE_CODES[rows.dtype], m, rows.stride(0) if m else k, N.ptr(g),
+           g.numel(), k_tiles, n_tiles, 0 if rate_axis == "k" else 1, bits, N.ptr(labels), N.ptr(su), N.ptr(sv),
+           N.DTYPE_CODES[out_dtype], N.ptr(out), n, N.ptr(ws) if need else None, need, N.stream(gpu))
+    out = out.reshape(*x.shape[:-1], n)
     return out if host is None else out.to(host)

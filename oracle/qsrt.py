@@ -12,6 +12,8 @@ numpy restatements of:
   decode_qsrt_weight                          kquant/exl3_reference.py:149-192,
       270-295 (per-record rate tables, then B_K W B_N with suh / svh)
   record tile order of a packed payload       kquant/qsrt.py:974-1018
+  qsrt_linear                                 x @ decode_qsrt_weight(...), the
+      dense serving use (scripts/stream_k3_pytorch.py:771-775)
 Pinned in tests/test_oracle_qsrt.py by the reference's own known answers
 (tests/test_qsrt.py:215-268: packed word prefixes, low-bit round trips, the
 scalar recurrence) and tests/test_sqg_e4m3.py:163-200 (custom-codebook and
@@ -136,3 +138,10 @@ def decode_qsrt_weight(payload, k_tiles, n_tiles, record_bits, rate_axis, labels
         return weight
     w = blockwise_hadamard(weight, 3)
     return w * np.asarray(suh, dtype=np.float64)[:, None] * np.asarray(svh, dtype=np.float64)[None, :]
+
+
+def qsrt_linear(x, payload, k_tiles, n_tiles, record_bits, rate_axis, labels_by_bits, suh=None, svh=None):
+    """x [M, K] @ W in f64, W = decode_qsrt_weight(...) (the dense serving
+    path: decode, then the linear; scripts/stream_k3_pytorch.py:771-775)."""
+    weight = decode_qsrt_weight(payload, k_tiles, n_tiles, record_bits, rate_axis, labels_by_bits, suh, svh)
+    return np.asarray(x, dtype=np.float64) @ np.asarray(weight, dtype=np.float64)

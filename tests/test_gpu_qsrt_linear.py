@@ -1,0 +1,147 @@
+"""GPU parity of the fused QSRT linear (kq_qsrt_linear through
+kquant_amd.qsrt.qsrt_linear) against oracle/qsrt.py (x @ the decoded weight,
+f64).  One-hot activation rows read the regularized weight back exactly
+(each output is one product 1 * label plus exact zeros), which pins the
+state windows, label lookup and tensor-core order bit for bit; random rows
+through the rotated weight must agree with the f64 product to within 4e-6
+of max |ref| for fp32 output (fp32 products and sums over K <= 2048), and
+bf16 output must be that result rounded once (within one bf16 ulp of the
+f64 value).  Row counts cover every row tile (1, 2, 4, 8), several row
+groups, single- and multi-chunk K splits, both rate axes and mixed rates."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from kquant_amd import qsrt
+from oracle import qsrt as oq
+
+pytestmark = pytest.mark.gpu
+
+_LABELS = {b: oracle.sqg_xor_cheb_t12_bytes(b) for b in (2, 3, 4)}
+
+
+def _random_matrix(k_tiles, n_tiles, rate_axis, record_bits, seed):
+    rng = np.random.default_rng(seed)
+    states = np.zeros((k_tiles, n_tiles, 256), dtype=np.int16)
+    for kt in range(k_tiles):
+        for nt in range(n_tiles):
+            bits = record_bits[(kt if rate_axis == "k" else nt) // 8]
+            states[kt, nt] = oq.reconstruct_trellis_states(rng.integers(0, 1 << bits, 256), bits)
+    return oq.pack_payload(states, record_bits, rate_axis)
+
+
+def _scales(k_tiles, n_tiles, seed):
+    rng = np.random.default_rng(seed)
+    suh = rng.choice([-1.0, 1.0], k_tiles * 16).astype(np.float32) * rng.uniform(0.5, 1.5, k_tiles * 16)
+    svh = rng.uniform(0.5, 2.0, n_tiles * 16).astype(np.float32)
+    return suh.astype(np.float32), svh
+
+
+@pytest.mark.parametrize("rate_axis", ["k", "n"])
+def test_one_hot_rows_read_the_weight_exactly(gpu, rate_axis):
+    k_tiles, n_tiles = (24, 16) if rate_axis == "k" else (16, 24)
+    record_bits = (2, 4, 3)
+    payload = _random_matrix(k_tiles, n_tiles, rate_axis, record_bits, 11)
+    want = oq.decode_qsrt_weight(payload, k_tiles, n_tiles, record_bits, rate_axis, _LABELS)
+    rows = np.arange(0, k_tiles * 16, 7)  # every residue of the tile rows and both k halves
+    x = np.zeros((rows.size, k_tiles * 16), dtype=np.float32)
+    x[np.arange(rows.size), rows] = 1.0
+    got = qsrt.qsrt_linear(torch.from_numpy(x).to(gpu), torch.from_numpy(payload).to(gpu), k_tiles=k_tiles,
+                           n_tiles=n_tiles, rate_axis=rate_axis, record_bits=record_bits)
+    assert got.dtype == torch.float32
+    assert np.array_equal(got.cpu().numpy(), want[rows])
+
+
+@pytest.mark.parametrize("rate_axis,m,shape,record_bits", [
+    ("n", 1, (16, 24), (3, 2, 4)),
+    ("n", 2, (128, 16), (4, 3)),
+    ("k", 3, (24, 16), (2, 4, 3)),
+    ("k", 8, (64, 8), (3, 3, 2, 2, 4, 4, 3, 2)),
+    ("n", 13, (32, 32), (2, 3, 4, 3)),
+    ("k", 37, (16, 40), (4, 2)),
+])
+def test_rotated_product_matches_oracle(gpu, rate_axis, m, shape, record_bits):
+    k_tiles, n_tiles = shape
+    payload = _random_matrix(k_tiles, n_tiles, rate_axis, record_bits, m)
+    suh, svh = _scales(k_tiles, n_tiles, m + 1)
+    x = np.random.default_rng(m + 2).standard_normal((m, k_tiles * 16)).astype(np.float32)
+    ref = oq.qsrt_linear(x, payload, k_tiles, n_tiles, record_bits, rate_axis, _LABELS, suh, svh)
+    args = dict(k_tiles=k_tiles, n_tiles=n_tiles, rate_axis=rate_axis, record_bits=record_bits,
+                suh=torch.from_numpy(suh), svh=torch.from_numpy(svh))
+    p = torch.from_numpy(payload).to(gpu)
+    xg = torch.from_numpy(x).to(gpu)
+    got = qsrt.qsrt_linear(xg, p, **args).cpu().numpy().astype(np.float64)
+    scale = np.abs(ref).max()
+    assert np.abs(got - ref).max() <= 4e-6 * scale
+    # bf16 output: the fp32 result rounded once
+    got16 = qsrt.qsrt_linear(xg, p, out_dtype=torch.bfloat16, **args).cpu().float().numpy()
+    assert np.all(np.abs(got16 - ref) <= np.abs(ref) * 2.0 ** -8 + 4e-6 * scale)
+    # bf16 activations: the same product of the bf16-rounded rows
+    xb = xg.to(torch.bfloat16)
+    refb = oq.qsrt_linear(xb.float().cpu().numpy(), payload, k_tiles, n_tiles, record_bits, rate_axis, _LABELS,
+                          suh, svh)
+    gotb = qsrt.qsrt_linear(xb, p, out_dtype=torch.float32, **args).cpu().numpy()
+    assert np.abs(gotb - refb).max() <= 4e-6 * np.abs(refb).max()
+
+
+def test_matches_decode_then_matmul_and_reuses_workspace(gpu):
+    """Kimi-K3 w1 geometry (EXL [K=3584, N=3072], 24 records along n):
+    several calls in a row, shrinking and growing, share the workspace whose
+    completion counters every call leaves at zero."""
+    k_tiles, n_tiles = 224, 192
+    record_bits = (2, 4) * 2 + (3,) * 20
+    g = torch.Generator(device=gpu).manual_seed(3)
+    words = sum(8 * k_tiles * 16 * b for b in record_bits)
+    p = torch.randint(-32768, 32768, (words,), dtype=torch.int16, generator=g, device=gpu)
+    suh = torch.randn(k_tiles * 16, generator=g, device=gpu).sign()
+    svh = torch.rand(n_tiles * 16, generator=g, device=gpu) + 0.5
+    args = dict(k_tiles=k_tiles, n_tiles=n_tiles, rate_axis="n", record_bits=record_bits, suh=suh, svh=svh)
+    w = qsrt.decode_qsrt_payload(p, **args).double()
+    for m in (4, 1, 16, 5):
+        x = torch.randn(m, k_tiles * 16, generator=g, device=gpu)
+        ref = x.double() @ w
+        got = qsrt.qsrt_linear(x, p, **args).double()
+        assert (got - ref).abs().max().item() <= 4e-6 * ref.abs().max().item(), m
+    assert qsrt.qsrt_linear(torch.empty(0, k_tiles * 16, device=gpu), p, **args).shape == (0, n_tiles * 16)
+
+
+def test_argument_errors(gpu):
+    p = torch.zeros(8 * 8 * 16 * 3 * 2, dtype=torch.int16, device=gpu)
+    x = torch.zeros(1, 128, device=gpu)
+    with pytest.raises(ValueError, match="features"):
+        qsrt.qsrt_linear(torch.zeros(1, 64, device=gpu), p, k_tiles=8, n_tiles=16, rate_axis="n", record_bits=(3, 3))
+    with pytest.raises(ValueError, match="K2, K3, or K4"):
+        qsrt.qsrt_linear(x, p, k_tiles=8, n_tiles=16, rate_axis="n", record_bits=(3, 5))
+    with pytest.raises(RuntimeError, match="payload has"):
+        qsrt.qsrt_linear(x, p, k_tiles=8, n_tiles=16, rate_axis="n", record_bits=(3, 2))
+
+
+def test_launcher_in_a_graph_replays_the_eager_result(gpu):
+    """The prepared launcher captured in a HIP graph: every replay (with eager
+    work and synchronizations between) equals the eager call bit for bit,
+    since the K split and its summation order are fixed."""
+    k_tiles, n_tiles = 64, 24
+    record_bits = (3, 2, 4)
+    payload = torch.from_numpy(_random_matrix(k_tiles, n_tiles, "n", record_bits, 21)).to(gpu)
+    suh, svh = (torch.from_numpy(v).to(gpu) for v in _scales(k_tiles, n_tiles, 22))
+    x = torch.randn(3, k_tiles * 16, generator=torch.Generator(device=gpu).manual_seed(23), device=gpu)
+    args = dict(k_tiles=k_tiles, n_tiles=n_tiles, rate_axis="n", record_bits=record_bits, suh=suh, svh=svh)
+    eager = qsrt.qsrt_linear(x, payload, **args)
+    out = torch.empty_like(eager)
+    run = qsrt.qsrt_linear_launcher(x, payload, out, **args)
+    run()
+    torch.cuda.synchronize()
+    assert torch.equal(out, eager)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        run()
+    for i in range(4):
+        out.zero_()
+        qsrt.qsrt_linear(x[:1], payload, **args)  # eager work sharing nothing with the graph
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), i

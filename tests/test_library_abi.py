@@ -34,7 +34,7 @@ def test_python_binding_covers_every_entry_point():
     bound = set(_native.SIGNATURES) | {"kq_version", "kq_last_error", "kq_moe_workspace_size",
                                         "kq_moe_x4t_workspace_size", "kq_mx_linear_f32_workspace_size",
                                         "kq_cholesky_workspace_size", "kq_block_ldl_workspace_size",
-                                        "kq_sqg_quantize_workspace_size",
+                                        "kq_sqg_quantize_workspace_size", "kq_qsrt_linear_workspace_size",
                                         "kq_route_sort_workspace_size"}
     assert set(declared_symbols()) <= bound
 
@@ -87,3 +87,30 @@ def test_ldl_argument_errors_need_no_gpu():
     assert rc == _native.KQ_ERR_INVALID and b"multiple of 128" in lib.kq_last_error()
     rc = lib.kq_h_regularize(fake, 10, 10, -1.0, 0.025, None, fake, None)
     assert rc == _native.KQ_ERR_INVALID
+
+
+def test_qsrt_linear_argument_errors_need_no_gpu():
+    lib = _native.library()
+    fake = ctypes.c_void_p(256)  # never dereferenced: validation fails first
+    bits = bytes([3] * 2)
+    assert lib.kq_qsrt_linear_workspace_size(1, 12, 16) == 0  # K not a multiple of 128
+    args = [fake, _native.DT_BF16, 1, 256, fake, 2 * 8 * 16 * 16 * 3, 16, 16, 1, bits, fake, None, None,
+            _native.DT_F32, fake, 256, None, 0, None]
+    bad_axis = list(args)
+    bad_axis[8] = 2
+    assert lib.kq_qsrt_linear(*bad_axis) == _native.KQ_ERR_INVALID and b"rate_axis" in lib.kq_last_error()
+    bad_words = list(args)
+    bad_words[5] -= 1
+    assert lib.kq_qsrt_linear(*bad_words) == _native.KQ_ERR_INVALID and b"payload has" in lib.kq_last_error()
+    bad_rate = list(args)
+    bad_rate[9] = bytes([3, 5])
+    assert lib.kq_qsrt_linear(*bad_rate) == _native.KQ_ERR_INVALID and b"rate 5" in lib.kq_last_error()
+    odd = list(args)
+    odd[4] = ctypes.c_void_p(258)
+    assert lib.kq_qsrt_linear(*odd) == _native.KQ_ERR_INVALID and b"4-byte aligned" in lib.kq_last_error()
+    half = list(args)
+    half[11] = fake
+    assert lib.kq_qsrt_linear(*half) == _native.KQ_ERR_INVALID and b"suh and svh" in lib.kq_last_error()
+    narrow = list(args)
+    narrow[3] = 100
+    assert lib.kq_qsrt_linear(*narrow) == _native.KQ_ERR_INVALID and b"ldx" in lib.kq_last_error()
