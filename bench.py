@@ -481,6 +481,39 @@ def main() -> int:
                 row[f"m{m}_us"] = round(_time_loop(torch, graph.replay, 10, 3) / reps * 1e6, 2)
             row["weight_bytes"] = int(p_.numel() * 2)
             lin[name] = row
+        # routed experts at the Kimi-K3 TP12-local geometry (H = 3584, 256
+        # intermediate channels per rank, top-16), QSRT P33-like rates (K3)
+        h_, i_, n_exp, topk_ = 3584, 256, 64, 16
+
+        def rand_mat(k, n, axis, bits_each):
+            records = (k if axis == "k" else n) // 128
+            per = 8 * ((n if axis == "k" else k) // 16)
+            w_ = per * 16 * bits_each * records
+            return (torch.randint(-32768, 32768, (w_,), dtype=torch.int16, generator=gq, device=dev),
+                    (bits_each,) * records, torch.randn(k, generator=gq, device=dev).sign(),
+                    torch.rand(n, generator=gq, device=dev) + 0.5)
+
+        mats_ = [[rand_mat(h_, i_, "n", 3), rand_mat(h_, i_, "n", 3), rand_mat(i_, h_, "k", 3)] for _ in range(n_exp)]
+        qexp = kq_qsrt.QSRTExperts([m[0] for m in mats_], [m[1] for m in mats_], [m[2] for m in mats_],
+                                   hidden=h_, inter=i_)
+        moe_q = {}
+        for toks in (1, 4):
+            xq = torch.randn(toks, h_, generator=gq, device=dev).to(torch.bfloat16)
+            ids_ = torch.stack([torch.randperm(n_exp, generator=torch.Generator().manual_seed(t))[:topk_]
+                                for t in range(toks)]).to(device=dev, dtype=torch.int32)
+            wts_ = torch.rand(toks, topk_, generator=gq, device=dev)
+            kq_qsrt.qsrt_expert_forward(xq, ids_, wts_, qexp)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                for _ in range(reps):
+                    kq_qsrt.qsrt_expert_forward(xq, ids_, wts_, qexp)
+            moe_q[f"tokens{toks}_us"] = round(_time_loop(torch, graph.replay, 10, 3) / reps * 1e6, 2)
+        qres["qsrt_moe_decode_tp12"] = {
+            "workload": "routed expert forward, H=3584, I=256 per rank, top-16, QSRT K3 w1/w3/w2, bf16 in/out, "
+                        "fp32 math; time per forward from a HIP graph of 20",
+            **moe_q,
+            "reference_split_k_w4a16_qsrt_us": {"P33": 56.90, "P24": 65.09},
+        }
         qres["qsrt_linear"] = {
             "workload": "x[m, K] bf16 @ QSRT W (rotated, fp32 math) -> bf16; time per call from a HIP "
                         "graph of 20 back-to-back calls",

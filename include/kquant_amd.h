@@ -392,14 +392,57 @@ int kq_qsrt_decode_states(const int16_t* states, int64_t k_tiles, int64_t n_tile
  * bf16), so the result is the exact product up to fp32 summation order.
  * Meant for decode-sized batches: every 16 rows decode the weight once more.
  * workspace: kq_qsrt_linear_workspace_size(rows, k_tiles, n_tiles) bytes
- * (may be 0), 256-byte aligned and zeroed before its first use; each call
- * leaves it zeroed again.  Calls sharing a workspace must not overlap. */
+ * (may be 0), 256-byte aligned and zeroed before its first use with these
+ * sizes; each call leaves its completion counters at zero again, so it
+ * serves repeated calls of the same sizes (zero it again before other
+ * sizes: the counters' place depends on them).  Calls sharing a workspace
+ * must not overlap. */
 int64_t kq_qsrt_linear_workspace_size(int64_t rows, int64_t k_tiles, int64_t n_tiles);
 int kq_qsrt_linear(const void* x, int x_dtype, int64_t rows, int64_t ldx, const int16_t* payload,
                    int64_t payload_words, int64_t k_tiles, int64_t n_tiles, int rate_axis,
                    const uint8_t* record_bits, const uint8_t* labels, const float* suh, const float* svh,
                    int out_dtype, void* out, int64_t ldo, void* workspace, int64_t workspace_bytes,
                    void* stream);
+
+/* One QSRT-coded matrix as kq_qsrt_moe_decode reads it (device pointers):
+ * its packed payload (4-byte aligned), record_prefix [records + 1] uint32
+ * with record_prefix[r] = the sum of the rates of the records before r (so
+ * record r has rate record_prefix[r + 1] - record_prefix[r], 2..4), and its
+ * suh [K] / svh [N] fp32 scales. */
+typedef struct {
+  const int16_t* payload;
+  const uint32_t* record_prefix;
+  const float* suh;
+  const float* svh;
+} kq_qsrt_matrix;
+
+/* Routed expert forward of a decode batch with QSRT-coded experts (no
+ * kquant counterpart as a kernel: the reference decodes each routed
+ * expert's w1 / w3 / w2 to dense bf16, scripts/stream_k3_pytorch.py:771-775,
+ * and runs the expert MLP of scripts/closure_exl3_layer.py:557-598):
+ *   for every pair (t, s) with e = route_ids[t, s] in [0, experts):
+ *     g = x_t W1_e, u = x_t W3_e        (EXL orientation: W1, W3 [H, I])
+ *     out_t += route_weights[t, s] * act(g, u) W2_e     (W2 [I, H])
+ * in fp32 (the intermediate is not rounded), out = 0 for tokens with no
+ * valid expert.  mats: device array [experts][3] (w1, w3, w2) of
+ * kq_qsrt_matrix, all experts of one geometry: hidden H = 16 hidden_tiles,
+ * intermediate I = 16 inter_tiles (multiples of 128), w1 / w3 records
+ * along rate13_axis, w2 along rate2_axis (0 = k, 1 = n), payload sizes as
+ * their records require (not checked here: the descriptors live on the
+ * device).  x [tokens, ldx >= H] x_dtype, route_ids int32 / route_weights
+ * fp32 [tokens, topk], labels 2 x 3 x 65536 E4M3 bytes: the K2..K4 state
+ * labels (as kq_qsrt_decode_weight) for w1 / w3, then for w2 (a codebook
+ * may depend on the rate axis, kquant/sqg_e4m3.py:305-340), out [tokens,
+ * ldo >= H] out_dtype.  Two launches; deterministic.  workspace:
+ * kq_qsrt_moe_workspace_size bytes, 256-byte aligned, zeroed before its
+ * first use with these sizes (calls leave its counters at zero; zero it
+ * again before other sizes); calls sharing it must not overlap. */
+int64_t kq_qsrt_moe_workspace_size(int64_t tokens, int topk, int64_t hidden_tiles, int64_t inter_tiles);
+int kq_qsrt_moe_decode(int act, float beta, float linear_beta, const void* x, int x_dtype, int64_t tokens,
+                       int64_t ldx, const int32_t* route_ids, const float* route_weights, int topk,
+                       const kq_qsrt_matrix* mats, int experts, int64_t hidden_tiles, int64_t inter_tiles,
+                       int rate13_axis, int rate2_axis, const uint8_t* labels, int out_dtype, void* out,
+                       int64_t ldo, void* workspace, int64_t workspace_bytes, void* stream);
 
 /* SQG trellis quantizer: the tail-biting Viterbi search of
  * kquant/csrc/qsrt_quantize_tiles_kernel.cuh with the SQG E4M3 labels of

@@ -101,6 +101,8 @@ SIGNATURES: dict[str, list] = {
     "kq_qsrt_decode_weight": [_VP, _I64, _I64, _I64, _INT, _VP, _VP, _VP, _VP, _INT, _VP, _I64, _U32, _VP],
     "kq_qsrt_decode_states": [_VP, _I64, _I64, _INT, _VP, _VP, _VP, _VP, _INT, _VP, _I64, _U32, _VP],
     "kq_sqg_quantize_tiles": [_VP, _I64, _VP, _INT, _INT, _VP, _VP, _VP, _I64, _INT, _VP],
+    "kq_qsrt_moe_decode": [_INT, _F32, _F32, _VP, _INT, _I64, _I64, _VP, _VP, _INT, _VP, _INT, _I64, _I64, _INT,
+                           _INT, _VP, _INT, _VP, _I64, _VP, _I64, _VP],
     "kq_qsrt_linear": [_VP, _INT, _I64, _I64, _VP, _I64, _I64, _I64, _INT, _VP, _VP, _VP, _VP, _INT, _VP, _I64,
                        _VP, _I64, _VP],
 }
@@ -141,6 +143,8 @@ def library() -> ctypes.CDLL:
         lib.kq_block_ldl_workspace_size.argtypes = [_I64, _INT, _I64]
         lib.kq_sqg_quantize_workspace_size.restype = ctypes.c_int64
         lib.kq_sqg_quantize_workspace_size.argtypes = [_INT, _INT]
+        lib.kq_qsrt_moe_workspace_size.restype = ctypes.c_int64
+        lib.kq_qsrt_moe_workspace_size.argtypes = [_I64, _INT, _I64, _I64]
         lib.kq_qsrt_linear_workspace_size.restype = ctypes.c_int64
         lib.kq_qsrt_linear_workspace_size.argtypes = [_I64, _I64, _I64]
         lib.kq_route_sort_workspace_size.restype = ctypes.c_int64

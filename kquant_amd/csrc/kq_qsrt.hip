@@ -16,6 +16,7 @@
 // its own rate (kquant/qsrt.py:974-1018), so a 128 x 128 output block is one
 // record: one workgroup decodes its 64 tiles into LDS, transforms both sides
 // there and writes the block.
+#include "kq_act.h"
 #include "kq_dma.h"
 #include "kq_hadamard.h"
 #include "kq_internal.h"
@@ -281,6 +282,71 @@ __device__ __forceinline__ void stage_labels(const uint8_t* labels, int bits, ui
   }
 }
 
+// Wait until this wave's stage loads older than the `younger` most recent
+// ones have landed (stage loads complete in order), then barrier.
+__device__ __forceinline__ void wait_stage(int younger) {
+  static_assert(LIN_STAGES == 4, "the waits below count up to three younger stages");
+  if (younger >= 3) __builtin_amdgcn_s_waitcnt(dma::waitcnt_vm(3));
+  else if (younger == 2) __builtin_amdgcn_s_waitcnt(dma::waitcnt_vm(2));
+  else if (younger == 1) __builtin_amdgcn_s_waitcnt(dma::waitcnt_vm(1));
+  else __builtin_amdgcn_s_waitcnt(dma::waitcnt_vm(0));
+  __syncthreads();
+}
+
+// acc[m] += this lane's part of xs[m][k rows of the block] . W[block, column]
+// for one staged k block: the lane's 4 tiles (k tiles half * 4 + i of the
+// block, n tile ntl), 4 symbols each.  xs points at row 0, k block kbi.
+template <int M>
+__device__ __forceinline__ void accumulate_block(const uint32_t* stage, int bits, const uint8_t* lut,
+                                                 const float* xs, int xs_stride, int half, int ntl, int lane,
+                                                 float (&acc)[M]) {
+  const int r0 = 2 * ((lane >> 1) & 3);
+  const int sb = ((4 * lane + 1) * bits - 16 + 256 * bits) % (256 * bits);
+  const int d0 = sb >> 5, d1 = (d0 + 1) % (8 * bits), off = sb & 31, sh = 64 - (16 + 3 * bits);
+  uint32_t st[16];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t* t = stage + ((half * 4 + i) * 8 + ntl) * 8 * bits;
+    const uint64_t v = (((uint64_t)t[d0] << 32) | t[d1]) << off;
+    const uint32_t win = (uint32_t)(v >> sh);
+    st[4 * i + 0] = (win >> (3 * bits)) & 0xffffu;
+    st[4 * i + 1] = (win >> (2 * bits)) & 0xffffu;
+    st[4 * i + 2] = (win >> bits) & 0xffffu;
+    st[4 * i + 3] = win & 0xffffu;
+  }
+  float w[16];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) w[e] = e4m3_scaled(lut[st[e]]);
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float* xr = xs + m * xs_stride + (half * 4 + i) * 16 + r0;
+      const float2 xa = *reinterpret_cast<const float2*>(xr);
+      const float2 xb = *reinterpret_cast<const float2*>(xr + 8);
+      acc[m] = fmaf(xa.x, w[4 * i + 0], acc[m]);
+      acc[m] = fmaf(xa.y, w[4 * i + 1], acc[m]);
+      acc[m] = fmaf(xb.x, w[4 * i + 2], acc[m]);
+      acc[m] = fmaf(xb.y, w[4 * i + 3], acc[m]);
+    }
+  }
+  // pin the products here: sunk past the caller's next barrier, they would
+  // keep every activation value of the block live across it
+#pragma unroll
+  for (int m = 0; m < M; ++m) asm volatile("" : "+v"(acc[m]));
+}
+
+// Sum the four lanes of a column (lanes differing in bits 1 and 2), then
+// lanes with (lane & 6) == 0 hold column (lane >> 3) + 8 (lane & 1).
+template <int M>
+__device__ __forceinline__ void column_sums(float (&acc)[M]) {
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    acc[m] += __shfl_xor(acc[m], 2);
+    acc[m] += __shfl_xor(acc[m], 4);
+  }
+}
+
 // One k block's 64 tiles as a stage of the LDS ring: every wave issues
 // exactly one 16-byte-per-lane direct load (waves past the block's 2 K
 // kilobytes read nothing, through an empty resource, into a scratch
@@ -353,76 +419,30 @@ __global__ __launch_bounds__(LIN_THREADS) void linear_kernel(LinArgs a, LinRecor
     xs[m][kbi * 128 + lane + 64] = v1;
   }
 
-  const int r0 = 2 * ((lane >> 1) & 3);
   float acc[M];
 #pragma unroll
   for (int m = 0; m < M; ++m) acc[m] = 0.f;
 
   for (int kbi = 0; kbi < kbn; ++kbi) {
     const int bits = record_rate(rec, a.rate_n ? nb : kb0 + kbi);
-    // stage loads complete in order: block kbi has landed once no more than
-    // the younger stages (min(LIN_STAGES - 1, kbn - 1 - kbi)) are in flight;
-    // the barrier makes every wave's visible (and, on the first pass, the
+    // block kbi has landed once only the younger stages are in flight; the
+    // barrier makes every wave's loads visible (and, on the first pass, the
     // activation rows and the labels)
-    static_assert(LIN_STAGES == 4, "the waits below count up to three younger stages");
-    const int younger = min(LIN_STAGES - 1, kbn - 1 - kbi);
-    if (younger >= 3) __builtin_amdgcn_s_waitcnt(dma::waitcnt_vm(3));
-    else if (younger == 2) __builtin_amdgcn_s_waitcnt(dma::waitcnt_vm(2));
-    else if (younger == 1) __builtin_amdgcn_s_waitcnt(dma::waitcnt_vm(1));
-    else __builtin_amdgcn_s_waitcnt(dma::waitcnt_vm(0));
-    __syncthreads();
+    wait_stage(min(LIN_STAGES - 1, kbn - 1 - kbi));
     if (bits != lut_bits) {  // rate along k changed: restage the labels (uniform)
       stage_labels(a.labels, bits, lut, wave, lane);
       __builtin_amdgcn_s_waitcnt(dma::waitcnt_vm(0));
       __syncthreads();
       lut_bits = bits;
     }
-    const uint32_t* stage = ring[kbi % LIN_STAGES];
-    const int sb = ((4 * lane + 1) * bits - 16 + 256 * bits) % (256 * bits);
-    const int d0 = sb >> 5, d1 = (d0 + 1) % (8 * bits), off = sb & 31, sh = 64 - (16 + 3 * bits);
-    uint32_t st[16];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t* t = stage + ((half * 4 + i) * 8 + ntl) * 8 * bits;
-      const uint64_t v = (((uint64_t)t[d0] << 32) | t[d1]) << off;
-      const uint32_t win = (uint32_t)(v >> sh);
-      st[4 * i + 0] = (win >> (3 * bits)) & 0xffffu;
-      st[4 * i + 1] = (win >> (2 * bits)) & 0xffffu;
-      st[4 * i + 2] = (win >> bits) & 0xffffu;
-      st[4 * i + 3] = win & 0xffffu;
-    }
-    float w[16];
-#pragma unroll
-    for (int e = 0; e < 16; ++e) w[e] = e4m3_scaled(lut[st[e]]);
-#pragma unroll
-    for (int m = 0; m < M; ++m) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int kk = kbi * 128 + (half * 4 + i) * 16 + r0;
-        const float2 xa = *reinterpret_cast<const float2*>(&xs[m][kk]);
-        const float2 xb = *reinterpret_cast<const float2*>(&xs[m][kk + 8]);
-        acc[m] = fmaf(xa.x, w[4 * i + 0], acc[m]);
-        acc[m] = fmaf(xa.y, w[4 * i + 1], acc[m]);
-        acc[m] = fmaf(xb.x, w[4 * i + 2], acc[m]);
-        acc[m] = fmaf(xb.y, w[4 * i + 3], acc[m]);
-      }
-    }
-    // pin the products here: sunk past the barrier below, they would keep
-    // every activation value of the block live across it
-#pragma unroll
-    for (int m = 0; m < M; ++m) asm volatile("" : "+v"(acc[m]));
+    accumulate_block<M>(ring[kbi % LIN_STAGES], bits, lut, &xs[0][kbi * 128], lin_max_kb(M) * 128, half, ntl,
+                        lane, acc);
     // every wave is done with this stage: refill it with block kbi + stages
     __syncthreads();
     if (kbi + LIN_STAGES < kbn)
       stage_block(a, rec, nb, kb0 + kbi + LIN_STAGES, ring[kbi % LIN_STAGES], spill, wave, lane);
   }
-
-  // the four lanes of a column (lanes differing in bits 1 and 2) hold its rows
-#pragma unroll
-  for (int m = 0; m < M; ++m) {
-    acc[m] += __shfl_xor(acc[m], 2);
-    acc[m] += __shfl_xor(acc[m], 4);
-  }
+  column_sums<M>(acc);
   if ((lane & 6) == 0) {
     const int c = ntl * 16 + (lane >> 3) + 8 * (lane & 1);
 #pragma unroll
@@ -490,6 +510,214 @@ __global__ __launch_bounds__(LIN_THREADS) void linear_kernel(LinArgs a, LinRecor
 #pragma unroll
     for (int sft = 1; sft < TPO; sft <<= 1) sum += __shfl_xor(sum, sft);
     if (j == 0 && m < mc) store_out(a.out, a.out_dtype, (m0 + m) * a.ldo + col0 + c, sum);
+  }
+  if (tid == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+
+// ------------------------------------------------------ routed experts --
+// The routed expert forward of a decode batch with QSRT-coded experts, as
+// two launches of the fused linear's workgroup (M = 1 row per job):
+//   gate/up  job (pair p, matrix j in {w1, w3}, n block, K chunk):
+//            h[p, j I + n] = x[t] . W_j(e)[:, n]          (fp32)
+//   down     job (pair p, n block of the hidden, K chunk):
+//            out[t, n] += sum_p w_p act(h_gate, h_up)[p] . W2(e)[:, n]
+// with t = p / topk, e = route_ids[p] (ids outside [0, experts) contribute
+// nothing) and act = SiTU / SwiGLU in fp32.  This is the expert MLP of
+// scripts/closure_exl3_layer.py:557-598 on weights that
+// scripts/stream_k3_pytorch.py:771-775 would decode to dense bf16 first;
+// here nothing is decoded to memory and the intermediate stays fp32.  The
+// route weight scales the down projection's activation row (linear), and
+// the last workgroup of a (token, hidden block) sums every pair's and
+// chunk's partial in a fixed order, so the result is deterministic.
+struct MoeArgs {
+  const void* x;
+  int64_t ldx;
+  const int* route_ids;
+  const float* route_w;
+  const kq_qsrt_matrix* mats;  // [experts][3]: w1, w3, w2
+  const uint8_t* labels;
+  float* h;         // [pairs][2 I]
+  float* partial;   // gate/up: [pairs][2][chunks][I]; down: [pairs][chunks][H]
+  int* counters;    // gate/up: [pairs][2][I / 128]; down: [tokens][H / 128]
+  void* out;
+  int64_t ldo, pairs;
+  int topk, experts, hidden_tiles, inter_tiles, rate13_n, rate2_n, kbw, chunks, x_dtype, out_dtype;
+  ActParams act;
+};
+
+// Stage k block kb of a matrix whose record prefix sums sit in device
+// memory (prefix[r] = sum of the rates of records before r).
+// A wave-uniform pointer held in scalar registers.
+template <typename T>
+__device__ __forceinline__ T* uniform_ptr(T* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32));
+  return reinterpret_cast<T*>(((uint64_t)hi << 32) | lo);
+}
+
+__device__ __forceinline__ int prefix_stage(const kq_qsrt_matrix& mt, int k_tiles, int n_tiles, int rate_n, int nb,
+                                            int kb, uint32_t* stage, uint32_t* spill, int wave, int lane) {
+  const int record = __builtin_amdgcn_readfirstlane(rate_n ? nb : kb);
+  const uint32_t p0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)mt.record_prefix[record]);
+  const int bits = __builtin_amdgcn_readfirstlane((int)(mt.record_prefix[record + 1] - p0));
+  const int64_t record_dw = (int64_t)RECORD_TILES * (rate_n ? k_tiles : n_tiles) * 8;
+  const int tile_bytes = 32 * bits;
+  const bool live = wave < 2 * bits;
+  const int64_t first_tile = rate_n ? (int64_t)kb * 64 : (int64_t)nb * 8;
+  const uint8_t* base = uniform_ptr(reinterpret_cast<const uint8_t*>(mt.payload) +
+                                    ((int64_t)p0 * record_dw * 4 + first_tile * tile_bytes));
+  const int byte = wave * 1024 + lane * 16;
+  const int u = byte / tile_bytes, within = byte - u * tile_bytes;
+  const int64_t rel = rate_n ? (int64_t)u : (int64_t)(u >> 3) * n_tiles + (u & 7);
+  const dma::i32x4_t rs = dma::make_rsrc(base, live ? (uint32_t)dma::MAX_RANGE : 0u);
+  const uint32_t lds = (uint32_t)__builtin_amdgcn_readfirstlane(
+      (int)(live ? dma::lds_offset_of(stage) + (uint32_t)wave * 1024u : dma::lds_offset_of(spill)));
+  dma::load_to_lds16(rs, live ? (uint32_t)(rel * tile_bytes + within) : 0u, lds);
+  return bits;
+}
+
+__device__ __forceinline__ int prefix_rate(const kq_qsrt_matrix& mt, int record) {
+  record = __builtin_amdgcn_readfirstlane(record);
+  return __builtin_amdgcn_readfirstlane((int)(mt.record_prefix[record + 1] - mt.record_prefix[record]));
+}
+
+template <bool DOWN>
+__global__ __launch_bounds__(LIN_THREADS) void moe_kernel(MoeArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t lut[65536];
+  __shared__ __attribute__((aligned(16))) uint32_t ring[LIN_STAGES][2048];
+  __shared__ __attribute__((aligned(16))) uint32_t spill[256];
+  __shared__ __attribute__((aligned(16))) float xs[lin_max_kb(1) * 128];
+  __shared__ float yb[2][128];
+  __shared__ int s_last;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int half = wave >> 3, ntl = wave & 7;
+  const int H = a.hidden_tiles * TILE, I = a.inter_tiles * TILE;
+  const int k_tiles = DOWN ? a.inter_tiles : a.hidden_tiles, n_tiles = DOWN ? a.hidden_tiles : a.inter_tiles;
+  const int rate_n = DOWN ? a.rate2_n : a.rate13_n;
+  const int n_blocks = n_tiles >> 3, k_blocks = k_tiles >> 3, N = n_tiles * TILE;
+  int job = (int)blockIdx.x;
+  const int chunk = job % a.chunks;
+  job /= a.chunks;
+  const int nb = job % n_blocks;
+  job /= n_blocks;
+  const int j = DOWN ? 2 : job % 2;
+  const int64_t p = DOWN ? job : job / 2;
+  const int64_t t = p / a.topk;
+  const int kb0 = chunk * a.kbw;
+  const int kbn = min(a.kbw, k_blocks - kb0);
+  const int e = __builtin_amdgcn_readfirstlane(a.route_ids[p]);
+  const bool valid = e >= 0 && e < a.experts;
+  kq_qsrt_matrix mt{};
+  if (valid) mt = a.mats[(int64_t)e * 3 + j];
+  const uint8_t* labels = a.labels + (DOWN ? 3 * 65536 : 0);  // the down projection's rate axis has its own
+
+  float acc[1] = {0.f};
+  if (valid) {
+    int lut_bits = prefix_rate(mt, rate_n ? nb : kb0);
+    stage_labels(labels, lut_bits, lut, wave, lane);
+#pragma unroll
+    for (int s = 0; s < LIN_STAGES; ++s)
+      if (s < kbn) prefix_stage(mt, k_tiles, n_tiles, rate_n, nb, kb0 + s, ring[s], spill, wave, lane);
+    // the activation row of this chunk, rotated: one wave per k block
+    for (int kbi = wave; kbi < kbn; kbi += 16) {
+      const int64_t k = (int64_t)(kb0 + kbi) * 128 + lane;
+      float v0, v1;
+      if constexpr (DOWN) {
+        const float* hp = a.h + p * 2 * I;
+        const float wgt = a.route_w[p];
+        v0 = activate(a.act, hp[k], hp[I + k]) * wgt;
+        v1 = activate(a.act, hp[k + 64], hp[I + k + 64]) * wgt;
+      } else {
+        v0 = load_x(a.x, a.x_dtype, t * a.ldx + k);
+        v1 = load_x(a.x, a.x_dtype, t * a.ldx + k + 64);
+      }
+      v0 *= mt.suh[k];
+      v1 *= mt.suh[k + 64];
+      fwht128(v0, v1, lane);
+      xs[kbi * 128 + lane] = v0;
+      xs[kbi * 128 + lane + 64] = v1;
+    }
+    for (int kbi = 0; kbi < kbn; ++kbi) {
+      const int bits = prefix_rate(mt, rate_n ? nb : kb0 + kbi);
+      wait_stage(min(LIN_STAGES - 1, kbn - 1 - kbi));
+      if (bits != lut_bits) {
+        stage_labels(labels, bits, lut, wave, lane);
+        __builtin_amdgcn_s_waitcnt(dma::waitcnt_vm(0));
+        __syncthreads();
+        lut_bits = bits;
+      }
+      accumulate_block<1>(ring[kbi % LIN_STAGES], bits, lut, &xs[kbi * 128], 0, half, ntl, lane, acc);
+      __syncthreads();
+      if (kbi + LIN_STAGES < kbn)
+        prefix_stage(mt, k_tiles, n_tiles, rate_n, nb, kb0 + kbi + LIN_STAGES, ring[kbi % LIN_STAGES], spill, wave,
+                     lane);
+    }
+    column_sums<1>(acc);
+  }
+  if ((lane & 6) == 0) yb[half][ntl * 16 + (lane >> 3) + 8 * (lane & 1)] = acc[0];
+  __syncthreads();
+
+  const int64_t col0 = (int64_t)nb * 128;
+  float v0 = 0.f, v1 = 0.f;
+  if (wave == 0 && valid) {
+    v0 = yb[0][lane] + yb[1][lane];
+    v1 = yb[0][lane + 64] + yb[1][lane + 64];
+    fwht128(v0, v1, lane);
+    v0 *= (1.f / 128.f) * mt.svh[col0 + lane];
+    v1 *= (1.f / 128.f) * mt.svh[col0 + lane + 64];
+  }
+  if (!DOWN && a.chunks == 1) {
+    if (wave == 0) {
+      float* hp = a.h + p * 2 * I + j * I + col0;
+      hp[lane] = v0;
+      hp[lane + 64] = v1;
+    }
+    return;
+  }
+  // partials through agent-scope atomics (written through / read past the
+  // per-XCD L2s); the last workgroup of the output block sums them in order
+  int64_t slot;    // this workgroup's partial row
+  int64_t first;   // the output block's first partial row
+  int count;       // partial rows of the output block
+  int* counter;
+  if constexpr (DOWN) {
+    slot = p * a.chunks + chunk;
+    first = t * a.topk * a.chunks;
+    count = a.topk * a.chunks;
+    counter = a.counters + t * n_blocks + nb;
+  } else {
+    slot = (p * 2 + j) * a.chunks + chunk;
+    first = (p * 2 + j) * a.chunks;
+    count = a.chunks;
+    counter = a.counters + (p * 2 + j) * n_blocks + nb;
+  }
+  if (wave == 0) {
+    float* q = a.partial + slot * N + col0;
+    __hip_atomic_store(q + lane, v0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(q + lane + 64, v1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __builtin_amdgcn_s_waitcnt(dma::waitcnt_vm(0));
+  __syncthreads();
+  if (tid == 0) s_last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == count - 1;
+  __syncthreads();
+  if (!s_last) return;
+  // 8 threads per output column, thread r summing partial rows r, r + 8, ...
+  {
+    const int c = tid >> 3, r = tid & 7;
+    const float* q = a.partial + first * N + col0 + c;
+    float sum = 0.f;
+    for (int i = r; i < count; i += 8)
+      sum += __hip_atomic_load(q + (int64_t)i * N, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    sum += __shfl_xor(sum, 1);
+    sum += __shfl_xor(sum, 2);
+    sum += __shfl_xor(sum, 4);
+    if (r == 0) {
+      if constexpr (DOWN) store_out(a.out, a.out_dtype, t * a.ldo + col0 + c, sum);
+      else a.h[p * 2 * I + j * I + col0 + c] = sum;
+    }
   }
   if (tid == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -735,5 +963,132 @@ extern "C" int kq_qsrt_linear(const void* x, int x_dtype, int64_t m, int64_t ldx
     case 8: launch_linear_m<8>(a, rec, rot, grid, st); break;
     default: launch_linear_m<16>(a, rec, rot, grid, st); break;
   }
+  return kq_check_launch(hipGetLastError(), fn);
+}
+
+// --------------------------------------------------------- routed experts --
+namespace {
+
+struct MoePlan {
+  int kbw13, chunks13, kbw2, chunks2;
+  int64_t h_bytes, part13_bytes, part2_bytes, cnt13_bytes, cnt2_bytes;
+};
+
+int64_t align256(int64_t v) { return (v + 255) / 256 * 256; }
+
+// Same cost model as the single linear: rounds of workgroups times k blocks
+// per workgroup, plus the cross-workgroup sum where it is optional.
+void moe_chunking(int64_t jobs, int64_t k_blocks, int64_t slots, bool sum_anyway, int* kbw_out, int* chunks_out) {
+  int64_t best = -1;
+  const int64_t max_kb = k_blocks < lin_max_kb(1) ? k_blocks : lin_max_kb(1);
+  for (int kbw = 1; kbw <= max_kb; ++kbw) {
+    const int64_t chunks = (k_blocks + kbw - 1) / kbw;
+    const int64_t rounds = (jobs * chunks + slots - 1) / slots;
+    const int64_t cost = rounds * kbw + (!sum_anyway && chunks > 1 ? LIN_REDUCE_KB : 0);
+    if (best < 0 || cost <= best) {
+      best = cost;
+      *kbw_out = kbw;
+      *chunks_out = (int)chunks;
+    }
+  }
+}
+
+hipError_t moe_plan(int64_t tokens, int topk, int64_t hidden_tiles, int64_t inter_tiles, MoePlan* p) {
+  int dev = 0, cus = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e != hipSuccess) return e;
+  const int64_t slots = cus > 0 ? cus : 1;
+  const int64_t pairs = tokens * topk, H = hidden_tiles * TILE, I = inter_tiles * TILE;
+  moe_chunking(pairs * 2 * (inter_tiles / RECORD_TILES), hidden_tiles / RECORD_TILES, slots, false, &p->kbw13,
+               &p->chunks13);
+  moe_chunking(pairs * (hidden_tiles / RECORD_TILES), inter_tiles / RECORD_TILES, slots, true, &p->kbw2,
+               &p->chunks2);
+  p->h_bytes = align256(pairs * 2 * I * 4);
+  p->part13_bytes = p->chunks13 > 1 ? align256(pairs * 2 * p->chunks13 * I * 4) : 0;
+  p->part2_bytes = align256(pairs * p->chunks2 * H * 4);
+  p->cnt13_bytes = p->chunks13 > 1 ? align256(pairs * 2 * (inter_tiles / RECORD_TILES) * 4) : 0;
+  p->cnt2_bytes = align256(tokens * (hidden_tiles / RECORD_TILES) * 4);
+  return hipSuccess;
+}
+
+}  // namespace
+
+extern "C" int64_t kq_qsrt_moe_workspace_size(int64_t tokens, int topk, int64_t hidden_tiles, int64_t inter_tiles) {
+  if (tokens <= 0 || topk <= 0 || hidden_tiles <= 0 || inter_tiles <= 0 || hidden_tiles % RECORD_TILES ||
+      inter_tiles % RECORD_TILES)
+    return 0;
+  MoePlan p;
+  if (moe_plan(tokens, topk, hidden_tiles, inter_tiles, &p) != hipSuccess) return -1;
+  return p.h_bytes + p.part13_bytes + p.part2_bytes + p.cnt13_bytes + p.cnt2_bytes;
+}
+
+extern "C" int kq_qsrt_moe_decode(int act, float beta, float linear_beta, const void* x, int x_dtype, int64_t tokens,
+                                  int64_t ldx, const int32_t* route_ids, const float* route_weights, int topk,
+                                  const kq_qsrt_matrix* mats, int experts, int64_t hidden_tiles, int64_t inter_tiles,
+                                  int rate13_axis, int rate2_axis, const uint8_t* labels, int out_dtype, void* out,
+                                  int64_t ldo, void* workspace, int64_t ws_bytes, void* stream) {
+  const char* fn = "kq_qsrt_moe_decode";
+  if (act != KQ_ACT_SITU && act != KQ_ACT_SWIGLU) return kq_fail(KQ_ERR_INVALID, "%s: unknown activation", fn);
+  if (tokens < 0 || topk <= 0 || experts <= 0) return kq_fail(KQ_ERR_INVALID, "%s: bad tokens, topk or experts", fn);
+  if (hidden_tiles <= 0 || inter_tiles <= 0 || hidden_tiles % RECORD_TILES || inter_tiles % RECORD_TILES)
+    return kq_fail(KQ_ERR_INVALID, "%s: hidden and intermediate sizes must be positive multiples of 128", fn);
+  if ((rate13_axis != 0 && rate13_axis != 1) || (rate2_axis != 0 && rate2_axis != 1))
+    return kq_fail(KQ_ERR_INVALID, "%s: rate axes must be 0 (k) or 1 (n)", fn);
+  if (x_dtype < KQ_DT_BF16 || x_dtype > KQ_DT_F32 || out_dtype < KQ_DT_BF16 || out_dtype > KQ_DT_F32)
+    return kq_fail(KQ_ERR_INVALID, "%s: bad activation or output dtype", fn);
+  if (act == KQ_ACT_SITU && !(beta > 0.f && linear_beta > 0.f))
+    return kq_fail(KQ_ERR_INVALID, "%s: SiTU betas must be positive", fn);
+  const int64_t H = hidden_tiles * TILE;
+  if (ldx < H || ldo < H) return kq_fail(KQ_ERR_INVALID, "%s: ldx or ldo too small", fn);
+  if (tokens == 0) return KQ_OK;
+  if (!x || !route_ids || !route_weights || !mats || !labels || !out)
+    return kq_fail(KQ_ERR_INVALID, "%s: null buffer", fn);
+  MoePlan p;
+  hipError_t err = moe_plan(tokens, topk, hidden_tiles, inter_tiles, &p);
+  if (err != hipSuccess) return kq_check_launch(err, fn);
+  const int64_t need = p.h_bytes + p.part13_bytes + p.part2_bytes + p.cnt13_bytes + p.cnt2_bytes;
+  if (!workspace || ws_bytes < need || kq_misaligned(workspace, 256))
+    return kq_fail(KQ_ERR_INVALID, "%s: workspace needs %lld bytes (256-byte aligned, zeroed before first use)", fn,
+                   (long long)need);
+  const int64_t pairs = tokens * topk;
+  const int64_t jobs13 = pairs * 2 * (inter_tiles / RECORD_TILES) * p.chunks13;
+  const int64_t jobs2 = pairs * (hidden_tiles / RECORD_TILES) * p.chunks2;
+  if (jobs13 > 0x7fffffff || jobs2 > 0x7fffffff) return kq_fail(KQ_ERR_LIMIT, "%s: too many workgroups", fn);
+  char* ws = static_cast<char*>(workspace);
+  MoeArgs a{};
+  a.x = x;
+  a.ldx = ldx;
+  a.route_ids = route_ids;
+  a.route_w = route_weights;
+  a.mats = mats;
+  a.labels = labels;
+  a.h = reinterpret_cast<float*>(ws);
+  a.out = out;
+  a.ldo = ldo;
+  a.pairs = pairs;
+  a.topk = topk;
+  a.experts = experts;
+  a.hidden_tiles = (int)hidden_tiles;
+  a.inter_tiles = (int)inter_tiles;
+  a.rate13_n = rate13_axis;
+  a.rate2_n = rate2_axis;
+  a.x_dtype = x_dtype;
+  a.out_dtype = out_dtype;
+  a.act = kq::ActParams{act, beta, linear_beta};
+  const hipStream_t st = (hipStream_t)stream;
+  MoeArgs g = a;
+  g.kbw = p.kbw13;
+  g.chunks = p.chunks13;
+  g.partial = reinterpret_cast<float*>(ws + p.h_bytes);
+  g.counters = reinterpret_cast<int*>(ws + p.h_bytes + p.part13_bytes + p.part2_bytes);
+  moe_kernel<false><<<(unsigned)jobs13, LIN_THREADS, 0, st>>>(g);
+  if ((err = hipGetLastError()) != hipSuccess) return kq_check_launch(err, fn);
+  MoeArgs d = a;
+  d.kbw = p.kbw2;
+  d.chunks = p.chunks2;
+  d.partial = reinterpret_cast<float*>(ws + p.h_bytes + p.part13_bytes);
+  d.counters = reinterpret_cast<int*>(ws + p.h_bytes + p.part13_bytes + p.part2_bytes + p.cnt13_bytes);
+  moe_kernel<true><<<(unsigned)jobs2, LIN_THREADS, 0, st>>>(d);
   return kq_check_launch(hipGetLastError(), fn);
 }

@@ -84,7 +84,7 @@ def unpack_trellis_states(packed: torch.Tensor, bits: int) -> torch.Tensor:
 
 
 _LABELS: dict[tuple[str, str | None, torch.device], torch.Tensor] = {}
-_LINEAR_WORKSPACES: dict[torch.device, torch.Tensor] = {}
+_LINEAR_WORKSPACES: dict[tuple, torch.Tensor] = {}
 
 
 def rate_labels(codebook: str = SQG_XOR_CHEB_T12, *, rate_axis: str | None = None,
@@ -270,12 +270,133 @@ def qsrt_linear(
     need = int(N.library().kq_qsrt_linear_workspace_size(max(m, 1), k_tiles, n_tiles)) if m else 0
     if need < 0:
         raise RuntimeError("kq_qsrt_linear_workspace_size: no HIP device")
-    ws = _LINEAR_WORKSPACES.get(gpu)
-    if need and (ws is None or ws.numel() < need):
-        ws = torch.zeros(need, dtype=torch.uint8, device=gpu)  # counters start (and stay) at zero
-        _LINEAR_WORKSPACES[gpu] = ws
+    # one zeroed workspace per geometry: its counters return to zero after
+    # every call, but their place depends on the sizes
+    ws = None
+    if need:
+        key = (gpu, m, k_tiles, n_tiles)
+        ws = _LINEAR_WORKSPACES.get(key)
+        if ws is None:
+            ws = torch.zeros(need, dtype=torch.uint8, device=gpu)
+            _LINEAR_WORKSPACES[key] = ws
     N.call("kq_qsrt_linear", N.ptr(rows), N.DTYPE_CODES[rows.dtype], m, rows.stride(0) if m else k, N.ptr(g),
            g.numel(), k_tiles, n_tiles, 0 if rate_axis == "k" else 1, bits, N.ptr(labels), N.ptr(su), N.ptr(sv),
            N.DTYPE_CODES[out_dtype], N.ptr(out), n, N.ptr(ws) if need else None, need, N.stream(gpu))
     out = out.reshape(*x.shape[:-1], n)
+    return out if host is None else out.to(host)
+
+
+class QSRTExperts:
+    """QSRT-coded routed experts on one GPU, as ``kq_qsrt_moe_decode`` reads
+    them: per expert a w1, w3 (EXL [H, I], records along ``rate13_axis``,
+    the reference's MATRIX_RATE_AXIS, kquant/qsrt.py:83-87) and w2 ([I, H],
+    records along ``rate2_axis``), each given as ``(payload, record_bits,
+    suh, svh)`` with the payload of ``pack_qsrt_trellis`` (int16 words).
+    Every payload's length is checked against its record rates here, since
+    the kernel reads the descriptors from device memory."""
+
+    KINDS = ("w1", "w3", "w2")
+
+    def __init__(self, w1, w3, w2, *, hidden: int, inter: int, rate13_axis: str = "n", rate2_axis: str = "k",
+                 codebook: str = SQG_XOR_CHEB_T12, device: torch.device | str | None = None):
+        if hidden % RECORD_CHANNELS or inter % RECORD_CHANNELS or hidden <= 0 or inter <= 0:
+            raise ValueError("hidden and intermediate sizes must be positive multiples of 128")
+        if rate13_axis not in ("k", "n") or rate2_axis not in ("k", "n"):
+            raise ValueError("rate axes must be 'k' or 'n'")
+        if not (len(w1) == len(w3) == len(w2)) or not w1:
+            raise ValueError("w1, w3 and w2 must list the same, non-zero number of experts")
+        gpu = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+        if gpu.index is None:
+            gpu = torch.device(gpu.type, torch.cuda.current_device())
+        self.device, self.hidden, self.inter = gpu, hidden, inter
+        self.rate13_axis, self.rate2_axis, self.codebook = rate13_axis, rate2_axis, codebook
+        self.experts = len(w1)
+        self._keep = []
+        rows = []
+        for e in range(self.experts):
+            row = []
+            for kind, spec in zip(self.KINDS, (w1[e], w3[e], w2[e])):
+                k, n = (hidden, inter) if kind != "w2" else (inter, hidden)
+                axis = rate13_axis if kind != "w2" else rate2_axis
+                payload, record_bits, suh, svh = spec
+                bits = _check_record_bits(record_bits)
+                records = (k if axis == "k" else n) // RECORD_CHANNELS
+                if len(bits) != records:
+                    raise ValueError(f"expert {e} {kind}: {len(bits)} record rates for {records} records")
+                per_record = 8 * ((n if axis == "k" else k) // TILE_CHANNELS)  # tiles per record
+                words = sum(per_record * TILE_CHANNELS * b for b in bits)
+                if payload.dtype != torch.int16 or payload.ndim != 1 or payload.numel() != words:
+                    raise ValueError(f"expert {e} {kind}: payload must be {words} int16 words")
+                if suh.numel() != k or svh.numel() != n:
+                    raise ValueError(f"expert {e} {kind}: suh / svh must have {k} / {n} values")
+                p = N.aligned(payload.to(gpu), 4)
+                prefix = torch.tensor([0, *torch.tensor(list(bits)).cumsum(0).tolist()], dtype=torch.int32,
+                                      device=gpu)
+                su = N.aligned(suh.to(device=gpu, dtype=torch.float32).reshape(-1), 4)
+                sv = N.aligned(svh.to(device=gpu, dtype=torch.float32).reshape(-1), 4)
+                self._keep += [p, prefix, su, sv]
+                row.append([p.data_ptr(), prefix.data_ptr(), su.data_ptr(), sv.data_ptr()])
+            rows.append(row)
+        self.descriptors = torch.tensor(rows, dtype=torch.int64, device=gpu).contiguous()  # [E, 3, 4]
+        # K2..K4 labels for w1 / w3, then for w2 (a codebook may depend on the rate axis)
+        self.labels = torch.cat([rate_labels(codebook, rate_axis=rate13_axis, device=gpu),
+                                 rate_labels(codebook, rate_axis=rate2_axis, device=gpu)]).contiguous()
+
+
+_MOE_WORKSPACES: dict[tuple, torch.Tensor] = {}
+
+
+def qsrt_expert_forward(
+    x: torch.Tensor,
+    route_ids: torch.Tensor,
+    route_weights: torch.Tensor,
+    experts: QSRTExperts,
+    *,
+    activation: str = "situ",
+    beta: float = 4.0,
+    linear_beta: float = 25.0,
+    out_dtype: torch.dtype | None = None,
+) -> torch.Tensor:
+    """Routed expert forward of a decode batch on QSRT experts
+    (``kq_qsrt_moe_decode``): out[t] = sum_s w[t, s] act(x_t W1_e, x_t W3_e)
+    W2_e for e = route_ids[t, s] in [0, experts), computed from the trellis
+    words in fp32 - the expert MLP of scripts/closure_exl3_layer.py:557-598
+    without the dense bf16 weights scripts/stream_k3_pytorch.py:771-775
+    decodes first.  x [tokens, H]; route_ids / route_weights [tokens, topk]."""
+
+    if activation not in ("situ", "swiglu"):
+        raise ValueError("activation must be 'situ' or 'swiglu'")
+    if x.ndim != 2 or x.shape[1] != experts.hidden:
+        raise ValueError(f"x must be [tokens, {experts.hidden}]")
+    if route_ids.shape != route_weights.shape or route_ids.ndim != 2 or route_ids.shape[0] != x.shape[0]:
+        raise ValueError("route_ids and route_weights must be [tokens, topk]")
+    if x.dtype not in N.DTYPE_CODES:
+        raise TypeError("x must be bfloat16, float16 or float32")
+    gpu = experts.device
+    out_dtype = x.dtype if out_dtype is None else out_dtype
+    host = None if x.is_cuda else x.device
+    xg = x.to(gpu)
+    xg = xg if xg.stride(1) == 1 else xg.contiguous()
+    ids = N.aligned(route_ids.to(device=gpu, dtype=torch.int32), 4)
+    wts = N.aligned(route_weights.to(device=gpu, dtype=torch.float32), 4)
+    tokens, topk = ids.shape
+    out = torch.empty(tokens, experts.hidden, dtype=out_dtype, device=gpu)
+    if tokens:
+        h_tiles, i_tiles = experts.hidden // TILE_CHANNELS, experts.inter // TILE_CHANNELS
+        need = int(N.library().kq_qsrt_moe_workspace_size(tokens, topk, h_tiles, i_tiles))
+        if need < 0:
+            raise RuntimeError("kq_qsrt_moe_workspace_size: no HIP device")
+        # one zeroed workspace per geometry: its counters return to zero after
+        # every call, but their place depends on the sizes
+        key = (gpu, tokens, topk, h_tiles, i_tiles)
+        ws = _MOE_WORKSPACES.get(key)
+        if ws is None:
+            ws = torch.zeros(max(need, 1), dtype=torch.uint8, device=gpu)
+            _MOE_WORKSPACES[key] = ws
+        act = N.ACT_SITU if activation == "situ" else N.ACT_SWIGLU
+        N.call("kq_qsrt_moe_decode", act, float(beta), float(linear_beta), N.ptr(xg), N.DTYPE_CODES[xg.dtype],
+               tokens, xg.stride(0), N.ptr(ids), N.ptr(wts), topk, N.ptr(experts.descriptors), experts.experts,
+               h_tiles, i_tiles, 0 if experts.rate13_axis == "k" else 1, 0 if experts.rate2_axis == "k" else 1,
+               N.ptr(experts.labels), N.DTYPE_CODES[out_dtype], N.ptr(out), experts.hidden, N.ptr(ws), need,
+               N.stream(gpu))
     return out if host is None else out.to(host)

@@ -145,3 +145,39 @@ def qsrt_linear(x, payload, k_tiles, n_tiles, record_bits, rate_axis, labels_by_
     path: decode, then the linear; scripts/stream_k3_pytorch.py:771-775)."""
     weight = decode_qsrt_weight(payload, k_tiles, n_tiles, record_bits, rate_axis, labels_by_bits, suh, svh)
     return np.asarray(x, dtype=np.float64) @ np.asarray(weight, dtype=np.float64)
+
+
+def situ64(gate, up, beta: float = 4.0, linear_beta: float = 25.0):
+    """kquant/tp_simulator.py:83-94 in f64: beta tanh(g / beta) sigmoid(g) *
+    linear_beta tanh(u / linear_beta)."""
+    g = np.asarray(gate, dtype=np.float64)
+    u = np.asarray(up, dtype=np.float64)
+    return beta * np.tanh(g / beta) / (1.0 + np.exp(-g)) * (linear_beta * np.tanh(u / linear_beta))
+
+
+def qsrt_expert_forward(x, route_ids, route_weights, experts, hidden, inter, labels13, labels2,
+                        rate13_axis="n", rate2_axis="k", activation="situ"):
+    """The routed expert MLP (scripts/closure_exl3_layer.py:557-598 with
+    situ) on QSRT experts decoded in f64: experts[e] = (w1, w3, w2), each
+    (payload, record_bits, suh, svh); W1, W3 [H, I], W2 [I, H] in the EXL
+    orientation; ids outside [0, E) contribute nothing."""
+    x = np.asarray(x, dtype=np.float64)
+    out = np.zeros((x.shape[0], hidden))
+    ht, it = hidden // TILE, inter // TILE
+    cache = {}
+
+    def weight(e, j):
+        if (e, j) not in cache:
+            payload, bits, suh, svh = experts[e][j]
+            kt, nt, axis, labels = (ht, it, rate13_axis, labels13) if j < 2 else (it, ht, rate2_axis, labels2)
+            cache[e, j] = decode_qsrt_weight(payload, kt, nt, bits, axis, labels, suh, svh)
+        return cache[e, j]
+
+    for t in range(x.shape[0]):
+        for e, w in zip(np.asarray(route_ids[t]).tolist(), np.asarray(route_weights[t], dtype=np.float64).tolist()):
+            if not 0 <= e < len(experts):
+                continue
+            g, u = x[t] @ weight(e, 0), x[t] @ weight(e, 1)
+            a = situ64(g, u) if activation == "situ" else g / (1.0 + np.exp(-g)) * u
+            out[t] += w * (a @ weight(e, 2))
+    return out

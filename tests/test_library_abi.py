@@ -35,6 +35,7 @@ def test_python_binding_covers_every_entry_point():
                                         "kq_moe_x4t_workspace_size", "kq_mx_linear_f32_workspace_size",
                                         "kq_cholesky_workspace_size", "kq_block_ldl_workspace_size",
                                         "kq_sqg_quantize_workspace_size", "kq_qsrt_linear_workspace_size",
+                                        "kq_qsrt_moe_workspace_size",
                                         "kq_route_sort_workspace_size"}
     assert set(declared_symbols()) <= bound
 
@@ -114,3 +115,26 @@ def test_qsrt_linear_argument_errors_need_no_gpu():
     narrow = list(args)
     narrow[3] = 100
     assert lib.kq_qsrt_linear(*narrow) == _native.KQ_ERR_INVALID and b"ldx" in lib.kq_last_error()
+
+
+def test_qsrt_moe_argument_errors_need_no_gpu():
+    lib = _native.library()
+    fake = ctypes.c_void_p(256)  # never dereferenced: validation fails first
+    assert lib.kq_qsrt_moe_workspace_size(1, 16, 224, 12) == 0  # I not a multiple of 128
+    args = [_native.ACT_SITU, 4.0, 25.0, fake, _native.DT_BF16, 1, 3584, fake, fake, 16, fake, 896, 224, 16, 1, 0,
+            fake, _native.DT_BF16, fake, 3584, fake, 1 << 20, None]
+    bad = list(args)
+    bad[0] = 7
+    assert lib.kq_qsrt_moe_decode(*bad) == _native.KQ_ERR_INVALID and b"activation" in lib.kq_last_error()
+    bad = list(args)
+    bad[13] = 12
+    assert lib.kq_qsrt_moe_decode(*bad) == _native.KQ_ERR_INVALID and b"multiples of 128" in lib.kq_last_error()
+    bad = list(args)
+    bad[15] = 2
+    assert lib.kq_qsrt_moe_decode(*bad) == _native.KQ_ERR_INVALID and b"rate axes" in lib.kq_last_error()
+    bad = list(args)
+    bad[1] = 0.0
+    assert lib.kq_qsrt_moe_decode(*bad) == _native.KQ_ERR_INVALID and b"betas" in lib.kq_last_error()
+    bad = list(args)
+    bad[19] = 100
+    assert lib.kq_qsrt_moe_decode(*bad) == _native.KQ_ERR_INVALID and b"ldo" in lib.kq_last_error()
