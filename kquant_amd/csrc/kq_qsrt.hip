@@ -282,23 +282,52 @@ __device__ __forceinline__ void stage_labels(const uint8_t* labels, int bits, ui
   }
 }
 
+// A wave-uniform pointer held in scalar registers.
+template <typename T>
+__device__ __forceinline__ T* uniform_ptr(T* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32));
+  return reinterpret_cast<T*>(((uint64_t)hi << 32) | lo);
+}
+
 // Wait until this wave's stage loads older than the `younger` most recent
-// ones have landed (stage loads complete in order), then barrier.
-__device__ __forceinline__ void wait_stage(int younger) {
-  static_assert(LIN_STAGES == 4, "the waits below count up to three younger stages");
-  if (younger >= 3) __builtin_amdgcn_s_waitcnt(dma::waitcnt_vm(3));
+// ones have landed (its direct loads complete in order).
+__device__ __forceinline__ void wait_own_stage(int younger) {
+  static_assert(LIN_STAGES == 4, "the waits below count up to four younger loads");
+  if (younger >= 4) __builtin_amdgcn_s_waitcnt(dma::waitcnt_vm(4));
+  else if (younger == 3) __builtin_amdgcn_s_waitcnt(dma::waitcnt_vm(3));
   else if (younger == 2) __builtin_amdgcn_s_waitcnt(dma::waitcnt_vm(2));
   else if (younger == 1) __builtin_amdgcn_s_waitcnt(dma::waitcnt_vm(1));
   else __builtin_amdgcn_s_waitcnt(dma::waitcnt_vm(0));
-  __syncthreads();
+}
+
+// This wave's 4 tiles of k block kb - k tiles kb * 8 + half * 4 + i, n tile
+// nb * 8 + ntl - into its own 512-byte slot of a ring stage (tile i at byte
+// 32 K i): 2 K lanes of 16 bytes per tile, one direct load per wave, so a
+// wave waits for its own loads only and the ring needs no barrier.  rec0:
+// dword offset of the block's record in the payload.
+__device__ __forceinline__ void stage_wave(const uint32_t* payload, int64_t rec0, int bits, int rate_n,
+                                           int n_tiles, int nb, int kb, uint32_t* stage, int wave, int lane) {
+  const int half = wave >> 3, ntl = wave & 7;
+  const int tile_bytes = 32 * bits;
+  const int64_t first = rate_n ? (int64_t)kb * 64 + half * 32 + ntl : (int64_t)half * 4 * n_tiles + nb * 8 + ntl;
+  const int64_t step = rate_n ? RECORD_TILES : n_tiles;  // tiles from one k tile of the block to the next
+  const uint8_t* base = uniform_ptr(reinterpret_cast<const uint8_t*>(payload) + rec0 * 4 + first * tile_bytes);
+  const dma::i32x4_t rs = dma::make_rsrc(base, (uint32_t)dma::MAX_RANGE);
+  const uint32_t lds =
+      (uint32_t)__builtin_amdgcn_readfirstlane((int)(dma::lds_offset_of(stage) + (uint32_t)wave * 512u));
+  const int i = lane / (2 * bits), within = (lane - i * 2 * bits) * 16;
+  if (lane < 8 * bits) dma::load_to_lds16(rs, (uint32_t)(i * step * tile_bytes + within), lds);
 }
 
 // acc[m] += this lane's part of xs[m][k rows of the block] . W[block, column]
-// for one staged k block: the lane's 4 tiles (k tiles half * 4 + i of the
-// block, n tile ntl), 4 symbols each.  xs points at row 0, k block kbi.
+// for one staged k block: the wave's 4 tiles in its slot (k tiles
+// half * 4 + i of the block), 4 symbols each.  xs points at row 0, k block
+// kbi.
 template <int M>
-__device__ __forceinline__ void accumulate_block(const uint32_t* stage, int bits, const uint8_t* lut,
-                                                 const float* xs, int xs_stride, int half, int ntl, int lane,
+__device__ __forceinline__ void accumulate_block(const uint32_t* slot, int bits, const uint8_t* lut,
+                                                 const float* xs, int xs_stride, int half, int lane,
                                                  float (&acc)[M]) {
   const int r0 = 2 * ((lane >> 1) & 3);
   const int sb = ((4 * lane + 1) * bits - 16 + 256 * bits) % (256 * bits);
@@ -306,7 +335,7 @@ __device__ __forceinline__ void accumulate_block(const uint32_t* stage, int bits
   uint32_t st[16];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const uint32_t* t = stage + ((half * 4 + i) * 8 + ntl) * 8 * bits;
+    const uint32_t* t = slot + i * 8 * bits;
     const uint64_t v = (((uint64_t)t[d0] << 32) | t[d1]) << off;
     const uint32_t win = (uint32_t)(v >> sh);
     st[4 * i + 0] = (win >> (3 * bits)) & 0xffffu;
@@ -347,38 +376,19 @@ __device__ __forceinline__ void column_sums(float (&acc)[M]) {
   }
 }
 
-// One k block's 64 tiles as a stage of the LDS ring: every wave issues
-// exactly one 16-byte-per-lane direct load (waves past the block's 2 K
-// kilobytes read nothing, through an empty resource, into a scratch
-// kilobyte), so every wave has the same number of stage loads in flight.
-// Local tile u = (k tile in block) * 8 + (n tile in block) lands at dword
-// u * 8 K of the stage.  wave is the (uniform) wave index.
+// Stage this wave's tiles of k block kb of the kernel-argument matrix.
 __device__ __forceinline__ void stage_block(const LinArgs& a, const LinRecords& rec, int nb, int kb,
-                                            uint32_t* stage, uint32_t* spill, int wave, int lane) {
+                                            uint32_t* stage, int wave, int lane) {
   const int record = a.rate_n ? nb : kb;
-  const int bits = record_rate(rec, record);
   const int64_t record_dw = (int64_t)RECORD_TILES * (a.rate_n ? a.k_tiles : a.n_tiles) * 8;
-  const int64_t rec0 = (int64_t)record_rates_before(rec, record) * record_dw;
-  const int tile_bytes = 32 * bits;
-  const bool live = wave < 2 * bits;
-  // rate n: the block is 64 consecutive tiles of its record; rate k: 8 runs
-  // of 8 tiles, one per k tile of the block, n_tiles tiles apart
-  const int64_t first_tile = a.rate_n ? (int64_t)kb * 64 : (int64_t)nb * 8;
-  const uint8_t* base = reinterpret_cast<const uint8_t*>(a.payload) + (rec0 * 4 + first_tile * tile_bytes);
-  const int byte = wave * 1024 + lane * 16;
-  const int u = byte / tile_bytes, within = byte - u * tile_bytes;
-  const int64_t rel = a.rate_n ? (int64_t)u : (int64_t)(u >> 3) * a.n_tiles + (u & 7);
-  const dma::i32x4_t rs = dma::make_rsrc(base, live ? (uint32_t)dma::MAX_RANGE : 0u);
-  const uint32_t lds = (uint32_t)__builtin_amdgcn_readfirstlane(
-      (int)(live ? dma::lds_offset_of(stage) + (uint32_t)wave * 1024u : dma::lds_offset_of(spill)));
-  dma::load_to_lds16(rs, live ? (uint32_t)(rel * tile_bytes + within) : 0u, lds);
+  stage_wave(a.payload, (int64_t)record_rates_before(rec, record) * record_dw, record_rate(rec, record), a.rate_n,
+             a.n_tiles, nb, kb, stage, wave, lane);
 }
 
 template <int M, bool ROT>
 __global__ __launch_bounds__(LIN_THREADS) void linear_kernel(LinArgs a, LinRecords rec) {
   __shared__ __attribute__((aligned(16))) uint8_t lut[65536];
-  __shared__ __attribute__((aligned(16))) uint32_t ring[LIN_STAGES][2048];
-  __shared__ __attribute__((aligned(16))) uint32_t spill[256];
+  __shared__ __attribute__((aligned(16))) uint32_t ring[LIN_STAGES][2048];  // 16 waves x 512 bytes
   __shared__ __attribute__((aligned(16))) float xs[M][lin_max_kb(M) * 128];
   __shared__ float yb[2][M][128];
   __shared__ int s_last;
@@ -398,7 +408,7 @@ __global__ __launch_bounds__(LIN_THREADS) void linear_kernel(LinArgs a, LinRecor
   stage_labels(a.labels, lut_bits, lut, wave, lane);
 #pragma unroll
   for (int j = 0; j < LIN_STAGES; ++j)
-    if (j < kbn) stage_block(a, rec, nb, kb0 + j, ring[j], spill, wave, lane);
+    if (j < kbn) stage_block(a, rec, nb, kb0 + j, ring[j], wave, lane);
 
   // rotated activation rows of this chunk: lines (row m, k block kbi)
   for (int line = wave; line < M * kbn; line += 16) {
@@ -422,25 +432,26 @@ __global__ __launch_bounds__(LIN_THREADS) void linear_kernel(LinArgs a, LinRecor
   float acc[M];
 #pragma unroll
   for (int m = 0; m < M; ++m) acc[m] = 0.f;
+  // every wave's labels (older than its stage loads) and activation rows
+  wait_own_stage(min(LIN_STAGES, kbn));
+  __syncthreads();
 
   for (int kbi = 0; kbi < kbn; ++kbi) {
     const int bits = record_rate(rec, a.rate_n ? nb : kb0 + kbi);
-    // block kbi has landed once only the younger stages are in flight; the
-    // barrier makes every wave's loads visible (and, on the first pass, the
-    // activation rows and the labels)
-    wait_stage(min(LIN_STAGES - 1, kbn - 1 - kbi));
     if (bits != lut_bits) {  // rate along k changed: restage the labels (uniform)
+      __syncthreads();
       stage_labels(a.labels, bits, lut, wave, lane);
       __builtin_amdgcn_s_waitcnt(dma::waitcnt_vm(0));
       __syncthreads();
       lut_bits = bits;
     }
-    accumulate_block<M>(ring[kbi % LIN_STAGES], bits, lut, &xs[0][kbi * 128], lin_max_kb(M) * 128, half, ntl,
-                        lane, acc);
-    // every wave is done with this stage: refill it with block kbi + stages
-    __syncthreads();
+    // this wave's block kbi has landed once only its younger stages are in flight
+    wait_own_stage(min(LIN_STAGES - 1, kbn - 1 - kbi));
+    accumulate_block<M>(ring[kbi % LIN_STAGES] + wave * 128, bits, lut, &xs[0][kbi * 128], lin_max_kb(M) * 128,
+                        half, lane, acc);
+    // the wave has consumed its slot: refill it with block kbi + stages
     if (kbi + LIN_STAGES < kbn)
-      stage_block(a, rec, nb, kb0 + kbi + LIN_STAGES, ring[kbi % LIN_STAGES], spill, wave, lane);
+      stage_block(a, rec, nb, kb0 + kbi + LIN_STAGES, ring[kbi % LIN_STAGES], wave, lane);
   }
   column_sums<M>(acc);
   if ((lane & 6) == 0) {
@@ -546,36 +557,17 @@ struct MoeArgs {
   ActParams act;
 };
 
-// Stage k block kb of a matrix whose record prefix sums sit in device
-// memory (prefix[r] = sum of the rates of records before r).
-// A wave-uniform pointer held in scalar registers.
-template <typename T>
-__device__ __forceinline__ T* uniform_ptr(T* p) {
-  const uint64_t v = reinterpret_cast<uint64_t>(p);
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
-  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32));
-  return reinterpret_cast<T*>(((uint64_t)hi << 32) | lo);
-}
-
-__device__ __forceinline__ int prefix_stage(const kq_qsrt_matrix& mt, int k_tiles, int n_tiles, int rate_n, int nb,
-                                            int kb, uint32_t* stage, uint32_t* spill, int wave, int lane) {
+// Stage this wave's tiles of k block kb of a matrix whose record prefix
+// sums sit in device memory (prefix[r] = sum of the rates of records
+// before r).
+__device__ __forceinline__ void prefix_stage(const kq_qsrt_matrix& mt, int k_tiles, int n_tiles, int rate_n, int nb,
+                                             int kb, uint32_t* stage, int wave, int lane) {
   const int record = __builtin_amdgcn_readfirstlane(rate_n ? nb : kb);
   const uint32_t p0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)mt.record_prefix[record]);
   const int bits = __builtin_amdgcn_readfirstlane((int)(mt.record_prefix[record + 1] - p0));
   const int64_t record_dw = (int64_t)RECORD_TILES * (rate_n ? k_tiles : n_tiles) * 8;
-  const int tile_bytes = 32 * bits;
-  const bool live = wave < 2 * bits;
-  const int64_t first_tile = rate_n ? (int64_t)kb * 64 : (int64_t)nb * 8;
-  const uint8_t* base = uniform_ptr(reinterpret_cast<const uint8_t*>(mt.payload) +
-                                    ((int64_t)p0 * record_dw * 4 + first_tile * tile_bytes));
-  const int byte = wave * 1024 + lane * 16;
-  const int u = byte / tile_bytes, within = byte - u * tile_bytes;
-  const int64_t rel = rate_n ? (int64_t)u : (int64_t)(u >> 3) * n_tiles + (u & 7);
-  const dma::i32x4_t rs = dma::make_rsrc(base, live ? (uint32_t)dma::MAX_RANGE : 0u);
-  const uint32_t lds = (uint32_t)__builtin_amdgcn_readfirstlane(
-      (int)(live ? dma::lds_offset_of(stage) + (uint32_t)wave * 1024u : dma::lds_offset_of(spill)));
-  dma::load_to_lds16(rs, live ? (uint32_t)(rel * tile_bytes + within) : 0u, lds);
-  return bits;
+  stage_wave(reinterpret_cast<const uint32_t*>(mt.payload), (int64_t)p0 * record_dw, bits, rate_n, n_tiles, nb, kb,
+             stage, wave, lane);
 }
 
 __device__ __forceinline__ int prefix_rate(const kq_qsrt_matrix& mt, int record) {
@@ -586,8 +578,7 @@ __device__ __forceinline__ int prefix_rate(const kq_qsrt_matrix& mt, int record)
 template <bool DOWN>
 __global__ __launch_bounds__(LIN_THREADS) void moe_kernel(MoeArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t lut[65536];
-  __shared__ __attribute__((aligned(16))) uint32_t ring[LIN_STAGES][2048];
-  __shared__ __attribute__((aligned(16))) uint32_t spill[256];
+  __shared__ __attribute__((aligned(16))) uint32_t ring[LIN_STAGES][2048];  // 16 waves x 512 bytes
   __shared__ __attribute__((aligned(16))) float xs[lin_max_kb(1) * 128];
   __shared__ float yb[2][128];
   __shared__ int s_last;
@@ -620,7 +611,7 @@ __global__ __launch_bounds__(LIN_THREADS) void moe_kernel(MoeArgs a) {
     stage_labels(labels, lut_bits, lut, wave, lane);
 #pragma unroll
     for (int s = 0; s < LIN_STAGES; ++s)
-      if (s < kbn) prefix_stage(mt, k_tiles, n_tiles, rate_n, nb, kb0 + s, ring[s], spill, wave, lane);
+      if (s < kbn) prefix_stage(mt, k_tiles, n_tiles, rate_n, nb, kb0 + s, ring[s], wave, lane);
     // the activation row of this chunk, rotated: one wave per k block
     for (int kbi = wave; kbi < kbn; kbi += 16) {
       const int64_t k = (int64_t)(kb0 + kbi) * 128 + lane;
@@ -640,20 +631,21 @@ __global__ __launch_bounds__(LIN_THREADS) void moe_kernel(MoeArgs a) {
       xs[kbi * 128 + lane] = v0;
       xs[kbi * 128 + lane + 64] = v1;
     }
+    wait_own_stage(min(LIN_STAGES, kbn));  // every wave's labels, then the activation row
+    __syncthreads();
     for (int kbi = 0; kbi < kbn; ++kbi) {
       const int bits = prefix_rate(mt, rate_n ? nb : kb0 + kbi);
-      wait_stage(min(LIN_STAGES - 1, kbn - 1 - kbi));
       if (bits != lut_bits) {
+        __syncthreads();
         stage_labels(labels, bits, lut, wave, lane);
         __builtin_amdgcn_s_waitcnt(dma::waitcnt_vm(0));
         __syncthreads();
         lut_bits = bits;
       }
-      accumulate_block<1>(ring[kbi % LIN_STAGES], bits, lut, &xs[kbi * 128], 0, half, ntl, lane, acc);
-      __syncthreads();
+      wait_own_stage(min(LIN_STAGES - 1, kbn - 1 - kbi));
+      accumulate_block<1>(ring[kbi % LIN_STAGES] + wave * 128, bits, lut, &xs[kbi * 128], 0, half, lane, acc);
       if (kbi + LIN_STAGES < kbn)
-        prefix_stage(mt, k_tiles, n_tiles, rate_n, nb, kb0 + kbi + LIN_STAGES, ring[kbi % LIN_STAGES], spill, wave,
-                     lane);
+        prefix_stage(mt, k_tiles, n_tiles, rate_n, nb, kb0 + kbi + LIN_STAGES, ring[kbi % LIN_STAGES], wave, lane);
     }
     column_sums<1>(acc);
   }
