@@ -100,3 +100,49 @@ def test_payload_round_trip_and_rotation(rate_axis):
     bn = np.kron(np.eye(n_tiles // 8), h)
     undone = bk.T @ (full / suh[:, None] / svh[None, :]) @ bn.T
     assert np.allclose(undone, reg, atol=1e-9)
+
+
+def test_situ64_is_the_pinned_fp32_situ_in_double():
+    """situ64 restates kquant/tp_simulator.py:83-94 in f64; oracle.situ (the
+    fp32 restatement, pinned by the reference's known answers in the GPU MLP
+    tests) must agree to fp32 rounding, and the closed forms hold: 0 at
+    g = 0 or u = 0, odd in u, and -> beta * linear_beta * tanh(u / lb) for
+    large g."""
+    rng = np.random.default_rng(3)
+    g = rng.standard_normal(4096) * 6
+    u = rng.standard_normal(4096) * 40
+    a64 = qsrt.situ64(g, u)
+    a32 = oracle.situ(g.astype(np.float32), u.astype(np.float32)).astype(np.float64)
+    assert np.allclose(a64, a32, rtol=2e-6, atol=1e-6)
+    assert np.all(qsrt.situ64(np.zeros(8), u[:8]) == 0) and np.all(qsrt.situ64(g[:8], np.zeros(8)) == 0)
+    assert np.allclose(qsrt.situ64(g, -u), -a64)
+    assert np.allclose(qsrt.situ64(np.full(4, 60.0), u[:4]), 4.0 * 25.0 * np.tanh(u[:4] / 25.0))
+
+
+def test_linear_and_expert_oracles_reduce_to_the_decoded_weight():
+    """qsrt_linear with one-hot rows returns rows of decode_qsrt_weight; the
+    expert oracle is linear in the route weights and ignores invalid ids."""
+    rng = np.random.default_rng(4)
+    labels = {b: oracle.sqg_xor_cheb_t12_bytes(b) for b in (2, 3, 4)}
+    k_tiles, n_tiles, bits = 16, 8, (3, 2)
+    states = np.stack([qsrt.reconstruct_trellis_states(rng.integers(0, 8, (n_tiles, 256)), 3)
+                       for _ in range(k_tiles)]).astype(np.int16)
+    payload = qsrt.pack_payload(states, bits, "k")
+    w = qsrt.decode_qsrt_weight(payload, k_tiles, n_tiles, bits, "k", labels)
+    rows = np.array([0, 5, 130, 255])
+    x = np.zeros((4, k_tiles * 16))
+    x[np.arange(4), rows] = 1.0
+    assert np.array_equal(qsrt.qsrt_linear(x, payload, k_tiles, n_tiles, bits, "k", labels), w[rows])
+
+    def mat(k, n, axis):
+        recs = (k if axis == "k" else n) // 128
+        per = 8 * ((n if axis == "k" else k) // 16)
+        return (rng.integers(-32768, 32768, per * 16 * 3 * recs).astype(np.int16), (3,) * recs,
+                rng.uniform(0.5, 1.5, k), rng.uniform(0.5, 1.5, n))
+
+    experts = [(mat(256, 128, "n"), mat(256, 128, "n"), mat(128, 256, "k")) for _ in range(2)]
+    x = rng.standard_normal((1, 256)) * 0.05
+    one = qsrt.qsrt_expert_forward(x, [[0, 1]], [[1.0, 0.0]], experts, 256, 128, labels, labels)
+    two = qsrt.qsrt_expert_forward(x, [[0, 1]], [[2.0, 0.0]], experts, 256, 128, labels, labels)
+    skip = qsrt.qsrt_expert_forward(x, [[0, 7]], [[1.0, 3.0]], experts, 256, 128, labels, labels)
+    assert np.allclose(two, 2 * one) and np.array_equal(skip, one) and np.abs(one).max() > 0
