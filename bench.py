@@ -156,6 +156,17 @@ def main() -> int:
 
     t_quant = _time_loop(torch, quantize_step, args.steps, args.warmup) if want("quantize") else float("nan")
     quant_gbs = quant_bytes / t_quant / 1e9
+    if want("quantize"):
+        # what a plain device copy of the same weight reaches on this box (read + write)
+        copy_dst = torch.empty_like(w2)
+        t_copy = _time_loop(torch, lambda: copy_dst.copy_(w2), args.steps, args.warmup)
+        copy_gbs = 2 * w2.numel() * w2.element_size() / t_copy / 1e9
+        result["hbm_copy_reference"] = {
+            "what": "torch device copy of the cfg2 bf16 weight (176 MB read + 176 MB written)",
+            "gbs": round(copy_gbs, 1),
+            "quantize_over_copy": round(quant_gbs / copy_gbs, 3),
+        }
+        del copy_dst
 
     # ---------------------------------------------- config 2 GEMM (A16) --
     if not args.quick and want("linear"):
