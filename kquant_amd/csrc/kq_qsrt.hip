@@ -251,12 +251,9 @@ __device__ __forceinline__ void fwht128(float& v0, float& v1, int lane) {
   }
 }
 
-// E4M3 byte -> fp32 by placing its bits in an fp32 pattern (exponent bias
-// 7 instead of 127, codes with a zero exponent landing on fp32 denormals,
-// which these kernels keep) and one exact multiply by 2^120.
-__device__ __forceinline__ float e4m3_scaled(uint32_t b) {
-  return __builtin_bit_cast(float, ((b & 0x7Fu) << 20) | ((b & 0x80u) << 24)) * 0x1p120f;
-}
+// E4M3 (OCP, fn) byte -> fp32 with the gfx950 conversion instruction (exact:
+// every finite E4M3 value is an fp32 value).
+__device__ __forceinline__ float e4m3_scaled(uint32_t b) { return __builtin_amdgcn_cvt_f32_fp8((int)b, 0); }
 
 __device__ __forceinline__ float load_x(const void* x, int dtype, int64_t i) {
   if (dtype == KQ_DT_F32) return reinterpret_cast<const float*>(x)[i];
@@ -317,7 +314,9 @@ __device__ __forceinline__ void stage_wave(const uint32_t* payload, int64_t rec0
   const dma::i32x4_t rs = dma::make_rsrc(base, (uint32_t)dma::MAX_RANGE);
   const uint32_t lds =
       (uint32_t)__builtin_amdgcn_readfirstlane((int)(dma::lds_offset_of(stage) + (uint32_t)wave * 512u));
-  const int i = lane / (2 * bits), within = (lane - i * 2 * bits) * 16;
+  // i = lane / (2 K) by a multiply: exact for lane < 64 and 2 K in {4, 6, 8}
+  const int magic = bits == 2 ? 16385 : bits == 3 ? 10923 : 8193;
+  const int i = (lane * magic) >> 16, within = (lane - i * 2 * bits) * 16;
   if (lane < 8 * bits) dma::load_to_lds16(rs, (uint32_t)(i * step * tile_bytes + within), lds);
 }
 
@@ -330,8 +329,10 @@ __device__ __forceinline__ void accumulate_block(const uint32_t* slot, int bits,
                                                  const float* xs, int xs_stride, int half, int lane,
                                                  float (&acc)[M]) {
   const int r0 = 2 * ((lane >> 1) & 3);
-  const int sb = ((4 * lane + 1) * bits - 16 + 256 * bits) % (256 * bits);
-  const int d0 = sb >> 5, d1 = (d0 + 1) % (8 * bits), off = sb & 31, sh = 64 - (16 + 3 * bits);
+  // first stream bit of the window: (4 lane + 1) K - 16, cyclic (lane 0 wraps)
+  int sb = (4 * lane + 1) * bits - 16;
+  if (sb < 0) sb += 256 * bits;
+  const int d0 = sb >> 5, d1 = d0 + 1 == 8 * bits ? 0 : d0 + 1, off = sb & 31, sh = 64 - (16 + 3 * bits);
   uint32_t st[16];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {

@@ -145,3 +145,27 @@ def test_launcher_in_a_graph_replays_the_eager_result(gpu):
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, eager), i
+
+
+def test_every_finite_e4m3_label_converts_exactly(gpu):
+    """Labels equal to the state's low byte (the two NaN codes mapped to
+    zero) put every finite E4M3 code into the weight; identity activation
+    rows read W back, which must equal the oracle's E4M3 values exactly."""
+    from kquant_amd import _native as N
+
+    k_tiles, n_tiles, bits = 8, 16, (3, 2)
+    payload = _random_matrix(k_tiles, n_tiles, "n", bits, 31)
+    table = (np.arange(65536) & 0xFF).astype(np.uint8)
+    table[(table & 0x7F) == 0x7F] = 0
+    labels = torch.from_numpy(np.stack([table] * 3)).to(gpu)
+    want = oq.decode_qsrt_weight(payload, k_tiles, n_tiles, bits, "n", {2: table, 3: table, 4: table})
+    assert len(np.unique(want)) == 253  # every finite code (the two zeros compare equal)
+    p = torch.from_numpy(payload).to(gpu)
+    x = torch.eye(k_tiles * 16, device=gpu)
+    out = torch.empty(k_tiles * 16, n_tiles * 16, device=gpu)
+    need = int(N.library().kq_qsrt_linear_workspace_size(x.shape[0], k_tiles, n_tiles))
+    ws = torch.zeros(max(need, 1), dtype=torch.uint8, device=gpu)
+    N.call("kq_qsrt_linear", N.ptr(x), N.DT_F32, x.shape[0], x.shape[1], N.ptr(p), p.numel(), k_tiles, n_tiles, 1,
+           bytes(bits), N.ptr(labels), None, None, N.DT_F32, N.ptr(out), out.shape[1], N.ptr(ws), need,
+           N.stream(gpu))
+    assert np.array_equal(out.cpu().numpy(), want)
