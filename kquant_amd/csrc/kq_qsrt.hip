@@ -554,7 +554,7 @@ struct MoeArgs {
   int* counters;    // gate/up: [pairs][2][I / 128]; down: [tokens][H / 128]
   void* out;
   int64_t ldo, pairs;
-  int topk, experts, hidden_tiles, inter_tiles, rate13_n, rate2_n, kbw, chunks, x_dtype, out_dtype;
+  int topk, experts, hidden_tiles, inter_tiles, rate13_n, rate2_n, kbw, chunks, nbw, x_dtype, out_dtype;
   ActParams act;
 };
 
@@ -576,6 +576,20 @@ __device__ __forceinline__ int prefix_rate(const kq_qsrt_matrix& mt, int record)
   return __builtin_amdgcn_readfirstlane((int)(mt.record_prefix[record + 1] - mt.record_prefix[record]));
 }
 
+// Sum the partial rows [first, first + count) of a 128-column block into
+// dst (fp32 h row or the output in its dtype): 8 threads per column, thread
+// r taking rows r, r + 8, ... (loads issued together), then a fixed tree.
+__device__ __forceinline__ float sum_partials(const float* q, int64_t stride, int count, int tid) {
+  const int r = tid & 7;
+  float sum = 0.f;
+  for (int i = r; i < count; i += 8)
+    sum += __hip_atomic_load(q + (int64_t)i * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  sum += __shfl_xor(sum, 1);
+  sum += __shfl_xor(sum, 2);
+  sum += __shfl_xor(sum, 4);
+  return sum;
+}
+
 template <bool DOWN>
 __global__ __launch_bounds__(LIN_THREADS) void moe_kernel(MoeArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t lut[65536];
@@ -586,33 +600,36 @@ __global__ __launch_bounds__(LIN_THREADS) void moe_kernel(MoeArgs a) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int half = wave >> 3, ntl = wave & 7;
-  const int H = a.hidden_tiles * TILE, I = a.inter_tiles * TILE;
+  const int I = a.inter_tiles * TILE;
   const int k_tiles = DOWN ? a.inter_tiles : a.hidden_tiles, n_tiles = DOWN ? a.hidden_tiles : a.inter_tiles;
   const int rate_n = DOWN ? a.rate2_n : a.rate13_n;
   const int n_blocks = n_tiles >> 3, k_blocks = k_tiles >> 3, N = n_tiles * TILE;
+  const int n_groups = (n_blocks + a.nbw - 1) / a.nbw;
   int job = (int)blockIdx.x;
   const int chunk = job % a.chunks;
   job /= a.chunks;
-  const int nb = job % n_blocks;
-  job /= n_blocks;
+  const int nb0 = (job % n_groups) * a.nbw;
+  job /= n_groups;
+  const int nbc = min(a.nbw, n_blocks - nb0);  // n blocks of this workgroup, one after the other
   const int j = DOWN ? 2 : job % 2;
   const int64_t p = DOWN ? job : job / 2;
   const int64_t t = p / a.topk;
   const int kb0 = chunk * a.kbw;
   const int kbn = min(a.kbw, k_blocks - kb0);
+  const int total = nbc * kbn;  // (n block, k block) steps through the ring
   const int e = __builtin_amdgcn_readfirstlane(a.route_ids[p]);
   const bool valid = e >= 0 && e < a.experts;
   kq_qsrt_matrix mt{};
   if (valid) mt = a.mats[(int64_t)e * 3 + j];
   const uint8_t* labels = a.labels + (DOWN ? 3 * 65536 : 0);  // the down projection's rate axis has its own
 
-  float acc[1] = {0.f};
+  int lut_bits = 0;
   if (valid) {
-    int lut_bits = prefix_rate(mt, rate_n ? nb : kb0);
+    lut_bits = prefix_rate(mt, rate_n ? nb0 : kb0);
     stage_labels(labels, lut_bits, lut, wave, lane);
 #pragma unroll
     for (int s = 0; s < LIN_STAGES; ++s)
-      if (s < kbn) prefix_stage(mt, k_tiles, n_tiles, rate_n, nb, kb0 + s, ring[s], wave, lane);
+      if (s < total) prefix_stage(mt, k_tiles, n_tiles, rate_n, nb0 + s / kbn, kb0 + s % kbn, ring[s], wave, lane);
     // the activation row of this chunk, rotated: one wave per k block
     for (int kbi = wave; kbi < kbn; kbi += 16) {
       const int64_t k = (int64_t)(kb0 + kbi) * 128 + lane;
@@ -632,87 +649,94 @@ __global__ __launch_bounds__(LIN_THREADS) void moe_kernel(MoeArgs a) {
       xs[kbi * 128 + lane] = v0;
       xs[kbi * 128 + lane + 64] = v1;
     }
-    wait_own_stage(min(LIN_STAGES, kbn));  // every wave's labels, then the activation row
+    wait_own_stage(min(LIN_STAGES, total));  // every wave's labels, then the activation row
     __syncthreads();
-    for (int kbi = 0; kbi < kbn; ++kbi) {
+  }
+
+  float acc[1] = {0.f};
+  int nbi = 0, kbi = 0;
+  for (int u = 0; u < (valid ? total : nbc); ++u) {
+    const int nb = nb0 + nbi;
+    if (valid) {
       const int bits = prefix_rate(mt, rate_n ? nb : kb0 + kbi);
-      if (bits != lut_bits) {
+      if (bits != lut_bits) {  // the rate changed (uniform): restage the labels
         __syncthreads();
         stage_labels(labels, bits, lut, wave, lane);
         __builtin_amdgcn_s_waitcnt(dma::waitcnt_vm(0));
         __syncthreads();
         lut_bits = bits;
       }
-      wait_own_stage(min(LIN_STAGES - 1, kbn - 1 - kbi));
-      accumulate_block<1>(ring[kbi % LIN_STAGES] + wave * 128, bits, lut, &xs[kbi * 128], 0, half, lane, acc);
-      if (kbi + LIN_STAGES < kbn)
-        prefix_stage(mt, k_tiles, n_tiles, rate_n, nb, kb0 + kbi + LIN_STAGES, ring[kbi % LIN_STAGES], wave, lane);
+      wait_own_stage(min(LIN_STAGES - 1, total - 1 - u));
+      accumulate_block<1>(ring[u % LIN_STAGES] + wave * 128, bits, lut, &xs[kbi * 128], 0, half, lane, acc);
+      if (u + LIN_STAGES < total) {
+        const int un = u + LIN_STAGES;
+        prefix_stage(mt, k_tiles, n_tiles, rate_n, nb0 + un / kbn, kb0 + un % kbn, ring[u % LIN_STAGES], wave, lane);
+      }
     }
+    if (++kbi < kbn && valid) continue;
+    // -------- n block nb done: rotate, scale, and hand over its partial --
+    kbi = 0;
+    ++nbi;
     column_sums<1>(acc);
-  }
-  if ((lane & 6) == 0) yb[half][ntl * 16 + (lane >> 3) + 8 * (lane & 1)] = acc[0];
-  __syncthreads();
-
-  const int64_t col0 = (int64_t)nb * 128;
-  float v0 = 0.f, v1 = 0.f;
-  if (wave == 0 && valid) {
-    v0 = yb[0][lane] + yb[1][lane];
-    v1 = yb[0][lane + 64] + yb[1][lane + 64];
-    fwht128(v0, v1, lane);
-    v0 *= (1.f / 128.f) * mt.svh[col0 + lane];
-    v1 *= (1.f / 128.f) * mt.svh[col0 + lane + 64];
-  }
-  if (!DOWN && a.chunks == 1) {
+    if ((lane & 6) == 0) yb[half][ntl * 16 + (lane >> 3) + 8 * (lane & 1)] = acc[0];
+    acc[0] = 0.f;
+    __syncthreads();
+    const int64_t col0 = (int64_t)nb * 128;
+    float v0 = 0.f, v1 = 0.f;
+    if (wave == 0 && valid) {
+      v0 = yb[0][lane] + yb[1][lane];
+      v1 = yb[0][lane + 64] + yb[1][lane + 64];
+      fwht128(v0, v1, lane);
+      v0 *= (1.f / 128.f) * mt.svh[col0 + lane];
+      v1 *= (1.f / 128.f) * mt.svh[col0 + lane + 64];
+    }
+    if (!DOWN && a.chunks == 1) {
+      if (wave == 0) {
+        float* hp = a.h + p * 2 * I + j * I + col0;
+        hp[lane] = v0;
+        hp[lane + 64] = v1;
+      }
+      __syncthreads();  // yb is rewritten by the next n block
+      continue;
+    }
+    // partials through agent-scope atomics (written through / read past the
+    // per-XCD L2s); the last workgroup of the output block sums them in order
+    int64_t slot, first;
+    int count;
+    int* counter;
+    if constexpr (DOWN) {
+      slot = p * a.chunks + chunk;
+      first = t * a.topk * a.chunks;
+      count = a.topk * a.chunks;
+      counter = a.counters + t * n_blocks + nb;
+    } else {
+      slot = (p * 2 + j) * a.chunks + chunk;
+      first = (p * 2 + j) * a.chunks;
+      count = a.chunks;
+      counter = a.counters + (p * 2 + j) * n_blocks + nb;
+    }
     if (wave == 0) {
-      float* hp = a.h + p * 2 * I + j * I + col0;
-      hp[lane] = v0;
-      hp[lane + 64] = v1;
+      float* q = a.partial + slot * N + col0;
+      __hip_atomic_store(q + lane, v0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(q + lane + 64, v1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    return;
-  }
-  // partials through agent-scope atomics (written through / read past the
-  // per-XCD L2s); the last workgroup of the output block sums them in order
-  int64_t slot;    // this workgroup's partial row
-  int64_t first;   // the output block's first partial row
-  int count;       // partial rows of the output block
-  int* counter;
-  if constexpr (DOWN) {
-    slot = p * a.chunks + chunk;
-    first = t * a.topk * a.chunks;
-    count = a.topk * a.chunks;
-    counter = a.counters + t * n_blocks + nb;
-  } else {
-    slot = (p * 2 + j) * a.chunks + chunk;
-    first = (p * 2 + j) * a.chunks;
-    count = a.chunks;
-    counter = a.counters + (p * 2 + j) * n_blocks + nb;
-  }
-  if (wave == 0) {
-    float* q = a.partial + slot * N + col0;
-    __hip_atomic_store(q + lane, v0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(q + lane + 64, v1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  __builtin_amdgcn_s_waitcnt(dma::waitcnt_vm(0));
-  __syncthreads();
-  if (tid == 0) s_last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == count - 1;
-  __syncthreads();
-  if (!s_last) return;
-  // 8 threads per output column, thread r summing partial rows r, r + 8, ...
-  {
-    const int c = tid >> 3, r = tid & 7;
-    const float* q = a.partial + first * N + col0 + c;
-    float sum = 0.f;
-    for (int i = r; i < count; i += 8)
-      sum += __hip_atomic_load(q + (int64_t)i * N, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    sum += __shfl_xor(sum, 1);
-    sum += __shfl_xor(sum, 2);
-    sum += __shfl_xor(sum, 4);
-    if (r == 0) {
-      if constexpr (DOWN) store_out(a.out, a.out_dtype, t * a.ldo + col0 + c, sum);
-      else a.h[p * 2 * I + j * I + col0 + c] = sum;
+    // wave 0's partial stores have completed before the barrier that
+    // precedes the count
+    if (wave == 0) __builtin_amdgcn_s_waitcnt(dma::waitcnt_vm(0));
+    __syncthreads();
+    if (tid == 0) s_last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == count - 1;
+    __syncthreads();
+    if (s_last) {
+      const float sum = sum_partials(a.partial + first * N + col0 + (tid >> 3), N, count, tid);
+      if ((tid & 7) == 0) {
+        const int c = tid >> 3;
+        if constexpr (DOWN) store_out(a.out, a.out_dtype, t * a.ldo + col0 + c, sum);
+        else a.h[p * 2 * I + j * I + col0 + c] = sum;
+      }
+      if (tid == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+    __syncthreads();  // s_last and yb are rewritten by the next n block
   }
-  if (tid == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 }  // namespace qsrt
@@ -832,10 +856,14 @@ struct LinPlan {
   int64_t counters_bytes, partial_bytes;
 };
 
-// K chunk per workgroup: the fewest rounds of workgroups times k blocks per
-// workgroup, plus the cost of a cross-workgroup reduction when K is split
-// (ties to the larger chunk: fewer partials to sum).
-constexpr int LIN_REDUCE_KB = 4;
+// K chunk per workgroup: the least (rounds of workgroups) x (fixed cost of a
+// workgroup + its k blocks), plus the cost of a cross-workgroup reduction
+// when K is split (ties to the larger chunk: fewer partials to sum).  Costs
+// in units of one k block of one workgroup (measured: about 1.3 us; a
+// workgroup's fixed part, launch to last store, about 4 us; a
+// cross-workgroup sum about 2.7 us).
+constexpr int LIN_FIXED_KB = 3;
+constexpr int LIN_REDUCE_KB = 2;
 hipError_t lin_plan(int64_t m, int64_t k_tiles, int64_t n_tiles, LinPlan* p) {
   int dev = 0, cus = 0;
   hipError_t e = hipGetDevice(&dev);
@@ -853,7 +881,7 @@ hipError_t lin_plan(int64_t m, int64_t k_tiles, int64_t n_tiles, LinPlan* p) {
     const int64_t rounds = (n_blocks * chunks * p->groups + slots - 1) / slots;
     // time in units of one k block per workgroup; summing partials across
     // workgroups costs about LIN_REDUCE_KB more (store, count, reload)
-    const int64_t cost = rounds * kbw + (chunks > 1 ? LIN_REDUCE_KB : 0);
+    const int64_t cost = rounds * (LIN_FIXED_KB + kbw) + (chunks > 1 ? LIN_REDUCE_KB : 0);
     if (best < 0 || cost <= best) {
       best = cost;
       p->kbw = kbw;
@@ -963,25 +991,31 @@ extern "C" int kq_qsrt_linear(const void* x, int x_dtype, int64_t m, int64_t ldx
 namespace {
 
 struct MoePlan {
-  int kbw13, chunks13, kbw2, chunks2;
+  int kbw13, chunks13, nbw13, kbw2, chunks2, nbw2;
   int64_t h_bytes, part13_bytes, part2_bytes, cnt13_bytes, cnt2_bytes;
 };
 
 int64_t align256(int64_t v) { return (v + 255) / 256 * 256; }
 
-// Same cost model as the single linear: rounds of workgroups times k blocks
-// per workgroup, plus the cross-workgroup sum where it is optional.
-void moe_chunking(int64_t jobs, int64_t k_blocks, int64_t slots, bool sum_anyway, int* kbw_out, int* chunks_out) {
+// Same cost model as the single linear, with nbw n blocks walked one after
+// the other by a workgroup (sharing its activation row and labels).
+void moe_chunking(int64_t jobs, int64_t n_blocks, int64_t k_blocks, int64_t slots, bool sum_anyway, int* kbw_out,
+                  int* chunks_out, int* nbw_out) {
   int64_t best = -1;
   const int64_t max_kb = k_blocks < lin_max_kb(1) ? k_blocks : lin_max_kb(1);
-  for (int kbw = 1; kbw <= max_kb; ++kbw) {
-    const int64_t chunks = (k_blocks + kbw - 1) / kbw;
-    const int64_t rounds = (jobs * chunks + slots - 1) / slots;
-    const int64_t cost = rounds * kbw + (!sum_anyway && chunks > 1 ? LIN_REDUCE_KB : 0);
-    if (best < 0 || cost <= best) {
-      best = cost;
-      *kbw_out = kbw;
-      *chunks_out = (int)chunks;
+  for (int nbw = 1; nbw <= n_blocks && nbw <= 32; ++nbw) {
+    const int64_t groups = (n_blocks + nbw - 1) / nbw;
+    for (int kbw = 1; kbw <= max_kb; ++kbw) {
+      const int64_t chunks = (k_blocks + kbw - 1) / kbw;
+      const int64_t rounds = (jobs * groups * chunks + slots - 1) / slots;
+      const int64_t cost = rounds * (LIN_FIXED_KB + (int64_t)nbw * kbw) +
+                           (!sum_anyway && chunks > 1 ? LIN_REDUCE_KB : 0);
+      if (best < 0 || cost < best || (cost == best && kbw * nbw > *kbw_out * *nbw_out)) {
+        best = cost;
+        *kbw_out = kbw;
+        *chunks_out = (int)chunks;
+        *nbw_out = nbw;
+      }
     }
   }
 }
@@ -993,10 +1027,10 @@ hipError_t moe_plan(int64_t tokens, int topk, int64_t hidden_tiles, int64_t inte
   if (e != hipSuccess) return e;
   const int64_t slots = cus > 0 ? cus : 1;
   const int64_t pairs = tokens * topk, H = hidden_tiles * TILE, I = inter_tiles * TILE;
-  moe_chunking(pairs * 2 * (inter_tiles / RECORD_TILES), hidden_tiles / RECORD_TILES, slots, false, &p->kbw13,
-               &p->chunks13);
-  moe_chunking(pairs * (hidden_tiles / RECORD_TILES), inter_tiles / RECORD_TILES, slots, true, &p->kbw2,
-               &p->chunks2);
+  moe_chunking(pairs * 2, inter_tiles / RECORD_TILES, hidden_tiles / RECORD_TILES, slots, false, &p->kbw13,
+               &p->chunks13, &p->nbw13);
+  moe_chunking(pairs, hidden_tiles / RECORD_TILES, inter_tiles / RECORD_TILES, slots, true, &p->kbw2, &p->chunks2,
+               &p->nbw2);
   p->h_bytes = align256(pairs * 2 * I * 4);
   p->part13_bytes = p->chunks13 > 1 ? align256(pairs * 2 * p->chunks13 * I * 4) : 0;
   p->part2_bytes = align256(pairs * p->chunks2 * H * 4);
@@ -1045,8 +1079,10 @@ extern "C" int kq_qsrt_moe_decode(int act, float beta, float linear_beta, const 
     return kq_fail(KQ_ERR_INVALID, "%s: workspace needs %lld bytes (256-byte aligned, zeroed before first use)", fn,
                    (long long)need);
   const int64_t pairs = tokens * topk;
-  const int64_t jobs13 = pairs * 2 * (inter_tiles / RECORD_TILES) * p.chunks13;
-  const int64_t jobs2 = pairs * (hidden_tiles / RECORD_TILES) * p.chunks2;
+  const int64_t groups13 = (inter_tiles / RECORD_TILES + p.nbw13 - 1) / p.nbw13;
+  const int64_t groups2 = (hidden_tiles / RECORD_TILES + p.nbw2 - 1) / p.nbw2;
+  const int64_t jobs13 = pairs * 2 * groups13 * p.chunks13;
+  const int64_t jobs2 = pairs * groups2 * p.chunks2;
   if (jobs13 > 0x7fffffff || jobs2 > 0x7fffffff) return kq_fail(KQ_ERR_LIMIT, "%s: too many workgroups", fn);
   char* ws = static_cast<char*>(workspace);
   MoeArgs a{};
@@ -1073,6 +1109,7 @@ extern "C" int kq_qsrt_moe_decode(int act, float beta, float linear_beta, const 
   MoeArgs g = a;
   g.kbw = p.kbw13;
   g.chunks = p.chunks13;
+  g.nbw = p.nbw13;
   g.partial = reinterpret_cast<float*>(ws + p.h_bytes);
   g.counters = reinterpret_cast<int*>(ws + p.h_bytes + p.part13_bytes + p.part2_bytes);
   moe_kernel<false><<<(unsigned)jobs13, LIN_THREADS, 0, st>>>(g);
@@ -1080,6 +1117,7 @@ extern "C" int kq_qsrt_moe_decode(int act, float beta, float linear_beta, const 
   MoeArgs d = a;
   d.kbw = p.kbw2;
   d.chunks = p.chunks2;
+  d.nbw = p.nbw2;
   d.partial = reinterpret_cast<float*>(ws + p.h_bytes + p.part13_bytes);
   d.counters = reinterpret_cast<int*>(ws + p.h_bytes + p.part13_bytes + p.part2_bytes + p.cnt13_bytes);
   moe_kernel<true><<<(unsigned)jobs2, LIN_THREADS, 0, st>>>(d);
