@@ -83,6 +83,9 @@ def unpack_trellis_states(packed: torch.Tensor, bits: int) -> torch.Tensor:
     return _unpack(packed, bits, True)
 
 
+# rows up to which qsrt_linear runs the fused kernel (decode batches)
+FUSED_MAX_ROWS = 64
+
 _LABELS: dict[tuple[str, str | None, torch.device], torch.Tensor] = {}
 _LINEAR_WORKSPACES: dict[tuple, torch.Tensor] = {}
 
@@ -239,7 +242,11 @@ def qsrt_linear(
     (bf16, fp16 or fp32) -> [..., N] in ``out_dtype`` (default x's dtype),
     fp32 arithmetic inside.  For the reference's dense path this is
     ``F.linear(x, decode_qsrt_exl3_weight(...).T)`` without the bf16 weight
-    it materializes (scripts/stream_k3_pytorch.py:771-775)."""
+    it materializes (scripts/stream_k3_pytorch.py:771-775).  Beyond
+    ``FUSED_MAX_ROWS`` rows (prefill), where the fused kernel would decode
+    the weight once per 16 rows, the matrix is decoded once to bf16
+    (``kq_qsrt_decode_weight``) and applied with the bf16 GEMM - the
+    reference's own path, with its bf16 weight rounding."""
 
     if rate_axis not in ("k", "n"):
         raise ValueError("rate_axis must be 'k' or 'n'")
@@ -266,6 +273,12 @@ def qsrt_linear(
             raise ValueError("suh and svh must match the K and N dimensions")
         su = N.aligned(suh.to(device=gpu, dtype=torch.float32).reshape(-1), 4)
         sv = N.aligned(svh.to(device=gpu, dtype=torch.float32).reshape(-1), 4)
+    if m > FUSED_MAX_ROWS:
+        dense = decode_qsrt_payload(g, k_tiles=k_tiles, n_tiles=n_tiles, rate_axis=rate_axis, record_bits=bits,
+                                    suh=su, svh=sv, codebook=codebook, out_dtype=torch.bfloat16, transposed=True)
+        out = torch.nn.functional.linear(rows.to(torch.bfloat16), dense).to(out_dtype)
+        out = out.reshape(*x.shape[:-1], n)
+        return out if host is None else out.to(host)
     out = torch.empty(m, n, dtype=out_dtype, device=gpu)
     need = int(N.library().kq_qsrt_linear_workspace_size(max(m, 1), k_tiles, n_tiles)) if m else 0
     if need < 0:

@@ -169,3 +169,26 @@ def test_every_finite_e4m3_label_converts_exactly(gpu):
            bytes(bits), N.ptr(labels), None, None, N.DT_F32, N.ptr(out), out.shape[1], N.ptr(ws), need,
            N.stream(gpu))
     assert np.array_equal(out.cpu().numpy(), want)
+
+
+def test_prefill_rows_take_the_decoded_bf16_path(gpu):
+    """Beyond FUSED_MAX_ROWS rows the matrix is decoded once to bf16 and
+    applied with the bf16 GEMM (the reference's path, bf16 result): equal
+    to bf16(x) @ bf16(W) in f64 up to fp32 accumulation and the bf16 output
+    rounding, and within bf16 rounding of the exact product."""
+    k_tiles, n_tiles, bits = 32, 16, (3, 4)
+    payload = _random_matrix(k_tiles, n_tiles, "n", bits, 41)
+    suh, svh = _scales(k_tiles, n_tiles, 42)
+    m = qsrt.FUSED_MAX_ROWS + 37
+    x = np.random.default_rng(43).standard_normal((m, k_tiles * 16)).astype(np.float32)
+    args = dict(k_tiles=k_tiles, n_tiles=n_tiles, rate_axis="n", record_bits=bits, suh=torch.from_numpy(suh),
+                svh=torch.from_numpy(svh))
+    got = qsrt.qsrt_linear(torch.from_numpy(x).to(gpu), torch.from_numpy(payload).to(gpu), out_dtype=torch.float32,
+                           **args).cpu().numpy().astype(np.float64)
+    w = oq.decode_qsrt_weight(payload, k_tiles, n_tiles, bits, "n", _LABELS, suh, svh)
+    xb = torch.from_numpy(x).to(torch.bfloat16).double().numpy()
+    wb = torch.from_numpy(w).to(torch.bfloat16).double().numpy()
+    ref_b = xb @ wb
+    assert np.all(np.abs(got - ref_b) <= np.abs(ref_b) * 2.0 ** -8 + 1e-5 * np.abs(ref_b).max())
+    exact = x.astype(np.float64) @ w
+    assert np.abs(got - exact).max() <= 2e-2 * np.abs(exact).max()
