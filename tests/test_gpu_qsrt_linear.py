@@ -192,3 +192,19 @@ def test_prefill_rows_take_the_decoded_bf16_path(gpu):
     assert np.all(np.abs(got - ref_b) <= np.abs(ref_b) * 2.0 ** -8 + 1e-5 * np.abs(ref_b).max())
     exact = x.astype(np.float64) @ w
     assert np.abs(got - exact).max() <= 2e-2 * np.abs(exact).max()
+
+
+def test_chunks_spanning_records_of_different_rates(gpu):
+    """K = 5120 along the rate axis k with alternating record rates: the
+    planner gives a workgroup two or more k blocks, so it crosses records of
+    different rates and restages the label table mid-chunk."""
+    k_tiles, n_tiles = 320, 64
+    record_bits = (2, 4, 3) * 13 + (4,)
+    payload = _random_matrix(k_tiles, n_tiles, "k", record_bits, 51)
+    suh, svh = _scales(k_tiles, n_tiles, 52)
+    x = np.random.default_rng(53).standard_normal((1, k_tiles * 16)).astype(np.float32)
+    ref = oq.qsrt_linear(x, payload, k_tiles, n_tiles, record_bits, "k", _LABELS, suh, svh)
+    got = qsrt.qsrt_linear(torch.from_numpy(x).to(gpu), torch.from_numpy(payload).to(gpu), k_tiles=k_tiles,
+                           n_tiles=n_tiles, rate_axis="k", record_bits=record_bits, suh=torch.from_numpy(suh),
+                           svh=torch.from_numpy(svh)).cpu().numpy()
+    assert np.abs(got - ref).max() <= 4e-6 * np.abs(ref).max()

@@ -113,3 +113,19 @@ def test_tp12_geometry_matches_dense_product(gpu):
             a = 4.0 * torch.tanh(g / 4.0) * torch.sigmoid(g) * 25.0 * torch.tanh(u / 25.0)
             ref[t] += float(wts[t, s]) * (a @ dense(e, 2))
     assert (got - ref).abs().max().item() <= 2e-5 * ref.abs().max().item()
+
+
+def test_workgroups_walking_several_n_blocks_match_oracle(gpu):
+    """16 tokens x top-8: the planner lets a gate/up workgroup walk both n
+    blocks of a matrix (records of different rates along n, so the labels
+    are restaged between them) and a down workgroup several hidden blocks."""
+    hidden, inter, count, tokens, topk = 640, 256, 6, 16, 8
+    spec, experts = _experts(13, count, hidden, inter)
+    rng = np.random.default_rng(14)
+    x = (rng.standard_normal((tokens, hidden)) * 0.05).astype(np.float32)
+    ids = np.stack([rng.permutation(count + 2)[:topk] for _ in range(tokens)]).astype(np.int32) - 1
+    wts = rng.uniform(0.1, 1.0, (tokens, topk)).astype(np.float32)
+    got = qsrt.qsrt_expert_forward(torch.from_numpy(x).to(gpu), torch.from_numpy(ids).to(gpu),
+                                   torch.from_numpy(wts).to(gpu), experts, out_dtype=torch.float32)
+    ref = oq.qsrt_expert_forward(x, ids, wts, spec, hidden, inter, _LABELS, _LABELS)
+    assert np.abs(got.cpu().numpy() - ref).max() <= 2e-5 * np.abs(ref).max()
