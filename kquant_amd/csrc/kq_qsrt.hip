@@ -430,6 +430,13 @@ __global__ __launch_bounds__(LIN_THREADS) void linear_kernel(LinArgs a, LinRecor
     xs[m][kbi * 128 + lane + 64] = v1;
   }
 
+  // the output scales of this column block, loaded now so the epilogue does
+  // not wait on memory
+  float sv0 = 1.f, sv1 = 1.f;
+  if constexpr (ROT) {
+    sv0 = a.svh[(int64_t)nb * 128 + lane] * (1.f / 128.f);
+    sv1 = a.svh[(int64_t)nb * 128 + lane + 64] * (1.f / 128.f);
+  }
   float acc[M];
 #pragma unroll
   for (int m = 0; m < M; ++m) acc[m] = 0.f;
@@ -469,8 +476,8 @@ __global__ __launch_bounds__(LIN_THREADS) void linear_kernel(LinArgs a, LinRecor
     float v1 = yb[0][m][lane + 64] + yb[1][m][lane + 64];
     if constexpr (ROT) {
       fwht128(v0, v1, lane);
-      v0 *= (1.f / 128.f) * a.svh[col0 + lane];
-      v1 *= (1.f / 128.f) * a.svh[col0 + lane + 64];
+      v0 *= sv0;
+      v1 *= sv1;
     }
     if (a.chunks == 1) {
       store_out(a.out, a.out_dtype, (m0 + m) * a.ldo + col0 + lane, v0);
@@ -653,6 +660,12 @@ __global__ __launch_bounds__(LIN_THREADS) void moe_kernel(MoeArgs a) {
     __syncthreads();
   }
 
+  // output scales of the current n block, loaded a block ahead of use
+  float sv0 = 0.f, sv1 = 0.f;
+  if (valid) {
+    sv0 = mt.svh[(int64_t)nb0 * 128 + lane] * (1.f / 128.f);
+    sv1 = mt.svh[(int64_t)nb0 * 128 + lane + 64] * (1.f / 128.f);
+  }
   float acc[1] = {0.f};
   int nbi = 0, kbi = 0;
   for (int u = 0; u < (valid ? total : nbc); ++u) {
@@ -687,8 +700,12 @@ __global__ __launch_bounds__(LIN_THREADS) void moe_kernel(MoeArgs a) {
       v0 = yb[0][lane] + yb[1][lane];
       v1 = yb[0][lane + 64] + yb[1][lane + 64];
       fwht128(v0, v1, lane);
-      v0 *= (1.f / 128.f) * mt.svh[col0 + lane];
-      v1 *= (1.f / 128.f) * mt.svh[col0 + lane + 64];
+      v0 *= sv0;
+      v1 *= sv1;
+    }
+    if (valid && nbi < nbc) {  // the next n block's scales
+      sv0 = mt.svh[col0 + 128 + lane] * (1.f / 128.f);
+      sv1 = mt.svh[col0 + 128 + lane + 64] * (1.f / 128.f);
     }
     if (!DOWN && a.chunks == 1) {
       if (wave == 0) {
