@@ -534,6 +534,131 @@ __global__ __launch_bounds__(LIN_THREADS) void linear_kernel(LinArgs a, LinRecor
 }
 
 
+// -------------------------------------------------------- fast decode --
+// kq_qsrt_decode_weight from a payload on the fused workgroup's machinery:
+// the rate's label table in LDS, every wave's 4 tiles of a 128 x 128 block
+// streamed through its LDS ring slot, the block's fp32 values in an LDS tile,
+// the two 128-point rotations as wave-level transforms over its rows and
+// columns, and coalesced stores in either orientation.  A workgroup walks a
+// chunk of k blocks of one n block (records along n share one rate).
+struct DecArgs {
+  const uint32_t* payload;
+  const uint8_t* labels;
+  const float* suh;
+  const float* svh;
+  void* out;
+  int64_t ldo;
+  int k_tiles, n_tiles, rate_n, kbw, transposed, out_dtype;
+};
+
+template <bool ROT>
+__global__ __launch_bounds__(LIN_THREADS) void decode_fast_kernel(DecArgs a, LinRecords rec) {
+  __shared__ __attribute__((aligned(16))) uint8_t lut[65536];
+  constexpr int ST = 3;  // ring stages (the fp32 tile takes the fourth's LDS)
+  __shared__ __attribute__((aligned(16))) uint32_t ring[ST][2048];  // 16 waves x 512 bytes
+  __shared__ float t[128][129];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int half = wave >> 3, ntl = wave & 7;
+  const int n_blocks = a.n_tiles >> 3, k_blocks = a.k_tiles >> 3;
+  const int nb = (int)(blockIdx.x % (unsigned)n_blocks), chunk = (int)(blockIdx.x / (unsigned)n_blocks);
+  const int kb0 = chunk * a.kbw;
+  const int kbn = min(a.kbw, k_blocks - kb0);
+  const int64_t record_dw_nb = (int64_t)RECORD_TILES * (a.rate_n ? a.k_tiles : a.n_tiles) * 8;
+
+  auto stage = [&](int kb, uint32_t* slot_stage) {
+    const int record = a.rate_n ? nb : kb;
+    stage_wave(a.payload, (int64_t)record_rates_before(rec, record) * record_dw_nb, record_rate(rec, record),
+               a.rate_n, a.n_tiles, nb, kb, slot_stage, wave, lane);
+  };
+  int lut_bits = record_rate(rec, a.rate_n ? nb : kb0);
+  stage_labels(a.labels, lut_bits, lut, wave, lane);
+#pragma unroll
+  for (int j = 0; j < ST; ++j)
+    if (j < kbn) stage(kb0 + j, ring[j]);
+  // output scales of this n block's columns (ROT), one pair per lane
+  float sv0 = 1.f, sv1 = 1.f;
+  if constexpr (ROT) {
+    sv0 = a.svh[(int64_t)nb * 128 + lane] * (1.f / 128.f);
+    sv1 = a.svh[(int64_t)nb * 128 + lane + 64] * (1.f / 128.f);
+  }
+  wait_own_stage(min(ST, kbn));  // every wave's labels
+  __syncthreads();
+
+  const int r0 = 2 * ((lane >> 1) & 3), col = ntl * 16 + (lane >> 3) + 8 * (lane & 1);
+  for (int kbi = 0; kbi < kbn; ++kbi) {
+    const int kb = kb0 + kbi;
+    const int bits = record_rate(rec, a.rate_n ? nb : kb);
+    if (bits != lut_bits) {  // the rate along k changed (uniform): restage the labels
+      __syncthreads();
+      stage_labels(a.labels, bits, lut, wave, lane);
+      __builtin_amdgcn_s_waitcnt(dma::waitcnt_vm(0));
+      __syncthreads();
+      lut_bits = bits;
+    }
+    wait_own_stage(min(ST - 1, kbn - 1 - kbi));
+    {  // this wave's 4 tiles -> the fp32 tile (rows of the k tiles, columns of n tile ntl)
+      const uint32_t* slot = ring[kbi % ST] + wave * 128;
+      int sb = (4 * lane + 1) * bits - 16;
+      if (sb < 0) sb += 256 * bits;
+      const int d0 = sb >> 5, d1 = d0 + 1 == 8 * bits ? 0 : d0 + 1, off = sb & 31, sh = 64 - (16 + 3 * bits);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t* w = slot + i * 8 * bits;
+        const uint64_t v = (((uint64_t)w[d0] << 32) | w[d1]) << off;
+        const uint32_t win = (uint32_t)(v >> sh);
+        const int row = (half * 4 + i) * 16 + r0;
+        t[row][col] = e4m3_scaled(lut[(win >> (3 * bits)) & 0xffffu]);
+        t[row + 1][col] = e4m3_scaled(lut[(win >> (2 * bits)) & 0xffffu]);
+        t[row + 8][col] = e4m3_scaled(lut[(win >> bits) & 0xffffu]);
+        t[row + 9][col] = e4m3_scaled(lut[win & 0xffffu]);
+      }
+    }
+    if (kbi + ST < kbn) stage(kb + ST, ring[kbi % ST]);
+    __syncthreads();
+    const int64_t row0 = (int64_t)kb * 128, col0 = (int64_t)nb * 128;
+    if constexpr (ROT) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {  // along the columns of every row: B_N (8 independent rows per wave)
+        const int r = wave + 16 * i;
+        float v0 = t[r][lane], v1 = t[r][lane + 64];
+        fwht128(v0, v1, lane);
+        t[r][lane] = v0 * sv0;
+        t[r][lane + 64] = v1 * sv1;
+      }
+      __syncthreads();
+      const float su0 = a.suh[row0 + lane], su1 = a.suh[row0 + lane + 64];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {  // along the rows of every column: B_K, then suh
+        const int c = wave + 16 * i;
+        float v0 = t[lane][c], v1 = t[lane + 64][c];
+        fwht128(v0, v1, lane);
+        t[lane][c] = v0 * su0;
+        t[lane + 64][c] = v1 * su1;
+      }
+      __syncthreads();
+    }
+    if (a.transposed) {  // out [N, K]: one output row (a column of the block) per wave pass
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int c = wave + 16 * i;
+        const int64_t o = (col0 + c) * a.ldo + row0;
+        store_out(a.out, a.out_dtype, o + lane, t[lane][c]);
+        store_out(a.out, a.out_dtype, o + lane + 64, t[lane + 64][c]);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int r = wave + 16 * i;
+        const int64_t o = (row0 + r) * a.ldo + col0;
+        store_out(a.out, a.out_dtype, o + lane, t[r][lane]);
+        store_out(a.out, a.out_dtype, o + lane + 64, t[r][lane + 64]);
+      }
+    }
+    __syncthreads();  // the tile is rewritten by the next block
+  }
+}
+
 // ------------------------------------------------------ routed experts --
 // The routed expert forward of a decode batch with QSRT-coded experts, as
 // two launches of the fused linear's workgroup (M = 1 row per job):
@@ -837,6 +962,31 @@ extern "C" int kq_qsrt_decode_weight(const int16_t* payload, int64_t payload_wor
   if (words != payload_words)
     return kq_fail(KQ_ERR_INVALID, "%s: payload has %lld words, the records need %lld", fn,
                    (long long)payload_words, (long long)words);
+  if (kq_misaligned(payload, 4) == false) {
+    // fast path: LDS labels and rotation (needs a 4-byte-aligned payload)
+    LinRecords lr{};
+    uint32_t sum = 0;
+    for (int64_t r = 0; r < records; ++r) {
+      if (r % 8 == 0) lr.prefix8[r / 8] = sum;
+      lr.bits[r] = rates.bits[r];
+      sum += rates.bits[r];
+    }
+    int dev = 0, cus = 0;
+    hipError_t err = hipGetDevice(&dev);
+    if (err == hipSuccess) err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (err != hipSuccess) return kq_check_launch(err, fn);
+    // k blocks per workgroup: enough workgroups to fill the device once
+    const int64_t n_blocks = n_tiles / RECORD_TILES, k_blocks = k_tiles / RECORD_TILES;
+    int64_t kbw = (n_blocks * k_blocks + (cus > 0 ? cus : 1) - 1) / (cus > 0 ? cus : 1);
+    kbw = kbw < 1 ? 1 : kbw > k_blocks ? k_blocks : kbw;
+    const int64_t chunks = (k_blocks + kbw - 1) / kbw;
+    DecArgs da{reinterpret_cast<const uint32_t*>(payload), labels, suh, svh, out, ldo, (int)k_tiles, (int)n_tiles,
+               rate_axis, (int)kbw, tr ? 1 : 0, out_dtype};
+    const dim3 grid((unsigned)(n_blocks * chunks));
+    if (suh) decode_fast_kernel<true><<<grid, LIN_THREADS, 0, (hipStream_t)stream>>>(da, lr);
+    else decode_fast_kernel<false><<<grid, LIN_THREADS, 0, (hipStream_t)stream>>>(da, lr);
+    return kq_check_launch(hipGetLastError(), fn);
+  }
   return launch_decode<false>(payload, k_tiles, n_tiles, rate_axis, rates, nullptr, labels, suh, svh, out_dtype,
                               out, ldo, tr, (hipStream_t)stream, fn);
 }

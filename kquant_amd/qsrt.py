@@ -138,7 +138,7 @@ def decode_qsrt_payload(
     if any(b not in (2, 3, 4) for b in bits):
         raise ValueError("tile_bits must contain only integer K2, K3, or K4")
     g, host = _on_gpu(payload)
-    g = N.aligned(g, 2)
+    g = N.aligned(g, 4)  # 4-byte aligned: the fast decode reads dwords
     gpu = g.device
     k, n = k_tiles * TILE_CHANNELS, n_tiles * TILE_CHANNELS
     labels = rate_labels(codebook, rate_axis=rate_axis, device=gpu)

@@ -189,7 +189,9 @@ def test_prefill_rows_take_the_decoded_bf16_path(gpu):
     xb = torch.from_numpy(x).to(torch.bfloat16).double().numpy()
     wb = torch.from_numpy(w).to(torch.bfloat16).double().numpy()
     ref_b = xb @ wb
-    assert np.all(np.abs(got - ref_b) <= np.abs(ref_b) * 2.0 ** -8 + 1e-5 * np.abs(ref_b).max())
+    # bf16 output rounding, plus weights whose fp32 decode sits next to a bf16
+    # rounding boundary and rounds the other way (a 1-ulp weight change)
+    assert np.all(np.abs(got - ref_b) <= np.abs(ref_b) * 2.0 ** -8 + 2.0 ** -10 * np.abs(ref_b).max())
     exact = x.astype(np.float64) @ w
     assert np.abs(got - exact).max() <= 2e-2 * np.abs(exact).max()
 
