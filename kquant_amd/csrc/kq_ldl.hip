@@ -29,6 +29,7 @@ namespace kq {
 namespace ldl {
 
 using kq::had::fwht_lines;
+using kq::had::fwht128;
 using kq::had::HAD;
 using kq::had::HLD;
 
@@ -70,30 +71,81 @@ __global__ __launch_bounds__(256) void regularize_kernel(float* __restrict__ h, 
 // --------------------------------------------------------------- rotation --
 // sides: bit 0 = left (B X: each column of a tile transformed), bit 1 = right
 // (X B: each row).  Row / column scales (or none) apply before the transforms.
-__global__ __launch_bounds__(256) void hadamard_kernel(float* __restrict__ x, int64_t rows, int64_t cols,
-                                                       int64_t ld, int64_t stride, int sides,
-                                                       const float* __restrict__ rs,
-                                                       const float* __restrict__ cs, float post) {
+__global__ __launch_bounds__(1024) void hadamard_kernel(float* __restrict__ x, int64_t rows, int64_t cols,
+                                                        int64_t ld, int64_t stride, int sides,
+                                                        const float* __restrict__ rs,
+                                                        const float* __restrict__ cs, float post, int vec) {
+  // one 128 x 128 block per workgroup: 16-byte loads (vec: ld and the block
+  // 16-byte aligned) or single ones at ragged edges, both scales at load,
+  // then 8 independent lines per wave per direction with the wave-level
+  // transform, and the post scale at store
   __shared__ float t[HAD][HLD];
   float* X = x + (int64_t)blockIdx.z * stride;
   const int64_t r0 = (int64_t)blockIdx.y * HAD, c0 = (int64_t)blockIdx.x * HAD;
-  const int tid = threadIdx.x;
-  for (int i = tid; i < HAD * HAD; i += 256) {
-    const int r = i >> 7, c = i & (HAD - 1);
-    float v = 0.f;
-    if (r0 + r < rows && c0 + c < cols) {
-      v = X[(r0 + r) * ld + c0 + c];
-      if (rs) v *= rs[r0 + r];
-      if (cs) v *= cs[c0 + c];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const bool full = vec && r0 + HAD <= rows && c0 + HAD <= cols;
+  if (full) {
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      const int i = tid + 1024 * it, r = i >> 5, c = (i & 31) * 4;
+      float4 v = *reinterpret_cast<const float4*>(X + (r0 + r) * ld + c0 + c);
+      if (rs) {
+        const float s = rs[r0 + r];
+        v.x *= s; v.y *= s; v.z *= s; v.w *= s;
+      }
+      if (cs) {
+        const float4 s = *reinterpret_cast<const float4*>(cs + c0 + c);
+        v.x *= s.x; v.y *= s.y; v.z *= s.z; v.w *= s.w;
+      }
+      t[r][c] = v.x; t[r][c + 1] = v.y; t[r][c + 2] = v.z; t[r][c + 3] = v.w;
     }
-    t[r][c] = v;
+  } else {
+    for (int i = tid; i < HAD * HAD; i += 1024) {
+      const int r = i >> 7, c = i & (HAD - 1);
+      float v = 0.f;
+      if (r0 + r < rows && c0 + c < cols) {
+        v = X[(r0 + r) * ld + c0 + c];
+        if (rs) v *= rs[r0 + r];
+        if (cs) v *= cs[c0 + c];
+      }
+      t[r][c] = v;
+    }
   }
   __syncthreads();
-  if (sides & 2) fwht_lines<true>(t);
-  if (sides & 1) fwht_lines<false>(t);
-  for (int i = tid; i < HAD * HAD; i += 256) {
-    const int r = i >> 7, c = i & (HAD - 1);
-    if (r0 + r < rows && c0 + c < cols) X[(r0 + r) * ld + c0 + c] = t[r][c] * post;
+  if (sides & 2) {  // every row
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int r = wave + 16 * i;
+      float v0 = t[r][lane], v1 = t[r][lane + 64];
+      fwht128(v0, v1, lane);
+      t[r][lane] = v0;
+      t[r][lane + 64] = v1;
+    }
+    __syncthreads();
+  }
+  if (sides & 1) {  // every column
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int c = wave + 16 * i;
+      float v0 = t[lane][c], v1 = t[lane + 64][c];
+      fwht128(v0, v1, lane);
+      t[lane][c] = v0;
+      t[lane + 64][c] = v1;
+    }
+    __syncthreads();
+  }
+  if (full) {
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      const int i = tid + 1024 * it, r = i >> 5, c = (i & 31) * 4;
+      const float4 v = {t[r][c] * post, t[r][c + 1] * post, t[r][c + 2] * post, t[r][c + 3] * post};
+      *reinterpret_cast<float4*>(X + (r0 + r) * ld + c0 + c) = v;
+    }
+  } else {
+    for (int i = tid; i < HAD * HAD; i += 1024) {
+      const int r = i >> 7, c = i & (HAD - 1);
+      if (r0 + r < rows && c0 + c < cols) X[(r0 + r) * ld + c0 + c] = t[r][c] * post;
+    }
   }
 }
 
@@ -379,8 +431,10 @@ extern "C" int kq_blockwise_hadamard(float* x, int64_t rows, int64_t cols, int64
     return kq_fail(KQ_ERR_LIMIT, "kq_blockwise_hadamard: too many blocks");
   const float post = sides == 3 ? 1.f / 128.f : 0.08838834764831845f;  // 1/128, fl(1/sqrt(128))
   const dim3 grid((unsigned)((cols + HAD - 1) / HAD), (unsigned)((rows + HAD - 1) / HAD), (unsigned)batch);
-  hadamard_kernel<<<grid, 256, 0, (hipStream_t)stream>>>(x, rows, cols, ld, stride, sides, row_scale, col_scale,
-                                                         post);
+  const int vec = !kq_misaligned(x, 16) && ld % 4 == 0 && (batch == 1 || stride % 4 == 0) &&
+                  !kq_misaligned(col_scale, 16);
+  hadamard_kernel<<<grid, 1024, 0, (hipStream_t)stream>>>(x, rows, cols, ld, stride, sides, row_scale, col_scale,
+                                                         post, vec);
   return kq_check_launch(hipGetLastError(), "kq_blockwise_hadamard");
 }
 
