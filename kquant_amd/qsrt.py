@@ -83,8 +83,10 @@ def unpack_trellis_states(packed: torch.Tensor, bits: int) -> torch.Tensor:
     return _unpack(packed, bits, True)
 
 
-# rows up to which qsrt_linear runs the fused kernel (decode batches)
-FUSED_MAX_ROWS = 64
+# rows up to which qsrt_linear runs the fused kernel (decode batches): it
+# decodes the weight once per 16 rows, so past two row groups the one-time
+# decode (about 35 us for a K3 3584 x 3072 matrix) plus a bf16 GEMM is faster
+FUSED_MAX_ROWS = 32
 
 _LABELS: dict[tuple[str, str | None, torch.device], torch.Tensor] = {}
 _LINEAR_WORKSPACES: dict[tuple, torch.Tensor] = {}
