@@ -217,3 +217,22 @@ def test_block_ldl_batched(gpu):
     for e in range(experts):
         if e != 3:
             assert _rel(ldl.block_ldl(a[e], 16), got[e]) <= 1e-4
+
+
+@pytest.mark.parametrize("ld", [260, 257])
+def test_hadamard_ragged_rows_and_row_strides(gpu, ld):
+    """Right-side rotation of a [200, 256] matrix inside a wider buffer: the
+    last row block is ragged (single-element path), ld = 260 keeps 16-byte
+    rows (vector path for full blocks), ld = 257 does not (single-element
+    path throughout); padding columns stay untouched."""
+    rng = np.random.default_rng(ld)
+    rows, cols = 200, 256
+    buf = rng.standard_normal((rows, ld)).astype(np.float32)
+    cs = rng.uniform(0.5, 1.5, cols).astype(np.float32)
+    t = torch.from_numpy(buf).to(gpu)
+    cst = torch.from_numpy(cs).to(gpu)
+    N.call("kq_blockwise_hadamard", N.ptr(t), rows, cols, ld, 1, 0, 2, None, N.ptr(cst), N.stream(gpu))
+    got = t.cpu().numpy()
+    ref = ldl.blockwise_hadamard(buf[:, :cols], 2, None, cs)
+    assert np.abs(got[:, :cols] - ref).max() <= 2e-6 * np.abs(ref).max()
+    assert np.array_equal(got[:, cols:], buf[:, cols:])
