@@ -110,3 +110,33 @@ def test_dropin_reference_decoders(gpu):
     assert np.array_equal(xr.reconstruct_trellis_states(edges.to(gpu), 3).cpu().numpy(),
                           oq.reconstruct_trellis_states(edges.numpy(), 3))
     assert torch.equal(xr.tensor_core_permutation(), torch.from_numpy(oq.tensor_core_permutation()))
+
+
+def test_payload_decode_paths_agree(gpu):
+    """A 4-byte-aligned payload takes the LDS decode, a 2-byte-aligned one the
+    first kernel: the regularized weights agree bit for bit, the rotated ones
+    to fp32 rounding."""
+    from kquant_amd import _native as N
+
+    k_tiles, n_tiles, record_bits = 16, 24, (2, 4, 3)
+    _, payload = _random_matrix(k_tiles, n_tiles, "n", record_bits, 17)
+    buf = torch.zeros(payload.size + 2, dtype=torch.int16, device=gpu)
+    buf[1:1 + payload.size] = torch.from_numpy(payload).to(gpu)
+    odd = buf[1:1 + payload.size]  # 2-byte aligned
+    even = torch.from_numpy(payload).to(gpu)
+    assert odd.data_ptr() % 4 == 2 and even.data_ptr() % 4 == 0
+    labels = qsrt.rate_labels(rate_axis="n", device=gpu)
+    rng = np.random.default_rng(18)
+    suh = torch.from_numpy(rng.choice([-1.0, 1.0], k_tiles * 16).astype(np.float32)).to(gpu)
+    svh = torch.from_numpy(rng.uniform(0.5, 2.0, n_tiles * 16).astype(np.float32)).to(gpu)
+    outs = {}
+    for name, p in (("odd", odd), ("even", even)):
+        for rot in (False, True):
+            out = torch.empty(k_tiles * 16, n_tiles * 16, device=gpu)
+            N.call("kq_qsrt_decode_weight", N.ptr(p), p.numel(), k_tiles, n_tiles, 1, bytes(record_bits),
+                   N.ptr(labels), N.ptr(suh) if rot else None, N.ptr(svh) if rot else None, N.DT_F32, N.ptr(out),
+                   n_tiles * 16, 0, N.stream(gpu))
+            outs[name, rot] = out.cpu().numpy()
+    assert np.array_equal(outs["odd", False], outs["even", False])
+    ref = outs["even", True]
+    assert np.abs(outs["odd", True] - ref).max() <= 2e-6 * np.abs(ref).max()
