@@ -189,6 +189,27 @@ int kq_moe_forward_x4t(int activation, float act_beta, float act_linear_beta,
                        const uint32_t* w2_tile_index, int out_dtype, void* out,
                        void* workspace, int64_t workspace_bytes, uint32_t flags, void* stream);
 
+/* Size of the device array kq_moe_forward_noalloc uses as its workspace. */
+#define KQ_MOE_NOALLOC_SCRATCH_BYTES (16ll << 20)
+
+/* kq_moe_forward without a workspace argument: the forward runs in a
+ * 16 MiB device array of this library (one per GPU, held until the process
+ * ends), so the call allocates nothing.  No counterpart in kquant: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * serving loops that forbid hipMalloc).  Same arguments (minus the workspace),
+ * flags and results, bit for bit, as kq_moe_forward.  Sizes whose
+ * kq_moe_workspace_size exceeds KQ_MOE_NOALLOC_SCRATCH_BYTES fail with
+ * KQ_ERR_LIMIT (at hidden 7168, intermediate 2048: up to 256 routed pairs,
+ * e.g. 32 decode tokens at top-8).  The array keeps the last call's contents;
+ * calls that overlap on one GPU (concurrent streams or threads) share it and
+ * race, so the caller serializes them. */
+int kq_moe_forward_noalloc(int activation, float act_beta, float act_linear_beta,
+                           const void* x, int64_t ldx, int64_t tokens, int64_t hidden,
+                           const int32_t* route_ids, const float* route_weights, int topk,
+                           int experts, int64_t inter, const uint8_t* w13_t,
+                           const uint8_t* w13_st, const uint8_t* w2_t, const uint8_t* w2_st,
+                           int out_dtype, void* out, uint32_t flags, void* stream);
+
 /* --------------------------------------------------------- dense linear -- */
 
 /* C [m, n] = A [m, k] (bf16, row stride lda) x dequant(W)^T, W [n, k] in

@@ -38,6 +38,7 @@ MOE_ACT_MXFP8 = 2
 MOE_ACT_MXFP4 = 4
 ACT_SITU = 0
 ACT_SWIGLU = 1
+MOE_NOALLOC_SCRATCH_BYTES = 16 << 20  # KQ_MOE_NOALLOC_SCRATCH_BYTES
 
 DTYPE_CODES = {torch.bfloat16: DT_BF16, torch.float16: DT_F16, torch.float32: DT_F32}
 
@@ -67,6 +68,8 @@ SIGNATURES: dict[str, list] = {
     "kq_x4t_emit_exceptions": [_VP, _I64, _I64, _I64, _VP, _VP, _VP, _VP],
     "kq_x4t_decode": [_VP, _VP, _I64, _VP, _I64, _I64, _I64, _VP, _VP, _VP],
     "kq_x4t_tile_index": [_VP, _I64, _VP, _I64, _I64, _I64, _VP, _VP],
+    "kq_moe_forward_noalloc": [_INT, _F32, _F32, _VP, _I64, _I64, _I64, _VP, _VP, _INT, _INT, _I64,
+                               _VP, _VP, _VP, _VP, _INT, _VP, _U32, _VP],
     "kq_moe_forward_x4t": [_INT, _F32, _F32, _VP, _I64, _I64, _I64, _VP, _VP, _INT, _INT, _I64,
                            _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _INT, _VP, _VP,
                            _I64, _U32, _VP],

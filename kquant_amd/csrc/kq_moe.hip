@@ -25,6 +25,8 @@
 #include "kq_internal.h"
 #include "kq_act.h"
 
+#include <mutex>
+
 namespace kq {
 namespace moe {
 
@@ -2012,6 +2014,75 @@ extern "C" int kq_moe_forward_x4t(int activation, float act_beta, float act_line
   return moe_forward_impl(fn, activation, act_beta, act_linear_beta, x, ldx, tokens, hidden, route_ids,
                           route_weights, topk, experts, inter, w13_t, nullptr, w2_t, nullptr, &xa,
                           out_dtype, out, workspace, workspace_bytes, flags, stream);
+}
+
+// ------------------------------------------------- allocation-free forward --
+// kq_moe_forward with its workspace in this library's own device array, for
+// callers that cannot allocate (code under HIP graph capture, serving loops).
+// Each GPU holds one copy of the array, at its own address, until the process
+// ends.  The forward writes every workspace entry before reading it (routing
+// lists, intermediates, pair rows), so the previous call's contents need no
+// clearing; calls that overlap on one GPU share the array and race.
+static __device__ __align__(256) unsigned char scratch[KQ_MOE_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int SCRATCH_DEVICES = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[SCRATCH_DEVICES];  // device address of `scratch`, per device
+}  // namespace
+
+// The address of `scratch` on the device that owns `stream` (the current
+// device for the null stream), looked up once per device with that device
+// current.
+static int scratch_for_stream(const char* fn, void* stream, void** out) {
+  int dev = -1;
+  hipError_t e = stream ? hipStreamGetDevice((hipStream_t)stream, &dev) : hipGetDevice(&dev);
+  if (e != hipSuccess) return kq_check_launch(e, fn);
+  if (dev < 0 || dev >= SCRATCH_DEVICES) return kq_fail(KQ_ERR_LIMIT, "%s: device %d out of range", fn, dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    int cur = -1;
+    if ((e = hipGetDevice(&cur)) != hipSuccess) return kq_check_launch(e, fn);
+    if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess) return kq_check_launch(e, fn);
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (cur != dev) {
+      const hipError_t r = hipSetDevice(cur);
+      if (e == hipSuccess) e = r;
+    }
+    if (e != hipSuccess) return kq_check_launch(e, fn);
+    if (!p || kq_misaligned(p, 256)) return kq_fail(KQ_ERR_HIP, "%s: bad scratch address", fn);
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return KQ_OK;
+}
+
+extern "C" int kq_moe_forward_noalloc(int activation, float act_beta, float act_linear_beta,
+                                      const void* x, int64_t ldx, int64_t tokens, int64_t hidden,
+                                      const int32_t* route_ids, const float* route_weights, int topk,
+                                      int experts, int64_t inter, const uint8_t* w13_t,
+                                      const uint8_t* w13_st, const uint8_t* w2_t, const uint8_t* w2_st,
+                                      int out_dtype, void* out, uint32_t flags, void* stream) {
+  const char* fn = "kq_moe_forward_noalloc";
+  if (!w13_st || !w2_st) return kq_fail(KQ_ERR_INVALID, "%s: null scale tiles", fn);
+  // sizes the forward itself accepts are priced here; the others reach its
+  // own argument checks below
+  if (tokens >= 0 && topk > 0 && topk <= 64 && experts > 0 && experts <= MAX_EXPERTS && hidden > 0 &&
+      inter > 0 && hidden <= (1 << 20) && inter <= (1 << 20) && tokens <= INT32_MAX / 2 / topk) {
+    const int64_t need = (int64_t)make_layout(tokens, topk, experts, hidden, inter).total;
+    if (need > KQ_MOE_NOALLOC_SCRATCH_BYTES)
+      return kq_fail(KQ_ERR_LIMIT,
+                     "%s: %lld tokens x top-%d need %lld bytes of workspace, more than the %lld-byte "
+                     "scratch array; use kq_moe_forward with a caller workspace", fn, (long long)tokens,
+                     topk, (long long)need, (long long)KQ_MOE_NOALLOC_SCRATCH_BYTES);
+  }
+  void* ws = nullptr;
+  const int rc = scratch_for_stream(fn, stream, &ws);
+  if (rc != KQ_OK) return rc;
+  return moe_forward_impl(fn, activation, act_beta, act_linear_beta, x, ldx, tokens, hidden, route_ids,
+                          route_weights, topk, experts, inter, w13_t, w13_st, w2_t, w2_st, nullptr,
+                          out_dtype, out, ws, KQ_MOE_NOALLOC_SCRATCH_BYTES, flags, stream);
 }
 
 // Routing sort alone (for per-expert calibration statistics): the pairs
