@@ -3,15 +3,20 @@
 
 Prints ONE JSON line.  The headline (``value``) is benchmark configuration 2's
 MXFP8 weight quantization: W [12288, 7168] bf16 -> E4M3 codes + E8M0 scales;
-a step is one quantization of that weight, inputs resident in HBM.  The
+a step is one quantization of that weight, inputs resident in HBM and cold:
+the steps take four copies of the weight and its outputs in turn (1.07 GB,
+four times the Infinity Cache), and the warm figure is reported beside it.  The
 second half of the metric, the MXFP4 expert GEMM TFLOP/s, is the configuration
 3 grouped MoE prefill (``moe_prefill``).  Every other configuration is
 reported beside it with its own roofline fraction (``configs``).
 
 Rooflines use MI355X published peaks: HBM 8 TB/s; dense MFMA bf16 2.5 PF/s,
 fp4 10.1 PF/s.  Kernel durations come from HIP events on the stream the
-kernels run on (torch's current stream).  ``traffic`` (measured HBM bytes per
-launch) is read from the committed rocprof PMC summary when one exists.
+kernels run on (torch's current stream).  ``traffic`` (bytes per launch
+between the L2 and the fabric) is read from the committed rocprofv3 PMC
+summaries, profiles/traffic_<section>.json (``--summarize-pmc`` writes them).
+Each configuration carries a ``cpu_baseline``: the reference's CPU path
+(oracle/torch_ref.py) on a stated sample, on every CPU the process may use.
 """
 
 from __future__ import annotations
@@ -43,9 +48,22 @@ def _args():
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--quick", action="store_true", help="headline only (skip the other configs)")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-warm", action="store_true",
+                   help="skip the warm repeat of the headline (a rocprofv3 --stats run then averages cold launches only)")
     p.add_argument("--only", default="", help="comma list of sections to run (profiling)")
     p.add_argument("--copy-calibration", action="store_true",
                    help="run only a plain device copy of 1 GiB (PMC byte calibration)")
+    p.add_argument("--calibrate-first", action="store_true",
+                   help="start with three plain 1 GiB device copies, so that a rocprofv3 --pmc run of "
+                        "a section also holds the byte calibration of its counters")
+    p.add_argument("--summarize-pmc", nargs="+", metavar="DIR",
+                   help="summarize rocprofv3 --pmc databases (FETCH_SIZE; WRITE_SIZE, TCC_HIT_sum, "
+                        "TCC_MISS_sum) of one bench section into profiles/traffic_<section>.json")
+    p.add_argument("--summarize-stats", nargs="+", metavar="DIR",
+                   help="print the per-kernel table (calls, average and total time) of rocprofv3 "
+                        "--kernel-trace --stats databases as markdown")
+    p.add_argument("--section", default="", help="section name for --summarize-pmc")
+    p.add_argument("--summary-dir", default=str(ROOT / "profiles"), help="where --summarize-pmc writes")
     return p.parse_args()
 
 
@@ -88,30 +106,177 @@ def _bound(N, name: str, *args):
     return run
 
 
-def _traffic(name: str):
-    path = ROOT / "profiles" / f"{name}_traffic.json"
-    if path.exists():
-        try:
-            return json.loads(path.read_text()).get("bytes_per_launch")
-        except (OSError, ValueError):
-            return None
-    return None
-
-
-def _roofline(bound: str, achieved: float, traffic_name: str | None = None):
-    peak = HBM_PEAK_GBS if bound == "hbm" else BF16_PEAK_TFLOPS
+def _roofline(bound: str, achieved: float, pmc: dict | None = None, peak: float | None = None):
+    if peak is None:
+        peak = HBM_PEAK_GBS if bound == "hbm" else BF16_PEAK_TFLOPS
     return {
         "bound": bound,
         "achieved": round(achieved, 2),
         "peak": peak,
         "unit": "GB/s" if bound == "hbm" else "TFLOP/s",
         "frac": round(achieved / peak, 4),
-        "traffic": _traffic(traffic_name) if traffic_name else None,
+        "traffic": None if pmc is None else pmc["bytes_per_launch"],
     }
+
+
+COPY_KERNEL = "__amd_rocclr_copyBuffer"
+CALIBRATION_BYTES = 1 << 30
+
+
+def _short_kernel(name: str) -> str:
+    import re
+
+    name = re.sub(r"^void ", "", name).replace("(anonymous namespace)::", "")
+    depth, out = 0, []
+    for ch in name:  # drop the argument list, keep template arguments
+        if ch == "(" and depth == 0:
+            break
+        depth += ch == "<"
+        depth -= ch == ">"
+        out.append(ch)
+    return "".join(out)
+
+
+def summarize_pmc(dirs: list[str], section: str, out_dir: str) -> int:
+    """Per-kernel PMC averages of a section's rocprofv3 databases, scaled to
+    bytes by the 1 GiB copy the same runs made (--calibrate-first), into
+    profiles/traffic_<section>.json.  FETCH_SIZE and WRITE_SIZE are counted
+    at the L2's fabric side: traffic the Infinity Cache serves is included."""
+    import sqlite3
+
+    per: dict[tuple[str, int], dict[str, list[float]]] = {}
+    for d in dirs:
+        for db in sorted(Path(d).rglob("*.db")):
+            con = sqlite3.connect(str(db))
+            for name, grid, counter, value in con.execute(
+                    "select kernel_name, grid_size, counter_name, value from counters_collection"):
+                per.setdefault((_short_kernel(name), int(grid)), {}).setdefault(counter, []).append(float(value))
+    copy = {k: v for k, v in per.items() if k[0].startswith(COPY_KERNEL)}
+    if not copy:
+        print("no calibration copy in the databases (run the section with --calibrate-first)", file=sys.stderr)
+        return 1
+    def mean(v):
+        return sum(v) / len(v) if v else None
+
+    # the 1 GiB copy is the copy dispatch that moves the most bytes (smaller
+    # copies of the run may share its kernel and grid)
+    ref = {c: [max(max(v.get(c, [0.0])) for v in copy.values())] for c in ("FETCH_SIZE", "WRITE_SIZE")}
+    kib = CALIBRATION_BYTES / 1024
+
+    fetch_scale = kib / mean(ref["FETCH_SIZE"])
+    write_scale = kib / mean(ref["WRITE_SIZE"])
+    kernels = []
+    for (name, grid), c in sorted(per.items()):
+        if name.startswith(COPY_KERNEL):
+            continue
+        f, w = mean(c.get("FETCH_SIZE", [])), mean(c.get("WRITE_SIZE", []))
+        hit, miss = mean(c.get("TCC_HIT_sum", [])), mean(c.get("TCC_MISS_sum", []))
+        kernels.append({
+            "kernel": name, "grid_size": grid, "dispatches": len(c.get("FETCH_SIZE", [])),
+            "fetch_kib_raw": None if f is None else round(f, 1),
+            "write_kib_raw": None if w is None else round(w, 1),
+            "bytes_per_launch": None if f is None or w is None else
+            int(round((f * fetch_scale + w * write_scale) * 1024)),
+            "fetch_bytes": None if f is None else int(round(f * fetch_scale * 1024)),
+            "write_bytes": None if w is None else int(round(w * write_scale * 1024)),
+            "l2_hit_rate": None if hit is None or miss is None or hit + miss == 0 else round(hit / (hit + miss), 4),
+        })
+    out = {
+        "section": section,
+        "calibration": {"copy_bytes": CALIBRATION_BYTES, "copy_fetch_kib_raw": round(mean(ref["FETCH_SIZE"]), 1),
+                        "copy_write_kib_raw": round(mean(ref["WRITE_SIZE"]), 1),
+                        "fetch_scale": round(fetch_scale, 4), "write_scale": round(write_scale, 4)},
+        "commands": [
+            f"rocprofv3 --kernel-include-regex 'kq::|copyBuffer' --pmc FETCH_SIZE -d gpurun_out/pmc_{section}_F "
+            f"-o p -- python bench.py --only "
+            f"{section} --steps 5 --warmup 1 --no-cpu-baseline --calibrate-first",
+            f"rocprofv3 --kernel-include-regex 'kq::|copyBuffer' --pmc WRITE_SIZE TCC_HIT_sum TCC_MISS_sum "
+            f"-d gpurun_out/pmc_{section}_W -o p -- "
+            f"python bench.py --only {section} --steps 5 --warmup 1 --no-cpu-baseline --calibrate-first",
+            f"python bench.py --summarize-pmc gpurun_out/pmc_{section}_F gpurun_out/pmc_{section}_W "
+            f"--section {section}",
+        ],
+        "note": "FETCH_SIZE / WRITE_SIZE count L2-to-fabric traffic (Infinity Cache hits included); "
+                "bytes = counter KiB x the factor that maps the 1 GiB copy to 1 GiB",
+        "kernels": kernels,
+    }
+    path = Path(out_dir) / f"traffic_{section}.json"
+    path.write_text(json.dumps(out, indent=1) + "\n")
+    print(f"wrote {path} ({len(kernels)} kernels)")
+    return 0
+
+
+def summarize_stats(dirs: list[str]) -> int:
+    """Markdown table of the top_kernels view of rocprofv3 databases."""
+    import sqlite3
+
+    rows = []
+    for d in dirs:
+        for db in sorted(Path(d).rglob("*.db")):
+            con = sqlite3.connect(str(db))
+            rows += con.execute("select name, total_calls, total_duration, average, percentage "
+                                "from top_kernels").fetchall()
+    print("| kernel | calls | average (us) | total (us) | % |\n|---|---:|---:|---:|---:|")
+    for name, calls, total, avg, pct in sorted(rows, key=lambda r: -r[2]):
+        print(f"| `{_short_kernel(name)}` | {calls} | {avg:.3f} | {total:.1f} | {pct:.2f} |")
+    return 0
+
+
+def _measured(section: str, kernel_prefix: str, pick: str = "max_bytes"):
+    """The PMC entry of a kernel in profiles/traffic_<section>.json (the
+    instance with the most bytes per launch when several grids ran)."""
+    path = ROOT / "profiles" / f"traffic_{section}.json"
+    try:
+        data = json.loads(path.read_text())
+    except (OSError, ValueError):
+        return None
+    hits = [k for k in data.get("kernels", []) if k["kernel"].startswith(kernel_prefix)
+            and k.get("bytes_per_launch") is not None]
+    if not hits:
+        return None
+    return max(hits, key=lambda k: k["bytes_per_launch"])
+
+
+def _traffic_entry(section: str, kernel_prefix: str, algorithmic: float):
+    m = _measured(section, kernel_prefix)
+    if m is None:
+        return None
+    return {"kernel": m["kernel"], "bytes_per_launch": m["bytes_per_launch"], "algorithmic_bytes": int(algorithmic),
+            "ratio": round(m["bytes_per_launch"] / algorithmic, 3), "l2_hit_rate": m["l2_hit_rate"],
+            "source": f"profiles/traffic_{section}.json"}
+
+
+def _cpu_env(torch) -> dict:
+    """All CPUs this process may run on: their count, and the host's model string."""
+    affinity = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    model = platform.processor() or platform.machine()
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    torch.set_num_threads(affinity)
+    return {"cores": torch.get_num_threads(), "os_cpu_count": os.cpu_count(), "affinity": affinity, "cpu": model}
+
+
+def _cpu_median(fn, reps: int = 3) -> float:
+    fn()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times)
 
 
 def main() -> int:
     args = _args()
+    if args.summarize_stats:
+        return summarize_stats(args.summarize_stats)
+    if args.summarize_pmc:
+        return summarize_pmc(args.summarize_pmc, args.section or "section", args.summary_dir)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
               "(this build has no multi-GPU path)", file=sys.stderr)
@@ -141,32 +306,69 @@ def main() -> int:
         print(json.dumps({"copy_calibration_bytes": 1 << 30, "launches": 5}))
         return 0
 
+    if args.calibrate_first:
+        src = torch.empty(CALIBRATION_BYTES, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
     stream = N.stream(dev)
     result = {}
 
     # ---------------------------------------------------------- headline --
+    # Cold: each step quantizes the next of COLD_SETS copies of the weight
+    # into its own outputs (1.07 GB in all, four times the 256 MB Infinity
+    # Cache), so no launch finds its bytes cached by the launches before it.
+    # Warm (reported beside it): the same buffers every step.
+    COLD_SETS = 4
     w2 = workloads.cfg2_weight().to(dev)
     rows, cols = w2.shape
-    q8 = torch.empty(rows, cols, dtype=torch.uint8, device=dev)
-    s8 = torch.empty(rows, cols // 32, dtype=torch.uint8, device=dev)
     quant_bytes = rows * cols * 2 + rows * cols + rows * cols // 32
+    sets = []
+    for i in range(COLD_SETS):
+        src = w2 if i == 0 else w2.clone()
+        sets.append((src, torch.empty(rows, cols, dtype=torch.uint8, device=dev),
+                     torch.empty(rows, cols // 32, dtype=torch.uint8, device=dev)))
+    q8, s8 = sets[0][1], sets[0][2]
+    steps_q = [_bound(N, "kq_mx_quantize", N.FMT_MXFP8_E4M3, N.DT_BF16, N.ptr(a), cols, rows, cols,
+                      N.ptr(q), N.ptr(sc), 0, stream) for a, q, sc in sets]
+    quantize_step = steps_q[0]
+    turn = [0]
 
-    quantize_step = _bound(N, "kq_mx_quantize", N.FMT_MXFP8_E4M3, N.DT_BF16, N.ptr(w2), cols, rows, cols,
-                           N.ptr(q8), N.ptr(s8), 0, stream)
+    def quantize_cold_step():
+        steps_q[turn[0] % COLD_SETS]()
+        turn[0] += 1
 
-    t_quant = _time_loop(torch, quantize_step, args.steps, args.warmup) if want("quantize") else float("nan")
+    if want("quantize"):
+        t_quant = _time_loop(torch, quantize_cold_step, args.steps, args.warmup)
+        t_warm = float("nan") if args.no_warm else _time_loop(torch, quantize_step, args.steps, args.warmup)
+    else:
+        t_quant = t_warm = float("nan")
     quant_gbs = quant_bytes / t_quant / 1e9
     if want("quantize"):
         # what a plain device copy of the same weight reaches on this box (read + write)
         copy_dst = torch.empty_like(w2)
-        t_copy = _time_loop(torch, lambda: copy_dst.copy_(w2), args.steps, args.warmup)
+        t_copy = float("nan") if args.no_warm else _time_loop(torch, lambda: copy_dst.copy_(w2), args.steps,
+                                                                args.warmup)
         copy_gbs = 2 * w2.numel() * w2.element_size() / t_copy / 1e9
+        result["cfg2_mxfp8_quantize"] = {
+            "cold_sets": COLD_SETS,
+            "cold_footprint_bytes": COLD_SETS * quant_bytes,
+            "cold_gbs": round(quant_gbs, 1),
+            "cold_us": round(t_quant * 1e6, 2),
+            "warm_gbs": round(quant_bytes / t_warm / 1e9, 1),
+            "warm_us": round(t_warm * 1e6, 2),
+            "note": "value is the cold figure; warm re-quantizes one 267 MB buffer set every step",
+        }
         result["hbm_copy_reference"] = {
             "what": "torch device copy of the cfg2 bf16 weight (176 MB read + 176 MB written)",
             "gbs": round(copy_gbs, 1),
-            "quantize_over_copy": round(quant_gbs / copy_gbs, 3),
+            "quantize_cold_over_copy": round(quant_gbs / copy_gbs, 3),
         }
         del copy_dst
+    del sets[1:]
 
     # ---------------------------------------------- config 2 GEMM (A16) --
     if not args.quick and want("linear"):
@@ -180,11 +382,14 @@ def main() -> int:
         quantize_step()
         t_gemm = _time_loop(torch, gemm_step, max(5, args.steps // 5), 3, 0.3)
         flops = 2.0 * x2.shape[0] * rows * cols
+        lin_bytes = x2.numel() * 2 + rows * cols + rows * cols // 32 + out2.numel() * 2
+        lin_pmc = _traffic_entry("linear", "kq::mx_linear_dma_kernel<0, 0>", lin_bytes)
         result["cfg2_mxfp8_linear"] = {
             "workload": "X[4096x7168] bf16 @ dequant(MXFP8 W[12288x7168])^T -> bf16, fp32 accumulate",
             "tflops": round(flops / t_gemm / 1e12, 1),
             "us": round(t_gemm * 1e6, 1),
-            "roofline": _roofline("mfma", flops / t_gemm / 1e12, "mx_linear_cfg2"),
+            "roofline": _roofline("mfma", flops / t_gemm / 1e12, lin_pmc),
+            "pmc": lin_pmc,
         }
         del x2, out2
 
@@ -207,6 +412,25 @@ def main() -> int:
         t_moe = _time_loop(torch, moe_step, max(3, args.steps // 10), 2, 0.3)
         flops = workloads.moe_flops(ids.numel())
         tflops = flops / t_moe / 1e12
+        # algorithmic bytes of each kernel: every operand byte once (gathered
+        # token rows once per routed pair)
+        cnt = torch.bincount(ids.flatten().long(), minlength=workloads.EXPERTS)
+        big = cnt > 16
+        p_l, e_l = int(cnt[big].sum()), int(big.sum())
+        H, I = workloads.HIDDEN, workloads.INTER
+        w13_b, w2_b = 2 * I * H // 2 + 2 * I * H // 32, H * I // 2 + H * I // 32
+        moe_pmc = {
+            "gateup_grouped": _traffic_entry("moe_prefill", "kq::moe::moe_large_dma_kernel<true>",
+                                             p_l * H * 2 + e_l * w13_b + p_l * I * 2),
+            "down_grouped": _traffic_entry("moe_prefill", "kq::moe::moe_large_dma_kernel<false>",
+                                           p_l * I * 2 + e_l * w2_b + p_l * H * 4),
+            "combine": _traffic_entry("moe_prefill", "kq::moe::moe_combine_kernel",
+                                      ids.numel() * (H * 4 + 8) + 8192 * H * 4),
+            "gateup_grouped_w4a4": _traffic_entry("moe_prefill", "kq::moe::moe_large_mx_kernel<true, 4>",
+                                                  p_l * (H // 2 + H // 32) + e_l * w13_b + p_l * I * 2),
+            "down_grouped_w4a4": _traffic_entry("moe_prefill", "kq::moe::moe_large_mx_kernel<false, 4>",
+                                                p_l * (I // 2 + I // 32) + e_l * w2_b + p_l * H * 4),
+        }
         wbytes = len(active) * workloads.bytes_per_expert()
         moe_result = {
             "workload": "cfg3: 8192 tok, top-8 Zipf(1.1) over 384 experts, H=7168 I=2048, "
@@ -215,7 +439,8 @@ def main() -> int:
             "ms": round(t_moe * 1e3, 3),
             "active_experts": len(active),
             "weight_bytes": wbytes,
-            "roofline": _roofline("mfma", tflops, "moe_prefill_cfg3"),
+            "roofline": _roofline("mfma", tflops, moe_pmc.get("gateup_grouped")),
+            "pmc": moe_pmc,
             "frac_of_fp4_dense_peak": round(tflops / FP4_PEAK_TFLOPS, 4),
         }
 
@@ -242,66 +467,104 @@ def main() -> int:
                 "workload": f"cfg3 shapes, activations {fmt.upper()}-quantized per row, block-scaled MFMA",
                 "tflops": round(tf, 1),
                 "ms": round(t_mx * 1e3, 3),
-                "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": peak, "unit": "TFLOP/s",
-                             "frac": round(tf / peak, 4), "traffic": None},
+                "roofline": _roofline("mfma", tf, moe_pmc["gateup_grouped_w4a4"] if fmt == "mxfp4" else None, peak),
             }
+            if fmt == "mxfp4":
+                result["cfg3_moe_prefill_w4a4"]["pmc"] = {k: moe_pmc[k] for k in ("gateup_grouped_w4a4",
+                                                                                  "down_grouped_w4a4")}
         del weights, x3
 
     # -------------------------------------------------- config 5 decode --
+    # Cold: each step runs the next of `sets` routings (random_routing with
+    # seeds tokens * 100 + i), each over its own random experts, so a step's
+    # weights were last read more than 1 GB of weight traffic earlier (the
+    # Infinity Cache holds 256 MB).  Warm: routing 0 every step.
     if not args.quick and want("moe_decode"):
         dec = {}
-        for tokens in (1, 4, 16):
-            ids, rw = workloads.random_routing(tokens, seed=tokens)
-            active = torch.unique(ids).tolist()
-            raw = workloads.quantized_experts(active, device=dev)
-            weights = moe.prepare_expert_weights(*raw)
-            # the same experts with X4T-coded scales, expanded per call
-            weights_x4t = moe.prepare_expert_weights(*raw, scale_format="x4t")
-            del raw
+        plan = {1: 8, 4: 4, 16: 3}
+        routings = {b: [workloads.random_routing(b, seed=b * 100 + i) for i in range(n)] for b, n in plan.items()}
+        union = sorted({int(e) for rs in routings.values() for ids, _ in rs for e in ids.flatten().tolist()})
+        raw = workloads.quantized_experts(union, device=dev)
+        weights = moe.prepare_expert_weights(*raw)
+        weights_x4t = moe.prepare_expert_weights(*raw, scale_format="x4t")
+        del raw
+        for tokens, rs in routings.items():
             x5 = torch.randn(tokens, workloads.HIDDEN, generator=torch.Generator().manual_seed(5)).to(torch.bfloat16).to(dev)
-            ids_d, rw_d = ids.to(dev), rw.to(dev)
+            dev_r = [(ids.to(dev), rw.to(dev)) for ids, rw in rs]
+            nbytes = [len(torch.unique(ids)) * workloads.bytes_per_expert() + tokens * workloads.HIDDEN * 2
+                      for ids, _ in rs]
+            turn = [0]
 
-            def dec_step():
-                moe.grouped_expert_forward(x5, ids_d, rw_d, weights)
+            def dec_cold(w=weights):
+                ids_d, rw_d = dev_r[turn[0] % len(dev_r)]
+                turn[0] += 1
+                moe.grouped_expert_forward(x5, ids_d, rw_d, w)
 
-            def dec_x4t_step():
-                moe.grouped_expert_forward(x5, ids_d, rw_d, weights_x4t)
+            def dec_warm(w=weights):
+                moe.grouped_expert_forward(x5, dev_r[0][0], dev_r[0][1], w)
 
-            t = _time_loop(torch, dec_step, max(10, args.steps), 5)
-            t_x = _time_loop(torch, dec_x4t_step, max(10, args.steps), 5)
-            nbytes = len(active) * workloads.bytes_per_expert() + tokens * workloads.HIDDEN * 2
+            n_steps = max(10, args.steps) // len(rs) * len(rs)
+            t = _time_loop(torch, dec_cold, n_steps, len(rs) * 2)
+            turn[0] = 0
+            t_x = _time_loop(torch, lambda: dec_cold(weights_x4t), n_steps, len(rs) * 2)
+            t_w = _time_loop(torch, dec_warm, max(10, args.steps), 5)
+            mean_bytes = sum(nbytes) / len(nbytes)
             dec[f"batch{tokens}"] = {
                 "us": round(t * 1e6, 1),
-                "distinct_experts": len(active),
-                "gbs": round(nbytes / t / 1e9, 1),
-                "hbm_frac": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4),
+                "routings": len(rs),
+                "distinct_experts": round(mean_bytes / workloads.bytes_per_expert(), 1),
+                "gbs": round(mean_bytes / t / 1e9, 1),
+                "hbm_frac": round(mean_bytes / t / 1e9 / HBM_PEAK_GBS, 4),
+                "warm_us": round(t_w * 1e6, 1),
+                "warm_gbs": round(nbytes[0] / t_w / 1e9, 1),
                 "x4t_scales_us": round(t_x * 1e6, 1),
                 "x4t_added_us": round((t_x - t) * 1e6, 1),
             }
-            del weights, weights_x4t
+        del weights, weights_x4t
+        dec["note"] = ("cold: routings rotated over fresh experts (weights read once per forward from HBM); "
+                       "bytes = distinct experts' MXFP4 weights + the token rows")
         result["cfg5_moe_decode"] = dec
 
     # ------------------------------------------------- config 1 codec --
+    # Cold: 28 copies of the 37 MB working set (1.04 GB) taken in turn.
     if not args.quick and want("cfg1"):
+        sets1 = 28
         w1 = workloads.cfg1_weight().to(dev)
-        q4 = torch.empty(7168, 1024, dtype=torch.uint8, device=dev)
-        s4 = torch.empty(7168, 64, dtype=torch.uint8, device=dev)
-        d4 = torch.empty(7168, 2048, dtype=torch.bfloat16, device=dev)
         b1 = 7168 * 2048 * 2 + 7168 * 1024 + 7168 * 64
+        cset = [(w1 if i == 0 else w1.clone(), torch.empty(7168, 1024, dtype=torch.uint8, device=dev),
+                 torch.empty(7168, 64, dtype=torch.uint8, device=dev),
+                 torch.empty(7168, 2048, dtype=torch.bfloat16, device=dev)) for i in range(sets1)]
+        q_steps = [_bound(N, "kq_mx_quantize", N.FMT_MXFP4_E2M1, N.DT_BF16, N.ptr(w), 2048, 7168, 2048,
+                          N.ptr(q), N.ptr(sc), 0, stream) for w, q, sc, _ in cset]
+        d_steps = [_bound(N, "kq_mx_dequant", N.FMT_MXFP4_E2M1, N.ptr(q), N.ptr(sc), 7168, 2048,
+                          N.DT_BF16, N.ptr(d), 0, stream) for _, q, sc, d in cset]
+        for f in q_steps:
+            f()
+        turn = [0]
 
-        q_step = _bound(N, "kq_mx_quantize", N.FMT_MXFP4_E2M1, N.DT_BF16, N.ptr(w1), 2048, 7168, 2048,
-                        N.ptr(q4), N.ptr(s4), 0, stream)
-        d_step = _bound(N, "kq_mx_dequant", N.FMT_MXFP4_E2M1, N.ptr(q4), N.ptr(s4), 7168, 2048,
-                        N.DT_BF16, N.ptr(d4), 0, stream)
+        def rot(fns):
+            def step():
+                fns[turn[0] % len(fns)]()
+                turn[0] += 1
+            return step
 
-        tq = _time_loop(torch, q_step, args.steps, args.warmup)
-        td = _time_loop(torch, d_step, args.steps, args.warmup)
+        n1 = max(args.steps, 2 * sets1) // sets1 * sets1
+        tq = _time_loop(torch, rot(q_steps), n1, sets1)
+        td = _time_loop(torch, rot(d_steps), n1, sets1)
+        tq_w = _time_loop(torch, q_steps[0], args.steps, args.warmup)
+        td_w = _time_loop(torch, d_steps[0], args.steps, args.warmup)
         result["cfg1_mxfp4_codec"] = {
             "quantize_gbs": round(b1 / tq / 1e9, 1), "quantize_us": round(tq * 1e6, 2),
             "dequant_gbs": round(b1 / td / 1e9, 1), "dequant_us": round(td * 1e6, 2),
             "hbm_frac_quantize": round(b1 / tq / 1e9 / HBM_PEAK_GBS, 4),
-            "note": "37 MB working set stays within the 256 MB last-level cache across back-to-back launches",
+            "hbm_frac_dequant": round(b1 / td / 1e9 / HBM_PEAK_GBS, 4),
+            "bytes_per_launch": b1,
+            "pmc": _traffic_entry("cfg1", "kq::mx_quantize_kernel<0, 1", b1),
+            "warm_quantize_us": round(tq_w * 1e6, 2), "warm_dequant_us": round(td_w * 1e6, 2),
+            "note": f"cold: {sets1} buffer sets (1.04 GB) in turn; warm: one 37 MB set, which the "
+                    "256 MB Infinity Cache holds across launches",
         }
+        del cset, q_steps, d_steps
 
     # ---------------------------------------------- config 4 Hessian --
     if not args.quick and want("hessian"):
@@ -317,30 +580,22 @@ def main() -> int:
 
         th = _time_loop(torch, h_step, 3, 1)
         flops = workloads.syrk_flops(65536, 7168)
+        # rows once + the upper 256 x 256 tiles of the fp32 accumulator written once
+        syrk_pmc = _traffic_entry("hessian", "kq::syrk256_dma_kernel", 65536 * 7168 * 2 + 28 * 29 // 2 * 256 * 256 * 4)
         result["cfg4_hessian_k7168"] = {
             "tflops": round(flops / th / 1e12, 1),
             "ms": round(th * 1e3, 3),
-            "roofline": _roofline("mfma", flops / th / 1e12, "syrk_cfg4"),
+            "roofline": _roofline("mfma", flops / th / 1e12, syrk_pmc),
+            "pmc": syrk_pmc,
         }
         del x4, acc
 
     # --------------------------- config 4 (ii) per-expert Hessians, K=2048 --
     if not args.quick and want("hessian_experts"):
-        ids, rw = workloads.zipf_routing(65536)
         experts = workloads.EXPERTS
-        counts = torch.bincount(ids[ids >= 0].flatten().long(), minlength=experts)
-        offsets = torch.zeros(experts + 1, dtype=torch.int64)
-        offsets[1:] = torch.cumsum(counts, 0)
-        pairs = int(offsets[-1])
         k2 = workloads.INTER
-        g = torch.Generator(device=dev).manual_seed(1)
-        rows = torch.empty(pairs, k2, dtype=torch.bfloat16, device=dev)
-        for c0 in range(0, pairs, 65536):  # Student-t(4) rows, generated in slabs
-            n = min(65536, pairs - c0)
-            z = torch.randn(n, k2, generator=g, device=dev)
-            chi = sum(torch.randn(n, k2, generator=g, device=dev).square() for _ in range(4))
-            rows[c0:c0 + n] = (z / torch.sqrt(chi / 4)).to(torch.bfloat16)
-        gates = torch.rand(pairs, generator=g, device=dev)
+        rows, gates, offsets, counts = workloads.cfg4_expert_rows(dev)
+        pairs = int(offsets[-1])
         offsets_d = offsets.to(dev)
         hacc = torch.empty(experts, k2, k2, dtype=torch.float32, device=dev)
 
@@ -351,14 +606,20 @@ def main() -> int:
         the = _time_loop(torch, he_step, 3, 1)
         flops = float((counts.double() * k2 * (k2 + 1)).sum())
         hbytes = pairs * k2 * 2 + pairs * 4 + experts * k2 * k2 * 4
+        # the kernel writes the upper 256 x 256 tiles of each expert's accumulator
+        he_pmc = _traffic_entry("hessian_experts", "kq::syrk256_kernel<true, true>", pairs * k2 * 2 + pairs * 4
+                                + experts * 36 * 256 * 256 * 4)
         result["cfg4_hessian_experts_k2048"] = {
             "workload": "cfg4 (ii): gate^2-weighted X^T X of each expert's routed rows, 65536 tokens "
                         "top-8 Zipf(1.1) over 384 experts (524288 rows of 2048 bf16), one grouped launch",
             "ms": round(the * 1e3, 3),
             "tflops": round(flops / the / 1e12, 1),
             "gbs": round(hbytes / the / 1e9, 1),
-            "roofline": _roofline("hbm", hbytes / the / 1e9),
+            "roofline": _roofline("hbm", hbytes / the / 1e9, he_pmc),
+            "pmc": he_pmc,
             "active_experts": int((counts > 0).sum()),
+            "flops": flops,
+            "bytes": hbytes,
         }
         del rows, hacc
 
@@ -595,33 +856,114 @@ def main() -> int:
             "sqg_labels": int(labels.numel()),
         }
 
-    # ------------------------------------------------- CPU baseline --
+    # ------------------------------------------------- CPU baselines --
+    # The reference's CPU path for each configuration (oracle/torch_ref.py,
+    # the reference's own torch op sequences), on every CPU this process may
+    # use, on a bounded sample; rates extrapolate by bytes or flops.
     cpu = None
     if not args.no_cpu_baseline and want("cpu"):
         from oracle import torch_ref
 
-        torch.set_num_threads(min(os.cpu_count() or 1, 16))
-        w_cpu = workloads.cfg2_weight()
-        sample_rows = 3072  # a quarter of the matrix: ~5-20 s of CPU work over 5 runs
-        sample = w_cpu[:sample_rows].contiguous()
-        torch_ref.mxfp8_quantize_cpu(sample)
-        times = []
-        for _ in range(5):
-            t0 = time.perf_counter()
-            torch_ref.mxfp8_quantize_cpu(sample)
-            times.append(time.perf_counter() - t0)
-        tmed = statistics.median(times)
-        sbytes = sample_rows * cols * 2 + sample_rows * cols + sample_rows * cols // 32
-        cpu = {
-            "value": round(sbytes / tmed / 1e9, 3),
-            "unit": "GB/s",
-            "cores": torch.get_num_threads(),
-            "kind": "port",
-            "sample": f"kquant/mxfp8.py:34-50 formula on torch CPU ops, rows 0..{sample_rows} of the "
-                      f"cfg2 weight (bf16 [{sample_rows}x{cols}]), median of 5 runs",
-            "cpu": platform.processor() or platform.machine(),
-        }
+        env = _cpu_env(torch)
 
+        def base(value, unit, kind, sample):
+            return {"value": round(value, 4), "unit": unit, "cores": env["cores"], "kind": kind,
+                    "sample": sample, "cpu": env["cpu"], "os_cpu_count": env["os_cpu_count"],
+                    "affinity": env["affinity"]}
+
+        w_cpu = workloads.cfg2_weight()
+        sample_rows = 3072
+        sample = w_cpu[:sample_rows].contiguous()
+        tmed = _cpu_median(lambda: torch_ref.mxfp8_quantize_cpu(sample), 5)
+        cols = w_cpu.shape[1]
+        sbytes = sample_rows * cols * 2 + sample_rows * cols + sample_rows * cols // 32
+        cpu = base(sbytes / tmed / 1e9, "GB/s", "port",
+                   f"kquant/mxfp8.py:34-50 on torch CPU ops, rows 0..{sample_rows} of the cfg2 weight "
+                   f"(bf16 [{sample_rows}x{cols}]), median of 5 runs")
+        if "cfg2_mxfp8_quantize" in result:
+            result["cfg2_mxfp8_quantize"]["cpu_baseline"] = cpu
+
+        if "cfg2_mxfp8_linear" in result:
+            wq, ws = torch_ref.mxfp8_quantize_cpu(w_cpu)
+            wd = torch_ref.mxfp8_dequantize_cpu(wq, ws)
+            xs = workloads.cfg2_activations()[:256].float()
+            t = _cpu_median(lambda: torch.nn.functional.linear(xs, wd))
+            result["cfg2_mxfp8_linear"]["cpu_baseline"] = base(
+                2.0 * 256 * wd.shape[0] * wd.shape[1] / t / 1e12, "TFLOP/s", "port",
+                "scripts/closure_mxfp8_mlp.py:146-160 (fp32 matmul on the dequantized operands), 256 of the "
+                "4096 activation rows against the whole dequantized cfg2 weight, median of 3")
+            del wq, ws, wd
+
+        if moe_result is not None or "cfg5_moe_decode" in result:
+            gexp = torch.Generator().manual_seed(9)
+
+            def dense_expert():
+                return ((torch.randn(2 * workloads.INTER, workloads.HIDDEN, generator=gexp) * 0.02),
+                        (torch.randn(workloads.HIDDEN, workloads.INTER, generator=gexp) * 0.02))
+
+            if moe_result is not None:
+                ids3, rw3 = workloads.zipf_routing(8192)
+                ids3, rw3 = ids3[:1024], rw3[:1024]
+                hot = torch.bincount(ids3.flatten().long(), minlength=384).argsort(descending=True)[:4].tolist()
+                wts = {e: dense_expert() for e in hot}
+                x3c = torch.randn(1024, workloads.HIDDEN, generator=gexp)
+                npairs = int(sum((ids3 == e).sum() for e in hot))
+                t = _cpu_median(lambda: torch_ref.reference_rank(x3c, ids3, rw3, wts))
+                rate = workloads.moe_flops(npairs) / t / 1e12
+                moe_result["cpu_baseline"] = base(
+                    rate, "TFLOP/s", "port",
+                    f"scripts/closure_exl3_layer.py:557-598 loop with fp32 operands over the 4 most-routed "
+                    f"experts of the first 1024 tokens ({npairs} pairs), median of 3; the whole cfg3 "
+                    f"forward at this rate: {workloads.moe_flops(65536) / rate / 1e12:.1f} s")
+                del wts
+            if "cfg5_moe_decode" in result:
+                ids5, rw5 = workloads.random_routing(1, seed=100)
+                wts = {int(e): dense_expert() for e in ids5.flatten().tolist()}
+                x5c = torch.randn(1, workloads.HIDDEN, generator=gexp)
+                t = _cpu_median(lambda: torch_ref.reference_rank(x5c, ids5, rw5, wts))
+                nb = 8 * workloads.bytes_per_expert() + workloads.HIDDEN * 2
+                result["cfg5_moe_decode"]["cpu_baseline"] = base(
+                    nb / t / 1e9, "GB/s", "port",
+                    "the same loop for one decode token (8 experts, fp32 weights resident), median of 3; "
+                    "GB/s of the MXFP4 bytes the GPU path reads")
+                del wts
+
+        if "cfg1_mxfp4_codec" in result:
+            w1c = workloads.cfg1_weight()
+            tq = _cpu_median(lambda: torch_ref.mxfp4_quantize_cpu(w1c))
+            q1, s1 = torch_ref.mxfp4_quantize_cpu(w1c)
+            td = _cpu_median(lambda: torch_ref.dequant_mxfp4(q1, s1).to(torch.bfloat16))
+            b1 = result["cfg1_mxfp4_codec"]["bytes_per_launch"]
+            result["cfg1_mxfp4_codec"]["cpu_baseline"] = base(
+                b1 / tq / 1e9, "GB/s", "port",
+                "MXFP4 quantize of the whole cfg1 weight with the frozen rule on torch CPU ops (kquant has no "
+                "MXFP4 quantizer; kquant/mxfp8.py:34-50 with E2M1), median of 3")
+            result["cfg1_mxfp4_codec"]["cpu_baseline_dequant"] = base(
+                b1 / td / 1e9, "GB/s", "port", "kquant/io/mxfp4.py:52-64 LUT dequant of the cfg1 codes to bf16, "
+                "median of 3")
+
+        if "cfg4_hessian_k7168" in result:
+            xh = workloads.student_t4(4096, 7168, seed=3)
+            ones = torch.ones(4096)
+            t = _cpu_median(lambda: torch_ref.weighted_covariance(xh, ones, 256), 2)
+            result["cfg4_hessian_k7168"]["cpu_baseline"] = base(
+                workloads.syrk_flops(4096, 7168) / t / 1e12, "TFLOP/s", "port",
+                "kquant/candidate_hessian.py:98-107 (chunked fp32 addmm_, chunk 256) over 4096 of the 65536 "
+                "rows, useful flops N K (K+1), median of 2")
+        if "cfg4_hessian_experts_k2048" in result:
+            xe = workloads.student_t4(8192, 2048, seed=4)
+            ge = torch.rand(8192, generator=torch.Generator().manual_seed(4)).square()
+            t = _cpu_median(lambda: torch_ref.weighted_covariance(xe, ge, 256))
+            full = result["cfg4_hessian_experts_k2048"]
+            t_full = t * full["flops"] / workloads.syrk_flops(8192, 2048)
+            result["cfg4_hessian_experts_k2048"]["cpu_baseline"] = base(
+                full["bytes"] / t_full / 1e9, "GB/s", "port",
+                "the same loop with gate^2 weights over 8192 rows of one expert at K = 2048, extrapolated "
+                f"to the whole workload by flops ({t_full:.1f} s), median of 3")
+
+    head_pmc = _traffic_entry("quantize", "kq::mx_quantize_kernel<0, 0, true, true>", quant_bytes)
+    if "cfg2_mxfp8_quantize" in result:
+        result["cfg2_mxfp8_quantize"]["pmc"] = head_pmc
     line = {
         "metric": METRIC,
         "value": round(quant_gbs, 1),
@@ -636,11 +978,12 @@ def main() -> int:
         "dtype": "bf16->e4m3",
         "data": "synthetic (seeded N(0,0.015) bf16 weight, BASELINE config 2)",
         "config": {
-            "workload": "cfg2: MXFP8 E4M3 quantize of W[12288x7168] bf16 (32-elem blocks, E8M0 scale)",
+            "workload": "cfg2: MXFP8 E4M3 quantize of W[12288x7168] bf16 (32-elem blocks, E8M0 scale), cold: "
+                        "4 copies of the weight and its outputs (1.07 GB) quantized in turn",
             "bytes_per_step": quant_bytes,
             "parallelism": "1 GPU",
         },
-        "roofline": _roofline("hbm", quant_gbs, "mx_quantize_cfg2"),
+        "roofline": _roofline("hbm", quant_gbs, head_pmc),
         "cpu_baseline": cpu,
         "moe_prefill": moe_result,
         "configs": result,

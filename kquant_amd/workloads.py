@@ -85,6 +85,31 @@ def zipf_routing(
     return ids.to(torch.int32), weights.float()
 
 
+def cfg4_expert_rows(device, tokens: int = 65536, k: int = INTER, experts: int = EXPERTS, seed: int = 1):
+    """Configuration 4 (ii): every expert's routed rows at K = 2048, grouped.
+
+    The routing is ``zipf_routing(tokens)`` (configuration 3's recipe); expert
+    e owns rows [offsets[e], offsets[e + 1]) of ``rows`` (bf16 [pairs, k],
+    Student-t(4), generated on ``device`` in slabs by a seeded device
+    generator) with one gate per row (``gates`` fp32 [pairs], U(0, 1)).
+    Returns (rows, gates, offsets int64 [experts + 1] on the CPU, counts).
+    """
+    ids, _ = zipf_routing(tokens, experts)
+    counts = torch.bincount(ids[ids >= 0].flatten().long(), minlength=experts)
+    offsets = torch.zeros(experts + 1, dtype=torch.int64)
+    offsets[1:] = torch.cumsum(counts, 0)
+    pairs = int(offsets[-1])
+    g = torch.Generator(device=device).manual_seed(seed)
+    rows = torch.empty(pairs, k, dtype=torch.bfloat16, device=device)
+    for c0 in range(0, pairs, 65536):
+        n = min(65536, pairs - c0)
+        z = torch.randn(n, k, generator=g, device=device)
+        chi = sum(torch.randn(n, k, generator=g, device=device).square() for _ in range(4))
+        rows[c0:c0 + n] = (z / torch.sqrt(chi / 4)).to(torch.bfloat16)
+    gates = torch.rand(pairs, generator=g, device=device)
+    return rows, gates, offsets, counts
+
+
 def random_routing(tokens: int, experts: int = EXPERTS, topk: int = TOPK, seed: int = 0):
     """Decode routing: per token randperm(experts)[:topk], softmax(randn(topk)) weights."""
     g = torch.Generator().manual_seed(seed)

@@ -107,14 +107,20 @@ def mx_quantize(fmt: str, x: np.ndarray, dtype: str) -> tuple[np.ndarray, np.nda
     return q, s
 
 
-def mx_dequant(fmt: str, q: np.ndarray, s: np.ndarray) -> np.ndarray:
-    """fp32 [rows, k] = value(code) * 2^(s-127) (scale byte 255 -> inf)."""
+def mx_dequant(fmt: str, q: np.ndarray, s: np.ndarray, out: np.ndarray | None = None) -> np.ndarray:
+    """fp32 [rows, k] = value(code) * 2^(s-127) (scale byte 255 -> inf).
+
+    ``out`` (optional): a C-contiguous float32 [rows, k] array to write into,
+    so that callers dequantizing many matrices reuse one buffer."""
     lib = _load()
     q = np.ascontiguousarray(q, dtype=np.uint8)
     s = np.ascontiguousarray(s, dtype=np.uint8)
     rows = q.shape[0]
     k = s.shape[1] * 32
-    out = np.zeros((rows, k), dtype=np.float32)
+    if out is None:
+        out = np.empty((rows, k), dtype=np.float32)
+    elif out.shape != (rows, k) or out.dtype != np.float32 or not out.flags.c_contiguous:
+        raise ValueError("out must be a C-contiguous float32 [rows, k] array")
     lib.mxo_dequant(0 if fmt == "mxfp8" else 1, _ptr(q), _ptr(s), rows, k, _ptr(out))
     return out
 

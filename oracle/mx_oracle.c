@@ -151,15 +151,17 @@ void mxo_dequant(int fmt, const uint8_t* q, const uint8_t* scale, int64_t rows, 
   const int64_t nblk = k / 32;
 #pragma omp parallel for schedule(static)
   for (int64_t r = 0; r < rows; ++r)
-    for (int64_t i = 0; i < k; ++i) {
-      float s = mxo_scale_value(scale[r * nblk + i / 32]);
-      float v;
-      if (fmt == 0) v = mxo_e4m3_value(q[r * k + i]);
-      else {
-        uint8_t byte = q[r * (k / 2) + i / 2];
-        v = mxo_e2m1_value(i % 2 == 0 ? (byte & 15u) : (byte >> 4));
+    for (int64_t b = 0; b < nblk; ++b) {
+      const float s = mxo_scale_value(scale[r * nblk + b]);
+      for (int64_t i = b * 32; i < b * 32 + 32; ++i) {
+        float v;
+        if (fmt == 0) v = mxo_e4m3_value(q[r * k + i]);
+        else {
+          uint8_t byte = q[r * (k / 2) + i / 2];
+          v = mxo_e2m1_value(i % 2 == 0 ? (byte & 15u) : (byte >> 4));
+        }
+        out[r * k + i] = v * s;
       }
-      out[r * k + i] = v * s;
     }
 }
 

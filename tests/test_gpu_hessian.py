@@ -111,6 +111,46 @@ def test_cfg4_full_size_sampled_entries(gpu):
     assert abs(float(torch.trace(h.double())) - trace_exact) / trace_exact <= 1e-6
 
 
+def test_cfg4_expert_bench_workload_sampled_entries(gpu):
+    """Configuration 4 (ii) exactly as bench.py runs it: 524,288 Zipf-routed
+    rows of K = 2,048 over 384 experts (up to ~60k rows each), gate^2
+    weights, one grouped launch with in-kernel ranking by row count.  The 10
+    largest and 10 smallest non-empty experts are each checked on 4,096
+    entries (a 64 x 64 block of random rows and columns, 8 of them on the
+    diagonal) against exact float64 weighted dot products, and on their
+    trace against its exact float64 value."""
+    rows, gates, offsets, counts = workloads.cfg4_expert_rows(gpu)
+    k = rows.shape[1]
+    h, den = ch.expert_hessians_from_rows(rows, offsets, gates, square_weights=True)
+    torch.cuda.synchronize()
+    nonempty = torch.nonzero(counts).flatten()
+    order = nonempty[torch.argsort(counts[nonempty], descending=True)]
+    check = order[:10].tolist() + order[-10:].tolist()
+    assert counts[check[0]] > 50000 and counts[check[-1]] <= 3
+    rng = np.random.default_rng(3)
+    g2 = gates.float().square().double()  # weights = fp32 gate^2, as the reference forms them
+    worst = 0.0
+    for e in check:
+        a, b = int(offsets[e]), int(offsets[e + 1])
+        xe = rows[a:b].double()
+        we = g2[a:b]
+        denom = float(we.sum())
+        assert float(den[e]) == pytest.approx(denom, rel=1e-12)
+        i = torch.from_numpy(rng.choice(k, 64, replace=False)).to(gpu)
+        j = torch.from_numpy(rng.choice(k, 64, replace=False)).to(gpu)
+        j[:8] = i[:8]  # a few diagonal entries in the block
+        exact = (xe[:, i] * we[:, None]).T @ xe[:, j] / denom
+        got = h[e][i][:, j].double()
+        rel = float(torch.linalg.matrix_norm(got - exact) / torch.linalg.matrix_norm(exact))
+        worst = max(worst, rel)
+        assert rel <= TOL, (e, int(counts[e]), rel)
+        trace_exact = float((xe.square() * we[:, None]).sum()) / denom
+        # the trace sums ~60k positive fp32-accumulated terms per diagonal entry: the 1e-5 bar
+        assert abs(float(torch.trace(h[e].double())) - trace_exact) / trace_exact <= TOL, e
+        assert torch.equal(h[e], h[e].T)
+    print(f"cfg4 (ii) bench workload: worst sampled-entry relative error {worst:.3e}", flush=True)
+
+
 def test_repeat_runs_are_bitwise_identical(gpu):
     x = workloads.student_t4(4096, 512, seed=9).to(gpu)
     a, _ = ch.damped_hessian(x, damp=0.0)

@@ -122,24 +122,6 @@ def test_tile_layout_matches_oracle(gpu):
         assert np.array_equal(prep.w2_scale_tiles[e].cpu().numpy().reshape(st.shape), st)
 
 
-def test_prefill_zipf_full_size_sampled_tokens(gpu):
-    """Configuration 3: 8192 tokens, Zipf(1.1) top-8 over 384 experts."""
-    ids, w = workloads.zipf_routing(8192)
-    counts = torch.bincount(ids.flatten().long(), minlength=384)
-    assert counts.max() > 16 and (counts[counts > 0] <= 16).any()  # both kernel paths
-    x = torch.randn(8192, 7168, generator=torch.Generator().manual_seed(6)).to(torch.bfloat16)
-    weights = workloads.quantized_experts(torch.unique(ids).tolist(), device=gpu)
-    prep = moe.prepare_expert_weights(*weights)
-    out = moe.grouped_expert_forward(x.to(gpu), ids.to(gpu), w.to(gpu), prep)
-    out2 = moe.grouped_expert_forward(x.to(gpu), ids.to(gpu), w.to(gpu), prep)
-    assert torch.equal(out, out2)  # bitwise reproducible
-    check = np.array([0, 4097, 8191])
-    ref = _oracle(x, ids, w, weights, "situ", tokens=check)
-    rel = _max_rel(ref, out[torch.from_numpy(check)].cpu().numpy())
-    print(f"moe prefill sampled max-rel {rel:.2e}", flush=True)
-    assert rel <= TOL
-
-
 @pytest.mark.parametrize("register_staged", [False, True])
 def test_many_tiles_per_workgroup(gpu, register_staged):
     """More row tiles than one pass of the persistent grid, experts spanning
@@ -241,15 +223,75 @@ def _oracle_mx(x, ids, w, weights, fmt, tokens=None):
                               "situ", tokens=tokens, act_format=fmt)
 
 
-@pytest.mark.parametrize("fmt", ["mxfp8", "mxfp4"])
-def test_activation_quantized_cfg3_full_size_sampled_tokens(gpu, fmt):
-    """Configuration 3 shapes in the W4A8 / W4A4 modes, oracle on sampled tokens."""
+# ------------------------------------------------ configuration 3 at bench size --
+def cfg3_check_tokens(ids: torch.Tensor, hot: int = 20) -> np.ndarray:
+    """Tokens of the configuration-3 routing that cover, for each of the
+    ``hot`` most-routed experts, the first and last pair of its first and of
+    its last 256-row tile of the grouped GEMM (pairs sit in an expert's rows
+    in token order), plus one token of every expert on the GEMV path (1..16
+    pairs) and every token with more than one GEMV-path slot.  (No token of
+    this routing is routed only to GEMV-path experts.)"""
+    flat = ids.flatten().long()
+    counts = torch.bincount(flat, minlength=384)
+    sel = set()
+    for e in torch.argsort(counts, descending=True)[:hot].tolist():
+        pos = torch.nonzero(flat == e).flatten()
+        last = (pos.numel() - 1) // 256 * 256
+        for p in (pos[0], pos[min(255, pos.numel() - 1)], pos[last], pos[-1]):
+            sel.add(int(p) // ids.shape[1])
+    gemv = (counts >= 1) & (counts <= 16)
+    for e in torch.nonzero(gemv).flatten().tolist():
+        sel.add(int(torch.nonzero((ids == e).any(1)).flatten()[0]))
+    multi = torch.nonzero(gemv[ids.long()].sum(1) > 1).flatten().tolist()
+    sel.update(multi)
+    return np.array(sorted(sel))
+
+
+@pytest.fixture(scope="module")
+def cfg3(gpu):
     ids, w = workloads.zipf_routing(8192)
     x = torch.randn(8192, 7168, generator=torch.Generator().manual_seed(6)).to(torch.bfloat16)
     weights = workloads.quantized_experts(torch.unique(ids).tolist(), device=gpu)
     prep = moe.prepare_expert_weights(*weights)
+    return ids, w, x, weights, prep
+
+
+def _cfg3_oracle(x, ids, w, weights, check, fmt):
+    """oracle.moe_forward on the checked tokens only, every expert's weights
+    dequantized by the C oracle into two reused buffers."""
+    w13q, w13s, w2q, w2s = weights
+    b13 = np.empty((w13q.shape[1], w13s.shape[2] * 32), np.float32)
+    b2 = np.empty((w2q.shape[1], w2s.shape[2] * 32), np.float32)
+
+    def w13(e):
+        return oracle.mx_dequant("mxfp4", w13q[e].cpu().numpy(), w13s[e].cpu().numpy(), out=b13)
+
+    def w2(e):
+        return oracle.mx_dequant("mxfp4", w2q[e].cpu().numpy(), w2s[e].cpu().numpy(), out=b2)
+
+    sel = torch.from_numpy(check)
+    return oracle.moe_forward(x[sel].float().numpy(), ids[sel].numpy(), w[sel].numpy(), w13, w2, "situ",
+                              act_format=None if fmt == "bf16" else fmt)
+
+
+@pytest.mark.parametrize("fmt", ["bf16", "mxfp8", "mxfp4"])
+def test_cfg3_bench_size_covers_every_tile_kind(gpu, cfg3, fmt):
+    """Configuration 3 at bench size (8192 tokens, Zipf(1.1) top-8 over 384
+    experts, 205 active) in the W4A16, W4A8 and W4A4 modes: the output rows
+    of cfg3_check_tokens (first / last row tile of the 20 hottest experts,
+    every GEMV-path expert) against the oracle, and two runs bitwise equal."""
+    ids, w, x, weights, prep = cfg3
+    check = cfg3_check_tokens(ids)
+    assert len(check) >= 150
     out = moe.grouped_expert_forward(x.to(gpu), ids.to(gpu), w.to(gpu), prep, activation_format=fmt)
-    check = np.array([0, 1, 4097, 8191])
-    ref = _oracle_mx(x, ids, w, weights, fmt, tokens=check)
-    med = _check_operand_exact(ref, out[torch.from_numpy(check)].cpu().numpy(), fmt)
-    print(f"moe cfg3 {fmt} median rel {med:.2e}", flush=True)
+    again = moe.grouped_expert_forward(x.to(gpu), ids.to(gpu), w.to(gpu), prep, activation_format=fmt)
+    assert torch.equal(out, again)
+    got = out[torch.from_numpy(check).to(gpu)].cpu().numpy()
+    ref = _cfg3_oracle(x, ids, w, weights, check, fmt)
+    if fmt == "bf16":
+        rel = _max_rel(ref, got)
+        print(f"moe cfg3 W4A16 {len(check)} tokens max-rel {rel:.2e}", flush=True)
+        assert rel <= TOL
+    else:
+        med = _check_operand_exact(ref, got, fmt)
+        print(f"moe cfg3 {fmt} {len(check)} tokens median rel {med:.2e}", flush=True)

@@ -7,7 +7,8 @@ the bar is bitwise equality with kq_moe_forward over the dense scales: in
 each routing regime (decode, one-workgroup prep, multi-block prep), each
 mode (bf16 activations on the direct-to-LDS or register-staged GEMMs, W4A8,
 W4A4), with stale slots from earlier calls, and under HIP graph replay.
-Plain kq_moe_forward is itself pinned to the fp32 oracle in test_gpu_moe.py.
+Plain kq_moe_forward is itself pinned to the fp32 oracle in test_gpu_moe.py,
+and the X4T forward is also checked against that oracle directly.
 The tile index is checked against numpy.searchsorted over each matrix's
 exception positions and against the encoder's own per-tile offsets.
 """
@@ -195,3 +196,43 @@ def test_x4t_decode_real_shapes(gpu, tokens):
     coded = moe.prepare_expert_weights(*weights, scale_format="x4t")
     args = (x.to(gpu), ids.to(gpu), w.to(gpu))
     assert torch.equal(moe.grouped_expert_forward(*args, coded), moe.grouped_expert_forward(*args, dense))
+
+
+@pytest.mark.parametrize("T", [4, 600])
+def test_x4t_forward_matches_oracle(gpu, T):
+    """The X4T-scale forward against oracle.moe_forward on the dequantized
+    weights directly (kquant/x4t.py:477-524 decodes the planes to the dense
+    scales the oracle dequantizes with), at a decode routing (T=4: every
+    expert on the GEMV kernel, scales decoded in its prologue) and a prefill
+    routing (T=600: expanded scale slots for the grouped-GEMM experts, GEMV
+    for the rest), W4A16 and W4A4, with exception-heavy planes on two experts."""
+    import oracle
+
+    k, E, H, I = 4, 8, 512, 1024
+    g = torch.Generator().manual_seed(40 + T)
+    p = torch.tensor([0.4, 0.2, 0.15, 0.1, 0.08, 0.05, 0.02, 0.0])
+    ids = torch.stack([torch.multinomial(p, k, replacement=False, generator=g) for _ in range(T)])
+    ids = ids.to(torch.int32)
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    w = torch.softmax(torch.randn(T, k, generator=g), -1)
+    weights = _weights(E, H, I, 23, gpu, spread=(0, 3))
+    coded = moe.prepare_expert_weights(*weights, scale_format="x4t")
+    w13q, w13s, w2q, w2s = (t.cpu().numpy() for t in weights)
+
+    def w13(e):
+        return oracle.mx_dequant("mxfp4", w13q[e], w13s[e])
+
+    def w2(e):
+        return oracle.mx_dequant("mxfp4", w2q[e], w2s[e])
+
+    args = (x.to(gpu), ids.to(gpu), w.to(gpu))
+    for fmt in ("bf16", "mxfp4"):
+        got = moe.grouped_expert_forward(*args, coded, activation_format=fmt).cpu().numpy()
+        ref = oracle.moe_forward(x.float().numpy(), ids.numpy(), w.numpy(), w13, w2, "situ",
+                                 act_format=None if fmt == "bf16" else fmt)
+        err = np.abs(got.astype(np.float64) - ref) / np.abs(ref).max()
+        print(f"x4t forward vs oracle T={T} {fmt}: max rel {err.max():.2e}", flush=True)
+        if fmt == "bf16":
+            assert err.max() <= 2e-3
+        else:  # the W4A4 bars of test_gpu_moe.py
+            assert np.mean(err <= 1e-5) >= 0.999 and err.max() <= 0.05

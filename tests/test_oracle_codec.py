@@ -220,3 +220,25 @@ def test_fp16_and_fp32_inputs_match_torch_formula():
         rq = t.div(torch.exp2(e).unsqueeze(-1)).clamp(-448, 448).view(64, 512).to(torch.float8_e4m3fn)
         assert np.array_equal(s, (e + 127).to(torch.uint8).numpy())
         assert np.array_equal(q, rq.view(torch.uint8).numpy())
+
+
+def test_mxfp4_rule_two_restatements_agree():
+    """The C oracle's MXFP4 quantizer (nearest-value search, ties to even)
+    and oracle/torch_ref.mxfp4_quantize_cpu (torch CPU ops: the MXFP8 rule of
+    kquant/mxfp8.py:34-50 with E2M1, codes by bucketize over the midpoints)
+    are written independently; they agree byte for byte on every finite bf16
+    value (blocks of 32 consecutive bit patterns) and on the cfg1 weight."""
+    import torch
+
+    from kquant_amd import workloads
+    from oracle import torch_ref
+
+    bits = np.arange(65536, dtype=np.uint16)
+    vals = oracle.bf16_bits_to_f32(bits)
+    fin = bits[np.isfinite(vals)]
+    fin = fin[: len(fin) // 32 * 32].reshape(-1, 32)
+    w = workloads.cfg1_weight(256, 2048)
+    for b in (fin, w.view(torch.int16).numpy().view(np.uint16)):
+        rq, rs = oracle.mx_quantize("mxfp4", b, "bf16")
+        q, s = torch_ref.mxfp4_quantize_cpu(torch.from_numpy(b.view(np.int16).copy()).view(torch.bfloat16))
+        assert np.array_equal(q.numpy(), rq) and np.array_equal(s.numpy(), rs)
