@@ -35,6 +35,7 @@ constexpr int DECODE_MAX_PAIRS = 256;  // at most this many pairs: decode routin
 constexpr int PREP = 256;            // pairs per prep block
 constexpr int MAX_EXPERTS = 4096;
 constexpr int BM = 256, BN = 256, BK = 64, THREADS = 512;  // large tiles
+constexpr int DMA_BM = 128, DMA_BN = 512;  // tiles of the bf16-activation direct-to-LDS grouped GEMM
 constexpr int A_ROW = BK * 2 + 16;
 constexpr int B_ROW = 36;            // 32 packed bytes + pad
 constexpr int A_BYTES = BM * A_ROW;
@@ -61,7 +62,7 @@ static Layout make_layout(int64_t tokens, int topk, int experts, int64_t hidden,
                : L.pairs / (SMALL_MAX + 1) < experts ? L.pairs / (SMALL_MAX + 1) : experts;
   L.nblk = (L.pairs + PREP - 1) / PREP;
   L.max_small = L.pairs < experts ? L.pairs : experts;
-  L.max_large = L.pairs / (SMALL_MAX + 1) + L.pairs / BM + 1;
+  L.max_large = L.pairs / (SMALL_MAX + 1) + L.pairs / DMA_BM + 1;
   // GEMV list entries: one per small expert, or (decode) one per 16 pairs of
   // every routed expert, at most experts + pairs / 16
   L.max_list = L.pairs <= DECODE_MAX_PAIRS ? L.max_small + L.pairs / SMALL_MAX + 1 : L.max_small;
@@ -176,7 +177,7 @@ __global__ __launch_bounds__(1024) void route_scan_kernel(
     int* __restrict__ block_counts, int nblk, int experts, int* __restrict__ counts,
     int* __restrict__ offsets, int* __restrict__ small_list, int* __restrict__ large_tiles,
     int* __restrict__ meta, int max_large, int* __restrict__ rank_of, int* __restrict__ routed,
-    int max_routed) {
+    int max_routed, int bm) {
   __shared__ int s_cnt[MAX_EXPERTS];
   __shared__ int s_small[MAX_EXPERTS];
   __shared__ int s_tiles[MAX_EXPERTS];
@@ -199,7 +200,7 @@ __global__ __launch_bounds__(1024) void route_scan_kernel(
     counts[e] = s;
     s_cnt[e] = s;
     s_small[e] = (s >= 1 && s <= SMALL_MAX) ? 1 : 0;
-    s_tiles[e] = s > SMALL_MAX ? (s + BM - 1) / BM : 0;
+    s_tiles[e] = s > SMALL_MAX ? (s + bm - 1) / bm : 0;
   }
   __syncthreads();
   if (rank_of) routed_ranks(counts, experts, rank_of, routed, max_routed, s_small, scratch);
@@ -215,12 +216,12 @@ __global__ __launch_bounds__(1024) void route_scan_kernel(
       small_list[3 * s_small[e] + 2] = n;
     }
     if (n > SMALL_MAX) {
-      const int nt = (n + BM - 1) / BM;
+      const int nt = (n + bm - 1) / bm;
       for (int t = 0; t < nt; ++t) {
         const int slot = s_tiles[e] + t;
         if (slot < max_large) {
           large_tiles[2 * slot] = e;
-          large_tiles[2 * slot + 1] = t * BM;
+          large_tiles[2 * slot + 1] = t * bm;
         }
       }
     }
@@ -257,7 +258,7 @@ __global__ __launch_bounds__(1024) void route_prep_one_kernel(
     const int* __restrict__ ids, int pairs, int experts, int* __restrict__ counts,
     int* __restrict__ offsets, int* __restrict__ sorted, int* __restrict__ small_list,
     int* __restrict__ large_tiles, int* __restrict__ meta, int max_large, int* __restrict__ rank_of,
-    int* __restrict__ routed, int max_routed) {
+    int* __restrict__ routed, int max_routed, int bm) {
   __shared__ int s_cnt[MAX_EXPERTS];
   __shared__ int s_small[MAX_EXPERTS];
   __shared__ int s_tiles[MAX_EXPERTS];
@@ -278,7 +279,7 @@ __global__ __launch_bounds__(1024) void route_prep_one_kernel(
     const int c = s_cnt[e];
     counts[e] = c;
     s_small[e] = (c >= 1 && c <= SMALL_MAX) ? 1 : 0;
-    s_tiles[e] = c > SMALL_MAX ? (c + BM - 1) / BM : 0;
+    s_tiles[e] = c > SMALL_MAX ? (c + bm - 1) / bm : 0;
   }
   __syncthreads();
   if (rank_of) routed_ranks(counts, experts, rank_of, routed, max_routed, s_small, scratch);
@@ -294,12 +295,12 @@ __global__ __launch_bounds__(1024) void route_prep_one_kernel(
       small_list[3 * s_small[e] + 2] = c;
     }
     if (c > SMALL_MAX) {
-      const int nt = (c + BM - 1) / BM;
+      const int nt = (c + bm - 1) / bm;
       for (int k = 0; k < nt; ++k) {
         const int slot = s_tiles[e] + k;
         if (slot < max_large) {
           large_tiles[2 * slot] = e;
-          large_tiles[2 * slot + 1] = k * BM;
+          large_tiles[2 * slot + 1] = k * bm;
         }
       }
     }
@@ -1074,12 +1075,13 @@ __global__ __launch_bounds__(512, 1) void moe_large_kernel(
 // activation row tiles and a few weight tiles in its L2 (instead of one row
 // tile against all of the expert's weight tiles).  A permutation within each
 // expert's range: results do not depend on it.
+template <int TM = BM>
 __device__ __forceinline__ void grouped_tile(int t, int col_tiles, int nblk, const int* __restrict__ tiles,
                                              const int* __restrict__ offsets, int& mt, int& nt) {
   const int mt0 = t / col_tiles;
   const int e = tiles[2 * mt0], m0 = tiles[2 * mt0 + 1];
-  const int first = mt0 - m0 / BM;
-  const int cnt = (offsets[e + 1] - offsets[e] + BM - 1) / BM;
+  const int first = mt0 - m0 / TM;
+  const int cnt = (offsets[e + 1] - offsets[e] + TM - 1) / TM;
   const int u = t - first * col_tiles;
   const int nb = u / (cnt * nblk), rem = u - nb * cnt * nblk;
   mt = first + rem / nblk;
@@ -1087,18 +1089,21 @@ __device__ __forceinline__ void grouped_tile(int t, int col_tiles, int nblk, con
 }
 
 // ------------------------------------- grouped GEMM, direct-to-LDS loads --
-// Same tiles, waves, fragments and epilogues as moe_large_kernel, reorganised
-// around direct HBM -> LDS loads:
-//  * persistent: one workgroup per CU walks the (row tile, column tile) list,
-//    tile T = row_tile * col_tiles + col_tile.  Worker w (workgroups are
-//    numbered so the G/8 workers of one XCD are consecutive) takes tiles w,
-//    w + G, ...; the 32 workgroups of one XCD therefore work on neighbouring
-//    tiles of the same rows at the same time, and the gathered activation rows
-//    of a row tile are fetched into that XCD's L2 once.
-//  * loads go through a ring of three LDS stages (K step 64) issued two steps
-//    ahead, continuing across tile boundaries: the first two stages of a
-//    workgroup's next tile are in flight while it finishes and stores the
-//    current one.
+// The bf16-activation grouped GEMM (W4A16), organised around direct HBM ->
+// LDS loads:
+//  * tiles of 128 gathered token rows x 512 weight rows (gate/up: 256 gate
+//    and the matching 256 up channels), 8 waves of 64 x 128 (2 x 4).  The
+//    bf16 activations are four fifths of a 256 x 256 tile's operand bytes;
+//    this shape moves 33 KiB per 64-k step instead of 41 for the same MFMA
+//    work, and four stages fit in LDS, so three steps are in flight.
+//  * persistent: one workgroup per CU walks the (row tile, column tile) list
+//    (grouped_tile order).  Worker w (the G/8 workers of one XCD are
+//    consecutive) takes tiles w, w + G, ...; the 32 workgroups of one XCD
+//    therefore work on neighbouring tiles of the same expert at the same
+//    time and share operand rows in that XCD's L2.
+//  * the ring of LDS stages continues across tile boundaries: the first
+//    stages of a workgroup's next tile are in flight while it finishes and
+//    stores the current one.
 //  * activation rows: 128 bytes of a row per stage, 16-byte chunk c of tile
 //    row r stored at slot c ^ ((r / 2) % 8), so the 16 lanes of an MFMA
 //    fragment read hit 16 distinct bank groups.  Rows past the expert's count
@@ -1110,12 +1115,12 @@ __device__ __forceinline__ void grouped_tile(int t, int col_tiles, int nblk, con
 //    the one scale byte of block f.
 //  * waves whose 64 rows are all past the expert's count skip their MFMAs.
 namespace dma_gemm {
-constexpr int NSTAGE = 3;
-constexpr int DA_BYTES = BM * BK * 2;        // 32 KiB, unpadded 128-byte rows
-constexpr int DB_BYTES = BN * BK / 2;        // 8 KiB: 16 row groups x 512 B half tiles
-constexpr int DS_BYTES = BN * BK / 32;       // 512 B: 16 row groups x 32 B
+constexpr int NSTAGE = 4;
+constexpr int DA_BYTES = DMA_BM * BK * 2;    // 16 KiB, unpadded 128-byte rows
+constexpr int DB_BYTES = DMA_BN * BK / 2;    // 16 KiB: 32 row groups x 512 B half tiles
+constexpr int DS_BYTES = DMA_BN * BK / 32;   // 1 KiB: 32 row groups x 32 B
 constexpr int DSTAGE = DA_BYTES + DB_BYTES + DS_BYTES;
-constexpr int LOADS_PER_STAGE = 6;          // per wave: 4 activation, 1 weight, 1 scale
+constexpr int LOADS_PER_STAGE = 5;           // per wave: 2 activation, 2 weight, 1 scale
 }  // namespace dma_gemm
 
 __shared__ __attribute__((aligned(16))) unsigned char moe_dma_lds[dma_gemm::NSTAGE * dma_gemm::DSTAGE];
@@ -1141,41 +1146,41 @@ __global__ __launch_bounds__(512, 1) void moe_large_dma_kernel(
   const uint32_t b_bytes = (uint32_t)(rgs * nchunk * 1024), s_bytes = (uint32_t)(rgs * nchunk * 64);
   const int steps = (int)(K / BK);
   const uint32_t lds0 = dma::lds_offset_of(moe_dma_lds);
-  const int nblk = col_tiles % 8 == 0 ? 8 : col_tiles % 4 == 0 ? 4 : 1;
+  int nblk = 8;  // column tiles per block of grouped_tile: the largest divisor <= 8
+  while (col_tiles % nblk != 0) --nblk;
   const i32x4_t a_rsrc = dma::make_rsrc(a, a_bytes);
 
-  // global row group of local group lrg (16 per tile) for column tile c0
+  // global row group of local group lrg (32 per tile) for column tile c0
   auto grow_group = [&](int64_t c0, int lrg) -> int64_t {
-    if (GATEUP) return lrg < 8 ? c0 / 16 + lrg : inter / 16 + c0 / 16 + (lrg - 8);
+    if (GATEUP) return lrg < 16 ? c0 / 16 + lrg : inter / 16 + c0 / 16 + (lrg - 16);
     return c0 / 16 + lrg;
   };
 
   // ---- load side: tile lt, step ls; per-lane byte offsets (invalid -> past the range)
   int lt = worker, ls = 0;
-  uint32_t a_off[4], b_off = 0, s_off = 0;
+  uint32_t a_off[2], b_off[2], s_off = 0;
   i32x4_t b_rsrc = dma::make_rsrc(wt, 0), s_rsrc = dma::make_rsrc(wst, 0);
   auto set_load_tile = [&]() {
     if (lt >= total) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) a_off[q] = a_bytes;
-      b_off = b_bytes;
+      a_off[0] = a_off[1] = a_bytes;
+      b_off[0] = b_off[1] = b_bytes;
       s_off = s_bytes;
       return;
     }
     int mt, nt;
-    grouped_tile(lt, col_tiles, nblk, tiles, offsets, mt, nt);
+    grouped_tile<DMA_BM>(lt, col_tiles, nblk, tiles, offsets, mt, nt);
     const int e = tiles[2 * mt], m0 = tiles[2 * mt + 1];
     const int beg = offsets[e], n = offsets[e + 1] - beg;
-    const int64_t c0 = (int64_t)nt * (GATEUP ? BN / 2 : BN);
-    // all four row lookups are issued before the first is used (one wait)
-    int src[4];
+    const int64_t c0 = (int64_t)nt * (GATEUP ? DMA_BN / 2 : DMA_BN);
+    // both row lookups are issued before the first is used (one wait)
+    int src[2];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < 2; ++q) {
       const int slot = m0 + 8 * (8 * q + wave) + (lane >> 3);
       src[q] = GATEUP ? sorted[beg + (slot < n ? slot : n - 1)] : beg + slot;
     }
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < 2; ++q) {
       const int row = 8 * (8 * q + wave) + (lane >> 3);
       const int c = (lane & 7) ^ ((row >> 1) & 7);
       const int64_t r = GATEUP ? src[q] / topk : src[q];
@@ -1183,12 +1188,13 @@ __global__ __launch_bounds__(512, 1) void moe_large_dma_kernel(
     }
     b_rsrc = dma::make_rsrc(wt + (int64_t)e * rgs * nchunk * 1024, b_bytes);
     s_rsrc = dma::make_rsrc(wst + (int64_t)(sslot ? sslot[e] : e) * rgs * nchunk * 64, s_bytes);
-    {
-      const int64_t rg = grow_group(c0, 2 * wave + (lane >> 5));
-      b_off = 16 * rg < nrows ? (uint32_t)(rg * nchunk * 1024 + (lane & 31) * 16) : b_bytes;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int64_t rg = grow_group(c0, 4 * wave + 2 * q + (lane >> 5));
+      b_off[q] = 16 * rg < nrows ? (uint32_t)(rg * nchunk * 1024 + (lane & 31) * 16) : b_bytes;
     }
     {
-      const int64_t rg = grow_group(c0, 2 * wave + ((lane >> 1) & 1));
+      const int64_t rg = grow_group(c0, 4 * wave + ((lane >> 1) & 3));
       s_off = 16 * rg < nrows ? (uint32_t)(rg * nchunk * 64 + (lane & 1) * 16) : s_bytes;
     }
   };
@@ -1197,15 +1203,17 @@ __global__ __launch_bounds__(512, 1) void moe_large_dma_kernel(
     const uint32_t k0 = (uint32_t)(ls * BK);
     const uint32_t chunk = k0 / 128, h = (k0 / 64) & 1;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < 2; ++q) {
       const uint32_t off = a_off[q] >= a_bytes ? a_bytes : a_off[q] + 2 * k0;
       dma::load_to_lds16(a_rsrc, off, base + (uint32_t)((8 * q + wave) * 1024));
     }
-    dma::load_to_lds16(b_rsrc, b_off >= b_bytes ? b_bytes : b_off + chunk * 1024 + h * 512,
-                       base + (uint32_t)(DA_BYTES + wave * 1024));
-    if (lane < 4)
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+      dma::load_to_lds16(b_rsrc, b_off[q] >= b_bytes ? b_bytes : b_off[q] + chunk * 1024 + h * 512,
+                         base + (uint32_t)(DA_BYTES + (2 * wave + q) * 1024));
+    if (lane < 8)
       dma::load_to_lds16(s_rsrc, s_off >= s_bytes ? s_bytes : s_off + chunk * 64 + h * 32,
-                         base + (uint32_t)(DA_BYTES + DB_BYTES + wave * 64));
+                         base + (uint32_t)(DA_BYTES + DB_BYTES + wave * 128));
   };
   auto advance = [&]() {
     if (++ls == steps) {
@@ -1216,7 +1224,7 @@ __global__ __launch_bounds__(512, 1) void moe_large_dma_kernel(
   };
 
   // ---- compute side: per-lane LDS read offsets (fixed for the whole kernel)
-  const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+  const int wm = (wave >> 2) * 64, wn = (wave & 3) * 64;
   const int frow = lane & 31, fk = lane >> 5;
   int arow[2], axor[2], boff[4], soff[4];
 #pragma unroll
@@ -1227,23 +1235,24 @@ __global__ __launch_bounds__(512, 1) void moe_large_dma_kernel(
   }
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const int r = GATEUP ? (j < 2 ? 0 : BN / 2) + wn + (j & 1) * 32 + frow : 2 * wn + j * 32 + frow;
+    const int r = GATEUP ? (j < 2 ? 0 : DMA_BN / 2) + wn + (j & 1) * 32 + frow : 2 * wn + j * 32 + frow;
     boff[j] = DA_BYTES + (r >> 4) * 512 + (fk * 16 + (r & 15)) * 16;
     soff[j] = DA_BYTES + DB_BYTES + (r >> 4) * 32 + fk * 16 + (r & 15);
   }
 
   set_load_tile();
-  issue(0);
-  advance();
-  issue(1);
-  advance();
+#pragma unroll
+  for (int p = 0; p < NSTAGE - 1; ++p) {
+    issue(p);
+    advance();
+  }
   int cslot = 0;
   for (int t = worker; t < total; t += G) {
     int mt, nt;
-    grouped_tile(t, col_tiles, nblk, tiles, offsets, mt, nt);
+    grouped_tile<DMA_BM>(t, col_tiles, nblk, tiles, offsets, mt, nt);
     const int e = tiles[2 * mt], m0 = tiles[2 * mt + 1];
     const int beg = offsets[e], n = offsets[e + 1] - beg;
-    const int64_t c0 = (int64_t)nt * (GATEUP ? BN / 2 : BN);
+    const int64_t c0 = (int64_t)nt * (GATEUP ? DMA_BN / 2 : DMA_BN);
     const bool active = m0 + wm < n;
 
     float16_t acc[2][4];
@@ -1255,10 +1264,10 @@ __global__ __launch_bounds__(512, 1) void moe_large_dma_kernel(
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
     for (int s = 0; s < steps; ++s) {
-      // this step's loads landed (the next step's may be in flight); every
+      // this step's loads landed (the next steps' may be in flight); every
       // wave is done with the slot the next issue overwrites
-      dma::wait_and_barrier<LOADS_PER_STAGE>();
-      issue(cslot == 0 ? 2 : cslot - 1);
+      dma::wait_and_barrier<(NSTAGE - 2) * LOADS_PER_STAGE>();
+      issue(cslot == 0 ? NSTAGE - 1 : cslot - 1);
       advance();
       if (active) {
         const unsigned char* st = moe_dma_lds + cslot * DSTAGE;
@@ -1284,7 +1293,7 @@ __global__ __launch_bounds__(512, 1) void moe_large_dma_kernel(
               acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
         }
       }
-      cslot = cslot == 2 ? 0 : cslot + 1;
+      cslot = cslot == NSTAGE - 1 ? 0 : cslot + 1;
     }
 
     if (active) {
@@ -1830,6 +1839,13 @@ static int moe_forward_impl(const char* fn, int activation, float act_beta, floa
   // Decode: few pairs.  Every routed expert takes the GEMV path (in entries
   // of up to 16 pairs) and the grouped GEMM is not launched.
   const bool decode = L.pairs <= DECODE_MAX_PAIRS;
+  // bf16 activations: the direct-to-LDS grouped GEMM (128-row tiles) unless a
+  // buffer exceeds one 32-bit buffer range; the register-staged and the
+  // activation-quantized kernels take 256-row tiles
+  const uint64_t x_bytes = (uint64_t)tokens * ldx * 2, act_bytes = (uint64_t)L.pairs * inter * 2;
+  const bool dma_path = act_fmt < 0 && !(flags & KQ_MOE_REGISTER_STAGED) && x_bytes <= dma::MAX_RANGE &&
+                        act_bytes <= dma::MAX_RANGE && (uint64_t)(2 * inter) * hidden / 2 <= dma::MAX_RANGE;
+  const int tile_rows = dma_path ? DMA_BM : BM;
 
   if (decode) {
     route_decode_kernel<<<1, DECODE_MAX_PAIRS, 0, st>>>(route_ids, (int)L.pairs, experts, sorted,
@@ -1838,14 +1854,14 @@ static int moe_forward_impl(const char* fn, int activation, float act_beta, floa
   } else if (L.pairs <= PREP_ONE) {
     route_prep_one_kernel<<<1, 1024, 0, st>>>(route_ids, (int)L.pairs, experts, counts, offsets,
                                                sorted, small_list, large_tiles, meta, (int)L.max_large,
-                                               rank_of, routed, max_routed);
+                                               rank_of, routed, max_routed, tile_rows);
     if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_moe_forward/prep");
   } else {
     route_hist_kernel<<<(unsigned)L.nblk, PREP, 0, st>>>(route_ids, L.pairs, experts, block_counts);
     if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_moe_forward/hist");
     route_scan_kernel<<<1, 1024, 0, st>>>(block_counts, (int)L.nblk, experts, counts, offsets,
                                           small_list, large_tiles, meta, (int)L.max_large, rank_of,
-                                          routed, max_routed);
+                                          routed, max_routed, tile_rows);
     if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_moe_forward/scan");
     route_scatter_kernel<<<(unsigned)L.nblk, PREP, 0, st>>>(route_ids, L.pairs, experts, offsets,
                                                             block_counts, sorted);
@@ -1904,11 +1920,6 @@ static int moe_forward_impl(const char* fn, int activation, float act_beta, floa
   }
   const size_t lds = 2 * (size_t)STAGE + BM * sizeof(int);
   const bool any_large = !decode && L.pairs > SMALL_MAX;
-  // direct-to-LDS path unless a buffer exceeds one 32-bit buffer range
-  const uint64_t x_bytes = (uint64_t)tokens * ldx * 2, act_bytes = (uint64_t)L.pairs * inter * 2;
-  const bool dma_path = !(flags & KQ_MOE_REGISTER_STAGED) && x_bytes <= dma::MAX_RANGE &&
-                        act_bytes <= dma::MAX_RANGE &&
-                        (uint64_t)(2 * inter) * hidden / 2 <= dma::MAX_RANGE;
   int grid_dma = 0;
   if (any_large && dma_path) {
     int dev = 0, cus = 0;
@@ -1916,7 +1927,7 @@ static int moe_forward_impl(const char* fn, int activation, float act_beta, floa
       e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
     if (e != hipSuccess) return kq_check_launch(e, "kq_moe_forward/device");
     grid_dma = cus / 8 * 8 > 0 ? cus / 8 * 8 : 8;
-    const int col_tiles = (int)(inter / (BN / 2));
+    const int col_tiles = (int)(inter / (DMA_BN / 2));
     moe_large_dma_kernel<true><<<grid_dma, THREADS, 0, st>>>(
         xb, ldx, (uint32_t)x_bytes, topk, offsets, sorted, large_tiles, meta, w13_t, w13_st, sslot,
         2 * inter, hidden, inter, col_tiles, ap, route_weights, act, y, hidden);
@@ -1942,7 +1953,7 @@ static int moe_forward_impl(const char* fn, int activation, float act_beta, floa
     if (e != hipSuccess) return kq_check_launch(e, "kq_moe_forward/down_small");
   }
   if (any_large && dma_path) {
-    const int col_tiles = (int)(hidden / BN);
+    const int col_tiles = (int)(hidden / DMA_BN);
     moe_large_dma_kernel<false><<<grid_dma, THREADS, 0, st>>>(
         act, inter, (uint32_t)act_bytes, topk, offsets, sorted, large_tiles, meta, w2_t, w2_st, sslot,
         hidden, inter, inter, col_tiles, ap, route_weights, act, y, hidden);
@@ -2138,12 +2149,13 @@ extern "C" int kq_route_sort(const int32_t* route_ids, int64_t tokens, int topk,
   hipError_t e;
   if (pairs <= PREP_ONE) {
     route_prep_one_kernel<<<1, 1024, 0, st>>>(route_ids, (int)pairs, experts, counts, off32, sorted,
-                                               small_list, large_tiles, meta, max_large, nullptr, nullptr, 0);
+                                               small_list, large_tiles, meta, max_large, nullptr, nullptr, 0,
+                                               BM);
   } else {
     route_hist_kernel<<<(unsigned)nblk, PREP, 0, st>>>(route_ids, pairs, experts, block_counts);
     if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_route_sort");
     route_scan_kernel<<<1, 1024, 0, st>>>(block_counts, (int)nblk, experts, counts, off32, small_list,
-                                          large_tiles, meta, max_large, nullptr, nullptr, 0);
+                                          large_tiles, meta, max_large, nullptr, nullptr, 0, BM);
     if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_route_sort");
     route_scatter_kernel<<<(unsigned)nblk, PREP, 0, st>>>(route_ids, pairs, experts, off32,
                                                           block_counts, sorted);

@@ -42,6 +42,30 @@ def test_situ_and_swiglu(gpu, dtype):
     torch.testing.assert_close(got, expected)
 
 
+def test_activation_accuracy_sweep(gpu):
+    """The epilogue activations (hardware exp2 / reciprocal, a fitted tanh
+    polynomial below |y| = 0.625) against float64 SiTU / SwiGLU over a wide
+    fp32 grid: tiny values, both signs, the tanh branch point, saturation and
+    exp overflow (|x| up to 200).  Bar: a few ulp relative plus 1e-30
+    absolute (denormal-range sigmoid tails)."""
+    mags = np.concatenate([np.geomspace(1e-20, 1e-3, 64), np.linspace(1e-3, 3.0, 900),
+                           np.array([0.625 * 4, 0.625 * 4 * (1 - 2 ** -23), 0.625 * 25, 0.625 * 25 * (1 + 2 ** -23)]),
+                           np.linspace(3.0, 200.0, 400)])
+    vals = np.concatenate([mags, -mags, [0.0, -0.0]]).astype(np.float32)
+    gate = torch.from_numpy(np.repeat(vals, 16).reshape(-1, 16))
+    up = torch.from_numpy(np.tile(vals[:: max(1, len(vals) // 16)][:16], (len(vals), 1)).astype(np.float32))
+    g64, u64 = gate.double().numpy(), up.double().numpy()
+    sig = 1.0 / (1.0 + np.exp(-g64))
+    refs = {"situ": 4.0 * np.tanh(g64 / 4.0) * sig * (25.0 * np.tanh(u64 / 25.0)), "swiglu": g64 * sig * u64}
+    for name, fn in (("situ", tp.situ), ("swiglu", tp.swiglu)):
+        got = fn(gate.to(gpu), up.to(gpu)).cpu().double().numpy()
+        ref = refs[name]
+        assert np.isfinite(got).all()
+        err = np.abs(got - ref) / (np.abs(ref) * 2.0 ** -23 + 1e-30)
+        print(f"{name}: max error {err.max():.2f} ulp (fp32 relative)", flush=True)
+        assert err.max() <= 16.0
+
+
 def test_reduce_partials(gpu):
     g = torch.Generator().manual_seed(1)
     parts = [torch.randn(6, 129, generator=g) for _ in range(5)]
