@@ -565,6 +565,20 @@ def main() -> int:
                     "256 MB Infinity Cache holds across launches",
         }
         del cset, q_steps, d_steps
+        # sixteen experts' [7168 x 2048] weights quantized in one launch (how a
+        # checkpoint is converted): 594 MB, past every cache, no rotation needed
+        stack = torch.cat([w1] + [w1.roll(e, 0) for e in range(1, 16)], 0)
+        sq = torch.empty(stack.shape[0], 1024, dtype=torch.uint8, device=dev)
+        ss = torch.empty(stack.shape[0], 64, dtype=torch.uint8, device=dev)
+        st_step = _bound(N, "kq_mx_quantize", N.FMT_MXFP4_E2M1, N.DT_BF16, N.ptr(stack), 2048, stack.shape[0],
+                         2048, N.ptr(sq), N.ptr(ss), 0, stream)
+        t16 = _time_loop(torch, st_step, max(10, args.steps // 2), args.warmup)
+        result["cfg1_mxfp4_codec"]["stacked16"] = {
+            "workload": "MXFP4 quantize of 16 stacked [7168 x 2048] bf16 expert weights, one launch",
+            "bytes": 16 * b1, "us": round(t16 * 1e6, 2), "gbs": round(16 * b1 / t16 / 1e9, 1),
+            "hbm_frac": round(16 * b1 / t16 / 1e9 / HBM_PEAK_GBS, 4),
+        }
+        del stack, sq, ss
 
     # ---------------------------------------------- config 4 Hessian --
     if not args.quick and want("hessian"):

@@ -248,9 +248,16 @@ __device__ __forceinline__ float load_x(const void* x, int dtype, int64_t i) {
   return (float)reinterpret_cast<const __bf16*>(x)[i];
 }
 
+// output codes of store_out: KQ_DT_* and, for the regularized weight only,
+// its E4M3 label bytes (every value is an E4M3 label, so the conversion
+// returns the label byte exactly)
+constexpr int OUT_E4M3 = 3;
+
 __device__ __forceinline__ void store_out(void* out, int dtype, int64_t i, float v) {
   if (dtype == KQ_DT_F32) reinterpret_cast<float*>(out)[i] = v;
   else if (dtype == KQ_DT_F16) reinterpret_cast<_Float16*>(out)[i] = (_Float16)v;
+  else if (dtype == OUT_E4M3)
+    reinterpret_cast<uint8_t*>(out)[i] = (uint8_t)(__builtin_amdgcn_cvt_pk_fp8_f32(v, v, 0, false) & 0xff);
   else reinterpret_cast<__bf16*>(out)[i] = (__bf16)v;
 }
 
@@ -646,6 +653,43 @@ __global__ __launch_bounds__(LIN_THREADS) void decode_fast_kernel(DecArgs a, Lin
   }
 }
 
+// ---------------------------------------------------------------- prefill --
+// Row-wise 128-point rotation for the prefill form of the QSRT linear: one
+// wave per (row, 128-column block), the block held as (lane, lane + 64), the
+// wave-level Sylvester transform, scales applied before (PRE: the input's
+// suh) or after it (the output's svh), and a power-of-two post factor.
+// Without ROT it converts only.  All 64 lanes of a wave take the same row.
+template <bool PRE, bool ROT>
+__global__ __launch_bounds__(256) void rot_rows_kernel(const void* __restrict__ in, int in_dtype, int64_t ldi,
+                                                       int64_t rows, const float* __restrict__ scale, float post,
+                                                       void* __restrict__ out, int out_dtype, int64_t ldo) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.y * 4 + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const int64_t c = (int64_t)blockIdx.x * 128 + lane;
+  float v0 = load_x(in, in_dtype, r * ldi + c), v1 = load_x(in, in_dtype, r * ldi + c + 64);
+  if (PRE && scale) {
+    v0 *= scale[c];
+    v1 *= scale[c + 64];
+  }
+  if (ROT) {
+    fwht128(v0, v1, lane);
+    v0 *= post;
+    v1 *= post;
+  }
+  if (!PRE && scale) {
+    v0 *= scale[c];
+    v1 *= scale[c + 64];
+  }
+  store_out(out, out_dtype, r * ldo + c, v0);
+  store_out(out, out_dtype, r * ldo + c + 64, v1);
+}
+
+__global__ __launch_bounds__(256) void fill_u8_kernel(uint8_t* __restrict__ p, int64_t n, uint8_t v) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
 // ------------------------------------------------------ routed experts --
 // The routed expert forward of a decode batch with QSRT-coded experts, as
 // two launches of the fused linear's workgroup (M = 1 row per job):
@@ -930,7 +974,10 @@ extern "C" int kq_qsrt_decode_weight(const int16_t* payload, int64_t payload_wor
   if (!payload || !record_bits || !labels || !out)
     return kq_fail(KQ_ERR_INVALID, "%s: null buffer", fn);
   if ((suh == nullptr) != (svh == nullptr)) return kq_fail(KQ_ERR_INVALID, "%s: give both suh and svh or neither", fn);
-  if (out_dtype < KQ_DT_BF16 || out_dtype > KQ_DT_F32) return kq_fail(KQ_ERR_INVALID, "%s: bad output dtype", fn);
+  if ((out_dtype < KQ_DT_BF16 || out_dtype > KQ_DT_F32) && out_dtype != OUT_E4M3)
+    return kq_fail(KQ_ERR_INVALID, "%s: bad output dtype", fn);
+  if (out_dtype == OUT_E4M3 && (suh || kq_misaligned(payload, 16) || kq_misaligned(labels, 16)))
+    return kq_fail(KQ_ERR_INVALID, "%s: E4M3 bytes need the regularized weight and 16-byte aligned buffers", fn);
   const bool tr = flags & KQ_QSRT_TRANSPOSED;
   const int64_t rows = k_tiles * TILE, cols = n_tiles * TILE;
   if (ldo < (tr ? rows : cols)) return kq_fail(KQ_ERR_INVALID, "%s: ldo too small", fn);
@@ -949,8 +996,10 @@ extern "C" int kq_qsrt_decode_weight(const int16_t* payload, int64_t payload_wor
   if (words != payload_words)
     return kq_fail(KQ_ERR_INVALID, "%s: payload has %lld words, the records need %lld", fn,
                    (long long)payload_words, (long long)words);
-  if (kq_misaligned(payload, 4) == false) {
-    // fast path: LDS labels and rotation (needs a 4-byte-aligned payload)
+  if (!kq_misaligned(payload, 16) && !kq_misaligned(labels, 16)) {
+    // fast path: LDS labels and rotation; its 16-byte direct loads need a
+    // 16-byte aligned payload and label table (record and tile offsets are
+    // multiples of 16 bytes)
     LinRecords lr{};
     uint32_t sum = 0;
     for (int64_t r = 0; r < records; ++r) {
@@ -1055,11 +1104,86 @@ void launch_linear_m(const LinArgs& a, const LinRecords& rec, bool rot, dim3 gri
 
 }  // namespace
 
+// Rows from which kq_qsrt_linear takes the prefill form: the fused kernel
+// decodes the weight once per 16 rows, so past two row groups one decode to
+// E4M3 label bytes plus the MXFP8 MFMA linear is faster.
+static constexpr int64_t PREFILL_ROWS = 33;
+
+// Prefill workspace: rotated activations xr [m, K] (fp32, or bf16 for bf16
+// x), the regularized weight's E4M3 bytes [N, K] with unit E8M0 scales
+// [N, K / 32], the product y [m, N] fp32, and kq_mx_linear_f32's split.
+struct PrefillLayout {
+  int64_t xr, w, s, y, split, total, split_bytes;
+};
+
+static PrefillLayout prefill_layout(int64_t m, int64_t k, int64_t n, bool f32) {
+  auto al = [](int64_t v) { return (v + 255) / 256 * 256; };
+  PrefillLayout L{};
+  L.split_bytes = f32 ? kq_mx_linear_f32_workspace_size(m, k) : 0;
+  int64_t o = 0;
+  L.xr = o;    o = al(o + m * k * (f32 ? 4 : 2));
+  L.w = o;     o = al(o + n * k);
+  L.s = o;     o = al(o + n * k / 32);
+  L.y = o;     o = al(o + m * n * 4);
+  L.split = o; o = al(o + (L.split_bytes > 0 ? L.split_bytes : 0));
+  L.total = o;
+  return L;
+}
+
 extern "C" int64_t kq_qsrt_linear_workspace_size(int64_t m, int64_t k_tiles, int64_t n_tiles) {
   if (m <= 0 || k_tiles <= 0 || n_tiles <= 0 || k_tiles % RECORD_TILES || n_tiles % RECORD_TILES) return 0;
+  if (m >= PREFILL_ROWS) return prefill_layout(m, k_tiles * TILE, n_tiles * TILE, true).total;
   LinPlan p;
   if (lin_plan(m, k_tiles, n_tiles, &p) != hipSuccess) return -1;
   return p.counters_bytes + p.partial_bytes;
+}
+
+// x @ W for prefill-sized row counts: xr = (x o suh) B_K (unscaled
+// transform; bf16 x gives bf16 xr, f16 / fp32 x fp32 xr), W_reg decoded once
+// to its E4M3 label bytes [N, K] (exact: W_reg is an MXFP8 matrix with unit
+// scales), y = xr W_reg^T on the MXFP8 MFMA linear (fp32 accumulation; fp32
+// xr through the exact three-term bf16 split), out = (y B_N) / 128 o svh.
+// Without suh / svh the matrix is W_reg itself and both rotations are plain
+// conversions.  Argument checks are the caller's.
+static int qsrt_prefill(const void* x, int x_dtype, int64_t m, int64_t ldx, const int16_t* payload,
+                        int64_t payload_words, int64_t k_tiles, int64_t n_tiles, int rate_axis,
+                        const uint8_t* record_bits, const uint8_t* labels, const float* suh, const float* svh,
+                        int out_dtype, void* out, int64_t ldo, void* workspace, int64_t ws_bytes, hipStream_t st,
+                        const char* fn) {
+  const int64_t K = k_tiles * TILE, N = n_tiles * TILE;
+  const bool f32 = x_dtype != KQ_DT_BF16;
+  const PrefillLayout L = prefill_layout(m, K, N, f32);
+  if (L.split_bytes < 0) return kq_fail(KQ_ERR_INVALID, "%s: bad sizes for the prefill product", fn);
+  if (!workspace || ws_bytes < L.total || kq_misaligned(workspace, 256))
+    return kq_fail(KQ_ERR_INVALID, "%s: workspace needs %lld bytes (256-byte aligned) for %lld rows", fn,
+                   (long long)L.total, (long long)m);
+  if ((m + 3) / 4 > 65535) return kq_fail(KQ_ERR_LIMIT, "%s: too many rows (%lld)", fn, (long long)m);
+  unsigned char* w = static_cast<unsigned char*>(workspace);
+  void* xr = w + L.xr;
+  uint8_t* wq = w + L.w;
+  uint8_t* ws = w + L.s;
+  float* y = reinterpret_cast<float*>(w + L.y);
+  const bool rot = suh != nullptr;
+  const int xr_dtype = f32 ? KQ_DT_F32 : KQ_DT_BF16;
+  const dim3 gin((unsigned)(K / 128), (unsigned)((m + 3) / 4));
+  if (rot) rot_rows_kernel<true, true><<<gin, 256, 0, st>>>(x, x_dtype, ldx, m, suh, 1.f, xr, xr_dtype, K);
+  else rot_rows_kernel<true, false><<<gin, 256, 0, st>>>(x, x_dtype, ldx, m, nullptr, 1.f, xr, xr_dtype, K);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return kq_check_launch(e, fn);
+  int rc = kq_qsrt_decode_weight(payload, payload_words, k_tiles, n_tiles, rate_axis, record_bits, labels, nullptr,
+                                 nullptr, OUT_E4M3, wq, K, KQ_QSRT_TRANSPOSED, st);
+  if (rc != KQ_OK) return rc;
+  const int64_t nscale = N * (K / 32);
+  fill_u8_kernel<<<(unsigned)((nscale + 255) / 256), 256, 0, st>>>(ws, nscale, 127);
+  if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, fn);
+  rc = f32 ? kq_mx_linear_f32(KQ_FMT_MXFP8_E4M3, static_cast<const float*>(xr), K, wq, ws, m, N, K, y, N,
+                              w + L.split, L.split_bytes, st)
+           : kq_mx_linear(KQ_FMT_MXFP8_E4M3, xr, K, wq, ws, m, N, K, KQ_DT_F32, y, N, st);
+  if (rc != KQ_OK) return rc;
+  const dim3 gout((unsigned)(N / 128), (unsigned)((m + 3) / 4));
+  if (rot) rot_rows_kernel<false, true><<<gout, 256, 0, st>>>(y, KQ_DT_F32, N, m, svh, 1.f / 128.f, out, out_dtype, ldo);
+  else rot_rows_kernel<false, false><<<gout, 256, 0, st>>>(y, KQ_DT_F32, N, m, nullptr, 1.f, out, out_dtype, ldo);
+  return kq_check_launch(hipGetLastError(), fn);
 }
 
 extern "C" int kq_qsrt_linear(const void* x, int x_dtype, int64_t m, int64_t ldx, const int16_t* payload,
@@ -1079,7 +1203,8 @@ extern "C" int kq_qsrt_linear(const void* x, int x_dtype, int64_t m, int64_t ldx
   const int64_t rows = k_tiles * TILE, cols = n_tiles * TILE;
   if (m == 0) return KQ_OK;
   if (!x || !payload || !record_bits || !labels || !out) return kq_fail(KQ_ERR_INVALID, "%s: null buffer", fn);
-  if (kq_misaligned(payload, 4)) return kq_fail(KQ_ERR_INVALID, "%s: payload must be 4-byte aligned", fn);
+  if (kq_misaligned(payload, 16) || kq_misaligned(labels, 16))
+    return kq_fail(KQ_ERR_INVALID, "%s: payload and labels must be 16-byte aligned", fn);
   if (ldx < rows || ldo < cols) return kq_fail(KQ_ERR_INVALID, "%s: ldx or ldo too small", fn);
   const int64_t records = (rate_axis ? n_tiles : k_tiles) / RECORD_TILES;
   if (records > MAX_RECORDS)
@@ -1099,6 +1224,9 @@ extern "C" int kq_qsrt_linear(const void* x, int x_dtype, int64_t m, int64_t ldx
   if (words != payload_words)
     return kq_fail(KQ_ERR_INVALID, "%s: payload has %lld words, the records need %lld", fn,
                    (long long)payload_words, (long long)words);
+  if (m >= PREFILL_ROWS)
+    return qsrt_prefill(x, x_dtype, m, ldx, payload, payload_words, k_tiles, n_tiles, rate_axis, record_bits,
+                        labels, suh, svh, out_dtype, out, ldo, workspace, ws_bytes, (hipStream_t)stream, fn);
   LinPlan p;
   hipError_t e = lin_plan(m, k_tiles, n_tiles, &p);
   if (e != hipSuccess) return kq_check_launch(e, fn);

@@ -83,9 +83,10 @@ def unpack_trellis_states(packed: torch.Tensor, bits: int) -> torch.Tensor:
     return _unpack(packed, bits, True)
 
 
-# rows up to which qsrt_linear runs the fused kernel (decode batches): it
-# decodes the weight once per 16 rows, so past two row groups the one-time
-# decode (about 35 us for a K3 3584 x 3072 matrix) plus a bf16 GEMM is faster
+# rows up to which kq_qsrt_linear runs the fused kernel (decode batches): it
+# decodes the weight once per 16 rows, so past two row groups the library
+# takes its prefill form (one decode to E4M3 label bytes and the MXFP8 MFMA
+# linear between the two rotations)
 FUSED_MAX_ROWS = 32
 
 _LABELS: dict[tuple[str, str | None, torch.device], torch.Tensor] = {}
@@ -140,9 +141,10 @@ def decode_qsrt_payload(
     if any(b not in (2, 3, 4) for b in bits):
         raise ValueError("tile_bits must contain only integer K2, K3, or K4")
     g, host = _on_gpu(payload)
-    g = N.aligned(g, 4)  # 4-byte aligned: the fast decode reads dwords
+    g = N.aligned(g, 16)  # the fast decode stages 16-byte pieces by direct loads
     gpu = g.device
     k, n = k_tiles * TILE_CHANNELS, n_tiles * TILE_CHANNELS
+    _check_record_count(bits, k_tiles, n_tiles, rate_axis)
     labels = rate_labels(codebook, rate_axis=rate_axis, device=gpu)
     su = sv = None
     if suh is not None:
@@ -164,6 +166,27 @@ def _check_record_bits(record_bits) -> bytes:
     if any(b not in (2, 3, 4) for b in bits):
         raise ValueError("tile_bits must contain only integer K2, K3, or K4")
     return bits
+
+
+def _check_record_count(bits: bytes, k_tiles: int, n_tiles: int, rate_axis: str) -> None:
+    """One rate per 128-channel record along the rate axis (the library reads
+    that many bytes of the host array)."""
+    if k_tiles <= 0 or n_tiles <= 0 or k_tiles % 8 or n_tiles % 8:
+        raise ValueError("both dimensions must be positive multiples of 128")
+    records = (k_tiles if rate_axis == "k" else n_tiles) // 8
+    if len(bits) != records:
+        raise ValueError(f"{len(bits)} record rates for {records} records along {rate_axis}")
+
+
+def _workspace(cache: dict, key: tuple, nbytes: int, gpu: torch.device) -> torch.Tensor:
+    """A zeroed workspace per (device, stream, geometry): the fused kernels'
+    completion counters return to zero after every call, but calls on two
+    streams must not share them."""
+    ws = cache.get(key)
+    if ws is None:
+        ws = torch.zeros(max(nbytes, 1), dtype=torch.uint8, device=gpu)
+        cache[key] = ws
+    return ws
 
 
 def qsrt_linear_launcher(
@@ -200,9 +223,10 @@ def qsrt_linear_launcher(
     gpu = payload.device
     if x.device != gpu or out.device != gpu:
         raise ValueError("x, out and the payload must be on one GPU")
-    if payload.data_ptr() % 4:
-        raise ValueError("the payload must be 4-byte aligned")
+    if payload.data_ptr() % 16:
+        raise ValueError("the payload must be 16-byte aligned")
     bits = _check_record_bits(record_bits)
+    _check_record_count(bits, k_tiles, n_tiles, rate_axis)
     m = x.shape[0]
     labels = rate_labels(codebook, rate_axis=rate_axis, device=gpu)
     su = sv = None
@@ -246,9 +270,10 @@ def qsrt_linear(
     ``F.linear(x, decode_qsrt_exl3_weight(...).T)`` without the bf16 weight
     it materializes (scripts/stream_k3_pytorch.py:771-775).  Beyond
     ``FUSED_MAX_ROWS`` rows (prefill), where the fused kernel would decode
-    the weight once per 16 rows, the matrix is decoded once to bf16
-    (``kq_qsrt_decode_weight``) and applied with the bf16 GEMM - the
-    reference's own path, with its bf16 weight rounding."""
+    the weight once per 16 rows, ``kq_qsrt_linear`` rotates the rows, decodes
+    the regularized weight once to its exact E4M3 label bytes and runs the
+    MXFP8 MFMA linear, then rotates the output: fp32 and fp16 rows keep fp32
+    accuracy (exact three-term bf16 split); bf16 rows are rotated to bf16."""
 
     if rate_axis not in ("k", "n"):
         raise ValueError("rate_axis must be 'k' or 'n'")
@@ -262,9 +287,10 @@ def qsrt_linear(
     if x.shape[-1] != k:
         raise ValueError(f"x has {x.shape[-1]} features, the matrix has K = {k}")
     bits = _check_record_bits(record_bits)
+    _check_record_count(bits, k_tiles, n_tiles, rate_axis)
     out_dtype = x.dtype if out_dtype is None else out_dtype
     (g, xg), gpu, host = N.to_gpu([payload, x])
-    g = N.aligned(g, 4)
+    g = N.aligned(g, 16)
     rows = xg.reshape(-1, k)
     rows = rows if rows.stride(-1) == 1 else rows.contiguous()
     m = rows.shape[0]
@@ -275,28 +301,15 @@ def qsrt_linear(
             raise ValueError("suh and svh must match the K and N dimensions")
         su = N.aligned(suh.to(device=gpu, dtype=torch.float32).reshape(-1), 4)
         sv = N.aligned(svh.to(device=gpu, dtype=torch.float32).reshape(-1), 4)
-    if m > FUSED_MAX_ROWS:
-        dense = decode_qsrt_payload(g, k_tiles=k_tiles, n_tiles=n_tiles, rate_axis=rate_axis, record_bits=bits,
-                                    suh=su, svh=sv, codebook=codebook, out_dtype=torch.bfloat16, transposed=True)
-        out = torch.nn.functional.linear(rows.to(torch.bfloat16), dense).to(out_dtype)
-        out = out.reshape(*x.shape[:-1], n)
-        return out if host is None else out.to(host)
     out = torch.empty(m, n, dtype=out_dtype, device=gpu)
     need = int(N.library().kq_qsrt_linear_workspace_size(max(m, 1), k_tiles, n_tiles)) if m else 0
     if need < 0:
         raise RuntimeError("kq_qsrt_linear_workspace_size: no HIP device")
-    # one zeroed workspace per geometry: its counters return to zero after
-    # every call, but their place depends on the sizes
-    ws = None
-    if need:
-        key = (gpu, m, k_tiles, n_tiles)
-        ws = _LINEAR_WORKSPACES.get(key)
-        if ws is None:
-            ws = torch.zeros(need, dtype=torch.uint8, device=gpu)
-            _LINEAR_WORKSPACES[key] = ws
+    stream = N.stream(gpu)
+    ws = _workspace(_LINEAR_WORKSPACES, (gpu, stream.value, m, k_tiles, n_tiles), need, gpu) if need else None
     N.call("kq_qsrt_linear", N.ptr(rows), N.DTYPE_CODES[rows.dtype], m, rows.stride(0) if m else k, N.ptr(g),
            g.numel(), k_tiles, n_tiles, 0 if rate_axis == "k" else 1, bits, N.ptr(labels), N.ptr(su), N.ptr(sv),
-           N.DTYPE_CODES[out_dtype], N.ptr(out), n, N.ptr(ws) if need else None, need, N.stream(gpu))
+           N.DTYPE_CODES[out_dtype], N.ptr(out), n, N.ptr(ws) if need else None, need, stream)
     out = out.reshape(*x.shape[:-1], n)
     return out if host is None else out.to(host)
 
@@ -344,7 +357,7 @@ class QSRTExperts:
                     raise ValueError(f"expert {e} {kind}: payload must be {words} int16 words")
                 if suh.numel() != k or svh.numel() != n:
                     raise ValueError(f"expert {e} {kind}: suh / svh must have {k} / {n} values")
-                p = N.aligned(payload.to(gpu), 4)
+                p = N.aligned(payload.to(gpu), 16)  # the kernels stage 16-byte pieces by direct loads
                 prefix = torch.tensor([0, *torch.tensor(list(bits)).cumsum(0).tolist()], dtype=torch.int32,
                                       device=gpu)
                 su = N.aligned(suh.to(device=gpu, dtype=torch.float32).reshape(-1), 4)
@@ -401,17 +414,12 @@ def qsrt_expert_forward(
         need = int(N.library().kq_qsrt_moe_workspace_size(tokens, topk, h_tiles, i_tiles))
         if need < 0:
             raise RuntimeError("kq_qsrt_moe_workspace_size: no HIP device")
-        # one zeroed workspace per geometry: its counters return to zero after
-        # every call, but their place depends on the sizes
-        key = (gpu, tokens, topk, h_tiles, i_tiles)
-        ws = _MOE_WORKSPACES.get(key)
-        if ws is None:
-            ws = torch.zeros(max(need, 1), dtype=torch.uint8, device=gpu)
-            _MOE_WORKSPACES[key] = ws
+        stream = N.stream(gpu)
+        ws = _workspace(_MOE_WORKSPACES, (gpu, stream.value, tokens, topk, h_tiles, i_tiles), need, gpu)
         act = N.ACT_SITU if activation == "situ" else N.ACT_SWIGLU
         N.call("kq_qsrt_moe_decode", act, float(beta), float(linear_beta), N.ptr(xg), N.DTYPE_CODES[xg.dtype],
                tokens, xg.stride(0), N.ptr(ids), N.ptr(wts), topk, N.ptr(experts.descriptors), experts.experts,
                h_tiles, i_tiles, 0 if experts.rate13_axis == "k" else 1, 0 if experts.rate2_axis == "k" else 1,
                N.ptr(experts.labels), N.DTYPE_CODES[out_dtype], N.ptr(out), experts.hidden, N.ptr(ws), need,
-               N.stream(gpu))
+               stream)
     return out if host is None else out.to(host)

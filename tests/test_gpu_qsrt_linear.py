@@ -7,7 +7,9 @@ through the rotated weight must agree with the f64 product to within 4e-6
 of max |ref| for fp32 output (fp32 products and sums over K <= 2048), and
 bf16 output must be that result rounded once (within one bf16 ulp of the
 f64 value).  Row counts cover every row tile (1, 2, 4, 8), several row
-groups, single- and multi-chunk K splits, both rate axes and mixed rates."""
+groups, single- and multi-chunk K splits, both rate axes and mixed rates,
+and the prefill form past FUSED_MAX_ROWS rows (fp32 rows within 8e-6 of max
+|ref|, one-hot rows bit-exact)."""
 
 from __future__ import annotations
 
@@ -174,29 +176,91 @@ def test_every_finite_e4m3_label_converts_exactly(gpu):
     assert np.array_equal(out.cpu().numpy(), want)
 
 
-def test_prefill_rows_take_the_decoded_bf16_path(gpu):
-    """Beyond FUSED_MAX_ROWS rows the matrix is decoded once to bf16 and
-    applied with the bf16 GEMM (the reference's path, bf16 result): equal
-    to bf16(x) @ bf16(W) in f64 up to fp32 accumulation and the bf16 output
-    rounding, and within bf16 rounding of the exact product."""
-    k_tiles, n_tiles, bits = 32, 16, (3, 4)
-    payload = _random_matrix(k_tiles, n_tiles, "n", bits, 41)
-    suh, svh = _scales(k_tiles, n_tiles, 42)
-    m = qsrt.FUSED_MAX_ROWS + 37
-    x = np.random.default_rng(43).standard_normal((m, k_tiles * 16)).astype(np.float32)
-    args = dict(k_tiles=k_tiles, n_tiles=n_tiles, rate_axis="n", record_bits=bits, suh=torch.from_numpy(suh),
-                svh=torch.from_numpy(svh))
-    got = qsrt.qsrt_linear(torch.from_numpy(x).to(gpu), torch.from_numpy(payload).to(gpu), out_dtype=torch.float32,
-                           **args).cpu().numpy().astype(np.float64)
-    w = oq.decode_qsrt_weight(payload, k_tiles, n_tiles, bits, "n", _LABELS, suh, svh)
-    xb = torch.from_numpy(x).to(torch.bfloat16).double().numpy()
-    wb = torch.from_numpy(w).to(torch.bfloat16).double().numpy()
-    ref_b = xb @ wb
-    # bf16 output rounding, plus weights whose fp32 decode sits next to a bf16
-    # rounding boundary and rounds the other way (a 1-ulp weight change)
-    assert np.all(np.abs(got - ref_b) <= np.abs(ref_b) * 2.0 ** -8 + 2.0 ** -10 * np.abs(ref_b).max())
-    exact = x.astype(np.float64) @ w
-    assert np.abs(got - exact).max() <= 2e-2 * np.abs(exact).max()
+@pytest.mark.parametrize("rate_axis,m,shape,record_bits", [
+    ("n", qsrt.FUSED_MAX_ROWS + 1, (32, 16), (3, 4)),
+    ("k", 100, (24, 40), (2, 4, 3)),
+    ("n", 257, (64, 24), (4, 2, 3)),
+])
+def test_prefill_rows_match_oracle(gpu, rate_axis, m, shape, record_bits):
+    """More than FUSED_MAX_ROWS rows take kq_qsrt_linear's prefill form
+    (rows rotated, the regularized weight decoded once to E4M3 label bytes,
+    the MXFP8 MFMA linear, the output rotated).  fp32 rows keep fp32
+    accuracy (exact three-term bf16 split): within 8e-6 of max |ref| of the
+    f64 product, rotated or regularized; bf16 rows are rotated to bf16, so
+    their bar is bf16 rounding of the rotated rows (4e-3 of max |ref|)."""
+    k_tiles, n_tiles = shape
+    payload = _random_matrix(k_tiles, n_tiles, rate_axis, record_bits, m + 40)
+    suh, svh = _scales(k_tiles, n_tiles, m + 41)
+    x = np.random.default_rng(m + 42).standard_normal((m, k_tiles * 16)).astype(np.float32)
+    p = torch.from_numpy(payload).to(gpu)
+    xg = torch.from_numpy(x).to(gpu)
+    base = dict(k_tiles=k_tiles, n_tiles=n_tiles, rate_axis=rate_axis, record_bits=record_bits)
+    for rotated in (True, False):
+        args = dict(base, suh=torch.from_numpy(suh), svh=torch.from_numpy(svh)) if rotated else base
+        ref = oq.qsrt_linear(x, payload, k_tiles, n_tiles, record_bits, rate_axis, _LABELS,
+                             suh if rotated else None, svh if rotated else None)
+        got = qsrt.qsrt_linear(xg, p, **args).cpu().numpy().astype(np.float64)
+        rel = np.abs(got - ref).max() / np.abs(ref).max()
+        print(f"prefill m={m} rotated={rotated} fp32 max-rel {rel:.2e}", flush=True)
+        assert rel <= 8e-6
+        xb = xg.to(torch.bfloat16)
+        refb = oq.qsrt_linear(xb.float().cpu().numpy(), payload, k_tiles, n_tiles, record_bits, rate_axis,
+                              _LABELS, suh if rotated else None, svh if rotated else None)
+        gotb = qsrt.qsrt_linear(xb, p, out_dtype=torch.float32, **args).cpu().numpy().astype(np.float64)
+        relb = np.abs(gotb - refb).max() / np.abs(refb).max()
+        print(f"prefill m={m} rotated={rotated} bf16 rows max-rel {relb:.2e}", flush=True)
+        assert relb <= (4e-3 if rotated else 8e-6)
+
+
+def test_prefill_one_hot_rows_read_the_weight_exactly(gpu):
+    """One-hot fp32 rows through the prefill form of the regularized product
+    return the weight bit for bit: the E4M3 label bytes the decode writes,
+    their unit E8M0 scales and the exact split."""
+    k_tiles, n_tiles, record_bits = 16, 24, (2, 4, 3)
+    payload = _random_matrix(k_tiles, n_tiles, "n", record_bits, 61)
+    want = oq.decode_qsrt_weight(payload, k_tiles, n_tiles, record_bits, "n", _LABELS)
+    rows = np.arange(0, k_tiles * 16, 3)
+    assert rows.size > qsrt.FUSED_MAX_ROWS
+    x = np.zeros((rows.size, k_tiles * 16), dtype=np.float32)
+    x[np.arange(rows.size), rows] = 1.0
+    got = qsrt.qsrt_linear(torch.from_numpy(x).to(gpu), torch.from_numpy(payload).to(gpu), k_tiles=k_tiles,
+                           n_tiles=n_tiles, rate_axis="n", record_bits=record_bits)
+    assert np.array_equal(got.cpu().numpy(), want[rows])
+
+
+def test_payload_alignment(gpu):
+    """The fast kernels stage 16-byte pieces by direct loads: the decode
+    entry point takes its first kernel for a payload 4 bytes past a 16-byte
+    boundary (same weight), the linear entry point rejects one, and the
+    Python functions copy such a payload to an aligned buffer."""
+    from kquant_amd import _native as N
+
+    k_tiles, n_tiles, bits = 16, 16, (3, 2)  # two 128-column records along n
+    payload = _random_matrix(k_tiles, n_tiles, "n", bits, 71)
+    big = torch.zeros(payload.size + 16, dtype=torch.int16, device=gpu)
+    p = big[2:2 + payload.size]
+    p.copy_(torch.from_numpy(payload))
+    assert p.data_ptr() % 16 == 4
+    labels = qsrt.rate_labels(device=gpu)
+    want = qsrt.decode_qsrt_payload(p.clone(), k_tiles=k_tiles, n_tiles=n_tiles, rate_axis="n", record_bits=bits)
+    out = torch.empty_like(want)
+    N.call("kq_qsrt_decode_weight", N.ptr(p), p.numel(), k_tiles, n_tiles, 1, bytes(bits), N.ptr(labels), None,
+           None, N.DT_F32, N.ptr(out), out.shape[1], 0, N.stream(gpu))
+    assert torch.equal(out, want)
+    x = torch.randn(2, k_tiles * 16, device=gpu)
+    y = torch.empty(2, n_tiles * 16, device=gpu)
+    need = int(N.library().kq_qsrt_linear_workspace_size(2, k_tiles, n_tiles))
+    ws = torch.zeros(max(need, 256), dtype=torch.uint8, device=gpu)
+    with pytest.raises(RuntimeError, match="16-byte aligned"):
+        N.call("kq_qsrt_linear", N.ptr(x), N.DT_F32, 2, x.shape[1], N.ptr(p), p.numel(), k_tiles, n_tiles, 1,
+               bytes(bits), N.ptr(labels), None, None, N.DT_F32, N.ptr(y), y.shape[1], N.ptr(ws), need,
+               N.stream(gpu))
+    args = dict(k_tiles=k_tiles, n_tiles=n_tiles, rate_axis="n", record_bits=bits)
+    assert torch.equal(qsrt.qsrt_linear(x, p, **args), qsrt.qsrt_linear(x, p.clone(), **args))
+    with pytest.raises(ValueError, match="16-byte aligned"):
+        qsrt.qsrt_linear_launcher(x, p, y, **args)
+    with pytest.raises(ValueError, match="record rates"):
+        qsrt.qsrt_linear(x, p.clone(), k_tiles=k_tiles, n_tiles=n_tiles, rate_axis="n", record_bits=(3,))
 
 
 def test_chunks_spanning_records_of_different_rates(gpu):

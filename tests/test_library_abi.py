@@ -107,8 +107,8 @@ def test_qsrt_linear_argument_errors_need_no_gpu():
     bad_rate[9] = bytes([3, 5])
     assert lib.kq_qsrt_linear(*bad_rate) == _native.KQ_ERR_INVALID and b"rate 5" in lib.kq_last_error()
     odd = list(args)
-    odd[4] = ctypes.c_void_p(258)
-    assert lib.kq_qsrt_linear(*odd) == _native.KQ_ERR_INVALID and b"4-byte aligned" in lib.kq_last_error()
+    odd[4] = ctypes.c_void_p(260)  # 4 bytes past a 16-byte boundary: the direct loads need 16
+    assert lib.kq_qsrt_linear(*odd) == _native.KQ_ERR_INVALID and b"16-byte aligned" in lib.kq_last_error()
     half = list(args)
     half[11] = fake
     assert lib.kq_qsrt_linear(*half) == _native.KQ_ERR_INVALID and b"suh and svh" in lib.kq_last_error()
