@@ -385,7 +385,12 @@ int kq_trellis_unpack(const int16_t* packed, int64_t tiles, int bits, int states
  * out_dtype values with row stride ldo, [K, N] or, with KQ_QSRT_TRANSPOSED,
  * [N, K] (the loader's dense orientation).  Both dimensions are multiples of
  * 128, at most 1024 records.  The regularized weight is exact; the rotated
- * one equals the reference's fp32 matmuls up to fp32 rounding. */
+ * one equals the reference's fp32 matmuls up to fp32 rounding.  A payload
+ * and label table both 16-byte aligned take the direct-load kernel, others
+ * a generic one with the same result.  out_dtype KQ_QSRT_OUT_E4M3 writes the
+ * regularized weight's E4M3 label bytes themselves (suh = svh = NULL,
+ * aligned buffers): the weight operand of an MXFP8 product with unit scales. */
+#define KQ_QSRT_OUT_E4M3 3
 int kq_qsrt_decode_weight(const int16_t* payload, int64_t payload_words, int64_t k_tiles,
                           int64_t n_tiles, int rate_axis, const uint8_t* record_bits,
                           const uint8_t* labels, const float* suh, const float* svh, int out_dtype,
@@ -411,7 +416,14 @@ int kq_qsrt_decode_states(const int16_t* states, int64_t k_tiles, int64_t n_tile
  * out_dtype values [rows, ldo >= N]; fp32 arithmetic throughout (the
  * activation rows are rotated in fp32, the weight is never rounded to
  * bf16), so the result is the exact product up to fp32 summation order.
- * Meant for decode-sized batches: every 16 rows decode the weight once more.
+ * Up to 32 rows (decode batches) the weight is decoded inside the product,
+ * once per 16 rows.  From 33 rows on (prefill) the call runs in four
+ * launches: the activation rows rotated by suh and the 128-point blockwise
+ * Hadamard, the regularized weight decoded once to its E4M3 labels, the
+ * MXFP8 MFMA linear (kq_mx_linear_f32 for fp32 / fp16 x, exact to fp32
+ * summation order; kq_mx_linear for bf16 x, whose rotated rows are rounded
+ * to bf16 first), and the output rotated by 1/128, the Hadamard and svh.
+ * payload and labels must be 16-byte aligned (KQ_ERR_INVALID otherwise).
  * workspace: kq_qsrt_linear_workspace_size(rows, k_tiles, n_tiles) bytes
  * (may be 0), 256-byte aligned and zeroed before its first use with these
  * sizes; each call leaves its completion counters at zero again, so it
@@ -426,7 +438,7 @@ int kq_qsrt_linear(const void* x, int x_dtype, int64_t rows, int64_t ldx, const 
                    void* stream);
 
 /* One QSRT-coded matrix as kq_qsrt_moe_decode reads it (device pointers):
- * its packed payload (4-byte aligned), record_prefix [records + 1] uint32
+ * its packed payload (16-byte aligned), record_prefix [records + 1] uint32
  * with record_prefix[r] = the sum of the rates of the records before r (so
  * record r has rate record_prefix[r + 1] - record_prefix[r], 2..4), and its
  * suh [K] / svh [N] fp32 scales. */
@@ -451,7 +463,7 @@ typedef struct {
  * along rate13_axis, w2 along rate2_axis (0 = k, 1 = n), payload sizes as
  * their records require (not checked here: the descriptors live on the
  * device).  x [tokens, ldx >= H] x_dtype, route_ids int32 / route_weights
- * fp32 [tokens, topk], labels 2 x 3 x 65536 E4M3 bytes: the K2..K4 state
+ * fp32 [tokens, topk], labels (16-byte aligned) 2 x 3 x 65536 E4M3 bytes: the K2..K4 state
  * labels (as kq_qsrt_decode_weight) for w1 / w3, then for w2 (a codebook
  * may depend on the rate axis, kquant/sqg_e4m3.py:305-340), out [tokens,
  * ldo >= H] out_dtype.  Two launches; deterministic.  workspace:
@@ -480,6 +492,20 @@ int64_t kq_sqg_quantize_workspace_size(int bits, int workgroups);
 int kq_sqg_quantize_tiles(const float* tiles, int64_t n_tiles, const uint8_t* lut, int bits,
                           int tailbite_context, float* out_tiles, int16_t* out_states, void* workspace,
                           int64_t workspace_bytes, int workgroups, void* stream);
+
+/* The same search against a procedural EXL3 control codebook
+ * (quantize_tiles_procedural_cuda, kquant/csrc/sqg_quantize.cu:261-330, with
+ * the decoders of kquant/csrc/exl3_compat/quant/codebook.cuh):
+ *   codebook 1, MCG:  x = state * 0xCBAC1FED mod 2^32,
+ *                     x = (x & 0x8fff8fff) ^ 0x3b603b60, label = fp16(lo + hi)
+ *                     of the two fp16 halves of x;
+ *   codebook 2, MUL1: x = state * 0x83DCD12D mod 2^32, h = fp16(1024 + the
+ *                     sum of x's bytes), label = fp16(h * 0x1eee + 0xc931)
+ *                     (fp16 bit patterns, one rounding).
+ * Arguments and workspace as kq_sqg_quantize_tiles, without the table. */
+int kq_sqg_quantize_tiles_procedural(const float* tiles, int64_t n_tiles, int bits, int codebook,
+                                     int tailbite_context, float* out_tiles, int16_t* out_states,
+                                     void* workspace, int64_t workspace_bytes, int workgroups, void* stream);
 
 /* ---------------------------------------------------- scale-plane codecs --
  * Lossless codings of a uint8 E8M0 scale plane [rows, cols], cols <= 255,

@@ -104,6 +104,7 @@ SIGNATURES: dict[str, list] = {
     "kq_qsrt_decode_weight": [_VP, _I64, _I64, _I64, _INT, _VP, _VP, _VP, _VP, _INT, _VP, _I64, _U32, _VP],
     "kq_qsrt_decode_states": [_VP, _I64, _I64, _INT, _VP, _VP, _VP, _VP, _INT, _VP, _I64, _U32, _VP],
     "kq_sqg_quantize_tiles": [_VP, _I64, _VP, _INT, _INT, _VP, _VP, _VP, _I64, _INT, _VP],
+    "kq_sqg_quantize_tiles_procedural": [_VP, _I64, _INT, _INT, _INT, _VP, _VP, _VP, _I64, _INT, _VP],
     "kq_qsrt_moe_decode": [_INT, _F32, _F32, _VP, _INT, _I64, _I64, _VP, _VP, _INT, _VP, _INT, _I64, _I64, _INT,
                            _INT, _VP, _INT, _VP, _I64, _VP, _I64, _VP],
     "kq_qsrt_linear": [_VP, _INT, _I64, _I64, _VP, _I64, _I64, _I64, _INT, _VP, _VP, _VP, _VP, _INT, _VP, _I64,

@@ -251,7 +251,7 @@ __device__ __forceinline__ float load_x(const void* x, int dtype, int64_t i) {
 // output codes of store_out: KQ_DT_* and, for the regularized weight only,
 // its E4M3 label bytes (every value is an E4M3 label, so the conversion
 // returns the label byte exactly)
-constexpr int OUT_E4M3 = 3;
+constexpr int OUT_E4M3 = KQ_QSRT_OUT_E4M3;
 
 __device__ __forceinline__ void store_out(void* out, int dtype, int64_t i, float v) {
   if (dtype == KQ_DT_F32) reinterpret_cast<float*>(out)[i] = v;

@@ -24,6 +24,18 @@
 // thread evaluating node pairs with packed fp16 arithmetic.  The decisions
 // (K bits per node and step, packed as the reference packs them) go to a
 // per-workgroup global workspace for the traceback.
+//
+// The same search runs against the two procedural EXL3 control codebooks of
+// kquant/csrc/exl3_compat/quant/codebook.cuh (sqg_quantize.cu:261-330), whose
+// label of a state is computed, not looked up (no LDS table then):
+//   MCG  (1): x = state * 0xCBAC1FED mod 2^32; x = (x & 0x8fff8fff) ^ 0x3b603b60;
+//             label = fp16(lo + hi), lo / hi the fp16 numbers x's two halves encode
+//             (codebook.cuh:50-59, 64-79);
+//   MUL1 (2): x = state * 0x83DCD12D mod 2^32; h = the fp16 1024 + (sum of x's
+//             four bytes); label = fp16(h * fp16(0x1eee) + fp16(0xc931)), one
+//             rounding (codebook.cuh:27-47, 80-92).
+// The products of successive predecessors differ by C << (16 - K) mod 2^32,
+// so each predecessor costs an add, as in qsrt_quantize_tiles_kernel.cuh:131-145.
 #include "kq_internal.h"
 
 namespace kq {
@@ -62,7 +74,31 @@ __device__ __forceinline__ h2_t pair_labels(uint32_t word16) {
 
 __device__ __forceinline__ int bitrev5(int v) { return (int)(__builtin_bitreverse32((uint32_t)v) >> 27); }
 
-template <int K>
+// codebook ids: 0 = an SQG E4M3 table, 1 = MCG, 2 = MUL1
+template <int CB> constexpr uint32_t cb_mult() { return CB == 1 ? 0xCBAC1FEDu : 0x83DCD12Du; }
+
+// procedural labels of states s and s + 1 from their products x0 = s C and
+// x1 = x0 + C (mod 2^32)
+template <int CB>
+__device__ __forceinline__ h2_t procedural_pair(uint32_t x0, uint32_t x1) {
+  if constexpr (CB == 1) {
+    const uint32_t v0 = (x0 & 0x8fff8fffu) ^ 0x3b603b60u;
+    const uint32_t v1 = (x1 & 0x8fff8fffu) ^ 0x3b603b60u;
+    const uint32_t lo = (v0 & 0xffffu) | (v1 << 16);
+    const uint32_t hi = (v0 >> 16) | (v1 & 0xffff0000u);
+    return __builtin_bit_cast(h2_t, lo) + __builtin_bit_cast(h2_t, hi);
+  } else {
+    // v_sad_u8 against zero: the sum of the four bytes, plus 0x6400 (1024.0)
+    const uint32_t s0 = __builtin_amdgcn_sad_u8(x0, 0u, 0x6400u);
+    const uint32_t s1 = __builtin_amdgcn_sad_u8(x1, 0u, 0x6400u);
+    h2_t k_inv, k_bias;
+    k_inv[0] = k_inv[1] = __builtin_bit_cast(_Float16, (uint16_t)0x1eee);   // 1 / 147.7
+    k_bias[0] = k_bias[1] = __builtin_bit_cast(_Float16, (uint16_t)0xc931); // -10.38
+    return __builtin_elementwise_fma(__builtin_bit_cast(h2_t, (s0 & 0xffffu) | (s1 << 16)), k_inv, k_bias);
+  }
+}
+
+template <int K, int CB>
 __global__ __launch_bounds__(THREADS) void sqg_viterbi_kernel(const float* __restrict__ tiles, int64_t n_tiles,
                                                               const uint8_t* __restrict__ lut, int ctx,
                                                               float* __restrict__ out_tiles,
@@ -70,8 +106,9 @@ __global__ __launch_bounds__(THREADS) void sqg_viterbi_kernel(const float* __res
                                                               uint8_t* __restrict__ dec_ws) {
   constexpr int E = edges<K>(), PAIRS = E / 2, PER = PAIRS / THREADS, Q = 1 << K;
   constexpr int KR = 16 - K, PSTEP = 1 << (16 - 2 * K), RB = row_bytes<K>();
+  constexpr uint32_t CM = cb_mult<CB>(), CSTEP = CM << KR;
   static_assert(PER >= 1 && PAIRS % THREADS == 0, "node pairs per thread");
-  __shared__ __attribute__((aligned(16))) uint8_t lab[65536];  // [pair][k][2]
+  __shared__ __attribute__((aligned(16))) uint8_t lab[CB == 0 ? 65536 : 16];  // [pair][k][2]
   __shared__ __attribute__((aligned(16))) _Float16 cost[2][E];
   __shared__ _Float16 w16[256];
   __shared__ float red_c[THREADS];
@@ -80,9 +117,11 @@ __global__ __launch_bounds__(THREADS) void sqg_viterbi_kernel(const float* __res
   const int tid = threadIdx.x;
   uint8_t* dec = dec_ws + (int64_t)blockIdx.x * 256 * RB;
 
-  for (int s = tid; s < 65536; s += THREADS) {
-    const int k = s >> KR, o = s & (E - 1);
-    lab[(o >> 1) * (2 * Q) + 2 * k + (o & 1)] = lut[s];
+  if constexpr (CB == 0) {
+    for (int s = tid; s < 65536; s += THREADS) {
+      const int k = s >> KR, o = s & (E - 1);
+      lab[(o >> 1) * (2 * Q) + 2 * k + (o & 1)] = lut[s];
+    }
   }
 
   int cb = 0;  // cost[cb] = the buffer the next step writes; cost[cb ^ 1] its input
@@ -109,7 +148,9 @@ __global__ __launch_bounds__(THREADS) void sqg_viterbi_kernel(const float* __res
           const int p = tid + THREADS * j;  // node pair (2p, 2p + 1)
           const int in0 = (2 * p) >> K;
           uint32_t words[Q / 2];  // two predecessors' label pairs per word
-          if constexpr (K == 2) {
+          uint32_t x0 = (uint32_t)(2 * p) * CM;  // product of state (0 << KR) | 2p
+          if constexpr (CB != 0) {
+          } else if constexpr (K == 2) {
             const u32x2_t v = *reinterpret_cast<const u32x2_t*>(lab + p * 2 * Q);
             words[0] = v[0];
             words[1] = v[1];
@@ -131,7 +172,14 @@ __global__ __launch_bounds__(THREADS) void sqg_viterbi_kernel(const float* __res
 #pragma unroll
           for (int k = 0; k < Q; ++k) {
             const int in = in0 + k * PSTEP;
-            const h2_t d = pair_labels(words[k >> 1] >> (16 * (k & 1))) - w2;
+            h2_t label;
+            if constexpr (CB == 0) {
+              label = pair_labels(words[k >> 1] >> (16 * (k & 1)));
+            } else {
+              label = procedural_pair<CB>(x0, x0 + CM);
+              x0 += CSTEP;
+            }
+            const h2_t d = label - w2;
             h2_t err;
             if (i == 0) {
               err = d * d;
@@ -232,8 +280,13 @@ __global__ __launch_bounds__(THREADS) void sqg_viterbi_kernel(const float* __res
         const int prev_edge = (decision_at(i, edge) << (16 - 2 * K)) | (edge >> K);
         const int state = ((prev_edge << K) | edge) & 0xffff;
         out_states[tile * 256 + i] = (int16_t)(uint16_t)state;
-        const int k = state >> KR, o = state & (E - 1);
-        out_tiles[tile * 256 + i] = (float)e4m3_to_f16(lab[(o >> 1) * (2 * Q) + 2 * k + (o & 1)]);
+        if constexpr (CB == 0) {
+          const int k = state >> KR, o = state & (E - 1);
+          out_tiles[tile * 256 + i] = (float)e4m3_to_f16(lab[(o >> 1) * (2 * Q) + 2 * k + (o & 1)]);
+        } else {
+          const uint32_t x = (uint32_t)state * CM;
+          out_tiles[tile * 256 + i] = (float)procedural_pair<CB>(x, x + CM)[0];
+        }
         edge = prev_edge;
       }
     }
@@ -251,27 +304,66 @@ extern "C" int64_t kq_sqg_quantize_workspace_size(int bits, int workgroups) {
   return (int64_t)workgroups * 256 * rb;
 }
 
+namespace {
+
+template <int CB>
+void launch_viterbi(int bits, unsigned grid, hipStream_t st, const float* tiles, int64_t n_tiles, const uint8_t* lut,
+                    int ctx, float* out_tiles, int16_t* out_states, uint8_t* ws) {
+  if (bits == 2)
+    sqg_viterbi_kernel<2, CB><<<grid, THREADS, 0, st>>>(tiles, n_tiles, lut, ctx, out_tiles, out_states, ws);
+  else if (bits == 3)
+    sqg_viterbi_kernel<3, CB><<<grid, THREADS, 0, st>>>(tiles, n_tiles, lut, ctx, out_tiles, out_states, ws);
+  else
+    sqg_viterbi_kernel<4, CB><<<grid, THREADS, 0, st>>>(tiles, n_tiles, lut, ctx, out_tiles, out_states, ws);
+}
+
+// shared checks of both entry points; 1 = nothing to do, 0 = launch, <0 = error
+int check_search(const char* fn, const char* kname, const float* tiles, int64_t n_tiles, int bits,
+                 int tailbite_context, float* out_tiles, int16_t* out_states, void* workspace,
+                 int64_t workspace_bytes, int workgroups) {
+  if (bits < 2 || bits > 4) return kq_fail(KQ_ERR_INVALID, "%s: %s supports K2--K4", fn, kname);
+  if (tailbite_context < 1 || tailbite_context > 128)
+    return kq_fail(KQ_ERR_INVALID, "%s: tailbite_context must be in 1..128", fn);
+  if (n_tiles < 0 || workgroups <= 0) return kq_fail(KQ_ERR_INVALID, "%s: bad tile or workgroup count", fn);
+  if (n_tiles == 0) return 1;
+  if (!tiles || !out_tiles || !out_states || !workspace) return kq_fail(KQ_ERR_INVALID, "%s: null buffer", fn);
+  if (workspace_bytes < kq_sqg_quantize_workspace_size(bits, workgroups))
+    return kq_fail(KQ_ERR_INVALID, "%s: workspace too small", fn);
+  return 0;
+}
+
+}  // namespace
+
 extern "C" int kq_sqg_quantize_tiles(const float* tiles, int64_t n_tiles, const uint8_t* lut, int bits,
                                      int tailbite_context, float* out_tiles, int16_t* out_states, void* workspace,
                                      int64_t workspace_bytes, int workgroups, void* stream) {
   const char* fn = "kq_sqg_quantize_tiles";
-  if (bits < 2 || bits > 4) return kq_fail(KQ_ERR_INVALID, "%s: SQG validation kernel supports K2--K4", fn);
-  if (tailbite_context < 1 || tailbite_context > 128)
-    return kq_fail(KQ_ERR_INVALID, "%s: tailbite_context must be in 1..128", fn);
-  if (n_tiles < 0 || workgroups <= 0) return kq_fail(KQ_ERR_INVALID, "%s: bad tile or workgroup count", fn);
-  if (n_tiles == 0) return KQ_OK;
-  if (!tiles || !lut || !out_tiles || !out_states || !workspace)
-    return kq_fail(KQ_ERR_INVALID, "%s: null buffer", fn);
-  if (workspace_bytes < kq_sqg_quantize_workspace_size(bits, workgroups))
-    return kq_fail(KQ_ERR_INVALID, "%s: workspace too small", fn);
+  const int rc = check_search(fn, "SQG validation kernel", tiles, n_tiles, bits, tailbite_context, out_tiles,
+                              out_states, workspace, workspace_bytes, workgroups);
+  if (rc) return rc > 0 ? KQ_OK : rc;
+  if (!lut) return kq_fail(KQ_ERR_INVALID, "%s: null buffer", fn);
   const unsigned grid = (unsigned)(n_tiles < workgroups ? n_tiles : workgroups);
-  hipStream_t st = (hipStream_t)stream;
-  uint8_t* ws = (uint8_t*)workspace;
-  if (bits == 2)
-    sqg_viterbi_kernel<2><<<grid, THREADS, 0, st>>>(tiles, n_tiles, lut, tailbite_context, out_tiles, out_states, ws);
-  else if (bits == 3)
-    sqg_viterbi_kernel<3><<<grid, THREADS, 0, st>>>(tiles, n_tiles, lut, tailbite_context, out_tiles, out_states, ws);
+  launch_viterbi<0>(bits, grid, (hipStream_t)stream, tiles, n_tiles, lut, tailbite_context, out_tiles, out_states,
+                    (uint8_t*)workspace);
+  return kq_check_launch(hipGetLastError(), fn);
+}
+
+extern "C" int kq_sqg_quantize_tiles_procedural(const float* tiles, int64_t n_tiles, int bits, int codebook,
+                                                int tailbite_context, float* out_tiles, int16_t* out_states,
+                                                void* workspace, int64_t workspace_bytes, int workgroups,
+                                                void* stream) {
+  const char* fn = "kq_sqg_quantize_tiles_procedural";
+  if (codebook != 1 && codebook != 2)
+    return kq_fail(KQ_ERR_INVALID, "%s: procedural codebook must be 1 (MCG) or 2 (MUL1)", fn);
+  const int rc = check_search(fn, "procedural control", tiles, n_tiles, bits, tailbite_context, out_tiles,
+                              out_states, workspace, workspace_bytes, workgroups);
+  if (rc) return rc > 0 ? KQ_OK : rc;
+  const unsigned grid = (unsigned)(n_tiles < workgroups ? n_tiles : workgroups);
+  if (codebook == 1)
+    launch_viterbi<1>(bits, grid, (hipStream_t)stream, tiles, n_tiles, nullptr, tailbite_context, out_tiles,
+                      out_states, (uint8_t*)workspace);
   else
-    sqg_viterbi_kernel<4><<<grid, THREADS, 0, st>>>(tiles, n_tiles, lut, tailbite_context, out_tiles, out_states, ws);
+    launch_viterbi<2>(bits, grid, (hipStream_t)stream, tiles, n_tiles, nullptr, tailbite_context, out_tiles,
+                      out_states, (uint8_t*)workspace);
   return kq_check_launch(hipGetLastError(), fn);
 }

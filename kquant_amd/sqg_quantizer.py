@@ -12,9 +12,13 @@ so the same states and values) and:
       [N, 256], states int16 [N, 256]);
   ``install_sqg_quantizer(quantizer_module)`` (sqg_quantizer.py:64-164)
       the same patch, with the same argument checks and messages, routing the
-      SQG laws to that kernel.  The MCG / MUL1 procedural controls (a ``None``
-      entry in ``sqg_e4m3_luts_by_bits``) are research controls of the
-      reference's extension that are not built here; they raise.
+      SQG laws to that kernel and a ``None`` entry of ``sqg_e4m3_luts_by_bits``
+      to the MCG control;
+  ``quantize_tiles_procedural(tiles, bits, codebook, tailbite_context)``
+      the extension call ``quantize_tiles_procedural`` (sqg_quantize.cu:
+      261-330): the same search against the procedural EXL3 codebooks,
+      1 = MCG, 2 = MUL1 (kquant/csrc/exl3_compat/quant/codebook.cuh:27-92),
+      whose labels the kernel computes per state.
 """
 
 from __future__ import annotations
@@ -54,14 +58,45 @@ def quantize_tiles_sqg(tiles: torch.Tensor, lut: torch.Tensor, bits: int,
     table = N.aligned(lut.to(device=device).contiguous(), 16)
     out = torch.empty_like(x)
     states = torch.empty(x.shape, dtype=torch.int16, device=device)
-    wg = _workgroups(device)
-    need = int(N.library().kq_sqg_quantize_workspace_size(bits, wg))
+    ws = _workspace(device, bits)
+    N.call("kq_sqg_quantize_tiles", N.ptr(x), x.shape[0], N.ptr(table), bits, int(tailbite_context), N.ptr(out),
+           N.ptr(states), N.ptr(ws), ws.numel(), _workgroups(device), N.stream(device))
+    return out, states
+
+
+def _workspace(device: torch.device, bits: int) -> torch.Tensor:
+    need = int(N.library().kq_sqg_quantize_workspace_size(bits, _workgroups(device)))
     ws = _WORKSPACES.get((device, bits))
     if ws is None or ws.numel() < need:
         ws = torch.empty(need, dtype=torch.uint8, device=device)
         _WORKSPACES[(device, bits)] = ws
-    N.call("kq_sqg_quantize_tiles", N.ptr(x), x.shape[0], N.ptr(table), bits, int(tailbite_context), N.ptr(out),
-           N.ptr(states), N.ptr(ws), ws.numel(), wg, N.stream(device))
+    return ws
+
+
+def quantize_tiles_procedural(tiles: torch.Tensor, bits: int, codebook: int,
+                              tailbite_context: int = 128) -> tuple[torch.Tensor, torch.Tensor]:
+    """Trellis-quantize fp32 tiles [N, 256] against the MCG (1) or MUL1 (2)
+    procedural codebook."""
+
+    if not tiles.is_cuda:
+        raise ValueError("input_tiles must be CUDA")
+    if tiles.dtype != torch.float32:
+        raise ValueError("input_tiles must be FP32")
+    if tiles.ndim != 2 or tiles.shape[1] != 256:
+        raise ValueError("input_tiles must have shape [tiles, 256]")
+    if bits not in (2, 3, 4):
+        raise ValueError("procedural control supports K2--K4")
+    if codebook not in (1, 2):
+        raise ValueError("procedural codebook must be 1 (MCG) or 2 (MUL1)")
+    if not 1 <= tailbite_context <= 128:
+        raise ValueError("tailbite_context must be in 1..128")
+    device = tiles.device
+    x = N.aligned(tiles.contiguous(), 4)
+    out = torch.empty_like(x)
+    states = torch.empty(x.shape, dtype=torch.int16, device=device)
+    ws = _workspace(device, bits)
+    N.call("kq_sqg_quantize_tiles_procedural", N.ptr(x), x.shape[0], bits, codebook, int(tailbite_context),
+           N.ptr(out), N.ptr(states), N.ptr(ws), ws.numel(), _workgroups(device), N.stream(device))
     return out, states
 
 
@@ -97,8 +132,8 @@ def install_sqg_quantizer(quantizer_module) -> None:
                 codebook = rate_codebooks[bits]
             except KeyError as exc:
                 raise ValueError(f"missing rate-specific SQG K{bits} LUT") from exc
-            if codebook is None:
-                raise NotImplementedError("the MCG/MUL1 procedural controls are not built in kquant_amd")
+            if codebook is None:  # the MCG control
+                return quantize_tiles_procedural(tiles, bits, 1, int(quant_args.get("tailbite_context", 128)))
         elif codebook is None:
             if mode != "normal":
                 raise ValueError("the supported R44 mode is 'normal'")

@@ -18,9 +18,11 @@ Contents, each following the cited reference code:
       kquant/tp_simulator.py:72-80, 114-160; kquant/pack/qsrt_validation.py:240-258.
   sqg_* tables
       kquant/sqg_e4m3.py:38-60, 84-127, 197-302, 356-438.
-  sqg_quantize_tiles
+  sqg_quantize_tiles / procedural_labels / sqg_quantize_tiles_procedural
       C restatement in sqg_viterbi.c of the SQG trellis (Viterbi) quantizer,
-      kquant/csrc/qsrt_quantize_tiles_kernel.cuh, kquant/csrc/sqg_quantize.cu.
+      kquant/csrc/qsrt_quantize_tiles_kernel.cuh, kquant/csrc/sqg_quantize.cu,
+      and of the MCG / MUL1 procedural codebooks,
+      kquant/csrc/exl3_compat/quant/codebook.cuh:27-92.
   scale_plane (submodule): X4T and KQSC scale-plane codecs
       kquant/x4t.py, kquant/mxfp4_scale_codec.py.
   ldl (submodule): the encoder's Hessian finalize — Hadamard rotation,
@@ -62,6 +64,10 @@ def _load():
         lib.mxo_pack_codes.restype = None
         lib.sqgo_quantize_tiles.argtypes = [vp, ctypes.c_int64, vp, i32, i32, vp, vp]
         lib.sqgo_quantize_tiles.restype = None
+        lib.sqgo_quantize_tiles_f16.argtypes = [vp, ctypes.c_int64, vp, i32, i32, vp, vp]
+        lib.sqgo_quantize_tiles_f16.restype = None
+        lib.sqgo_procedural_labels.argtypes = [i32, vp]
+        lib.sqgo_procedural_labels.restype = None
         lib.sqgo_f64_to_f16.argtypes = [vp, ctypes.c_int64, vp]
         lib.sqgo_f64_to_f16.restype = None
         lib.mxo_f32_to_e4m3.argtypes = [ctypes.c_float]
@@ -152,6 +158,28 @@ def sqg_quantize_tiles(tiles: np.ndarray, lut: np.ndarray, bits: int, tailbite_c
     out = np.empty_like(x)
     states = np.empty(x.shape, dtype=np.int16)
     lib.sqgo_quantize_tiles(_ptr(x), x.shape[0], _ptr(lab), bits, tailbite_context, _ptr(out), _ptr(states))
+    return out, states
+
+
+def procedural_labels(codebook: int) -> np.ndarray:
+    """fp16 labels (as float16) of all 65536 states of the procedural EXL3
+    codebook 1 (MCG) or 2 (MUL1), sqg_viterbi.c / codebook.cuh:27-92."""
+    if codebook not in (1, 2):
+        raise ValueError("procedural codebook must be 1 (MCG) or 2 (MUL1)")
+    out = np.empty(65536, dtype=np.uint16)
+    _load().sqgo_procedural_labels(codebook, _ptr(out))
+    return out.view(np.float16)
+
+
+def sqg_quantize_tiles_procedural(tiles: np.ndarray, bits: int, codebook: int, tailbite_context: int = 128):
+    """The trellis quantizer against a procedural codebook
+    (quantize_tiles_procedural_cuda, kquant/csrc/sqg_quantize.cu:261-330)."""
+    lib = _load()
+    lab = procedural_labels(codebook).view(np.uint16)
+    x = np.ascontiguousarray(tiles, dtype=np.float32).reshape(-1, 256)
+    out = np.empty_like(x)
+    states = np.empty(x.shape, dtype=np.int16)
+    lib.sqgo_quantize_tiles_f16(_ptr(x), x.shape[0], _ptr(lab), bits, tailbite_context, _ptr(out), _ptr(states))
     return out, states
 
 

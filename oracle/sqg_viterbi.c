@@ -20,6 +20,17 @@
  *   traceback to the node before position 0; closing pass over 0 .. 255
  *   from that node; traceback writes every position's state and label.
  *
+ * The procedural control codebooks (quantize_tiles_procedural_cuda,
+ * kquant/csrc/sqg_quantize.cu:261-330) run the same search on labels
+ * computed per state by the EXL3 decoders of
+ * kquant/csrc/exl3_compat/quant/codebook.cuh:
+ *   MCG (1, :50-59 and :64-79): x = state * 0xCBAC1FED mod 2^32, then
+ *     x = (x & 0x8fff8fff) ^ 0x3b603b60 (lop3 with truth table 0x6a =
+ *     (a & b) ^ c), label = fp16(lo + hi) of x's two halves read as fp16;
+ *   MUL1 (2, :27-47 and :80-92): x = state * 0x83DCD12D mod 2^32, h = the
+ *     fp16 with bits 0x6400 + (sum of x's four bytes) = 1024 + that sum,
+ *     label = fp16(h * fp16(0x1eee) + fp16(0xc931)) rounded once (hfma).
+ *
  * fp16 values are kept as their bit patterns; every operation is computed
  * exactly in double and rounded once to fp16 (nearest, ties to even,
  * subnormals kept, overflow to +inf), which is the IEEE result. */
@@ -136,11 +147,26 @@ static int argmin_cost(const Trellis* t) {
   return best < 0 ? 0 : best;
 }
 
-void sqgo_quantize_tiles(const float* tiles, int64_t n, const uint8_t* lut, int K, int ctx, float* out_tiles,
-                         int16_t* out_states) {
+static uint16_t procedural_label(int codebook, uint32_t state) {
+  if (codebook == 1) {
+    const uint32_t x = ((state * 0xCBAC1FEDu) & 0x8fff8fffu) ^ 0x3b603b60u;
+    return f64_to_f16(f16_to_f64((uint16_t)(x & 0xffffu)) + f16_to_f64((uint16_t)(x >> 16)));
+  }
+  const uint32_t x = state * 0x83DCD12Du;
+  const uint32_t sum = (x & 0xffu) + ((x >> 8) & 0xffu) + ((x >> 16) & 0xffu) + (x >> 24);
+  const double h = f16_to_f64((uint16_t)(0x6400u + sum));
+  return f64_to_f16(h * f16_to_f64(0x1eee) + f16_to_f64(0xc931));
+}
+
+/* fp16 labels of all 65536 states of procedural codebook 1 (MCG) or 2 (MUL1) */
+void sqgo_procedural_labels(int codebook, uint16_t* out) {
+  for (uint32_t s = 0; s < 65536; ++s) out[s] = procedural_label(codebook, s);
+}
+
+/* The search against fp16 labels in state order. */
+void sqgo_quantize_tiles_f16(const float* tiles, int64_t n, const uint16_t* lab, int K, int ctx, float* out_tiles,
+                             int16_t* out_states) {
   const int edges = 65536 >> K;
-  uint16_t* lab = (uint16_t*)malloc(65536 * sizeof(uint16_t));
-  for (int s = 0; s < 65536; ++s) lab[s] = e4m3_to_f16(lut[s]);
 #pragma omp parallel for schedule(dynamic, 1)
   for (int64_t tile = 0; tile < n; ++tile) {
     uint16_t w[256];
@@ -177,6 +203,13 @@ void sqgo_quantize_tiles(const float* tiles, int64_t n, const uint8_t* lut, int 
     free(t.cur);
     free(t.dec);
   }
+}
+
+void sqgo_quantize_tiles(const float* tiles, int64_t n, const uint8_t* lut, int K, int ctx, float* out_tiles,
+                         int16_t* out_states) {
+  uint16_t* lab = (uint16_t*)malloc(65536 * sizeof(uint16_t));
+  for (int s = 0; s < 65536; ++s) lab[s] = e4m3_to_f16(lut[s]);
+  sqgo_quantize_tiles_f16(tiles, n, lab, K, ctx, out_tiles, out_states);
   free(lab);
 }
 

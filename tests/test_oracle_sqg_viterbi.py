@@ -59,3 +59,64 @@ def test_search_is_optimal_against_one_edge_changes(bits):
             assert _path_cost(alt_states, w16, lab16) >= best
         # rate-distortion sanity: about 6 dB per bit (a wrong search is far worse)
         assert float(((out[t] - x[t]) ** 2).mean()) < 0.15 * (2.0 ** (-2 * (bits - 2)))
+
+
+def _state_products(mult: int) -> np.ndarray:
+    """state * mult mod 2^32 for every 16-bit state (numpy's uint32 wraps)."""
+    return np.arange(65536, dtype=np.uint32) * np.uint32(mult)
+
+
+def test_mcg_labels_follow_their_bit_layout():
+    """MCG (kquant/csrc/exl3_compat/quant/codebook.cuh:50-59; multiplier of
+    kquant/exl3_encoder_backend.py:24).  The mask keeps sign, exponent bits
+    0-1 and the mantissa of each half; the xor sets the exponent's top bits
+    to 011 and flips bit 1, so each half is a random sign times
+    2^(e - 15) (1 + m/1024) with e in 12..15: |label| < 4 and, for
+    equidistributed products, E[label^2] = 2 E[h^2] with
+    E[h^2] = (1/4)(4^-3 + 4^-2 + 4^-1 + 1)(7/3) = 595/768."""
+    lab = oracle.procedural_labels(1).astype(np.float64)
+    assert np.all(np.abs(lab) < 4.0)
+    assert abs(lab.mean()) < 0.01
+    assert abs(lab.std() / np.sqrt(2 * 595 / 768) - 1.0) < 0.002
+    # the two halves read as fp16 numbers and added in float32 (exact for
+    # these exponents) with one rounding to fp16: numpy's own arithmetic
+    x = (_state_products(0xCBAC1FED) & np.uint32(0x8FFF8FFF)) ^ np.uint32(0x3B603B60)
+    halves = x.view(np.float16).reshape(-1, 2).astype(np.float32)
+    assert np.array_equal(oracle.procedural_labels(1), (halves[:, 0] + halves[:, 1]).astype(np.float16))
+
+
+def test_mul1_labels_are_scaled_byte_sums():
+    """MUL1 (codebook.cuh:27-47, 80-92; multiplier of
+    kquant/exl3_encoder_backend.py:25): the byte sum s of the product, mean
+    510 and standard deviation sqrt(4 (2^16 - 1) / 12) = 147.8 for uniform
+    bytes, standardised as (s - 510) / 147.7, to within the fp16 rounding of
+    the constants and the result (<= 0.0045 over the label range)."""
+    s = _state_products(0x83DCD12D).view(np.uint8).reshape(-1, 4).astype(np.int64).sum(axis=1)
+    lab = oracle.procedural_labels(2).astype(np.float64)
+    assert np.abs(lab - (s - 510) / 147.7).max() <= 0.0045
+    assert abs(s.mean() - 510) < 1.0 and abs(s.std() - np.sqrt(4 * 65535 / 12)) < 0.5
+    assert abs(lab.std() - 1.0) < 0.005
+    # one label per byte sum: the map s -> label is monotone
+    order = np.argsort(s, kind="stable")
+    assert np.all(np.diff(lab[order]) >= 0)
+
+
+@pytest.mark.parametrize("codebook,bits", [(1, 2), (2, 3), (1, 4), (2, 4)])
+def test_procedural_search_is_optimal_against_one_edge_changes(codebook, bits):
+    lab16 = oracle.procedural_labels(codebook)
+    x = np.random.default_rng(20 + bits).standard_normal((1, 256)).astype(np.float32)
+    out, states = oracle.sqg_quantize_tiles_procedural(x, bits, codebook, 16)
+    span = -(-16 // bits)
+    rng = np.random.default_rng(30 + bits)
+    st = states[0].view(np.uint16).astype(np.int64)
+    edges = st & ((1 << bits) - 1)
+    assert np.array_equal(qsrt.reconstruct_trellis_states(edges, bits).view(np.uint16), st)
+    assert np.array_equal(out[0], lab16[st].astype(np.float32))
+    w16 = x[0].astype(np.float16)
+    best = _path_cost(st, w16, lab16)
+    for p in rng.choice(np.arange(0, 256 - span), 24, replace=False):
+        alt = edges.copy()
+        alt[p] = (alt[p] + rng.integers(1, 1 << bits)) % (1 << bits)
+        alt_states = qsrt.reconstruct_trellis_states(alt, bits).view(np.uint16).astype(np.int64)
+        assert _path_cost(alt_states, w16, lab16) >= best
+    assert float(((out[0] - x[0]) ** 2).mean()) < 0.15 * (2.0 ** (-2 * (bits - 2)))
