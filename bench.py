@@ -587,10 +587,13 @@ def main() -> int:
               / torch.sqrt(sum(torch.randn(65536, 7168, generator=g, device=dev).square() for _ in range(4)) / 4)
               ).to(torch.bfloat16)
         acc = torch.empty(7168, 7168, dtype=torch.float32, device=dev)
+        # stream-K partial slots: one 256 x 256 fp32 tile per CU
+        h_ws_bytes = int(N.library().kq_syrk_accumulate_workspace_size(N.DT_BF16, 65536, 7168, 0))
+        h_ws = torch.empty(max(h_ws_bytes, 256), dtype=torch.uint8, device=dev)
 
         def h_step():
-            N.call("kq_syrk_accumulate", N.DT_BF16, N.ptr(x4), 7168, 65536, 7168, N.ptr(None),
-                   N.ptr(acc), 7168, N.SYRK_OVERWRITE, stream)
+            N.call("kq_syrk_accumulate_ws", N.DT_BF16, N.ptr(x4), 7168, 65536, 7168, N.ptr(None),
+                   N.ptr(acc), 7168, N.SYRK_OVERWRITE, N.ptr(h_ws), h_ws_bytes, stream)
 
         th = _time_loop(torch, h_step, 3, 1)
         flops = workloads.syrk_flops(65536, 7168)
@@ -602,7 +605,7 @@ def main() -> int:
             "roofline": _roofline("mfma", flops / th / 1e12, syrk_pmc),
             "pmc": syrk_pmc,
         }
-        del x4, acc
+        del x4, acc, h_ws
 
     # --------------------------- config 4 (ii) per-expert Hessians, K=2048 --
     if not args.quick and want("hessian_experts"):
@@ -621,7 +624,7 @@ def main() -> int:
         flops = float((counts.double() * k2 * (k2 + 1)).sum())
         hbytes = pairs * k2 * 2 + pairs * 4 + experts * k2 * k2 * 4
         # the kernel writes the upper 256 x 256 tiles of each expert's accumulator
-        he_pmc = _traffic_entry("hessian_experts", "kq::syrk256_kernel<true, true>", pairs * k2 * 2 + pairs * 4
+        he_pmc = _traffic_entry("hessian_experts", "kq::syrk256w_dma_kernel", pairs * k2 * 2 + pairs * 4
                                 + experts * 36 * 256 * 256 * 4)
         result["cfg4_hessian_experts_k2048"] = {
             "workload": "cfg4 (ii): gate^2-weighted X^T X of each expert's routed rows, 65536 tokens "

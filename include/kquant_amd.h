@@ -230,14 +230,32 @@ int kq_mx_linear(int w_fmt, const void* a, int64_t lda, const void* w_q,
  * 16-byte aligned rows), w fp32 [n] or NULL (all ones).  Replaces the chunked
  * fp32 addmm_ of kquant/candidate_hessian.py:98-105 and
  * kquant/capture.py:713-730 (accumulator.addmm_(x.T, x * w[:, None])).
- * Only 128x128 tiles with tile_row <= tile_col of acc [k, k] (row stride
- * ld_acc) are written; kq_syrk_finalize reads exactly those.  With
+ * Only upper tiles (tile_row <= tile_col) of acc [k, k] (row stride ld_acc)
+ * are written: 256x256 tiles for bf16 rows, 128x128 otherwise; both cover
+ * the 128x128 upper tiles, which is what kq_syrk_finalize reads.  With
  * KQ_SYRK_OVERWRITE the tiles are written instead of accumulated (acc need
  * not be initialised).  bf16 rows use bf16 MFMA with exact products; fp16 /
  * fp32 rows and weights use a two-term bf16 split (16 significant bits). */
 int kq_syrk_accumulate(int in_dtype, const void* x, int64_t ld, int64_t n, int64_t k,
                        const float* weights, float* acc, int64_t ld_acc, uint32_t flags,
                        void* stream);
+
+/* kq_syrk_accumulate with a workspace for partial tiles.  When the upper
+ * 256 x 256 tiles fill the rounds of workgroups poorly (fill below 0.72: the
+ * 300 tiles of k = 6144 on 256 CUs fill 0.59), the tile x 32-row work is cut
+ * into one contiguous range per CU (stream-K):
+ * a range that starts inside a tile leaves its part in a partial slot, and a
+ * second launch adds each tile's slots, in range order, to the value the
+ * tile's first range wrote.  Results are deterministic for a given CU count
+ * and agree with kq_syrk_accumulate to fp32 summation order.  Only
+ * unweighted bf16 rows take the split; other calls, or a workspace smaller
+ * than kq_syrk_accumulate_workspace_size (0 when the split does not pay),
+ * run as kq_syrk_accumulate.  workspace: 256-byte aligned, uninitialised,
+ * used by one call at a time (size for the current device's CU count). */
+int64_t kq_syrk_accumulate_workspace_size(int in_dtype, int64_t n, int64_t k, int weighted);
+int kq_syrk_accumulate_ws(int in_dtype, const void* x, int64_t ld, int64_t n, int64_t k,
+                          const float* weights, float* acc, int64_t ld_acc, uint32_t flags,
+                          void* workspace, int64_t workspace_bytes, void* stream);
 
 /* out [k, k] = symmetric(acc) / denominator, then
  * diag(out) += damp * mean(diag(out)).  Mirrors the upper tiles written by

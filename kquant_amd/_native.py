@@ -58,6 +58,7 @@ SIGNATURES: dict[str, list] = {
     "kq_pack_codes": [_VP, _I64, _VP, _VP],
     "kq_decode_bytes": [_INT, _VP, _I64, _INT, _VP, _VP],
     "kq_syrk_accumulate": [_INT, _VP, _I64, _I64, _I64, _VP, _VP, _I64, _U32, _VP],
+    "kq_syrk_accumulate_ws": [_INT, _VP, _I64, _I64, _I64, _VP, _VP, _I64, _U32, _VP, _I64, _VP],
     "kq_syrk_finalize": [_VP, _I64, _I64, _F64, _F32, _VP, _I64, _VP],
     "kq_sym_lerp": [_VP, _F32, _VP, _I64, _F32, _VP, _VP],
     "kq_cov_stats": [_VP, _I64, _VP, _VP, _VP],
@@ -151,6 +152,8 @@ def library() -> ctypes.CDLL:
         lib.kq_qsrt_moe_workspace_size.argtypes = [_I64, _INT, _I64, _I64]
         lib.kq_qsrt_linear_workspace_size.restype = ctypes.c_int64
         lib.kq_qsrt_linear_workspace_size.argtypes = [_I64, _I64, _I64]
+        lib.kq_syrk_accumulate_workspace_size.restype = ctypes.c_int64
+        lib.kq_syrk_accumulate_workspace_size.argtypes = [_INT, _I64, _I64, _INT]
         lib.kq_route_sort_workspace_size.restype = ctypes.c_int64
         lib.kq_route_sort_workspace_size.argtypes = [_I64, _INT, _INT]
         for name, argtypes in SIGNATURES.items():

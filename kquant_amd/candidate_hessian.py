@@ -49,6 +49,23 @@ def _prepare_rows(rows: torch.Tensor, gpu: torch.device) -> tuple[torch.Tensor, 
     return x, k
 
 
+_SPLIT_WORKSPACES: dict[tuple[torch.device, int], torch.Tensor] = {}
+
+
+def _split_workspace(gpu: torch.device, dtype_code: int, n: int, k: int, weighted: bool) -> torch.Tensor | None:
+    """Partial-tile slots of the split launch (None when it does not pay),
+    cached per device and stream: calls sharing slots must not overlap."""
+    need = int(N.library().kq_syrk_accumulate_workspace_size(dtype_code, n, k, int(weighted)))
+    if need <= 0:
+        return None
+    key = (gpu, torch.cuda.current_stream(gpu).stream_id)
+    ws = _SPLIT_WORKSPACES.get(key)
+    if ws is None or ws.numel() < need:
+        ws = torch.empty(need, dtype=torch.uint8, device=gpu)
+        _SPLIT_WORKSPACES[key] = ws
+    return ws
+
+
 def _syrk(x: torch.Tensor, weights: torch.Tensor | None, gpu: torch.device) -> torch.Tensor:
     """Upper-tile accumulator of X^T diag(w) X, [kp, kp] fp32 (kp = padded k)."""
     n, kp = x.shape
@@ -56,8 +73,10 @@ def _syrk(x: torch.Tensor, weights: torch.Tensor | None, gpu: torch.device) -> t
     w = None
     if weights is not None:
         w = N.aligned(weights.detach().to(device=gpu, dtype=torch.float32))
-    N.call("kq_syrk_accumulate", N.DTYPE_CODES[x.dtype], N.ptr(x), kp, n, kp, N.ptr(w),
-           N.ptr(acc), kp, N.SYRK_OVERWRITE, N.stream(gpu))
+    code = N.DTYPE_CODES[x.dtype]
+    ws = _split_workspace(gpu, code, n, kp, w is not None)
+    N.call("kq_syrk_accumulate_ws", code, N.ptr(x), kp, n, kp, N.ptr(w), N.ptr(acc), kp, N.SYRK_OVERWRITE,
+           N.ptr(ws), 0 if ws is None else ws.numel(), N.stream(gpu))
     return acc
 
 

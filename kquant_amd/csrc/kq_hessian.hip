@@ -46,6 +46,22 @@ __device__ __forceinline__ void transpose8x8_b16(const u32x4_t in[8], u32x4_t ou
   }
 }
 
+// w times a packed pair of bf16 values, split into packed bf16 hi (round to
+// nearest) and bf16 lo = the fp32 residual rounded: one v_cvt_pk_bf16_f32 per
+// part and pair.
+__device__ __forceinline__ void split_bf16_pair(uint32_t pair, float w, uint32_t& hi, uint32_t& lo) {
+  float2_t v;
+  v[0] = __builtin_bit_cast(float, pair << 16) * w;
+  v[1] = __builtin_bit_cast(float, pair & 0xffff0000u) * w;
+  const bf16x2_t h = __builtin_convertvector(v, bf16x2_t);
+  const uint32_t hb = __builtin_bit_cast(uint32_t, h);
+  float2_t r;
+  r[0] = v[0] - __builtin_bit_cast(float, hb << 16);
+  r[1] = v[1] - __builtin_bit_cast(float, hb & 0xffff0000u);
+  hi = hb;
+  lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(r, bf16x2_t));
+}
+
 // Split fp32 values into bf16 hi (round to nearest) and bf16 lo = fp32 residual.
 __device__ __forceinline__ void split_bf16(float v, uint32_t& hi, uint32_t& lo) {
   __bf16 h = (__bf16)v;
@@ -454,11 +470,15 @@ __global__ __launch_bounds__(512, 1) void syrk256_kernel(
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < 4; ++j)
           accv[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], accv[i][j], 0, 0, 0);
-          if (WEIGHTED)
+      if (WEIGHTED) {  // residual products after all high parts: no back-to-back accumulator updates
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
             accv[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fbl[j], accv[i][j], 0, 0, 0);
-        }
+      }
     }
     if (s + 1 < steps) store(buf ^ 1);
     __syncthreads();
@@ -507,19 +527,14 @@ using dma::lds_offset_of;
 using dma::make_rsrc;
 using dma::waitcnt_vm;
 
-__global__ __launch_bounds__(512, 1) void syrk256_dma_kernel(
-    const uint16_t* __restrict__ x, int64_t ld, int64_t n, int64_t k, float* __restrict__ acc,
-    int64_t ld_acc, int nt, int overwrite, uint32_t nbytes) {
+// One tile's token range [t_begin, t_end) through the four-stage ring into
+// accv.  Every wave of the workgroup calls it with the same arguments; it
+// starts and ends with the ring idle (all loads landed, all reads done).
+__device__ __forceinline__ void syrk3_range(const i32x4_t rsrc, uint32_t nbytes, int64_t ld, int64_t t_begin,
+                                            int64_t t_end, int64_t row0, int64_t col0, bool share_b,
+                                            float16_t (&accv)[2][4], int wave, int lane) {
   using namespace syrk3;
-  int ti, tj;
-  if (!upper_tile_for_block(blockIdx.x, nt, false, ti, tj)) return;  // spare block
-  const bool share_b = ti == tj;
-  const int64_t row0 = (int64_t)ti * TILE, col0 = (int64_t)tj * TILE;
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const i32x4_t rsrc = make_rsrc(x, nbytes);
   const uint32_t lds0 = lds_offset_of(syrk3_lds);
-
   // Loads: wave w, part q in {0, 1}: token rows 2 (2w + q) + lane / 32 of a
   // stage, this lane's 16-byte slot lane % 32 holds global chunk slot ^ 4 (row % 4).
   int drow[2], dchunk[2];
@@ -533,7 +548,7 @@ __global__ __launch_bounds__(512, 1) void syrk256_dma_kernel(
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
       const int64_t tok = t0 + drow[q];
-      const bool ok = tok < n;
+      const bool ok = tok < t_end;
       const uint32_t base = ok ? (uint32_t)(tok * ld * 2) : nbytes;  // nbytes: first offset past the range
       const uint32_t dst = lds0 + (uint32_t)(2 * SLAB * stage + (2 * wave + q) * 1024);
       load_to_lds16(rsrc, ok ? base + (uint32_t)((row0 + dchunk[q] * 8) * 2) : base, dst);
@@ -542,18 +557,10 @@ __global__ __launch_bounds__(512, 1) void syrk256_dma_kernel(
     }
   };
 
-  const int wm = (wave >> 1) * 64, wn = (wave & 1) * 128;
-  float16_t accv[2][4];
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) accv[i][j][r] = 0.0f;
-
   // Transposed reads: 16-lane group g covers features 16 (g % 2) of a 32-feature
   // block and tokens 8 (g / 2) + [0, 8); lane s16 reads token s16 / 4 (+4 for
   // the second half) and features 4 (s16 % 4) .. +3.
+  const int wm = (wave >> 1) * 64, wn = (wave & 1) * 128;
   const int g16 = lane >> 4, s16 = lane & 15;
   const int trow = 8 * (g16 >> 1) + (s16 >> 2);
   const int xorv = 4 * (s16 >> 2);
@@ -574,17 +581,17 @@ __global__ __launch_bounds__(512, 1) void syrk256_dma_kernel(
   // is done with the stage the next loads overwrite), issue the loads of step
   // s + 3, compute.  Steps past the end load zeros, which keeps the per-step
   // count of outstanding loads fixed.
-  const int64_t steps = (n + BK - 1) / BK;
-  issue(0, 0);
-  issue(1, BK);
-  issue(2, 2 * BK);
+  const int64_t steps = (t_end - t_begin + BK - 1) / BK;
+  issue(0, t_begin);
+  issue(1, t_begin + BK);
+  issue(2, t_begin + 2 * BK);
   for (int64_t s = 0; s < steps; ++s) {
     const int stage = (int)(s & 3);
     if (share_b) __builtin_amdgcn_s_waitcnt(waitcnt_vm(4));
     else __builtin_amdgcn_s_waitcnt(waitcnt_vm(8));
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    issue((stage + 3) & 3, (s + 3) * BK);
+    issue((stage + 3) & 3, t_begin + (s + 3) * BK);
     const unsigned char* a_base = syrk3_lds + 2 * SLAB * stage;
     const unsigned char* b_base = share_b ? a_base : a_base + SLAB;
 #pragma unroll
@@ -611,31 +618,426 @@ __global__ __launch_bounds__(512, 1) void syrk256_dma_kernel(
           accv[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], accv[i][j], 0, 0, 0);
     }
   }
-  __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));  // no load may land after the workgroup ends
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));  // the three steps issued past the end have landed
+  __syncthreads();                            // every wave is done reading the ring
+}
 
+// Store a wave's 64 x 128 part of a 256 x 256 tile: dst[r][c] (row stride
+// ld) for r < rlim, c < clim, written or added.
+__device__ __forceinline__ void syrk3_store(const float16_t (&accv)[2][4], float* dst, int64_t ld, int64_t rlim,
+                                            int64_t clim, bool overwrite, int wave, int lane) {
+  const int wm = (wave >> 1) * 64, wn = (wave & 1) * 128;
   const int ccol = lane & 31, crow = (lane >> 5) * 4;
+  // opaque to the optimiser: keeps a persistent caller from hoisting (and
+  // spilling) the 128 element offsets out of its item loop
+  asm volatile("" : "+s"(ld));
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int64_t gr = row0 + wm + i * 32 + 8 * (r >> 2) + crow + (r & 3);
-        const int64_t gc = col0 + wn + j * 32 + ccol;
-        if (gr < k && gc < k) {
-          float* p = acc + gr * ld_acc + gc;
+        const int64_t gr = wm + i * 32 + 8 * (r >> 2) + crow + (r & 3);
+        const int64_t gc = wn + j * 32 + ccol;
+        if (gr < rlim && gc < clim) {
+          float* p = dst + gr * ld + gc;
           *p = overwrite ? accv[i][j][r] : *p + accv[i][j][r];
         }
       }
 }
 
+// Work split of a stream-K launch: the ntiles * steps units (tile, 32-token
+// step) in tile order are cut into `grid` contiguous ranges, range v =
+// [v units / grid, (v + 1) units / grid).  Workgroup b takes range v(b) =
+// (b % 8) grid / 8 + b / 8, so the workgroups of one XCD (b % 8) hold
+// neighbouring tiles.  A range that starts inside a tile leaves that first
+// part in partial slot v; the fix-up kernel adds the slots of a tile, in
+// ascending v, to the value its first range wrote.
+__device__ __forceinline__ int64_t split_begin(int64_t v, int64_t units, int grid) { return v * units / grid; }
+
+__global__ __launch_bounds__(512, 1) void syrk256_dma_kernel(
+    const uint16_t* __restrict__ x, int64_t ld, int64_t n, int64_t k, float* __restrict__ acc,
+    int64_t ld_acc, int nt, int overwrite, uint32_t nbytes, float* __restrict__ partial) {
+  using namespace syrk3;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const i32x4_t rsrc = make_rsrc(x, nbytes);
+  // Segments: without partial slots, the one tile of this block over every
+  // row; with them, the tile parts of this block's stream-K range.
+  const int grid = gridDim.x;
+  const int64_t b = blockIdx.x;
+  const int64_t v = grid % SYRK_XCDS ? b : (b % SYRK_XCDS) * (grid / SYRK_XCDS) + b / SYRK_XCDS;
+  const int64_t steps = partial ? (n + BK - 1) / BK : 1;
+  const int64_t units = (int64_t)(nt * (nt + 1) / 2) * steps;
+  int64_t r = partial ? split_begin(v, units, grid) : 0;
+  const int64_t r_end = partial ? split_begin(v + 1, units, grid) : 1;
+  while (r < r_end) {
+    int ti, tj;
+    int64_t s0 = 0, s1 = 1, t_begin = 0, t_end = n;
+    if (partial) {
+      const int64_t t = r / steps;
+      s0 = r - t * steps;
+      s1 = s0 + (r_end - r) < steps ? s0 + (r_end - r) : steps;
+      upper_tile_for_block((int)t, nt, true, ti, tj);
+      t_begin = s0 * BK;
+      t_end = s1 * BK < n ? s1 * BK : n;
+    } else if (!upper_tile_for_block(blockIdx.x, nt, false, ti, tj)) {
+      return;  // spare block
+    }
+    const int64_t row0 = (int64_t)ti * TILE, col0 = (int64_t)tj * TILE;
+    float16_t accv[2][4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int q = 0; q < 16; ++q) accv[i][j][q] = 0.0f;
+    syrk3_range(rsrc, nbytes, ld, t_begin, t_end, row0, col0, ti == tj, accv, wave, lane);
+    // a part that starts inside its tile goes to partial slot v (only a
+    // range's first part can); the others are written or added in place
+    const bool to_slot = s0 != 0;
+    float* dst = to_slot ? partial + v * (TILE * TILE) : acc + row0 * ld_acc + col0;
+    syrk3_store(accv, dst, to_slot ? TILE : ld_acc, to_slot ? TILE : k - row0, to_slot ? TILE : k - col0,
+                to_slot || overwrite, wave, lane);
+    r += s1 - s0;
+  }
+}
+
+// acc tile += partial slots of the ranges that start inside it, in ascending
+// range order.  Block (v, y): range v if it is the first to start inside its
+// tile; rows 16 y .. 16 y + 15 of the tile.
+__global__ __launch_bounds__(256) void syrk_splitk_fixup_kernel(const float* __restrict__ partial, int64_t n,
+                                                                int nt, int grid, float* __restrict__ acc,
+                                                                int64_t ld_acc, int64_t k) {
+  const int64_t steps = (n + syrk3::BK - 1) / syrk3::BK;
+  const int64_t units = (int64_t)(nt * (nt + 1) / 2) * steps;
+  const int64_t v = blockIdx.x;
+  const int64_t r0 = split_begin(v, units, grid);
+  if (r0 % steps == 0 || r0 >= units) return;  // starts on a tile boundary: no slot
+  const int64_t t = r0 / steps;
+  if (v > 0 && split_begin(v - 1, units, grid) > t * steps) return;  // not the tile's first slot
+  int ti, tj;
+  upper_tile_for_block((int)t, nt, true, ti, tj);
+  const int64_t row0 = (int64_t)ti * syrk3::TILE, col0 = (int64_t)tj * syrk3::TILE;
+  const int c = threadIdx.x;
+  if (col0 + c >= k) return;
+  for (int rr = 0; rr < 16; ++rr) {
+    const int row = blockIdx.y * 16 + rr;
+    if (row0 + row >= k) break;
+    float* p = acc + (row0 + row) * ld_acc + col0 + c;
+    float sum = *p;
+    for (int64_t u = v; u < grid && split_begin(u, units, grid) < (t + 1) * steps; ++u)
+      if (split_begin(u + 1, units, grid) > split_begin(u, units, grid))  // empty ranges write no slot
+        sum += partial[u * (syrk3::TILE * syrk3::TILE) + row * syrk3::TILE + c];
+    *p = sum;
+  }
+}
+
+// Stream-K pays when the tiles fill the rounds of workgroups poorly: its
+// ranges start at scattered rows, so concurrent workgroups share fewer rows
+// in L2 than one tile per workgroup (which all stream the rows in step).
+// Measured on MI355X at 65,536 rows: 300 tiles (fill 0.59) 11% faster, 528
+// tiles (0.69) 10% faster, 406 tiles (0.79) 15% slower.
+static bool splitk_pays(int ntiles, int cus, int64_t n) {
+  if (cus < 8 || n < 4 * syrk3::BK || (int64_t)ntiles * ((n + syrk3::BK - 1) / syrk3::BK) < 2 * (int64_t)cus)
+    return false;
+  const int rounds = (ntiles + cus - 1) / cus;
+  return (double)ntiles / ((double)rounds * cus) < 0.72;
+}
+
+static int device_cus() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  return cus;
+}
+
+static int64_t syrk_split_bytes(int cus) { return (int64_t)cus * syrk3::TILE * syrk3::TILE * 4; }
+
 static hipError_t launch_syrk256_dma(const void* x, int64_t ld, int64_t n, int64_t k, float* acc,
-                                     int64_t ld_acc, int overwrite, hipStream_t st) {
+                                     int64_t ld_acc, int overwrite, hipStream_t st, void* workspace = nullptr,
+                                     int64_t ws_bytes = 0) {
   const int nt = (int)((k + syrk3::TILE - 1) / syrk3::TILE);
   const int ntiles = nt * (nt + 1) / 2;
+  const uint32_t nbytes = (uint32_t)(n * ld * 2);
+  if (workspace) {
+    const int cus = device_cus();
+    if (splitk_pays(ntiles, cus, n) && ws_bytes >= syrk_split_bytes(cus)) {
+      syrk256_dma_kernel<<<dim3(cus), dim3(512), 0, st>>>((const uint16_t*)x, ld, n, k, acc, ld_acc, nt,
+                                                           overwrite, nbytes, (float*)workspace);
+      hipError_t e = hipGetLastError();
+      if (e != hipSuccess) return e;
+      syrk_splitk_fixup_kernel<<<dim3(cus, syrk3::TILE / 16), dim3(256), 0, st>>>((const float*)workspace, n, nt,
+                                                                                cus, acc, ld_acc, k);
+      return hipGetLastError();
+    }
+  }
   const int blocks = SYRK_XCDS * ((ntiles + SYRK_XCDS - 1) / SYRK_XCDS);
   syrk256_dma_kernel<<<dim3(blocks), dim3(512), 0, st>>>((const uint16_t*)x, ld, n, k, acc, ld_acc, nt,
-                                                          overwrite, (uint32_t)(n * ld * 2));
+                                                          overwrite, nbytes, nullptr);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Weighted grouped bf16 SYRK with direct loads (rows of each group
+// contiguous, no row index).  Same 256 x 256 tiles, waves and transposed
+// reads as syrk256_dma_kernel; X rows go from HBM straight into LDS
+// (global_load_lds_dwordx4: 64-bit addresses, so any row count), 16 tokens a
+// step through a six-stage ring, and the row weights of a step ride along
+// into LDS (wave 0, 16 lanes x 4 bytes).  The weight goes on the A side:
+// once a stage has landed, the workgroup rewrites its A slab in place as the
+// bf16 high part of w x and writes the bf16 residual to a third slab
+// (w x = hi + lo to 16 significant bits), so each product is
+// (a_hi + a_lo) b, two MFMAs, with the B slab exact.  That conversion runs a
+// step ahead of the MFMAs, in the same barrier interval, so the VALU work
+// overlaps the matrix cores.  A diagonal tile loads one slab and keeps it as
+// B, writing hi and lo to the other two.  Rows past the group's end load the
+// group's last row and convert to zeros.
+#ifndef KQ_SYRK4_BK
+#define KQ_SYRK4_BK 16
+#endif
+namespace syrk4 {
+constexpr int TILE = 256;
+constexpr int BK = KQ_SYRK4_BK;   // tokens per step
+constexpr int ROW = TILE * 2;     // bytes per token row
+constexpr int SLAB = BK * ROW;
+constexpr int STAGE = 3 * SLAB;   // raw / hi, B (or hi), lo
+constexpr int NS = 147456 / STAGE;  // ring stages (144 KiB): loads run NS - 3 steps ahead of their conversion
+constexpr int LPW = BK / 16;      // load instructions per wave and slab (two token rows each)
+static_assert(BK == 16 || BK == 32, "steps of 16 or 32 tokens");
+}  // namespace syrk4
+
+__shared__ __attribute__((aligned(16))) unsigned char syrk4_lds[syrk4::NS * syrk4::STAGE];
+__shared__ __attribute__((aligned(16))) float syrk4_w[syrk4::NS][syrk4::BK];
+
+__device__ __forceinline__ void global_load_to_lds16(const void* src, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
+               :
+               : "s"(lds_addr), "v"(src)
+               : "memory", "m0");
+}
+
+__device__ __forceinline__ void global_load_to_lds4(const void* src, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off"
+               :
+               : "s"(lds_addr), "v"(src)
+               : "memory", "m0");
+}
+
+// wait until this wave has at most n (< 16) direct loads in flight, then barrier
+__device__ __forceinline__ void syrk4_wait(int n) {
+  switch (n) {
+#define KQ_WAIT_CASE(c) \
+  case c: __builtin_amdgcn_s_waitcnt(waitcnt_vm(c)); break;
+    KQ_WAIT_CASE(0) KQ_WAIT_CASE(1) KQ_WAIT_CASE(2) KQ_WAIT_CASE(3) KQ_WAIT_CASE(4) KQ_WAIT_CASE(5)
+    KQ_WAIT_CASE(6) KQ_WAIT_CASE(7) KQ_WAIT_CASE(8) KQ_WAIT_CASE(9) KQ_WAIT_CASE(10) KQ_WAIT_CASE(11)
+    KQ_WAIT_CASE(12) KQ_WAIT_CASE(13) KQ_WAIT_CASE(14)
+#undef KQ_WAIT_CASE
+    default: __builtin_amdgcn_s_waitcnt(waitcnt_vm(0)); break;
+  }
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Persistent: `gridDim.x` workgroups walk the items (group rank, tile) in
+// snake order (round q gives item q G + b to workgroup b, reversed on odd
+// rounds).  Ranks order the groups by row count, largest first (ties by
+// index), computed once per workgroup in LDS for up to LPT_MAX_GROUPS groups
+// (natural order beyond); every item's result is independent of the order.
+__shared__ int syrk4_rank_order[LPT_MAX_GROUPS];
+__shared__ int syrk4_rank_size[LPT_MAX_GROUPS];
+
+__global__ __launch_bounds__(512, 1) void syrk256w_dma_kernel(
+    const uint16_t* __restrict__ x, int64_t ld, int64_t k, const float* __restrict__ w, float* __restrict__ acc,
+    int nt, const int64_t* __restrict__ offsets, int groups, int square_w) {
+  using namespace syrk4;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool lpt = groups <= LPT_MAX_GROUPS;
+  if (lpt) {
+    for (int g = tid; g < groups; g += 512) {
+      const int64_t ng = offsets[g + 1] - offsets[g];
+      syrk4_rank_size[g] = ng < 0x7fffffff ? (int)ng : 0x7fffffff;
+    }
+    __syncthreads();
+    for (int g = tid; g < groups; g += 512) {
+      const int ng = syrk4_rank_size[g];
+      int rank = 0;
+      for (int h = 0; h < groups; ++h) {
+        const int nh = syrk4_rank_size[h];
+        rank += (nh > ng || (nh == ng && h < g)) ? 1 : 0;
+      }
+      syrk4_rank_order[rank] = g;
+    }
+    __syncthreads();
+  }
+  const int ntiles = nt * (nt + 1) / 2;
+  const int64_t items = (int64_t)ntiles * groups;
+  const int grid = gridDim.x;
+  const uint32_t lds0 = lds_offset_of(syrk4_lds), wl0 = lds_offset_of(syrk4_w);
+  // loads: instruction q of wave w moves token rows 2 (LPW w + q) + lane / 32;
+  // lane % 32 is the LDS slot, holding global chunk slot ^ 4 (row % 4) of the
+  // row's 256 features (row % 4 is the same for every q)
+  const int drow = 2 * LPW * wave + (lane >> 5);
+  const int dchunk = (lane & 31) ^ (4 * (drow & 3));
+  // conversion: chunk c = tid + 512 u -> token row c / 32, LDS slot c % 32
+  // (the layout is kept, so the swizzle does not matter)
+  const int cr = tid >> 5;
+  const int coff = cr * ROW + (tid & 31) * 16;
+  // transposed reads (as syrk256_dma_kernel, 16-token steps)
+  const int wm = (wave >> 1) * 64, wn = (wave & 1) * 128;
+  const int g16 = lane >> 4, s16 = lane & 15;
+  const int trow = 8 * (g16 >> 1) + (s16 >> 2);
+  const int xorv = 4 * (s16 >> 2);
+  int offa[2], offb[4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int f = wm + i * 32 + 16 * (g16 & 1) + 4 * (s16 & 3);
+    offa[i] = trow * ROW + (((f >> 3) ^ xorv) << 4) + (f & 7) * 2;
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int f = wn + j * 32 + 16 * (g16 & 1) + 4 * (s16 & 3);
+    offb[j] = trow * ROW + (((f >> 3) ^ xorv) << 4) + (f & 7) * 2;
+  }
+
+  for (int64_t q = 0;; ++q) {
+    const int64_t item = q * grid + ((q & 1) ? grid - 1 - blockIdx.x : blockIdx.x);
+    if (item >= items) break;
+    const int rank = (int)(item / ntiles);
+    const int64_t g = lpt ? syrk4_rank_order[rank] : rank;
+    int ti, tj;
+    upper_tile_for_block((int)(item - (int64_t)rank * ntiles), nt, true, ti, tj);
+    const bool share = ti == tj;
+    const int64_t row0 = (int64_t)ti * TILE, col0 = (int64_t)tj * TILE;
+    const int64_t list0 = offsets[g];
+    const int n = (int)(offsets[g + 1] - list0);
+    const int per_step = LPW * (share ? 1 : 2) + (wave == 0 ? 1 : 0);
+
+    float16_t accv[2][4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) accv[i][j][r] = 0.0f;
+
+    const int steps = (n + BK - 1) / BK;
+    if (steps > 0) {
+      // a chunk past feature k (edge tiles) reads feature 0 instead: such
+      // features only reach accumulator rows / columns past k, never stored
+      const int64_t fa = row0 + dchunk * 8, fb = col0 + dchunk * 8;
+      const uint16_t* xa = x + list0 * ld + (fa < k ? fa : 0);
+      const uint16_t* xb = x + list0 * ld + (fb < k ? fb : 0);
+      const float* wg = w + list0;
+      auto issue = [&](int stage, int t0) {
+#pragma unroll
+        for (int q = 0; q < LPW; ++q) {
+          const int pos = t0 + drow + 2 * q < n ? t0 + drow + 2 * q : n - 1;
+          const int64_t roff = (int64_t)pos * ld;
+          const uint32_t dst = lds0 + (uint32_t)(STAGE * stage + (LPW * wave + q) * 1024);
+          global_load_to_lds16(xa + roff, dst);  // A (raw) slab
+          if (!share) global_load_to_lds16(xb + roff, dst + SLAB);
+        }
+        if (wave == 0 && lane < BK) {
+          const int wp = t0 + lane < n ? t0 + lane : n - 1;
+          global_load_to_lds4(wg + wp, wl0 + (uint32_t)(stage * BK * 4));
+        }
+      };
+      // rows past the end get weight 0: finite rows then convert to zeros
+      auto convert = [&](int stage, int t0) {
+        unsigned char* st = syrk4_lds + STAGE * stage;
+#pragma unroll
+        for (int u = 0; u < BK / 16; ++u) {
+          const int off = coff + u * 16 * ROW, row = cr + 16 * u;
+          const u32x4_t raw = *reinterpret_cast<const u32x4_t*>(st + off);
+          float wt = syrk4_w[stage][row];
+          if (square_w) wt *= wt;
+          if (t0 + row >= n) wt = 0.0f;
+          u32x4_t hi, lo;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            uint32_t h, l;
+            split_bf16_pair(raw[e], wt, h, l);
+            hi[e] = h;
+            lo[e] = l;
+          }
+          // non-diagonal: hi replaces the raw A slab; diagonal: the raw slab stays (as B)
+          *reinterpret_cast<u32x4_t*>(st + (share ? SLAB : 0) + off) = hi;
+          *reinterpret_cast<u32x4_t*>(st + 2 * SLAB + off) = lo;
+        }
+      };
+      const int hi_slab = share ? SLAB : 0, b_slab = share ? 0 : SLAB;
+
+      // Step s: wait for step s + 1's loads (three later steps may still be
+      // in flight) and barrier (step s's conversion is complete; every wave
+      // is done with step s - 1's stage), issue the loads of step s + NS - 1
+      // into that stage, convert step s + 1, then run step s's MFMAs.  Steps
+      // past the end load the last row again (never converted or used),
+      // which keeps the per-step count of outstanding loads fixed.
+#pragma unroll
+      for (int st = 0; st < NS - 1; ++st) issue(st, st * BK);
+      syrk4_wait(per_step * (NS - 2));  // step 0 has landed
+      convert(0, 0);
+      int stage = 0;
+      for (int s = 0; s < steps; ++s) {
+        const int next = stage == NS - 1 ? 0 : stage + 1;
+        const int prev = stage == 0 ? NS - 1 : stage - 1;
+        syrk4_wait(per_step * (NS - 3));
+        issue(prev, (s + NS - 1) * BK);
+        const unsigned char* base = syrk4_lds + STAGE * stage;
+#pragma unroll
+        for (int kk = 0; kk < BK / 16; ++kk) {
+          const int ko = kk * 16 * ROW;
+          bf16x8_t fh[2], fl[2], fb[4];
+#pragma unroll
+          for (int i = 0; i < 2; ++i) {
+            const s16x4_t h0 = lds_read_tr16(base + hi_slab, ko + offa[i]);
+            const s16x4_t h1 = lds_read_tr16(base + hi_slab, ko + offa[i] + 4 * ROW);
+            fh[i] = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(h0, h1, 0, 1, 2, 3, 4, 5, 6, 7));
+            const s16x4_t l0 = lds_read_tr16(base + 2 * SLAB, ko + offa[i]);
+            const s16x4_t l1 = lds_read_tr16(base + 2 * SLAB, ko + offa[i] + 4 * ROW);
+            fl[i] = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(l0, l1, 0, 1, 2, 3, 4, 5, 6, 7));
+          }
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const s16x4_t b0 = lds_read_tr16(base + b_slab, ko + offb[j]);
+            const s16x4_t b1 = lds_read_tr16(base + b_slab, ko + offb[j] + 4 * ROW);
+            fb[j] = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(b0, b1, 0, 1, 2, 3, 4, 5, 6, 7));
+          }
+          // (the last step converts the stage loaded past the end: unused, harmless)
+          if (kk == 0) convert(next, (s + 1) * BK);
+          // the eight high-part products, then the eight residual ones: the two
+          // updates of an accumulator are eight MFMAs apart, not back to back
+#pragma unroll
+          for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              accv[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fh[i], fb[j], accv[i][j], 0, 0, 0);
+#pragma unroll
+          for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              accv[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fl[i], fb[j], accv[i][j], 0, 0, 0);
+        }
+        stage = next;
+      }
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));  // the loads issued past the end have landed
+      __syncthreads();                            // every wave is done with the ring
+    }
+    syrk3_store(accv, acc + g * k * k + row0 * k + col0, k, k - row0, k - col0, true, wave, lane);
+  }
+}
+
+static hipError_t launch_syrk256w_dma(const void* x, int64_t ld, int64_t k, const float* w, float* acc,
+                                      const int64_t* offsets, int groups, int square_w, hipStream_t st) {
+  const int nt = (int)((k + syrk4::TILE - 1) / syrk4::TILE);
+  const int64_t items = (int64_t)(nt * (nt + 1) / 2) * groups;
+  int cus = device_cus();
+  if (cus <= 0) cus = 256;
+  const int grid = (int)(items < cus ? items : cus);
+  syrk256w_dma_kernel<<<dim3(grid), dim3(512), 0, st>>>((const uint16_t*)x, ld, k, w, acc, nt, offsets, groups,
+                                                          square_w);
   return hipGetLastError();
 }
 
@@ -920,9 +1322,41 @@ static hipError_t launch_syrk(const void* x, int64_t ld, int64_t n, int64_t k, c
   return hipGetLastError();
 }
 
+// The direct-load kernel serves unweighted bf16 rows whose byte range fits
+// the buffer descriptor's 32-bit offsets.
+static bool dma_syrk(int in_dtype, const void* weights, int64_t n, int64_t ld) {
+  return in_dtype == KQ_DT_BF16 && !weights && n * ld * 2 < ((int64_t)1 << 32) - 4096;
+}
+
+static int syrk_accumulate(int in_dtype, const void* x, int64_t ld, int64_t n, int64_t k, const float* weights,
+                           float* acc, int64_t ld_acc, uint32_t flags, void* workspace, int64_t ws_bytes,
+                           void* stream);
+
+extern "C" int64_t kq_syrk_accumulate_workspace_size(int in_dtype, int64_t n, int64_t k, int weighted) {
+  if (n < 0 || k <= 0) return -1;
+  if (!dma_syrk(in_dtype, weighted ? (const void*)1 : nullptr, n, k)) return 0;
+  const int cus = device_cus();
+  const int nt = (int)((k + syrk3::TILE - 1) / syrk3::TILE);
+  return splitk_pays(nt * (nt + 1) / 2, cus, n) ? syrk_split_bytes(cus) : 0;
+}
+
+extern "C" int kq_syrk_accumulate_ws(int in_dtype, const void* x, int64_t ld, int64_t n, int64_t k,
+                                     const float* weights, float* acc, int64_t ld_acc, uint32_t flags,
+                                     void* workspace, int64_t workspace_bytes, void* stream) {
+  if (workspace && (workspace_bytes < 0 || kq_misaligned(workspace, 256)))
+    return kq_fail(KQ_ERR_INVALID, "kq_syrk_accumulate_ws: workspace must be 256-byte aligned");
+  return syrk_accumulate(in_dtype, x, ld, n, k, weights, acc, ld_acc, flags, workspace, workspace_bytes, stream);
+}
+
 extern "C" int kq_syrk_accumulate(int in_dtype, const void* x, int64_t ld, int64_t n, int64_t k,
                                   const float* weights, float* acc, int64_t ld_acc, uint32_t flags,
                                   void* stream) {
+  return syrk_accumulate(in_dtype, x, ld, n, k, weights, acc, ld_acc, flags, nullptr, 0, stream);
+}
+
+static int syrk_accumulate(int in_dtype, const void* x, int64_t ld, int64_t n, int64_t k, const float* weights,
+                           float* acc, int64_t ld_acc, uint32_t flags, void* workspace, int64_t ws_bytes,
+                           void* stream) {
   if (in_dtype < KQ_DT_BF16 || in_dtype > KQ_DT_F32)
     return kq_fail(KQ_ERR_INVALID, "kq_syrk_accumulate: unknown input dtype %d", in_dtype);
   if (n < 0 || k <= 0 || k % 8 != 0 || ld < k || ld % 8 != 0 || ld_acc < k)
@@ -941,8 +1375,8 @@ extern "C" int kq_syrk_accumulate(int in_dtype, const void* x, int64_t ld, int64
   if (in_dtype == KQ_DT_BF16) {
     if (weighted)
       e = launch_syrk256<true, false>(x, ld, n, k, weights, acc, ld_acc, overwrite, st);
-    else if (n * ld * 2 < ((int64_t)1 << 32) - 4096)  // the buffer descriptor's 32-bit range
-      e = launch_syrk256_dma(x, ld, n, k, acc, ld_acc, overwrite, st);
+    else if (dma_syrk(in_dtype, weights, n, ld))
+      e = launch_syrk256_dma(x, ld, n, k, acc, ld_acc, overwrite, st, workspace, ws_bytes);
     else
       e = launch_syrk256<false, false>(x, ld, n, k, weights, acc, ld_acc, overwrite, st);
   } else if (in_dtype == KQ_DT_F16) {
@@ -991,15 +1425,18 @@ extern "C" int kq_syrk_grouped(int in_dtype, const void* x, int64_t ld, const in
     return kq_fail(KQ_ERR_INVALID,
                    "kq_syrk_grouped: need 1 <= groups <= 65535, k %% 8 == 0, ld >= k, ld %% 8 == 0 "
                    "(groups=%d k=%lld ld=%lld)", groups, (long long)k, (long long)ld);
-  if (kq_misaligned(x, 16) || kq_misaligned(offsets, 8) || kq_misaligned(row_index, 4))
-    return kq_fail(KQ_ERR_INVALID, "kq_syrk_grouped: misaligned rows, offsets or index");
+  if (kq_misaligned(x, 16) || kq_misaligned(offsets, 8) || kq_misaligned(row_index, 4) ||
+      kq_misaligned(weights, 4))
+    return kq_fail(KQ_ERR_INVALID, "kq_syrk_grouped: misaligned rows, offsets, index or weights");
   if (k > 16384) return kq_fail(KQ_ERR_LIMIT, "kq_syrk_grouped: k=%lld exceeds 16384", (long long)k);
   const int sq = (flags & KQ_SYRK_SQUARE_WEIGHTS) ? 1 : 0;
   hipStream_t st = (hipStream_t)stream;
   hipError_t e;
   const bool weighted = weights != nullptr;
   if (in_dtype == KQ_DT_BF16)
-    e = weighted ? launch_syrk256<true, true>(x, ld, 0, k, weights, acc, k, 1, st, offsets, row_index, groups, sq)
+    e = weighted && !row_index
+            ? launch_syrk256w_dma(x, ld, k, weights, acc, offsets, groups, sq, st)
+        : weighted ? launch_syrk256<true, true>(x, ld, 0, k, weights, acc, k, 1, st, offsets, row_index, groups, sq)
                  : launch_syrk256<false, true>(x, ld, 0, k, weights, acc, k, 1, st, offsets, row_index, groups, sq);
   else if (in_dtype == KQ_DT_F16)
     e = weighted ? launch_syrk<1, true, true, true>(x, ld, 0, k, weights, acc, k, 1, st, offsets, row_index, groups, sq)

@@ -255,6 +255,29 @@ def test_expert_hessians_from_rows_cfg4_expert_shape(gpu):
             assert rel <= 1e-5, (gi, rel)
 
 
+@pytest.mark.parametrize("k", [200, 520])
+def test_expert_hessians_from_rows_edge_tiles(gpu, k):
+    """Weighted grouped rows at widths that end inside a 256-feature tile
+    (the direct-load kernel reads a valid chunk for features past k), plain
+    fp32 weights with zeros, an empty group first and last, ragged steps."""
+    sizes = [0, 5, 40, 333, 17, 0]
+    n = sum(sizes)
+    x = workloads.student_t4(n, k, seed=k)
+    offsets = torch.tensor(np.concatenate([[0], np.cumsum(sizes)]), dtype=torch.int64)
+    w = torch.rand(n, generator=torch.Generator().manual_seed(k)) * 3.0
+    w[::5] = 0.0
+    h, den = ch.expert_hessians_from_rows(x.to(gpu), offsets, w)
+    for gi, (a, b) in enumerate(zip(offsets[:-1].tolist(), offsets[1:].tolist())):
+        if a == b or not float(w[a:b].sum()):
+            assert float(den[gi]) == 0.0 and not torch.any(h[gi] != 0)
+            continue
+        ref, denom = oracle.weighted_covariance(x[a:b].float().numpy(), w[a:b].numpy())
+        got = h[gi].cpu().numpy()
+        assert float(den[gi]) == pytest.approx(denom, rel=1e-12)
+        assert np.linalg.norm(got - ref) / np.linalg.norm(ref) <= 1e-5, gi
+        assert np.array_equal(got, got.T)
+
+
 def test_build_expert_hessians_composes_reference_steps(gpu):
     """kquant/qsrt_candidates.py:534-618 on one expert, both H2 policies and a
     nonzero H13 alpha, against the tested primitives composed as the reference does."""
@@ -296,3 +319,45 @@ def test_covariance_comparison_matches_oracle(gpu):
     want = oracle.covariance_comparison(r.numpy(), c.numpy())
     for key, value in want.items():
         assert got[key] == pytest.approx(value, rel=1e-9, abs=1e-12), key
+
+
+@pytest.mark.parametrize("n,k", [(4096, 2048), (2048, 6144), (3001, 520)])
+def test_split_launch_matches_plain_launch(gpu, n, k):
+    """The stream-K launch (kq_syrk_accumulate_ws): 36 tiles shared by many
+    ranges, 300 tiles split at range boundaries, and ragged edge tiles with a
+    row count that is not a multiple of 32.  Written (overwrite) and
+    accumulated onto a prefilled accumulator; against exact float64 X^T X
+    and the one-tile-per-workgroup launch; repeat calls bitwise identical."""
+    print(f"case split syrk n={n} k={k}", flush=True)
+    lib = N.library()
+    need = int(lib.kq_syrk_accumulate_workspace_size(N.DT_BF16, n, k, 0))
+    assert need > 0, "the split launch should pay for this shape"
+    assert lib.kq_syrk_accumulate_workspace_size(N.DT_BF16, n, k, 1) == 0  # weighted rows: plain launch
+    x = workloads.student_t4(n, k, seed=n + 3 * k, dtype=torch.bfloat16).to(gpu)
+    ws = torch.empty(need, dtype=torch.uint8, device=gpu).fill_(0xFF)  # slots need no initialisation
+    st = N.stream(gpu)
+    acc_plain = torch.zeros(k, k, dtype=torch.float32, device=gpu)
+    N.call("kq_syrk_accumulate", N.DT_BF16, N.ptr(x), k, n, k, None, N.ptr(acc_plain), k, N.SYRK_OVERWRITE, st)
+    runs = []
+    for _ in range(2):
+        acc = torch.full((k, k), float("nan"), dtype=torch.float32, device=gpu)
+        N.call("kq_syrk_accumulate_ws", N.DT_BF16, N.ptr(x), k, n, k, None, N.ptr(acc), k, N.SYRK_OVERWRITE,
+               N.ptr(ws), need, st)
+        runs.append(acc)
+    upper = torch.ones(k, k, dtype=torch.bool, device=gpu).triu()  # the lower triangle is not written
+    assert torch.equal(runs[0][upper], runs[1][upper])
+    got = runs[0][upper].double()
+    x64 = x.double()
+    exact = (x64.T @ x64)[upper]
+    rel = float(torch.linalg.vector_norm(got - exact) / torch.linalg.vector_norm(exact))
+    plain = acc_plain[upper].double()
+    rel_plain = float(torch.linalg.vector_norm(got - plain) / torch.linalg.vector_norm(plain))
+    print(f"split vs exact {rel:.2e}, vs plain {rel_plain:.2e}", flush=True)
+    assert rel <= TOL and rel_plain <= TOL
+    # accumulate mode: acc0 + X^T X
+    acc0 = torch.randn(k, k, generator=torch.Generator(device=gpu).manual_seed(1), device=gpu)
+    acc = acc0.clone()
+    N.call("kq_syrk_accumulate_ws", N.DT_BF16, N.ptr(x), k, n, k, None, N.ptr(acc), k, 0, N.ptr(ws), need, st)
+    want = acc0[upper].double() + exact
+    rel_acc = float(torch.linalg.vector_norm(acc[upper].double() - want) / torch.linalg.vector_norm(want))
+    assert rel_acc <= TOL

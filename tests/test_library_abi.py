@@ -36,7 +36,7 @@ def test_python_binding_covers_every_entry_point():
                                         "kq_cholesky_workspace_size", "kq_block_ldl_workspace_size",
                                         "kq_sqg_quantize_workspace_size", "kq_qsrt_linear_workspace_size",
                                         "kq_qsrt_moe_workspace_size",
-                                        "kq_route_sort_workspace_size"}
+                                        "kq_route_sort_workspace_size", "kq_syrk_accumulate_workspace_size"}
     assert set(declared_symbols()) <= bound
 
 
