@@ -553,6 +553,10 @@ def main() -> int:
         td = _time_loop(torch, rot(d_steps), n1, sets1)
         tq_w = _time_loop(torch, q_steps[0], args.steps, args.warmup)
         td_w = _time_loop(torch, d_steps[0], args.steps, args.warmup)
+        # the same-size floor: a device copy of the 29 MB bf16 weight (59 MB
+        # moved), rotated over the same buffer sets
+        c_steps = [(lambda w=w, d=d: d.copy_(w)) for w, _, _, d in cset]
+        tc = _time_loop(torch, rot(c_steps), n1, sets1)
         result["cfg1_mxfp4_codec"] = {
             "quantize_gbs": round(b1 / tq / 1e9, 1), "quantize_us": round(tq * 1e6, 2),
             "dequant_gbs": round(b1 / td / 1e9, 1), "dequant_us": round(td * 1e6, 2),
@@ -561,6 +565,9 @@ def main() -> int:
             "bytes_per_launch": b1,
             "pmc": _traffic_entry("cfg1", "kq::mx_quantize_kernel<0, 1", b1),
             "warm_quantize_us": round(tq_w * 1e6, 2), "warm_dequant_us": round(td_w * 1e6, 2),
+            "copy_reference": {"what": "torch device copy of the cfg1 bf16 weight (29 MB read + 29 MB written), "
+                                       "same rotation", "us": round(tc * 1e6, 2),
+                               "gbs": round(2 * 7168 * 2048 * 2 / tc / 1e9, 1)},
             "note": f"cold: {sets1} buffer sets (1.04 GB) in turn; warm: one 37 MB set, which the "
                     "256 MB Infinity Cache holds across launches",
         }
