@@ -877,9 +877,10 @@ __global__ __launch_bounds__(512, 1) void syrk256w_dma_kernel(
   const uint32_t lds0 = lds_offset_of(syrk4_lds), wl0 = lds_offset_of(syrk4_w);
   // loads: instruction q of wave w moves token rows 2 (LPW w + q) + lane / 32;
   // lane % 32 is the LDS slot, holding global chunk slot ^ 4 (row % 4) of the
-  // row's 256 features (row % 4 is the same for every q)
+  // row's 256 features
   const int drow = 2 * LPW * wave + (lane >> 5);
-  const int dchunk = (lane & 31) ^ (4 * (drow & 3));
+  static_assert(LPW <= 2, "two load instructions per wave at most");
+  const int dchunk[2] = {(lane & 31) ^ (4 * (drow & 3)), (lane & 31) ^ (4 * ((drow + 2) & 3))};
   // conversion: chunk c = tid + 512 u -> token row c / 32, LDS slot c % 32
   // (the layout is kept, so the swizzle does not matter)
   const int cr = tid >> 5;
@@ -926,13 +927,13 @@ __global__ __launch_bounds__(512, 1) void syrk256w_dma_kernel(
     if (steps > 0) {
       // a chunk past feature k (edge tiles) reads feature 0 instead: such
       // features only reach accumulator rows / columns past k, never stored
-      const int64_t fa = row0 + dchunk * 8, fb = col0 + dchunk * 8;
-      const uint16_t* xa = x + list0 * ld + (fa < k ? fa : 0);
-      const uint16_t* xb = x + list0 * ld + (fb < k ? fb : 0);
       const float* wg = w + list0;
       auto issue = [&](int stage, int t0) {
 #pragma unroll
         for (int q = 0; q < LPW; ++q) {
+          const int64_t fa = row0 + dchunk[q] * 8, fb = col0 + dchunk[q] * 8;
+          const uint16_t* xa = x + list0 * ld + (fa < k ? fa : 0);
+          const uint16_t* xb = x + list0 * ld + (fb < k ? fb : 0);
           const int pos = t0 + drow + 2 * q < n ? t0 + drow + 2 * q : n - 1;
           const int64_t roff = (int64_t)pos * ld;
           const uint32_t dst = lds0 + (uint32_t)(STAGE * stage + (LPW * wave + q) * 1024);
