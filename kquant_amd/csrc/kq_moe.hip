@@ -550,26 +550,45 @@ __device__ __forceinline__ void x4t_finish(const X4TGemv& xg, int e, int64_t til
 //
 // GATEUP: rows of w13, output act -> bf16 intermediates.
 // !GATEUP: rows of w2, output route_weight * partial -> fp32 pair rows.
-template <bool GATEUP, bool X4T, int NBP, int S, int RW, int P, int STEPS>
+// ROUTE (a decode of at most DD_PAIRS pairs, dense scales): no routing
+// launch and no list; workgroup x takes pair x alone (expert route.ids[x],
+// one token slot) and writes its intermediate to row x.  Each MFMA output
+// row depends only on its own A row, so the values are those of the listed
+// form; a pair whose expert repeats reads that expert's weights again.
+struct DecodeRouteArgs {
+  const int* ids;
+  int experts;
+};
+
+template <bool GATEUP, bool X4T, int NBP, int S, int RW, int P, int STEPS, bool ROUTE = false>
 __global__ __launch_bounds__(S * RW * 64) void moe_small_kernel(
     const uint16_t* __restrict__ a, int64_t lda, int topk, const int* __restrict__ sorted,
     const int* __restrict__ small_list, const uint8_t* __restrict__ wt,
     const uint8_t* __restrict__ wst, const int* __restrict__ sslot, X4TGemv xg, int64_t rows_per_expert,
     int64_t K, int64_t inter, ActParams act, const float* __restrict__ route_w,
-    uint16_t* __restrict__ act_out, float* __restrict__ y_out, int64_t hidden) {
+    uint16_t* __restrict__ act_out, float* __restrict__ y_out, int64_t hidden, DecodeRouteArgs route) {
   constexpr int NB = GATEUP ? 2 * NBP : NBP;      // 16-row blocks per wave
   constexpr int CH = RW * 16 * NBP;               // channels per workgroup
   constexpr int NBUF = P + 1;
   constexpr int T = S * RW * 64, NRB = RW * NB;
   static_assert(NB * 33 <= 128 * S, "fixed tiles of the row blocks: at most two 16-byte loads per thread");
+  static_assert(!ROUTE || (!X4T && GATEUP), "per-pair decode: dense scales, gate/up");
   extern __shared__ __attribute__((aligned(16))) unsigned char x4t_lds[];
-  const int e = small_list[3 * blockIdx.x];       // -1 past the last entry
-  if (e < 0) return;
+  int e, beg, n;
+  if constexpr (ROUTE) {
+    e = route.ids[blockIdx.x];
+    if (e < 0 || e >= route.experts) return;
+    beg = blockIdx.x;
+    n = 1;
+  } else {
+    e = small_list[3 * blockIdx.x];               // -1 past the last entry
+    if (e < 0) return;
+    beg = small_list[3 * blockIdx.x + 1];
+    n = small_list[3 * blockIdx.x + 2];
+  }
   X4TPending pd;
   const int64_t tile0 = (int64_t)blockIdx.y * RW * NBP;  // first tile of this workgroup's row blocks
   if constexpr (X4T) x4t_issue<GATEUP, NB, NBP, NRB, T>(xg, e, tile0, pd);
-  const int beg = small_list[3 * blockIdx.x + 1];
-  const int n = small_list[3 * blockIdx.x + 2];
   const int se = sslot ? sslot[e] : e;            // scale slot of the expert
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int kpart = wave % S, rgw = wave / S;
@@ -618,7 +637,7 @@ __global__ __launch_bounds__(S * RW * 64) void moe_small_kernel(
   // are never stored, so the duplicate needs no masking, and the loads stay
   // unconditional so the compiler keeps them in flight across steps.
   const int mslot = m < n ? m : 0;
-  const int apair = sorted[beg + mslot];
+  const int apair = ROUTE ? (int)blockIdx.x : sorted[beg + mslot];
   const int64_t arow = GATEUP ? (int64_t)(apair / topk) : (int64_t)(beg + mslot);
   const uint16_t* ap = a + arow * lda + 32 * g;
   auto load_a = [&](int s, ABuf& B) {
@@ -1631,6 +1650,133 @@ using namespace kq::moe;
 // Pick the small-path instantiation for a reduction length K: 8 waves with a
 // compile-time step count when K is a multiple of 1024 (K/1024 steps of 128
 // per wave, 1..8), else 4 waves with a runtime loop (K % 512 == 0).
+// ------------------------------- decode down projection with the combine --
+// For at most DD_PAIRS pairs (one decode token at top-8): workgroup b owns
+// the 16 NBP output channels from 16 NBP b of every token and runs every
+// pair on them: wave w takes pair w / 2 (intermediate row w / 2, as the
+// per-pair gate/up GEMV wrote it) and K half w % 2 (the split, chunk order
+// and MFMA order of moe_small_kernel's down shape with S = 2), the halves
+// are summed in LDS in the same order and scaled by the route weight into
+// the pair's row of an LDS buffer, and each token's pairs are then summed in
+// slot order as moe_combine_kernel sums them.  Same operations in the same
+// order, so the output is bitwise that of the routing, down GEMV and
+// combine launches it replaces -- without the fp32 pair rows in HBM.
+constexpr int DD_PAIRS = 8;
+template <int NBP, int P, int STEPS, int OUT>
+__global__ __launch_bounds__(DD_PAIRS * 2 * 64) void moe_decode_down_kernel(
+    const uint16_t* __restrict__ act, int64_t inter, const int* __restrict__ ids, int topk, int experts,
+    int tokens, const uint8_t* __restrict__ wt, const uint8_t* __restrict__ wst, int64_t hidden,
+    const float* __restrict__ route_w, void* __restrict__ out) {
+  constexpr int CH = 16 * NBP, NBUF = P + 1;
+  static_assert(STEPS > 0, "compile-time K steps");
+  __shared__ f32x4_t red[2 * DD_PAIRS][NBP][64];
+  __shared__ float ybuf[DD_PAIRS][CH];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int m = lane & 15, g = lane >> 4;
+  const int pair = wave >> 1, kpart = wave & 1;   // pair = intermediate row
+  const int pairs = tokens * topk;
+  const int pe = pair < pairs ? ids[pair] : -1;
+  const bool valid = pe >= 0 && pe < experts;
+  const int64_t c0 = (int64_t)blockIdx.x * CH;
+  const int64_t nchunk = inter / 128, rgs = hidden / 16;
+  const int64_t c_first = kpart * nchunk / 2;
+  f32x4_t acc[NBP];
+#pragma unroll
+  for (int b = 0; b < NBP; ++b) acc[b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  if (valid) {
+    const int e = pe;
+    const uint8_t* wtile[NBP];
+    const uint8_t* stile[NBP];
+#pragma unroll
+    for (int b = 0; b < NBP; ++b) {
+      const int64_t rg = c0 / 16 + b;
+      const int64_t t0 = ((int64_t)e * rgs + rg) * nchunk + c_first;
+      wtile[b] = wt + t0 * 1024 + 16 * lane;
+      stile[b] = wst + t0 * 64 + lane;
+    }
+    struct WBuf {
+      u32x4_t w[NBP];
+      uint32_t ws[NBP];
+    };
+    struct ABuf {
+      u32x4_t v[4];
+    };
+    auto load_w = [&](int s, WBuf& B) {
+#pragma unroll
+      for (int b = 0; b < NBP; ++b) {
+        B.w[b] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(wtile[b] + (int64_t)s * 1024));
+        B.ws[b] = stile[b][(int64_t)s * 64];
+      }
+    };
+    WBuf wb[NBUF];
+    ABuf ab[NBUF];
+#pragma unroll
+    for (int s = 0; s < P && s < STEPS; ++s) load_w(s, wb[s]);
+    __builtin_amdgcn_sched_barrier(0);
+    // every token slot reads the pair's row; only slot 0 is stored
+    const uint16_t* ap = act + (int64_t)pair * inter + 32 * g;
+    auto load_a = [&](int s, ABuf& B) {
+      const int64_t c = c_first + s;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) B.v[t] = *reinterpret_cast<const u32x4_t*>(ap + 128 * c + 8 * t);
+    };
+    auto compute = [&](const WBuf& W, const ABuf& A) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const bf16x8_t fa = __builtin_bit_cast(bf16x8_t, A.v[t]);
+#pragma unroll
+        for (int b = 0; b < NBP; ++b) {
+          const bf16x8_t fb = gemm::dequant8<1>(u32x2_t{W.w[b][t], 0u}, W.ws[b]);
+          acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa, fb, acc[b], 0, 0, 0);
+        }
+      }
+    };
+#pragma unroll
+    for (int s = 0; s < P && s < STEPS; ++s) load_a(s, ab[s]);
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s) {
+      if (s + P < STEPS) {
+        load_w(s + P, wb[(s + P) % NBUF]);
+        load_a(s + P, ab[(s + P) % NBUF]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      compute(wb[s % NBUF], ab[s % NBUF]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+#pragma unroll
+  for (int b = 0; b < NBP; ++b) red[wave][b][lane] = acc[b];
+  __syncthreads();
+  if (valid && kpart == 0 && g == 0) {  // slot 0: D rows 4 (lane / 16) + j, j = 0
+#pragma unroll
+    for (int b = 0; b < NBP; ++b) {
+      f32x4_t x0 = red[wave][b][lane];
+      x0 += red[wave + 1][b][lane];
+      ybuf[pair][16 * b + m] = route_w[pair] * x0[0];
+    }
+  }
+  __syncthreads();
+  // combine: two adjacent channels per thread, each token's slots in order
+  for (int o = threadIdx.x; o < tokens * (CH / 2); o += blockDim.x) {
+    const int t = o / (CH / 2), c = 2 * (o % (CH / 2));
+    float s0 = 0.f, s1 = 0.f;
+    for (int k = 0; k < topk; ++k) {
+      const int e = ids[t * topk + k];
+      if (e < 0 || e >= experts) continue;
+      s0 += ybuf[t * topk + k][c];
+      s1 += ybuf[t * topk + k][c + 1];
+    }
+    if (OUT == 2) {
+      float* op = static_cast<float*>(out) + (int64_t)t * hidden + c0 + c;
+      op[0] = s0;
+      op[1] = s1;
+    } else {
+      *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(out) + (int64_t)t * hidden + c0 + c) =
+          f32x2_to_bf16x2_bits(s0, s1);
+    }
+  }
+}
+
 // GEMV launch shapes (channels per workgroup = RW * 16 * NBP), measured on
 // the decode batches of 1, 4 and 16 tokens (hidden 7168, intermediate 2048):
 // K split over 4 waves for gate/up (14 steps of 128 each) and over 2 for down
@@ -1651,26 +1797,34 @@ using namespace kq::moe;
 
 // x4t: the instantiation decoding X4T scales in its prologue, with that
 // decode's dynamic LDS.
+// route: one workgroup per decode pair, no list (dense scales, gate/up shape)
 template <bool GATEUP, int NBP, int S, int RW, int P, typename... Args>
 static hipError_t launch_small(bool x4t, int64_t experts_max, int64_t channels, int64_t K, int cols,
-                               hipStream_t st, Args... args) {
+                               hipStream_t st, const DecodeRouteArgs* route, Args... args) {
   constexpr int CH = RW * 16 * NBP, NB = GATEUP ? 2 * NBP : NBP;
   const dim3 grid((unsigned)experts_max, (unsigned)(channels / CH));
   const int64_t nchunk = K / 128;
   const int64_t steps = nchunk % S == 0 ? nchunk / S : 0;
   const size_t shm = x4t ? x4t_gemv_lds(RW * NB, nchunk, cols) : 0;
+  const DecodeRouteArgs none{nullptr, 0};
+  constexpr bool CAN_ROUTE = GATEUP;
+  if (route && (x4t || !CAN_ROUTE)) return hipErrorInvalidValue;
   switch (steps) {
-#define KQ_SMALL_CASE(N)                                                                        \
-    case N:                                                                                     \
-      if (x4t) moe_small_kernel<GATEUP, true, NBP, S, RW, P, N><<<grid, S * RW * 64, shm, st>>>(args...); \
-      else moe_small_kernel<GATEUP, false, NBP, S, RW, P, N><<<grid, S * RW * 64, 0, st>>>(args...);       \
+#define KQ_SMALL_CASE(N)                                                                                      \
+    case N:                                                                                                   \
+      if (x4t) moe_small_kernel<GATEUP, true, NBP, S, RW, P, N><<<grid, S * RW * 64, shm, st>>>(args..., none); \
+      else if (route) moe_small_kernel<GATEUP, false, NBP, S, RW, P, N, CAN_ROUTE>                            \
+          <<<grid, S * RW * 64, 0, st>>>(args..., *route);                                                    \
+      else moe_small_kernel<GATEUP, false, NBP, S, RW, P, N><<<grid, S * RW * 64, 0, st>>>(args..., none);    \
       break;
     KQ_SMALL_CASE(2) KQ_SMALL_CASE(4) KQ_SMALL_CASE(7) KQ_SMALL_CASE(8) KQ_SMALL_CASE(14)
     KQ_SMALL_CASE(16) KQ_SMALL_CASE(28)
 #undef KQ_SMALL_CASE
     default:
-      if (x4t) moe_small_kernel<GATEUP, true, NBP, S, RW, P, 0><<<grid, S * RW * 64, shm, st>>>(args...);
-      else moe_small_kernel<GATEUP, false, NBP, S, RW, P, 0><<<grid, S * RW * 64, 0, st>>>(args...);
+      if (x4t) moe_small_kernel<GATEUP, true, NBP, S, RW, P, 0><<<grid, S * RW * 64, shm, st>>>(args..., none);
+      else if (route)
+        moe_small_kernel<GATEUP, false, NBP, S, RW, P, 0, CAN_ROUTE><<<grid, S * RW * 64, 0, st>>>(args..., *route);
+      else moe_small_kernel<GATEUP, false, NBP, S, RW, P, 0><<<grid, S * RW * 64, 0, st>>>(args..., none);
   }
   return hipGetLastError();
 }
@@ -1847,10 +2001,17 @@ static int moe_forward_impl(const char* fn, int activation, float act_beta, floa
                         act_bytes <= dma::MAX_RANGE && (uint64_t)(2 * inter) * hidden / 2 <= dma::MAX_RANGE;
   const int tile_rows = dma_path ? DMA_BM : BM;
 
-  if (decode) {
+  // A decode of at most DD_PAIRS pairs with dense scales and bf16
+  // activations needs no routing launch: one gate/up workgroup per pair, and
+  // the down projection with the combine in one launch.
+  const bool route_in_gemv = decode && !xa && act_fmt < 0 && L.pairs <= DD_PAIRS && hidden % 32 == 0 &&
+                             (inter == 512 || inter == 1024 || inter == 2048 || inter == 4096);
+  const DecodeRouteArgs dra{route_ids, experts};
+  if (decode && !route_in_gemv) {
     route_decode_kernel<<<1, DECODE_MAX_PAIRS, 0, st>>>(route_ids, (int)L.pairs, experts, sorted,
                                                          small_list, (int)L.max_list, meta);
     if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_moe_forward/route");
+  } else if (decode) {
   } else if (L.pairs <= PREP_ONE) {
     route_prep_one_kernel<<<1, 1024, 0, st>>>(route_ids, (int)L.pairs, experts, counts, offsets,
                                                sorted, small_list, large_tiles, meta, (int)L.max_large,
@@ -1913,7 +2074,9 @@ static int moe_forward_impl(const char* fn, int activation, float act_beta, floa
   // gate/up
   {
     e = launch_small<true, KQ_GU_NBP, KQ_GU_S, KQ_GU_RW, KQ_GU_P>(
-        xa != nullptr, L.max_list, inter, hidden, (int)(hidden / 32), st, xb, ldx, topk, (const int*)sorted,
+        xa != nullptr, route_in_gemv ? L.pairs : L.max_list, inter, hidden, (int)(hidden / 32), st,
+        route_in_gemv ? &dra : nullptr, xb,
+        ldx, topk, (const int*)sorted,
         (const int*)small_list, w13_t, w13_st, gslot, x4t_gemv(xa, true), 2 * inter, hidden, inter, ap,
         route_weights, act, y, hidden);
     if (e != hipSuccess) return kq_check_launch(e, "kq_moe_forward/gateup_small");
@@ -1945,9 +2108,29 @@ static int moe_forward_impl(const char* fn, int activation, float act_beta, floa
     if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_moe_forward/gateup_large");
   }
   // down
+  if (route_in_gemv) {
+    const int64_t steps = inter / 128 / 2;
+    const dim3 grid((unsigned)(hidden / 32));
+    const bool f32 = out_dtype == KQ_DT_F32;
+#define KQ_DD_CASE(NS)                                                                                        \
+    if (steps == NS) {                                                                                        \
+      if (f32)                                                                                                \
+        moe_decode_down_kernel<2, 2, NS, 2><<<grid, DD_PAIRS * 2 * 64, 0, st>>>(                              \
+            (const uint16_t*)act, inter, route_ids, topk, experts, (int)tokens, w2_t, w2_st, hidden,          \
+            route_weights, out);                                                                              \
+      else                                                                                                    \
+        moe_decode_down_kernel<2, 2, NS, 0><<<grid, DD_PAIRS * 2 * 64, 0, st>>>(                              \
+            (const uint16_t*)act, inter, route_ids, topk, experts, (int)tokens, w2_t, w2_st, hidden,          \
+            route_weights, out);                                                                              \
+      return kq_check_launch(hipGetLastError(), "kq_moe_forward/decode_down");                               \
+    }
+    KQ_DD_CASE(2) KQ_DD_CASE(4) KQ_DD_CASE(8) KQ_DD_CASE(16)
+#undef KQ_DD_CASE
+    return kq_fail(KQ_ERR_INVALID, "%s: decode down shape", fn);
+  }
   {
     e = launch_small<false, KQ_DN_NBP, KQ_DN_S, KQ_DN_RW, KQ_DN_P>(
-        xa != nullptr, L.max_list, hidden, inter, (int)(inter / 32), st, (const uint16_t*)act, inter, topk,
+        xa != nullptr, L.max_list, hidden, inter, (int)(inter / 32), st, nullptr, (const uint16_t*)act, inter, topk,
         (const int*)sorted, (const int*)small_list, w2_t, w2_st, gslot, x4t_gemv(xa, false), hidden, inter,
         inter, ap, route_weights, act, y, hidden);
     if (e != hipSuccess) return kq_check_launch(e, "kq_moe_forward/down_small");

@@ -95,6 +95,33 @@ def test_no_valid_pair_gives_zeros(gpu, out_dtype):
     assert out.dtype == out_dtype and torch.count_nonzero(out) == 0
 
 
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
+def test_per_pair_decode_matches_listed_path_bitwise(gpu, out_dtype):
+    """At most 8 pairs the forward skips the routing launch (one gate/up
+    workgroup per pair) and fuses the down projection with the combine.  Its
+    output is bitwise that of the routed-list path (which the X4T-scale
+    forward still takes, on the same scale bytes), here with an expert
+    repeated across tokens, invalid ids, a token with no valid expert, and
+    every supported intermediate width's step count (I = 512)."""
+    T, k, E, H, I = 4, 2, 4, 512, 512
+    ids = torch.tensor([[1, 3], [3, -1], [0, 99], [-2, -1]], dtype=torch.int32)
+    w = torch.rand(T, k, generator=torch.Generator().manual_seed(8))
+    x = torch.randn(T, H, generator=torch.Generator().manual_seed(9)).to(torch.bfloat16)
+    raw = workloads.quantized_experts(range(E), E, H, I, seed=5, device=gpu)
+    dense = moe.prepare_expert_weights(*raw)
+    x4t = moe.prepare_expert_weights(*raw, scale_format="x4t")
+    args = (x.to(gpu), ids.to(gpu), w.to(gpu))
+    fused = moe.grouped_expert_forward(*args, dense, out_dtype=out_dtype)
+    listed = moe.grouped_expert_forward(*args, x4t, out_dtype=out_dtype)
+    assert torch.equal(fused, listed)
+    assert torch.count_nonzero(fused[3]) == 0
+    valid = (ids >= 0) & (ids < E)
+    ref = _oracle(x, torch.where(valid, ids, torch.zeros_like(ids)), w * valid, raw, "situ")
+    assert _max_rel(ref, fused.float().cpu().numpy()) <= (TOL if out_dtype == torch.float32 else 2 ** -8)
+    again = moe.grouped_expert_forward(*args, dense, out_dtype=out_dtype)
+    assert torch.equal(again, fused)
+
+
 @pytest.mark.parametrize("tokens", [1, 4, 16])
 def test_decode_real_shapes(gpu, tokens):
     """Configuration 5: hidden 7168, intermediate 2048, 384 experts, top-8."""
