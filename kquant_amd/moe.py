@@ -27,14 +27,17 @@ from .source_weights import PackedMXFP4Matrix
 from .tp_simulator import situ, swiglu
 from .x4t import pack_x4t_scale_components_batched, x4t_fixed_bytes, x4t_tile_index
 
-_WORKSPACES: dict[torch.device, torch.Tensor] = {}
+_WORKSPACES: dict[tuple[torch.device, int], torch.Tensor] = {}
 
 
 def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    buf = _WORKSPACES.get(device)
+    """The forward's workspace, one per (device, stream): calls on one stream
+    serialize, calls on different streams must not share it."""
+    key = (device, torch.cuda.current_stream(device).stream_id)
+    buf = _WORKSPACES.get(key)
     if buf is None or buf.numel() < nbytes:
         buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
-        _WORKSPACES[device] = buf
+        _WORKSPACES[key] = buf
     return buf
 
 

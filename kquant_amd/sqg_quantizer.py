@@ -30,7 +30,7 @@ import torch
 from . import _native as N
 from .sqg_e4m3 import sqg_e4m3_bytes
 
-_WORKSPACES: dict[tuple[torch.device, int], torch.Tensor] = {}
+_WORKSPACES: dict[tuple[torch.device, int, int], torch.Tensor] = {}
 
 
 def _workgroups(device: torch.device) -> int:
@@ -65,11 +65,13 @@ def quantize_tiles_sqg(tiles: torch.Tensor, lut: torch.Tensor, bits: int,
 
 
 def _workspace(device: torch.device, bits: int) -> torch.Tensor:
+    """Decision workspace, one per (device, stream, rate)."""
     need = int(N.library().kq_sqg_quantize_workspace_size(bits, _workgroups(device)))
-    ws = _WORKSPACES.get((device, bits))
+    key = (device, torch.cuda.current_stream(device).stream_id, bits)
+    ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < need:
         ws = torch.empty(need, dtype=torch.uint8, device=device)
-        _WORKSPACES[(device, bits)] = ws
+        _WORKSPACES[key] = ws
     return ws
 
 
