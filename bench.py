@@ -594,7 +594,7 @@ def main() -> int:
               / torch.sqrt(sum(torch.randn(65536, 7168, generator=g, device=dev).square() for _ in range(4)) / 4)
               ).to(torch.bfloat16)
         acc = torch.empty(7168, 7168, dtype=torch.float32, device=dev)
-        # stream-K partial slots: one 256 x 256 fp32 tile per CU
+        # partial slots of the chunked last round of tiles (152 MiB here)
         h_ws_bytes = int(N.library().kq_syrk_accumulate_workspace_size(N.DT_BF16, 65536, 7168, 0))
         h_ws = torch.empty(max(h_ws_bytes, 256), dtype=torch.uint8, device=dev)
 

@@ -241,17 +241,17 @@ int kq_syrk_accumulate(int in_dtype, const void* x, int64_t ld, int64_t n, int64
                        void* stream);
 
 /* kq_syrk_accumulate with a workspace for partial tiles.  When the upper
- * 256 x 256 tiles fill the rounds of workgroups poorly (fill below 0.72: the
- * 300 tiles of k = 6144 on 256 CUs fill 0.59), the tile x 32-row work is cut
- * into one contiguous range per CU (stream-K):
- * a range that starts inside a tile leaves its part in a partial slot, and a
- * second launch adds each tile's slots, in range order, to the value the
- * tile's first range wrote.  Results are deterministic for a given CU count
- * and agree with kq_syrk_accumulate to fp32 summation order.  Only
- * unweighted bf16 rows take the split; other calls, or a workspace smaller
- * than kq_syrk_accumulate_workspace_size (0 when the split does not pay),
- * run as kq_syrk_accumulate.  workspace: 256-byte aligned, uninitialised,
- * used by one call at a time (size for the current device's CU count). */
+ * 256 x 256 tiles leave the last round of workgroups partly filled (406
+ * tiles of k = 7168 on 256 CUs: one full round, then 150 tiles), the tiles
+ * of that last round are cut by 32-row steps into 2..16 equal chunks: chunk
+ * 0 writes the tile, the others write partial slots, and a second launch
+ * adds each tile's slots, in chunk order, to it.  Results are deterministic
+ * for a given CU count and agree with kq_syrk_accumulate to fp32 summation
+ * order.  Only unweighted bf16 rows take the split; other calls, or a
+ * workspace smaller than kq_syrk_accumulate_workspace_size (0 when the
+ * split does not pay), run as kq_syrk_accumulate.  workspace: 256-byte
+ * aligned, uninitialised, used by one call at a time (size for the current
+ * device's CU count). */
 int64_t kq_syrk_accumulate_workspace_size(int in_dtype, int64_t n, int64_t k, int weighted);
 int kq_syrk_accumulate_ws(int in_dtype, const void* x, int64_t ld, int64_t n, int64_t k,
                           const float* weights, float* acc, int64_t ld_acc, uint32_t flags,

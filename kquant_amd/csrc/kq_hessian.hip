@@ -646,103 +646,107 @@ __device__ __forceinline__ void syrk3_store(const float16_t (&accv)[2][4], float
       }
 }
 
-// Work split of a stream-K launch: the ntiles * steps units (tile, 32-token
-// step) in tile order are cut into `grid` contiguous ranges, range v =
-// [v units / grid, (v + 1) units / grid).  Workgroup b takes range v(b) =
-// (b % 8) grid / 8 + b / 8, so the workgroups of one XCD (b % 8) hold
-// neighbouring tiles.  A range that starts inside a tile leaves that first
-// part in partial slot v; the fix-up kernel adds the slots of a tile, in
-// ascending v, to the value its first range wrote.
-__device__ __forceinline__ int64_t split_begin(int64_t v, int64_t units, int grid) { return v * units / grid; }
+// Chunked tail.  Tiles go to XCDs in contiguous runs of per = ceil(tiles / 8)
+// (tile x per + j on XCD x = workgroup % 8).  The workgroups of an XCD take
+// its tiles j < j1 whole, j1 a multiple of the XCD's CU count, so those
+// rounds are full.  With chunks > 1 the remaining tiles of each XCD (at most
+// nmax) are cut by 32-token steps into `chunks` equal parts, and the XCD's
+// workgroups take them chunk-major (chunk 0 of every tail tile, then chunk 1
+// ...), so the workgroups that run together stream the same token rows, as
+// the whole tiles of a round do.  Chunk 0 writes (or adds to) the tile; chunk
+// c >= 1 writes partial slot (x nmax + i)(chunks - 1) + c - 1 for tail tile
+// i; the fix-up kernel then adds slots 1 .. chunks - 1, in that order.
+struct TailPlan {
+  int j1, nmax, chunks;
+};
 
 __global__ __launch_bounds__(512, 1) void syrk256_dma_kernel(
     const uint16_t* __restrict__ x, int64_t ld, int64_t n, int64_t k, float* __restrict__ acc,
-    int64_t ld_acc, int nt, int overwrite, uint32_t nbytes, float* __restrict__ partial) {
+    int64_t ld_acc, int nt, int overwrite, uint32_t nbytes, float* __restrict__ partial, TailPlan plan) {
   using namespace syrk3;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const i32x4_t rsrc = make_rsrc(x, nbytes);
-  // Segments: without partial slots, the one tile of this block over every
-  // row; with them, the tile parts of this block's stream-K range.
-  const int grid = gridDim.x;
-  const int64_t b = blockIdx.x;
-  const int64_t v = grid % SYRK_XCDS ? b : (b % SYRK_XCDS) * (grid / SYRK_XCDS) + b / SYRK_XCDS;
-  const int64_t steps = partial ? (n + BK - 1) / BK : 1;
-  const int64_t units = (int64_t)(nt * (nt + 1) / 2) * steps;
-  int64_t r = partial ? split_begin(v, units, grid) : 0;
-  const int64_t r_end = partial ? split_begin(v + 1, units, grid) : 1;
-  while (r < r_end) {
-    int ti, tj;
-    int64_t s0 = 0, s1 = 1, t_begin = 0, t_end = n;
-    if (partial) {
-      const int64_t t = r / steps;
-      s0 = r - t * steps;
-      s1 = s0 + (r_end - r) < steps ? s0 + (r_end - r) : steps;
-      upper_tile_for_block((int)t, nt, true, ti, tj);
-      t_begin = s0 * BK;
-      t_end = s1 * BK < n ? s1 * BK : n;
-    } else if (!upper_tile_for_block(blockIdx.x, nt, false, ti, tj)) {
-      return;  // spare block
-    }
-    const int64_t row0 = (int64_t)ti * TILE, col0 = (int64_t)tj * TILE;
-    float16_t accv[2][4];
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int q = 0; q < 16; ++q) accv[i][j][q] = 0.0f;
-    syrk3_range(rsrc, nbytes, ld, t_begin, t_end, row0, col0, ti == tj, accv, wave, lane);
-    // a part that starts inside its tile goes to partial slot v (only a
-    // range's first part can); the others are written or added in place
-    const bool to_slot = s0 != 0;
-    float* dst = to_slot ? partial + v * (TILE * TILE) : acc + row0 * ld_acc + col0;
-    syrk3_store(accv, dst, to_slot ? TILE : ld_acc, to_slot ? TILE : k - row0, to_slot ? TILE : k - col0,
-                to_slot || overwrite, wave, lane);
-    r += s1 - s0;
+  const int total = nt * (nt + 1) / 2, per = (total + SYRK_XCDS - 1) / SYRK_XCDS;
+  const int b = blockIdx.x;
+  const int64_t steps = (n + BK - 1) / BK;
+  int xcd = b % SYRK_XCDS, j = b / SYRK_XCDS;
+  int64_t s0 = 0, s1 = steps;
+  int slot = -1;
+  if (plan.chunks > 1 && j >= plan.j1) {
+    const int nx = min(per, total - xcd * per) - plan.j1;
+    if (nx <= 0) return;  // spare block
+    const int q = j - plan.j1, c = q / nx, i = q - c * nx;
+    if (c >= plan.chunks) return;
+    j = plan.j1 + i;
+    s0 = c * steps / plan.chunks;
+    s1 = (c + 1) * steps / plan.chunks;
+    if (c > 0) slot = (xcd * plan.nmax + i) * (plan.chunks - 1) + c - 1;
   }
+  const int t = xcd * per + j;
+  int ti, tj;
+  if (t >= total || !upper_tile_for_block(t, nt, true, ti, tj)) return;  // spare block
+  const int64_t row0 = (int64_t)ti * TILE, col0 = (int64_t)tj * TILE;
+  float16_t accv[2][4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+      for (int q = 0; q < 16; ++q) accv[i][jj][q] = 0.0f;
+  const int64_t t_end = s1 * BK < n ? s1 * BK : n;
+  syrk3_range(rsrc, nbytes, ld, s0 * BK, t_end, row0, col0, ti == tj, accv, wave, lane);
+  const bool to_slot = slot >= 0;
+  float* dst = to_slot ? partial + (int64_t)slot * (TILE * TILE) : acc + row0 * ld_acc + col0;
+  syrk3_store(accv, dst, to_slot ? TILE : ld_acc, to_slot ? TILE : k - row0, to_slot ? TILE : k - col0,
+              to_slot || overwrite, wave, lane);
 }
 
-// acc tile += partial slots of the ranges that start inside it, in ascending
-// range order.  Block (v, y): range v if it is the first to start inside its
-// tile; rows 16 y .. 16 y + 15 of the tile.
-__global__ __launch_bounds__(256) void syrk_splitk_fixup_kernel(const float* __restrict__ partial, int64_t n,
-                                                                int nt, int grid, float* __restrict__ acc,
-                                                                int64_t ld_acc, int64_t k) {
-  const int64_t steps = (n + syrk3::BK - 1) / syrk3::BK;
-  const int64_t units = (int64_t)(nt * (nt + 1) / 2) * steps;
-  const int64_t v = blockIdx.x;
-  const int64_t r0 = split_begin(v, units, grid);
-  if (r0 % steps == 0 || r0 >= units) return;  // starts on a tile boundary: no slot
-  const int64_t t = r0 / steps;
-  if (v > 0 && split_begin(v - 1, units, grid) > t * steps) return;  // not the tile's first slot
+// acc tile += partial slots 1 .. chunks - 1 of a tail tile, in chunk order.
+// Block (x nmax + i, y): tail tile i of XCD x, rows 16 y .. 16 y + 15.
+__global__ __launch_bounds__(256) void syrk_tail_fixup_kernel(const float* __restrict__ partial, int nt,
+                                                              TailPlan plan, float* __restrict__ acc,
+                                                              int64_t ld_acc, int64_t k) {
+  const int total = nt * (nt + 1) / 2, per = (total + SYRK_XCDS - 1) / SYRK_XCDS;
+  const int xcd = blockIdx.x / plan.nmax, i = blockIdx.x - xcd * plan.nmax;
+  if (i >= min(per, total - xcd * per) - plan.j1) return;
   int ti, tj;
-  upper_tile_for_block((int)t, nt, true, ti, tj);
+  upper_tile_for_block(xcd * per + plan.j1 + i, nt, true, ti, tj);
   const int64_t row0 = (int64_t)ti * syrk3::TILE, col0 = (int64_t)tj * syrk3::TILE;
   const int c = threadIdx.x;
   if (col0 + c >= k) return;
+  const float* slots = partial + (int64_t)blockIdx.x * (plan.chunks - 1) * (syrk3::TILE * syrk3::TILE);
   for (int rr = 0; rr < 16; ++rr) {
     const int row = blockIdx.y * 16 + rr;
     if (row0 + row >= k) break;
     float* p = acc + (row0 + row) * ld_acc + col0 + c;
     float sum = *p;
-    for (int64_t u = v; u < grid && split_begin(u, units, grid) < (t + 1) * steps; ++u)
-      if (split_begin(u + 1, units, grid) > split_begin(u, units, grid))  // empty ranges write no slot
-        sum += partial[u * (syrk3::TILE * syrk3::TILE) + row * syrk3::TILE + c];
+    for (int s = 0; s < plan.chunks - 1; ++s) sum += slots[(int64_t)s * (syrk3::TILE * syrk3::TILE) + row * syrk3::TILE + c];
     *p = sum;
   }
 }
 
-// Stream-K pays when the tiles fill the rounds of workgroups poorly: its
-// ranges start at scattered rows, so concurrent workgroups share fewer rows
-// in L2 than one tile per workgroup (which all stream the rows in step).
-// Measured on MI355X at 65,536 rows: 300 tiles (fill 0.59) 11% faster, 528
-// tiles (0.69) 10% faster, 406 tiles (0.79) 15% slower.
-static bool splitk_pays(int ntiles, int cus, int64_t n) {
-  if (cus < 8 || n < 4 * syrk3::BK || (int64_t)ntiles * ((n + syrk3::BK - 1) / syrk3::BK) < 2 * (int64_t)cus)
-    return false;
-  const int rounds = (ntiles + cus - 1) / cus;
-  return (double)ntiles / ((double)rounds * cus) < 0.72;
+// The tail split pays when an XCD's last round of tiles leaves CUs idle.
+// Rounds are priced in whole-tile times: the tail's chunked rounds cost
+// ceil(nmax chunks / cus_x) / chunks, plus 0.01 a chunk for the partial
+// slots and the fix-up pass; chunks of fewer than 4 steps are not taken, and
+// the split is used only below 0.85 of the one plain tail round.
+static TailPlan plan_tail(int ntiles, int cus, int64_t n) {
+  TailPlan p{0, 0, 1};
+  if (cus < SYRK_XCDS || cus % SYRK_XCDS) return p;
+  const int cx = cus / SYRK_XCDS, per = (ntiles + SYRK_XCDS - 1) / SYRK_XCDS;
+  const int j1 = per / cx * cx, nmax = per - j1;
+  const int64_t steps = (n + syrk3::BK - 1) / syrk3::BK;
+  if (nmax == 0) return p;
+  double best = 0.85;
+  for (int c = 2; c <= 16 && steps >= 4 * c; ++c) {
+    const double cost = (double)((nmax * c + cx - 1) / cx) / c + 0.01 * (c - 1);
+    if (cost < best) {
+      best = cost;
+      p = TailPlan{j1, nmax, c};
+    }
+  }
+  return p;
 }
 
 static int device_cus() {
@@ -752,7 +756,9 @@ static int device_cus() {
   return cus;
 }
 
-static int64_t syrk_split_bytes(int cus) { return (int64_t)cus * syrk3::TILE * syrk3::TILE * 4; }
+static int64_t tail_slot_bytes(const TailPlan& p) {
+  return p.chunks > 1 ? (int64_t)SYRK_XCDS * p.nmax * (p.chunks - 1) * syrk3::TILE * syrk3::TILE * 4 : 0;
+}
 
 static hipError_t launch_syrk256_dma(const void* x, int64_t ld, int64_t n, int64_t k, float* acc,
                                      int64_t ld_acc, int overwrite, hipStream_t st, void* workspace = nullptr,
@@ -760,21 +766,19 @@ static hipError_t launch_syrk256_dma(const void* x, int64_t ld, int64_t n, int64
   const int nt = (int)((k + syrk3::TILE - 1) / syrk3::TILE);
   const int ntiles = nt * (nt + 1) / 2;
   const uint32_t nbytes = (uint32_t)(n * ld * 2);
+  const int per = (ntiles + SYRK_XCDS - 1) / SYRK_XCDS;
+  TailPlan plan{0, 0, 1};
   if (workspace) {
-    const int cus = device_cus();
-    if (splitk_pays(ntiles, cus, n) && ws_bytes >= syrk_split_bytes(cus)) {
-      syrk256_dma_kernel<<<dim3(cus), dim3(512), 0, st>>>((const uint16_t*)x, ld, n, k, acc, ld_acc, nt,
-                                                           overwrite, nbytes, (float*)workspace);
-      hipError_t e = hipGetLastError();
-      if (e != hipSuccess) return e;
-      syrk_splitk_fixup_kernel<<<dim3(cus, syrk3::TILE / 16), dim3(256), 0, st>>>((const float*)workspace, n, nt,
-                                                                                cus, acc, ld_acc, k);
-      return hipGetLastError();
-    }
+    plan = plan_tail(ntiles, device_cus(), n);
+    if (tail_slot_bytes(plan) > ws_bytes) plan = TailPlan{0, 0, 1};
   }
-  const int blocks = SYRK_XCDS * ((ntiles + SYRK_XCDS - 1) / SYRK_XCDS);
-  syrk256_dma_kernel<<<dim3(blocks), dim3(512), 0, st>>>((const uint16_t*)x, ld, n, k, acc, ld_acc, nt,
-                                                          overwrite, nbytes, nullptr);
+  const int blocks = SYRK_XCDS * (plan.chunks > 1 ? plan.j1 + plan.nmax * plan.chunks : per);
+  syrk256_dma_kernel<<<dim3(blocks), dim3(512), 0, st>>>((const uint16_t*)x, ld, n, k, acc, ld_acc, nt, overwrite,
+                                                          nbytes, (float*)workspace, plan);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || plan.chunks <= 1) return e;
+  syrk_tail_fixup_kernel<<<dim3(SYRK_XCDS * plan.nmax, syrk3::TILE / 16), dim3(256), 0, st>>>(
+      (const float*)workspace, nt, plan, acc, ld_acc, k);
   return hipGetLastError();
 }
 
@@ -1336,9 +1340,8 @@ static int syrk_accumulate(int in_dtype, const void* x, int64_t ld, int64_t n, i
 extern "C" int64_t kq_syrk_accumulate_workspace_size(int in_dtype, int64_t n, int64_t k, int weighted) {
   if (n < 0 || k <= 0) return -1;
   if (!dma_syrk(in_dtype, weighted ? (const void*)1 : nullptr, n, k)) return 0;
-  const int cus = device_cus();
   const int nt = (int)((k + syrk3::TILE - 1) / syrk3::TILE);
-  return splitk_pays(nt * (nt + 1) / 2, cus, n) ? syrk_split_bytes(cus) : 0;
+  return tail_slot_bytes(plan_tail(nt * (nt + 1) / 2, device_cus(), n));
 }
 
 extern "C" int kq_syrk_accumulate_ws(int in_dtype, const void* x, int64_t ld, int64_t n, int64_t k,

@@ -323,9 +323,10 @@ def test_covariance_comparison_matches_oracle(gpu):
 
 @pytest.mark.parametrize("n,k", [(4096, 2048), (2048, 6144), (3001, 520)])
 def test_split_launch_matches_plain_launch(gpu, n, k):
-    """The stream-K launch (kq_syrk_accumulate_ws): 36 tiles shared by many
-    ranges, 300 tiles split at range boundaries, and ragged edge tiles with a
-    row count that is not a multiple of 32.  Written (overwrite) and
+    """The chunked-tail launch (kq_syrk_accumulate_ws; chunk counts for 256
+    CUs): 36 tiles all in the chunked tail (6 chunks), 300 tiles with a full
+    round then 5 chunks, and 6 ragged edge tiles (k = 520) over a row count
+    that is not a multiple of 32, in 10 chunks.  Written (overwrite) and
     accumulated onto a prefilled accumulator; against exact float64 X^T X
     and the one-tile-per-workgroup launch; repeat calls bitwise identical."""
     print(f"case split syrk n={n} k={k}", flush=True)
