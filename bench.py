@@ -602,7 +602,7 @@ def main() -> int:
             N.call("kq_syrk_accumulate_ws", N.DT_BF16, N.ptr(x4), 7168, 65536, 7168, N.ptr(None),
                    N.ptr(acc), 7168, N.SYRK_OVERWRITE, N.ptr(h_ws), h_ws_bytes, stream)
 
-        th = _time_loop(torch, h_step, 3, 1)
+        th = _time_loop(torch, h_step, 10, 2, 0.3)
         flops = workloads.syrk_flops(65536, 7168)
         # rows once + the upper 256 x 256 tiles of the fp32 accumulator written once
         syrk_pmc = _traffic_entry("hessian", "kq::syrk256_dma_kernel", 65536 * 7168 * 2 + 28 * 29 // 2 * 256 * 256 * 4)
@@ -627,7 +627,7 @@ def main() -> int:
             N.call("kq_syrk_grouped", N.DT_BF16, N.ptr(rows), k2, N.ptr(offsets_d), experts, None,
                    N.ptr(gates), k2, N.ptr(hacc), N.SYRK_SQUARE_WEIGHTS, stream)
 
-        the = _time_loop(torch, he_step, 3, 1)
+        the = _time_loop(torch, he_step, 10, 2, 0.3)
         flops = float((counts.double() * k2 * (k2 + 1)).sum())
         hbytes = pairs * k2 * 2 + pairs * 4 + experts * k2 * k2 * 4
         # the kernel writes the upper 256 x 256 tiles of each expert's accumulator
