@@ -70,6 +70,8 @@ def _load():
         lib.sqgo_procedural_labels.restype = None
         lib.sqgo_f64_to_f16.argtypes = [vp, ctypes.c_int64, vp]
         lib.sqgo_f64_to_f16.restype = None
+        lib.sqgo_argmin_edges.argtypes = [vp, i32]
+        lib.sqgo_argmin_edges.restype = i32
         lib.mxo_f32_to_e4m3.argtypes = [ctypes.c_float]
         lib.mxo_f32_to_e4m3.restype = u32
         lib.mxo_f32_to_e2m1.argtypes = [ctypes.c_float]
@@ -190,6 +192,14 @@ def f64_to_f16_bits(x: np.ndarray) -> np.ndarray:
     out = np.empty(v.shape, dtype=np.uint16)
     lib.sqgo_f64_to_f16(_ptr(v), v.size, _ptr(out))
     return out
+
+
+def sqg_argmin_edges(costs_f16_bits: np.ndarray) -> int:
+    """sqg_viterbi.c's argmin over one cost buffer (uint16 fp16 bits): the
+    smallest cost, ties by the key order the reference's reductions give."""
+    lib = _load()
+    c = np.ascontiguousarray(costs_f16_bits, dtype=np.uint16)
+    return int(lib.sqgo_argmin_edges(_ptr(c), c.size))
 
 
 def f32_to_e4m3(values: np.ndarray) -> np.ndarray:

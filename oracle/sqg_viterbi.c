@@ -136,16 +136,21 @@ static void forward(Trellis* t, int roll, int steps, int pre_state, int trace_st
  * pass holds the costs of the pass's second-to-last step
  * (qsrt_quantize_tiles_kernel.cuh:343-352 read temp_costs_inc after the
  * swaps of :75-79 and :202-204); entries at +inf are never selected. */
-static int argmin_cost(const Trellis* t) {
-  const uint16_t* c = t->prev;
+static int argmin_edges(const uint16_t* c, int edges) {
   int best = -1;
-  for (int e = 0; e < t->edges; ++e) {
+  for (int e = 0; e < edges; ++e) {
     if (c[e] == 0x7c00) continue;
     if (best < 0 || less16(c[e], c[best]) || (c[e] == c[best] && argmin_key(e) < argmin_key(best)))
       best = e;
   }
   return best < 0 ? 0 : best;
 }
+
+static int argmin_cost(const Trellis* t) { return argmin_edges(t->prev, t->edges); }
+
+/* The argmin alone, for its tests: index of the smallest of `edges` fp16
+ * costs (non-negative or +inf) under the tie order above. */
+int sqgo_argmin_edges(const uint16_t* costs, int edges) { return argmin_edges(costs, edges); }
 
 static uint16_t procedural_label(int codebook, uint32_t state) {
   if (codebook == 1) {

@@ -120,3 +120,64 @@ def test_procedural_search_is_optimal_against_one_edge_changes(codebook, bits):
         alt_states = qsrt.reconstruct_trellis_states(alt, bits).view(np.uint16).astype(np.int64)
         assert _path_cost(alt_states, w16, lab16) >= best
     assert float(((out[0] - x[0]) ** 2).mean()) < 0.15 * (2.0 ** (-2 * (bits - 2)))
+
+
+def _reference_argmin(costs: np.ndarray, bits: int) -> int:
+    """The reference kernel's argmin procedure, step by step
+    (kquant/csrc/qsrt_quantize_tiles_kernel.cuh:330-412): strided per-thread
+    scans keeping the first strictly smaller cost, warp shuffle-down trees
+    (a lane past the warp's end reads its own value; strictly smaller
+    wins), per-warp results in shared slots, and warp 0's final tree.  K2:
+    1024 threads with stride 1024; K3/K4: threads 0..511 each run two
+    streams (from t and from t + 512, stride 1024) into slots w and 16 + w."""
+    edges = costs.size
+
+    def scan(start, stride, nthreads):
+        t = np.arange(nthreads)
+        best_v, best_i = np.full(nthreads, np.inf), np.full(nthreads, -1)
+        for j in range(-(-(edges - start) // stride)):
+            e = start + t + j * stride
+            v = np.where(e < edges, costs[np.minimum(e, edges - 1)], np.inf)
+            take = v < best_v
+            best_v, best_i = np.where(take, v, best_v), np.where(take, e, best_i)
+        return best_v, best_i
+
+    def warp_tree(v, i):
+        v, i = v.reshape(-1, 32), i.reshape(-1, 32)
+        lanes = np.arange(32)
+        for off in (16, 8, 4, 2, 1):
+            src = np.where(lanes + off < 32, lanes + off, lanes)
+            ov, oi = v[:, src], i[:, src]
+            take = ov < v
+            v, i = np.where(take, ov, v), np.where(take, oi, i)
+        return v[:, 0], i[:, 0]
+
+    if bits == 2:
+        slot_v, slot_i = warp_tree(*scan(0, 1024, 1024))
+    else:
+        a_v, a_i = warp_tree(*scan(0, 1024, 512))
+        b_v, b_i = warp_tree(*scan(512, 1024, 512))
+        slot_v, slot_i = np.concatenate([a_v, b_v]), np.concatenate([a_i, b_i])
+    return int(warp_tree(slot_v, slot_i)[1][0])
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4])
+def test_argmin_tie_order_follows_the_reference_reduction(bits):
+    """Pins the closed-form tie key of the oracle's argmin against the
+    reference's reduction procedure simulated step by step: cost buffers
+    whose minimum is shared by 2, 3 or many entries (some +inf entries,
+    which are never picked), and buffers of few distinct values."""
+    edges = 65536 >> bits
+    rng = np.random.default_rng(bits)
+    cases = 0
+    for trial in range(60):
+        c = rng.choice(np.array([0.75, 1.0, 2.0, np.inf]), size=edges, p=[0.0, 0.6, 0.3, 0.1])
+        ties = rng.choice(edges, size=[2, 3, 17][trial % 3], replace=False)
+        c[ties] = 0.5
+        if trial % 5 == 0:                       # few values: the minimum everywhere
+            c = rng.choice(np.array([0.5, 1.0]), size=edges)
+        bits16 = c.astype(np.float16).view(np.uint16)
+        want = _reference_argmin(c, bits)
+        assert oracle.sqg_argmin_edges(bits16) == want, (trial, sorted(ties.tolist()))
+        cases += 1
+    assert cases == 60
