@@ -243,7 +243,7 @@ int kq_syrk_accumulate(int in_dtype, const void* x, int64_t ld, int64_t n, int64
 /* kq_syrk_accumulate with a workspace for partial tiles.  When the upper
  * 256 x 256 tiles leave the last round of workgroups partly filled (406
  * tiles of k = 7168 on 256 CUs: one full round, then 150 tiles), the tiles
- * of that last round are cut by 48-row steps into 2..16 equal chunks: chunk
+ * of that last round are cut by 64-row steps into 2..16 equal chunks: chunk
  * 0 writes the tile, the others write partial slots, and a second launch
  * adds each tile's slots, in chunk order, to it.  Results are deterministic
  * for a given CU count and agree with kq_syrk_accumulate to fp32 summation

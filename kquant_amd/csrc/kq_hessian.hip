@@ -504,22 +504,22 @@ __global__ __launch_bounds__(512, 1) void syrk256_kernel(
 // ---------------------------------------------------------------------------
 // Unweighted bf16 SYRK with direct-to-LDS loads.  Same tiles, waves and
 // transposed operand reads as syrk256_kernel, but X rows go from HBM into LDS
-// by buffer_load_dwordx4 ... lds (no register staging), through a ring of
-// three stages of 48 tokens, issued two steps ahead of their use, so the
-// memory latency is covered by two steps of MFMA work (48-token steps put 24
-// MFMAs per wave between barriers: 2-4 % faster than four stages of 32).  A
-// wave's load writes 1 KiB of LDS contiguously (two token rows), so rows are
-// not padded:
+// by buffer_load_dwordx4 ... lds (no register staging), double-buffered in
+// steps of 64 tokens: a step's loads are issued one step ahead, so the
+// memory latency is covered by one step of MFMA work (32 MFMAs per wave
+// between barriers: 4-5 % faster than four stages of 32 tokens, and as fast
+// as two of 80).  A wave's load writes 1 KiB of LDS contiguously (two token
+// rows), so rows are not padded:
 // 16-byte chunk c of token row r is stored at slot c ^ 4 (r % 4), which puts
 // the four rows of each transposed read on distinct LDS banks.  Tokens past n
 // get an out-of-range buffer offset and read as zeros; features past k only
 // reach output rows and columns past k, which are not stored.
 namespace syrk3 {
 constexpr int TILE = 256;
-constexpr int BK = 48;
+constexpr int BK = 64;
 constexpr int ROW = TILE * 2;      // bytes per token row
-constexpr int SLAB = BK * ROW;     // 24 KiB
-constexpr int NST = 3;             // ring stages
+constexpr int SLAB = BK * ROW;     // 32 KiB
+constexpr int NST = 2;             // ring stages
 constexpr int QPW = BK / 16;       // load instructions per wave and slab (two token rows each)
 }  // namespace syrk3
 
@@ -531,7 +531,7 @@ using dma::lds_offset_of;
 using dma::make_rsrc;
 using dma::waitcnt_vm;
 
-// One tile's token range [t_begin, t_end) through the three-stage ring into
+// One tile's token range [t_begin, t_end) through the two-stage ring into
 // accv.  Every wave of the workgroup calls it with the same arguments; it
 // starts and ends with the ring idle (all loads landed, all reads done).
 __device__ __forceinline__ void syrk3_range(const i32x4_t rsrc, uint32_t nbytes, int64_t ld, int64_t t_begin,
@@ -580,21 +580,20 @@ __device__ __forceinline__ void syrk3_range(const i32x4_t rsrc, uint32_t nbytes,
     offb[j] = trow * ROW + (((f >> 3) ^ xorv) << 4) + (f & 7) * 2;
   }
 
-  // Step s on stage s % 3: wait for this step's loads (the next step's may
-  // still be in flight), barrier (every wave's loads have landed; every wave
-  // is done with the stage the next loads overwrite), issue the loads of step
-  // s + 2, compute.  Steps past the end load zeros, which keeps the per-step
-  // count of outstanding loads fixed.
+  // Step s on stage s % NST: wait for this step's loads (NST - 2 later steps'
+  // may still be in flight), barrier (every wave's loads have landed; every
+  // wave is done with the stage the next loads overwrite), issue the loads of
+  // step s + NST - 1, compute.  Steps past the end load zeros, which keeps the
+  // per-step count of outstanding loads fixed.
   const int64_t steps = (t_end - t_begin + BK - 1) / BK;
-  issue(0, t_begin);
-  issue(1, t_begin + BK);
+  for (int p = 0; p < NST - 1; ++p) issue(p, t_begin + p * BK);
   int stage = 0;
   for (int64_t s = 0; s < steps; ++s) {
-    if (share_b) __builtin_amdgcn_s_waitcnt(waitcnt_vm(QPW));
-    else __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * QPW));
+    if (share_b) __builtin_amdgcn_s_waitcnt(waitcnt_vm((NST - 2) * QPW));
+    else __builtin_amdgcn_s_waitcnt(waitcnt_vm((NST - 2) * 2 * QPW));
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    issue(stage == 0 ? 2 : stage - 1, t_begin + (s + 2) * BK);
+    issue(stage == 0 ? NST - 1 : stage - 1, t_begin + (s + NST - 1) * BK);
     const unsigned char* a_base = syrk3_lds + 2 * SLAB * stage;
     const unsigned char* b_base = share_b ? a_base : a_base + SLAB;
 #pragma unroll
@@ -620,9 +619,9 @@ __device__ __forceinline__ void syrk3_range(const i32x4_t rsrc, uint32_t nbytes,
         for (int j = 0; j < 4; ++j)
           accv[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], accv[i][j], 0, 0, 0);
     }
-    stage = stage == 2 ? 0 : stage + 1;
+    stage = stage == NST - 1 ? 0 : stage + 1;
   }
-  __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));  // the two steps issued past the end have landed
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));  // the loads issued past the end have landed
   __syncthreads();                            // every wave is done reading the ring
 }
 
@@ -654,7 +653,7 @@ __device__ __forceinline__ void syrk3_store(const float16_t (&accv)[2][4], float
 // (tile x per + j on XCD x = workgroup % 8).  The workgroups of an XCD take
 // its tiles j < j1 whole, j1 a multiple of the XCD's CU count, so those
 // rounds are full.  With chunks > 1 the remaining tiles of each XCD (at most
-// nmax) are cut by 48-token steps into `chunks` equal parts, and the XCD's
+// nmax) are cut by 64-token steps into `chunks` equal parts, and the XCD's
 // workgroups take them chunk-major (chunk 0 of every tail tile, then chunk 1
 // ...), so the workgroups that run together stream the same token rows, as
 // the whole tiles of a round do.  Chunk 0 writes (or adds to) the tile; chunk
