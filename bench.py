@@ -764,7 +764,9 @@ def main() -> int:
         reps = 20
         for name, (kt_, nt_, axis, bits_, p_, su_, sv_) in lin_cases.items():
             row = {}
-            for m in (1, 4, 16):
+            # 512 rows: the prefill path (rows rotated, the weight decoded once
+            # to its E4M3 labels, the MXFP8 MFMA linear, the output rotated)
+            for m in (1, 4, 16, 512) if name == "k3_w1" else (1, 4, 16):
                 xq = torch.randn(m, kt_ * 16, generator=gq, device=dev).to(torch.bfloat16)
                 outq = torch.empty(m, nt_ * 16, dtype=torch.bfloat16, device=dev)
                 run = kq_qsrt.qsrt_linear_launcher(xq, p_, outq, k_tiles=kt_, n_tiles=nt_, rate_axis=axis,
@@ -775,6 +777,23 @@ def main() -> int:
                     for _ in range(reps):
                         run()
                 row[f"m{m}_us"] = round(_time_loop(torch, graph.replay, 10, 3) / reps * 1e6, 2)
+                if m == 512:
+                    row["m512_tflops"] = round(2.0 * m * kt_ * 16 * nt_ * 16 / (row["m512_us"] * 1e-6) / 1e12, 1)
+                    # the reference's dense path at the same rows: decode to bf16, then F.linear
+                    dense = kq_qsrt.decode_qsrt_payload(p_, k_tiles=kt_, n_tiles=nt_, rate_axis=axis,
+                                                        record_bits=bits_, suh=su_, svh=sv_,
+                                                        out_dtype=torch.bfloat16, transposed=True)
+
+                    def ref_path(xq=xq, p_=p_, kt_=kt_, nt_=nt_, axis=axis, bits_=bits_, su_=su_, sv_=sv_):
+                        w_ = kq_qsrt.decode_qsrt_payload(p_, k_tiles=kt_, n_tiles=nt_, rate_axis=axis,
+                                                         record_bits=bits_, suh=su_, svh=sv_,
+                                                         out_dtype=torch.bfloat16, transposed=True)
+                        torch.nn.functional.linear(xq, w_)
+
+                    row["m512_decode_then_f_linear_us"] = round(_time_loop(torch, ref_path, 20, 3) * 1e6, 2)
+                    row["m512_f_linear_on_decoded_us"] = round(
+                        _time_loop(torch, lambda: torch.nn.functional.linear(xq, dense), 20, 3) * 1e6, 2)
+                    del dense
             row["weight_bytes"] = int(p_.numel() * 2)
             lin[name] = row
         # routed experts at the Kimi-K3 TP12-local geometry (H = 3584, 256

@@ -186,6 +186,11 @@ __global__ __launch_bounds__(512, 1) void mx_linear_kernel(
 //  * scales: one aligned dword per weight row per stage (four blocks, two of
 //    them this step's) by 4-byte direct loads; needs KB % 128 == 0.
 //  * rows past M or N read as zero (out-of-range offsets) and are not stored.
+//  * split K (fp32 output only): with `slices` > 1 the work items are
+//    (slice, tile), slice-major, and item (s, t) runs steps
+//    [s steps / slices, (s + 1) steps / slices) of tile t into plane s of c
+//    (c + s plane); the caller sums the planes.  Needs slices <= steps.
+//  * UNIT: every E8M0 scale is 127 (x 1); no scale array is read.
 namespace lin3 {
 constexpr int NSTAGE = 3;
 constexpr int A_BYTES = lin::BM * lin::BK * 2;                      // 32 KiB
@@ -198,16 +203,17 @@ template <int FMT> constexpr int loads() { return 4 + (FMT == 0 ? 2 : 1) + 1; } 
 
 __shared__ __attribute__((aligned(16))) unsigned char lin3_lds[lin3::NSTAGE * lin3::stage<0>()];
 
-template <int FMT, int OUT>
+template <int FMT, int OUT, bool UNIT = false>
 __global__ __launch_bounds__(512, 1) void mx_linear_dma_kernel(
     const uint16_t* __restrict__ a, int64_t lda, uint32_t a_bytes, const uint8_t* __restrict__ wq,
     const uint8_t* __restrict__ ws, uint32_t w_bytes, uint32_t s_bytes, void* __restrict__ c,
-    int64_t ldc, int M, int N, int K, int KB) {
+    int64_t ldc, int M, int N, int K, int KB, int slices, int64_t plane) {
   using namespace lin3;
   using dma::i32x4_t;
-  constexpr int WROW = w_row<FMT>(), STAGE = stage<FMT>(), LOADS = loads<FMT>();
+  constexpr int WROW = w_row<FMT>(), STAGE = stage<FMT>(), LOADS = loads<FMT>() - (UNIT ? 1 : 0);
   constexpr int BM = lin::BM, BN = lin::BN, BK = lin::BK;
-  const int mtiles = (M + BM - 1) / BM, ntiles = (N + BN - 1) / BN, total = mtiles * ntiles;
+  const int mtiles = (M + BM - 1) / BM, ntiles = (N + BN - 1) / BN, tiles = mtiles * ntiles;
+  const int total = tiles * slices;
   const int G = gridDim.x;
   const int worker = (int)(blockIdx.x % 8) * (G / 8) + (int)(blockIdx.x / 8);
   if (worker >= total) return;
@@ -221,12 +227,15 @@ __global__ __launch_bounds__(512, 1) void mx_linear_dma_kernel(
   const i32x4_t w_rsrc = dma::make_rsrc(wq, w_bytes);
   const i32x4_t s_rsrc = dma::make_rsrc(ws, s_bytes);
 
-  // ---- load side (tile lt, step ls); per-lane row offsets, invalid -> past the range
-  int lt = worker, ls = 0;
+  // ---- load side (item lt, step ls < ls_end); per-lane row offsets, invalid -> past the range
+  int lt = worker, ls = 0, ls_end = steps;
   uint32_t a_off[4], w_off[2], s_off;
   auto set_load_tile = [&]() {
     const bool live = lt < total;
-    const int mt = live ? lt / ntiles : 0, nt = live ? lt - mt * ntiles : 0;
+    const int sl = live ? lt / tiles : 0, tl = live ? lt - sl * tiles : 0;
+    ls = (int)((int64_t)sl * steps / slices);
+    ls_end = (int)((int64_t)(sl + 1) * steps / slices);
+    const int mt = live ? tl / ntiles : 0, nt = live ? tl - mt * ntiles : 0;
     const int m0 = mt * BM, n0 = nt * BN;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -258,13 +267,12 @@ __global__ __launch_bounds__(512, 1) void mx_linear_dma_kernel(
     for (int q = 0; q < (FMT == 0 ? 2 : 1); ++q)
       dma::load_to_lds16(w_rsrc, w_off[q] >= w_bytes ? w_bytes : w_off[q] + wk,
                          base + (uint32_t)(A_BYTES + (8 * q + wave) * 1024));
-    if (lane < 32)
+    if (!UNIT && lane < 32)
       dma::load_to_lds4(s_rsrc, s_off >= s_bytes ? s_bytes : s_off + (uint32_t)((kb0 / 32) & ~3),
                         base + (uint32_t)(A_BYTES + b_bytes<FMT>() + wave * 128));
   };
   auto advance = [&]() {
-    if (++ls == steps) {
-      ls = 0;
+    if (++ls == ls_end) {
       lt += G;
       set_load_tile();
     }
@@ -299,7 +307,9 @@ __global__ __launch_bounds__(512, 1) void mx_linear_dma_kernel(
   advance();
   int cslot = 0;
   for (int t = worker; t < total; t += G) {
-    const int mt = t / ntiles, nt = t - mt * ntiles;
+    const int sl = t / tiles, tl = t - sl * tiles;
+    const int mt = tl / ntiles, nt = tl - mt * ntiles;
+    const int s_begin = (int)((int64_t)sl * steps / slices), s_end = (int)((int64_t)(sl + 1) * steps / slices);
     const int m0 = mt * BM, n0 = nt * BN;
     const bool active = m0 + wm < M && n0 + wn < N;
     float16_t acc[2][4];
@@ -310,7 +320,7 @@ __global__ __launch_bounds__(512, 1) void mx_linear_dma_kernel(
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    for (int s = 0; s < steps; ++s) {
+    for (int s = s_begin; s < s_end; ++s) {
       const int kb0 = (s * BK) % KB;
       dma::wait_and_barrier<LOADS>();
       issue(cslot == 0 ? 2 : cslot - 1);
@@ -325,7 +335,7 @@ __global__ __launch_bounds__(512, 1) void mx_linear_dma_kernel(
 #pragma unroll
           for (int h = 0; h < (FMT == 0 ? 2 : 1); ++h)
             wv[j][h] = *reinterpret_cast<const u32x4_t*>(st + woff[j][h]);
-          sc[j] = st[soff[j] + sbyte];
+          sc[j] = UNIT ? 127u : st[soff[j] + sbyte];
         }
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -360,7 +370,7 @@ __global__ __launch_bounds__(512, 1) void mx_linear_dma_kernel(
             const int gm = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * f + (r & 3);
             const int gn = n0 + wn + j * 32 + frow;
             if (gm < M && gn < N) {
-              if (OUT == 2) static_cast<float*>(c)[(int64_t)gm * ldc + gn] = acc[i][j][r];
+              if (OUT == 2) static_cast<float*>(c)[sl * plane + (int64_t)gm * ldc + gn] = acc[i][j][r];
               else static_cast<__bf16*>(c)[(int64_t)gm * ldc + gn] = (__bf16)acc[i][j][r];
             }
           }
@@ -410,10 +420,10 @@ using namespace kq;
 // Direct-to-LDS path: needs 4-byte aligned scale rows (KB % 128 == 0, scale
 // pointer 4-byte aligned); operands larger than one 32-bit buffer range are
 // cut into row chunks of M and N.
-template <int FMT, int OUT>
+template <int FMT, int OUT, bool UNIT = false>
 static hipError_t launch_linear_dma(const uint16_t* a, int64_t lda, const uint8_t* wq,
                                     const uint8_t* ws, void* c, int64_t ldc, int M, int N, int K,
-                                    int KB, hipStream_t st) {
+                                    int KB, hipStream_t st, int slices = 1, int64_t plane = 0) {
   int dev = 0, cus = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
@@ -425,14 +435,14 @@ static hipError_t launch_linear_dma(const uint16_t* a, int64_t lda, const uint8_
     const int mc = (int)(M - m0 < m_chunk ? M - m0 : m_chunk);
     for (int64_t n0 = 0; n0 < N; n0 += n_chunk) {
       const int nc = (int)(N - n0 < n_chunk ? N - n0 : n_chunk);
-      const int tiles = ((mc + lin::BM - 1) / lin::BM) * ((nc + lin::BN - 1) / lin::BN);
+      const int tiles = ((mc + lin::BM - 1) / lin::BM) * ((nc + lin::BN - 1) / lin::BN) * slices;
       int grid = cus / 8 * 8 > 0 ? cus / 8 * 8 : 8;
       if (grid > (tiles + 7) / 8 * 8) grid = (tiles + 7) / 8 * 8;
       void* cp = OUT == 2 ? (void*)(static_cast<float*>(c) + m0 * ldc + n0)
                           : (void*)(static_cast<uint16_t*>(c) + m0 * ldc + n0);
-      mx_linear_dma_kernel<FMT, OUT><<<grid, lin::THREADS, 0, st>>>(
+      mx_linear_dma_kernel<FMT, OUT, UNIT><<<grid, lin::THREADS, 0, st>>>(
           a + m0 * lda, lda, (uint32_t)(mc * lda * 2), wq + n0 * kw, ws + n0 * ks,
-          (uint32_t)(nc * kw), (uint32_t)(nc * ks), cp, ldc, mc, nc, K, KB);
+          (uint32_t)(nc * kw), (uint32_t)(nc * ks), cp, ldc, mc, nc, K, KB, slices, plane);
       if ((e = hipGetLastError()) != hipSuccess) return e;
     }
   }
@@ -453,6 +463,38 @@ static hipError_t launch_linear(const uint16_t* a, int64_t lda, const uint8_t* w
   kern<<<grid, lin::THREADS, lds, st>>>(a, lda, wq, ws, c, ldc, M, N, K, KB);
   return hipGetLastError();
 }
+
+namespace kq {
+
+int mx_linear_slices(int64_t m, int64_t n, int64_t k_steps) {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    return 1;
+  const int64_t tiles = ((m + lin::BM - 1) / lin::BM) * ((n + lin::BN - 1) / lin::BN);
+  if (tiles <= 0 || 2 * tiles > cus) return 1;
+  int64_t sl = cus / tiles;
+  if (sl > k_steps / 8) sl = k_steps / 8;
+  if (sl > 16) sl = 16;
+  return sl < 1 ? 1 : (int)sl;
+}
+
+bool mx_linear_planes_ok(int64_t lda, int64_t kb) {
+  return kb % 128 == 0 && (uint64_t)lda * 2 * lin::BM <= dma::MAX_RANGE && (uint64_t)kb * lin::BN <= dma::MAX_RANGE;
+}
+
+hipError_t mx_linear_planes_unit(const uint16_t* a, int64_t lda, const uint8_t* wq, float* c, int64_t ldc,
+                                 int64_t plane, int m, int n, int k, int kb, int slices, hipStream_t st) {
+  return launch_linear_dma<0, 2, true>(a, lda, wq, nullptr, c, ldc, m, n, k, kb, st, slices, plane);
+}
+
+hipError_t split3_rows(const float* a, int64_t lda, int64_t m, int64_t k, uint16_t* out, hipStream_t st) {
+  const int64_t quads = m * (k / 4);
+  split3_bf16_kernel<<<(unsigned)((quads + 255) / 256), 256, 0, st>>>(a, lda, m, k, out);
+  return hipGetLastError();
+}
+
+}  // namespace kq
 
 extern "C" int kq_mx_linear(int w_fmt, const void* a, int64_t lda, const void* w_q,
                             const uint8_t* w_scale, int64_t m, int64_t n, int64_t k,

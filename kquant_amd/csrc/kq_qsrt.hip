@@ -659,15 +659,22 @@ __global__ __launch_bounds__(LIN_THREADS) void decode_fast_kernel(DecArgs a, Lin
 // wave-level Sylvester transform, scales applied before (PRE: the input's
 // suh) or after it (the output's svh), and a power-of-two post factor.
 // Without ROT it converts only.  All 64 lanes of a wave take the same row.
+// An input of several planes (element stride `plane`) is their sum.
 template <bool PRE, bool ROT>
 __global__ __launch_bounds__(256) void rot_rows_kernel(const void* __restrict__ in, int in_dtype, int64_t ldi,
                                                        int64_t rows, const float* __restrict__ scale, float post,
-                                                       void* __restrict__ out, int out_dtype, int64_t ldo) {
+                                                       void* __restrict__ out, int out_dtype, int64_t ldo,
+                                                       int planes = 1, int64_t plane = 0) {
   const int lane = threadIdx.x & 63;
   const int64_t r = (int64_t)blockIdx.y * 4 + (threadIdx.x >> 6);
   if (r >= rows) return;
   const int64_t c = (int64_t)blockIdx.x * 128 + lane;
   float v0 = load_x(in, in_dtype, r * ldi + c), v1 = load_x(in, in_dtype, r * ldi + c + 64);
+  // fp32 input split over planes (a split-K product): summed in plane order
+  for (int p = 1; p < planes; ++p) {
+    v0 += load_x(in, in_dtype, p * plane + r * ldi + c);
+    v1 += load_x(in, in_dtype, p * plane + r * ldi + c + 64);
+  }
   if (PRE && scale) {
     v0 *= scale[c];
     v1 *= scale[c + 64];
@@ -683,11 +690,6 @@ __global__ __launch_bounds__(256) void rot_rows_kernel(const void* __restrict__ 
   }
   store_out(out, out_dtype, r * ldo + c, v0);
   store_out(out, out_dtype, r * ldo + c + 64, v1);
-}
-
-__global__ __launch_bounds__(256) void fill_u8_kernel(uint8_t* __restrict__ p, int64_t n, uint8_t v) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i < n) p[i] = v;
 }
 
 // ------------------------------------------------------ routed experts --
@@ -1110,22 +1112,26 @@ void launch_linear_m(const LinArgs& a, const LinRecords& rec, bool rot, dim3 gri
 static constexpr int64_t PREFILL_ROWS = 33;
 
 // Prefill workspace: rotated activations xr [m, K] (fp32, or bf16 for bf16
-// x), the regularized weight's E4M3 bytes [N, K] with unit E8M0 scales
-// [N, K / 32], the product y [m, N] fp32, and kq_mx_linear_f32's split.
+// x), the regularized weight's E4M3 bytes [N, K] (an MXFP8 matrix whose
+// block scales are all 1, which the linear takes without a scale array),
+// the product y fp32 as `slices` K-slice planes [m, N] (split K when the
+// output tiles alone would leave CUs idle), and the three-term bf16 split of
+// fp32 rows [m, 3K].
 struct PrefillLayout {
-  int64_t xr, w, s, y, split, total, split_bytes;
+  int64_t xr, w, y, split, total, split_bytes;
+  int slices;
 };
 
 static PrefillLayout prefill_layout(int64_t m, int64_t k, int64_t n, bool f32) {
   auto al = [](int64_t v) { return (v + 255) / 256 * 256; };
   PrefillLayout L{};
-  L.split_bytes = f32 ? kq_mx_linear_f32_workspace_size(m, k) : 0;
+  L.split_bytes = f32 ? m * 3 * k * 2 : 0;
+  L.slices = kq::mx_linear_slices(m, n, (f32 ? 3 * k : k) / 64);
   int64_t o = 0;
   L.xr = o;    o = al(o + m * k * (f32 ? 4 : 2));
   L.w = o;     o = al(o + n * k);
-  L.s = o;     o = al(o + n * k / 32);
-  L.y = o;     o = al(o + m * n * 4);
-  L.split = o; o = al(o + (L.split_bytes > 0 ? L.split_bytes : 0));
+  L.y = o;     o = al(o + m * n * 4 * L.slices);
+  L.split = o; o = al(o + L.split_bytes);
   L.total = o;
   return L;
 }
@@ -1142,7 +1148,9 @@ extern "C" int64_t kq_qsrt_linear_workspace_size(int64_t m, int64_t k_tiles, int
 // transform; bf16 x gives bf16 xr, f16 / fp32 x fp32 xr), W_reg decoded once
 // to its E4M3 label bytes [N, K] (exact: W_reg is an MXFP8 matrix with unit
 // scales), y = xr W_reg^T on the MXFP8 MFMA linear (fp32 accumulation; fp32
-// xr through the exact three-term bf16 split), out = (y B_N) / 128 o svh.
+// xr through the exact three-term bf16 split; split over K into planes when
+// the output tiles are too few for the CUs), out = (sum of the planes B_N) /
+// 128 o svh.
 // Without suh / svh the matrix is W_reg itself and both rotations are plain
 // conversions.  Argument checks are the caller's.
 static int qsrt_prefill(const void* x, int x_dtype, int64_t m, int64_t ldx, const int16_t* payload,
@@ -1161,7 +1169,6 @@ static int qsrt_prefill(const void* x, int x_dtype, int64_t m, int64_t ldx, cons
   unsigned char* w = static_cast<unsigned char*>(workspace);
   void* xr = w + L.xr;
   uint8_t* wq = w + L.w;
-  uint8_t* ws = w + L.s;
   float* y = reinterpret_cast<float*>(w + L.y);
   const bool rot = suh != nullptr;
   const int xr_dtype = f32 ? KQ_DT_F32 : KQ_DT_BF16;
@@ -1173,16 +1180,25 @@ static int qsrt_prefill(const void* x, int x_dtype, int64_t m, int64_t ldx, cons
   int rc = kq_qsrt_decode_weight(payload, payload_words, k_tiles, n_tiles, rate_axis, record_bits, labels, nullptr,
                                  nullptr, OUT_E4M3, wq, K, KQ_QSRT_TRANSPOSED, st);
   if (rc != KQ_OK) return rc;
-  const int64_t nscale = N * (K / 32);
-  fill_u8_kernel<<<(unsigned)((nscale + 255) / 256), 256, 0, st>>>(ws, nscale, 127);
-  if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, fn);
-  rc = f32 ? kq_mx_linear_f32(KQ_FMT_MXFP8_E4M3, static_cast<const float*>(xr), K, wq, ws, m, N, K, y, N,
-                              w + L.split, L.split_bytes, st)
-           : kq_mx_linear(KQ_FMT_MXFP8_E4M3, xr, K, wq, ws, m, N, K, KQ_DT_F32, y, N, st);
-  if (rc != KQ_OK) return rc;
+  if (!kq::mx_linear_planes_ok(f32 ? 3 * K : K, K))
+    return kq_fail(KQ_ERR_LIMIT, "%s: %lld rows exceed the prefill product's operand range", fn, (long long)m);
+  const uint16_t* a_rows = static_cast<const uint16_t*>(xr);
+  if (f32) {
+    uint16_t* a3 = reinterpret_cast<uint16_t*>(w + L.split);
+    if ((e = kq::split3_rows(static_cast<const float*>(xr), K, m, K, a3, st)) != hipSuccess)
+      return kq_check_launch(e, fn);
+    a_rows = a3;
+  }
+  e = kq::mx_linear_planes_unit(a_rows, f32 ? 3 * K : K, wq, y, N, m * N, (int)m, (int)N, (int)(f32 ? 3 * K : K),
+                                (int)K, L.slices, st);
+  if (e != hipSuccess) return kq_check_launch(e, fn);
   const dim3 gout((unsigned)(N / 128), (unsigned)((m + 3) / 4));
-  if (rot) rot_rows_kernel<false, true><<<gout, 256, 0, st>>>(y, KQ_DT_F32, N, m, svh, 1.f / 128.f, out, out_dtype, ldo);
-  else rot_rows_kernel<false, false><<<gout, 256, 0, st>>>(y, KQ_DT_F32, N, m, nullptr, 1.f, out, out_dtype, ldo);
+  if (rot)
+    rot_rows_kernel<false, true><<<gout, 256, 0, st>>>(y, KQ_DT_F32, N, m, svh, 1.f / 128.f, out, out_dtype, ldo,
+                                                       L.slices, m * N);
+  else
+    rot_rows_kernel<false, false><<<gout, 256, 0, st>>>(y, KQ_DT_F32, N, m, nullptr, 1.f, out, out_dtype, ldo,
+                                                        L.slices, m * N);
   return kq_check_launch(hipGetLastError(), fn);
 }
 
