@@ -212,11 +212,12 @@ def test_prefill_rows_match_oracle(gpu, rate_axis, m, shape, record_bits):
         assert relb <= (4e-3 if rotated else 8e-6)
 
 
-def test_prefill_one_hot_rows_read_the_weight_exactly(gpu):
+@pytest.mark.parametrize("k_tiles,n_tiles,record_bits", [(16, 24, (2, 4, 3)), (64, 24, (4, 3, 2))])
+def test_prefill_one_hot_rows_read_the_weight_exactly(gpu, k_tiles, n_tiles, record_bits):
     """One-hot fp32 rows through the prefill form of the regularized product
     return the weight bit for bit: the E4M3 label bytes the decode writes,
-    their unit E8M0 scales and the exact split."""
-    k_tiles, n_tiles, record_bits = 16, 24, (2, 4, 3)
+    their unit block scales and the exact split; at K = 1024 (342 rows, four
+    output tiles) the product is also split over K into fp32 planes."""
     payload = _random_matrix(k_tiles, n_tiles, "n", record_bits, 61)
     want = oq.decode_qsrt_weight(payload, k_tiles, n_tiles, record_bits, "n", _LABELS)
     rows = np.arange(0, k_tiles * 16, 3)
