@@ -383,7 +383,7 @@ def main() -> int:
         t_gemm = _time_loop(torch, gemm_step, max(5, args.steps // 5), 3, 0.3)
         flops = 2.0 * x2.shape[0] * rows * cols
         lin_bytes = x2.numel() * 2 + rows * cols + rows * cols // 32 + out2.numel() * 2
-        lin_pmc = _traffic_entry("linear", "kq::mx_linear_dma_kernel<0, 0>", lin_bytes)
+        lin_pmc = _traffic_entry("linear", "kq::mx_linear_dma_kernel<0, 0", lin_bytes)
         result["cfg2_mxfp8_linear"] = {
             "workload": "X[4096x7168] bf16 @ dequant(MXFP8 W[12288x7168])^T -> bf16, fp32 accumulate",
             "tflops": round(flops / t_gemm / 1e12, 1),
