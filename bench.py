@@ -430,6 +430,10 @@ def main() -> int:
                                                   p_l * (H // 2 + H // 32) + e_l * w13_b + p_l * I * 2),
             "down_grouped_w4a4": _traffic_entry("moe_prefill", "kq::moe::moe_large_mx_kernel<false, 4>",
                                                 p_l * (I // 2 + I // 32) + e_l * w2_b + p_l * H * 4),
+            "gateup_grouped_w4a8": _traffic_entry("moe_prefill", "kq::moe::moe_large_mx_kernel<true, 0>",
+                                                  p_l * (H + H // 32) + e_l * w13_b + p_l * I * 2),
+            "down_grouped_w4a8": _traffic_entry("moe_prefill", "kq::moe::moe_large_mx_kernel<false, 0>",
+                                                p_l * (I + I // 32) + e_l * w2_b + p_l * H * 4),
         }
         wbytes = len(active) * workloads.bytes_per_expert()
         moe_result = {
@@ -463,15 +467,14 @@ def main() -> int:
 
             t_mx = _time_loop(torch, mx_step, max(3, args.steps // 10), 2, 0.3)
             tf = flops / t_mx / 1e12
-            result[f"cfg3_moe_prefill_{'w4a8' if fmt == 'mxfp8' else 'w4a4'}"] = {
+            tag = "w4a8" if fmt == "mxfp8" else "w4a4"
+            result[f"cfg3_moe_prefill_{tag}"] = {
                 "workload": f"cfg3 shapes, activations {fmt.upper()}-quantized per row, block-scaled MFMA",
                 "tflops": round(tf, 1),
                 "ms": round(t_mx * 1e3, 3),
-                "roofline": _roofline("mfma", tf, moe_pmc["gateup_grouped_w4a4"] if fmt == "mxfp4" else None, peak),
+                "roofline": _roofline("mfma", tf, moe_pmc[f"gateup_grouped_{tag}"], peak),
+                "pmc": {k: moe_pmc[k] for k in (f"gateup_grouped_{tag}", f"down_grouped_{tag}")},
             }
-            if fmt == "mxfp4":
-                result["cfg3_moe_prefill_w4a4"]["pmc"] = {k: moe_pmc[k] for k in ("gateup_grouped_w4a4",
-                                                                                  "down_grouped_w4a4")}
         del weights, x3
 
     # -------------------------------------------------- config 5 decode --
