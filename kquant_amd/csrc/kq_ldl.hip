@@ -12,11 +12,14 @@
 //    workgroup per tile, a fast Walsh-Hadamard transform along the rows and /
 //    or columns in LDS (adds only), then one scale (1/128 exactly for both
 //    sides, fl(1/sqrt(128)) for one).
-//  * Cholesky (lower, fp32): right-looking over 64-column panels, two
-//    launches per step and all matrices of a batch per launch.  A diagonal
-//    block is factored and inverted by one wave in registers, by the
-//    trailing-update workgroup that completes it; the panel below is
-//    A21 inv(L11)^T and the trailing update A22 -= L21 L21^T, both on
+//  * Cholesky (lower, fp32): blocked over 64-column panels grouped into
+//    super-panels (four panels for batches of 8 and more, else one), all
+//    matrices of a batch per launch.  Within a super-panel one launch per
+//    panel brings its block column up to date with the super-panel's earlier
+//    panels and computes the panel below the diagonal as A21 inv(L11)^T;
+//    diagonal blocks are factored and inverted by one wave in registers, by
+//    the workgroup that completes them.  One update A22 -= L21 L21^T over
+//    the super-panel's columns then covers the trailing matrix.  Products on
 //    v_mfma_f32_16x16x4f32 from LDS.  A failing pivot (<= 0 or NaN) records
 //    the leading-minor order in info (LAPACK's convention) and the
 //    factorization continues with pivot 1, so every launch still completes.
@@ -206,9 +209,13 @@ __global__ __launch_bounds__(256) void chol_init_kernel(const float* a, int64_t 
   l[b * sl + i * ldl + j] = v;
 }
 
+// inv(L11) of panel p lives in slot p % 2 of the matrix's two winv slots
+// (winv + (2 b + p % 2) 64 x 64): a launch reads one slot while its
+// diagonal-factoring workgroup writes the other.
+//
 // Factor the diagonal block of panel 0 (one wave per matrix; the later
-// panels' diagonal blocks are factored by the trailing update that finishes
-// them), writing L11 back (zeros above its diagonal) and inv(L11) to winv.
+// panels' diagonal blocks are factored by the launch that finishes them),
+// writing L11 back (zeros above its diagonal) and inv(L11) to slot 0.
 __device__ __forceinline__ void store_diag(float (*a)[LD], float (*xi)[LD], float* L, int64_t ldl, int64_t c0,
                                            int nb, float* W, int bad, int* info) {
   const int lane = threadIdx.x & 63;
@@ -234,7 +241,7 @@ __global__ __launch_bounds__(64) void chol_diag_kernel(float* __restrict__ l, in
   __syncthreads();
   const int bad = factor64_wave(a, xi);
   __syncthreads();
-  store_diag(a, xi, L, ldl, 0, nb, winv + b * NB * NB, bad, info + b);
+  store_diag(a, xi, L, ldl, 0, nb, winv + b * 2 * NB * NB, bad, info + b);
 }
 
 // acc (this wave's 32x32 of a 64x64 tile, as 2x2 16x16 blocks) += X Y^T over
@@ -265,38 +272,116 @@ __device__ __forceinline__ void load_tile(float (*T)[LD], const float* M, int64_
   }
 }
 
-// Panel: L[i, p] = A[i, p] inv(L[p, p])^T for row block i = p + 1 + blockIdx.x.
+// The lane's (row, column) in a 64 x 64 tile for acc[bi][bj][q] of mm_nt.
+__device__ __forceinline__ void mm_pos(int bi, int bj, int q, int& r, int& c) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  r = 32 * (wave >> 1) + 16 * bi + 4 * (lane >> 4) + q;
+  c = 32 * (wave & 1) + 16 * bj + (lane & 15);
+}
+
+// Panel p of the super-panel [s0, s1), row block i = p + 1 + blockIdx.x:
+// A[i, p] -= sum over q in [s0, p) of L[i, q] L[p, q]^T (the updates of the
+// super-panel's earlier panels, left-looking), then L[i, p] = A[i, p]
+// inv(L[p, p])^T.  The workgroup of row block p + 1, when that is still in
+// the super-panel, then brings the diagonal block (p + 1, p + 1) up to date
+// with panels s0 .. p and factors it.
 __global__ __launch_bounds__(256) void chol_panel_kernel(float* __restrict__ l, int64_t n, int64_t ldl, int64_t sl,
-                                                         int p, const float* __restrict__ winv) {
+                                                         int p, int s0, int s1, float* __restrict__ winv,
+                                                         int* __restrict__ info) {
   __shared__ float av[NB][LD];
-  __shared__ float iv[NB][LD];
+  __shared__ float xi[NB][LD];
+  __shared__ float xj[NB][LD];
   const int64_t b = blockIdx.y;
   float* L = l + b * sl;
   const int64_t r0 = (int64_t)(p + 1 + blockIdx.x) * NB, c0 = (int64_t)p * NB;
-  load_tile(av, L, ldl, n, r0, c0);
-  const float* W = winv + b * NB * NB;
-  for (int i = threadIdx.x; i < NB * NB; i += 256) iv[i / NB][i % NB] = W[i];
-  __syncthreads();
   f32x4_t acc[2][2] = {};
-  mm_nt(av, iv, acc);
+  for (int q = s0; q < p; ++q) {
+    if (q > s0) __syncthreads();
+    load_tile(xi, L, ldl, n, r0, (int64_t)q * NB);
+    load_tile(xj, L, ldl, n, c0, (int64_t)q * NB);
+    __syncthreads();
+    mm_nt(xi, xj, acc);
+  }
+  load_tile(av, L, ldl, n, r0, c0);
+  const float* W = winv + (b * 2 + (p & 1)) * NB * NB;
+  __syncthreads();  // every wave is done with xi / xj; av is loaded
+  for (int i = threadIdx.x; i < NB * NB; i += 256) xi[i / NB][i % NB] = W[i];
+#pragma unroll
+  for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+    for (int bj = 0; bj < 2; ++bj)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        int r, c;
+        mm_pos(bi, bj, q, r, c);
+        av[r][c] -= acc[bi][bj][q];
+      }
+  __syncthreads();
+  f32x4_t lp[2][2] = {};
+  mm_nt(av, xi, lp);
+#pragma unroll
+  for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+    for (int bj = 0; bj < 2; ++bj)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        int r, c;
+        mm_pos(bi, bj, q, r, c);
+        if (r0 + r < n && c0 + c < n) L[(r0 + r) * ldl + c0 + c] = lp[bi][bj][q];
+      }
+  if (blockIdx.x != 0 || p + 1 >= s1) return;
+  // diagonal block p + 1: A[p + 1, p + 1] -= sum over q in [s0, p] of
+  // L[p + 1, q] L[p + 1, q]^T, where L[p + 1, p] is this workgroup's lp
+  __syncthreads();  // every wave is done reading av / xi
+#pragma unroll
+  for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+    for (int bj = 0; bj < 2; ++bj)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        int r, c;
+        mm_pos(bi, bj, q, r, c);
+        av[r][c] = lp[bi][bj][q];  // rows past n are zero (their A rows are)
+      }
+  __syncthreads();
+  f32x4_t dg[2][2] = {};
+  mm_nt(av, av, dg);
+  for (int q = s0; q < p; ++q) {
+    __syncthreads();
+    load_tile(xi, L, ldl, n, r0, (int64_t)q * NB);
+    __syncthreads();
+    mm_nt(xi, xi, dg);
+  }
+  __syncthreads();
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
   for (int bi = 0; bi < 2; ++bi)
 #pragma unroll
     for (int bj = 0; bj < 2; ++bj)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int64_t r = r0 + 32 * (wave >> 1) + 16 * bi + 4 * (lane >> 4) + j;
-        const int64_t c = c0 + 32 * (wave & 1) + 16 * bj + (lane & 15);
-        if (r < n && c < n) L[r * ldl + c] = acc[bi][bj][j];
+      for (int q = 0; q < 4; ++q) {
+        int r, c;
+        mm_pos(bi, bj, q, r, c);
+        xi[r][c] = (r0 + r < n && r0 + c < n) ? L[(r0 + r) * ldl + r0 + c] - dg[bi][bj][q] : (r == c ? 1.f : 0.f);
       }
+  __syncthreads();
+  if (wave == 0) {
+    const int bad = factor64_wave(xi, xj);
+    const int nb = (int)(n - r0 < NB ? n - r0 : NB);
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    store_diag(xi, xj, L, ldl, r0, nb, winv + (b * 2 + ((p + 1) & 1)) * NB * NB, bad, info + b);
+  }
+  (void)lane;
 }
 
-// Trailing update: A[bi, bj] -= L[bi, p] L[bj, p]^T over the lower tiles
-// bi >= bj > p (blockIdx.x enumerates them row by row).  The workgroup of
-// tile (p + 1, p + 1) then factors it as the next panel's diagonal block.
+// Trailing update A[bi, bj] -= sum over panels q in [q0, q1) of
+// L[bi, q] L[bj, q]^T over the lower tiles bi >= bj >= b0 (blockIdx.x
+// enumerates them row by row; the panels' products are summed in registers,
+// so A is read and written once).  The workgroup of tile (b0, b0) then
+// factors it as panel b0's diagonal block.
 __global__ __launch_bounds__(256) void chol_update_kernel(float* __restrict__ l, int64_t n, int64_t ldl, int64_t sl,
-                                                          int p, float* __restrict__ winv, int* __restrict__ info) {
+                                                          int b0, int q0, int q1, float* __restrict__ winv,
+                                                          int* __restrict__ info) {
   __shared__ float xi[NB][LD];
   __shared__ float xj[NB][LD];
   const int64_t b = blockIdx.y;
@@ -306,14 +391,17 @@ __global__ __launch_bounds__(256) void chol_update_kernel(float* __restrict__ l,
   while ((i + 1) * (i + 2) / 2 <= t) ++i;
   while (i * (i + 1) / 2 > t) --i;
   const int64_t j = t - i * (i + 1) / 2;
-  const int64_t ri = (int64_t)(p + 1 + i) * NB, rj = (int64_t)(p + 1 + j) * NB, c0 = (int64_t)p * NB;
-  load_tile(xi, L, ldl, n, ri, c0);
-  load_tile(xj, L, ldl, n, rj, c0);
-  __syncthreads();
+  const int64_t ri = (int64_t)(b0 + i) * NB, rj = (int64_t)(b0 + j) * NB;
   f32x4_t acc[2][2] = {};
-  mm_nt(xi, xj, acc);
+  for (int q = q0; q < q1; ++q) {
+    if (q > q0) __syncthreads();  // every wave is done reading the previous panel's tiles
+    load_tile(xi, L, ldl, n, ri, (int64_t)q * NB);
+    load_tile(xj, L, ldl, n, rj, (int64_t)q * NB);
+    __syncthreads();
+    mm_nt(xi, xj, acc);
+  }
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const bool next_diag = t == 0;  // tile (p + 1, p + 1): the next panel's diagonal block
+  const bool next_diag = t == 0;  // tile (b0, b0): panel b0's diagonal block
   if (next_diag) __syncthreads();  // every wave is done reading xi / xj
 #pragma unroll
   for (int bi = 0; bi < 2; ++bi)
@@ -338,7 +426,7 @@ __global__ __launch_bounds__(256) void chol_update_kernel(float* __restrict__ l,
     const int bad = factor64_wave(xi, xj);
     const int nb = (int)(n - ri < NB ? n - ri : NB);
     __builtin_amdgcn_s_waitcnt(0xc07f);
-    store_diag(xi, xj, L, ldl, ri, nb, winv + b * NB * NB, bad, info + b);
+    store_diag(xi, xj, L, ldl, ri, nb, winv + (b * 2 + (b0 & 1)) * NB * NB, bad, info + b);
   }
 }
 
@@ -440,7 +528,7 @@ extern "C" int kq_blockwise_hadamard(float* x, int64_t rows, int64_t cols, int64
 
 extern "C" int64_t kq_cholesky_workspace_size(int64_t n, int64_t batch) {
   if (n <= 0 || batch <= 0) return -1;
-  return batch * NB * NB * (int64_t)sizeof(float);
+  return batch * 2 * NB * NB * (int64_t)sizeof(float);  // two inv(L11) slots per matrix
 }
 
 extern "C" int kq_cholesky(const float* a, int64_t lda, int64_t stride_a, float* l, int64_t ldl, int64_t stride_l,
@@ -466,13 +554,29 @@ extern "C" int kq_cholesky(const float* a, int64_t lda, int64_t stride_a, float*
   const int m = (int)((n + NB - 1) / NB);
   chol_diag_kernel<<<(unsigned)batch, 64, 0, st>>>(l, n, ldl, stride_l, winv, info);
   if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_cholesky/diag");
-  for (int p = 0; p + 1 < m; ++p) {
-    const int q = m - p - 1;
-    chol_panel_kernel<<<dim3((unsigned)q, (unsigned)batch), 256, 0, st>>>(l, n, ldl, stride_l, p, winv);
-    if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_cholesky/panel");
-    chol_update_kernel<<<dim3((unsigned)((int64_t)q * (q + 1) / 2), (unsigned)batch), 256, 0, st>>>(
-        l, n, ldl, stride_l, p, winv, info);
-    if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_cholesky/update");
+  // Super-panels of `rank` panels: one launch per panel (its block column
+  // brought up to date with the super-panel's earlier panels, the panel
+  // below its diagonal block, and the next diagonal block factored), then one
+  // rank-(64 rank) update of everything to the right, so the trailing matrix
+  // is read and written once per super-panel.  Batches of 8 and more take
+  // four panels (48 matrices of n = 2048: 8.9 -> 7.3 ms on MI355X); fewer
+  // matrices take one, the right-looking form, whose panel launches are too
+  // small to carry the column updates and diagonal factorizations on their
+  // critical path (one n = 7168 matrix: 9.2 ms with one panel, 11.2 with four).
+  const int rank = batch >= 8 ? 4 : 1;
+  for (int s0 = 0; s0 < m; s0 += rank) {
+    const int s1 = s0 + rank < m ? s0 + rank : m;
+    for (int p = s0; p < s1 && p + 1 < m; ++p) {
+      chol_panel_kernel<<<dim3((unsigned)(m - p - 1), (unsigned)batch), 256, 0, st>>>(l, n, ldl, stride_l, p, s0,
+                                                                                     s1, winv, info);
+      if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_cholesky/panel");
+    }
+    if (s1 < m) {
+      const int64_t q = m - s1;
+      chol_update_kernel<<<dim3((unsigned)(q * (q + 1) / 2), (unsigned)batch), 256, 0, st>>>(l, n, ldl, stride_l,
+                                                                                          s1, s0, s1, winv, info);
+      if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_cholesky/update");
+    }
   }
   return KQ_OK;
 }

@@ -110,6 +110,27 @@ def test_cholesky_batched_and_in_place(gpu):
     assert torch.equal(again, got)
 
 
+@pytest.mark.parametrize("batch,n", [(8, 300), (12, 777)])
+def test_cholesky_super_panels(gpu, batch, n):
+    """Batches of 8 and more factor four 64-column panels per trailing
+    update (column updates inside the panel launches, diagonal blocks
+    factored by the workgroup that completes them): every matrix against
+    numpy's f64 factor, ragged last panels included."""
+    a = np.stack([_spd(n, 100 + i) for i in range(batch)])
+    got, info = _cholesky(torch.from_numpy(a).to(gpu), batch)
+    assert info.cpu().tolist() == [0] * batch
+    lower = got.cpu().numpy()
+    for i in range(batch):
+        assert np.array_equal(np.triu(lower[i], 1), np.zeros((n, n), dtype=lower.dtype))
+        back = _rel(a[i], lower[i].astype(np.float64) @ lower[i].T.astype(np.float64))
+        fwd = _rel(np.linalg.cholesky(a[i].astype(np.float64)), lower[i])
+        assert back <= 2e-6 and fwd <= 2e-5, (i, back, fwd)
+    bad = a.copy()
+    bad[5][200, 200] = -1.0
+    _, info = _cholesky(torch.from_numpy(bad).to(gpu), batch)
+    assert info.cpu().tolist()[5] == 201 and sum(info.cpu().tolist()) == 201
+
+
 def test_cholesky_large(gpu):
     """H13-sized (7168): input and residual built with f64 GEMMs on the GPU."""
     n = 7168
