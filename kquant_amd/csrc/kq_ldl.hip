@@ -263,9 +263,22 @@ __device__ __forceinline__ void mm_nt(const float (*X)[LD], const float (*Y)[LD]
   }
 }
 
-// Load rows [r0, r0 + 64) x cols [c0, c0 + 64) of M (zero past n).
+// Load rows [r0, r0 + 64) x cols [c0, c0 + 64) of M (zero past n): 16-byte
+// loads when the tile's columns are all in range and rows 16-byte aligned.
 __device__ __forceinline__ void load_tile(float (*T)[LD], const float* M, int64_t ld, int64_t n, int64_t r0,
                                           int64_t c0) {
+  if (c0 + NB <= n && ld % 4 == 0 && (reinterpret_cast<uintptr_t>(M) & 15) == 0) {
+    for (int i = threadIdx.x; i < NB * NB / 4; i += 256) {
+      const int r = i / (NB / 4), c = 4 * (i % (NB / 4));
+      f32x4_t v = {0.f, 0.f, 0.f, 0.f};
+      if (r0 + r < n) v = *reinterpret_cast<const f32x4_t*>(M + (r0 + r) * ld + c0 + c);
+      T[r][c] = v[0];
+      T[r][c + 1] = v[1];
+      T[r][c + 2] = v[2];
+      T[r][c + 3] = v[3];
+    }
+    return;
+  }
   for (int i = threadIdx.x; i < NB * NB; i += 256) {
     const int r = i / NB, c = i % NB;
     T[r][c] = (r0 + r < n && c0 + c < n) ? M[(r0 + r) * ld + c0 + c] : 0.f;
