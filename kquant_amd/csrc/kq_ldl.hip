@@ -405,6 +405,19 @@ __global__ __launch_bounds__(256) void chol_update_kernel(float* __restrict__ l,
   while (i * (i + 1) / 2 > t) --i;
   const int64_t j = t - i * (i + 1) / 2;
   const int64_t ri = (int64_t)(b0 + i) * NB, rj = (int64_t)(b0 + j) * NB;
+  // this lane's A entries, loaded first: their latency hides behind the products
+  float av[2][2][4];
+#pragma unroll
+  for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+    for (int bj = 0; bj < 2; ++bj)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        int lr, lc;
+        mm_pos(bi, bj, q, lr, lc);
+        const int64_t r = ri + lr, c = rj + lc;
+        av[bi][bj][q] = r < n && c < n ? L[r * ldl + c] : 0.f;
+      }
   f32x4_t acc[2][2] = {};
   for (int q = q0; q < q1; ++q) {
     if (q > q0) __syncthreads();  // every wave is done reading the previous panel's tiles
@@ -413,7 +426,7 @@ __global__ __launch_bounds__(256) void chol_update_kernel(float* __restrict__ l,
     __syncthreads();
     mm_nt(xi, xj, acc);
   }
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wave = threadIdx.x >> 6;
   const bool next_diag = t == 0;  // tile (b0, b0): panel b0's diagonal block
   if (next_diag) __syncthreads();  // every wave is done reading xi / xj
 #pragma unroll
@@ -422,11 +435,11 @@ __global__ __launch_bounds__(256) void chol_update_kernel(float* __restrict__ l,
     for (int bj = 0; bj < 2; ++bj)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int lr = 32 * (wave >> 1) + 16 * bi + 4 * (lane >> 4) + q;
-        const int lc = 32 * (wave & 1) + 16 * bj + (lane & 15);
+        int lr, lc;
+        mm_pos(bi, bj, q, lr, lc);
         const int64_t r = ri + lr, c = rj + lc;
         if (r < n && c < n) {
-          const float v = L[r * ldl + c] - acc[bi][bj][q];
+          const float v = av[bi][bj][q] - acc[bi][bj][q];
           if (next_diag) xi[lr][lc] = v;
           else L[r * ldl + c] = v;
         } else if (next_diag) {
