@@ -150,21 +150,20 @@ __device__ __forceinline__ void quantize_qchunk(const QChunk<IN>& ch, int64_t bl
   }
 }
 
-
 // Each thread handles ITERS chunks 256 apart (a wave covers 16 consecutive
 // blocks per step, so every load and store of a wave is one contiguous
 // range); all loads are issued before the first block is converted.  With
 // contiguous rows the input offset is the chunk index times 8 elements, so
-// no division by the row length is needed.
-#ifndef KQ_QUANT_ITERS
-#define KQ_QUANT_ITERS 2
-#endif
-constexpr int QUANT_ITERS = KQ_QUANT_ITERS;
+// no division by the row length is needed.  Measured on MI355X (cold):
+// MXFP8 at cfg2 is fastest with 2 (6.32 TB/s; 1: 5.78, 4: 6.01), MXFP4 at
+// cfg1 with 4 (8.44 us; 2: 8.75, 8: 9.65).
+template <int FMT> constexpr int quant_iters() { return FMT == 1 ? 4 : 2; }
 
 template <int IN, int FMT, bool HW, bool CONTIG>
 __global__ __launch_bounds__(256) void mx_quantize_kernel(
     const void* __restrict__ in, int64_t ld_in, int64_t nblk, int64_t total_blocks,
     uint8_t* __restrict__ out_q, uint8_t* __restrict__ out_scale) {
+  constexpr int QUANT_ITERS = quant_iters<FMT>();
   const int64_t c0 = (int64_t)blockIdx.x * (256 * QUANT_ITERS) + threadIdx.x;
   QChunk<IN> v[QUANT_ITERS];
 #pragma unroll
@@ -375,6 +374,7 @@ template <int IN, int FMT>
 static hipError_t launch_quantize(bool hw, const void* in, int64_t ld, int64_t nblk,
                                   int64_t total, void* oq, uint8_t* os, hipStream_t st) {
   const int64_t chunks = total * 4;
+  constexpr int QUANT_ITERS = quant_iters<FMT>();
   const dim3 grid((unsigned)((chunks + 256 * QUANT_ITERS - 1) / (256 * QUANT_ITERS)));
   const bool contig = ld == nblk * 32;
   uint8_t* q = (uint8_t*)oq;
