@@ -117,7 +117,6 @@ __global__ __launch_bounds__(256, 1) void syrk_upper_kernel(
   int rem = blockIdx.x, ti = 0;
   while (rem >= ntiles - ti) { rem -= ntiles - ti; ++ti; }
   const int tj = ti + rem;
-  const bool diag = ti == tj;
   const int64_t row0 = (int64_t)ti * TILE, col0 = (int64_t)tj * TILE;
 
   // LDS: [buffer][slab] with slabs A(hi) B(hi) [A(lo) B(lo)]
@@ -265,7 +264,6 @@ __global__ __launch_bounds__(256, 1) void syrk_upper_kernel(
           *p = overwrite ? accv[i][j][r] : *p + accv[i][j][r];
         }
       }
-  (void)diag;
 }
 
 // ---------------------------------------------------------------------------

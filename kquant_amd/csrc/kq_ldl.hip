@@ -366,7 +366,7 @@ __global__ __launch_bounds__(256) void chol_panel_kernel(float* __restrict__ l, 
     mm_nt(xi, xi, dg);
   }
   __syncthreads();
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wave = threadIdx.x >> 6;
 #pragma unroll
   for (int bi = 0; bi < 2; ++bi)
 #pragma unroll
@@ -384,7 +384,6 @@ __global__ __launch_bounds__(256) void chol_panel_kernel(float* __restrict__ l, 
     __builtin_amdgcn_s_waitcnt(0xc07f);
     store_diag(xi, xj, L, ldl, r0, nb, winv + (b * 2 + ((p + 1) & 1)) * NB * NB, bad, info + b);
   }
-  (void)lane;
 }
 
 // Trailing update A[bi, bj] -= sum over panels q in [q0, q1) of

@@ -79,7 +79,7 @@ def test_damped_hessian(gpu):
     assert denom == n
     assert _rel_fro(ref, h.cpu().numpy()) <= TOL
     d = torch.diagonal(h).cpu().double()
-    assert torch.allclose(d, torch.from_numpy(np.diag(ref)).double(), rtol=1e-5, atol=0)
+    assert torch.allclose(d, torch.from_numpy(np.diag(ref).copy()).double(), rtol=1e-5, atol=0)
 
 
 def test_cfg4_full_size_sampled_entries(gpu):
