@@ -173,8 +173,18 @@ __global__ __launch_bounds__(512, 1) void mx_linear_kernel(
 // mx_linear_kernel, with every operand moved HBM -> LDS by
 // buffer_load ... lds through a ring of three stages issued two steps ahead,
 // continuing across tile boundaries: the kernel is persistent (one workgroup
-// per CU, tiles t = worker, worker + G, ... with N fastest, workers of one XCD
-// numbered consecutively so they share A rows in its L2).
+// per CU, tiles t = worker, worker + G, ... in groups of LIN_GROUP_M row
+// tiles with N fastest inside a group, workers of one XCD numbered
+// consecutively so the 32 tiles they run together share 4 A row tiles and
+// 8 weight column tiles in its L2).
+//  * two wave groups in ping-pong: waves 0-3 and 4-7 put one wave on each
+//    SIMD, and group 1 runs half a step behind group 0.  A step of a group is
+//    a memory phase (every LDS read of the step into registers) and a compute
+//    phase (expansion and the 32 MFMAs, registers only), separated by
+//    workgroup barriers, so on every SIMD one wave streams MFMAs while the
+//    other reads LDS.  Group 0 also issues all of a stage's direct loads
+//    (13 / 11 per wave) and waits for them; group 1 starts with one extra
+//    barrier and group 0 ends with one, so both cross the same number.
 //  * k order: in a 64-k step, lane half f of MFMA q (0..3) takes
 //    k = 32 f + 8 q + [0, 8) on both operands, so a lane's weights for the
 //    step are one 16-byte chunk (E2M1) or two (E4M3) of its row, read with
@@ -198,7 +208,15 @@ template <int FMT> constexpr int w_row() { return FMT == 0 ? 64 : 32; }  // byte
 template <int FMT> constexpr int b_bytes() { return lin::BN * w_row<FMT>(); }
 constexpr int S_BYTES = lin::BN * 4;
 template <int FMT> constexpr int stage() { return A_BYTES + b_bytes<FMT>() + S_BYTES; }
-template <int FMT> constexpr int loads() { return 4 + (FMT == 0 ? 2 : 1) + 1; }  // per wave per stage
+constexpr int LIN_GROUP_M = 4;  // row tiles per group of the tile order
+
+// Tile tl of the grouped order -> (row tile mt, column tile nt).
+__device__ __forceinline__ void tile_mn(int tl, int mtiles, int ntiles, int& mt, int& nt) {
+  const int per = LIN_GROUP_M * ntiles, g = tl / per, rem = tl - g * per;
+  const int gsz = min(LIN_GROUP_M, mtiles - g * LIN_GROUP_M);
+  mt = g * LIN_GROUP_M + rem % gsz;
+  nt = rem / gsz;
+}
 }  // namespace lin3
 
 __shared__ __attribute__((aligned(16))) unsigned char lin3_lds[lin3::NSTAGE * lin3::stage<0>()];
@@ -210,7 +228,9 @@ __global__ __launch_bounds__(512, 1) void mx_linear_dma_kernel(
     int64_t ldc, int M, int N, int K, int KB, int slices, int64_t plane) {
   using namespace lin3;
   using dma::i32x4_t;
-  constexpr int WROW = w_row<FMT>(), STAGE = stage<FMT>(), LOADS = loads<FMT>() - (UNIT ? 1 : 0);
+  constexpr int WQ = FMT == 0 ? 4 : 2;  // weight loads per loading wave per stage
+  constexpr int H = FMT == 0 ? 2 : 1;   // 16-byte weight chunks per row and step
+  constexpr int WROW = w_row<FMT>(), STAGE = stage<FMT>(), LOADS = 8 + WQ + (UNIT ? 0 : 1);
   constexpr int BM = lin::BM, BN = lin::BN, BK = lin::BK;
   const int mtiles = (M + BM - 1) / BM, ntiles = (N + BN - 1) / BN, tiles = mtiles * ntiles;
   const int total = tiles * slices;
@@ -219,39 +239,46 @@ __global__ __launch_bounds__(512, 1) void mx_linear_dma_kernel(
   if (worker >= total) return;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int64_t kw = FMT == 0 ? KB : KB / 2;  // packed bytes per weight row
-  const int64_t ks = KB / 32;                 // scale bytes per weight row
+  const bool g0 = wave < 4;  // group 0 (waves 0-3) loads and leads; group 1 trails by half a step
+  const int lw = wave & 3;
+  const int64_t kw = FMT == 0 ? KB : KB / 2;
+  const int64_t ks = KB / 32;
   const int steps = K / BK;
   const uint32_t lds0 = dma::lds_offset_of(lin3_lds);
   const i32x4_t a_rsrc = dma::make_rsrc(a, a_bytes);
   const i32x4_t w_rsrc = dma::make_rsrc(wq, w_bytes);
   const i32x4_t s_rsrc = dma::make_rsrc(ws, s_bytes);
 
-  // ---- load side (item lt, step ls < ls_end); per-lane row offsets, invalid -> past the range
   int lt = worker, ls = 0, ls_end = steps;
-  uint32_t a_off[4], w_off[2], s_off;
+  // loading lane's first A row and weight row of the tile, and how many of
+  // the rows 32 q (A) / 64 q (E4M3) or 128 q (E2M1) past them are in range
+  uint32_t a_base = 0, w_base = 0, s_off = 0;
+  int a_lim = 0, w_lim = 0;
+  const uint32_t a_qstep = (uint32_t)(32 * lda * 2);
+  constexpr int WSTEP = FMT == 0 ? 64 : 128;
+  const uint32_t w_qstep = (uint32_t)(WSTEP * kw);
   auto set_load_tile = [&]() {
     const bool live = lt < total;
     const int sl = live ? lt / tiles : 0, tl = live ? lt - sl * tiles : 0;
     ls = (int)((int64_t)sl * steps / slices);
     ls_end = (int)((int64_t)(sl + 1) * steps / slices);
-    const int mt = live ? tl / ntiles : 0, nt = live ? tl - mt * ntiles : 0;
+    int mt = 0, nt = 0;
+    if (live) tile_mn(tl, mtiles, ntiles, mt, nt);
     const int m0 = mt * BM, n0 = nt * BN;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int row = 8 * (8 * q + wave) + (lane >> 3);
+    {
+      const int row = 8 * lw + (lane >> 3);  // + 32 q; the swizzle does not depend on q
       const int ch = (lane & 7) ^ ((row >> 1) & 7);
-      a_off[q] = live && m0 + row < M ? (uint32_t)((int64_t)(m0 + row) * lda * 2 + ch * 16) : a_bytes;
-    }
-#pragma unroll
-    for (int q = 0; q < (FMT == 0 ? 2 : 1); ++q) {
-      // E4M3: 16 rows x 4 chunks per instruction; E2M1: 32 rows x 2 chunks
-      const int row = FMT == 0 ? 16 * (8 * q + wave) + (lane >> 2) : 32 * wave + (lane >> 1);
-      const int ch = FMT == 0 ? (lane & 3) ^ ((row >> 2) & 3) : (lane & 1) ^ ((row >> 3) & 1);
-      w_off[q] = live && n0 + row < N ? (uint32_t)((int64_t)(n0 + row) * kw + ch * 16) : w_bytes;
+      a_lim = live ? M - m0 - row : 0;
+      a_base = a_lim > 0 ? (uint32_t)((int64_t)(m0 + row) * lda * 2 + ch * 16) : 0u;
     }
     {
-      const int row = 32 * wave + (lane & 31);
+      const int row = FMT == 0 ? 16 * lw + (lane >> 2) : 32 * lw + (lane >> 1);  // + WSTEP q
+      const int ch = FMT == 0 ? (lane & 3) ^ ((row >> 2) & 3) : (lane & 1) ^ ((row >> 3) & 1);
+      w_lim = live ? N - n0 - row : 0;
+      w_base = w_lim > 0 ? (uint32_t)((int64_t)(n0 + row) * kw + ch * 16) : 0u;
+    }
+    {
+      const int row = 64 * lw + lane;
       s_off = live && n0 + row < N ? (uint32_t)((int64_t)(n0 + row) * ks) : s_bytes;
     }
   };
@@ -259,17 +286,17 @@ __global__ __launch_bounds__(512, 1) void mx_linear_dma_kernel(
     const uint32_t base = lds0 + (uint32_t)(slot * STAGE);
     const int k0 = ls * BK, kb0 = k0 % KB;
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-      dma::load_to_lds16(a_rsrc, a_off[q] >= a_bytes ? a_bytes : a_off[q] + 2 * (uint32_t)k0,
-                         base + (uint32_t)((8 * q + wave) * 1024));
+    for (int q = 0; q < 8; ++q)
+      dma::load_to_lds16(a_rsrc, 32 * q < a_lim ? a_base + q * a_qstep + 2 * (uint32_t)k0 : a_bytes,
+                         base + (uint32_t)((4 * q + lw) * 1024));
     const uint32_t wk = FMT == 0 ? (uint32_t)kb0 : (uint32_t)kb0 / 2;
 #pragma unroll
-    for (int q = 0; q < (FMT == 0 ? 2 : 1); ++q)
-      dma::load_to_lds16(w_rsrc, w_off[q] >= w_bytes ? w_bytes : w_off[q] + wk,
-                         base + (uint32_t)(A_BYTES + (8 * q + wave) * 1024));
-    if (!UNIT && lane < 32)
+    for (int q = 0; q < WQ; ++q)
+      dma::load_to_lds16(w_rsrc, WSTEP * q < w_lim ? w_base + q * w_qstep + wk : w_bytes,
+                         base + (uint32_t)(A_BYTES + (4 * q + lw) * 1024));
+    if (!UNIT)
       dma::load_to_lds4(s_rsrc, s_off >= s_bytes ? s_bytes : s_off + (uint32_t)((kb0 / 32) & ~3),
-                        base + (uint32_t)(A_BYTES + b_bytes<FMT>() + wave * 128));
+                        base + (uint32_t)(A_BYTES + b_bytes<FMT>() + lw * 256));
   };
   auto advance = [&]() {
     if (++ls == ls_end) {
@@ -278,10 +305,9 @@ __global__ __launch_bounds__(512, 1) void mx_linear_dma_kernel(
     }
   };
 
-  // ---- compute side: per-lane LDS offsets
   const int wm = (wave >> 1) * 64, wn = (wave & 1) * 128;
   const int frow = lane & 31, f = lane >> 5;
-  int arow[2], axor[2], woff[4][FMT == 0 ? 2 : 1], soff[4];
+  int arow[2], axor[2], woff[4][H], soff[4];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int row = wm + i * 32 + frow;
@@ -293,22 +319,27 @@ __global__ __launch_bounds__(512, 1) void mx_linear_dma_kernel(
     const int row = wn + j * 32 + frow;
     if (FMT == 0) {
       woff[j][0] = A_BYTES + row * WROW + 16 * ((2 * f) ^ ((row >> 2) & 3));
-      woff[j][FMT == 0 ? 1 : 0] = A_BYTES + row * WROW + 16 * ((2 * f + 1) ^ ((row >> 2) & 3));
+      woff[j][H - 1] = A_BYTES + row * WROW + 16 * ((2 * f + 1) ^ ((row >> 2) & 3));
     } else {
       woff[j][0] = A_BYTES + row * WROW + 16 * (f ^ ((row >> 3) & 1));
     }
     soff[j] = A_BYTES + b_bytes<FMT>() + row * 4 + f;
   }
 
-  set_load_tile();
-  issue(0);
-  advance();
-  issue(1);
-  advance();
+  if (g0) {
+    set_load_tile();
+    issue(0);
+    advance();
+    issue(1);
+    advance();
+  } else {
+    __builtin_amdgcn_s_barrier();  // group 1 starts half a step behind
+  }
   int cslot = 0;
   for (int t = worker; t < total; t += G) {
     const int sl = t / tiles, tl = t - sl * tiles;
-    const int mt = tl / ntiles, nt = tl - mt * ntiles;
+    int mt, nt;
+    tile_mn(tl, mtiles, ntiles, mt, nt);
     const int s_begin = (int)((int64_t)sl * steps / slices), s_end = (int)((int64_t)(sl + 1) * steps / slices);
     const int m0 = mt * BM, n0 = nt * BN;
     const bool active = m0 + wm < M && n0 + wn < N;
@@ -322,27 +353,41 @@ __global__ __launch_bounds__(512, 1) void mx_linear_dma_kernel(
 
     for (int s = s_begin; s < s_end; ++s) {
       const int kb0 = (s * BK) % KB;
-      dma::wait_and_barrier<LOADS>();
-      issue(cslot == 0 ? 2 : cslot - 1);
-      advance();
+      if (g0) {
+        dma::wait_and_barrier<LOADS>();  // stage s landed; group 1 is done reading slot s - 1
+        issue(cslot == 0 ? 2 : cslot - 1);
+        advance();
+      } else {
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+      }
+      // memory phase: this step's weight chunks, scales and activation fragments into registers
+      u32x4_t wv[4][H];
+      uint32_t sc[4];
+      bf16x8_t fa[4][2];
       if (active) {
         const unsigned char* st = lin3_lds + cslot * STAGE;
-        const int sbyte = (kb0 / 32) & 3;  // 0 or 2: this step's blocks in the scale dword
-        u32x4_t wv[4][FMT == 0 ? 2 : 1];
-        uint32_t sc[4];
+        const int sbyte = (kb0 / 32) & 3;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
 #pragma unroll
-          for (int h = 0; h < (FMT == 0 ? 2 : 1); ++h)
-            wv[j][h] = *reinterpret_cast<const u32x4_t*>(st + woff[j][h]);
+          for (int h = 0; h < H; ++h) wv[j][h] = *reinterpret_cast<const u32x4_t*>(st + woff[j][h]);
           sc[j] = UNIT ? 127u : st[soff[j] + sbyte];
         }
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          bf16x8_t fa[2], fb[4];
+        for (int q = 0; q < 4; ++q)
 #pragma unroll
           for (int i = 0; i < 2; ++i)
-            fa[i] = *reinterpret_cast<const bf16x8_t*>(st + arow[i] + 16 * (q ^ axor[i]));
+            fa[q][i] = *reinterpret_cast<const bf16x8_t*>(st + arow[i] + 16 * (q ^ axor[i]));
+      }
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the slot's reads are in registers
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      // compute phase
+      if (active) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          bf16x8_t fb[4];
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             u32x2_t w;
@@ -354,7 +399,7 @@ __global__ __launch_bounds__(512, 1) void mx_linear_dma_kernel(
           for (int i = 0; i < 2; ++i)
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[q][i], fb[j], acc[i][j], 0, 0, 0);
         }
       }
       cslot = cslot == 2 ? 0 : cslot + 1;
@@ -376,6 +421,7 @@ __global__ __launch_bounds__(512, 1) void mx_linear_dma_kernel(
           }
     }
   }
+  if (g0) __builtin_amdgcn_s_barrier();  // matches group 1's first barrier
   __builtin_amdgcn_s_waitcnt(dma::waitcnt_vm(0));  // no load may land after the workgroup ends
 }
 
