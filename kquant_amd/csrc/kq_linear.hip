@@ -380,9 +380,15 @@ __global__ __launch_bounds__(512, 1) void mx_linear_dma_kernel(
           for (int i = 0; i < 2; ++i)
             fa[q][i] = *reinterpret_cast<const bf16x8_t*>(st + arow[i] + 16 * (q ^ axor[i]));
       }
-      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the slot's reads are in registers
+      // every LDS read of the slot stays above the barrier and has returned
+      // (the barrier builtin alone does not order memory accesses), and no
+      // MFMA is scheduled into the memory phase
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
+      __builtin_amdgcn_sched_barrier(0);
       // compute phase
       if (active) {
 #pragma unroll
