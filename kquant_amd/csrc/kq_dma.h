@@ -60,9 +60,12 @@ __device__ __forceinline__ uint32_t lds_offset_of(const void* p) {
 
 // Wait until at most N of this wave's direct loads are outstanding, then
 // barrier: after it every wave's older loads have landed in LDS and every
-// wave has finished the LDS reads it issued before the barrier.
+// wave has finished the LDS reads it issued before the barrier.  The barrier
+// builtin does not order memory accesses by itself, so compiler memory
+// clobbers on both sides keep every LDS access on its side of it.
 template <int N>
 __device__ __forceinline__ void wait_and_barrier() {
+  asm volatile("" ::: "memory");
   __builtin_amdgcn_s_waitcnt(waitcnt_vm(N));
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");

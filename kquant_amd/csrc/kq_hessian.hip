@@ -587,6 +587,7 @@ __device__ __forceinline__ void syrk3_range(const i32x4_t rsrc, uint32_t nbytes,
   for (int p = 0; p < NST - 1; ++p) issue(p, t_begin + p * BK);
   int stage = 0;
   for (int64_t s = 0; s < steps; ++s) {
+    asm volatile("" ::: "memory");  // the barrier builtin alone does not order LDS accesses
     if (share_b) __builtin_amdgcn_s_waitcnt(waitcnt_vm((NST - 2) * QPW));
     else __builtin_amdgcn_s_waitcnt(waitcnt_vm((NST - 2) * 2 * QPW));
     __builtin_amdgcn_s_barrier();
@@ -831,6 +832,7 @@ __device__ __forceinline__ void global_load_to_lds4(const void* src, uint32_t ld
 
 // wait until this wave has at most n (< 16) direct loads in flight, then barrier
 __device__ __forceinline__ void syrk4_wait(int n) {
+  asm volatile("" ::: "memory");  // the barrier builtin alone does not order LDS accesses
   switch (n) {
 #define KQ_WAIT_CASE(c) \
   case c: __builtin_amdgcn_s_waitcnt(waitcnt_vm(c)); break;

@@ -358,6 +358,7 @@ __global__ __launch_bounds__(512, 1) void mx_linear_dma_kernel(
         issue(cslot == 0 ? 2 : cslot - 1);
         advance();
       } else {
+        asm volatile("" ::: "memory");
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
       }
