@@ -381,6 +381,21 @@ def main() -> int:
 
         quantize_step()
         t_gemm = _time_loop(torch, gemm_step, max(5, args.steps // 5), 3, 0.3)
+        # The reference's own path on this GPU, for comparison: dequantize the
+        # weight to bf16, then torch's bf16 GEMM (hipBLASLt).
+        wdq = torch.empty(rows, cols, dtype=torch.bfloat16, device=dev)
+
+        def dequant_step():
+            N.call("kq_mx_dequant", N.FMT_MXFP8_E4M3, N.ptr(q8), N.ptr(s8), rows, cols, N.DT_BF16,
+                   N.ptr(wdq), 0, stream)
+
+        def ref_step():
+            dequant_step()
+            torch.nn.functional.linear(x2, wdq)
+
+        t_ref = _time_loop(torch, ref_step, max(5, args.steps // 5), 3, 0.3)
+        t_mm = _time_loop(torch, lambda: torch.nn.functional.linear(x2, wdq), max(5, args.steps // 5), 3, 0.3)
+        del wdq
         flops = 2.0 * x2.shape[0] * rows * cols
         lin_bytes = x2.numel() * 2 + rows * cols + rows * cols // 32 + out2.numel() * 2
         lin_pmc = _traffic_entry("linear", "kq::mx_linear_dma_kernel<0, 0", lin_bytes)
@@ -388,6 +403,8 @@ def main() -> int:
             "workload": "X[4096x7168] bf16 @ dequant(MXFP8 W[12288x7168])^T -> bf16, fp32 accumulate",
             "tflops": round(flops / t_gemm / 1e12, 1),
             "us": round(t_gemm * 1e6, 1),
+            "dequant_then_bf16_gemm_us": round(t_ref * 1e6, 1),
+            "bf16_gemm_on_dequantized_us": round(t_mm * 1e6, 1),
             "roofline": _roofline("mfma", flops / t_gemm / 1e12, lin_pmc),
             "pmc": lin_pmc,
         }
