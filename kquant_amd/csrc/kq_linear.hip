@@ -183,7 +183,8 @@ __global__ __launch_bounds__(512, 1) void mx_linear_kernel(
 //    phase (expansion and the 32 MFMAs, registers only), separated by
 //    workgroup barriers, so on every SIMD one wave streams MFMAs while the
 //    other reads LDS.  Group 0 also issues all of a stage's direct loads
-//    (13 / 11 per wave) and waits for them; group 1 starts with one extra
+//    (13 E4M3 / 11 E2M1 per wave, one fewer with unit scales) and waits for
+//    them; group 1 starts with one extra
 //    barrier and group 0 ends with one, so both cross the same number.
 //  * k order: in a 64-k step, lane half f of MFMA q (0..3) takes
 //    k = 32 f + 8 q + [0, 8) on both operands, so a lane's weights for the
