@@ -22,6 +22,7 @@ Each configuration carries a ``cpu_baseline``: the reference's CPU path
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import platform
@@ -59,6 +60,9 @@ def _args():
     p.add_argument("--summarize-pmc", nargs="+", metavar="DIR",
                    help="summarize rocprofv3 --pmc databases (FETCH_SIZE; WRITE_SIZE, TCC_HIT_sum, "
                         "TCC_MISS_sum) of one bench section into profiles/traffic_<section>.json")
+    p.add_argument("--summarize-mfma", nargs="+", metavar="DIR",
+                   help="summarize rocprofv3 --pmc databases of MFMA_COUNTERS of one bench section into "
+                        "profiles/mfma_<section>.json")
     p.add_argument("--summarize-stats", nargs="+", metavar="DIR",
                    help="print the per-kernel table (calls, average and total time) of rocprofv3 "
                         "--kernel-trace --stats databases as markdown")
@@ -206,6 +210,72 @@ def summarize_pmc(dirs: list[str], section: str, out_dir: str) -> int:
     return 0
 
 
+MFMA_COUNTERS = ("SQ_VALU_MFMA_BUSY_CYCLES", "SQ_BUSY_CYCLES", "SQ_INSTS_VALU_MFMA_MOPS_BF16",
+                 "SQ_INSTS_VALU_MFMA_MOPS_F8", "SQ_INSTS_VALU_MFMA_MOPS_F6F4", "SQ_INSTS_VALU_MFMA_MOPS_F32",
+                 "GRBM_GUI_ACTIVE")
+XCDS, SIMDS = 8, 1024  # MI355X: 8 XCDs, 256 CUs x 4 SIMDs
+
+
+def summarize_mfma(dirs: list[str], section: str, out_dir: str) -> int:
+    """Per-kernel MFMA utilisation of a section's rocprofv3 --pmc databases
+    (MFMA_COUNTERS) into profiles/mfma_<section>.json: the clock
+    (GRBM_GUI_ACTIVE, summed over the XCDs, / XCDs / duration), MFMA-busy
+    cycles per SIMD-cycle, and the flops the MFMA MOPS counters count (x 512)
+    against the dense peak scaled to the measured clock.  Durations are those
+    of the counted dispatches (counter collection serializes dispatches)."""
+    import sqlite3
+
+    per: dict[tuple[str, int], dict] = {}
+    for d in dirs:
+        for db in sorted(Path(d).rglob("*.db")):
+            con = sqlite3.connect(str(db))
+            for name, grid, disp, counter, value, dur in con.execute(
+                    "select kernel_name, grid_size, dispatch_id, counter_name, value, duration "
+                    "from counters_collection"):
+                k = per.setdefault((_short_kernel(name), int(grid)), {"disp": {}, "dur": {}})
+                k["disp"].setdefault(int(disp), {})[counter] = k["disp"].get(int(disp), {}).get(counter, 0.0) + value
+                k["dur"][int(disp)] = float(dur)
+    peaks = {"BF16": BF16_PEAK_TFLOPS, "F8": FP8_PEAK_TFLOPS, "F6F4": FP4_PEAK_TFLOPS, "F32": FP32_PEAK_TFLOPS}
+    kernels = []
+    for (name, grid), k in sorted(per.items()):
+        disps = list(k["disp"].values())
+        n = len(disps)
+
+        def mean(c):
+            return sum(d.get(c, 0.0) for d in disps) / n
+
+        dur_ns = sum(k["dur"].values()) / n
+        gui = mean("GRBM_GUI_ACTIVE") / XCDS
+        busy = mean("SQ_VALU_MFMA_BUSY_CYCLES")
+        row = {"kernel": name, "grid_size": grid, "dispatches": n, "duration_us": round(dur_ns / 1e3, 2),
+               "clock_ghz": round(gui / dur_ns, 3) if dur_ns else None,
+               "mfma_busy_frac": round(busy / (gui * SIMDS), 4) if gui else None,
+               "raw": {c: round(mean(c), 1) for c in MFMA_COUNTERS}}
+        for fmt, peak in peaks.items():
+            mops = mean(f"SQ_INSTS_VALU_MFMA_MOPS_{fmt}")
+            if mops > 0 and dur_ns:
+                tflops = mops * 512 / dur_ns / 1e3
+                row[f"mfma_{fmt.lower()}"] = {
+                    "flops_per_launch": mops * 512, "tflops": round(tflops, 1),
+                    "frac_of_peak": round(tflops / peak, 4),
+                    "frac_of_peak_at_clock": round(tflops / (peak * (gui / dur_ns) / 2.4), 4) if gui else None}
+        kernels.append(row)
+    out = {
+        "section": section,
+        "command": f"rocprofv3 --kernel-include-regex 'kq::' --pmc {' '.join(MFMA_COUNTERS)} -d <dir> -o p -- "
+                   f"python3 bench.py --only {section} --steps 5 --warmup 1 --no-cpu-baseline; "
+                   f"python3 bench.py --summarize-mfma <dir> --section {section}",
+        "note": "clock = GRBM_GUI_ACTIVE / 8 XCDs / duration; mfma_busy_frac = SQ_VALU_MFMA_BUSY_CYCLES / "
+                "(GUI cycles x 1024 SIMDs); flops = MFMA MOPS x 512; peaks are the 2.4 GHz datasheet "
+                "figures, frac_of_peak_at_clock rescales them to the measured clock",
+        "kernels": kernels,
+    }
+    path = Path(out_dir) / f"mfma_{section}.json"
+    path.write_text(json.dumps(out, indent=1) + "\n")
+    print(f"wrote {path} ({len(kernels)} kernels)")
+    return 0
+
+
 def summarize_stats(dirs: list[str]) -> int:
     """Markdown table of the top_kernels view of rocprofv3 databases."""
     import sqlite3
@@ -277,6 +347,8 @@ def main() -> int:
         return summarize_stats(args.summarize_stats)
     if args.summarize_pmc:
         return summarize_pmc(args.summarize_pmc, args.section or "section", args.summary_dir)
+    if args.summarize_mfma:
+        return summarize_mfma(args.summarize_mfma, args.section or "section", args.summary_dir)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
               "(this build has no multi-GPU path)", file=sys.stderr)
@@ -408,7 +480,36 @@ def main() -> int:
             "roofline": _roofline("mfma", flops / t_gemm / 1e12, lin_pmc),
             "pmc": lin_pmc,
         }
-        del x2, out2
+        # The production operand form (scripts/closure_mxfp8_mlp.py:146-187):
+        # the input rows quantized to MXFP8, MXFP8 x MXFP8 on the fp8 matrix
+        # cores.  Timed on rows quantized once (the kernel), and with the
+        # per-call input quantization (kq_mx_linear_mm).
+        m2 = x2.shape[0]
+        xq = torch.empty(m2, cols, dtype=torch.uint8, device=dev)
+        xs = torch.empty(m2, cols // 32, dtype=torch.uint8, device=dev)
+        N.call("kq_mx_quantize", N.FMT_MXFP8_E4M3, N.DT_BF16, N.ptr(x2), cols, m2, cols, N.ptr(xq), N.ptr(xs), 0,
+               stream)
+        mm_ws_bytes = int(N.library().kq_mx_linear_mm_workspace_size(m2, cols))
+        mm_ws = torch.empty(mm_ws_bytes, dtype=torch.uint8, device=dev)
+        a8_step = _bound(N, "kq_mx_linear_mx", N.FMT_MXFP8_E4M3, N.ptr(xq), N.ptr(xs), cols, N.FMT_MXFP8_E4M3,
+                         N.ptr(q8), N.ptr(s8), m2, rows, cols, N.DT_BF16, N.ptr(out2), rows, stream)
+        mm_step = _bound(N, "kq_mx_linear_mm", N.FMT_MXFP8_E4M3, N.ptr(x2), N.DT_BF16, cols, N.ptr(q8), N.ptr(s8),
+                         m2, rows, cols, N.DT_BF16, N.ptr(out2), rows, N.ptr(mm_ws), mm_ws_bytes, stream)
+        t_a8 = _time_loop(torch, a8_step, max(5, args.steps // 5), 3, 0.3)
+        t_mm = _time_loop(torch, mm_step, max(5, args.steps // 5), 3, 0.3)
+        a8_bytes = m2 * cols + m2 * cols // 32 + rows * cols + rows * cols // 32 + out2.numel() * 2
+        a8_pmc = _traffic_entry("linear", "kq::mx_linear_a8_kernel<0", a8_bytes)
+        result["cfg2_mxfp8_linear_a8"] = {
+            "workload": "MXFP8(X [4096x7168]) @ MXFP8(W [12288x7168])^T -> bf16 on the block-scaled fp8 MFMA, "
+                        "fp32 accumulate (the reference's production operand form)",
+            "tflops": round(flops / t_a8 / 1e12, 1),
+            "us": round(t_a8 * 1e6, 1),
+            "with_input_quantize_us": round(t_mm * 1e6, 1),
+            "with_input_quantize_tflops": round(flops / t_mm / 1e12, 1),
+            "roofline": _roofline("mfma", flops / t_a8 / 1e12, a8_pmc, FP8_PEAK_TFLOPS),
+            "pmc": a8_pmc,
+        }
+        del x2, out2, xq, xs, mm_ws
 
     # ------------------------------------------ config 3 MoE prefill GEMM --
     moe_result = None
@@ -623,16 +724,34 @@ def main() -> int:
                    N.ptr(acc), 7168, N.SYRK_OVERWRITE, N.ptr(h_ws), h_ws_bytes, stream)
 
         th = _time_loop(torch, h_step, 10, 2, 0.3)
+        # the whole API step of configuration 4 (i): accumulate, then
+        # H = sym(acc) / n with diag += 0.01 mean(diag) (kq_syrk_finalize)
+        h_out = torch.empty_like(acc)
+
+        def h_api_step():
+            h_step()
+            N.call("kq_syrk_finalize", N.ptr(acc), 7168, 7168, ctypes.c_double(65536.0), ctypes.c_float(0.01),
+                   N.ptr(h_out), 7168, stream)
+
+        th_api = _time_loop(torch, h_api_step, 10, 2, 0.3)
         flops = workloads.syrk_flops(65536, 7168)
         # rows once + the upper 256 x 256 tiles of the fp32 accumulator written once
         syrk_pmc = _traffic_entry("hessian", "kq::syrk256_dma_kernel", 65536 * 7168 * 2 + 28 * 29 // 2 * 256 * 256 * 4)
         result["cfg4_hessian_k7168"] = {
+            "workload": "cfg4 (i): X^T X of 65536 Student-t(4) bf16 rows, K = 7168, fp32 accumulation",
             "tflops": round(flops / th / 1e12, 1),
             "ms": round(th * 1e3, 3),
             "roofline": _roofline("mfma", flops / th / 1e12, syrk_pmc),
             "pmc": syrk_pmc,
+            "with_finalize": {
+                "what": "accumulate + kq_syrk_finalize (sym / n, diag += 0.01 mean(diag)): the full H of config 4",
+                "ms": round(th_api * 1e3, 3),
+                "finalize_ms": round((th_api - th) * 1e3, 3),
+                "tflops": round(flops / th_api / 1e12, 1),
+                "frac_bf16": round(flops / th_api / 1e12 / BF16_PEAK_TFLOPS, 4),
+            },
         }
-        del x4, acc, h_ws
+        del x4, acc, h_ws, h_out
 
     # --------------------------- config 4 (ii) per-expert Hessians, K=2048 --
     if not args.quick and want("hessian_experts"):
@@ -648,11 +767,25 @@ def main() -> int:
                    N.ptr(gates), k2, N.ptr(hacc), N.SYRK_SQUARE_WEIGHTS, stream)
 
         the = _time_loop(torch, he_step, 10, 2, 0.3)
+        # the API step: accumulate, f64 weight sums, sym(acc) / sum per expert
+        # (expert_hessians_from_rows: every expert's full symmetric H)
+        hout = torch.empty_like(hacc)
+        dens = torch.empty(experts, dtype=torch.float64, device=dev)
+
+        def he_api_step():
+            he_step()
+            N.call("kq_segment_weight_sums", N.ptr(gates), N.ptr(offsets_d), experts, N.SYRK_SQUARE_WEIGHTS,
+                   N.ptr(dens), stream)
+            N.call("kq_syrk_finalize_grouped", N.ptr(hacc), k2, experts, N.ptr(dens), N.ptr(hout), stream)
+
+        the_api = _time_loop(torch, he_api_step, 10, 2, 0.3)
         flops = float((counts.double() * k2 * (k2 + 1)).sum())
-        hbytes = pairs * k2 * 2 + pairs * 4 + experts * k2 * k2 * 4
-        # the kernel writes the upper 256 x 256 tiles of each expert's accumulator
-        he_pmc = _traffic_entry("hessian_experts", "kq::syrk256w_dma_kernel", pairs * k2 * 2 + pairs * 4
-                                + experts * 36 * 256 * 256 * 4)
+        # what the timed kernel moves: rows and weights read once, the upper
+        # 256 x 256 tiles (36 at K = 2048) of each expert's accumulator written once
+        hbytes = pairs * k2 * 2 + pairs * 4 + experts * 36 * 256 * 256 * 4
+        # the API step's algorithmic bytes: rows and weights in, every expert's full symmetric H out
+        api_bytes = pairs * k2 * 2 + pairs * 4 + experts * k2 * k2 * 4
+        he_pmc = _traffic_entry("hessian_experts", "kq::syrk256w_dma_kernel", hbytes)
         result["cfg4_hessian_experts_k2048"] = {
             "workload": "cfg4 (ii): gate^2-weighted X^T X of each expert's routed rows, 65536 tokens "
                         "top-8 Zipf(1.1) over 384 experts (524288 rows of 2048 bf16), one grouped launch",
@@ -664,8 +797,15 @@ def main() -> int:
             "active_experts": int((counts > 0).sum()),
             "flops": flops,
             "bytes": hbytes,
+            "with_finalize": {
+                "what": "accumulate + weight sums + kq_syrk_finalize_grouped (every expert's full symmetric H)",
+                "ms": round(the_api * 1e3, 3),
+                "bytes": api_bytes,
+                "gbs": round(api_bytes / the_api / 1e9, 1),
+                "hbm_frac": round(api_bytes / the_api / 1e9 / HBM_PEAK_GBS, 4),
+            },
         }
-        del rows, hacc
+        del rows, hacc, hout
 
     # ------------------------------- encoder H finalize (rotation, block LDL) --
     if not args.quick and want("h_finalize"):
@@ -1048,11 +1188,54 @@ def main() -> int:
         },
         "roofline": _roofline("hbm", quant_gbs, head_pmc),
         "cpu_baseline": cpu,
-        "moe_prefill": moe_result,
         "configs": result,
+        "moe_prefill": moe_result,
+        # last, so that a reader keeping only the end of the line keeps it
+        "summary": _summary(result, moe_result),
     }
     print(json.dumps(line))
     return 0
+
+
+def _summary(result: dict, moe_result: dict | None) -> dict:
+    """The figure and roofline fraction of every configuration in a few
+    hundred bytes (times in us or ms, fractions of the MI355X peaks)."""
+    out = {}
+
+    def pick(name, src, **fields):
+        if src is None:
+            return
+        row = {}
+        for key, path in fields.items():
+            v = src
+            for part in path.split("."):
+                v = v.get(part) if isinstance(v, dict) else None
+            if v is not None:
+                row[key] = v
+        if row:
+            out[name] = row
+
+    pick("cfg2_quantize", result.get("cfg2_mxfp8_quantize"), us="cold_us", warm_us="warm_us")
+    if "cfg2_mxfp8_quantize" in result:
+        out["cfg2_quantize"]["frac"] = round(result["cfg2_mxfp8_quantize"]["cold_gbs"] / HBM_PEAK_GBS, 4)
+    pick("cfg2_linear_a16", result.get("cfg2_mxfp8_linear"), us="us", tflops="tflops", frac_bf16="roofline.frac",
+         ref_path_us="dequant_then_bf16_gemm_us")
+    pick("cfg2_linear_a8", result.get("cfg2_mxfp8_linear_a8"), us="us", tflops="tflops", frac_fp8="roofline.frac",
+         with_quantize_us="with_input_quantize_us")
+    pick("cfg3_w4a16", moe_result, ms="ms", tflops="tflops", frac_bf16="roofline.frac",
+         frac_fp4="frac_of_fp4_dense_peak")
+    pick("cfg3_w4a8", result.get("cfg3_moe_prefill_w4a8"), ms="ms", tflops="tflops", frac_fp8="roofline.frac")
+    pick("cfg3_w4a4", result.get("cfg3_moe_prefill_w4a4"), ms="ms", tflops="tflops", frac_fp4="roofline.frac")
+    dec = result.get("cfg5_moe_decode") or {}
+    for b in (1, 4, 16):
+        pick(f"cfg5_b{b}", dec.get(f"batch{b}"), us="us", frac="hbm_frac", x4t_us="x4t_scales_us")
+    pick("cfg1", result.get("cfg1_mxfp4_codec"), quantize_us="quantize_us", quantize_frac="hbm_frac_quantize",
+         dequant_us="dequant_us", dequant_frac="hbm_frac_dequant")
+    pick("cfg4_i", result.get("cfg4_hessian_k7168"), ms="ms", frac_bf16="roofline.frac",
+         with_finalize_ms="with_finalize.ms")
+    pick("cfg4_ii", result.get("cfg4_hessian_experts_k2048"), ms="ms", frac_hbm="roofline.frac",
+         with_finalize_ms="with_finalize.ms", with_finalize_frac="with_finalize.hbm_frac")
+    return out
 
 
 if __name__ == "__main__":

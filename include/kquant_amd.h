@@ -224,6 +224,35 @@ int kq_mx_linear(int w_fmt, const void* a, int64_t lda, const void* w_q,
                  const uint8_t* w_scale, int64_t m, int64_t n, int64_t k,
                  int out_dtype, void* c, int64_t ldc, void* stream);
 
+/* C [m, n] = dequant(A) [m, k] x dequant(W) [n, k]^T with both operands
+ * MXFP8: A E4M3 bytes [m, k] (row stride lda bytes, lda % 16 == 0) with E8M0
+ * scales [m, k/32], W E4M3 bytes [n, k] with E8M0 scales [n, k/32]; the
+ * block-scaled fp8 MFMA multiplies the bytes and scales as they are, fp32
+ * accumulation, C in bf16 or fp32 (row stride ldc).  This is the operand
+ * contract of kquant's production MXFP8 linear (scripts/closure_mxfp8_mlp.py:
+ * 146-160 _reference_from_packed: quantize the input, dequantize both
+ * operands, fp32 product; :163-187 _production_linear).  a_fmt and w_fmt
+ * must be KQ_FMT_MXFP8_E4M3; k % 128 == 0; a_q, w_q 16-byte aligned,
+ * scales 4-byte aligned.  The matrix cores sum the 64 products of a step
+ * with a few fp32 ulps of error (measured ~1e-5 relative). */
+int kq_mx_linear_mx(int a_fmt, const void* a_q, const uint8_t* a_scale, int64_t lda, int w_fmt,
+                    const void* w_q, const uint8_t* w_scale, int64_t m, int64_t n, int64_t k,
+                    int out_dtype, void* c, int64_t ldc, void* stream);
+
+/* Workspace bytes of kq_mx_linear_mm (the quantized input rows), -1 on bad
+ * sizes. */
+int64_t kq_mx_linear_mm_workspace_size(int64_t m, int64_t k);
+
+/* mxfp8_linear.mm of kquant's production MXFP8 linear
+ * (scripts/closure_mxfp8_mlp.py:172-177): the input rows A [m, k] (bf16, f16
+ * or f32, row stride lda elements) are quantized to MXFP8 with the
+ * kq_mx_quantize rule into the workspace (block_fp8_linear.quantize_input,
+ * :155), then kq_mx_linear_mx.  w_fmt: KQ_FMT_MXFP8_E4M3; k % 128 == 0;
+ * workspace 256-byte aligned, uninitialised. */
+int kq_mx_linear_mm(int w_fmt, const void* a, int a_dtype, int64_t lda, const void* w_q,
+                    const uint8_t* w_scale, int64_t m, int64_t n, int64_t k, int out_dtype, void* c,
+                    int64_t ldc, void* workspace, int64_t workspace_bytes, void* stream);
+
 /* -------------------------------------------------------------- Hessian -- */
 
 /* acc += X^T diag(w) X for X [n, k] (row stride ld elements, k % 8 == 0,
@@ -250,8 +279,10 @@ int kq_syrk_accumulate(int in_dtype, const void* x, int64_t ld, int64_t n, int64
  * order.  Only unweighted bf16 rows take the split; other calls, or a
  * workspace smaller than kq_syrk_accumulate_workspace_size (0 when the
  * split does not pay), run as kq_syrk_accumulate.  workspace: 256-byte
- * aligned, uninitialised, used by one call at a time (size for the current
- * device's CU count). */
+ * aligned, uninitialised, used by one call at a time.  The size function
+ * assumes dense rows (ld == k) and the CU count of the current device; the
+ * call plans with the CU count of its stream's device, so make that device
+ * current when sizing. */
 int64_t kq_syrk_accumulate_workspace_size(int in_dtype, int64_t n, int64_t k, int weighted);
 int kq_syrk_accumulate_ws(int in_dtype, const void* x, int64_t ld, int64_t n, int64_t k,
                           const float* weights, float* acc, int64_t ld_acc, uint32_t flags,

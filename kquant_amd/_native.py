@@ -63,6 +63,8 @@ SIGNATURES: dict[str, list] = {
     "kq_sym_lerp": [_VP, _F32, _VP, _I64, _F32, _VP, _VP],
     "kq_cov_stats": [_VP, _I64, _VP, _VP, _VP],
     "kq_mx_linear": [_INT, _VP, _I64, _VP, _VP, _I64, _I64, _I64, _INT, _VP, _I64, _VP],
+    "kq_mx_linear_mx": [_INT, _VP, _VP, _I64, _INT, _VP, _VP, _I64, _I64, _I64, _INT, _VP, _I64, _VP],
+    "kq_mx_linear_mm": [_INT, _VP, _INT, _I64, _VP, _VP, _I64, _I64, _I64, _INT, _VP, _I64, _VP, _I64, _VP],
     "kq_moe_forward": [_INT, _F32, _F32, _VP, _I64, _I64, _I64, _VP, _VP, _INT, _INT, _I64,
                        _VP, _VP, _VP, _VP, _INT, _VP, _VP, _I64, _U32, _VP],
     "kq_x4t_analyze": [_VP, _I64, _I64, _I64, _VP, _VP, _VP],
@@ -142,6 +144,8 @@ def library() -> ctypes.CDLL:
         lib.kq_moe_x4t_workspace_size.argtypes = [_I64, _INT, _INT, _I64, _I64]
         lib.kq_mx_linear_f32_workspace_size.restype = ctypes.c_int64
         lib.kq_mx_linear_f32_workspace_size.argtypes = [_I64, _I64]
+        lib.kq_mx_linear_mm_workspace_size.restype = ctypes.c_int64
+        lib.kq_mx_linear_mm_workspace_size.argtypes = [_I64, _I64]
         lib.kq_cholesky_workspace_size.restype = ctypes.c_int64
         lib.kq_cholesky_workspace_size.argtypes = [_I64, _I64]
         lib.kq_block_ldl_workspace_size.restype = ctypes.c_int64

@@ -751,9 +751,11 @@ static TailPlan plan_tail(int ntiles, int cus, int64_t n) {
   return p;
 }
 
-static int device_cus() {
+// CUs of the device a stream runs on (the current device for the null
+// stream), so the grid plan matches where the launch goes.
+static int device_cus(hipStream_t st = nullptr) {
   int dev = 0, cus = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  if (st ? hipStreamGetDevice(st, &dev) != hipSuccess : hipGetDevice(&dev) != hipSuccess) return 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
   return cus;
 }
@@ -771,7 +773,7 @@ static hipError_t launch_syrk256_dma(const void* x, int64_t ld, int64_t n, int64
   const int per = (ntiles + SYRK_XCDS - 1) / SYRK_XCDS;
   TailPlan plan{0, 0, 1};
   if (workspace) {
-    plan = plan_tail(ntiles, device_cus(), n);
+    plan = plan_tail(ntiles, device_cus(st), n);
     if (tail_slot_bytes(plan) > ws_bytes) plan = TailPlan{0, 0, 1};
   }
   const int blocks = SYRK_XCDS * (plan.chunks > 1 ? plan.j1 + plan.nmax * plan.chunks : per);
@@ -1041,7 +1043,7 @@ static hipError_t launch_syrk256w_dma(const void* x, int64_t ld, int64_t k, cons
                                       const int64_t* offsets, int groups, int square_w, hipStream_t st) {
   const int nt = (int)((k + syrk4::TILE - 1) / syrk4::TILE);
   const int64_t items = (int64_t)(nt * (nt + 1) / 2) * groups;
-  int cus = device_cus();
+  int cus = device_cus(st);
   if (cus <= 0) cus = 256;
   const int grid = (int)(items < cus ? items : cus);
   syrk256w_dma_kernel<<<dim3(grid), dim3(512), 0, st>>>((const uint16_t*)x, ld, k, w, acc, nt, offsets, groups,
@@ -1342,6 +1344,8 @@ static int syrk_accumulate(int in_dtype, const void* x, int64_t ld, int64_t n, i
 
 extern "C" int64_t kq_syrk_accumulate_workspace_size(int in_dtype, int64_t n, int64_t k, int weighted) {
   if (n < 0 || k <= 0) return -1;
+  // rows assumed dense (ld == k); a call with a wider ld whose rows pass the
+  // 4 GiB range of the direct loads takes the path without a workspace
   if (!dma_syrk(in_dtype, weighted ? (const void*)1 : nullptr, n, k)) return 0;
   const int nt = (int)((k + syrk3::TILE - 1) / syrk3::TILE);
   return tail_slot_bytes(plan_tail(nt * (nt + 1) / 2, device_cus(), n));

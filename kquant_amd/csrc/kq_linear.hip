@@ -433,6 +433,224 @@ __global__ __launch_bounds__(512, 1) void mx_linear_dma_kernel(
   __builtin_amdgcn_s_waitcnt(dma::waitcnt_vm(0));  // no load may land after the workgroup ends
 }
 
+// ------------------------------------------- MXFP8 x MXFP8 (A8W8) --
+// C[M, N] = dequant(A)[M, K] x dequant(W)[N, K]^T with both operands MXFP8
+// (E4M3 bytes, one E8M0 byte per 32 along K): the operand contract of
+// kquant's production MXFP8 linear, which quantizes its input rows before
+// the product (scripts/closure_mxfp8_mlp.py:146-160, :172-177).  One
+// v_mfma_scale_f32_32x32x64_f8f6f4 per 32x32 block and 64-k step multiplies
+// the E4M3 bytes with their E8M0 bytes as they are.  Lane (m, g) of a
+// 32x32x64 operand holds row m and byte i at k = 32 (i / 16) + 16 g + i % 16
+// (16-byte chunks g and 2 + g of the row's 64-k step) and gives the scale of
+// its row's block g (checked with an in-bounds one-wave probe).
+//  * persistent, tiles of 256 x 256 in mx_linear_dma_kernel's grouped order,
+//    workers of one XCD numbered consecutively; 8 waves of 64 x 128 (2 x 4
+//    blocks) as two ping-pong groups: group 0 issues every direct load and
+//    leads, group 1 runs half a step behind; a step is a memory phase (all
+//    LDS reads of the step into registers) and a compute phase (8 MFMAs).
+//  * 4-stage ring of 64-k steps (three steps in flight): per stage the A and
+//    W tiles, 256 rows x 64 B each, 16-byte chunk c of row r at slot
+//    c ^ ((r / 4) % 4) (the 16 lanes of a 128-bit read hit 16 distinct bank
+//    groups), and one scale dword per row of each (the four blocks of the
+//    row's 128-k window, two of them this step's; needs K % 128 == 0).
+//  * rows past M or N read as zero (out-of-range offsets) and are not stored.
+namespace lin8 {
+constexpr int NSTAGE = 4, BK = 64;
+constexpr int OP_BYTES = 256 * 64;             // one operand tile per stage
+constexpr int S_OFF = 2 * OP_BYTES;            // A scale dwords, then W's
+constexpr int STAGE = 2 * OP_BYTES + 2 * 1024;
+constexpr int LOADS = 4 + 4 + 1 + 1;           // direct loads per loading wave per stage
+}  // namespace lin8
+
+__shared__ __attribute__((aligned(16))) unsigned char lin8_lds[lin8::NSTAGE * lin8::STAGE];
+
+typedef int i32x8_t __attribute__((ext_vector_type(8)));
+
+template <int OUT>
+__global__ __launch_bounds__(512, 1) void mx_linear_a8_kernel(
+    const uint8_t* __restrict__ aq, int64_t lda, uint32_t a_bytes, const uint8_t* __restrict__ as,
+    uint32_t as_bytes, const uint8_t* __restrict__ wq, uint32_t w_bytes, const uint8_t* __restrict__ ws,
+    uint32_t ws_bytes, void* __restrict__ c, int64_t ldc, int M, int N, int K) {
+  using namespace lin8;
+  using dma::i32x4_t;
+  constexpr int BM = lin::BM, BN = lin::BN;
+  const int mtiles = (M + BM - 1) / BM, ntiles = (N + BN - 1) / BN, total = mtiles * ntiles;
+  const int G = gridDim.x;
+  const int worker = (int)(blockIdx.x % 8) * (G / 8) + (int)(blockIdx.x / 8);
+  if (worker >= total) return;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool g0 = wave < 4;
+  const int lw = wave & 3;
+  const int64_t ks = K / 32;  // scale bytes per row, both operands
+  const int steps = K / BK;
+  const uint32_t lds0 = dma::lds_offset_of(lin8_lds);
+  const i32x4_t a_rsrc = dma::make_rsrc(aq, a_bytes), w_rsrc = dma::make_rsrc(wq, w_bytes);
+  const i32x4_t as_rsrc = dma::make_rsrc(as, as_bytes), ws_rsrc = dma::make_rsrc(ws, ws_bytes);
+
+  // ---- load side: load q (0..3) of wave lw fills 16-row piece 4q + lw of
+  // both tiles (1 KiB each); lane l fetches row 16 (4q + lw) + l / 4, slot
+  // l % 4, i.e. logical chunk (l % 4) ^ ((l / 16) % 4)
+  int lt = worker, ls = 0;
+  const int prow = 16 * lw + (lane >> 2);            // + 64 q
+  const int pch = (lane & 3) ^ ((lane >> 4) & 3);
+  uint32_t a_base = 0, w_base = 0, as_off = 0, ws_off = 0;
+  int a_lim = 0, w_lim = 0;
+  const uint32_t a_qstep = (uint32_t)(64 * lda), w_qstep = (uint32_t)(64 * K);
+  auto set_load_tile = [&]() {
+    const bool live = lt < total;
+    int mt = 0, nt = 0;
+    if (live) lin3::tile_mn(lt, mtiles, ntiles, mt, nt);
+    const int m0 = mt * BM, n0 = nt * BN;
+    a_lim = live ? M - m0 - prow : 0;
+    a_base = a_lim > 0 ? (uint32_t)((int64_t)(m0 + prow) * lda + 16 * pch) : 0u;
+    w_lim = live ? N - n0 - prow : 0;
+    w_base = w_lim > 0 ? (uint32_t)((int64_t)(n0 + prow) * K + 16 * pch) : 0u;
+    const int srow = 64 * lw + lane;
+    as_off = live && m0 + srow < M ? (uint32_t)((int64_t)(m0 + srow) * ks) : as_bytes;
+    ws_off = live && n0 + srow < N ? (uint32_t)((int64_t)(n0 + srow) * ks) : ws_bytes;
+  };
+  auto issue = [&](int slot) {
+    const uint32_t base = lds0 + (uint32_t)(slot * STAGE);
+    const uint32_t k0 = (uint32_t)(ls * BK);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      dma::load_to_lds16(a_rsrc, 64 * q < a_lim ? a_base + q * a_qstep + k0 : a_bytes,
+                         base + (uint32_t)((4 * q + lw) * 1024));
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      dma::load_to_lds16(w_rsrc, 64 * q < w_lim ? w_base + q * w_qstep + k0 : w_bytes,
+                         base + (uint32_t)(OP_BYTES + (4 * q + lw) * 1024));
+    const uint32_t sk = (k0 / 32) & ~3u;
+    dma::load_to_lds4(as_rsrc, as_off >= as_bytes ? as_bytes : as_off + sk, base + (uint32_t)(S_OFF + lw * 256));
+    dma::load_to_lds4(ws_rsrc, ws_off >= ws_bytes ? ws_bytes : ws_off + sk,
+                      base + (uint32_t)(S_OFF + 1024 + lw * 256));
+  };
+  auto advance = [&]() {
+    if (++ls == steps) {
+      ls = 0;
+      lt += G;
+      set_load_tile();
+    }
+  };
+
+  // ---- compute side
+  const int wm = (wave >> 1) * 64, wn = (wave & 1) * 128;
+  const int fr = lane & 31, fg = lane >> 5;
+  int aoff[2][2], woff[4][2], asb[2], wsb[4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int r = wm + 32 * i + fr, sw = (r >> 2) & 3;
+    aoff[i][0] = r * 64 + 16 * (fg ^ sw);
+    aoff[i][1] = r * 64 + 16 * ((2 + fg) ^ sw);
+    asb[i] = S_OFF + 4 * r + fg;
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int r = wn + 32 * j + fr, sw = (r >> 2) & 3;
+    woff[j][0] = OP_BYTES + r * 64 + 16 * (fg ^ sw);
+    woff[j][1] = OP_BYTES + r * 64 + 16 * ((2 + fg) ^ sw);
+    wsb[j] = S_OFF + 1024 + 4 * r + fg;
+  }
+
+  if (g0) {
+    set_load_tile();
+#pragma unroll
+    for (int p = 0; p < NSTAGE - 1; ++p) {
+      issue(p);
+      advance();
+    }
+  } else {
+    __builtin_amdgcn_s_barrier();  // group 1 starts half a step behind
+  }
+  int cslot = 0;
+  for (int t = worker; t < total; t += G) {
+    int mt, nt;
+    lin3::tile_mn(t, mtiles, ntiles, mt, nt);
+    const int m0 = mt * BM, n0 = nt * BN;
+    const bool active = m0 + wm < M && n0 + wn < N;
+    float16_t acc[2][4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    for (int s = 0; s < steps; ++s) {
+      const int kb = (s * BK / 32) & 3;  // this step's first block in the stage's scale dwords
+      if (g0) {
+        dma::wait_and_barrier<2 * LOADS>();  // stage s landed; group 1 is done reading slot s - 1
+        issue(cslot == 0 ? NSTAGE - 1 : cslot - 1);
+        advance();
+      } else {
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+      }
+      // memory phase
+      gemm::u32x4_t av[2][2], wv[4][2];
+      uint32_t sa[2], sw[4];
+      if (active) {
+        const unsigned char* st = lin8_lds + cslot * STAGE;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          av[i][0] = *reinterpret_cast<const gemm::u32x4_t*>(st + aoff[i][0]);
+          av[i][1] = *reinterpret_cast<const gemm::u32x4_t*>(st + aoff[i][1]);
+          sa[i] = st[asb[i] + kb];
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          wv[j][0] = *reinterpret_cast<const gemm::u32x4_t*>(st + woff[j][0]);
+          wv[j][1] = *reinterpret_cast<const gemm::u32x4_t*>(st + woff[j][1]);
+          sw[j] = st[wsb[j] + kb];
+        }
+      }
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_sched_barrier(0);
+      // compute phase
+      if (active) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const i32x8_t b8{(int)wv[j][0][0], (int)wv[j][0][1], (int)wv[j][0][2], (int)wv[j][0][3],
+                           (int)wv[j][1][0], (int)wv[j][1][1], (int)wv[j][1][2], (int)wv[j][1][3]};
+#pragma unroll
+          for (int i = 0; i < 2; ++i) {
+            const i32x8_t a8{(int)av[i][0][0], (int)av[i][0][1], (int)av[i][0][2], (int)av[i][0][3],
+                             (int)av[i][1][0], (int)av[i][1][1], (int)av[i][1][2], (int)av[i][1][3]};
+            acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a8, b8, acc[i][j], 0, 0, 0, (int)sa[i],
+                                                                        0, (int)sw[j]);
+          }
+        }
+      }
+      cslot = cslot == NSTAGE - 1 ? 0 : cslot + 1;
+    }
+
+    if (active) {
+      // D (32x32): lane holds column l % 32, rows 8 (r / 4) + 4 (l / 32) + r % 4
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int gm = m0 + wm + 32 * i + 8 * (r >> 2) + 4 * fg + (r & 3);
+            const int gn = n0 + wn + 32 * j + fr;
+            if (gm < M && gn < N) {
+              if (OUT == 2) static_cast<float*>(c)[(int64_t)gm * ldc + gn] = acc[i][j][r];
+              else static_cast<__bf16*>(c)[(int64_t)gm * ldc + gn] = (__bf16)acc[i][j][r];
+            }
+          }
+    }
+  }
+  if (g0) __builtin_amdgcn_s_barrier();  // matches group 1's first barrier
+  __builtin_amdgcn_s_waitcnt(dma::waitcnt_vm(0));  // no load may land after the workgroup ends
+}
+
 // Exact three-term bf16 split of fp32 A: a = a0 + a1 + a2 (each step keeps
 // the next 8 significant bits and leaves an exactly representable residual),
 // written as row [a0 | a1 | a2] of a [rows, 3k] bf16 matrix.  Four columns
@@ -497,6 +715,37 @@ static hipError_t launch_linear_dma(const uint16_t* a, int64_t lda, const uint8_
       mx_linear_dma_kernel<FMT, OUT, UNIT><<<grid, lin::THREADS, 0, st>>>(
           a + m0 * lda, lda, (uint32_t)(mc * lda * 2), wq + n0 * kw, ws + n0 * ks,
           (uint32_t)(nc * kw), (uint32_t)(nc * ks), cp, ldc, mc, nc, K, KB, slices, plane);
+      if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+  }
+  return hipSuccess;
+}
+
+// MXFP8 x MXFP8 launch: operands larger than one 32-bit buffer range are cut
+// into row chunks of M and N.  Needs K % 128 == 0, lda % 16 == 0, 16-byte
+// aligned E4M3 operands and 4-byte aligned scale rows of K / 32 bytes.
+template <int OUT>
+static hipError_t launch_linear_a8(const uint8_t* aq, const uint8_t* as, int64_t lda, const uint8_t* wq,
+                                   const uint8_t* ws, void* c, int64_t ldc, int M, int N, int K, hipStream_t st) {
+  int dev = 0, cus = 0;
+  hipError_t e = st ? hipStreamGetDevice(st, &dev) : hipGetDevice(&dev);
+  if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e != hipSuccess) return e;
+  const int64_t ks = K / 32;
+  const int64_t m_chunk = (int64_t)(dma::MAX_RANGE / (uint64_t)lda) / lin::BM * lin::BM;
+  const int64_t n_chunk = (int64_t)(dma::MAX_RANGE / (uint64_t)K) / lin::BN * lin::BN;
+  for (int64_t m0 = 0; m0 < M; m0 += m_chunk) {
+    const int mc = (int)(M - m0 < m_chunk ? M - m0 : m_chunk);
+    for (int64_t n0 = 0; n0 < N; n0 += n_chunk) {
+      const int nc = (int)(N - n0 < n_chunk ? N - n0 : n_chunk);
+      const int tiles = ((mc + lin::BM - 1) / lin::BM) * ((nc + lin::BN - 1) / lin::BN);
+      int grid = cus / 8 * 8 > 0 ? cus / 8 * 8 : 8;
+      if (grid > (tiles + 7) / 8 * 8) grid = (tiles + 7) / 8 * 8;
+      void* cp = OUT == 2 ? (void*)(static_cast<float*>(c) + m0 * ldc + n0)
+                          : (void*)(static_cast<uint16_t*>(c) + m0 * ldc + n0);
+      mx_linear_a8_kernel<OUT><<<grid, lin::THREADS, 0, st>>>(
+          aq + m0 * lda, lda, (uint32_t)(mc * lda), as + m0 * ks, (uint32_t)(mc * ks), wq + n0 * K,
+          (uint32_t)(nc * K), ws + n0 * ks, (uint32_t)(nc * ks), cp, ldc, mc, nc, K);
       if ((e = hipGetLastError()) != hipSuccess) return e;
     }
   }
@@ -616,4 +865,68 @@ extern "C" int kq_mx_linear_f32(int w_fmt, const float* a, int64_t lda, const vo
           ? launch_linear<0, 2>(a3, 3 * k, wp, w_scale, c, ldc, (int)m, (int)n, (int)(3 * k), (int)k, st)
           : launch_linear<1, 2>(a3, 3 * k, wp, w_scale, c, ldc, (int)m, (int)n, (int)(3 * k), (int)k, st);
   return kq_check_launch(e, "kq_mx_linear_f32");
+}
+
+static int check_linear_mx(const char* fn, int a_fmt, int w_fmt, int64_t lda, int64_t m, int64_t n, int64_t k,
+                           int out_dtype, int64_t ldc) {
+  if (a_fmt != KQ_FMT_MXFP8_E4M3 || w_fmt != KQ_FMT_MXFP8_E4M3)
+    return kq_fail(KQ_ERR_INVALID, "%s: only MXFP8 (E4M3) x MXFP8 (E4M3) operands (a_fmt=%d, w_fmt=%d)", fn, a_fmt,
+                   w_fmt);
+  if (out_dtype != KQ_DT_BF16 && out_dtype != KQ_DT_F32)
+    return kq_fail(KQ_ERR_INVALID, "%s: output dtype must be bf16 or f32", fn);
+  if (m < 0 || n < 0 || k <= 0 || k % 128 != 0 || lda < k || lda % 16 != 0 || ldc < n)
+    return kq_fail(KQ_ERR_INVALID,
+                   "%s: need k %% 128 == 0, lda >= k, lda %% 16 == 0, ldc >= n "
+                   "(m=%lld n=%lld k=%lld lda=%lld ldc=%lld)",
+                   fn, (long long)m, (long long)n, (long long)k, (long long)lda, (long long)ldc);
+  if (m > INT32_MAX / 2 || n > INT32_MAX / 2 || k > INT32_MAX / 2 || (uint64_t)k * lin::BN > dma::MAX_RANGE ||
+      (uint64_t)lda * lin::BM > dma::MAX_RANGE)
+    return kq_fail(KQ_ERR_LIMIT, "%s: dimension too large", fn);
+  return KQ_OK;
+}
+
+extern "C" int kq_mx_linear_mx(int a_fmt, const void* a_q, const uint8_t* a_scale, int64_t lda, int w_fmt,
+                               const void* w_q, const uint8_t* w_scale, int64_t m, int64_t n, int64_t k,
+                               int out_dtype, void* c, int64_t ldc, void* stream) {
+  const char* fn = "kq_mx_linear_mx";
+  if (int rc = check_linear_mx(fn, a_fmt, w_fmt, lda, m, n, k, out_dtype, ldc)) return rc;
+  if (m == 0 || n == 0) return KQ_OK;
+  if (!a_q || !a_scale || !w_q || !w_scale || !c) return kq_fail(KQ_ERR_INVALID, "%s: null buffer", fn);
+  if (kq_misaligned(a_q, 16) || kq_misaligned(w_q, 16) || kq_misaligned(a_scale, 4) || kq_misaligned(w_scale, 4))
+    return kq_fail(KQ_ERR_INVALID, "%s: a_q and w_q must be 16-byte aligned, the scales 4-byte aligned", fn);
+  hipStream_t st = (hipStream_t)stream;
+  const uint8_t* ap = (const uint8_t*)a_q;
+  const uint8_t* wp = (const uint8_t*)w_q;
+  const hipError_t e =
+      out_dtype == KQ_DT_BF16
+          ? launch_linear_a8<0>(ap, a_scale, lda, wp, w_scale, c, ldc, (int)m, (int)n, (int)k, st)
+          : launch_linear_a8<2>(ap, a_scale, lda, wp, w_scale, c, ldc, (int)m, (int)n, (int)k, st);
+  return kq_check_launch(e, fn);
+}
+
+// Input rows quantized into the workspace: E4M3 [m, k] at 0, E8M0 [m, k / 32]
+// at the next 256-byte boundary.
+static int64_t mm_scale_offset(int64_t m, int64_t k) { return (m * k + 255) / 256 * 256; }
+
+extern "C" int64_t kq_mx_linear_mm_workspace_size(int64_t m, int64_t k) {
+  if (m < 0 || k <= 0) return -1;
+  return mm_scale_offset(m, k) + m * (k / 32);
+}
+
+extern "C" int kq_mx_linear_mm(int w_fmt, const void* a, int a_dtype, int64_t lda, const void* w_q,
+                               const uint8_t* w_scale, int64_t m, int64_t n, int64_t k, int out_dtype, void* c,
+                               int64_t ldc, void* workspace, int64_t workspace_bytes, void* stream) {
+  const char* fn = "kq_mx_linear_mm";
+  if (a_dtype != KQ_DT_BF16 && a_dtype != KQ_DT_F16 && a_dtype != KQ_DT_F32)
+    return kq_fail(KQ_ERR_INVALID, "%s: input dtype must be bf16, f16 or f32", fn);
+  if (lda < k) return kq_fail(KQ_ERR_INVALID, "%s: lda < k", fn);
+  if (int rc = check_linear_mx(fn, KQ_FMT_MXFP8_E4M3, w_fmt, k, m, n, k, out_dtype, ldc)) return rc;
+  if (m == 0 || n == 0) return KQ_OK;
+  if (!workspace || workspace_bytes < kq_mx_linear_mm_workspace_size(m, k) || kq_misaligned(workspace, 256))
+    return kq_fail(KQ_ERR_INVALID, "%s: workspace needs %lld bytes (256-byte aligned)", fn,
+                   (long long)kq_mx_linear_mm_workspace_size(m, k));
+  uint8_t* xq = static_cast<uint8_t*>(workspace);
+  uint8_t* xs = xq + mm_scale_offset(m, k);
+  if (int rc = kq_mx_quantize(KQ_FMT_MXFP8_E4M3, a_dtype, a, lda, m, k, xq, xs, 0, stream)) return rc;
+  return kq_mx_linear_mx(KQ_FMT_MXFP8_E4M3, xq, xs, k, w_fmt, w_q, w_scale, m, n, k, out_dtype, c, ldc, stream);
 }

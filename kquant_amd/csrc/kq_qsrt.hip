@@ -1369,6 +1369,8 @@ extern "C" int kq_qsrt_moe_decode(int act, float beta, float linear_beta, const 
   if (tokens == 0) return KQ_OK;
   if (!x || !route_ids || !route_weights || !mats || !labels || !out)
     return kq_fail(KQ_ERR_INVALID, "%s: null buffer", fn);
+  if (kq_misaligned(labels, 16))  // staged into LDS by 16-byte direct loads
+    return kq_fail(KQ_ERR_INVALID, "%s: labels must be 16-byte aligned", fn);
   MoePlan p;
   hipError_t err = moe_plan(tokens, topk, hidden_tiles, inter_tiles, &p);
   if (err != hipSuccess) return kq_check_launch(err, fn);

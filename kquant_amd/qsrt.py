@@ -204,8 +204,13 @@ def qsrt_linear_launcher(
 ):
     """A zero-argument callable that writes ``x @ W`` into ``out`` with fixed
     device buffers (x [m, K] and out [m, N] on the payload's GPU, row-major):
-    every check, table and workspace is settled once, so the call is one
-    launch and may be captured in a HIP graph."""
+    every check, table and workspace is settled once, so the call allocates
+    nothing and may be captured in a HIP graph.  Up to ``FUSED_MAX_ROWS`` rows
+    a call is one launch (the fused kernel).  From ``FUSED_MAX_ROWS + 1`` rows
+    it is the prefill form, four launches (five for fp32 / fp16 rows): the row
+    rotation, the weight decode to E4M3 label bytes, the three-term split of
+    fp32 rows, the MXFP8 MFMA product and the output rotation -- the weight is
+    decoded again on every call."""
 
     if rate_axis not in ("k", "n"):
         raise ValueError("rate_axis must be 'k' or 'n'")
@@ -306,7 +311,16 @@ def qsrt_linear(
     if need < 0:
         raise RuntimeError("kq_qsrt_linear_workspace_size: no HIP device")
     stream = N.stream(gpu)
-    ws = _workspace(_LINEAR_WORKSPACES, (gpu, stream.value, m, k_tiles, n_tiles), need, gpu) if need else None
+    if not need:
+        ws = None
+    elif m <= FUSED_MAX_ROWS:
+        # the fused kernel's completion counters: zeroed once, back at zero after every call
+        ws = _workspace(_LINEAR_WORKSPACES, (gpu, stream.value, m, k_tiles, n_tiles), need, gpu)
+    else:
+        # the prefill form keeps no state between calls: a buffer from torch's
+        # caching allocator, released with this call, so prompts of many
+        # lengths do not each pin a workspace of their own
+        ws = torch.empty(need, dtype=torch.uint8, device=gpu)
     N.call("kq_qsrt_linear", N.ptr(rows), N.DTYPE_CODES[rows.dtype], m, rows.stride(0) if m else k, N.ptr(g),
            g.numel(), k_tiles, n_tiles, 0 if rate_axis == "k" else 1, bits, N.ptr(labels), N.ptr(su), N.ptr(sv),
            N.DTYPE_CODES[out_dtype], N.ptr(out), n, N.ptr(ws) if need else None, need, stream)

@@ -83,7 +83,10 @@ def test_damped_hessian(gpu):
 
 
 def test_cfg4_full_size_sampled_entries(gpu):
-    """65,536 Student-t(4) bf16 rows at K = 7,168 (benchmark configuration)."""
+    """65,536 Student-t(4) bf16 rows at K = 7,168 with the 0.01 * mean(diag)
+    damping of benchmark configuration 4 (i), against exact float64 values:
+    sampled entries of X^T X / n plus the damping on the diagonal ones, and
+    the trace (1.01 times the exact undamped trace)."""
     n, k = 65536, 7168
     g = torch.Generator(device=gpu).manual_seed(0)
     z0 = torch.randn(n, k, generator=g, device=gpu)
@@ -92,9 +95,13 @@ def test_cfg4_full_size_sampled_entries(gpu):
         chi += torch.randn(n, k, generator=g, device=gpu).square()
     x = (z0 / torch.sqrt(chi / 4.0)).to(torch.bfloat16)
     del z0, chi
-    h, denom = ch.damped_hessian(x, damp=0.0)
+    damp = 0.01
+    h, denom = ch.damped_hessian(x, damp=damp)
     torch.cuda.synchronize()
+    assert denom == n
     assert torch.equal(h, h.T)
+    trace_exact = float(x.float().square().sum(dtype=torch.float64)) / n
+    shift = damp * trace_exact / k  # damp * mean(diag) of the exact undamped H
     # checker: exact float64 dot products of sampled entries (torch on the GPU)
     rng = np.random.default_rng(0)
     i = torch.from_numpy(rng.integers(0, k, 4096)).to(gpu)
@@ -103,12 +110,16 @@ def test_cfg4_full_size_sampled_entries(gpu):
     exact = torch.zeros(4096, dtype=torch.float64, device=gpu)
     for c in range(0, 4096, 512):
         exact[c:c + 512] = (x[:, i[c:c + 512]].double() * x[:, j[c:c + 512]].double()).sum(0) / n
+    exact += (i == j).double() * shift
     got = h[i, j].double()
     rel = float(torch.linalg.vector_norm(got - exact) / torch.linalg.vector_norm(exact))
-    print(f"cfg4 sampled-entry relative error {rel:.3e}", flush=True)
+    print(f"cfg4 damped sampled-entry relative error {rel:.3e}", flush=True)
     assert rel <= TOL
-    trace_exact = float(x.float().square().sum(dtype=torch.float64)) / n
-    assert abs(float(torch.trace(h.double())) - trace_exact) / trace_exact <= 1e-6
+    diag = (i == j).nonzero().flatten()
+    rel_diag = float(torch.linalg.vector_norm(got[diag] - exact[diag]) / torch.linalg.vector_norm(exact[diag]))
+    assert rel_diag <= TOL
+    trace_damped = trace_exact * (1.0 + damp)
+    assert abs(float(torch.trace(h.double())) - trace_damped) / trace_damped <= 1e-6
 
 
 def test_cfg4_expert_bench_workload_sampled_entries(gpu):

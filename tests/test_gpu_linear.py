@@ -128,3 +128,99 @@ def test_linear_rejects_bad_shapes(gpu):
     s = torch.zeros(8, 3, dtype=torch.uint8, device=gpu)
     with pytest.raises(ValueError, match="multiple of 64"):
         linear.mxfp8_linear(x, q, s)
+
+
+# ------------------------------------------------- MXFP8 x MXFP8 (A8W8) --
+# Oracle: scripts/closure_mxfp8_mlp.py:146-160 (_reference_from_packed): the
+# input rows quantized with the kernel's quantizer (here the oracle's own
+# restatement of the MXFP8 rule, itself pinned bit-exact elsewhere), both
+# operands dequantized, the product in float64.  The block-scaled fp8 matrix
+# cores do not sum a step's 64 products exactly in fp32 (an in-bounds probe of
+# one instruction measured ~1e-5 relative), so the bars are the GEMM bar of the
+# spec, max |C - R| / max |R| <= 2e-3, a normwise bar ten times the measured
+# error, and for bf16 output the closure's comparison after rounding the oracle
+# (scripts/closure_mxfp8_mlp.py:184-186) within one bf16 ulp, with the share of
+# bitwise-equal elements printed.
+A8_NORM_TOL = 1e-4
+
+
+def _a8_oracle(x: torch.Tensor, wq: torch.Tensor, ws: torch.Tensor) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    bits = x.contiguous().view(torch.int16).numpy().view(np.uint16)
+    xq, xs = oracle.mx_quantize("mxfp8", bits, "bf16")
+    xd = oracle.mx_dequant("mxfp8", xq, xs).astype(np.float64)
+    wd = oracle.mx_dequant("mxfp8", wq.view(torch.uint8).cpu().numpy(), ws.cpu().numpy()).astype(np.float64)
+    return xd @ wd.T, xq, xs
+
+
+def _rel_l2(ref: np.ndarray, got: np.ndarray) -> float:
+    return float(np.linalg.norm(got.astype(np.float64) - ref) / np.linalg.norm(ref))
+
+
+def check_a8_bf16_output(ref: np.ndarray, got: np.ndarray) -> float:
+    r16 = oracle.round_bf16(ref.astype(np.float32)).astype(np.float64)
+    slack = A8_NORM_TOL * np.abs(ref).max()
+    assert np.all(np.abs(got - r16) <= np.abs(r16) * 2.0 ** -7 + slack), "an element is more than one bf16 ulp off"
+    assert np.all(np.abs(got - ref) <= np.abs(ref) * 2.0 ** -8 + slack)
+    return float(np.mean(got == r16))
+
+
+@pytest.mark.parametrize("m,n,k", [(256, 256, 1024), (300, 257, 384), (1, 100, 128), (17, 512, 2048),
+                                   (513, 1000, 640), (4200, 520, 256)])
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+def test_linear_a8_matches_operand_exact_oracle(gpu, m, n, k, out_dtype):
+    print(f"case linear a8 m={m} n={n} k={k} {out_dtype}", flush=True)
+    g = torch.Generator().manual_seed(m * 11 + n + k)
+    w = (torch.randn(n, k, generator=g) * 0.015).to(torch.bfloat16).to(gpu)
+    x = (torch.randn(m, k, generator=g) * torch.exp(0.5 * torch.randn(k, generator=g))).to(torch.bfloat16)
+    q, s = mxfp8.mxfp8_quantize(w)
+    ref, xq, xs = _a8_oracle(x, q, s)
+    c = linear.mxfp8_linear_mm(x.to(gpu), q, s, out_dtype=out_dtype).float().cpu().numpy()
+    # the same product from the oracle's quantized rows: the kernel's input quantizer is the oracle's rule
+    c2 = linear.mxfp8_linear_mx(torch.from_numpy(xq).to(gpu), torch.from_numpy(xs).to(gpu), q, s,
+                                out_dtype=out_dtype).float().cpu().numpy()
+    assert np.array_equal(c, c2)
+    rel, l2 = _max_rel(ref, c), _rel_l2(ref, c)
+    if out_dtype == torch.float32:
+        print(f"  fp32 out: max-rel {rel:.2e} rel-L2 {l2:.2e}", flush=True)
+        assert rel <= TOL and l2 <= A8_NORM_TOL
+    else:
+        eq = check_a8_bf16_output(ref, c)
+        print(f"  bf16 out: max-rel {rel:.2e} bitwise-equal {eq:.4f}", flush=True)
+
+
+def test_linear_a8_cfg2_full_size(gpu):
+    """Benchmark configuration 2 in the production operand form: X [4096,
+    7168] bf16 quantized per row to MXFP8, times the MXFP8 W [12288, 7168].
+    The oracle runs on 192 rows: the first and last row of each of the 16
+    row tiles plus 160 sampled ones, against every column (all 48 column
+    tiles)."""
+    w = workloads.cfg2_weight().to(gpu)
+    x = workloads.cfg2_activations()
+    q, s = mxfp8.mxfp8_quantize(w)
+    c = linear.mxfp8_linear_mm(x.to(gpu), q, s)
+    c32 = linear.mxfp8_linear_mm(x.to(gpu), q, s, out_dtype=torch.float32)
+    again = linear.mxfp8_linear_mm(x.to(gpu), q, s)
+    assert torch.equal(c, again)
+    edges = np.concatenate([np.arange(0, 4096, 256), np.arange(255, 4096, 256)])
+    rest = np.setdiff1d(np.arange(4096), edges)
+    rows = np.sort(np.concatenate([edges, np.random.default_rng(0).choice(rest, 160, replace=False)]))
+    ref, _, _ = _a8_oracle(x[rows], q, s)
+    sel = torch.from_numpy(rows).to(gpu)
+    eq = check_a8_bf16_output(ref, c[sel].float().cpu().numpy())
+    got32 = c32[sel].cpu().numpy()
+    rel, l2 = _max_rel(ref, got32), _rel_l2(ref, got32)
+    print(f"cfg2 a8: fp32-output max-rel {rel:.2e} rel-L2 {l2:.2e}; bf16 bitwise-equal {eq:.4f}", flush=True)
+    assert rel <= TOL and l2 <= A8_NORM_TOL
+
+
+def test_linear_a8_pads_k(gpu):
+    """K = 96 (not a multiple of 128): source and weight are zero-padded to
+    128, which adds nothing."""
+    m, n, k = 33, 70, 96
+    g = torch.Generator().manual_seed(96)
+    w = (torch.randn(n, k, generator=g) * 0.02).to(torch.bfloat16).to(gpu)
+    x = torch.randn(m, k, generator=g).to(torch.bfloat16)
+    q, s = mxfp8.mxfp8_quantize(w)
+    ref, _, _ = _a8_oracle(x, q, s)
+    c = linear.mxfp8_linear_mm(x.to(gpu), q, s, out_dtype=torch.float32).cpu().numpy()
+    assert _max_rel(ref, c) <= TOL and _rel_l2(ref, c) <= A8_NORM_TOL

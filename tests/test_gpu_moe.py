@@ -95,15 +95,17 @@ def test_no_valid_pair_gives_zeros(gpu, out_dtype):
     assert out.dtype == out_dtype and torch.count_nonzero(out) == 0
 
 
+@pytest.mark.parametrize("inter", [512, 1024, 2048, 4096])
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
-def test_per_pair_decode_matches_listed_path_bitwise(gpu, out_dtype):
+def test_per_pair_decode_matches_listed_path_bitwise(gpu, out_dtype, inter):
     """At most 8 pairs the forward skips the routing launch (one gate/up
     workgroup per pair) and fuses the down projection with the combine.  Its
     output is bitwise that of the routed-list path (which the X4T-scale
     forward still takes, on the same scale bytes), here with an expert
     repeated across tokens, invalid ids, a token with no valid expert, and
-    every supported intermediate width's step count (I = 512)."""
-    T, k, E, H, I = 4, 2, 4, 512, 512
+    each intermediate width that selects its own instantiation of the fused
+    down kernel (2 / 4 / 8 / 16 K steps)."""
+    T, k, E, H, I = 4, 2, 4, 512, inter
     ids = torch.tensor([[1, 3], [3, -1], [0, 99], [-2, -1]], dtype=torch.int32)
     w = torch.rand(T, k, generator=torch.Generator().manual_seed(8))
     x = torch.randn(T, H, generator=torch.Generator().manual_seed(9)).to(torch.bfloat16)
@@ -127,12 +129,11 @@ def test_decode_real_shapes(gpu, tokens):
     """Configuration 5: hidden 7168, intermediate 2048, 384 experts, top-8."""
     ids, w = workloads.random_routing(tokens, seed=tokens)
     x = torch.randn(tokens, 7168, generator=torch.Generator().manual_seed(5)).to(torch.bfloat16)
-    check = np.arange(min(tokens, 4))
-    weights = workloads.quantized_experts(ids[: len(check)].flatten().tolist() + ids.flatten().tolist(),
-                                          device=gpu)
+    check = np.arange(tokens)  # every token: at 16 tokens every routed expert's GEMV entries
+    weights = workloads.quantized_experts(ids.flatten().tolist(), device=gpu)
     out = moe.grouped_expert_forward(x.to(gpu), ids.to(gpu), w.to(gpu), *weights)
-    ref = _oracle(x, ids, w, weights, "situ", tokens=check)
-    rel = _max_rel(ref, out[torch.from_numpy(check)].cpu().numpy())
+    ref = _cfg3_oracle(x, ids, w, weights, check, "bf16")
+    rel = _max_rel(ref, out.cpu().numpy())
     print(f"moe decode T={tokens} max-rel {rel:.2e}", flush=True)
     assert rel <= TOL
 
@@ -251,21 +252,24 @@ def _oracle_mx(x, ids, w, weights, fmt, tokens=None):
 
 
 # ------------------------------------------------ configuration 3 at bench size --
-def cfg3_check_tokens(ids: torch.Tensor, hot: int = 20) -> np.ndarray:
-    """Tokens of the configuration-3 routing that cover, for each of the
-    ``hot`` most-routed experts, the first and last pair of its first and of
-    its last 256-row tile of the grouped GEMM (pairs sit in an expert's rows
-    in token order), plus one token of every expert on the GEMV path (1..16
-    pairs) and every token with more than one GEMV-path slot.  (No token of
-    this routing is routed only to GEMV-path experts.)"""
+def cfg3_check_tokens(ids: torch.Tensor, tile: int = 128) -> np.ndarray:
+    """Tokens of the configuration-3 routing that cover the first and the
+    last pair of every ``tile``-row tile of every expert on the grouped-GEMM
+    path (more than 16 pairs; pairs sit in an expert's rows in token order):
+    128-row tiles are the W4A16 grouped GEMM's, and their boundaries include
+    those of the 256-row tiles of the activation-quantized kernels.  Plus one
+    token of every expert on the GEMV path (1..16 pairs) and every token with
+    more than one GEMV-path slot.  (No token of this routing is routed only
+    to GEMV-path experts.)"""
     flat = ids.flatten().long()
     counts = torch.bincount(flat, minlength=384)
     sel = set()
-    for e in torch.argsort(counts, descending=True)[:hot].tolist():
+    for e in torch.nonzero(counts > 16).flatten().tolist():
         pos = torch.nonzero(flat == e).flatten()
-        last = (pos.numel() - 1) // 256 * 256
-        for p in (pos[0], pos[min(255, pos.numel() - 1)], pos[last], pos[-1]):
-            sel.add(int(p) // ids.shape[1])
+        for first in range(0, pos.numel(), tile):
+            last = min(first + tile, pos.numel()) - 1
+            sel.add(int(pos[first]) // ids.shape[1])
+            sel.add(int(pos[last]) // ids.shape[1])
     gemv = (counts >= 1) & (counts <= 16)
     for e in torch.nonzero(gemv).flatten().tolist():
         sel.add(int(torch.nonzero((ids == e).any(1)).flatten()[0]))
@@ -305,11 +309,15 @@ def _cfg3_oracle(x, ids, w, weights, check, fmt):
 def test_cfg3_bench_size_covers_every_tile_kind(gpu, cfg3, fmt):
     """Configuration 3 at bench size (8192 tokens, Zipf(1.1) top-8 over 384
     experts, 205 active) in the W4A16, W4A8 and W4A4 modes: the output rows
-    of cfg3_check_tokens (first / last row tile of the 20 hottest experts,
-    every GEMV-path expert) against the oracle, and two runs bitwise equal."""
+    of cfg3_check_tokens (first and last row of every 128-row tile of every
+    grouped-GEMM expert, every GEMV-path expert) against the oracle, and two
+    runs bitwise equal."""
     ids, w, x, weights, prep = cfg3
     check = cfg3_check_tokens(ids)
-    assert len(check) >= 150
+    assert len(check) >= 1000
+    counts = torch.bincount(ids.flatten().long(), minlength=384)
+    # some expert's last 128-row tile ends inside its second 64-row wave half
+    assert bool(((counts > 16) & (counts % 128 > 64)).any())
     out = moe.grouped_expert_forward(x.to(gpu), ids.to(gpu), w.to(gpu), prep, activation_format=fmt)
     again = moe.grouped_expert_forward(x.to(gpu), ids.to(gpu), w.to(gpu), prep, activation_format=fmt)
     assert torch.equal(out, again)

@@ -36,7 +36,8 @@ def test_python_binding_covers_every_entry_point():
                                         "kq_cholesky_workspace_size", "kq_block_ldl_workspace_size",
                                         "kq_sqg_quantize_workspace_size", "kq_qsrt_linear_workspace_size",
                                         "kq_qsrt_moe_workspace_size",
-                                        "kq_route_sort_workspace_size", "kq_syrk_accumulate_workspace_size"}
+                                        "kq_route_sort_workspace_size", "kq_syrk_accumulate_workspace_size",
+                                        "kq_mx_linear_mm_workspace_size"}
     assert set(declared_symbols()) <= bound
 
 
@@ -46,6 +47,31 @@ def test_argument_errors_need_no_gpu():
     assert rc == _native.KQ_ERR_INVALID
     assert b"k % 32" in lib.kq_last_error()
     assert lib.kq_moe_workspace_size(8, 8, 384, 7168, 2048) > 8 * 8 * 7168 * 4
+
+
+def test_linear_a8_argument_errors_need_no_gpu():
+    lib = _native.library()
+    fake = ctypes.c_void_p(256)  # never dereferenced: validation fails first
+    e4m3, e2m1 = _native.FMT_MXFP8_E4M3, _native.FMT_MXFP4_E2M1
+    args = [e4m3, fake, fake, 256, e4m3, fake, fake, 8, 8, 256, _native.DT_BF16, fake, 8, None]
+    bad = list(args)
+    bad[4] = e2m1
+    assert lib.kq_mx_linear_mx(*bad) == _native.KQ_ERR_INVALID and b"only MXFP8" in lib.kq_last_error()
+    bad = list(args)
+    bad[9] = 192  # k % 128 != 0
+    assert lib.kq_mx_linear_mx(*bad) == _native.KQ_ERR_INVALID and b"k % 128" in lib.kq_last_error()
+    bad = list(args)
+    bad[3] = 264  # lda % 16 != 0
+    assert lib.kq_mx_linear_mx(*bad) == _native.KQ_ERR_INVALID and b"lda % 16" in lib.kq_last_error()
+    bad = list(args)
+    bad[1] = ctypes.c_void_p(264)
+    assert lib.kq_mx_linear_mx(*bad) == _native.KQ_ERR_INVALID and b"16-byte aligned" in lib.kq_last_error()
+    assert lib.kq_mx_linear_mm_workspace_size(4096, 7168) >= 4096 * 7168 + 4096 * 224
+    mm = [e4m3, fake, _native.DT_BF16, 256, fake, fake, 8, 8, 256, _native.DT_BF16, fake, 8, fake, 16, None]
+    assert lib.kq_mx_linear_mm(*mm) == _native.KQ_ERR_INVALID and b"workspace needs" in lib.kq_last_error()
+    bad = list(mm)
+    bad[2] = 9
+    assert lib.kq_mx_linear_mm(*bad) == _native.KQ_ERR_INVALID and b"input dtype" in lib.kq_last_error()
 
 
 def test_x4t_moe_argument_errors_need_no_gpu():
@@ -138,3 +164,6 @@ def test_qsrt_moe_argument_errors_need_no_gpu():
     bad = list(args)
     bad[19] = 100
     assert lib.kq_qsrt_moe_decode(*bad) == _native.KQ_ERR_INVALID and b"ldo" in lib.kq_last_error()
+    bad = list(args)
+    bad[16] = ctypes.c_void_p(260)  # the label table is staged by 16-byte direct loads
+    assert lib.kq_qsrt_moe_decode(*bad) == _native.KQ_ERR_INVALID and b"labels must be 16-byte" in lib.kq_last_error()
