@@ -289,6 +289,19 @@ def summarize_stats(dirs: list[str]) -> int:
     print("| kernel | calls | average (us) | total (us) | % |\n|---|---:|---:|---:|---:|")
     for name, calls, total, avg, pct in sorted(rows, key=lambda r: -r[2]):
         print(f"| `{_short_kernel(name)}` | {calls} | {avg:.3f} | {total:.1f} | {pct:.2f} |")
+    # the same kernel launched over different grids (e.g. one matrix and a
+    # stack of them) is averaged together above; here per grid
+    per: dict[tuple[str, int], list[float]] = {}
+    for d in dirs:
+        for db in sorted(Path(d).rglob("*.db")):
+            con = sqlite3.connect(str(db))
+            for name, gx, gy, gz, dur in con.execute("select name, grid_x, grid_y, grid_z, duration from kernels"):
+                per.setdefault((_short_kernel(name), int(gx) * int(gy) * int(gz)), []).append(float(dur) / 1e3)
+    print("\n| kernel | grid (threads) | calls | average (us) | median (us) | min (us) |\n|---|---:|---:|---:|---:|---:|")
+    for (name, grid), durs in sorted(per.items(), key=lambda kv: -sum(kv[1])):
+        short = name if len(name) <= 100 else name[:97] + "..."
+        print(f"| `{short}` | {grid} | {len(durs)} | {statistics.fmean(durs):.3f} | "
+              f"{statistics.median(durs):.3f} | {min(durs):.3f} |")
     return 0
 
 
@@ -489,10 +502,13 @@ def main() -> int:
         xs = torch.empty(m2, cols // 32, dtype=torch.uint8, device=dev)
         N.call("kq_mx_quantize", N.FMT_MXFP8_E4M3, N.DT_BF16, N.ptr(x2), cols, m2, cols, N.ptr(xq), N.ptr(xs), 0,
                stream)
-        mm_ws_bytes = int(N.library().kq_mx_linear_mm_workspace_size(m2, cols))
+        mm_ws_bytes = int(N.library().kq_mx_linear_mm_workspace_size(m2, rows, cols))
         mm_ws = torch.empty(mm_ws_bytes, dtype=torch.uint8, device=dev)
+        mx_ws_bytes = int(N.library().kq_mx_linear_mx_workspace_size(m2, rows, cols))
+        mx_ws = torch.empty(mx_ws_bytes, dtype=torch.uint8, device=dev)
         a8_step = _bound(N, "kq_mx_linear_mx", N.FMT_MXFP8_E4M3, N.ptr(xq), N.ptr(xs), cols, N.FMT_MXFP8_E4M3,
-                         N.ptr(q8), N.ptr(s8), m2, rows, cols, N.DT_BF16, N.ptr(out2), rows, stream)
+                         N.ptr(q8), N.ptr(s8), m2, rows, cols, N.DT_BF16, N.ptr(out2), rows, N.ptr(mx_ws),
+                         mx_ws_bytes, stream)
         mm_step = _bound(N, "kq_mx_linear_mm", N.FMT_MXFP8_E4M3, N.ptr(x2), N.DT_BF16, cols, N.ptr(q8), N.ptr(s8),
                          m2, rows, cols, N.DT_BF16, N.ptr(out2), rows, N.ptr(mm_ws), mm_ws_bytes, stream)
         t_a8 = _time_loop(torch, a8_step, max(5, args.steps // 5), 3, 0.3)
@@ -509,7 +525,7 @@ def main() -> int:
             "roofline": _roofline("mfma", flops / t_a8 / 1e12, a8_pmc, FP8_PEAK_TFLOPS),
             "pmc": a8_pmc,
         }
-        del x2, out2, xq, xs, mm_ws
+        del x2, out2, xq, xs, mm_ws, mx_ws
 
     # ------------------------------------------ config 3 MoE prefill GEMM --
     moe_result = None

@@ -233,15 +233,20 @@ int kq_mx_linear(int w_fmt, const void* a, int64_t lda, const void* w_q,
  * 146-160 _reference_from_packed: quantize the input, dequantize both
  * operands, fp32 product; :163-187 _production_linear).  a_fmt and w_fmt
  * must be KQ_FMT_MXFP8_E4M3; k % 128 == 0; a_q, w_q 16-byte aligned,
- * scales 4-byte aligned.  The matrix cores sum the 64 products of a step
- * with a few fp32 ulps of error (measured ~1e-5 relative). */
+ * scales 4-byte aligned.  workspace (kq_mx_linear_mx_workspace_size bytes,
+ * 256-byte aligned, uninitialised) takes both scale planes transposed to
+ * [k/128][rows] dwords, the layout the kernel loads a 128-k stage's scales
+ * from.  The matrix cores sum the 64 products of a step with a few fp32 ulps
+ * of error (measured ~1e-5 relative). */
+int64_t kq_mx_linear_mx_workspace_size(int64_t m, int64_t n, int64_t k);
 int kq_mx_linear_mx(int a_fmt, const void* a_q, const uint8_t* a_scale, int64_t lda, int w_fmt,
                     const void* w_q, const uint8_t* w_scale, int64_t m, int64_t n, int64_t k,
-                    int out_dtype, void* c, int64_t ldc, void* stream);
+                    int out_dtype, void* c, int64_t ldc, void* workspace, int64_t workspace_bytes,
+                    void* stream);
 
-/* Workspace bytes of kq_mx_linear_mm (the quantized input rows), -1 on bad
- * sizes. */
-int64_t kq_mx_linear_mm_workspace_size(int64_t m, int64_t k);
+/* Workspace bytes of kq_mx_linear_mm (the quantized input rows and
+ * kq_mx_linear_mx's workspace), -1 on bad sizes. */
+int64_t kq_mx_linear_mm_workspace_size(int64_t m, int64_t n, int64_t k);
 
 /* mxfp8_linear.mm of kquant's production MXFP8 linear
  * (scripts/closure_mxfp8_mlp.py:172-177): the input rows A [m, k] (bf16, f16

@@ -63,7 +63,7 @@ SIGNATURES: dict[str, list] = {
     "kq_sym_lerp": [_VP, _F32, _VP, _I64, _F32, _VP, _VP],
     "kq_cov_stats": [_VP, _I64, _VP, _VP, _VP],
     "kq_mx_linear": [_INT, _VP, _I64, _VP, _VP, _I64, _I64, _I64, _INT, _VP, _I64, _VP],
-    "kq_mx_linear_mx": [_INT, _VP, _VP, _I64, _INT, _VP, _VP, _I64, _I64, _I64, _INT, _VP, _I64, _VP],
+    "kq_mx_linear_mx": [_INT, _VP, _VP, _I64, _INT, _VP, _VP, _I64, _I64, _I64, _INT, _VP, _I64, _VP, _I64, _VP],
     "kq_mx_linear_mm": [_INT, _VP, _INT, _I64, _VP, _VP, _I64, _I64, _I64, _INT, _VP, _I64, _VP, _I64, _VP],
     "kq_moe_forward": [_INT, _F32, _F32, _VP, _I64, _I64, _I64, _VP, _VP, _INT, _INT, _I64,
                        _VP, _VP, _VP, _VP, _INT, _VP, _VP, _I64, _U32, _VP],
@@ -145,7 +145,9 @@ def library() -> ctypes.CDLL:
         lib.kq_mx_linear_f32_workspace_size.restype = ctypes.c_int64
         lib.kq_mx_linear_f32_workspace_size.argtypes = [_I64, _I64]
         lib.kq_mx_linear_mm_workspace_size.restype = ctypes.c_int64
-        lib.kq_mx_linear_mm_workspace_size.argtypes = [_I64, _I64]
+        lib.kq_mx_linear_mm_workspace_size.argtypes = [_I64, _I64, _I64]
+        lib.kq_mx_linear_mx_workspace_size.restype = ctypes.c_int64
+        lib.kq_mx_linear_mx_workspace_size.argtypes = [_I64, _I64, _I64]
         lib.kq_cholesky_workspace_size.restype = ctypes.c_int64
         lib.kq_cholesky_workspace_size.argtypes = [_I64, _I64]
         lib.kq_block_ldl_workspace_size.restype = ctypes.c_int64

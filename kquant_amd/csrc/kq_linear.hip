@@ -441,36 +441,43 @@ __global__ __launch_bounds__(512, 1) void mx_linear_dma_kernel(
 // v_mfma_scale_f32_32x32x64_f8f6f4 per 32x32 block and 64-k step multiplies
 // the E4M3 bytes with their E8M0 bytes as they are.  Lane (m, g) of a
 // 32x32x64 operand holds row m and byte i at k = 32 (i / 16) + 16 g + i % 16
-// (16-byte chunks g and 2 + g of the row's 64-k step) and gives the scale of
-// its row's block g (checked with an in-bounds one-wave probe).
+// (16-byte chunks g and 2 + g of the row's 64 k) and gives the scale of its
+// row's block g (checked with an in-bounds one-wave probe).
 //  * persistent, tiles of 256 x 256 in mx_linear_dma_kernel's grouped order,
 //    workers of one XCD numbered consecutively; 8 waves of 64 x 128 (2 x 4
 //    blocks) as two ping-pong groups: group 0 issues every direct load and
-//    leads, group 1 runs half a step behind; a step is a memory phase (all
-//    LDS reads of the step into registers) and a compute phase (8 MFMAs).
-//  * 4-stage ring of 64-k steps (three steps in flight): per stage the A and
-//    W tiles, 256 rows x 64 B each, 16-byte chunk c of row r at slot
-//    c ^ ((r / 4) % 4) (the 16 lanes of a 128-bit read hit 16 distinct bank
-//    groups), and one scale dword per row of each (the four blocks of the
-//    row's 128-k window, two of them this step's; needs K % 128 == 0).
+//    leads, group 1 runs half a step behind; a step (64 k) is a memory phase
+//    (all LDS reads of the step into registers) and a compute phase (8
+//    MFMAs).
+//  * two LDS stages of 128 k (double buffered; a stage is two steps): per
+//    stage the A and W tiles, 256 rows x 128 B each, so every direct load
+//    fetches whole 128-byte lines (8 rows x 128 B per instruction), 16-byte
+//    chunk c of row r at slot c ^ ((r / 2) % 8) (the 16 lanes of a 128-bit
+//    read hit 16 distinct bank groups); and the stage's scale dwords of both
+//    operands, read from scale planes transposed to [K / 128][rows] dwords
+//    (the four blocks of a row's 128 k), 1 KiB contiguous per operand.
+//    Fetching half lines, or one 4-byte scale per row, made this kernel's
+//    direct loads issue 2-4x more line requests than bytes need, which
+//    bounded it (measured: 376 us of loads alone at cfg2; 139 us for twice
+//    the bytes in whole lines without per-row scale dwords).
 //  * rows past M or N read as zero (out-of-range offsets) and are not stored.
 namespace lin8 {
-constexpr int NSTAGE = 4, BK = 64;
-constexpr int OP_BYTES = 256 * 64;             // one operand tile per stage
-constexpr int S_OFF = 2 * OP_BYTES;            // A scale dwords, then W's
+constexpr int BK = 64, SK = 128;             // MFMA step, LDS stage
+constexpr int OP_BYTES = 256 * SK;           // one operand tile per stage
+constexpr int S_OFF = 2 * OP_BYTES;          // A scale dwords, then W's
 constexpr int STAGE = 2 * OP_BYTES + 2 * 1024;
-constexpr int LOADS = 4 + 4 + 1 + 1;           // direct loads per loading wave per stage
+constexpr int LOADS = 8 + 8 + 1 + 1;         // direct loads per loading wave per stage
 }  // namespace lin8
 
-__shared__ __attribute__((aligned(16))) unsigned char lin8_lds[lin8::NSTAGE * lin8::STAGE];
+__shared__ __attribute__((aligned(16))) unsigned char lin8_lds[2 * lin8::STAGE];
 
 typedef int i32x8_t __attribute__((ext_vector_type(8)));
 
 template <int OUT>
 __global__ __launch_bounds__(512, 1) void mx_linear_a8_kernel(
-    const uint8_t* __restrict__ aq, int64_t lda, uint32_t a_bytes, const uint8_t* __restrict__ as,
-    uint32_t as_bytes, const uint8_t* __restrict__ wq, uint32_t w_bytes, const uint8_t* __restrict__ ws,
-    uint32_t ws_bytes, void* __restrict__ c, int64_t ldc, int M, int N, int K) {
+    const uint8_t* __restrict__ aq, int64_t lda, uint32_t a_bytes, const uint32_t* __restrict__ ast,
+    uint32_t ast_bytes, const uint8_t* __restrict__ wq, uint32_t w_bytes, const uint32_t* __restrict__ wst,
+    uint32_t wst_bytes, void* __restrict__ c, int64_t ldc, int M, int N, int K, int MS, int NS) {
   using namespace lin8;
   using dma::i32x4_t;
   constexpr int BM = lin::BM, BN = lin::BN;
@@ -482,21 +489,22 @@ __global__ __launch_bounds__(512, 1) void mx_linear_a8_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const bool g0 = wave < 4;
   const int lw = wave & 3;
-  const int64_t ks = K / 32;  // scale bytes per row, both operands
-  const int steps = K / BK;
+  const int stages = K / SK, steps = K / BK;
   const uint32_t lds0 = dma::lds_offset_of(lin8_lds);
   const i32x4_t a_rsrc = dma::make_rsrc(aq, a_bytes), w_rsrc = dma::make_rsrc(wq, w_bytes);
-  const i32x4_t as_rsrc = dma::make_rsrc(as, as_bytes), ws_rsrc = dma::make_rsrc(ws, ws_bytes);
+  const i32x4_t as_rsrc = dma::make_rsrc(ast, ast_bytes), ws_rsrc = dma::make_rsrc(wst, wst_bytes);
 
-  // ---- load side: load q (0..3) of wave lw fills 16-row piece 4q + lw of
-  // both tiles (1 KiB each); lane l fetches row 16 (4q + lw) + l / 4, slot
-  // l % 4, i.e. logical chunk (l % 4) ^ ((l / 16) % 4)
+  // ---- load side: load q (0..7) of wave lw fills the 8-row piece 4q + lw
+  // of both tiles (1 KiB each); lane l fetches row 8 (4q + lw) + l / 8,
+  // slot l % 8, i.e. logical chunk (l % 8) ^ ((row / 2) % 8).  Scale dwords:
+  // lane l of wave lw carries row 64 lw + l of the transposed planes
+  // (MS / NS rows per 128-k chunk).
   int lt = worker, ls = 0;
-  const int prow = 16 * lw + (lane >> 2);            // + 64 q
-  const int pch = (lane & 3) ^ ((lane >> 4) & 3);
+  const int prow = 8 * lw + (lane >> 3);  // + 32 q
+  const int pch = (lane & 7) ^ ((prow >> 1) & 7);
   uint32_t a_base = 0, w_base = 0, as_off = 0, ws_off = 0;
   int a_lim = 0, w_lim = 0;
-  const uint32_t a_qstep = (uint32_t)(64 * lda), w_qstep = (uint32_t)(64 * K);
+  const uint32_t a_qstep = (uint32_t)(32 * lda), w_qstep = (uint32_t)(32 * K);
   auto set_load_tile = [&]() {
     const bool live = lt < total;
     int mt = 0, nt = 0;
@@ -507,59 +515,61 @@ __global__ __launch_bounds__(512, 1) void mx_linear_a8_kernel(
     w_lim = live ? N - n0 - prow : 0;
     w_base = w_lim > 0 ? (uint32_t)((int64_t)(n0 + prow) * K + 16 * pch) : 0u;
     const int srow = 64 * lw + lane;
-    as_off = live && m0 + srow < M ? (uint32_t)((int64_t)(m0 + srow) * ks) : as_bytes;
-    ws_off = live && n0 + srow < N ? (uint32_t)((int64_t)(n0 + srow) * ks) : ws_bytes;
+    as_off = live && m0 + srow < M ? (uint32_t)(m0 + srow) * 4u : ast_bytes;
+    ws_off = live && n0 + srow < N ? (uint32_t)(n0 + srow) * 4u : wst_bytes;
   };
   auto issue = [&](int slot) {
     const uint32_t base = lds0 + (uint32_t)(slot * STAGE);
-    const uint32_t k0 = (uint32_t)(ls * BK);
+    const uint32_t k0 = (uint32_t)(ls * SK);
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-      dma::load_to_lds16(a_rsrc, 64 * q < a_lim ? a_base + q * a_qstep + k0 : a_bytes,
+    for (int q = 0; q < 8; ++q)
+      dma::load_to_lds16(a_rsrc, 32 * q < a_lim ? a_base + q * a_qstep + k0 : a_bytes,
                          base + (uint32_t)((4 * q + lw) * 1024));
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-      dma::load_to_lds16(w_rsrc, 64 * q < w_lim ? w_base + q * w_qstep + k0 : w_bytes,
+    for (int q = 0; q < 8; ++q)
+      dma::load_to_lds16(w_rsrc, 32 * q < w_lim ? w_base + q * w_qstep + k0 : w_bytes,
                          base + (uint32_t)(OP_BYTES + (4 * q + lw) * 1024));
-    const uint32_t sk = (k0 / 32) & ~3u;
-    dma::load_to_lds4(as_rsrc, as_off >= as_bytes ? as_bytes : as_off + sk, base + (uint32_t)(S_OFF + lw * 256));
-    dma::load_to_lds4(ws_rsrc, ws_off >= ws_bytes ? ws_bytes : ws_off + sk,
+    dma::load_to_lds4(as_rsrc, as_off >= ast_bytes ? ast_bytes : as_off + (uint32_t)ls * (uint32_t)MS * 4u,
+                      base + (uint32_t)(S_OFF + lw * 256));
+    dma::load_to_lds4(ws_rsrc, ws_off >= wst_bytes ? wst_bytes : ws_off + (uint32_t)ls * (uint32_t)NS * 4u,
                       base + (uint32_t)(S_OFF + 1024 + lw * 256));
   };
   auto advance = [&]() {
-    if (++ls == steps) {
+    if (++ls == stages) {
       ls = 0;
       lt += G;
       set_load_tile();
     }
   };
 
-  // ---- compute side
+  // ---- compute side: fragment offsets of step half h (k 64 h .. 64 h + 63 of the stage)
   const int wm = (wave >> 1) * 64, wn = (wave & 1) * 128;
   const int fr = lane & 31, fg = lane >> 5;
-  int aoff[2][2], woff[4][2], asb[2], wsb[4];
+  int aoff[2][2][2], woff[2][4][2], asb[2], wsb[4];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int r = wm + 32 * i + fr, sw = (r >> 2) & 3;
-    aoff[i][0] = r * 64 + 16 * (fg ^ sw);
-    aoff[i][1] = r * 64 + 16 * ((2 + fg) ^ sw);
-    asb[i] = S_OFF + 4 * r + fg;
+  for (int h = 0; h < 2; ++h) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int r = wm + 32 * i + fr, sw = (r >> 1) & 7;
+      aoff[h][i][0] = r * SK + 16 * ((4 * h + fg) ^ sw);
+      aoff[h][i][1] = r * SK + 16 * ((4 * h + 2 + fg) ^ sw);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int r = wn + 32 * j + fr, sw = (r >> 1) & 7;
+      woff[h][j][0] = OP_BYTES + r * SK + 16 * ((4 * h + fg) ^ sw);
+      woff[h][j][1] = OP_BYTES + r * SK + 16 * ((4 * h + 2 + fg) ^ sw);
+    }
   }
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int r = wn + 32 * j + fr, sw = (r >> 2) & 3;
-    woff[j][0] = OP_BYTES + r * 64 + 16 * (fg ^ sw);
-    woff[j][1] = OP_BYTES + r * 64 + 16 * ((2 + fg) ^ sw);
-    wsb[j] = S_OFF + 1024 + 4 * r + fg;
-  }
+  for (int i = 0; i < 2; ++i) asb[i] = S_OFF + 4 * (wm + 32 * i + fr) + fg;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) wsb[j] = S_OFF + 1024 + 4 * (wn + 32 * j + fr) + fg;
 
   if (g0) {
     set_load_tile();
-#pragma unroll
-    for (int p = 0; p < NSTAGE - 1; ++p) {
-      issue(p);
-      advance();
-    }
+    issue(0);
+    advance();
   } else {
     __builtin_amdgcn_s_barrier();  // group 1 starts half a step behind
   }
@@ -578,11 +588,19 @@ __global__ __launch_bounds__(512, 1) void mx_linear_a8_kernel(
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
     for (int s = 0; s < steps; ++s) {
-      const int kb = (s * BK / 32) & 3;  // this step's first block in the stage's scale dwords
+      const int h = s & 1;
       if (g0) {
-        dma::wait_and_barrier<2 * LOADS>();  // stage s landed; group 1 is done reading slot s - 1
-        issue(cslot == 0 ? NSTAGE - 1 : cslot - 1);
-        advance();
+        if (h == 0) {
+          // stage s / 2 landed (the only one in flight); both groups are done
+          // reading the other slot, which now takes the next stage
+          dma::wait_and_barrier<0>();
+          issue(cslot ^ 1);
+          advance();
+        } else {
+          asm volatile("" ::: "memory");
+          __builtin_amdgcn_s_barrier();
+          asm volatile("" ::: "memory");
+        }
       } else {
         asm volatile("" ::: "memory");
         __builtin_amdgcn_s_barrier();
@@ -595,15 +613,15 @@ __global__ __launch_bounds__(512, 1) void mx_linear_a8_kernel(
         const unsigned char* st = lin8_lds + cslot * STAGE;
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-          av[i][0] = *reinterpret_cast<const gemm::u32x4_t*>(st + aoff[i][0]);
-          av[i][1] = *reinterpret_cast<const gemm::u32x4_t*>(st + aoff[i][1]);
-          sa[i] = st[asb[i] + kb];
+          av[i][0] = *reinterpret_cast<const gemm::u32x4_t*>(st + (h ? aoff[1][i][0] : aoff[0][i][0]));
+          av[i][1] = *reinterpret_cast<const gemm::u32x4_t*>(st + (h ? aoff[1][i][1] : aoff[0][i][1]));
+          sa[i] = st[asb[i] + 2 * h];
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          wv[j][0] = *reinterpret_cast<const gemm::u32x4_t*>(st + woff[j][0]);
-          wv[j][1] = *reinterpret_cast<const gemm::u32x4_t*>(st + woff[j][1]);
-          sw[j] = st[wsb[j] + kb];
+          wv[j][0] = *reinterpret_cast<const gemm::u32x4_t*>(st + (h ? woff[1][j][0] : woff[0][j][0]));
+          wv[j][1] = *reinterpret_cast<const gemm::u32x4_t*>(st + (h ? woff[1][j][1] : woff[0][j][1]));
+          sw[j] = st[wsb[j] + 2 * h];
         }
       }
       asm volatile("" ::: "memory");
@@ -627,7 +645,7 @@ __global__ __launch_bounds__(512, 1) void mx_linear_a8_kernel(
           }
         }
       }
-      cslot = cslot == NSTAGE - 1 ? 0 : cslot + 1;
+      if (h) cslot ^= 1;
     }
 
     if (active) {
@@ -649,6 +667,27 @@ __global__ __launch_bounds__(512, 1) void mx_linear_a8_kernel(
   }
   if (g0) __builtin_amdgcn_s_barrier();  // matches group 1's first barrier
   __builtin_amdgcn_s_waitcnt(dma::waitcnt_vm(0));  // no load may land after the workgroup ends
+}
+
+// Scale plane [rows, K / 32] bytes -> [K / 128][rows] dwords (the four
+// blocks of each row's 128-k window), the layout mx_linear_a8_kernel loads a
+// stage's scales from.  Dword (r, c) of the input is bytes 4c .. 4c + 3 of row r.
+__global__ __launch_bounds__(256) void scale_dwords_t_kernel(const uint32_t* __restrict__ in, int64_t rows,
+                                                             int64_t chunks, uint32_t* __restrict__ out) {
+  __shared__ uint32_t tile[32][33];
+  const int64_t r0 = (int64_t)blockIdx.x * 32, c0 = (int64_t)blockIdx.y * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t r = r0 + ty + 8 * i, cc = c0 + tx;
+    tile[ty + 8 * i][tx] = r < rows && cc < chunks ? in[r * chunks + cc] : 0u;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t cc = c0 + ty + 8 * i, r = r0 + tx;
+    if (r < rows && cc < chunks) out[cc * rows + r] = tile[tx][ty + 8 * i];
+  }
 }
 
 // Exact three-term bf16 split of fp32 A: a = a0 + a1 + a2 (each step keeps
@@ -721,17 +760,30 @@ static hipError_t launch_linear_dma(const uint16_t* a, int64_t lda, const uint8_
   return hipSuccess;
 }
 
-// MXFP8 x MXFP8 launch: operands larger than one 32-bit buffer range are cut
-// into row chunks of M and N.  Needs K % 128 == 0, lda % 16 == 0, 16-byte
-// aligned E4M3 operands and 4-byte aligned scale rows of K / 32 bytes.
+// MXFP8 x MXFP8 launch: both scale planes are first transposed into the
+// workspace ([K / 128][rows] dwords); operands larger than one 32-bit buffer
+// range are cut into row chunks of M and N, each with its own plane rows.
+// Needs K % 128 == 0, lda % 16 == 0, 16-byte aligned E4M3 operands and
+// 4-byte aligned scale rows of K / 32 bytes.
+static int64_t a8_scale_plane_bytes(int64_t rows, int64_t k) { return (rows * (k / 32) + 255) / 256 * 256; }
+
 template <int OUT>
 static hipError_t launch_linear_a8(const uint8_t* aq, const uint8_t* as, int64_t lda, const uint8_t* wq,
-                                   const uint8_t* ws, void* c, int64_t ldc, int M, int N, int K, hipStream_t st) {
+                                   const uint8_t* ws, void* c, int64_t ldc, int M, int N, int K, void* workspace,
+                                   hipStream_t st) {
   int dev = 0, cus = 0;
   hipError_t e = st ? hipStreamGetDevice(st, &dev) : hipGetDevice(&dev);
   if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
   if (e != hipSuccess) return e;
-  const int64_t ks = K / 32;
+  const int64_t chunks = K / 128;
+  uint32_t* ast = static_cast<uint32_t*>(workspace);
+  uint32_t* wst = reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + a8_scale_plane_bytes(M, K));
+  scale_dwords_t_kernel<<<dim3((unsigned)((M + 31) / 32), (unsigned)((chunks + 31) / 32)), 256, 0, st>>>(
+      reinterpret_cast<const uint32_t*>(as), M, chunks, ast);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  scale_dwords_t_kernel<<<dim3((unsigned)((N + 31) / 32), (unsigned)((chunks + 31) / 32)), 256, 0, st>>>(
+      reinterpret_cast<const uint32_t*>(ws), N, chunks, wst);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
   const int64_t m_chunk = (int64_t)(dma::MAX_RANGE / (uint64_t)lda) / lin::BM * lin::BM;
   const int64_t n_chunk = (int64_t)(dma::MAX_RANGE / (uint64_t)K) / lin::BN * lin::BN;
   for (int64_t m0 = 0; m0 < M; m0 += m_chunk) {
@@ -743,9 +795,12 @@ static hipError_t launch_linear_a8(const uint8_t* aq, const uint8_t* as, int64_t
       if (grid > (tiles + 7) / 8 * 8) grid = (tiles + 7) / 8 * 8;
       void* cp = OUT == 2 ? (void*)(static_cast<float*>(c) + m0 * ldc + n0)
                           : (void*)(static_cast<uint16_t*>(c) + m0 * ldc + n0);
+      // the chunk's rows of each transposed plane start at row m0 / n0 of every
+      // 128-k chunk; its range reaches the last chunk's rows
+      const uint64_t ast_bytes = (uint64_t)((chunks - 1) * M + mc) * 4, wst_bytes = (uint64_t)((chunks - 1) * N + nc) * 4;
       mx_linear_a8_kernel<OUT><<<grid, lin::THREADS, 0, st>>>(
-          aq + m0 * lda, lda, (uint32_t)(mc * lda), as + m0 * ks, (uint32_t)(mc * ks), wq + n0 * K,
-          (uint32_t)(nc * K), ws + n0 * ks, (uint32_t)(nc * ks), cp, ldc, mc, nc, K);
+          aq + m0 * lda, lda, (uint32_t)(mc * lda), ast + m0, (uint32_t)ast_bytes, wq + n0 * K,
+          (uint32_t)(nc * K), wst + n0, (uint32_t)wst_bytes, cp, ldc, mc, nc, K, M, N);
       if ((e = hipGetLastError()) != hipSuccess) return e;
     }
   }
@@ -880,37 +935,47 @@ static int check_linear_mx(const char* fn, int a_fmt, int w_fmt, int64_t lda, in
                    "(m=%lld n=%lld k=%lld lda=%lld ldc=%lld)",
                    fn, (long long)m, (long long)n, (long long)k, (long long)lda, (long long)ldc);
   if (m > INT32_MAX / 2 || n > INT32_MAX / 2 || k > INT32_MAX / 2 || (uint64_t)k * lin::BN > dma::MAX_RANGE ||
-      (uint64_t)lda * lin::BM > dma::MAX_RANGE)
+      (uint64_t)lda * lin::BM > dma::MAX_RANGE || (uint64_t)(m > n ? m : n) * (uint64_t)(k / 32) > dma::MAX_RANGE)
     return kq_fail(KQ_ERR_LIMIT, "%s: dimension too large", fn);
   return KQ_OK;
 }
 
+extern "C" int64_t kq_mx_linear_mx_workspace_size(int64_t m, int64_t n, int64_t k) {
+  if (m < 0 || n < 0 || k <= 0) return -1;
+  return a8_scale_plane_bytes(m, k) + a8_scale_plane_bytes(n, k);
+}
+
 extern "C" int kq_mx_linear_mx(int a_fmt, const void* a_q, const uint8_t* a_scale, int64_t lda, int w_fmt,
                                const void* w_q, const uint8_t* w_scale, int64_t m, int64_t n, int64_t k,
-                               int out_dtype, void* c, int64_t ldc, void* stream) {
+                               int out_dtype, void* c, int64_t ldc, void* workspace, int64_t workspace_bytes,
+                               void* stream) {
   const char* fn = "kq_mx_linear_mx";
   if (int rc = check_linear_mx(fn, a_fmt, w_fmt, lda, m, n, k, out_dtype, ldc)) return rc;
   if (m == 0 || n == 0) return KQ_OK;
   if (!a_q || !a_scale || !w_q || !w_scale || !c) return kq_fail(KQ_ERR_INVALID, "%s: null buffer", fn);
   if (kq_misaligned(a_q, 16) || kq_misaligned(w_q, 16) || kq_misaligned(a_scale, 4) || kq_misaligned(w_scale, 4))
     return kq_fail(KQ_ERR_INVALID, "%s: a_q and w_q must be 16-byte aligned, the scales 4-byte aligned", fn);
+  const int64_t need = kq_mx_linear_mx_workspace_size(m, n, k);
+  if (!workspace || workspace_bytes < need || kq_misaligned(workspace, 256))
+    return kq_fail(KQ_ERR_INVALID, "%s: workspace needs %lld bytes (256-byte aligned)", fn, (long long)need);
   hipStream_t st = (hipStream_t)stream;
   const uint8_t* ap = (const uint8_t*)a_q;
   const uint8_t* wp = (const uint8_t*)w_q;
   const hipError_t e =
       out_dtype == KQ_DT_BF16
-          ? launch_linear_a8<0>(ap, a_scale, lda, wp, w_scale, c, ldc, (int)m, (int)n, (int)k, st)
-          : launch_linear_a8<2>(ap, a_scale, lda, wp, w_scale, c, ldc, (int)m, (int)n, (int)k, st);
+          ? launch_linear_a8<0>(ap, a_scale, lda, wp, w_scale, c, ldc, (int)m, (int)n, (int)k, workspace, st)
+          : launch_linear_a8<2>(ap, a_scale, lda, wp, w_scale, c, ldc, (int)m, (int)n, (int)k, workspace, st);
   return kq_check_launch(e, fn);
 }
 
-// Input rows quantized into the workspace: E4M3 [m, k] at 0, E8M0 [m, k / 32]
-// at the next 256-byte boundary.
+// kq_mx_linear_mm workspace: the input rows quantized, E4M3 [m, k] at 0 and
+// E8M0 [m, k / 32] at the next 256-byte boundary, then kq_mx_linear_mx's.
 static int64_t mm_scale_offset(int64_t m, int64_t k) { return (m * k + 255) / 256 * 256; }
+static int64_t mm_mx_offset(int64_t m, int64_t k) { return mm_scale_offset(m, k) + a8_scale_plane_bytes(m, k); }
 
-extern "C" int64_t kq_mx_linear_mm_workspace_size(int64_t m, int64_t k) {
-  if (m < 0 || k <= 0) return -1;
-  return mm_scale_offset(m, k) + m * (k / 32);
+extern "C" int64_t kq_mx_linear_mm_workspace_size(int64_t m, int64_t n, int64_t k) {
+  if (m < 0 || n < 0 || k <= 0) return -1;
+  return mm_mx_offset(m, k) + kq_mx_linear_mx_workspace_size(m, n, k);
 }
 
 extern "C" int kq_mx_linear_mm(int w_fmt, const void* a, int a_dtype, int64_t lda, const void* w_q,
@@ -922,11 +987,12 @@ extern "C" int kq_mx_linear_mm(int w_fmt, const void* a, int a_dtype, int64_t ld
   if (lda < k) return kq_fail(KQ_ERR_INVALID, "%s: lda < k", fn);
   if (int rc = check_linear_mx(fn, KQ_FMT_MXFP8_E4M3, w_fmt, k, m, n, k, out_dtype, ldc)) return rc;
   if (m == 0 || n == 0) return KQ_OK;
-  if (!workspace || workspace_bytes < kq_mx_linear_mm_workspace_size(m, k) || kq_misaligned(workspace, 256))
-    return kq_fail(KQ_ERR_INVALID, "%s: workspace needs %lld bytes (256-byte aligned)", fn,
-                   (long long)kq_mx_linear_mm_workspace_size(m, k));
+  const int64_t need = kq_mx_linear_mm_workspace_size(m, n, k);
+  if (!workspace || workspace_bytes < need || kq_misaligned(workspace, 256))
+    return kq_fail(KQ_ERR_INVALID, "%s: workspace needs %lld bytes (256-byte aligned)", fn, (long long)need);
   uint8_t* xq = static_cast<uint8_t*>(workspace);
   uint8_t* xs = xq + mm_scale_offset(m, k);
   if (int rc = kq_mx_quantize(KQ_FMT_MXFP8_E4M3, a_dtype, a, lda, m, k, xq, xs, 0, stream)) return rc;
-  return kq_mx_linear_mx(KQ_FMT_MXFP8_E4M3, xq, xs, k, w_fmt, w_q, w_scale, m, n, k, out_dtype, c, ldc, stream);
+  return kq_mx_linear_mx(KQ_FMT_MXFP8_E4M3, xq, xs, k, w_fmt, w_q, w_scale, m, n, k, out_dtype, c, ldc,
+                         xq + mm_mx_offset(m, k), need - mm_mx_offset(m, k), stream);
 }

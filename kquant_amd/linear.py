@@ -144,7 +144,7 @@ def mxfp8_linear_mm(source: torch.Tensor, weight: torch.Tensor, scale: torch.Ten
     a, w, s = N.aligned(a), N.aligned(w), N.aligned(s, 4)
     m, n = a.shape[0], w.shape[0]
     out = torch.empty(m, n, dtype=out_dtype, device=gpu)
-    ws = torch.empty(max(int(N.library().kq_mx_linear_mm_workspace_size(m, kp)), 256), dtype=torch.uint8,
+    ws = torch.empty(max(int(N.library().kq_mx_linear_mm_workspace_size(m, n, kp)), 256), dtype=torch.uint8,
                      device=gpu)
     N.call("kq_mx_linear_mm", N.FMT_MXFP8_E4M3, N.ptr(a), N.DTYPE_CODES[a.dtype], a.stride(0), N.ptr(w), N.ptr(s),
            m, n, kp, N.DTYPE_CODES[out_dtype], N.ptr(out), n, N.ptr(ws), ws.numel(), N.stream(gpu))
@@ -172,6 +172,8 @@ def mxfp8_linear_mx(source_q: torch.Tensor, source_scale: torch.Tensor, weight: 
     aq, as_, w, s = N.aligned(aq), N.aligned(as_, 4), N.aligned(w), N.aligned(s, 4)
     m, n = aq.shape[0], w.shape[0]
     out = torch.empty(m, n, dtype=out_dtype, device=gpu)
+    ws = torch.empty(max(int(N.library().kq_mx_linear_mx_workspace_size(m, n, kp)), 256), dtype=torch.uint8,
+                     device=gpu)
     N.call("kq_mx_linear_mx", N.FMT_MXFP8_E4M3, N.ptr(aq), N.ptr(as_), kp, N.FMT_MXFP8_E4M3, N.ptr(w), N.ptr(s),
-           m, n, kp, N.DTYPE_CODES[out_dtype], N.ptr(out), n, N.stream(gpu))
+           m, n, kp, N.DTYPE_CODES[out_dtype], N.ptr(out), n, N.ptr(ws), ws.numel(), N.stream(gpu))
     return out if host is None else out.to(host)

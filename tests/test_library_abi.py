@@ -37,7 +37,7 @@ def test_python_binding_covers_every_entry_point():
                                         "kq_sqg_quantize_workspace_size", "kq_qsrt_linear_workspace_size",
                                         "kq_qsrt_moe_workspace_size",
                                         "kq_route_sort_workspace_size", "kq_syrk_accumulate_workspace_size",
-                                        "kq_mx_linear_mm_workspace_size"}
+                                        "kq_mx_linear_mm_workspace_size", "kq_mx_linear_mx_workspace_size"}
     assert set(declared_symbols()) <= bound
 
 
@@ -53,7 +53,7 @@ def test_linear_a8_argument_errors_need_no_gpu():
     lib = _native.library()
     fake = ctypes.c_void_p(256)  # never dereferenced: validation fails first
     e4m3, e2m1 = _native.FMT_MXFP8_E4M3, _native.FMT_MXFP4_E2M1
-    args = [e4m3, fake, fake, 256, e4m3, fake, fake, 8, 8, 256, _native.DT_BF16, fake, 8, None]
+    args = [e4m3, fake, fake, 256, e4m3, fake, fake, 8, 8, 256, _native.DT_BF16, fake, 8, fake, 1 << 20, None]
     bad = list(args)
     bad[4] = e2m1
     assert lib.kq_mx_linear_mx(*bad) == _native.KQ_ERR_INVALID and b"only MXFP8" in lib.kq_last_error()
@@ -66,7 +66,11 @@ def test_linear_a8_argument_errors_need_no_gpu():
     bad = list(args)
     bad[1] = ctypes.c_void_p(264)
     assert lib.kq_mx_linear_mx(*bad) == _native.KQ_ERR_INVALID and b"16-byte aligned" in lib.kq_last_error()
-    assert lib.kq_mx_linear_mm_workspace_size(4096, 7168) >= 4096 * 7168 + 4096 * 224
+    bad = list(args)
+    bad[14] = 16
+    assert lib.kq_mx_linear_mx(*bad) == _native.KQ_ERR_INVALID and b"workspace needs" in lib.kq_last_error()
+    assert lib.kq_mx_linear_mx_workspace_size(4096, 12288, 7168) >= (4096 + 12288) * 224
+    assert lib.kq_mx_linear_mm_workspace_size(4096, 12288, 7168) >= 4096 * 7168 + (2 * 4096 + 12288) * 224
     mm = [e4m3, fake, _native.DT_BF16, 256, fake, fake, 8, 8, 256, _native.DT_BF16, fake, 8, fake, 16, None]
     assert lib.kq_mx_linear_mm(*mm) == _native.KQ_ERR_INVALID and b"workspace needs" in lib.kq_last_error()
     bad = list(mm)
