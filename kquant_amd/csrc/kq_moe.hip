@@ -1600,6 +1600,246 @@ __global__ __launch_bounds__(512, 1) void moe_large_mx_kernel(
   __builtin_amdgcn_s_waitcnt(dma::waitcnt_vm(0));  // no load may land after the workgroup ends
 }
 
+// -------------- grouped GEMM, MXFP4 activations (W4A4), whole-line stages --
+// moe_large_mx_kernel<*, 4> with two LDS stages of 256 k (two MFMA steps
+// each, double buffered) instead of four of 128 k: every direct load of a
+// gathered E2M1 row then fetches its whole 128-byte line for the stage (8
+// rows x 128 B per instruction), and a row's scales for the stage are one 8-
+// byte pair of dwords; with 128-k stages each row fetched half a line and a
+// 4-byte scale dword per step, which made the loads issue about 2.4x the
+// line requests their bytes need (the bound of these kernels: with their
+// MFMAs switched off they kept 80 % of their time).  Same tiles, waves, tile
+// order, MFMA sequence and epilogues, so the result is bitwise that of
+// moe_large_mx_kernel<*, 4>.  Per stage in LDS: A [row][8 chunks of 16 B],
+// chunk c of row r at slot c ^ ((r / 2) % 8); the A scale bytes [row][8];
+// the weight tiles [half][row group][1 KiB] and their scale tiles [row
+// group][half][64 B].  Needs K % 256 == 0.
+namespace mx4_gemm {
+constexpr int SK = 256;                      // k per stage
+constexpr int AS_OFF = BM * 128;             // A: 256 rows x 128 B
+constexpr int W_OFF = AS_OFF + BM * 8;       // A scales: 8 bytes per row
+constexpr int WS_OFF = W_OFF + 2 * 16 * 1024;
+constexpr int STAGE4 = WS_OFF + 16 * 128;
+constexpr int LOADS = 4 + 1 + 4 + 1;         // direct loads per wave per stage
+}  // namespace mx4_gemm
+
+__shared__ __attribute__((aligned(16))) unsigned char moe_mx4_lds[2 * mx4_gemm::STAGE4];
+
+template <bool GATEUP>
+__global__ __launch_bounds__(512, 1) void moe_large_mx4_kernel(
+    const uint8_t* __restrict__ aq, const uint8_t* __restrict__ as, uint32_t aq_bytes,
+    uint32_t as_bytes, int topk, const int* __restrict__ offsets, const int* __restrict__ sorted,
+    const int* __restrict__ tiles, const int* __restrict__ meta, const uint8_t* __restrict__ wt,
+    const uint8_t* __restrict__ wst, const int* __restrict__ sslot, int64_t rows_per_expert, int64_t K,
+    int64_t inter, int col_tiles, ActParams act, const float* __restrict__ route_w,
+    uint16_t* __restrict__ act_out, float* __restrict__ y_out, int64_t hidden) {
+  using namespace mx4_gemm;
+  using dma::i32x4_t;
+  const int G = gridDim.x;
+  const int worker = (int)(blockIdx.x % 8) * (G / 8) + (int)(blockIdx.x / 8);
+  const int total = meta[1] * col_tiles;
+  if (worker >= total) return;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t nchunk = K / 128, rgs = rows_per_expert / 16;
+  const int64_t nrows = GATEUP ? 2 * inter : hidden;
+  const int64_t arow_bytes = K / 2, asrow = K / 32;
+  const uint32_t b_bytes = (uint32_t)(rgs * nchunk * 1024), s_bytes = (uint32_t)(rgs * nchunk * 64);
+  const int stages = (int)(K / SK);
+  const uint32_t lds0 = dma::lds_offset_of(moe_mx4_lds);
+  const int nblk = col_tiles % 8 == 0 ? 8 : col_tiles % 4 == 0 ? 4 : 1;
+  const i32x4_t a_rsrc = dma::make_rsrc(aq, aq_bytes);
+  const i32x4_t as_rsrc = dma::make_rsrc(as, as_bytes);
+  auto grow_group = [&](int64_t c0, int lrg) -> int64_t {
+    if (GATEUP) return lrg < 8 ? c0 / 16 + lrg : inter / 16 + c0 / 16 + (lrg - 8);
+    return c0 / 16 + lrg;
+  };
+
+  // ---- load side.  A load q (0..3) of wave w: the 8-row piece w + 8 q,
+  // lane l: row 8 (w + 8 q) + l / 8, slot l % 8, i.e. logical chunk
+  // (l % 8) ^ ((row / 2) % 8).  A scales: lane l: row 32 w + l / 2, dword
+  // l % 2 of its 8 bytes.  W load q: tile 4 w + q of [half][row group].  W
+  // scales (lanes 0..15): row group 2 w + l / 8, 16-byte piece l % 8 of its
+  // two 64-byte scale tiles.
+  int lt = worker, ls = 0;
+  uint32_t a_off[4], as_off = 0, b_off[4], bs_off = 0;
+  i32x4_t b_rsrc = dma::make_rsrc(wt, 0), s_rsrc = dma::make_rsrc(wst, 0);
+  auto set_load_tile = [&]() {
+    if (lt >= total) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) a_off[q] = aq_bytes, b_off[q] = b_bytes;
+      as_off = as_bytes;
+      bs_off = s_bytes;
+      return;
+    }
+    int mt, nt;
+    grouped_tile(lt, col_tiles, nblk, tiles, offsets, mt, nt);
+    const int e = tiles[2 * mt], m0 = tiles[2 * mt + 1];
+    const int beg = offsets[e], n = offsets[e + 1] - beg;
+    const int64_t c0 = (int64_t)nt * (GATEUP ? BN / 2 : BN);
+    int src[5];  // every row lookup issued before the first use
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int slot = m0 + 8 * (wave + 8 * q) + (lane >> 3);
+      src[q] = GATEUP ? sorted[beg + (slot < n ? slot : n - 1)] : beg + slot;
+    }
+    {
+      const int slot = m0 + 32 * wave + (lane >> 1);
+      src[4] = GATEUP ? sorted[beg + (slot < n ? slot : n - 1)] : beg + slot;
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int row = 8 * (wave + 8 * q) + (lane >> 3);
+      const int ch = (lane & 7) ^ ((row >> 1) & 7);
+      const int64_t r = GATEUP ? src[q] / topk : src[q];
+      a_off[q] = m0 + row < n ? (uint32_t)(r * arow_bytes + ch * 16) : aq_bytes;
+    }
+    {
+      const int row = 32 * wave + (lane >> 1);
+      const int64_t r = GATEUP ? src[4] / topk : src[4];
+      as_off = m0 + row < n ? (uint32_t)(r * asrow + 4 * (lane & 1)) : as_bytes;
+    }
+    b_rsrc = dma::make_rsrc(wt + (int64_t)e * rgs * nchunk * 1024, b_bytes);
+    s_rsrc = dma::make_rsrc(wst + (int64_t)(sslot ? sslot[e] : e) * rgs * nchunk * 64, s_bytes);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int tile = 4 * wave + q, half = tile >> 4;
+      const int64_t rg = grow_group(c0, tile & 15);
+      b_off[q] = 16 * rg < nrows ? (uint32_t)((rg * nchunk + half) * 1024 + lane * 16) : b_bytes;
+    }
+    {
+      const int64_t rg = grow_group(c0, 2 * wave + ((lane >> 3) & 1));
+      bs_off = 16 * rg < nrows ? (uint32_t)(rg * nchunk * 64 + (lane & 7) * 16) : s_bytes;
+    }
+  };
+  auto issue = [&](int slot) {
+    const uint32_t base = lds0 + (uint32_t)(slot * STAGE4);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      dma::load_to_lds16(a_rsrc, a_off[q] >= aq_bytes ? aq_bytes : a_off[q] + (uint32_t)ls * 128u,
+                         base + (uint32_t)((wave + 8 * q) * 1024));
+    dma::load_to_lds4(as_rsrc, as_off >= as_bytes ? as_bytes : as_off + (uint32_t)ls * 8u,
+                      base + (uint32_t)(AS_OFF + wave * 256));
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      dma::load_to_lds16(b_rsrc, b_off[q] >= b_bytes ? b_bytes : b_off[q] + (uint32_t)ls * 2048u,
+                         base + (uint32_t)(W_OFF + (4 * wave + q) * 1024));
+    if (lane < 16)
+      dma::load_to_lds16(s_rsrc, bs_off >= s_bytes ? s_bytes : bs_off + (uint32_t)ls * 128u,
+                         base + (uint32_t)(WS_OFF + wave * 256));
+  };
+  auto advance = [&]() {
+    if (++ls == stages) {
+      ls = 0;
+      lt += G;
+      set_load_tile();
+    }
+  };
+
+  // ---- compute side (offsets of half 0; half h adds 64 h to the A chunk
+  // position, 4 h to the scale byte, 16 KiB / 64 B on the weight side)
+  const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+  const int fm = lane & 15, fg = lane >> 4;
+  int aoff[2][4], asoff[4], boff[8], bsoff[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = wm + 16 * i + fm, sw = (r >> 1) & 7;
+    aoff[0][i] = r * 128 + 16 * (fg ^ sw);
+    aoff[1][i] = r * 128 + 16 * ((4 + fg) ^ sw);
+    asoff[i] = AS_OFF + 8 * r + fg;
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int rr = GATEUP ? (j < 4 ? 0 : BN / 2) + wn + 16 * (j & 3) + fm : 2 * wn + 16 * j + fm;
+    boff[j] = W_OFF + (rr >> 4) * 1024 + (fg * 16 + (rr & 15)) * 16;
+    bsoff[j] = WS_OFF + (rr >> 4) * 128 + fg * 16 + (rr & 15);
+  }
+
+  set_load_tile();
+  issue(0);
+  advance();
+  int cslot = 0;
+  for (int t = worker; t < total; t += G) {
+    int mt, nt;
+    grouped_tile(t, col_tiles, nblk, tiles, offsets, mt, nt);
+    const int e = tiles[2 * mt], m0 = tiles[2 * mt + 1];
+    const int beg = offsets[e], n = offsets[e + 1] - beg;
+    const int64_t c0 = (int64_t)nt * (GATEUP ? BN / 2 : BN);
+    const bool active = m0 + wm < n;
+    f32x4_t acc[4][8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    for (int s = 0; s < stages; ++s) {
+      // stage s landed (the only one in flight) and every wave is done with
+      // the other slot, which now takes the next stage
+      dma::wait_and_barrier<0>();
+      issue(cslot ^ 1);
+      advance();
+      if (active) {
+        const unsigned char* st = moe_mx4_lds + cslot * STAGE4;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          i32x8_t a8[4];
+          uint32_t sa[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const u32x4_t v0 = *reinterpret_cast<const u32x4_t*>(st + aoff[h][i]);
+            a8[i] = i32x8_t{(int)v0[0], (int)v0[1], (int)v0[2], (int)v0[3], 0, 0, 0, 0};
+            sa[i] = st[asoff[i] + 4 * h];
+          }
+          u32x4_t wv[8];
+          int sb[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            wv[j] = *reinterpret_cast<const u32x4_t*>(st + boff[j] + h * 16384);
+            sb[j] = st[bsoff[j] + h * 64];
+          }
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const i32x8_t b8 = i32x8_t{(int)wv[j][0], (int)wv[j][1], (int)wv[j][2], (int)wv[j][3], 0, 0, 0, 0};
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a8[i], b8, acc[i][j], 4, 4, 0,
+                                                                           (int)sa[i], 0, sb[j]);
+          }
+        }
+      }
+      cslot ^= 1;
+    }
+
+    if (active) {
+      // D layout (16x16): lane holds rows 4 fg + r, column fm of its block
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int slot = m0 + wm + 16 * i + 4 * fg + r;
+          if (slot >= n) continue;
+          if (GATEUP) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const float v = activate(act, acc[i][j][r], acc[i][j + 4][r]);
+              const int64_t ch = c0 + wn + 16 * j + fm;
+              reinterpret_cast<__bf16*>(act_out)[(int64_t)(beg + slot) * inter + ch] = (__bf16)v;
+            }
+          } else {
+            const int pair = sorted[beg + slot];
+            const float rw = route_w[pair];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+              const int64_t h = c0 + 2 * wn + 16 * j + fm;
+              y_out[(int64_t)pair * hidden + h] = rw * acc[i][j][r];
+            }
+          }
+        }
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(dma::waitcnt_vm(0));  // no load may land after the workgroup ends
+}
+
 // ---------------------------------------------------------------- combine --
 template <int OUT>
 __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restrict__ y,
@@ -1901,7 +2141,15 @@ static int moe_forward_mx(const Layout& L, unsigned char* w, const ActParams& ap
       hidden, inter, ap, route_weights, act, y, hidden);
   if (e != hipSuccess) return kq_check_launch(e, "kq_moe_forward/gateup_small");
   const int64_t abytes = AF == 4 ? hidden / 2 : hidden;
-  if (any_large) {
+  // E2M1 activations with K a multiple of 256 take the whole-line kernel
+  const bool lines = AF == 4 && hidden % mx4_gemm::SK == 0 && inter % mx4_gemm::SK == 0;
+  if (any_large && lines) {
+    moe_large_mx4_kernel<true><<<grid_dma, THREADS, 0, st>>>(
+        xq, xs, (uint32_t)(tokens * abytes), (uint32_t)(tokens * hidden / 32), topk, offsets, sorted,
+        large_tiles, meta, w13_t, w13_st, sslot, 2 * inter, hidden, inter, (int)(inter / (BN / 2)), ap,
+        route_weights, act, y, hidden);
+    if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_moe_forward/gateup_large");
+  } else if (any_large) {
     moe_large_mx_kernel<true, AF><<<grid_dma, THREADS, 0, st>>>(
         xq, xs, (uint32_t)(tokens * abytes), (uint32_t)(tokens * hidden / 32), topk, offsets, sorted,
         large_tiles, meta, w13_t, w13_st, sslot, 2 * inter, hidden, inter, (int)(inter / (BN / 2)), ap,
@@ -1915,7 +2163,13 @@ static int moe_forward_mx(const Layout& L, unsigned char* w, const ActParams& ap
       (const uint8_t*)as, topk, sorted, small_list, w2_t, w2_st, gslot, x4t_gemv(xa, false), hidden, inter,
       inter, ap, route_weights, act, y, hidden);
   if (e != hipSuccess) return kq_check_launch(e, "kq_moe_forward/down_small");
-  if (any_large) {
+  if (any_large && lines) {
+    moe_large_mx4_kernel<false><<<grid_dma, THREADS, 0, st>>>(
+        aq, as, (uint32_t)(L.pairs * inter / 2), (uint32_t)(L.pairs * inter / 32), topk, offsets, sorted,
+        large_tiles, meta, w2_t, w2_st, sslot, hidden, inter, inter, (int)(hidden / BN), ap, route_weights, act,
+        y, hidden);
+    if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_moe_forward/down_large");
+  } else if (any_large) {
     const int64_t ibytes = AF == 4 ? inter / 2 : inter;
     moe_large_mx_kernel<false, AF><<<grid_dma, THREADS, 0, st>>>(
         aq, as, (uint32_t)(L.pairs * ibytes), (uint32_t)(L.pairs * inter / 32), topk, offsets, sorted,
