@@ -550,11 +550,12 @@ __device__ __forceinline__ void x4t_finish(const X4TGemv& xg, int e, int64_t til
 //
 // GATEUP: rows of w13, output act -> bf16 intermediates.
 // !GATEUP: rows of w2, output route_weight * partial -> fp32 pair rows.
-// ROUTE (a decode of at most DD_PAIRS pairs, dense scales): no routing
-// launch and no list; workgroup x takes pair x alone (expert route.ids[x],
-// one token slot) and writes its intermediate to row x.  Each MFMA output
-// row depends only on its own A row, so the values are those of the listed
-// form; a pair whose expert repeats reads that expert's weights again.
+// ROUTE (a decode of at most DD_PAIRS pairs): no routing launch and no
+// list; workgroup x takes pair x alone (expert route.ids[x], one token slot)
+// and writes its intermediate to row x.  Each MFMA output row depends only on
+// its own A row, so the values are those of the listed form; a pair whose
+// expert repeats reads that expert's weights again.  With X4T-coded scales
+// the workgroup decodes its expert's scale tiles as in the listed form.
 struct DecodeRouteArgs {
   const int* ids;
   int experts;
@@ -572,7 +573,7 @@ __global__ __launch_bounds__(S * RW * 64) void moe_small_kernel(
   constexpr int NBUF = P + 1;
   constexpr int T = S * RW * 64, NRB = RW * NB;
   static_assert(NB * 33 <= 128 * S, "fixed tiles of the row blocks: at most two 16-byte loads per thread");
-  static_assert(!ROUTE || (!X4T && GATEUP), "per-pair decode: dense scales, gate/up");
+  static_assert(!ROUTE || GATEUP, "per-pair decode: gate/up");
   extern __shared__ __attribute__((aligned(16))) unsigned char x4t_lds[];
   int e, beg, n;
   if constexpr (ROUTE) {
@@ -1901,16 +1902,28 @@ using namespace kq::moe;
 // slot order as moe_combine_kernel sums them.  Same operations in the same
 // order, so the output is bitwise that of the routing, down GEMV and
 // combine launches it replaces -- without the fp32 pair rows in HBM.
+// X4T: the w2 scales stay X4T-coded; the two waves of a pair each decode
+// one of its two 16-row scale tiles into LDS (scale-tile layout, exceptions
+// patched after the fixed bytes) while their first weight loads are in
+// flight, so the K loop reads each lane's scale byte from LDS -- the bytes of
+// the dense-scale form, hence the same output bit for bit.
 constexpr int DD_PAIRS = 8;
-template <int NBP, int P, int STEPS, int OUT>
+constexpr int DD_X4T_COLS = 128;  // w2 scale columns (I / 32) the fused X4T decode stages
+constexpr int DD_X4T_TP = 1 + DD_X4T_COLS / 8;  // 16-byte pieces of a fixed tile at most
+
+template <int NBP, int P, int STEPS, int OUT, bool X4T = false>
 __global__ __launch_bounds__(DD_PAIRS * 2 * 64) void moe_decode_down_kernel(
     const uint16_t* __restrict__ act, int64_t inter, const int* __restrict__ ids, int topk, int experts,
     int tokens, const uint8_t* __restrict__ wt, const uint8_t* __restrict__ wst, int64_t hidden,
-    const float* __restrict__ route_w, void* __restrict__ out) {
+    const float* __restrict__ route_w, void* __restrict__ out, X4TGemv xg) {
   constexpr int CH = 16 * NBP, NBUF = P + 1;
   static_assert(STEPS > 0, "compile-time K steps");
+  static_assert(!X4T || NBP == 2, "X4T: one 16-row scale tile per wave of a pair");
   __shared__ f32x4_t red[2 * DD_PAIRS][NBP][64];
   __shared__ float ybuf[DD_PAIRS][CH];
+  // X4T: decoded scale tiles [pair][row block][chunk][64] and each wave's staged fixed tile
+  __shared__ __attribute__((aligned(16))) uint8_t xsl[X4T ? DD_PAIRS * 2 * (DD_X4T_COLS / 4) * 64 : 16];
+  __shared__ __attribute__((aligned(16))) uint8_t xfl[X4T ? 2 * DD_PAIRS * 16 * DD_X4T_TP : 16];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int m = lane & 15, g = lane >> 4;
   const int pair = wave >> 1, kpart = wave & 1;   // pair = intermediate row
@@ -1923,6 +1936,50 @@ __global__ __launch_bounds__(DD_PAIRS * 2 * 64) void moe_decode_down_kernel(
   f32x4_t acc[NBP];
 #pragma unroll
   for (int b = 0; b < NBP; ++b) acc[b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  // X4T: this wave decodes tile c0 / 16 + kpart of its pair's expert; the
+  // fixed tile and the tile's exception range are loaded before the weights
+  u32x4_t xpiece = {0u, 0u, 0u, 0u};
+  uint32_t xr[2] = {0u, 0u};
+  const int64_t xt = c0 / 16 + kpart;
+  const int tp = X4T ? 1 + ((xg.cols + 7) >> 3) : 1;
+  if (X4T && valid) {
+    if (lane < tp)
+      xpiece = *reinterpret_cast<const u32x4_t*>(xg.fixed[0] + ((int64_t)pe * xg.tiles + xt) * (16 * tp) + 16 * lane);
+    xr[0] = xg.idx[0][(int64_t)pe * xg.tiles + xt];
+    xr[1] = xg.idx[0][(int64_t)pe * xg.tiles + xt + 1];
+  }
+  auto x4t_decode = [&]() {
+    const int cols = xg.cols, sb = (cols + 7) >> 3, span = 16 * cols;
+    uint8_t* fl = xfl + wave * 16 * DD_X4T_TP;
+    uint8_t* sl = xsl + (pair * 2 + kpart) * (DD_X4T_COLS / 4) * 64;
+    if (lane < tp) *reinterpret_cast<u32x4_t*>(fl + 16 * lane) = xpiece;
+    // one wave's LDS accesses complete in order: the staged bytes are read
+    // below, and the exception bytes overwrite the fixed ones
+    const int lo = (int)xr[0], hi = (int)xr[1];
+    const uint32_t w0 = lo + lane < hi ? xg.exc[0][lo + lane] : 0u;
+    for (int c = lane; c < cols; c += 64) {  // column c of the tile: base(row) + selector bit (row, c)
+      uint32_t v[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v[i] = 0;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = 4 * i + r;
+          const uint32_t bit = (fl[16 + row * sb + (c >> 3)] >> (c & 7)) & 1u;
+          v[i] |= ((fl[row] + bit) & 0xffu) << (8 * r);
+        }
+      }
+      *reinterpret_cast<u32x4_t*>(sl + (c >> 2) * 64 + (c & 3) * 16) = u32x4_t{v[0], v[1], v[2], v[3]};
+    }
+    for (int k = lo + lane; k < hi; k += 64) {
+      const uint32_t w = k == lo + lane ? w0 : xg.exc[0][k];
+      const uint32_t off = (w & 0xffffffu) - (uint32_t)(xt * span);  // wraps past the tile when outside
+      if (off < (uint32_t)span) {
+        const int r = (int)off / cols, c = (int)off - r * cols;
+        sl[(c >> 2) * 64 + (c & 3) * 16 + r] = (uint8_t)(w >> 24);
+      }
+    }
+  };
   if (valid) {
     const int e = pe;
     const uint8_t* wtile[NBP];
@@ -1932,7 +1989,7 @@ __global__ __launch_bounds__(DD_PAIRS * 2 * 64) void moe_decode_down_kernel(
       const int64_t rg = c0 / 16 + b;
       const int64_t t0 = ((int64_t)e * rgs + rg) * nchunk + c_first;
       wtile[b] = wt + t0 * 1024 + 16 * lane;
-      stile[b] = wst + t0 * 64 + lane;
+      stile[b] = X4T ? nullptr : wst + t0 * 64 + lane;
     }
     struct WBuf {
       u32x4_t w[NBP];
@@ -1945,13 +2002,15 @@ __global__ __launch_bounds__(DD_PAIRS * 2 * 64) void moe_decode_down_kernel(
 #pragma unroll
       for (int b = 0; b < NBP; ++b) {
         B.w[b] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(wtile[b] + (int64_t)s * 1024));
-        B.ws[b] = stile[b][(int64_t)s * 64];
+        if (!X4T) B.ws[b] = stile[b][(int64_t)s * 64];
       }
     };
     WBuf wb[NBUF];
     ABuf ab[NBUF];
 #pragma unroll
     for (int s = 0; s < P && s < STEPS; ++s) load_w(s, wb[s]);
+    __builtin_amdgcn_sched_barrier(0);
+    if (X4T) x4t_decode();
     __builtin_amdgcn_sched_barrier(0);
     // every token slot reads the pair's row; only slot 0 is stored
     const uint16_t* ap = act + (int64_t)pair * inter + 32 * g;
@@ -1960,19 +2019,26 @@ __global__ __launch_bounds__(DD_PAIRS * 2 * 64) void moe_decode_down_kernel(
 #pragma unroll
       for (int t = 0; t < 4; ++t) B.v[t] = *reinterpret_cast<const u32x4_t*>(ap + 128 * c + 8 * t);
     };
-    auto compute = [&](const WBuf& W, const ABuf& A) {
+    // X4T: this pair's decoded tiles; row block b is tile c0 / 16 + b
+    const uint8_t* xs = xsl + pair * 2 * (DD_X4T_COLS / 4) * 64 + c_first * 64 + lane;
+    auto compute = [&](const WBuf& W, const ABuf& A, int s) {
+      uint32_t ws[NBP];
+#pragma unroll
+      for (int b = 0; b < NBP; ++b) ws[b] = X4T ? (uint32_t)xs[(b * (DD_X4T_COLS / 4) + s) * 64] : W.ws[b];
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         const bf16x8_t fa = __builtin_bit_cast(bf16x8_t, A.v[t]);
 #pragma unroll
         for (int b = 0; b < NBP; ++b) {
-          const bf16x8_t fb = gemm::dequant8<1>(u32x2_t{W.w[b][t], 0u}, W.ws[b]);
+          const bf16x8_t fb = gemm::dequant8<1>(u32x2_t{W.w[b][t], 0u}, ws[b]);
           acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa, fb, acc[b], 0, 0, 0);
         }
       }
     };
 #pragma unroll
     for (int s = 0; s < P && s < STEPS; ++s) load_a(s, ab[s]);
+    // X4T: both tiles of every pair decoded before any wave reads them
+    if (X4T) lds_barrier();
 #pragma unroll
     for (int s = 0; s < STEPS; ++s) {
       if (s + P < STEPS) {
@@ -1980,9 +2046,11 @@ __global__ __launch_bounds__(DD_PAIRS * 2 * 64) void moe_decode_down_kernel(
         load_a(s + P, ab[(s + P) % NBUF]);
       }
       __builtin_amdgcn_sched_barrier(0);
-      compute(wb[s % NBUF], ab[s % NBUF]);
+      compute(wb[s % NBUF], ab[s % NBUF], s);
       __builtin_amdgcn_sched_barrier(0);
     }
+  } else if (X4T) {
+    lds_barrier();  // invalid pairs cross the decode barrier with the others
   }
 #pragma unroll
   for (int b = 0; b < NBP; ++b) red[wave][b][lane] = acc[b];
@@ -2048,11 +2116,13 @@ static hipError_t launch_small(bool x4t, int64_t experts_max, int64_t channels, 
   const size_t shm = x4t ? x4t_gemv_lds(RW * NB, nchunk, cols) : 0;
   const DecodeRouteArgs none{nullptr, 0};
   constexpr bool CAN_ROUTE = GATEUP;
-  if (route && (x4t || !CAN_ROUTE)) return hipErrorInvalidValue;
+  if (route && !CAN_ROUTE) return hipErrorInvalidValue;
   switch (steps) {
 #define KQ_SMALL_CASE(N)                                                                                      \
     case N:                                                                                                   \
-      if (x4t) moe_small_kernel<GATEUP, true, NBP, S, RW, P, N><<<grid, S * RW * 64, shm, st>>>(args..., none); \
+      if (x4t && route) moe_small_kernel<GATEUP, true, NBP, S, RW, P, N, CAN_ROUTE>                           \
+          <<<grid, S * RW * 64, shm, st>>>(args..., *route);                                                  \
+      else if (x4t) moe_small_kernel<GATEUP, true, NBP, S, RW, P, N><<<grid, S * RW * 64, shm, st>>>(args..., none); \
       else if (route) moe_small_kernel<GATEUP, false, NBP, S, RW, P, N, CAN_ROUTE>                            \
           <<<grid, S * RW * 64, 0, st>>>(args..., *route);                                                    \
       else moe_small_kernel<GATEUP, false, NBP, S, RW, P, N><<<grid, S * RW * 64, 0, st>>>(args..., none);    \
@@ -2061,7 +2131,9 @@ static hipError_t launch_small(bool x4t, int64_t experts_max, int64_t channels, 
     KQ_SMALL_CASE(16) KQ_SMALL_CASE(28)
 #undef KQ_SMALL_CASE
     default:
-      if (x4t) moe_small_kernel<GATEUP, true, NBP, S, RW, P, 0><<<grid, S * RW * 64, shm, st>>>(args..., none);
+      if (x4t && route)
+        moe_small_kernel<GATEUP, true, NBP, S, RW, P, 0, CAN_ROUTE><<<grid, S * RW * 64, shm, st>>>(args..., *route);
+      else if (x4t) moe_small_kernel<GATEUP, true, NBP, S, RW, P, 0><<<grid, S * RW * 64, shm, st>>>(args..., none);
       else if (route)
         moe_small_kernel<GATEUP, false, NBP, S, RW, P, 0, CAN_ROUTE><<<grid, S * RW * 64, 0, st>>>(args..., *route);
       else moe_small_kernel<GATEUP, false, NBP, S, RW, P, 0><<<grid, S * RW * 64, 0, st>>>(args..., none);
@@ -2258,8 +2330,9 @@ static int moe_forward_impl(const char* fn, int activation, float act_beta, floa
   // A decode of at most DD_PAIRS pairs with dense scales and bf16
   // activations needs no routing launch: one gate/up workgroup per pair, and
   // the down projection with the combine in one launch.
-  const bool route_in_gemv = decode && !xa && act_fmt < 0 && L.pairs <= DD_PAIRS && hidden % 32 == 0 &&
-                             (inter == 512 || inter == 1024 || inter == 2048 || inter == 4096);
+  const bool route_in_gemv = decode && act_fmt < 0 && L.pairs <= DD_PAIRS && hidden % 32 == 0 &&
+                             (inter == 512 || inter == 1024 || inter == 2048 || inter == 4096) &&
+                             (!xa || inter / 32 <= DD_X4T_COLS);
   const DecodeRouteArgs dra{route_ids, experts};
   if (decode && !route_in_gemv) {
     route_decode_kernel<<<1, DECODE_MAX_PAIRS, 0, st>>>(route_ids, (int)L.pairs, experts, sorted,
@@ -2366,20 +2439,23 @@ static int moe_forward_impl(const char* fn, int activation, float act_beta, floa
     const int64_t steps = inter / 128 / 2;
     const dim3 grid((unsigned)(hidden / 32));
     const bool f32 = out_dtype == KQ_DT_F32;
+    const X4TGemv xg2 = x4t_gemv(xa, false);
+#define KQ_DD_LAUNCH(NS, OUTC, X)                                                                             \
+    moe_decode_down_kernel<2, 2, NS, OUTC, X><<<grid, DD_PAIRS * 2 * 64, 0, st>>>(                            \
+        (const uint16_t*)act, inter, route_ids, topk, experts, (int)tokens, w2_t, w2_st, hidden, route_weights, \
+        out, xg2)
 #define KQ_DD_CASE(NS)                                                                                        \
     if (steps == NS) {                                                                                        \
-      if (f32)                                                                                                \
-        moe_decode_down_kernel<2, 2, NS, 2><<<grid, DD_PAIRS * 2 * 64, 0, st>>>(                              \
-            (const uint16_t*)act, inter, route_ids, topk, experts, (int)tokens, w2_t, w2_st, hidden,          \
-            route_weights, out);                                                                              \
-      else                                                                                                    \
-        moe_decode_down_kernel<2, 2, NS, 0><<<grid, DD_PAIRS * 2 * 64, 0, st>>>(                              \
-            (const uint16_t*)act, inter, route_ids, topk, experts, (int)tokens, w2_t, w2_st, hidden,          \
-            route_weights, out);                                                                              \
+      if (xa) {                                                                                               \
+        if (f32) KQ_DD_LAUNCH(NS, 2, true); else KQ_DD_LAUNCH(NS, 0, true);                                   \
+      } else {                                                                                                \
+        if (f32) KQ_DD_LAUNCH(NS, 2, false); else KQ_DD_LAUNCH(NS, 0, false);                                 \
+      }                                                                                                       \
       return kq_check_launch(hipGetLastError(), "kq_moe_forward/decode_down");                               \
     }
     KQ_DD_CASE(2) KQ_DD_CASE(4) KQ_DD_CASE(8) KQ_DD_CASE(16)
 #undef KQ_DD_CASE
+#undef KQ_DD_LAUNCH
     return kq_fail(KQ_ERR_INVALID, "%s: decode down shape", fn);
   }
   {

@@ -99,28 +99,39 @@ def test_no_valid_pair_gives_zeros(gpu, out_dtype):
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
 def test_per_pair_decode_matches_listed_path_bitwise(gpu, out_dtype, inter):
     """At most 8 pairs the forward skips the routing launch (one gate/up
-    workgroup per pair) and fuses the down projection with the combine.  Its
-    output is bitwise that of the routed-list path (which the X4T-scale
-    forward still takes, on the same scale bytes), here with an expert
-    repeated across tokens, invalid ids, a token with no valid expert, and
-    each intermediate width that selects its own instantiation of the fused
-    down kernel (2 / 4 / 8 / 16 K steps)."""
+    workgroup per pair) and fuses the down projection with the combine, with
+    dense or X4T-coded scales.  Its output is bitwise that of the routed-list
+    path, which the same 4 tokens take when 5 more tokens (18 pairs) ride
+    along (a token's output depends only on its own pairs): here with an
+    expert repeated across tokens, invalid ids, a token with no valid expert,
+    and each intermediate width that selects its own instantiation of the
+    fused down kernel (2 / 4 / 8 / 16 K steps)."""
     T, k, E, H, I = 4, 2, 4, 512, inter
     ids = torch.tensor([[1, 3], [3, -1], [0, 99], [-2, -1]], dtype=torch.int32)
     w = torch.rand(T, k, generator=torch.Generator().manual_seed(8))
     x = torch.randn(T, H, generator=torch.Generator().manual_seed(9)).to(torch.bfloat16)
+    extra = 5
+    ids_l = torch.cat([ids, torch.randint(0, E, (extra, k), generator=torch.Generator().manual_seed(10),
+                                          dtype=torch.int32)])
+    w_l = torch.cat([w, torch.rand(extra, k, generator=torch.Generator().manual_seed(11))])
+    x_l = torch.cat([x, torch.randn(extra, H, generator=torch.Generator().manual_seed(12)).to(torch.bfloat16)])
     raw = workloads.quantized_experts(range(E), E, H, I, seed=5, device=gpu)
     dense = moe.prepare_expert_weights(*raw)
     x4t = moe.prepare_expert_weights(*raw, scale_format="x4t")
-    args = (x.to(gpu), ids.to(gpu), w.to(gpu))
-    fused = moe.grouped_expert_forward(*args, dense, out_dtype=out_dtype)
-    listed = moe.grouped_expert_forward(*args, x4t, out_dtype=out_dtype)
-    assert torch.equal(fused, listed)
+    outs = {}
+    for name, prep in (("dense", dense), ("x4t", x4t)):
+        outs[f"fused_{name}"] = moe.grouped_expert_forward(x.to(gpu), ids.to(gpu), w.to(gpu), prep,
+                                                           out_dtype=out_dtype)
+        outs[f"listed_{name}"] = moe.grouped_expert_forward(x_l.to(gpu), ids_l.to(gpu), w_l.to(gpu), prep,
+                                                            out_dtype=out_dtype)[:T]
+    fused = outs["fused_dense"]
+    for name, got in outs.items():
+        assert torch.equal(got, fused), name
     assert torch.count_nonzero(fused[3]) == 0
     valid = (ids >= 0) & (ids < E)
     ref = _oracle(x, torch.where(valid, ids, torch.zeros_like(ids)), w * valid, raw, "situ")
     assert _max_rel(ref, fused.float().cpu().numpy()) <= (TOL if out_dtype == torch.float32 else 2 ** -8)
-    again = moe.grouped_expert_forward(*args, dense, out_dtype=out_dtype)
+    again = moe.grouped_expert_forward(x.to(gpu), ids.to(gpu), w.to(gpu), x4t, out_dtype=out_dtype)
     assert torch.equal(again, fused)
 
 
