@@ -658,6 +658,43 @@ def main() -> int:
                 "x4t_added_us": round((t_x - t) * 1e6, 1),
             }
         del weights, weights_x4t
+        # The reference's one published routed-MoE figure is at this shape
+        # (docs/qsrt-technical-brief.md:458-470: Kimi-K3 TP12 shard, hidden
+        # 3584, 256 intermediate channels per rank, top-16, one token, 1 .. 16
+        # distinct experts, dense vs X4T scales, CUDA-graph replays on another
+        # GPU).  Same shape here, time per forward from a HIP graph of 20.
+        tp_e, tp_h, tp_i, tp_k = 896, 3584, 256, 16
+        gtp = torch.Generator().manual_seed(21)
+        tp_pick = torch.randperm(tp_e, generator=gtp)[:16]
+        raw = workloads.quantized_experts(tp_pick.tolist(), tp_e, tp_h, tp_i, seed=21, device=dev)
+        tp_dense = moe.prepare_expert_weights(*raw)
+        tp_x4t = moe.prepare_expert_weights(*raw, scale_format="x4t")
+        del raw
+        xt = torch.randn(1, tp_h, generator=gtp).to(torch.bfloat16).to(dev)
+        tp_rows = {}
+        for n in (1, 2, 4, 8, 16):
+            ids_t = tp_pick[:n].repeat(tp_k // n).reshape(1, tp_k).to(torch.int32).to(dev)
+            w_t = torch.softmax(torch.randn(1, tp_k, generator=gtp), dim=-1).to(dev)
+            row = {}
+            for tag, wts in (("dense", tp_dense), ("x4t", tp_x4t)):
+                moe.grouped_expert_forward(xt, ids_t, w_t, wts)
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph):
+                    for _ in range(20):
+                        moe.grouped_expert_forward(xt, ids_t, w_t, wts)
+                row[f"{tag}_us"] = round(_time_loop(torch, graph.replay, 10, 3) / 20 * 1e6, 2)
+                del graph
+            row["x4t_added_us"] = round(row["x4t_us"] - row["dense_us"], 2)
+            tp_rows[f"experts{n}"] = row
+        del tp_dense, tp_x4t
+        dec["tp12_published_shape"] = {
+            "workload": "routed MoE decode, 1 token, hidden 3584, I 256 (TP12 shard), top-16 over 1..16 distinct "
+                        "experts, MXFP4 W4A16, dense vs X4T-coded scales; time per forward from a HIP graph of 20",
+            **tp_rows,
+            "reference_published_us": {"dense": [22.08, 22.11, 22.11, 24.16, 30.30],
+                                       "x4t": [24.16, 26.11, 26.21, 28.26, 32.35],
+                                       "experts": [1, 2, 4, 8, 16], "gpu": "RTX PRO 6000 Blackwell Max-Q"},
+        }
         dec["note"] = ("cold: routings rotated over fresh experts (weights read once per forward from HBM); "
                        "bytes = distinct experts' MXFP4 weights + the token rows")
         result["cfg5_moe_decode"] = dec

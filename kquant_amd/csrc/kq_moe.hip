@@ -2283,10 +2283,16 @@ static int moe_forward_impl(const char* fn, int activation, float act_beta, floa
   if (tokens < 0 || topk <= 0 || topk > 64 || experts <= 0 || experts > MAX_EXPERTS)
     return kq_fail(KQ_ERR_INVALID, "%s: need tokens >= 0, 1 <= topk <= 64, 1 <= experts <= %d", fn,
                    MAX_EXPERTS);
-  if (hidden <= 0 || inter <= 0 || hidden % 512 != 0 || inter % 512 != 0)
+  // A decode batch with bf16 activations runs only the GEMV kernels, whose K
+  // and channel blocks need multiples of 128 / 64: there an intermediate size
+  // that is a multiple of 256 (a tensor-parallel shard, e.g. 256 channels per
+  // rank at hidden 3584) is accepted too.
+  const bool gemv_only = act_fmt < 0 && tokens * topk <= DECODE_MAX_PAIRS;
+  if (hidden <= 0 || inter <= 0 || hidden % 512 != 0 || inter % (gemv_only ? 256 : 512) != 0)
     return kq_fail(KQ_ERR_INVALID,
-                   "%s: hidden and intermediate sizes must be multiples of 512 "
-                   "(hidden=%lld inter=%lld)", fn, (long long)hidden, (long long)inter);
+                   "%s: hidden and intermediate sizes must be multiples of 512, the intermediate size of a "
+                   "bf16-activation decode batch a multiple of 256 (hidden=%lld inter=%lld)",
+                   fn, (long long)hidden, (long long)inter);
   if (ldx < hidden || ldx % 8 != 0)
     return kq_fail(KQ_ERR_INVALID, "%s: ldx must be >= hidden and a multiple of 8", fn);
   if (kq_misaligned(x, 16) || kq_misaligned(w13_t, 16) || kq_misaligned(w2_t, 16) ||
@@ -2512,8 +2518,8 @@ extern "C" int kq_moe_forward_x4t(int activation, float act_beta, float act_line
                                   void* workspace, int64_t workspace_bytes, uint32_t flags,
                                   void* stream) {
   const char* fn = "kq_moe_forward_x4t";
-  if (hidden <= 0 || inter <= 0 || hidden % 512 != 0 || inter % 512 != 0)
-    return kq_fail(KQ_ERR_INVALID, "%s: hidden and intermediate sizes must be multiples of 512", fn);
+  if (hidden <= 0 || inter <= 0 || hidden % 512 != 0 || inter % 256 != 0)
+    return kq_fail(KQ_ERR_INVALID, "%s: hidden and intermediate sizes must be multiples of 512 / 256", fn);
   // X4T planes: w1 / w3 [inter, hidden / 32], w2 [hidden, inter / 32]; at most
   // 255 columns and 2^24 positions per matrix
   if (hidden / 32 > 255 || inter / 32 > 255 || inter * (hidden / 32) > (1 << 24) - 1 ||

@@ -144,8 +144,11 @@ def _expert_shapes(w13_packed: torch.Tensor, w2_packed: torch.Tensor) -> tuple[i
         raise ValueError(f"w13_packed shape {tuple(w13_packed.shape)} != {(experts, 2 * inter, hidden // 2)}")
     if w2_packed.shape != (experts, hidden, inter // 2):
         raise ValueError(f"w2_packed shape {tuple(w2_packed.shape)} != {(experts, hidden, inter // 2)}")
-    if hidden % 512 or inter % 512:
-        raise ValueError("hidden and intermediate sizes must be multiples of 512")
+    # prefill-sized batches need inter % 512 (the grouped GEMMs' tiles); a
+    # decode batch with bf16 activations takes inter % 256 (the library checks)
+    if hidden % 512 or inter % 256:
+        raise ValueError("hidden must be a multiple of 512 and the intermediate size of 256 "
+                         "(512 outside bf16-activation decode batches)")
     return experts, hidden, inter
 
 

@@ -149,6 +149,34 @@ def test_decode_real_shapes(gpu, tokens):
     assert rel <= TOL
 
 
+@pytest.mark.parametrize("distinct", [1, 4, 16])
+@pytest.mark.parametrize("tokens", [1, 4])
+def test_decode_tp12_shard_shape(gpu, tokens, distinct):
+    """The reference's published routed-MoE decode shape (Kimi-K3 TP12 shard:
+    hidden 3584, 256 intermediate channels per rank, top-16,
+    docs/qsrt-technical-brief.md:458-470): an intermediate size that is a
+    multiple of 256 only, accepted for bf16-activation decode batches.  Each
+    token's 16 slots cycle over ``distinct`` experts (repeated experts in one
+    token), dense and X4T-coded scales, against the oracle and bitwise against
+    each other."""
+    E, H, I, k = 64, 3584, 256, 16
+    g = torch.Generator().manual_seed(tokens * 100 + distinct)
+    ids = torch.stack([torch.randperm(E, generator=g)[:distinct].repeat(k // distinct) for _ in range(tokens)])
+    ids = ids.to(torch.int32)
+    w = torch.softmax(torch.randn(tokens, k, generator=g), dim=-1)
+    x = torch.randn(tokens, H, generator=g).to(torch.bfloat16)
+    raw = workloads.quantized_experts(torch.unique(ids).tolist(), E, H, I, seed=7, device=gpu)
+    dense = moe.prepare_expert_weights(*raw)
+    x4t = moe.prepare_expert_weights(*raw, scale_format="x4t")
+    out = moe.grouped_expert_forward(x.to(gpu), ids.to(gpu), w.to(gpu), dense)
+    out_x4t = moe.grouped_expert_forward(x.to(gpu), ids.to(gpu), w.to(gpu), x4t)
+    assert torch.equal(out, out_x4t)
+    ref = _oracle(x, ids, w, raw, "situ")
+    rel = _max_rel(ref, out.cpu().numpy())
+    print(f"moe tp12 T={tokens} distinct={distinct} max-rel {rel:.2e}", flush=True)
+    assert rel <= TOL
+
+
 def test_tile_layout_matches_oracle(gpu):
     w13q, w13s, w2q, w2s = workloads.quantized_experts([0, 2], 3, 512, 1024, seed=8, device=gpu)
     prep = moe.prepare_expert_weights(w13q, w13s, w2q, w2s)
