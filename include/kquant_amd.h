@@ -298,7 +298,8 @@ int kq_syrk_accumulate_ws(int in_dtype, const void* x, int64_t ld, int64_t n, in
  * kq_syrk_accumulate and averages (H + H^T)/2 inside diagonal tiles
  * (kquant/candidate_hessian.py:106-107, kquant/capture.py:861-862); damping
  * is kquant/exl3_encoder_backend.py:1613-1625 (sigma_reg * mean(diag)).
- * acc and out must not alias. */
+ * acc and out must not alias; k <= 2^20.  Each upper tile of acc is read
+ * once (one workgroup per 64 x 64 block and its mirror). */
 int kq_syrk_finalize(const float* acc, int64_t ld_acc, int64_t k, double denominator,
                      float damp, float* out, int64_t ld_out, void* stream);
 

@@ -1068,23 +1068,99 @@ static hipError_t launch_syrk256(const void* x, int64_t ld, int64_t n, int64_t k
   return hipGetLastError();
 }
 
-// out = sym(acc) * inv_denom : upper tiles are read for every (i, j) as
-// acc[min][max]; one thread per output element, rows of 256 columns.
+// out = sym(acc) * inv.  The computed region is tile(i) <= tile(j)
+// (128-wide tiles; inside a diagonal tile both halves exist).  One workgroup
+// per pair of 64 x 64 blocks (bi <= bj) and its mirror (bj, bi): it reads the
+// upper block acc[bi][bj] once (coalesced rows into LDS), writes it scaled,
+// and writes its transpose into the mirror block; for a pair inside a
+// diagonal tile it also reads acc[bj][bi] and writes the average of the two
+// halves, (acc[i][j] inv + acc[j][i] inv) / 2 (kquant's (H + H^T) / 2), each
+// product and the sum rounded on its own, with the diagonal acc[i][i] inv.
+constexpr int FIN_B = 64;
+template <bool FULL>
+__device__ __forceinline__ void finalize_pair_impl(const float* __restrict__ a, int64_t lda, int64_t k,
+                                                   float inv, float* __restrict__ o, int64_t ldo, int64_t bi,
+                                                   int64_t bj, float (*t)[FIN_B][FIN_B + 1]) {
+#pragma clang fp contract(off)
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const int64_t i0 = bi * FIN_B, j0 = bj * FIN_B;
+  const bool two = i0 / syrk::TILE == j0 / syrk::TILE && bi != bj;  // both halves of a diagonal tile
+  // t[0][r][c] = acc[i0 + r][j0 + c]; t[1][r][c] = acc[j0 + r][i0 + c]; all
+  // of a thread's loads are issued before the first LDS store
+  constexpr int R = FIN_B / 4;
+  float u[R];
+#pragma unroll
+  for (int q = 0; q < R; ++q) {
+    const int64_t i = i0 + ty + 4 * q, j = j0 + tx;
+    u[q] = FULL || (i < k && j < k) ? a[i * lda + j] : 0.0f;
+  }
+  if (two) {
+    float l[R];
+#pragma unroll
+    for (int q = 0; q < R; ++q) {
+      const int64_t p = j0 + ty + 4 * q, c = i0 + tx;
+      l[q] = FULL || (p < k && c < k) ? a[p * lda + c] : 0.0f;
+    }
+#pragma unroll
+    for (int q = 0; q < R; ++q) t[1][ty + 4 * q][tx] = l[q];
+  }
+#pragma unroll
+  for (int q = 0; q < R; ++q) t[0][ty + 4 * q][tx] = u[q];
+  __syncthreads();
+  // block (bi, bj): element (i0 + r, j0 + tx)
+#pragma unroll
+  for (int q = 0; q < R; ++q) {
+    const int r = ty + 4 * q;
+    const float up = t[0][r][tx] * inv;
+    float v = up;
+    if (bi == bj) {
+      if (r != tx) v = (up + t[0][tx][r] * inv) * 0.5f;
+    } else if (two) {
+      v = (up + t[1][tx][r] * inv) * 0.5f;
+    }
+    if (FULL || (i0 + r < k && j0 + tx < k)) o[(i0 + r) * ldo + j0 + tx] = v;
+  }
+  if (bi == bj) return;
+  // mirror block (bj, bi): element (j0 + r, i0 + tx) from acc[i0 + tx][j0 + r]
+  // (averaged with acc[j0 + r][i0 + tx] inside a diagonal tile)
+#pragma unroll
+  for (int q = 0; q < R; ++q) {
+    const int r = ty + 4 * q;
+    const float up = t[0][tx][r] * inv;
+    const float v = two ? (up + t[1][r][tx] * inv) * 0.5f : up;
+    if (FULL || (j0 + r < k && i0 + tx < k)) o[(j0 + r) * ldo + i0 + tx] = v;
+  }
+}
+
+__device__ __forceinline__ void finalize_pair(const float* __restrict__ a, int64_t lda, int64_t k, float inv,
+                                              float* __restrict__ o, int64_t ldo, int64_t bi, int64_t bj,
+                                              float (*t)[FIN_B][FIN_B + 1]) {
+  if ((bj + 1) * FIN_B <= k)  // bi <= bj: the whole pair is inside the matrix
+    finalize_pair_impl<true>(a, lda, k, inv, o, ldo, bi, bj, t);
+  else
+    finalize_pair_impl<false>(a, lda, k, inv, o, ldo, bi, bj, t);
+}
+
+// block pair b of the upper triangle of nb x nb blocks -> (bi <= bj)
+__device__ __forceinline__ void finalize_pair_of(int64_t b, int64_t& bi, int64_t& bj) {
+  int64_t c = (int64_t)((sqrt(8.0 * (double)b + 1.0) - 1.0) * 0.5);
+  while (c * (c + 1) / 2 > b) --c;
+  while ((c + 1) * (c + 2) / 2 <= b) ++c;
+  bj = c;
+  bi = b - c * (c + 1) / 2;
+}
+
 __global__ __launch_bounds__(256) void syrk_finalize_kernel(
     const float* __restrict__ acc, int64_t ld_acc, int64_t k, float inv_denom,
     float* __restrict__ out, int64_t ld_out) {
-  const int64_t i = blockIdx.y;
-  const int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (j >= k) return;
-  // computed region: tile(i) <= tile(j); inside a diagonal tile both halves exist
-  const int64_t ti = i / syrk::TILE, tj = j / syrk::TILE;
-  const float v = ti <= tj ? acc[i * ld_acc + j] : acc[j * ld_acc + i];
-  out[i * ld_out + j] = v * inv_denom;
+  __shared__ float t[2][FIN_B][FIN_B + 1];
+  int64_t bi, bj;
+  finalize_pair_of(blockIdx.x, bi, bj);
+  finalize_pair(acc, ld_acc, k, inv_denom, out, ld_out, bi, bj, t);
 }
 
-// Symmetrize the diagonal tiles ((H + H^T) / 2 inside each diagonal tile, the
-// off-diagonal tiles are exact mirrors already) and add damp * mean(diag).
-// One workgroup: reduce the diagonal, then update it.
+// diag += damp * mean(diag).  One workgroup: reduce the diagonal, then
+// update it.
 __global__ __launch_bounds__(1024) void syrk_damp_kernel(float* __restrict__ out, int64_t ld_out,
                                                          int64_t k, float damp) {
   __shared__ float partial[1024];
@@ -1098,22 +1174,6 @@ __global__ __launch_bounds__(1024) void syrk_damp_kernel(float* __restrict__ out
   }
   const float add = damp * (partial[0] / (float)k);
   for (int64_t i = threadIdx.x; i < k; i += 1024) out[i * ld_out + i] += add;
-}
-
-// Inside diagonal tiles the two halves are computed by different lanes with
-// different summation orders; average them like kquant's (H + H^T) / 2.
-__global__ __launch_bounds__(256) void syrk_sym_diag_kernel(float* __restrict__ out, int64_t ld_out,
-                                                            int64_t k) {
-  const int64_t t = blockIdx.y;  // diagonal tile
-  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int64_t r = e / syrk::TILE, c = e % syrk::TILE;
-  if (r >= syrk::TILE || c <= r) return;
-  const int64_t i = t * syrk::TILE + r, j = t * syrk::TILE + c;
-  if (i >= k || j >= k) return;
-  const float a = out[i * ld_out + j], b = out[j * ld_out + i];
-  const float m = (a + b) * 0.5f;
-  out[i * ld_out + j] = m;
-  out[j * ld_out + i] = m;
 }
 
 // out = sym(lerp(A, B, alpha)) with A = a, or a_scale * I when a is null.
@@ -1186,32 +1246,17 @@ __global__ __launch_bounds__(256) void cov_stats_final_kernel(const double* __re
 }
 
 // Grouped finalize: out[g] = sym(acc[g]) / denominators[g] (zeros when the
-// group has no weight), blockIdx.z = group.
+// group has no weight), blockIdx.y = group.
 __global__ __launch_bounds__(256) void syrk_finalize_grouped_kernel(
     const float* __restrict__ acc, int64_t k, const double* __restrict__ denominators,
     float* __restrict__ out) {
-  const int64_t g = blockIdx.z, i = blockIdx.y;
-  const int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (j >= k) return;
+  __shared__ float t[2][FIN_B][FIN_B + 1];
+  const int64_t g = blockIdx.y;
   const double d = denominators[g];
   const float inv = d > 0.0 ? (float)(1.0 / d) : 0.0f;
-  const float* a = acc + g * k * k;
-  const int64_t ti = i / syrk::TILE, tj = j / syrk::TILE;
-  const float v = ti <= tj ? a[i * k + j] : a[j * k + i];
-  out[g * k * k + i * k + j] = v * inv;
-}
-
-__global__ __launch_bounds__(256) void syrk_sym_diag_grouped_kernel(float* __restrict__ out, int64_t k) {
-  const int64_t g = blockIdx.z, t = blockIdx.y;
-  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int64_t r = e / syrk::TILE, c = e % syrk::TILE;
-  if (r >= syrk::TILE || c <= r) return;
-  const int64_t i = t * syrk::TILE + r, j = t * syrk::TILE + c;
-  if (i >= k || j >= k) return;
-  float* o = out + g * k * k;
-  const float m = (o[i * k + j] + o[j * k + i]) * 0.5f;
-  o[i * k + j] = m;
-  o[j * k + i] = m;
+  int64_t bi, bj;
+  finalize_pair_of(blockIdx.x, bi, bj);
+  finalize_pair(acc + g * k * k, k, k, inv, out + g * k * k, k, bi, bj, t);
 }
 
 // Per-group f64 sums of the row weights (of their fp32 squares with
@@ -1406,19 +1451,17 @@ extern "C" int kq_syrk_finalize(const float* acc, int64_t ld_acc, int64_t k, dou
     return kq_fail(KQ_ERR_INVALID, "kq_syrk_finalize: bad sizes (k=%lld)", (long long)k);
   if (!(denominator > 0.0))
     return kq_fail(KQ_ERR_INVALID, "kq_syrk_finalize: denominator must be positive");
+  if (k > (int64_t)1 << 20)
+    return kq_fail(KQ_ERR_LIMIT, "kq_syrk_finalize: k=%lld exceeds 2^20", (long long)k);
   if (acc == out && ld_acc != ld_out)
     return kq_fail(KQ_ERR_INVALID, "kq_syrk_finalize: in-place needs ld_acc == ld_out");
   if (acc == out)
     return kq_fail(KQ_ERR_INVALID, "kq_syrk_finalize: acc and out must not alias");
   hipStream_t st = (hipStream_t)stream;
   const float inv = (float)(1.0 / denominator);
-  syrk_finalize_kernel<<<dim3((unsigned)((k + 255) / 256), (unsigned)k), 256, 0, st>>>(
-      acc, ld_acc, k, inv, out, ld_out);
+  const int64_t nb = (k + FIN_B - 1) / FIN_B;
+  syrk_finalize_kernel<<<(unsigned)(nb * (nb + 1) / 2), 256, 0, st>>>(acc, ld_acc, k, inv, out, ld_out);
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return kq_check_launch(e, "kq_syrk_finalize");
-  const unsigned nt = (unsigned)((k + syrk::TILE - 1) / syrk::TILE);
-  syrk_sym_diag_kernel<<<dim3((syrk::TILE * syrk::TILE + 255) / 256, nt), 256, 0, st>>>(out, ld_out, k);
-  e = hipGetLastError();
   if (e != hipSuccess) return kq_check_launch(e, "kq_syrk_finalize");
   if (damp != 0.0f) {
     syrk_damp_kernel<<<1, 1024, 0, st>>>(out, ld_out, k, damp);
@@ -1475,13 +1518,9 @@ extern "C" int kq_syrk_finalize_grouped(const float* acc, int64_t k, int groups,
   if (acc == out) return kq_fail(KQ_ERR_INVALID, "kq_syrk_finalize_grouped: acc and out must not alias");
   if (k > 65535) return kq_fail(KQ_ERR_LIMIT, "kq_syrk_finalize_grouped: k too large");
   hipStream_t st = (hipStream_t)stream;
-  syrk_finalize_grouped_kernel<<<dim3((unsigned)((k + 255) / 256), (unsigned)k, (unsigned)groups), 256, 0,
-                                 st>>>(acc, k, denominators, out);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return kq_check_launch(e, "kq_syrk_finalize_grouped");
-  const unsigned nt = (unsigned)((k + syrk::TILE - 1) / syrk::TILE);
-  syrk_sym_diag_grouped_kernel<<<dim3((syrk::TILE * syrk::TILE + 255) / 256, nt, (unsigned)groups), 256, 0,
-                                 st>>>(out, k);
+  const int64_t nb = (k + FIN_B - 1) / FIN_B;
+  syrk_finalize_grouped_kernel<<<dim3((unsigned)(nb * (nb + 1) / 2), (unsigned)groups), 256, 0, st>>>(
+      acc, k, denominators, out);
   return kq_check_launch(hipGetLastError(), "kq_syrk_finalize_grouped");
 }
 

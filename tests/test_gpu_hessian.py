@@ -373,3 +373,45 @@ def test_split_launch_matches_plain_launch(gpu, n, k):
     want = acc0[upper].double() + exact
     rel_acc = float(torch.linalg.vector_norm(acc[upper].double() - want) / torch.linalg.vector_norm(want))
     assert rel_acc <= TOL
+
+
+def _finalize_expected(acc: np.ndarray, k: int, inv: np.float32, tile: int = 128) -> np.ndarray:
+    """sym(acc) * inv from the computed region only: entries with
+    tile(i) <= tile(j) (128-wide tiles; a diagonal tile holds both halves),
+    the rest mirrored, each product rounded to fp32, and inside diagonal tiles
+    (H + H^T) / 2 of the scaled entries (kquant's symmetrisation)."""
+    a = acc[:k, :k].astype(np.float32)
+    t = np.arange(k) // tile
+    full = np.where(t[:, None] <= t[None, :], a, a.T)
+    v = (full * inv).astype(np.float32)
+    avg = ((v + v.T) * np.float32(0.5)).astype(np.float32)
+    return np.where(t[:, None] == t[None, :], avg, v)
+
+
+@pytest.mark.parametrize("k, ld", [(64, 64), (200, 208), (333, 340), (1000, 1000)])
+def test_finalize_is_bitwise_mirror_scale_average(gpu, k, ld):
+    """kq_syrk_finalize and kq_syrk_finalize_grouped on an accumulator whose
+    never-computed lower tiles hold NaN (they must not be read), widths that
+    end inside a 64-block and a 128-tile, a padded row stride, one group
+    without weight (zeros)."""
+    g = torch.Generator().manual_seed(k)
+    acc = torch.randn(ld, ld, generator=g, dtype=torch.float32) * 3.0
+    t = torch.arange(ld) // 128
+    acc[t[:, None] > t[None, :]] = float("nan")
+    denom = 7.25
+    out = torch.full((ld, ld), -1.0, device=gpu)
+    N.call("kq_syrk_finalize", N.ptr(acc.to(gpu)), ld, k, float(denom), 0.0, N.ptr(out), ld, N.stream(gpu))
+    want = _finalize_expected(acc.numpy(), k, np.float32(1.0 / denom))
+    got = out.cpu().numpy()
+    assert np.array_equal(got[:k, :k], want)
+    assert np.all(got[:k, k:] == -1.0) and np.all(got[k:, :] == -1.0)
+
+    accg = torch.stack([acc[:k, :k], acc[:k, :k] * 0.5, acc[:k, :k]]).contiguous().to(gpu)
+    dens = torch.tensor([denom, 3.0, 0.0], dtype=torch.float64, device=gpu)
+    outg = torch.empty_like(accg)
+    N.call("kq_syrk_finalize_grouped", N.ptr(accg), k, 3, N.ptr(dens), N.ptr(outg), N.stream(gpu))
+    outg = outg.cpu().numpy()
+    assert np.array_equal(outg[0], want)
+    assert np.array_equal(outg[1], _finalize_expected(accg[1].cpu().numpy(), k, np.float32(1.0 / 3.0)))
+    # no weight: acc * 0, i.e. zeros where acc is finite and NaN where it is not
+    assert np.array_equal(outg[2], _finalize_expected(acc.numpy(), k, np.float32(0.0)), equal_nan=True)
