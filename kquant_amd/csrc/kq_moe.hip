@@ -9,16 +9,20 @@
 //
 // Pipeline (all on one stream, all buffers in the caller's workspace):
 //   1. route_hist / route_scan / route_scatter: deterministic counting sort of
-//      the T*topk pairs by expert (stable in pair order), the list of experts
-//      with 1..16 pairs ("small") and the (expert, row-tile) list of the others.
+//      the T*topk pairs by expert (stable in pair order), each pair's sorted
+//      position, the list of experts with 1..16 pairs ("small") and the
+//      (expert, row-tile) list of the others.
 //   2. gate/up: small experts on a GEMV-shaped MFMA kernel (16 token slots,
 //      weights streamed once with 16-byte loads, K split over 8 waves);
 //      large experts on a persistent 256x256-tile grouped GEMM (gathered
 //      token rows and packed weights loaded straight into LDS).  Both fuse
 //      the activation and write bf16 intermediates in expert-sorted order.
-//   3. down: same two shapes over W2; the epilogue scales by the route weight
-//      and writes one fp32 row per pair.
-//   4. combine: out[t] = sum of the topk pair rows in slot order.
+//   3. down: same two shapes over W2; the epilogue writes one fp32 row per
+//      pair, in expert-sorted order (row = the pair's sorted position, so
+//      the epilogue needs no index or weight loads).
+//   4. combine: out[t] = sum over its slots, in slot order, of
+//      route_weight * the pair's row (each product rounded to fp32 before
+//      the sum, as when the down epilogue applied the weight).
 // No atomics touch floating-point data, so results are bitwise reproducible.
 #include "kq_dma.h"
 #include "kq_gemm.h"
@@ -44,7 +48,7 @@ constexpr int S_BYTES = BN * 2;
 constexpr int STAGE = A_BYTES + B_BYTES + S_BYTES;
 
 struct Layout {
-  size_t counts, offsets, block_counts, sorted, small_list, large_tiles, meta, act, y;
+  size_t counts, offsets, block_counts, sorted, pos, small_list, large_tiles, meta, act, y;
   size_t xq, xs, aq, as;  // MX-quantized tokens / intermediates (activation-quantized modes)
   size_t rank_of, routed, s13, s2;  // routed-expert ranks and expanded scale slots (X4T scales)
   size_t total;
@@ -72,6 +76,7 @@ static Layout make_layout(int64_t tokens, int topk, int experts, int64_t hidden,
   L.offsets = o;      o = align256(o + sizeof(int) * (experts + 1));
   L.block_counts = o; o = align256(o + sizeof(int) * (size_t)L.nblk * experts);
   L.sorted = o;       o = align256(o + sizeof(int) * (size_t)L.pairs);
+  L.pos = o;          o = align256(o + sizeof(int) * (size_t)L.pairs);
   L.small_list = o;   o = align256(o + sizeof(int) * 3 * (size_t)list_cap);
   L.large_tiles = o;  o = align256(o + sizeof(int) * 2 * (size_t)L.max_large);
   L.meta = o;         o = align256(o + sizeof(int) * 4);
@@ -237,7 +242,7 @@ __global__ __launch_bounds__(1024) void route_scan_kernel(
 
 __global__ __launch_bounds__(PREP) void route_scatter_kernel(
     const int* __restrict__ ids, int64_t pairs, int experts, const int* __restrict__ offsets,
-    const int* __restrict__ block_counts, int* __restrict__ sorted) {
+    const int* __restrict__ block_counts, int* __restrict__ sorted, int* __restrict__ pos) {
   __shared__ int ex[PREP];
   const int64_t p = (int64_t)blockIdx.x * PREP + threadIdx.x;
   int e = p < pairs ? ids[p] : -1;
@@ -247,7 +252,9 @@ __global__ __launch_bounds__(PREP) void route_scatter_kernel(
   if (e >= 0) {
     int rank = 0;
     for (int j = 0; j < (int)threadIdx.x; ++j) rank += ex[j] == e ? 1 : 0;
-    sorted[offsets[e] + block_counts[(int64_t)blockIdx.x * experts + e] + rank] = (int)p;
+    const int at = offsets[e] + block_counts[(int64_t)blockIdx.x * experts + e] + rank;
+    sorted[at] = (int)p;
+    if (pos) pos[p] = at;
   }
 }
 
@@ -258,7 +265,7 @@ __global__ __launch_bounds__(1024) void route_prep_one_kernel(
     const int* __restrict__ ids, int pairs, int experts, int* __restrict__ counts,
     int* __restrict__ offsets, int* __restrict__ sorted, int* __restrict__ small_list,
     int* __restrict__ large_tiles, int* __restrict__ meta, int max_large, int* __restrict__ rank_of,
-    int* __restrict__ routed, int max_routed, int bm) {
+    int* __restrict__ routed, int max_routed, int bm, int* __restrict__ pos) {
   __shared__ int s_cnt[MAX_EXPERTS];
   __shared__ int s_small[MAX_EXPERTS];
   __shared__ int s_tiles[MAX_EXPERTS];
@@ -309,6 +316,7 @@ __global__ __launch_bounds__(1024) void route_prep_one_kernel(
     int rank = 0;
     for (int j = 0; j < t; ++j) rank += s_ids[j] == my ? 1 : 0;
     sorted[s_cnt[my] + rank] = t;
+    if (pos) pos[t] = s_cnt[my] + rank;
   }
   for (int i = nsmall + t; i < experts; i += 1024) small_list[3 * i] = -1;
   if (t == 0) {
@@ -325,7 +333,7 @@ __global__ __launch_bounds__(1024) void route_prep_one_kernel(
 // (expert, first sorted position, count <= 16), one per 16 of its pairs.
 __global__ __launch_bounds__(DECODE_MAX_PAIRS) void route_decode_kernel(
     const int* __restrict__ ids, int pairs, int experts, int* __restrict__ sorted,
-    int* __restrict__ small_list, int max_list, int* __restrict__ meta) {
+    int* __restrict__ small_list, int max_list, int* __restrict__ meta, int* __restrict__ pos) {
   // ids past `pairs` are -1 and the loops run over whole groups of four
   // (one 16-byte LDS read each), so no read waits on the previous one
   __shared__ __attribute__((aligned(16))) int s_id[DECODE_MAX_PAIRS];
@@ -366,7 +374,10 @@ __global__ __launch_bounds__(DECODE_MAX_PAIRS) void route_decode_kernel(
       e0 += (v4[i] >= 0 && v4[i] < my) ? n4[i] : 0;
     }
   }
-  if (my >= 0) sorted[below + rank] = t;
+  if (my >= 0) {
+    sorted[below + rank] = t;
+    pos[t] = below + rank;
+  }
   if (first) {
     for (int q = 0; q < nent; ++q) {
       small_list[3 * (e0 + q)] = my;
@@ -549,7 +560,7 @@ __device__ __forceinline__ void x4t_finish(const X4TGemv& xg, int e, int64_t til
 // step count, so the compiler counts the outstanding loads exactly).
 //
 // GATEUP: rows of w13, output act -> bf16 intermediates.
-// !GATEUP: rows of w2, output route_weight * partial -> fp32 pair rows.
+// !GATEUP: rows of w2, output partial -> fp32 pair rows (sorted order).
 // ROUTE (a decode of at most DD_PAIRS pairs): no routing launch and no
 // list; workgroup x takes pair x alone (expert route.ids[x], one token slot)
 // and writes its intermediate to row x.  Each MFMA output row depends only on
@@ -712,8 +723,7 @@ __global__ __launch_bounds__(S * RW * 64) void moe_small_kernel(
         const float v = activate(act, x0[j], x1[j]);
         reinterpret_cast<__bf16*>(act_out)[(int64_t)(beg + slot) * inter + ch] = (__bf16)v;
       } else {
-        const int pair = sorted[beg + slot];
-        y_out[(int64_t)pair * hidden + ch] = route_w[pair] * x0[j];
+        y_out[(int64_t)(beg + slot) * hidden + ch] = x0[j];
       }
     }
   };
@@ -892,8 +902,7 @@ __global__ __launch_bounds__(S * RW * 64) void moe_small_mx_kernel(
         const float v = activate(act, x0[j], x1[j]);
         reinterpret_cast<__bf16*>(act_out)[(int64_t)(beg + slot) * inter + ch] = (__bf16)v;
       } else {
-        const int pair = sorted[beg + slot];
-        y_out[(int64_t)pair * hidden + ch] = route_w[pair] * x0[j];
+        y_out[(int64_t)(beg + slot) * hidden + ch] = x0[j];
       }
     }
   };
@@ -1076,12 +1085,10 @@ __global__ __launch_bounds__(512, 1) void moe_large_kernel(
             reinterpret_cast<__bf16*>(act_out)[(int64_t)(beg + slot) * inter + ch] = (__bf16)v;
         }
       } else {
-        const int pair = sorted[beg + slot];
-        const float rw = route_w[pair];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int64_t h = c0 + 2 * wn + j * 32 + frow;
-          if (h < hidden) y_out[(int64_t)pair * hidden + h] = rw * acc[i][j][r];
+          if (h < hidden) y_out[(int64_t)(beg + slot) * hidden + h] = acc[i][j][r];
         }
       }
     }
@@ -1332,12 +1339,10 @@ __global__ __launch_bounds__(512, 1) void moe_large_dma_kernel(
               reinterpret_cast<__bf16*>(act_out)[(int64_t)(beg + slot) * inter + ch] = (__bf16)v;
             }
           } else {
-            const int pair = sorted[beg + slot];
-            const float rw = route_w[pair];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
               const int64_t h = c0 + 2 * wn + j * 32 + frow;
-              y_out[(int64_t)pair * hidden + h] = rw * acc[i][j][r];
+              y_out[(int64_t)(beg + slot) * hidden + h] = acc[i][j][r];
             }
           }
         }
@@ -1587,12 +1592,10 @@ __global__ __launch_bounds__(512, 1) void moe_large_mx_kernel(
               reinterpret_cast<__bf16*>(act_out)[(int64_t)(beg + slot) * inter + ch] = (__bf16)v;
             }
           } else {
-            const int pair = sorted[beg + slot];
-            const float rw = route_w[pair];
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
               const int64_t h = c0 + 2 * wn + 16 * j + fm;
-              y_out[(int64_t)pair * hidden + h] = rw * acc[i][j][r];
+              y_out[(int64_t)(beg + slot) * hidden + h] = acc[i][j][r];
             }
           }
         }
@@ -1827,12 +1830,10 @@ __global__ __launch_bounds__(512, 1) void moe_large_mx4_kernel(
               reinterpret_cast<__bf16*>(act_out)[(int64_t)(beg + slot) * inter + ch] = (__bf16)v;
             }
           } else {
-            const int pair = sorted[beg + slot];
-            const float rw = route_w[pair];
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
               const int64_t h = c0 + 2 * wn + 16 * j + fm;
-              y_out[(int64_t)pair * hidden + h] = rw * acc[i][j][r];
+              y_out[(int64_t)(beg + slot) * hidden + h] = acc[i][j][r];
             }
           }
         }
@@ -1844,9 +1845,12 @@ __global__ __launch_bounds__(512, 1) void moe_large_mx4_kernel(
 // ---------------------------------------------------------------- combine --
 template <int OUT>
 __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restrict__ y,
+                                                          const int* __restrict__ pos,
+                                                          const float* __restrict__ route_w,
                                                           const int* __restrict__ ids, int topk,
                                                           int experts, int64_t hidden,
                                                           void* __restrict__ out) {
+#pragma clang fp contract(off)
   const int64_t t = blockIdx.y;
   const int64_t h4 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
   if (h4 >= hidden) return;
@@ -1854,7 +1858,10 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restric
   for (int k = 0; k < topk; ++k) {
     const int e = ids[t * topk + k];
     if (e < 0 || e >= experts) continue;
-    s += *reinterpret_cast<const f32x4_t*>(y + (t * topk + k) * hidden + h4);
+    // route weight x the pair's row (each product rounded), summed in slot order
+    const float rw = route_w[t * topk + k];
+    const f32x4_t v = *reinterpret_cast<const f32x4_t*>(y + (int64_t)pos[t * topk + k] * hidden + h4);
+    s += f32x4_t{rw * v[0], rw * v[1], rw * v[2], rw * v[3]};
   }
   if (OUT == 2) {
     *reinterpret_cast<f32x4_t*>(static_cast<float*>(out) + t * hidden + h4) = s;
@@ -2312,6 +2319,7 @@ static int moe_forward_impl(const char* fn, int activation, float act_beta, floa
   int* offsets = (int*)(w + L.offsets);
   int* block_counts = (int*)(w + L.block_counts);
   int* sorted = (int*)(w + L.sorted);
+  int* pos = (int*)(w + L.pos);  // sorted position of every routed pair: its row of y
   int* small_list = (int*)(w + L.small_list);
   int* large_tiles = (int*)(w + L.large_tiles);
   int* meta = (int*)(w + L.meta);
@@ -2342,13 +2350,13 @@ static int moe_forward_impl(const char* fn, int activation, float act_beta, floa
   const DecodeRouteArgs dra{route_ids, experts};
   if (decode && !route_in_gemv) {
     route_decode_kernel<<<1, DECODE_MAX_PAIRS, 0, st>>>(route_ids, (int)L.pairs, experts, sorted,
-                                                         small_list, (int)L.max_list, meta);
+                                                         small_list, (int)L.max_list, meta, pos);
     if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_moe_forward/route");
   } else if (decode) {
   } else if (L.pairs <= PREP_ONE) {
     route_prep_one_kernel<<<1, 1024, 0, st>>>(route_ids, (int)L.pairs, experts, counts, offsets,
                                                sorted, small_list, large_tiles, meta, (int)L.max_large,
-                                               rank_of, routed, max_routed, tile_rows);
+                                               rank_of, routed, max_routed, tile_rows, pos);
     if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_moe_forward/prep");
   } else {
     route_hist_kernel<<<(unsigned)L.nblk, PREP, 0, st>>>(route_ids, L.pairs, experts, block_counts);
@@ -2358,7 +2366,7 @@ static int moe_forward_impl(const char* fn, int activation, float act_beta, floa
                                           routed, max_routed, tile_rows);
     if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_moe_forward/scan");
     route_scatter_kernel<<<(unsigned)L.nblk, PREP, 0, st>>>(route_ids, L.pairs, experts, offsets,
-                                                            block_counts, sorted);
+                                                            block_counts, sorted, pos);
     if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_moe_forward/scatter");
   }
 
@@ -2376,9 +2384,9 @@ static int moe_forward_impl(const char* fn, int activation, float act_beta, floa
   auto combine = [&]() -> int {
     const dim3 cgrid((unsigned)((hidden / 4 + 255) / 256), (unsigned)tokens);
     if (out_dtype == KQ_DT_F32)
-      moe_combine_kernel<2><<<cgrid, 256, 0, st>>>(y, route_ids, topk, experts, hidden, out);
+      moe_combine_kernel<2><<<cgrid, 256, 0, st>>>(y, pos, route_weights, route_ids, topk, experts, hidden, out);
     else
-      moe_combine_kernel<0><<<cgrid, 256, 0, st>>>(y, route_ids, topk, experts, hidden, out);
+      moe_combine_kernel<0><<<cgrid, 256, 0, st>>>(y, pos, route_weights, route_ids, topk, experts, hidden, out);
     return kq_check_launch(hipGetLastError(), "kq_moe_forward/combine");
   };
 
@@ -2669,7 +2677,7 @@ extern "C" int kq_route_sort(const int32_t* route_ids, int64_t tokens, int topk,
   if (pairs <= PREP_ONE) {
     route_prep_one_kernel<<<1, 1024, 0, st>>>(route_ids, (int)pairs, experts, counts, off32, sorted,
                                                small_list, large_tiles, meta, max_large, nullptr, nullptr, 0,
-                                               BM);
+                                               BM, nullptr);
   } else {
     route_hist_kernel<<<(unsigned)nblk, PREP, 0, st>>>(route_ids, pairs, experts, block_counts);
     if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_route_sort");
@@ -2677,7 +2685,7 @@ extern "C" int kq_route_sort(const int32_t* route_ids, int64_t tokens, int topk,
                                           large_tiles, meta, max_large, nullptr, nullptr, 0, BM);
     if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_route_sort");
     route_scatter_kernel<<<(unsigned)nblk, PREP, 0, st>>>(route_ids, pairs, experts, off32,
-                                                          block_counts, sorted);
+                                                          block_counts, sorted, nullptr);
   }
   if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_route_sort");
   const int64_t n = pairs > experts + 1 ? pairs : experts + 1;
