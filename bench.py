@@ -560,9 +560,9 @@ def main() -> int:
                                            p_l * I * 2 + e_l * w2_b + p_l * H * 4),
             "combine": _traffic_entry("moe_prefill", "kq::moe::moe_combine_kernel",
                                       ids.numel() * (H * 4 + 8) + 8192 * H * 4),
-            "gateup_grouped_w4a4": _traffic_entry("moe_prefill", "kq::moe::moe_large_mx_kernel<true, 4>",
+            "gateup_grouped_w4a4": _traffic_entry("moe_prefill", "kq::moe::moe_large_mx4_kernel<true>",
                                                   p_l * (H // 2 + H // 32) + e_l * w13_b + p_l * I * 2),
-            "down_grouped_w4a4": _traffic_entry("moe_prefill", "kq::moe::moe_large_mx_kernel<false, 4>",
+            "down_grouped_w4a4": _traffic_entry("moe_prefill", "kq::moe::moe_large_mx4_kernel<false>",
                                                 p_l * (I // 2 + I // 32) + e_l * w2_b + p_l * H * 4),
             "gateup_grouped_w4a8": _traffic_entry("moe_prefill", "kq::moe::moe_large_mx_kernel<true, 0>",
                                                   p_l * (H + H // 32) + e_l * w13_b + p_l * I * 2),
