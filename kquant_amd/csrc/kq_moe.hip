@@ -1889,15 +1889,6 @@ __global__ __launch_bounds__(256) void route_rows_kernel(const int* __restrict__
   if (w_out) w_out[i] = pair_w[pair];
 }
 
-}  // namespace moe
-}  // namespace kq
-
-using namespace kq;
-using namespace kq::moe;
-
-// Pick the small-path instantiation for a reduction length K: 8 waves with a
-// compile-time step count when K is a multiple of 1024 (K/1024 steps of 128
-// per wave, 1..8), else 4 waves with a runtime loop (K % 512 == 0).
 // ------------------------------- decode down projection with the combine --
 // For at most DD_PAIRS pairs (one decode token at top-8): workgroup b owns
 // the 16 NBP output channels from 16 NBP b of every token and runs every
@@ -1923,7 +1914,7 @@ __global__ __launch_bounds__(DD_PAIRS * 2 * 64) void moe_decode_down_kernel(
     const uint16_t* __restrict__ act, int64_t inter, const int* __restrict__ ids, int topk, int experts,
     int tokens, const uint8_t* __restrict__ wt, const uint8_t* __restrict__ wst, int64_t hidden,
     const float* __restrict__ route_w, void* __restrict__ out, X4TGemv xg) {
-  constexpr int CH = 16 * NBP, NBUF = P + 1;
+  constexpr int CH = 16 * NBP, NBUF = P < STEPS ? P + 1 : STEPS;
   static_assert(STEPS > 0, "compile-time K steps");
   static_assert(!X4T || NBP == 2, "X4T: one 16-row scale tile per wave of a pair");
   __shared__ f32x4_t red[2 * DD_PAIRS][NBP][64];
@@ -1987,8 +1978,18 @@ __global__ __launch_bounds__(DD_PAIRS * 2 * 64) void moe_decode_down_kernel(
       }
     }
   };
+  // this wave's K half of its pair's intermediate row, staged in LDS once:
+  // every lane group of the MFMA A operand reads the same row, so the K
+  // loop reads A as LDS broadcasts and only weight loads are in flight
+  __shared__ __attribute__((aligned(16))) uint16_t arow[2 * DD_PAIRS][STEPS * 128];
   if (valid) {
     const int e = pe;
+    constexpr int APIECES = STEPS * 16, APL = (APIECES + 63) / 64;  // 16-byte pieces of a K half
+    const u32x4_t* asrc = reinterpret_cast<const u32x4_t*>(act + (int64_t)pair * inter + c_first * 128);
+    u32x4_t apc[APL];
+#pragma unroll
+    for (int i = 0; i < APL; ++i)
+      if (lane + 64 * i < APIECES) apc[i] = asrc[lane + 64 * i];
     const uint8_t* wtile[NBP];
     const uint8_t* stile[NBP];
 #pragma unroll
@@ -2002,9 +2003,6 @@ __global__ __launch_bounds__(DD_PAIRS * 2 * 64) void moe_decode_down_kernel(
       u32x4_t w[NBP];
       uint32_t ws[NBP];
     };
-    struct ABuf {
-      u32x4_t v[4];
-    };
     auto load_w = [&](int s, WBuf& B) {
 #pragma unroll
       for (int b = 0; b < NBP; ++b) {
@@ -2013,28 +2011,26 @@ __global__ __launch_bounds__(DD_PAIRS * 2 * 64) void moe_decode_down_kernel(
       }
     };
     WBuf wb[NBUF];
-    ABuf ab[NBUF];
 #pragma unroll
     for (int s = 0; s < P && s < STEPS; ++s) load_w(s, wb[s]);
     __builtin_amdgcn_sched_barrier(0);
     if (X4T) x4t_decode();
-    __builtin_amdgcn_sched_barrier(0);
-    // every token slot reads the pair's row; only slot 0 is stored
-    const uint16_t* ap = act + (int64_t)pair * inter + 32 * g;
-    auto load_a = [&](int s, ABuf& B) {
-      const int64_t c = c_first + s;
+    // one wave's LDS accesses complete in order: its K loop reads what it staged here
+    u32x4_t* al = reinterpret_cast<u32x4_t*>(&arow[wave][0]);
 #pragma unroll
-      for (int t = 0; t < 4; ++t) B.v[t] = *reinterpret_cast<const u32x4_t*>(ap + 128 * c + 8 * t);
-    };
+    for (int i = 0; i < APL; ++i)
+      if (lane + 64 * i < APIECES) al[lane + 64 * i] = apc[i];
+    __builtin_amdgcn_sched_barrier(0);
     // X4T: this pair's decoded tiles; row block b is tile c0 / 16 + b
     const uint8_t* xs = xsl + pair * 2 * (DD_X4T_COLS / 4) * 64 + c_first * 64 + lane;
-    auto compute = [&](const WBuf& W, const ABuf& A, int s) {
+    // every token slot (lane group) reads the pair's row; only slot 0 is stored
+    auto compute = [&](const WBuf& W, int s) {
       uint32_t ws[NBP];
 #pragma unroll
       for (int b = 0; b < NBP; ++b) ws[b] = X4T ? (uint32_t)xs[(b * (DD_X4T_COLS / 4) + s) * 64] : W.ws[b];
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        const bf16x8_t fa = __builtin_bit_cast(bf16x8_t, A.v[t]);
+        const bf16x8_t fa = __builtin_bit_cast(bf16x8_t, al[16 * s + 4 * g + t]);
 #pragma unroll
         for (int b = 0; b < NBP; ++b) {
           const bf16x8_t fb = gemm::dequant8<1>(u32x2_t{W.w[b][t], 0u}, ws[b]);
@@ -2042,18 +2038,13 @@ __global__ __launch_bounds__(DD_PAIRS * 2 * 64) void moe_decode_down_kernel(
         }
       }
     };
-#pragma unroll
-    for (int s = 0; s < P && s < STEPS; ++s) load_a(s, ab[s]);
     // X4T: both tiles of every pair decoded before any wave reads them
     if (X4T) lds_barrier();
 #pragma unroll
     for (int s = 0; s < STEPS; ++s) {
-      if (s + P < STEPS) {
-        load_w(s + P, wb[(s + P) % NBUF]);
-        load_a(s + P, ab[(s + P) % NBUF]);
-      }
+      if (s + P < STEPS) load_w(s + P, wb[(s + P) % NBUF]);
       __builtin_amdgcn_sched_barrier(0);
-      compute(wb[s % NBUF], ab[s % NBUF], s);
+      compute(wb[s % NBUF], s);
       __builtin_amdgcn_sched_barrier(0);
     }
   } else if (X4T) {
@@ -2092,6 +2083,12 @@ __global__ __launch_bounds__(DD_PAIRS * 2 * 64) void moe_decode_down_kernel(
   }
 }
 
+}  // namespace moe
+}  // namespace kq
+
+using namespace kq;
+using namespace kq::moe;
+
 // GEMV launch shapes (channels per workgroup = RW * 16 * NBP), measured on
 // the decode batches of 1, 4 and 16 tokens (hidden 7168, intermediate 2048):
 // K split over 4 waves for gate/up (14 steps of 128 each) and over 2 for down
@@ -2102,6 +2099,9 @@ __global__ __launch_bounds__(DD_PAIRS * 2 * 64) void moe_decode_down_kernel(
 #define KQ_GU_S 4
 #define KQ_GU_RW 1
 #define KQ_GU_P 2
+#endif
+#ifndef KQ_DD_P
+#define KQ_DD_P 2
 #endif
 #ifndef KQ_DN_NBP
 #define KQ_DN_NBP 4
@@ -2455,7 +2455,7 @@ static int moe_forward_impl(const char* fn, int activation, float act_beta, floa
     const bool f32 = out_dtype == KQ_DT_F32;
     const X4TGemv xg2 = x4t_gemv(xa, false);
 #define KQ_DD_LAUNCH(NS, OUTC, X)                                                                             \
-    moe_decode_down_kernel<2, 2, NS, OUTC, X><<<grid, DD_PAIRS * 2 * 64, 0, st>>>(                            \
+    moe_decode_down_kernel<2, KQ_DD_P, NS, OUTC, X><<<grid, DD_PAIRS * 2 * 64, 0, st>>>(                            \
         (const uint16_t*)act, inter, route_ids, topk, experts, (int)tokens, w2_t, w2_st, hidden, route_weights, \
         out, xg2)
 #define KQ_DD_CASE(NS)                                                                                        \
