@@ -70,7 +70,7 @@ __device__ __forceinline__ void quantize_qchunk(const QChunk<IN>& ch, int64_t bl
   amax = quad_max(amax);
 
   const float qmax = FMT == 0 ? 448.0f : 6.0f;
-  const int e = IN == 2 ? mx_block_exponent_f32_log2(amax, qmax) : mx_block_exponent(amax, qmax);
+  const int e = IN == 2 ? mx_block_exponent_f32_log2(amax, qmax) : mx_block_exponent<FMT>(amax);
   const uint32_t sbyte = (uint32_t)(e + 127);
   if (part == 0) out_scale[blk] = (uint8_t)sbyte;
 

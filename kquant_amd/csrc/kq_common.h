@@ -51,25 +51,29 @@ __device__ __forceinline__ float e8m0_to_f32(uint32_t b) {
   return __uint_as_float(bits);
 }
 
-// Block exponent e = clamp(ceil(log2(max(amax,1e-30)/qmax)), -127, 128).
-// q = fl(amax/qmax) is always a normal float here (amax >= 1e-30), so the
-// exact ceil(log2(q)) is its unbiased exponent plus one unless q is a power
-// of two.  For bf16 and fp16 inputs this equals the rounded torch.log2 result
-// (their amax/qmax quotients are never within log2-rounding of a power of two
-// without being one).
-__device__ __forceinline__ int mx_block_exponent(float amax, float qmax) {
-  float a = fmaxf(amax, 1e-30f);
-  float q = __fdiv_rn(a, qmax);
-  uint32_t bits = __float_as_uint(q);
-  int expo = (int)(bits >> 23) & 0xff;
-  int e = expo - 127 + ((bits & 0x7fffffu) != 0u ? 1 : 0);
-  if (expo == 0xff) e = 128;  // amax = +inf
-  e = e < -127 ? -127 : e;
-  e = e > 128 ? 128 : e;
-  return e;
+// Block exponent e = clamp(ceil(log2(max(amax,1e-30)/qmax)), -127, 128)
+// for bf16 and fp16 inputs (FMT 0: qmax = 448, FMT 1: qmax = 6), without the
+// division.  q = fl(a/qmax) is always a normal float here (a >= 1e-30), so
+// the exact ceil(log2(q)) is its unbiased exponent plus one unless q is a
+// power of two; for bf16 and fp16 inputs this equals the rounded torch.log2
+// result (their quotients are never within log2-rounding of a power of two
+// without being one).  With a = m 2^E (1 <= m < 2) and qmax = t 2^T (448 =
+// 1.75 2^8, 6 = 1.5 2^2): q = 2^(E-T) exactly when m = t; q lies strictly
+// between 2^(E-T) and 2^(E-T+1) when m > t, and strictly between 2^(E-T-1)
+// and 2^(E-T) when m < t, because such an m (at most 11 significant bits, or
+// the 1e-30 floor) differs from t by far more than the 2^-24 relative step of
+// the rounding.  Hence e = E - T + (m > t); infinity gives 128, and finite
+// values stay inside [-127, 128].
+template <int FMT>
+__device__ __forceinline__ int mx_block_exponent(float amax) {
+  const uint32_t bits = __float_as_uint(fmaxf(amax, 1e-30f));  // amax >= 0
+  const int expo = (int)(bits >> 23);
+  if (expo == 0xff) return 128;  // amax = +inf
+  const uint32_t t_frac = FMT == 0 ? 0x600000u : 0x400000u;
+  return expo - 127 - (FMT == 0 ? 8 : 2) + ((bits & 0x7fffffu) > t_frac ? 1 : 0);
 }
 
-// The same exponent for fp32 inputs, whose quotients can sit a few ulps above
+// The block exponent for fp32 inputs, whose quotients can sit a few ulps above
 // a power of two: kquant/mxfp8.py:41-43 takes torch.log2 in float32, which
 // rounds k + log2(1 + f) down to k when log2(1 + f) is below half an ulp of
 // k, so the reference keeps exponent k there and clamps the block's top

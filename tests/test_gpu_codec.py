@@ -63,6 +63,38 @@ def test_quantize_exhaustive_bf16(gpu, fmt, flags):
     assert np.array_equal(q, rq), f"code mismatches: {np.count_nonzero(q != rq)}"
 
 
+@pytest.mark.parametrize("fmt", ["mxfp8", "mxfp4"])
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_scale_of_every_finite_amax(gpu, fmt, dtype):
+    """Every finite bf16 / fp16 value (both signs) as the largest magnitude of
+    a block of its own: the block exponent is derived from the value's bits
+    (no division) and must match the oracle's fl(amax / qmax) exponent on each
+    one, including the values whose significand equals, or sits one step
+    above or below, that of qmax."""
+    if dtype == "bf16":
+        mags = cases.finite_bf16_patterns()
+        mags = mags[mags < 0x8000]
+    else:
+        mags = np.arange(0x7C00, dtype=np.uint16)  # +0 .. largest finite fp16
+    vals = np.concatenate([mags, mags | 0x8000])
+    blocks = np.zeros((vals.size, 32), np.uint16)
+    blocks[:, 0] = vals
+    blocks[:, 1] = ((vals & 0x7FFF) >> 1) | (vals & 0x8000)  # a second value of smaller magnitude
+    pad = (-blocks.shape[0]) % 8
+    blocks = np.concatenate([blocks, np.zeros((pad, 32), np.uint16)]).reshape(-1, 256)
+    print(f"case scale-of-every-amax {fmt} {dtype} blocks={blocks.size // 32}", flush=True)
+    if dtype == "bf16":
+        x = _bits_tensor(blocks, gpu)
+        rq, rs = oracle.mx_quantize(fmt, blocks, "bf16")
+    else:
+        h = blocks.view(np.float16)
+        x = torch.from_numpy(h.copy()).to(gpu)
+        rq, rs = oracle.mx_quantize(fmt, h, "f16")
+    q, s = _quantize(fmt, x)
+    assert np.array_equal(s, rs), f"scale mismatches: {np.count_nonzero(s != rs)}"
+    assert np.array_equal(q, rq), f"code mismatches: {np.count_nonzero(q != rq)}"
+
+
 @pytest.mark.parametrize("flags", [0, N.FLAG_SOFTWARE_CVT], ids=["hw", "sw"])
 def test_cfg1_mxfp4_roundtrip_bit_exact(gpu, flags):
     w = workloads.cfg1_weight()
