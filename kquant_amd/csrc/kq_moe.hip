@@ -561,16 +561,37 @@ __device__ __forceinline__ void x4t_finish(const X4TGemv& xg, int e, int64_t til
 //
 // GATEUP: rows of w13, output act -> bf16 intermediates.
 // !GATEUP: rows of w2, output partial -> fp32 pair rows (sorted order).
-// ROUTE (a decode of at most DD_PAIRS pairs): no routing launch and no
-// list; workgroup x takes pair x alone (expert route.ids[x], one token slot)
-// and writes its intermediate to row x.  Each MFMA output row depends only on
-// its own A row, so the values are those of the listed form; a pair whose
-// expert repeats reads that expert's weights again.  With X4T-coded scales
-// the workgroup decodes its expert's scale tiles as in the listed form.
+// ROUTE (a decode of at most 64 pairs): no routing launch and no list.  The
+// pairs routed to one expert, in pair order, form entries of up to
+// SMALL_MAX token slots as in the listed form; workgroup x runs the entry
+// that pair x starts (x's rank among its expert's pairs is a multiple of
+// SMALL_MAX) and exits otherwise, so every expert's weights are read once.
+// Slot m holds the entry's m-th pair, whose intermediate goes to row = pair
+// index.  Each MFMA output row depends only on its own A row, so the values
+// are those of the listed form.  With X4T-coded scales the workgroup decodes
+// its expert's scale tiles as in the listed form.
 struct DecodeRouteArgs {
   const int* ids;
   int experts;
+  int pairs;  // entries of ids (<= 64)
 };
+
+// Pair of token slot m (< SMALL_MAX) of the entry pair x starts among the
+// pairs routed to expert e (ids[0 .. pairs)), the entry's slot count in n;
+// -1 when x does not start an entry.  Every lane of a wave calls it.
+__device__ __forceinline__ int route_entry_slot(const int* __restrict__ ids, int pairs, int x, int e, int m,
+                                                int& n) {
+  const int lane = threadIdx.x & 63;
+  const int ej = lane < pairs ? ids[lane] : -1;
+  const uint64_t same = __ballot(ej == e);
+  const int rank = __popcll(same & ((1ull << x) - 1));
+  if (rank % SMALL_MAX != 0) return -1;
+  const int cnt = __popcll(same) - rank;
+  n = cnt < SMALL_MAX ? cnt : SMALL_MAX;
+  uint64_t mk = same;
+  for (int i = rank + (m < n ? m : 0); i > 0; --i) mk &= mk - 1;  // drop the lower set bits
+  return (int)__builtin_ctzll(mk);
+}
 
 template <bool GATEUP, bool X4T, int NBP, int S, int RW, int P, int STEPS, bool ROUTE = false>
 __global__ __launch_bounds__(S * RW * 64) void moe_small_kernel(
@@ -586,12 +607,13 @@ __global__ __launch_bounds__(S * RW * 64) void moe_small_kernel(
   static_assert(NB * 33 <= 128 * S, "fixed tiles of the row blocks: at most two 16-byte loads per thread");
   static_assert(!ROUTE || GATEUP, "per-pair decode: gate/up");
   extern __shared__ __attribute__((aligned(16))) unsigned char x4t_lds[];
-  int e, beg, n;
+  int e, beg, n, spair = 0;
   if constexpr (ROUTE) {
     e = route.ids[blockIdx.x];
     if (e < 0 || e >= route.experts) return;
-    beg = blockIdx.x;
-    n = 1;
+    spair = route_entry_slot(route.ids, route.pairs, (int)blockIdx.x, e, (int)(threadIdx.x & 15), n);
+    if (spair < 0) return;  // uniform: x does not start an entry
+    beg = 0;
   } else {
     e = small_list[3 * blockIdx.x];               // -1 past the last entry
     if (e < 0) return;
@@ -649,7 +671,7 @@ __global__ __launch_bounds__(S * RW * 64) void moe_small_kernel(
   // are never stored, so the duplicate needs no masking, and the loads stay
   // unconditional so the compiler keeps them in flight across steps.
   const int mslot = m < n ? m : 0;
-  const int apair = ROUTE ? (int)blockIdx.x : sorted[beg + mslot];
+  const int apair = ROUTE ? spair : sorted[beg + mslot];
   const int64_t arow = GATEUP ? (int64_t)(apair / topk) : (int64_t)(beg + mslot);
   const uint16_t* ap = a + arow * lda + 32 * g;
   auto load_a = [&](int s, ABuf& B) {
@@ -712,7 +734,11 @@ __global__ __launch_bounds__(S * RW * 64) void moe_small_kernel(
     }
   }
 
-  // D layout (16x16): lane holds rows (token slots) 4*(lane/16) + j, column lane % 16
+  // D layout (16x16): lane holds rows (token slots) 4*(lane/16) + j, column lane % 16.
+  // ROUTE: output row of slot 4 g + j = that slot's pair (lane 4 g + j holds it)
+  int orow[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) orow[j] = ROUTE ? __shfl(spair, 4 * g + j) : beg + 4 * g + j;
   auto store = [&](int u, f32x4_t x0, f32x4_t x1) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -721,7 +747,7 @@ __global__ __launch_bounds__(S * RW * 64) void moe_small_kernel(
       const int64_t ch = c0 + 16 * u + m;
       if (GATEUP) {
         const float v = activate(act, x0[j], x1[j]);
-        reinterpret_cast<__bf16*>(act_out)[(int64_t)(beg + slot) * inter + ch] = (__bf16)v;
+        reinterpret_cast<__bf16*>(act_out)[(int64_t)orow[j] * inter + ch] = (__bf16)v;
       } else {
         y_out[(int64_t)(beg + slot) * hidden + ch] = x0[j];
       }
@@ -2083,6 +2109,191 @@ __global__ __launch_bounds__(DD_PAIRS * 2 * 64) void moe_decode_down_kernel(
   }
 }
 
+// ------------------------ decode down projection with the combine, 9-32 pairs --
+// For a decode of up to DW_PAIRS pairs (dense scales, intermediate 1024 or
+// 2048): workgroup b owns output channels 32 b .. 32 b + 31 of every token.
+// The pairs routed to one expert form entries of up to SMALL_MAX token slots
+// exactly as the per-pair gate/up GEMV groups them; the work units are
+// (entry, K half), unit u = 2 entry + half, and wave w runs units w, w + 16,
+// ... back to back with the weight prefetch running across unit boundaries.
+// A unit is the listed down GEMV's work for that entry, half and channel
+// block: the same chunk order and MFMA order, the intermediates of every
+// pair staged in LDS once and read as the MFMA A operand.  The two halves of
+// a pair meet in LDS and are summed in the GEMV's order, scaled by the route
+// weight and summed over each token's slots in the combine's order, so the
+// output is bitwise that of the routing, listed down GEMV and combine
+// launches this one kernel replaces.
+constexpr int DW_PAIRS = 32;
+#ifndef KQ_DW_P
+#define KQ_DW_P 2
+#endif
+
+template <int STEPS, int OUT>
+__global__ __launch_bounds__(1024) void moe_decode_down_wide_kernel(
+    const uint16_t* __restrict__ act, int64_t inter, const int* __restrict__ ids, int topk, int experts,
+    int tokens, const uint8_t* __restrict__ wt, const uint8_t* __restrict__ wst, int64_t hidden,
+    const float* __restrict__ route_w, void* __restrict__ out) {
+#pragma clang fp contract(off)
+  constexpr int NBP = 2, CH = 16 * NBP, NBUF = 4, P = KQ_DW_P;
+  constexpr int KH = STEPS * 128;                  // k per half
+  constexpr int AROW = 2 * KH + 8;                 // bf16 per staged row: both halves + 16 B of pad
+  static_assert(STEPS % NBUF == 0, "ring slot of step s is s % NBUF in every unit");
+  __shared__ __attribute__((aligned(16))) uint16_t a_lds[DW_PAIRS][AROW];
+  __shared__ float yh[DW_PAIRS][2][CH];            // each pair's two K-half partials
+  __shared__ float ybuf[DW_PAIRS][CH];             // route weight x (half 0 + half 1)
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int m = lane & 15, g = lane >> 4;
+  const int pairs = tokens * topk;
+  const int64_t c0 = (int64_t)blockIdx.x * CH;
+  const int64_t nchunk = inter / 128, rgs = hidden / 16;
+
+  // entries: lane j < pairs holds pair j's expert (-1 if invalid) and its
+  // rank among the pairs of that expert; pair j starts an entry when the rank
+  // is a multiple of SMALL_MAX
+  int ej = lane < pairs ? ids[lane] : -1;
+  if (ej >= experts) ej = -1;
+  int rank = 0;
+  for (int i = 0; i < pairs; ++i) {
+    const int ei = __shfl(ej, i);
+    rank += (i < lane && ei == ej) ? 1 : 0;
+  }
+  const uint64_t starts = __ballot(ej >= 0 && rank % SMALL_MAX == 0);
+  const int units = 2 * __popcll(starts);
+
+  // stage every pair's intermediate row (rows = pair index, as the gate/up
+  // GEMV wrote them) with direct loads: 1 KiB of a row per instruction,
+  // instruction q = wave + 16 i moving KiB q % CPR of row q / CPR; they are
+  // issued before the weight prefetch and waited for after it
+  constexpr int CPR = 2 * KH * 2 / 1024;           // KiB per row
+  const dma::i32x4_t a_rsrc = dma::make_rsrc(act, (uint32_t)(pairs * inter * 2));
+  const uint32_t a_lds0 = dma::lds_offset_of(a_lds);
+  int staged = 0;                                  // this wave's direct loads
+  for (int q = wave; q < pairs * CPR; q += 16) {
+    const int pr = q / CPR, kb = q - pr * CPR;
+    dma::load_to_lds16(a_rsrc, (uint32_t)(pr * inter * 2 + kb * 1024 + 16 * lane),
+                       a_lds0 + (uint32_t)(pr * AROW * 2 + kb * 1024));
+    ++staged;
+  }
+
+  // unit u: entry u / 2 starts at the (u / 2)-th set bit of `starts`; its
+  // expert, slot count and this lane's slot pair (slot m; slot 0 past n)
+  struct Unit {
+    const uint8_t* w[NBP];
+    const uint8_t* s[NBP];
+    int half, n, spair;
+  };
+  auto setup = [&](int u, Unit& U) {
+    uint64_t st = starts;
+    for (int i = u >> 1; i > 0; --i) st &= st - 1;
+    const int x = (int)__builtin_ctzll(st);
+    const int e = __shfl(ej, x);
+    const uint64_t same = __ballot(ej == e);
+    const int r0 = __popcll(same & ((1ull << x) - 1));
+    const int cnt = __popcll(same) - r0;
+    U.n = cnt < SMALL_MAX ? cnt : SMALL_MAX;
+    uint64_t mk = same;
+    for (int i = r0 + (m < U.n ? m : 0); i > 0; --i) mk &= mk - 1;
+    U.spair = (int)__builtin_ctzll(mk);
+    U.half = u & 1;
+#pragma unroll
+    for (int b = 0; b < NBP; ++b) {
+      const int64_t t0 = ((int64_t)e * rgs + c0 / 16 + b) * nchunk + U.half * STEPS;
+      U.w[b] = wt + t0 * 1024 + 16 * lane;
+      U.s[b] = wst + t0 * 64 + lane;
+    }
+  };
+  struct WBuf {
+    u32x4_t w[NBP];
+    uint32_t ws[NBP];
+  };
+  auto load_w = [&](const Unit& U, int s, WBuf& B) {
+#pragma unroll
+    for (int b = 0; b < NBP; ++b) {
+      B.w[b] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(U.w[b] + (int64_t)s * 1024));
+      B.ws[b] = U.s[b][(int64_t)s * 64];
+    }
+  };
+  WBuf wb[NBUF];
+  Unit cur, nxt;
+  int u = wave;
+  if (u < units) {
+    setup(u, cur);
+#pragma unroll
+    for (int s = 0; s < P; ++s) load_w(cur, s, wb[s]);
+  }
+  // the staged rows have landed once only the (younger) weight prefetch is in
+  // flight: 2 P loads per block, or none without a unit
+  if (u < units) __builtin_amdgcn_s_waitcnt(dma::waitcnt_vm(2 * NBP * P));
+  else __builtin_amdgcn_s_waitcnt(dma::waitcnt_vm(0));
+  (void)staged;
+  lds_barrier();  // every wave's rows are staged
+  while (u < units) {
+    const int un = u + 16;
+    if (un < units) setup(un, nxt);
+    f32x4_t acc[NBP];
+#pragma unroll
+    for (int b = 0; b < NBP; ++b) acc[b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    const u32x4_t* arow = reinterpret_cast<const u32x4_t*>(&a_lds[cur.spair][cur.half * KH]);
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s) {
+      if (s + P < STEPS) load_w(cur, s + P, wb[(s + P) % NBUF]);
+      else if (un < units) load_w(nxt, s + P - STEPS, wb[(s + P) % NBUF]);
+      __builtin_amdgcn_sched_barrier(0);
+      const WBuf& W = wb[s % NBUF];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const bf16x8_t fa = __builtin_bit_cast(bf16x8_t, arow[16 * s + 4 * g + t]);
+#pragma unroll
+        for (int b = 0; b < NBP; ++b) {
+          const bf16x8_t fb = gemm::dequant8<1>(u32x2_t{W.w[b][t], 0u}, W.ws[b]);
+          acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa, fb, acc[b], 0, 0, 0);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // D layout: lane holds rows (slots) 4 g + j, column m
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int slot = 4 * g + j;
+      const int pr = __shfl(cur.spair, slot);
+      if (slot < cur.n) {
+#pragma unroll
+        for (int b = 0; b < NBP; ++b) yh[pr][cur.half][16 * b + m] = acc[b][j];
+      }
+    }
+    u = un;
+    cur = nxt;
+  }
+  lds_barrier();
+  for (int o = threadIdx.x; o < pairs * CH; o += 1024) {
+    const int pr = o / CH, c = o - pr * CH;
+    if (pr < pairs) {
+      const int e = ids[pr];
+      if (e >= 0 && e < experts) ybuf[pr][c] = route_w[pr] * (yh[pr][0][c] + yh[pr][1][c]);
+    }
+  }
+  lds_barrier();
+  // combine: two adjacent channels per thread, each token's slots in order
+  for (int o = threadIdx.x; o < tokens * (CH / 2); o += 1024) {
+    const int t = o / (CH / 2), c = 2 * (o % (CH / 2));
+    float s0 = 0.f, s1 = 0.f;
+    for (int k = 0; k < topk; ++k) {
+      const int e = ids[t * topk + k];
+      if (e < 0 || e >= experts) continue;
+      s0 += ybuf[t * topk + k][c];
+      s1 += ybuf[t * topk + k][c + 1];
+    }
+    if (OUT == 2) {
+      float* op = static_cast<float*>(out) + (int64_t)t * hidden + c0 + c;
+      op[0] = s0;
+      op[1] = s1;
+    } else {
+      *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(out) + (int64_t)t * hidden + c0 + c) =
+          f32x2_to_bf16x2_bits(s0, s1);
+    }
+  }
+}
+
 }  // namespace moe
 }  // namespace kq
 
@@ -2121,7 +2332,7 @@ static hipError_t launch_small(bool x4t, int64_t experts_max, int64_t channels, 
   const int64_t nchunk = K / 128;
   const int64_t steps = nchunk % S == 0 ? nchunk / S : 0;
   const size_t shm = x4t ? x4t_gemv_lds(RW * NB, nchunk, cols) : 0;
-  const DecodeRouteArgs none{nullptr, 0};
+  const DecodeRouteArgs none{nullptr, 0, 0};
   constexpr bool CAN_ROUTE = GATEUP;
   if (route && !CAN_ROUTE) return hipErrorInvalidValue;
   switch (steps) {
@@ -2344,10 +2555,13 @@ static int moe_forward_impl(const char* fn, int activation, float act_beta, floa
   // A decode of at most DD_PAIRS pairs with dense scales and bf16
   // activations needs no routing launch: one gate/up workgroup per pair, and
   // the down projection with the combine in one launch.
-  const bool route_in_gemv = decode && act_fmt < 0 && L.pairs <= DD_PAIRS && hidden % 32 == 0 &&
-                             (inter == 512 || inter == 1024 || inter == 2048 || inter == 4096) &&
-                             (!xa || inter / 32 <= DD_X4T_COLS);
-  const DecodeRouteArgs dra{route_ids, experts};
+  // decodes of at most DD_PAIRS pairs: per-pair gate/up + moe_decode_down_kernel;
+  // up to DW_PAIRS pairs with dense scales: per-pair gate/up + moe_decode_down_wide_kernel
+  const bool dd = L.pairs <= DD_PAIRS && (inter == 512 || inter == 1024 || inter == 2048 || inter == 4096) &&
+                  (!xa || inter / 32 <= DD_X4T_COLS);
+  const bool dw = !dd && L.pairs <= DW_PAIRS && !xa && (inter == 1024 || inter == 2048) && tokens <= 64;
+  const bool route_in_gemv = decode && act_fmt < 0 && hidden % 32 == 0 && (dd || dw);
+  const DecodeRouteArgs dra{route_ids, experts, (int)L.pairs};
   if (decode && !route_in_gemv) {
     route_decode_kernel<<<1, DECODE_MAX_PAIRS, 0, st>>>(route_ids, (int)L.pairs, experts, sorted,
                                                          small_list, (int)L.max_list, meta, pos);
@@ -2449,6 +2663,21 @@ static int moe_forward_impl(const char* fn, int activation, float act_beta, floa
     if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_moe_forward/gateup_large");
   }
   // down
+  if (route_in_gemv && dw) {
+    const dim3 grid((unsigned)(hidden / 32));
+    const bool f32 = out_dtype == KQ_DT_F32;
+#define KQ_DW_LAUNCH(NS, OUTC)                                                                                 \
+    moe_decode_down_wide_kernel<NS, OUTC><<<grid, 1024, 0, st>>>((const uint16_t*)act, inter, route_ids, topk,   \
+                                                                 experts, (int)tokens, w2_t, w2_st, hidden,      \
+                                                                 route_weights, out)
+    if (inter == 1024) {
+      if (f32) KQ_DW_LAUNCH(4, 2); else KQ_DW_LAUNCH(4, 0);
+    } else {
+      if (f32) KQ_DW_LAUNCH(8, 2); else KQ_DW_LAUNCH(8, 0);
+    }
+#undef KQ_DW_LAUNCH
+    return kq_check_launch(hipGetLastError(), "kq_moe_forward/decode_down_wide");
+  }
   if (route_in_gemv) {
     const int64_t steps = inter / 128 / 2;
     const dim3 grid((unsigned)(hidden / 32));

@@ -135,6 +135,51 @@ def test_per_pair_decode_matches_listed_path_bitwise(gpu, out_dtype, inter):
     assert torch.equal(again, fused)
 
 
+@pytest.mark.parametrize("inter", [1024, 2048])
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("T", [2, 4])
+def test_wide_decode_matches_listed_path_bitwise(gpu, T, out_dtype, inter):
+    """9 .. 32 pairs with dense scales also skip the routing launch: the
+    per-pair gate/up GEMV groups each expert's pairs into entries of up to 16
+    token slots itself, and one kernel runs the down projection of every
+    entry and the combine.  Bitwise against the routed-list path (the same
+    tokens with 5 more riding along, 72 pairs) and against the X4T-scale
+    forward (which keeps the listed path above 8 pairs): with one expert
+    taking all 8 slots of a token (and, at 4 tokens, 17 or more pairs in
+    all: two entries), experts repeated across tokens, invalid ids and a
+    token with no valid expert."""
+    k, E, H, I = 8, 8, 512, inter
+    g = torch.Generator().manual_seed(20 + T)
+    ids = torch.stack([torch.randperm(E, generator=g)[:k] for _ in range(T)]).to(torch.int32)
+    ids[0] = 1                                  # one expert in all 8 slots of token 0
+    ids[1, :3] = torch.tensor([1, -1, 99], dtype=torch.int32)
+    if T == 4:
+        ids[2, :] = 1                           # >= 17 pairs of expert 1: entries of 16 + the rest
+        ids[3, :] = torch.tensor([-1, -2, 8, 99, -1, 100, -7, 8], dtype=torch.int32)  # nothing valid
+    w = torch.rand(T, k, generator=g)
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    extra = 5
+    ids_l = torch.cat([ids, torch.randint(0, E, (extra, k), generator=g, dtype=torch.int32)])
+    w_l = torch.cat([w, torch.rand(extra, k, generator=g)])
+    x_l = torch.cat([x, torch.randn(extra, H, generator=g).to(torch.bfloat16)])
+    raw = workloads.quantized_experts(range(E), E, H, I, seed=6, device=gpu)
+    dense = moe.prepare_expert_weights(*raw)
+    x4t = moe.prepare_expert_weights(*raw, scale_format="x4t")
+    print(f"case wide decode T={T} inter={I} {out_dtype}", flush=True)
+    wide = moe.grouped_expert_forward(x.to(gpu), ids.to(gpu), w.to(gpu), dense, out_dtype=out_dtype)
+    listed = moe.grouped_expert_forward(x_l.to(gpu), ids_l.to(gpu), w_l.to(gpu), dense, out_dtype=out_dtype)[:T]
+    listed_x4t = moe.grouped_expert_forward(x.to(gpu), ids.to(gpu), w.to(gpu), x4t, out_dtype=out_dtype)
+    assert torch.equal(wide, listed)
+    assert torch.equal(wide, listed_x4t)
+    if T == 4:
+        assert torch.count_nonzero(wide[3]) == 0
+    valid = (ids >= 0) & (ids < E)
+    ref = _oracle(x, torch.where(valid, ids, torch.zeros_like(ids)), w * valid, raw, "situ")
+    assert _max_rel(ref, wide.float().cpu().numpy()) <= (TOL if out_dtype == torch.float32 else 2 ** -8)
+    again = moe.grouped_expert_forward(x.to(gpu), ids.to(gpu), w.to(gpu), dense, out_dtype=out_dtype)
+    assert torch.equal(again, wide)
+
+
 @pytest.mark.parametrize("tokens", [1, 4, 16])
 def test_decode_real_shapes(gpu, tokens):
     """Configuration 5: hidden 7168, intermediate 2048, 384 experts, top-8."""
