@@ -157,46 +157,152 @@ __device__ __forceinline__ float readlane_f(float v, int lane) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
 }
 
-// One wave factors the 64 x 64 block a (LDS; rows past the matrix padded with
-// the identity) into L, written back to a with zeros above the diagonal, and
-// writes inv(L) to xi.  Lane r holds row r in registers; column c is
-// broadcast from lane q with readlane, so each step is an FMA per row and
-// trailing column.  Entries above the diagonal take meaningless values in
-// registers and are never read.  inv(L): lane j solves column j by forward
-// substitution, the rows of L read as LDS broadcasts.  Returns (uniformly)
-// the first failing column + 1, or 0; a failing pivot is replaced by 1.
-__device__ __forceinline__ int factor64_wave(float (*a)[LD], float (*xi)[LD]) {
-  const int lane = threadIdx.x & 63;
-  float v[NB];
+// The workgroup's 256 threads (4 waves) factor the 64 x 64 block a (LDS;
+// rows past the matrix padded with the identity) into L, written back to a
+// with zeros above the diagonal, and write inv(L) to xi.  By 16-column
+// panels, right-looking; per panel:
+//  * wave 0 factors the 16 x 16 diagonal block: lane r holds row r, column
+//    c is broadcast from lane c with readlane, and each step takes the
+//    pivot's reciprocal square root (hardware v_rsq: within an ulp or two,
+//    far inside the factorization's own rounding), scales the column by it
+//    and updates the trailing columns with one FMA per entry; then lane j
+//    solves column j of the block's inverse X by forward substitution, the
+//    rows of L broadcast the same way;
+//  * the rows below take L21 = A21 X^T and the trailing lower tiles
+//    A22 -= L21 L21^T, both on v_mfma_f32_16x16x4f32, a 16 x 16 tile per
+//    wave.
+// The off-diagonal blocks of inv(L) follow by block rows i = 1, 2, 3:
+// X[i][j] = -X[i][i] (sum over k = j .. i - 1 of L[i][k] X[k][j]) on the
+// MFMAs, wave j taking block (i, j).  Returns (uniformly) the first failing
+// column + 1, or 0; a failing pivot is replaced by 1.  Ends with a barrier:
+// a and xi are complete for every thread.
+__device__ int factor64_wg(float (*a)[LD], float (*xi)[LD]) {
+  constexpr int PB = 16;  // panel width
+  __shared__ float tb[3][PB][PB + 1];
+  __shared__ float dg[2][PB];  // L[c][c] and 1 / L[c][c] of the current diagonal block
+  __shared__ int s_bad;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int li = lane & 15, lk = lane >> 4;  // v_mfma_f32_16x16x4f32 operand position
+  if (tid == 0) s_bad = 0;
+  // zeros above the diagonal blocks of xi (the blocks themselves are written whole)
+  for (int e = tid; e < NB * NB; e += 256) {
+    const int rr = e / NB, cc = e % NB;
+    if ((cc >> 4) > (rr >> 4)) xi[rr][cc] = 0.f;
+  }
+  __syncthreads();
+  for (int p = 0; p < NB / PB; ++p) {
+    const int c0 = PB * p;
+    if (wave == 0) {
+      float v[PB];
 #pragma unroll
-  for (int c = 0; c < NB; ++c) v[c] = a[lane][c];
-  int bad = 0;
+      for (int c = 0; c < PB; ++c) v[c] = a[c0 + li][c0 + c];
+      int bad = 0;
 #pragma unroll
-  for (int c = 0; c < NB; ++c) {
-    float d = readlane_f(v[c], c);
-    if (!(d > 0.f)) {
-      if (bad == 0) bad = c + 1;
-      d = 1.f;
+      for (int c = 0; c < PB; ++c) {
+        float d = readlane_f(v[c], c);
+        if (!(d > 0.f)) {
+          if (bad == 0) bad = c0 + c + 1;
+          d = 1.f;
+        }
+        const float rs = __builtin_amdgcn_rsqf(d);  // 1 / L[c][c]
+        dg[0][c] = d * rs;                          // L[c][c] (every lane stores the same value)
+        dg[1][c] = rs;
+        v[c] *= rs;  // L[r][c] for r > c (row c's diagonal is in dg)
+#pragma unroll
+        for (int q = c + 1; q < PB; ++q) v[q] = fmaf(-v[c], readlane_f(v[c], q), v[q]);
+      }
+      if (lane < PB) {
+        const float dv = dg[0][li];
+#pragma unroll
+        for (int c = 0; c < PB; ++c) a[c0 + li][c0 + c] = c < li ? v[c] : (c == li ? dv : 0.f);
+      }
+      // column li of the block's inverse: x[i] = (delta - sum_{k<i} L[i][k] x[k]) / L[i][i]
+      float x[PB];
+#pragma unroll
+      for (int i = 0; i < PB; ++i) {
+        float acc = i == li ? 1.f : 0.f;
+#pragma unroll
+        for (int k = 0; k < i; ++k) acc = fmaf(-readlane_f(v[k], i), x[k], acc);
+        x[i] = acc * dg[1][i];
+      }
+      if (lane < PB) {
+#pragma unroll
+        for (int i = 0; i < PB; ++i) xi[c0 + i][c0 + li] = x[i];
+      }
+      if (lane == 0 && bad != 0 && s_bad == 0) s_bad = bad;
     }
-    const float s = sqrtf(d);
-    v[c] = lane == c ? s : v[c] / s;
+    __syncthreads();
+    // the panel below: L21 = A21 X^T, row tile w (rows c0 + 16 (1 + w) ..) on wave w
+    const int nt = NB / PB - 1 - p;
+    f32x4_t l21 = {0.f, 0.f, 0.f, 0.f};
+    if (wave < nt) {
+      const int r0 = c0 + PB * (1 + wave);
 #pragma unroll
-    for (int q = c + 1; q < NB; ++q) v[q] = fmaf(-v[c], readlane_f(v[c], q), v[q]);
+      for (int k = 0; k < PB; k += 4)
+        l21 = __builtin_amdgcn_mfma_f32_16x16x4f32(a[r0 + li][c0 + k + lk], xi[c0 + li][c0 + k + lk], l21, 0, 0,
+                                                   0);
+    }
+    __syncthreads();  // every wave has read A21
+    if (wave < nt) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) a[c0 + PB * (1 + wave) + 4 * lk + j][c0 + li] = l21[j];
+    }
+    __syncthreads();
+    // trailing lower tiles (ti >= tj) -= L21[ti] L21[tj]^T
+    for (int t = wave; t < nt * (nt + 1) / 2; t += 4) {
+      int ti = 0;
+      while ((ti + 1) * (ti + 2) / 2 <= t) ++ti;
+      const int tj = t - ti * (ti + 1) / 2;
+      const int r0 = c0 + PB * (1 + ti), q0 = c0 + PB * (1 + tj);
+      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int k = 0; k < PB; k += 4)
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[r0 + li][c0 + k + lk], a[q0 + li][c0 + k + lk], acc, 0, 0, 0);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) a[r0 + 4 * lk + j][q0 + li] -= acc[j];
+    }
+    __syncthreads();
   }
-#pragma unroll
-  for (int c = 0; c < NB; ++c) a[lane][c] = c <= lane ? v[c] : 0.f;
-  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the rows are in LDS before the broadcast reads
-  float x[NB];
-#pragma unroll
-  for (int i = 0; i < NB; ++i) {
-    float acc = i == lane ? 1.f : 0.f;
-#pragma unroll
-    for (int k = 0; k < i; ++k) acc = fmaf(-a[i][k], x[k], acc);
-    x[i] = acc / a[i][i];
+  // zeros above the diagonal of L (the diagonal blocks' upper parts are zero already)
+  for (int e = tid; e < NB * NB; e += 256) {
+    const int rr = e / NB, cc = e % NB;
+    if ((cc >> 4) > (rr >> 4)) a[rr][cc] = 0.f;
   }
+  for (int i = 1; i < NB / PB; ++i) {
+    if (wave < i) {
+      const int j = wave;
+      // T = sum over k = j .. i - 1 of L[i][k] X[k][j]
+      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+      for (int k = j; k < i; ++k) {
 #pragma unroll
-  for (int i = 0; i < NB; ++i) xi[i][lane] = x[i];
-  return bad;
+        for (int u = 0; u < PB; u += 4)
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[PB * i + li][PB * k + u + lk],
+                                                     xi[PB * k + u + lk][PB * j + li], acc, 0, 0, 0);
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) tb[j][4 * lk + q][li] = acc[q];
+      // one wave's LDS accesses complete in order: the T it stored is read back below
+      f32x4_t x = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int u = 0; u < PB; u += 4)
+        x = __builtin_amdgcn_mfma_f32_16x16x4f32(xi[PB * i + li][PB * i + u + lk], tb[j][u + lk][li], x, 0, 0, 0);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) xi[PB * i + 4 * lk + q][PB * j + li] = -x[q];
+    }
+    __syncthreads();
+  }
+  return s_bad;
+}
+
+// Stores of factor64_wg's results by all 256 threads.
+__device__ __forceinline__ void store_diag_wg(float (*a)[LD], float (*xi)[LD], float* L, int64_t ldl, int64_t c0,
+                                              int nb, float* W, int bad, int* info) {
+  for (int i = threadIdx.x; i < NB * NB; i += 256) {
+    const int r = i / NB, c = i % NB;
+    if (r < nb && c < nb) L[(c0 + r) * ldl + c0 + c] = a[r][c];
+    W[i] = xi[r][c];
+  }
+  if (threadIdx.x == 0 && bad != 0 && *info == 0) *info = (int)(c0 + bad);
 }
 
 // L = tril(A) (upper part zero); info = 0.  a and l may be the same buffer.
@@ -213,35 +319,23 @@ __global__ __launch_bounds__(256) void chol_init_kernel(const float* a, int64_t 
 // (winv + (2 b + p % 2) 64 x 64): a launch reads one slot while its
 // diagonal-factoring workgroup writes the other.
 //
-// Factor the diagonal block of panel 0 (one wave per matrix; the later
+// Factor the diagonal block of panel 0 (one workgroup per matrix; the later
 // panels' diagonal blocks are factored by the launch that finishes them),
 // writing L11 back (zeros above its diagonal) and inv(L11) to slot 0.
-__device__ __forceinline__ void store_diag(float (*a)[LD], float (*xi)[LD], float* L, int64_t ldl, int64_t c0,
-                                           int nb, float* W, int bad, int* info) {
-  const int lane = threadIdx.x & 63;
-  for (int i = lane; i < NB * NB; i += 64) {
-    const int r = i / NB, c = i % NB;
-    if (r < nb && c < nb) L[(c0 + r) * ldl + c0 + c] = a[r][c];
-    W[i] = xi[r][c];
-  }
-  if (lane == 0 && bad != 0 && *info == 0) *info = (int)(c0 + bad);
-}
-
-__global__ __launch_bounds__(64) void chol_diag_kernel(float* __restrict__ l, int64_t n, int64_t ldl, int64_t sl,
-                                                       float* __restrict__ winv, int* __restrict__ info) {
+__global__ __launch_bounds__(256) void chol_diag_kernel(float* __restrict__ l, int64_t n, int64_t ldl, int64_t sl,
+                                                        float* __restrict__ winv, int* __restrict__ info) {
   __shared__ float a[NB][LD];
   __shared__ float xi[NB][LD];
   const int64_t b = blockIdx.x;
   float* L = l + b * sl;
   const int nb = (int)(n < NB ? n : NB);
-  for (int i = threadIdx.x; i < NB * NB; i += 64) {
+  for (int i = threadIdx.x; i < NB * NB; i += 256) {
     const int r = i / NB, c = i % NB;
     a[r][c] = (r < nb && c < nb) ? (c <= r ? L[r * ldl + c] : 0.f) : (r == c ? 1.f : 0.f);
   }
   __syncthreads();
-  const int bad = factor64_wave(a, xi);
-  __syncthreads();
-  store_diag(a, xi, L, ldl, 0, nb, winv + b * 2 * NB * NB, bad, info + b);
+  const int bad = factor64_wg(a, xi);
+  store_diag_wg(a, xi, L, ldl, 0, nb, winv + b * 2 * NB * NB, bad, info + b);
 }
 
 // acc (this wave's 32x32 of a 64x64 tile, as 2x2 16x16 blocks) += X Y^T over
@@ -378,12 +472,9 @@ __global__ __launch_bounds__(256) void chol_panel_kernel(float* __restrict__ l, 
         xi[r][c] = (r0 + r < n && r0 + c < n) ? L[(r0 + r) * ldl + r0 + c] - dg[bi][bj][q] : (r == c ? 1.f : 0.f);
       }
   __syncthreads();
-  if (wave == 0) {
-    const int bad = factor64_wave(xi, xj);
-    const int nb = (int)(n - r0 < NB ? n - r0 : NB);
-    __builtin_amdgcn_s_waitcnt(0xc07f);
-    store_diag(xi, xj, L, ldl, r0, nb, winv + (b * 2 + ((p + 1) & 1)) * NB * NB, bad, info + b);
-  }
+  const int bad = factor64_wg(xi, xj);
+  const int nb = (int)(n - r0 < NB ? n - r0 : NB);
+  store_diag_wg(xi, xj, L, ldl, r0, nb, winv + (b * 2 + ((p + 1) & 1)) * NB * NB, bad, info + b);
 }
 
 // Trailing update A[bi, bj] -= sum over panels q in [q0, q1) of
@@ -391,7 +482,7 @@ __global__ __launch_bounds__(256) void chol_panel_kernel(float* __restrict__ l, 
 // enumerates them row by row; the panels' products are summed in registers,
 // so A is read and written once).  The workgroup of tile (b0, b0) then
 // factors it as panel b0's diagonal block.
-__global__ __launch_bounds__(256) void chol_update_kernel(float* __restrict__ l, int64_t n, int64_t ldl, int64_t sl,
+__global__ __launch_bounds__(256, 4) void chol_update_kernel(float* __restrict__ l, int64_t n, int64_t ldl, int64_t sl,
                                                           int b0, int q0, int q1, float* __restrict__ winv,
                                                           int* __restrict__ info) {
   __shared__ float xi[NB][LD];
@@ -447,12 +538,9 @@ __global__ __launch_bounds__(256) void chol_update_kernel(float* __restrict__ l,
       }
   if (!next_diag) return;
   __syncthreads();
-  if (wave == 0) {
-    const int bad = factor64_wave(xi, xj);
-    const int nb = (int)(n - ri < NB ? n - ri : NB);
-    __builtin_amdgcn_s_waitcnt(0xc07f);
-    store_diag(xi, xj, L, ldl, ri, nb, winv + (b * 2 + (b0 & 1)) * NB * NB, bad, info + b);
-  }
+  const int bad = factor64_wg(xi, xj);
+  const int nb = (int)(n - ri < NB ? n - ri : NB);
+  store_diag_wg(xi, xj, L, ldl, ri, nb, winv + (b * 2 + (b0 & 1)) * NB * NB, bad, info + b);
 }
 
 // -------------------------------------------------------------- block LDL --
@@ -577,7 +665,7 @@ extern "C" int kq_cholesky(const float* a, int64_t lda, int64_t stride_a, float*
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return kq_check_launch(e, "kq_cholesky/init");
   const int m = (int)((n + NB - 1) / NB);
-  chol_diag_kernel<<<(unsigned)batch, 64, 0, st>>>(l, n, ldl, stride_l, winv, info);
+  chol_diag_kernel<<<(unsigned)batch, 256, 0, st>>>(l, n, ldl, stride_l, winv, info);
   if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_cholesky/diag");
   // Super-panels of `rank` panels: one launch per panel (its block column
   // brought up to date with the super-panel's earlier panels, the panel
