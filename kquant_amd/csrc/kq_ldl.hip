@@ -173,16 +173,37 @@ __device__ __forceinline__ float readlane_f(float v, int lane) {
 //    wave.
 // The off-diagonal blocks of inv(L) follow by block rows i = 1, 2, 3:
 // X[i][j] = -X[i][i] (sum over k = j .. i - 1 of L[i][k] X[k][j]) on the
-// MFMAs, wave j taking block (i, j).  Returns (uniformly) the first failing
+// MFMAs, one block per wave; rows 1 and 2 on waves 1 .. i while wave 0
+// factors the next diagonal block, row 3 after the last one.  Returns (uniformly) the first failing
 // column + 1, or 0; a failing pivot is replaced by 1.  Ends with a barrier:
 // a and xi are complete for every thread.
-__device__ int factor64_wg(float (*a)[LD], float (*xi)[LD]) {
+__device__ __forceinline__ int factor64_wg(float (*a)[LD], float (*xi)[LD]) {
   constexpr int PB = 16;  // panel width
   __shared__ float tb[3][PB][PB + 1];
   __shared__ float dg[2][PB];  // L[c][c] and 1 / L[c][c] of the current diagonal block
   __shared__ int s_bad;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int li = lane & 15, lk = lane >> 4;  // v_mfma_f32_16x16x4f32 operand position
+  // block (i, j) of inv(L), j < i, on the calling wave: X[i][j] = -X[i][i] T with
+  // T = sum over k = j .. i - 1 of L[i][k] X[k][j]
+  auto inv_block = [&](int i, int j) {
+    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+    for (int k = j; k < i; ++k) {
+#pragma unroll
+      for (int u = 0; u < PB; u += 4)
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[PB * i + li][PB * k + u + lk], xi[PB * k + u + lk][PB * j + li],
+                                                   acc, 0, 0, 0);
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) tb[j][4 * lk + q][li] = acc[q];
+    // one wave's LDS accesses complete in order: the T it stored is read back below
+    f32x4_t x = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < PB; u += 4)
+      x = __builtin_amdgcn_mfma_f32_16x16x4f32(xi[PB * i + li][PB * i + u + lk], tb[j][u + lk][li], x, 0, 0, 0);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) xi[PB * i + 4 * lk + q][PB * j + li] = -x[q];
+  };
   if (tid == 0) s_bad = 0;
   // zeros above the diagonal blocks of xi (the blocks themselves are written whole)
   for (int e = tid; e < NB * NB; e += 256) {
@@ -230,6 +251,9 @@ __device__ int factor64_wg(float (*a)[LD], float (*xi)[LD]) {
         for (int i = 0; i < PB; ++i) xi[c0 + i][c0 + li] = x[i];
       }
       if (lane == 0 && bad != 0 && s_bad == 0) s_bad = bad;
+    } else if (p >= 2 && wave < p) {
+      // meanwhile block row p - 1 of inv(L): its L blocks and X[p - 1][p - 1] are done
+      inv_block(p - 1, wave - 1);
     }
     __syncthreads();
     // the panel below: L21 = A21 X^T, row tile w (rows c0 + 16 (1 + w) ..) on wave w
@@ -268,29 +292,9 @@ __device__ int factor64_wg(float (*a)[LD], float (*xi)[LD]) {
     const int rr = e / NB, cc = e % NB;
     if ((cc >> 4) > (rr >> 4)) a[rr][cc] = 0.f;
   }
-  for (int i = 1; i < NB / PB; ++i) {
-    if (wave < i) {
-      const int j = wave;
-      // T = sum over k = j .. i - 1 of L[i][k] X[k][j]
-      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-      for (int k = j; k < i; ++k) {
-#pragma unroll
-        for (int u = 0; u < PB; u += 4)
-          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[PB * i + li][PB * k + u + lk],
-                                                     xi[PB * k + u + lk][PB * j + li], acc, 0, 0, 0);
-      }
-#pragma unroll
-      for (int q = 0; q < 4; ++q) tb[j][4 * lk + q][li] = acc[q];
-      // one wave's LDS accesses complete in order: the T it stored is read back below
-      f32x4_t x = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int u = 0; u < PB; u += 4)
-        x = __builtin_amdgcn_mfma_f32_16x16x4f32(xi[PB * i + li][PB * i + u + lk], tb[j][u + lk][li], x, 0, 0, 0);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) xi[PB * i + 4 * lk + q][PB * j + li] = -x[q];
-    }
-    __syncthreads();
-  }
+  // the last block row of inv(L)
+  if (wave < NB / PB - 1) inv_block(NB / PB - 1, wave);
+  __syncthreads();
   return s_bad;
 }
 
