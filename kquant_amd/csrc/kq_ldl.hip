@@ -676,11 +676,11 @@ extern "C" int kq_cholesky(const float* a, int64_t lda, int64_t stride_a, float*
   // below its diagonal block, and the next diagonal block factored), then one
   // rank-(64 rank) update of everything to the right, so the trailing matrix
   // is read and written once per super-panel.  Batches of 8 and more take
-  // four panels (48 matrices of n = 2048: 5.3 ms with two, 4.8 with four on MI355X); fewer
-  // matrices take one, the right-looking form, whose panel launches are too
-  // small to carry the column updates and diagonal factorizations on their
-  // critical path (one n = 7168 matrix: 7.6 ms with one panel, 7.8 with four).
-  const int rank = batch >= 8 ? 4 : 1;
+  // four panels, fewer matrices two, whose panel launches are too small to
+  // carry more column updates on the critical path (measured on MI355X: 48
+  // matrices of n = 2048 3.90 ms with four, 4.12 with two or eight; one
+  // n = 7168 matrix 5.21 ms with two, 5.31 with one, 5.51 with four).
+  const int rank = batch >= 8 ? 4 : 2;
   for (int s0 = 0; s0 < m; s0 += rank) {
     const int s1 = s0 + rank < m ? s0 + rank : m;
     for (int p = s0; p < s1 && p + 1 < m; ++p) {
