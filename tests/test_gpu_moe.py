@@ -180,6 +180,43 @@ def test_wide_decode_matches_listed_path_bitwise(gpu, T, out_dtype, inter):
     assert torch.equal(again, wide)
 
 
+@pytest.mark.parametrize("T", [1, 4])
+def test_decode_without_routing_launch_graph_replay(gpu, T):
+    """The decode paths without a routing launch (8 pairs: per-pair gate/up
+    + fused down; 32 pairs: grouped entries + the 9-32 pair down kernel)
+    captured in a HIP graph: replays with new routings, tokens and weights
+    copied into the captured inputs (eager work and synchronisation between
+    replays) each equal the eager forward bit for bit."""
+    k, E, H, I = 8, 16, 512, 1024
+    raw = workloads.quantized_experts(range(E), E, H, I, seed=9, device=gpu)
+    prep = moe.prepare_expert_weights(*raw)
+    g = torch.Generator().manual_seed(30 + T)
+
+    def routing():
+        ids = torch.stack([torch.randperm(E, generator=g)[:k] for _ in range(T)]).to(torch.int32)
+        if T > 1:
+            ids[1, 0] = ids[0, 0]  # an expert shared by two tokens
+        return ids.to(gpu), torch.rand(T, k, generator=g).to(gpu), torch.randn(T, H, generator=g).to(
+            torch.bfloat16).to(gpu)
+
+    s_ids, s_w, s_x = routing()
+    moe.grouped_expert_forward(s_x, s_ids, s_w, prep)  # warm the workspace outside capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        s_out = moe.grouped_expert_forward(s_x, s_ids, s_w, prep)
+    for rep in range(4):
+        ids, w, x = routing()
+        s_ids.copy_(ids)
+        s_w.copy_(w)
+        s_x.copy_(x)
+        graph.replay()
+        torch.cuda.synchronize()
+        want = moe.grouped_expert_forward(x, ids, w, prep)
+        torch.cuda.synchronize()
+        assert torch.equal(s_out, want), f"replay {rep}"
+
+
 @pytest.mark.parametrize("tokens", [1, 4, 16])
 def test_decode_real_shapes(gpu, tokens):
     """Configuration 5: hidden 7168, intermediate 2048, 384 experts, top-8."""
