@@ -394,8 +394,11 @@ int kq_blockwise_hadamard(float* x, int64_t rows, int64_t cols, int64_t ld, int6
  * (exl3_encoder_backend.py:325-330).  Only the lower triangle of A is read;
  * a == l (same ld and stride) factors in place.  info: batch int32 (device),
  * 0 on success, else the order of the first leading minor that is not
- * positive definite (LAPACK's convention; the factor is then meaningless).
- * workspace: kq_cholesky_workspace_size bytes.  n, batch <= 65535. */
+ * positive definite (LAPACK's convention; the factor is then meaningless);
+ * -1 if a bounded wait between workgroups of one launch ran out (an internal
+ * error; the factor is then meaningless).  workspace:
+ * kq_cholesky_workspace_size bytes, not shared by concurrent calls.
+ * n, batch <= 65535. */
 int64_t kq_cholesky_workspace_size(int64_t n, int64_t batch);
 int kq_cholesky(const float* a, int64_t lda, int64_t stride_a, float* l, int64_t ldl,
                 int64_t stride_l, int64_t n, int64_t batch, int32_t* info, void* workspace,

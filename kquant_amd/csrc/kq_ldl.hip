@@ -25,6 +25,7 @@
 //    factorization continues with pivot 1, so every launch still completes.
 //  * block LDL: every b x b diagonal block DL_i of L is inverted, each block
 //    column multiplied by its inverse and the diagonal blocks set to I.
+#include "kq_dma.h"
 #include "kq_hadamard.h"
 #include "kq_internal.h"
 
@@ -298,22 +299,30 @@ __device__ __forceinline__ int factor64_wg(float (*a)[LD], float (*xi)[LD]) {
   return s_bad;
 }
 
-// Stores of factor64_wg's results by all 256 threads.
+// Stores of factor64_wg's results by all 256 threads.  AGENT: inv(L) goes
+// out as agent-scope atomic stores (written through the XCD's L2), for
+// workgroups of the same launch on other XCDs.
+template <bool AGENT = false>
 __device__ __forceinline__ void store_diag_wg(float (*a)[LD], float (*xi)[LD], float* L, int64_t ldl, int64_t c0,
                                               int nb, float* W, int bad, int* info) {
   for (int i = threadIdx.x; i < NB * NB; i += 256) {
     const int r = i / NB, c = i % NB;
     if (r < nb && c < nb) L[(c0 + r) * ldl + c0 + c] = a[r][c];
-    W[i] = xi[r][c];
+    if (AGENT) __hip_atomic_store(W + i, xi[r][c], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else W[i] = xi[r][c];
   }
   if (threadIdx.x == 0 && bad != 0 && *info == 0) *info = (int)(c0 + bad);
 }
 
 // L = tril(A) (upper part zero); info = 0.  a and l may be the same buffer.
 __global__ __launch_bounds__(256) void chol_init_kernel(const float* a, int64_t lda, int64_t sa, float* l,
-                                                        int64_t ldl, int64_t sl, int64_t n, int* __restrict__ info) {
+                                                        int64_t ldl, int64_t sl, int64_t n, int* __restrict__ info,
+                                                        int* __restrict__ diag_done) {
   const int64_t b = blockIdx.z, i = blockIdx.y, j = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i == 0 && j == 0) info[b] = 0;
+  if (i == 0 && j == 0) {
+    info[b] = 0;
+    diag_done[b] = -1;
+  }
   if (j >= n) return;
   const float v = j <= i ? a[b * sa + i * lda + j] : 0.f;
   l[b * sl + i * ldl + j] = v;
@@ -488,7 +497,7 @@ __global__ __launch_bounds__(256) void chol_panel_kernel(float* __restrict__ l, 
 // factors it as panel b0's diagonal block.
 __global__ __launch_bounds__(256, 4) void chol_update_kernel(float* __restrict__ l, int64_t n, int64_t ldl, int64_t sl,
                                                           int b0, int q0, int q1, float* __restrict__ winv,
-                                                          int* __restrict__ info) {
+                                                          int* __restrict__ info, int* __restrict__ diag_done) {
   __shared__ float xi[NB][LD];
   __shared__ float xj[NB][LD];
   const int64_t b = blockIdx.y;
@@ -520,9 +529,9 @@ __global__ __launch_bounds__(256, 4) void chol_update_kernel(float* __restrict__
     __syncthreads();
     mm_nt(xi, xj, acc);
   }
-  const int wave = threadIdx.x >> 6;
   const bool next_diag = t == 0;  // tile (b0, b0): panel b0's diagonal block
-  if (next_diag) __syncthreads();  // every wave is done reading xi / xj
+  const bool panel = diag_done != nullptr && j == 0 && i > 0;  // fused: a tile of panel b0 below it
+  if (next_diag || panel) __syncthreads();  // every wave is done reading xi / xj
 #pragma unroll
   for (int bi = 0; bi < 2; ++bi)
 #pragma unroll
@@ -534,17 +543,66 @@ __global__ __launch_bounds__(256, 4) void chol_update_kernel(float* __restrict__
         const int64_t r = ri + lr, c = rj + lc;
         if (r < n && c < n) {
           const float v = av[bi][bj][q] - acc[bi][bj][q];
-          if (next_diag) xi[lr][lc] = v;
+          if (next_diag || panel) xi[lr][lc] = v;
           else L[r * ldl + c] = v;
         } else if (next_diag) {
           xi[lr][lc] = lr == lc ? 1.f : 0.f;
+        } else if (panel) {
+          xi[lr][lc] = 0.f;
         }
       }
-  if (!next_diag) return;
+  float* W = winv + (b * 2 + (b0 & 1)) * NB * NB;
+  if (next_diag) {
+    __syncthreads();
+    const int bad = factor64_wg(xi, xj);
+    const int nb = (int)(n - ri < NB ? n - ri : NB);
+    if (diag_done) {
+      // inv(L[b0][b0]) written through to where every XCD reads it, then the count
+      store_diag_wg<true>(xi, xj, L, ldl, ri, nb, W, bad, info + b);
+      __builtin_amdgcn_s_waitcnt(dma::waitcnt_vm(0));
+      __syncthreads();
+      if (threadIdx.x == 0) __hip_atomic_store(diag_done + b, b0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+      store_diag_wg(xi, xj, L, ldl, ri, nb, W, bad, info + b);
+    }
+    return;
+  }
+  if (!panel) return;
+  // L[b0 + i][b0] = A[b0 + i][b0] inv(L[b0][b0])^T once tile (b0, b0) of this
+  // launch is factored.  That workgroup (the launch's first) waits for nothing
+  // and precedes this one in every XCD's dispatch order, so the wait ends;
+  // it is bounded all the same (info = -1 if it ever ran out).
+  __shared__ int s_ok;
+  if (threadIdx.x == 0) {
+    int ok = 0;
+    for (int it = 0; it < (1 << 22); ++it) {
+      if (__hip_atomic_load(diag_done + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == b0) {
+        ok = 1;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(2);
+    }
+    if (!ok) __hip_atomic_store(info + b, -1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_ok = ok;
+  }
   __syncthreads();
-  const int bad = factor64_wg(xi, xj);
-  const int nb = (int)(n - ri < NB ? n - ri : NB);
-  store_diag_wg(xi, xj, L, ldl, ri, nb, winv + (b * 2 + (b0 & 1)) * NB * NB, bad, info + b);
+  // agent-scope loads read past the L2s, which may hold this slot's older contents
+  for (int e = threadIdx.x; e < NB * NB; e += 256)
+    xj[e / NB][e % NB] = __hip_atomic_load(W + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  f32x4_t lp[2][2] = {};
+  mm_nt(xi, xj, lp);
+#pragma unroll
+  for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+    for (int bj = 0; bj < 2; ++bj)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        int lr, lc;
+        mm_pos(bi, bj, q, lr, lc);
+        if (ri + lr < n && rj + lc < n) L[(ri + lr) * ldl + rj + lc] = lp[bi][bj][q];
+      }
+  (void)s_ok;
 }
 
 // -------------------------------------------------------------- block LDL --
@@ -645,7 +703,8 @@ extern "C" int kq_blockwise_hadamard(float* x, int64_t rows, int64_t cols, int64
 
 extern "C" int64_t kq_cholesky_workspace_size(int64_t n, int64_t batch) {
   if (n <= 0 || batch <= 0) return -1;
-  return batch * 2 * NB * NB * (int64_t)sizeof(float);  // two inv(L11) slots per matrix
+  // two inv(L11) slots per matrix, then a diagonal-block counter per matrix
+  return batch * 2 * NB * NB * (int64_t)sizeof(float) + (batch * (int64_t)sizeof(int) + 255) / 256 * 256;
 }
 
 extern "C" int kq_cholesky(const float* a, int64_t lda, int64_t stride_a, float* l, int64_t ldl, int64_t stride_l,
@@ -664,23 +723,42 @@ extern "C" int kq_cholesky(const float* a, int64_t lda, int64_t stride_a, float*
     return kq_fail(KQ_ERR_INVALID, "kq_cholesky: workspace too small");
   hipStream_t st = (hipStream_t)stream;
   float* winv = (float*)workspace;
+  int* diag_done = (int*)(winv + batch * 2 * NB * NB);
   chol_init_kernel<<<dim3((unsigned)((n + 255) / 256), (unsigned)n, (unsigned)batch), 256, 0, st>>>(
-      a, lda, stride_a, l, ldl, stride_l, n, info);
+      a, lda, stride_a, l, ldl, stride_l, n, info, diag_done);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return kq_check_launch(e, "kq_cholesky/init");
   const int m = (int)((n + NB - 1) / NB);
   chol_diag_kernel<<<(unsigned)batch, 256, 0, st>>>(l, n, ldl, stride_l, winv, info);
   if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_cholesky/diag");
-  // Super-panels of `rank` panels: one launch per panel (its block column
+  if (batch < 8) {
+    // Right-looking, one launch per panel after the first: update launch s
+    // applies panel s - 1 to the trailing matrix, factors diagonal block s
+    // (its first workgroup) and, in the workgroups of the tiles below that
+    // block, once it is factored, computes panel s itself (measured on
+    // MI355X: one n = 7168 matrix 4.93 ms, against 5.21 with separate panel
+    // launches and two-panel super-panels, 5.29 with one panel each; four
+    // matrices of n = 2048: 1.18 against 1.23 ms).
+    if (m > 1) {
+      chol_panel_kernel<<<dim3((unsigned)(m - 1), (unsigned)batch), 256, 0, st>>>(l, n, ldl, stride_l, 0, 0, 1,
+                                                                                 winv, info);
+      if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_cholesky/panel");
+    }
+    for (int s = 1; s < m; ++s) {
+      const int64_t q = m - s;
+      chol_update_kernel<<<dim3((unsigned)(q * (q + 1) / 2), (unsigned)batch), 256, 0, st>>>(
+          l, n, ldl, stride_l, s, s - 1, s, winv, info, diag_done);
+      if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_cholesky/update");
+    }
+    return KQ_OK;
+  }
+  // Super-panels of four panels: one launch per panel (its block column
   // brought up to date with the super-panel's earlier panels, the panel
   // below its diagonal block, and the next diagonal block factored), then one
-  // rank-(64 rank) update of everything to the right, so the trailing matrix
-  // is read and written once per super-panel.  Batches of 8 and more take
-  // four panels, fewer matrices two, whose panel launches are too small to
-  // carry more column updates on the critical path (measured on MI355X: 48
-  // matrices of n = 2048 3.90 ms with four, 4.12 with two or eight; one
-  // n = 7168 matrix 5.21 ms with two, 5.31 with one, 5.51 with four).
-  const int rank = batch >= 8 ? 4 : 2;
+  // rank-256 update of everything to the right, so the trailing matrix is
+  // read and written once per super-panel (measured on MI355X, 48 matrices
+  // of n = 2048: 3.90 ms with four panels, 4.12 with two or eight).
+  const int rank = 4;
   for (int s0 = 0; s0 < m; s0 += rank) {
     const int s1 = s0 + rank < m ? s0 + rank : m;
     for (int p = s0; p < s1 && p + 1 < m; ++p) {
@@ -690,8 +768,8 @@ extern "C" int kq_cholesky(const float* a, int64_t lda, int64_t stride_a, float*
     }
     if (s1 < m) {
       const int64_t q = m - s1;
-      chol_update_kernel<<<dim3((unsigned)(q * (q + 1) / 2), (unsigned)batch), 256, 0, st>>>(l, n, ldl, stride_l,
-                                                                                          s1, s0, s1, winv, info);
+      chol_update_kernel<<<dim3((unsigned)(q * (q + 1) / 2), (unsigned)batch), 256, 0, st>>>(
+          l, n, ldl, stride_l, s1, s0, s1, winv, info, nullptr);
       if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_cholesky/update");
     }
   }
