@@ -106,7 +106,9 @@ def test_x4t_moe_argument_errors_need_no_gpu():
 def test_ldl_argument_errors_need_no_gpu():
     lib = _native.library()
     fake = ctypes.c_void_p(256)  # never dereferenced: validation fails first
-    assert lib.kq_cholesky_workspace_size(7168, 1) == 2 * 64 * 64 * 4
+    # two 64 x 64 fp32 inverse slots per matrix, then one int counter per matrix (256-byte granules)
+    assert lib.kq_cholesky_workspace_size(7168, 1) == 2 * 64 * 64 * 4 + 256
+    assert lib.kq_cholesky_workspace_size(7168, 65) == 65 * 2 * 64 * 64 * 4 + 512
     assert lib.kq_block_ldl_workspace_size(2048, 16, 3) == 3 * 2048 * 16 * 4
     rc = lib.kq_cholesky(fake, 0, 0, fake, 0, 0, 0, 1, fake, fake, 1 << 20, None)
     assert rc == _native.KQ_ERR_INVALID
