@@ -484,10 +484,11 @@ int kq_qsrt_decode_states(const int16_t* states, int64_t k_tiles, int64_t n_tile
  * payload and labels must be 16-byte aligned (KQ_ERR_INVALID otherwise).
  * workspace: kq_qsrt_linear_workspace_size(rows, k_tiles, n_tiles) bytes
  * (may be 0), 256-byte aligned and zeroed before its first use with these
- * sizes; each call leaves its completion counters at zero again, so it
- * serves repeated calls of the same sizes (zero it again before other
- * sizes: the counters' place depends on them).  Calls sharing a workspace
- * must not overlap. */
+ * sizes; each call up to 32 rows leaves it zero again (its completion
+ * counters, and for one or two rows the K chunks' partial sums, which the
+ * last chunk's workgroup polls), so it serves repeated calls of the same
+ * sizes (zero it again before other sizes, and after a prefill-sized call,
+ * which uses it as scratch).  Calls sharing a workspace must not overlap. */
 int64_t kq_qsrt_linear_workspace_size(int64_t rows, int64_t k_tiles, int64_t n_tiles);
 int kq_qsrt_linear(const void* x, int x_dtype, int64_t rows, int64_t ldx, const int16_t* payload,
                    int64_t payload_words, int64_t k_tiles, int64_t n_tiles, int rate_axis,

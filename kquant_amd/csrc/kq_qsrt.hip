@@ -214,8 +214,12 @@ struct LinArgs {
   const float* svh;
   void* out;
   int64_t ldo;
-  float* partial;  // [chunks][m][N] when chunks > 1
-  int* counters;   // [row groups][n blocks], zero between calls
+  // when chunks > 1: the partials [chunks][m][N] and, for more than two
+  // rows per workgroup, completion counters [row groups][n blocks]; both are
+  // zero between calls (a polled partial is never stored as +0.0, see
+  // store_partial)
+  float* partial;
+  int* counters;
   int k_tiles, n_tiles, rate_n, kbw, chunks, x_dtype, out_dtype;
 };
 
@@ -371,6 +375,56 @@ __device__ __forceinline__ void column_sums(float (&acc)[M]) {
   }
 }
 
+// Cross-workgroup partial sums polled by their reader (one or two rows per
+// workgroup, where the sum is a few words per thread and its latency is what
+// counts): the buffer is zero between calls, a partial is stored with +0.0
+// replaced by -0.0, so a word that is still +0.0 has not been stored yet, and
+// the reader clears every word after reading.  A relaxed agent-scope atomic
+// store is written through the XCD's L2 to the memory-side coherence point
+// shared by all XCDs, and a relaxed agent-scope atomic load reads that point,
+// so the reader sees a word once its store has been performed there.
+// (-0.0 + x == x for every x other than +0.0, so the sums change at most in
+// the sign of a zero.)
+__device__ __forceinline__ void store_partial(float* p, float v) {
+  __hip_atomic_store(p, v == 0.f ? -0.f : v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ float load_partial(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ bool stored(float v) { return __float_as_uint(v) != 0u; }
+
+// words a thread polls at once (more cost instruction fetches at the tail)
+constexpr int POLL_BATCH = 2;
+// Upper bound of re-reads of a batch (each one a memory round trip after a
+// short sleep: well beyond a second) before the reader gives up and returns
+// NaN for the words still missing.
+constexpr int POLL_LIMIT = 1 << 20;
+
+// v[u] = p[(ch0 + u * STEP) * stride] for the chunks below `count`, once all
+// of them have been stored (NaN for a word still unstored after POLL_LIMIT
+// re-reads).
+template <int U, int STEP>
+__device__ __forceinline__ void poll_partials(const float* p, int64_t stride, int ch0, int count, float (&v)[U]) {
+#pragma unroll
+  for (int u = 0; u < U; ++u) v[u] = ch0 + u * STEP < count ? load_partial(p + (ch0 + u * STEP) * stride) : 1.f;
+  for (int it = 0;; ++it) {
+    bool ready = true;
+#pragma unroll
+    for (int u = 0; u < U; ++u) ready &= stored(v[u]);
+    if (ready) return;
+    if (it == POLL_LIMIT) break;
+    __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (!stored(v[u])) v[u] = load_partial(p + (ch0 + u * STEP) * stride);
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+    if (!stored(v[u])) v[u] = __builtin_nanf("");
+}
+
 // Stage this wave's tiles of k block kb of the kernel-argument matrix.
 __device__ __forceinline__ void stage_block(const LinArgs& a, const LinRecords& rec, int nb, int kb,
                                             uint32_t* stage, int wave, int lane) {
@@ -463,7 +517,15 @@ __global__ __launch_bounds__(LIN_THREADS) void linear_kernel(LinArgs a, LinRecor
   }
   __syncthreads();
 
+  // The K chunks of a column block meet in one workgroup, which sums the
+  // partials in chunk order.  One or two rows: the workgroup of the last
+  // chunk keeps its own partial in LDS and polls the others (it is the last
+  // of the block's workgroups in dispatch order, and they wait on nothing, so
+  // every one of them runs to its stores).  More rows: the last workgroup to
+  // finish, found by a completion counter.
+  constexpr bool POLLED = M <= 2;
   const int64_t col0 = (int64_t)nb * 128;
+  const bool reader = POLLED && chunk == a.chunks - 1;
   if (wave < mc) {
     const int m = wave;
     float v0 = yb[0][m][lane] + yb[1][m][lane];
@@ -473,58 +535,90 @@ __global__ __launch_bounds__(LIN_THREADS) void linear_kernel(LinArgs a, LinRecor
       v0 *= sv0;
       v1 *= sv1;
     }
+    float* p = a.partial + ((int64_t)chunk * a.m + m0 + m) * n_cols + col0;
     if (a.chunks == 1) {
       store_out(a.out, a.out_dtype, (m0 + m) * a.ldo + col0 + lane, v0);
       store_out(a.out, a.out_dtype, (m0 + m) * a.ldo + col0 + lane + 64, v1);
+    } else if (reader) {
+      yb[0][m][lane] = v0;  // this thread's own reads above
+      yb[0][m][lane + 64] = v1;
+    } else if (POLLED) {
+      store_partial(p + lane, v0);
+      store_partial(p + lane + 64, v1);
     } else {
-      float* p = a.partial + ((int64_t)chunk * a.m + m0 + m) * n_cols + col0;
       __hip_atomic_store(p + lane, v0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_store(p + lane + 64, v1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
   if (a.chunks == 1) return;
-
-  // The last chunk to finish this block sums every chunk's partial in order.
-  // Partials travel as agent-scope atomic stores and loads, which bypass the
-  // per-XCD L2s (written through / always missed), so no device-wide fence
-  // (an L2 writeback and invalidate per workgroup) is needed: every wave
-  // waits for its stores to complete before the barrier that precedes the
-  // counter increment, and the last workgroup reads after seeing the count.
-  __builtin_amdgcn_s_waitcnt(dma::waitcnt_vm(0));
-  __syncthreads();
-  int* counter = a.counters + (int64_t)blockIdx.y * n_blocks + nb;
-  if (tid == 0)
-    s_last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == a.chunks - 1;
-  __syncthreads();
-  if (!s_last) return;
-  // TPO adjacent threads per output, thread j of them summing chunks j,
-  // j + TPO, ... (loads issued together), then a fixed shuffle tree
   constexpr int TPO = LIN_THREADS / (M * 128) > 0 ? LIN_THREADS / (M * 128) : 1;
-  for (int o0 = 0; o0 < M * 128; o0 += LIN_THREADS / TPO) {
-    const int o = o0 + tid / TPO, j = tid % TPO, m = o >> 7, c = o & 127;
+  const int64_t stride = a.m * n_cols;
+
+  if constexpr (POLLED) {
+    if (!reader) return;
+    __syncthreads();
+    // TPO adjacent threads per output, thread j of them summing chunks j,
+    // j + TPO, ... in order (the last chunk from LDS), then a fixed shuffle
+    // tree; each word is polled until it has been stored
+    const int o = tid / TPO, j = tid % TPO, m = o >> 7, c = o & 127;
+    const float* p = a.partial + (m0 + m) * n_cols + col0 + c;
     float sum = 0.f;
     if (m < mc) {
-      const float* p = a.partial + (m0 + m) * n_cols + col0 + c;
-      const int64_t stride = a.m * n_cols;
-      int ch = j;
-      for (; ch + 3 * TPO < a.chunks; ch += 4 * TPO) {
-        float v[4];
+      for (int ch0 = j; ch0 < a.chunks; ch0 += POLL_BATCH * TPO) {
+        float v[POLL_BATCH];
+        poll_partials<POLL_BATCH, TPO>(p, stride, ch0, a.chunks - 1, v);
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
-          v[u] = __hip_atomic_load(p + (ch + u * TPO) * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        sum += v[0];
-        sum += v[1];
-        sum += v[2];
-        sum += v[3];
+        for (int u = 0; u < POLL_BATCH; ++u) {
+          const int ch = ch0 + u * TPO;
+          if (ch < a.chunks - 1) sum += v[u];
+          else if (ch == a.chunks - 1) sum += yb[0][m][c];
+        }
       }
-      for (; ch < a.chunks; ch += TPO)
-        sum += __hip_atomic_load(p + ch * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 #pragma unroll
     for (int sft = 1; sft < TPO; sft <<= 1) sum += __shfl_xor(sum, sft);
-    if (j == 0 && m < mc) store_out(a.out, a.out_dtype, (m0 + m) * a.ldo + col0 + c, sum);
+    if (m >= mc) return;
+    if (j == 0) store_out(a.out, a.out_dtype, (m0 + m) * a.ldo + col0 + c, sum);
+    // clear the words read (after every load: a wait for a load would also
+    // wait for the stores issued before it)
+    for (int ch = j; ch < a.chunks - 1; ch += TPO)
+      __hip_atomic_store(const_cast<float*>(p) + ch * stride, 0.f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  } else {
+    // Every wave waits for its partial stores to complete before the barrier
+    // that precedes the counter increment; the last workgroup reads after
+    // seeing the count.
+    __builtin_amdgcn_s_waitcnt(dma::waitcnt_vm(0));
+    __syncthreads();
+    int* counter = a.counters + (int64_t)blockIdx.y * n_blocks + nb;
+    if (tid == 0)
+      s_last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == a.chunks - 1;
+    __syncthreads();
+    if (!s_last) return;
+    // TPO adjacent threads per output, thread j of them summing chunks j,
+    // j + TPO, ... (loads issued together), then a fixed shuffle tree
+    for (int o0 = 0; o0 < M * 128; o0 += LIN_THREADS / TPO) {
+      const int o = o0 + tid / TPO, j = tid % TPO, m = o >> 7, c = o & 127;
+      float sum = 0.f;
+      if (m < mc) {
+        const float* p = a.partial + (m0 + m) * n_cols + col0 + c;
+        int ch = j;
+        for (; ch + 3 * TPO < a.chunks; ch += 4 * TPO) {
+          float v[4];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) v[u] = load_partial(p + (ch + u * TPO) * stride);
+          sum += v[0];
+          sum += v[1];
+          sum += v[2];
+          sum += v[3];
+        }
+        for (; ch < a.chunks; ch += TPO) sum += load_partial(p + ch * stride);
+      }
+#pragma unroll
+      for (int sft = 1; sft < TPO; sft <<= 1) sum += __shfl_xor(sum, sft);
+      if (j == 0 && m < mc) store_out(a.out, a.out_dtype, (m0 + m) * a.ldo + col0 + c, sum);
+    }
+    if (tid == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  if (tid == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 
@@ -1066,7 +1160,8 @@ struct LinPlan {
 // when K is split (ties to the larger chunk: fewer partials to sum).  Costs
 // in units of one k block of one workgroup (measured: about 1.3 us; a
 // workgroup's fixed part, launch to last store, about 4 us; a
-// cross-workgroup sum about 2.7 us).
+// cross-workgroup sum about 2.7 us through the completion counter, about
+// 1.8 us polled).
 constexpr int LIN_FIXED_KB = 3;
 constexpr int LIN_REDUCE_KB = 2;
 hipError_t lin_plan(int64_t m, int64_t k_tiles, int64_t n_tiles, LinPlan* p) {
@@ -1093,8 +1188,11 @@ hipError_t lin_plan(int64_t m, int64_t k_tiles, int64_t n_tiles, LinPlan* p) {
       p->chunks = (int)chunks;
     }
   }
-  p->counters_bytes = (p->chunks > 1 ? (int64_t)p->groups * n_blocks * 4 + 255 : 0) / 256 * 256;
-  p->partial_bytes = p->chunks > 1 ? (int64_t)p->chunks * m * n_tiles * TILE * 4 : 0;
+  // one or two rows per workgroup: partials of every chunk but the last,
+  // polled by the last chunk's workgroup; more: every chunk's, and counters
+  const bool polled = p->mt <= 2;
+  p->counters_bytes = p->chunks > 1 && !polled ? ((int64_t)p->groups * n_blocks * 4 + 255) / 256 * 256 : 0;
+  p->partial_bytes = p->chunks > 1 ? (int64_t)(p->chunks - (polled ? 1 : 0)) * m * n_tiles * TILE * 4 : 0;
   return hipSuccess;
 }
 
@@ -1263,7 +1361,7 @@ extern "C" int kq_qsrt_linear(const void* x, int x_dtype, int64_t m, int64_t ldx
   a.svh = svh;
   a.out = out;
   a.ldo = ldo;
-  a.counters = need > 0 ? static_cast<int*>(workspace) : nullptr;
+  a.counters = p.counters_bytes > 0 ? static_cast<int*>(workspace) : nullptr;
   a.partial = need > 0 ? reinterpret_cast<float*>(static_cast<char*>(workspace) + p.counters_bytes) : nullptr;
   a.k_tiles = (int)k_tiles;
   a.n_tiles = (int)n_tiles;

@@ -180,8 +180,8 @@ def _check_record_count(bits: bytes, k_tiles: int, n_tiles: int, rate_axis: str)
 
 def _workspace(cache: dict, key: tuple, nbytes: int, gpu: torch.device) -> torch.Tensor:
     """A zeroed workspace per (device, stream, geometry): the fused kernels'
-    completion counters return to zero after every call, but calls on two
-    streams must not share them."""
+    completion counters and polled partial sums return to zero after every
+    call, but calls on two streams must not share them."""
     ws = cache.get(key)
     if ws is None:
         ws = torch.zeros(max(nbytes, 1), dtype=torch.uint8, device=gpu)
@@ -243,7 +243,7 @@ def qsrt_linear_launcher(
     need = int(N.library().kq_qsrt_linear_workspace_size(max(m, 1), k_tiles, n_tiles)) if m else 0
     if need < 0:
         raise RuntimeError("kq_qsrt_linear_workspace_size: no HIP device")
-    ws = torch.zeros(need, dtype=torch.uint8, device=gpu) if need else None  # counters start (and stay) at zero
+    ws = torch.zeros(need, dtype=torch.uint8, device=gpu) if need else None  # starts (and stays) zero
     args = (N.ptr(x), N.DTYPE_CODES[x.dtype], m, x.stride(0) if m else k, N.ptr(payload), payload.numel(),
             k_tiles, n_tiles, 0 if rate_axis == "k" else 1, bits, N.ptr(labels), N.ptr(su), N.ptr(sv),
             N.DTYPE_CODES[out.dtype], N.ptr(out), out.stride(0) if m else n, N.ptr(ws), need)
@@ -314,7 +314,7 @@ def qsrt_linear(
     if not need:
         ws = None
     elif m <= FUSED_MAX_ROWS:
-        # the fused kernel's completion counters: zeroed once, back at zero after every call
+        # the fused kernel's counters and polled partials: zeroed once, back at zero after every call
         ws = _workspace(_LINEAR_WORKSPACES, (gpu, stream.value, m, k_tiles, n_tiles), need, gpu)
     else:
         # the prefill form keeps no state between calls: a buffer from torch's

@@ -95,8 +95,8 @@ def test_rotated_product_matches_oracle(gpu, rate_axis, m, shape, record_bits):
 
 def test_matches_decode_then_matmul_and_reuses_workspace(gpu):
     """Kimi-K3 w1 geometry (EXL [K=3584, N=3072], 24 records along n):
-    several calls in a row, shrinking and growing, share the workspace whose
-    completion counters every call leaves at zero."""
+    several calls in a row, shrinking and growing, each with the workspace
+    that calls of its row count share (left zero by every call)."""
     k_tiles, n_tiles = 224, 192
     record_bits = (2, 4) * 2 + (3,) * 20
     g = torch.Generator(device=gpu).manual_seed(3)
@@ -150,6 +150,50 @@ def test_launcher_in_a_graph_replays_the_eager_result(gpu):
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, eager), i
+
+
+@pytest.mark.parametrize("m", [1, 2])
+def test_polled_partials_start_every_call_from_zero(gpu, m):
+    """One or two rows: the K chunks' partials are polled by the last chunk's
+    workgroup, in a workspace that each call must leave zero.  28 chunks of
+    one k block each; calls with different rows in a row (eager and graph
+    replays with new rows copied in) each match their own product, a repeat
+    of the first rows matches it bit for bit, and zero rows give +0.0
+    everywhere (a partial is stored as -0.0 when it is zero)."""
+    k_tiles, n_tiles = 224, 16
+    record_bits = (3, 2)
+    payload = torch.from_numpy(_random_matrix(k_tiles, n_tiles, "n", record_bits, 61)).to(gpu)
+    suh, svh = (torch.from_numpy(v).to(gpu) for v in _scales(k_tiles, n_tiles, 62))
+    args = dict(k_tiles=k_tiles, n_tiles=n_tiles, rate_axis="n", record_bits=record_bits, suh=suh, svh=svh)
+    w = qsrt.decode_qsrt_payload(payload, **args).double()
+    g = torch.Generator(device=gpu).manual_seed(63 + m)
+    xs = [torch.randn(m, k_tiles * 16, generator=g, device=gpu) for _ in range(3)]
+
+    def check(got, x):
+        ref = x.double() @ w
+        assert (got.double() - ref).abs().max().item() <= 4e-6 * ref.abs().max().item()
+
+    first = qsrt.qsrt_linear(xs[0], payload, **args)
+    check(first, xs[0])
+    check(qsrt.qsrt_linear(xs[1], payload, **args), xs[1])
+    assert torch.equal(qsrt.qsrt_linear(xs[0], payload, **args), first)
+    zero = qsrt.qsrt_linear(torch.zeros(m, k_tiles * 16, device=gpu), payload, **args)
+    assert torch.equal(zero, torch.zeros_like(zero)) and not torch.signbit(zero).any()
+
+    xin = xs[0].clone()
+    out = torch.empty_like(first)
+    run = qsrt.qsrt_linear_launcher(xin, payload, out, **args)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        run()
+    for i, x in enumerate(xs + xs[:1]):
+        xin.copy_(x)
+        qsrt.qsrt_linear(xs[2][:1], payload, **args)  # eager work sharing nothing with the graph
+        graph.replay()
+        torch.cuda.synchronize()
+        check(out, x)
+        if i == 3:
+            assert torch.equal(out, first)
 
 
 def test_every_finite_e4m3_label_converts_exactly(gpu):
