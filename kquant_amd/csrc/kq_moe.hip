@@ -2123,24 +2123,36 @@ __global__ __launch_bounds__(DD_PAIRS * 2 * 64) void moe_decode_down_kernel(
 // weight and summed over each token's slots in the combine's order, so the
 // output is bitwise that of the routing, listed down GEMV and combine
 // launches this one kernel replaces.
+// X4T: the w2 scales stay X4T-coded.  A unit's wave decodes the scale bytes
+// of its K half of the two 16-row scale tiles into its own LDS region in the
+// dense tiles' per-step order (row bases and selector bits, then the tiles'
+// exceptions in that half); the fixed bytes and the first 64 exception words
+// of the next unit are loaded at its setup, while the current unit runs, and
+// the region is rewritten after the current unit's last read of it (one
+// wave's LDS accesses complete in order).  The bytes are those of the dense
+// scale tiles, so the output is bitwise that of the dense-scale form.
 constexpr int DW_PAIRS = 32;
 #ifndef KQ_DW_P
 #define KQ_DW_P 2
 #endif
 
-template <int STEPS, int OUT>
+template <int STEPS, int OUT, bool X4T = false>
 __global__ __launch_bounds__(1024) void moe_decode_down_wide_kernel(
     const uint16_t* __restrict__ act, int64_t inter, const int* __restrict__ ids, int topk, int experts,
     int tokens, const uint8_t* __restrict__ wt, const uint8_t* __restrict__ wst, int64_t hidden,
-    const float* __restrict__ route_w, void* __restrict__ out) {
+    const float* __restrict__ route_w, void* __restrict__ out, X4TGemv xg) {
 #pragma clang fp contract(off)
   constexpr int NBP = 2, CH = 16 * NBP, NBUF = 4, P = KQ_DW_P;
   constexpr int KH = STEPS * 128;                  // k per half
   constexpr int AROW = 2 * KH + 8;                 // bf16 per staged row: both halves + 16 B of pad
+  // X4T: scale columns of a K half (cols = inter / 32 = 8 STEPS in all) and
+  // each wave's decoded bytes [b][s][64]
+  constexpr int XHC = 4 * STEPS, XREG = NBP * STEPS * 64;
   static_assert(STEPS % NBUF == 0, "ring slot of step s is s % NBUF in every unit");
   __shared__ __attribute__((aligned(16))) uint16_t a_lds[DW_PAIRS][AROW];
   __shared__ float yh[DW_PAIRS][2][CH];            // each pair's two K-half partials
   __shared__ float ybuf[DW_PAIRS][CH];             // route weight x (half 0 + half 1)
+  __shared__ __attribute__((aligned(16))) uint8_t xsl[X4T ? 16 * XREG : 16];
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int m = lane & 15, g = lane >> 4;
   const int pairs = tokens * topk;
@@ -2181,7 +2193,13 @@ __global__ __launch_bounds__(1024) void moe_decode_down_wide_kernel(
     const uint8_t* w[NBP];
     const uint8_t* s[NBP];
     int half, n, spair;
+    // X4T, lanes 0..31 = (tile b = lane / 16, row lane % 16): the row base
+    // and the selector bytes of the half's columns; every lane: one of the
+    // first 64 exception words of both tiles, and the tiles' exception range
+    uint32_t xbase, xb[XHC / 8], xexc;
+    int xlo, xhi;
   };
+  const int64_t xt0 = c0 / 16;  // X4T: the workgroup's first scale tile
   auto setup = [&](int u, Unit& U) {
     uint64_t st = starts;
     for (int i = u >> 1; i > 0; --i) st &= st - 1;
@@ -2199,8 +2217,56 @@ __global__ __launch_bounds__(1024) void moe_decode_down_wide_kernel(
     for (int b = 0; b < NBP; ++b) {
       const int64_t t0 = ((int64_t)e * rgs + c0 / 16 + b) * nchunk + U.half * STEPS;
       U.w[b] = wt + t0 * 1024 + 16 * lane;
-      U.s[b] = wst + t0 * 64 + lane;
+      U.s[b] = X4T ? nullptr : wst + t0 * 64 + lane;
     }
+    if constexpr (X4T) {
+      // the exception range of tiles xt0 and xt0 + 1 (one range: they are
+      // consecutive), then the fixed bytes; the words themselves are loaded
+      // by x4t_fetch once the range has landed
+      const int64_t ti = (int64_t)e * xg.tiles + xt0;
+      U.xlo = (int)xg.idx[0][ti];  // (kept in vector registers: a scalar copy would wait for the load here)
+      U.xhi = (int)xg.idx[0][ti + 2];
+      // (lanes 32..63 load what lanes 0..31 load: every lane issues the
+      // same loads, so the waits for them are counted exactly)
+      const uint8_t* pc = xg.fixed[0] + (ti + ((lane >> 4) & 1)) * (16 * (1 + XHC / 4));
+      U.xbase = pc[lane & 15];
+      // selector bytes of row lane % 16, columns XHC half .. XHC half + XHC - 1
+      const uint8_t* bm = pc + 16 + (lane & 15) * (XHC / 4) + U.half * (XHC / 8);
+#pragma unroll
+      for (int i = 0; i < XHC / 8; ++i) U.xb[i] = bm[i];
+    }
+  };
+  // (lanes past the range read a valid word they do not use, so that the
+  // load is issued by every lane)
+  auto x4t_fetch = [&](Unit& U) {
+    const uint32_t* src = U.xlo + lane < U.xhi ? xg.exc[0] + U.xlo + lane : xg.idx[0];
+    U.xexc = *src;
+  };
+  // X4T: decode unit U's bytes into this wave's region (after the wave's
+  // last read of the previous unit's bytes)
+  auto x4t_write = [&](const Unit& U) {
+    uint8_t* sl = xsl + wave * XREG;
+    if (lane < 32) {
+      const int b = lane >> 4, row = lane & 15;
+#pragma unroll
+      for (int j = 0; j < XHC; ++j) {  // column XHC half + j: base + selector bit
+        const uint32_t bit = (U.xb[j >> 3] >> (j & 7)) & 1u;
+        sl[(b * STEPS + (j >> 2)) * 64 + (j & 3) * 16 + row] = (uint8_t)(U.xbase + bit);
+      }
+    }
+    auto patch = [&](uint32_t w) {
+      const int cols = 8 * STEPS, span = 16 * cols;
+      const uint32_t off = (w & 0xffffffu) - (uint32_t)(xt0 * span);  // wraps past the tiles when outside
+      if (off < 2u * span) {
+        const int b = off >= (uint32_t)span ? 1 : 0, o = (int)off - b * span;
+        const int r = o / cols, j = o - r * cols - U.half * XHC;
+        if (j >= 0 && j < XHC) sl[(b * STEPS + (j >> 2)) * 64 + (j & 3) * 16 + r] = (uint8_t)(w >> 24);
+      }
+    };
+    if (U.xlo + lane < U.xhi) patch(U.xexc);
+    // more than 64 exceptions: the rest loaded here (its waits also wait for
+    // the weight prefetch in flight)
+    for (int k = U.xlo + 64 + lane; k < U.xhi; k += 64) patch(xg.exc[0][k]);
   };
   struct WBuf {
     u32x4_t w[NBP];
@@ -2210,7 +2276,7 @@ __global__ __launch_bounds__(1024) void moe_decode_down_wide_kernel(
 #pragma unroll
     for (int b = 0; b < NBP; ++b) {
       B.w[b] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(U.w[b] + (int64_t)s * 1024));
-      B.ws[b] = U.s[b][(int64_t)s * 64];
+      if constexpr (!X4T) B.ws[b] = U.s[b][(int64_t)s * 64];
     }
   };
   WBuf wb[NBUF];
@@ -2220,37 +2286,61 @@ __global__ __launch_bounds__(1024) void moe_decode_down_wide_kernel(
     setup(u, cur);
 #pragma unroll
     for (int s = 0; s < P; ++s) load_w(cur, s, wb[s]);
+    if constexpr (X4T) x4t_fetch(cur);
   }
   // the staged rows have landed once only the (younger) weight prefetch is in
-  // flight: 2 P loads per block, or none without a unit
-  if (u < units) __builtin_amdgcn_s_waitcnt(dma::waitcnt_vm(2 * NBP * P));
+  // flight: 2 P loads per block (with X4T scales one per block, and the
+  // exception word), or none without a unit
+  if (u < units) __builtin_amdgcn_s_waitcnt(dma::waitcnt_vm(X4T ? NBP * P + 1 : 2 * NBP * P));
   else __builtin_amdgcn_s_waitcnt(dma::waitcnt_vm(0));
   (void)staged;
+  if constexpr (X4T)
+    if (u < units) x4t_write(cur);
   lds_barrier();  // every wave's rows are staged
   while (u < units) {
     const int un = u + 16;
-    if (un < units) setup(un, nxt);
+    // the next unit; after the wave's last, this one again with its weight
+    // pointers on the first 2 KiB of the weights (cached by every wave that
+    // reads them): every unit issues the same loads, so the waits for them
+    // are counted exactly (with a conditional prefetch the compiler waits for
+    // all loads in flight at the last steps)
+    setup(un < units ? un : u, nxt);
+    if (un >= units) {
+#pragma unroll
+      for (int b = 0; b < NBP; ++b) {
+        nxt.w[b] = wt + 16 * lane;
+        nxt.s[b] = X4T ? nullptr : wst + lane;
+      }
+    }
     f32x4_t acc[NBP];
 #pragma unroll
     for (int b = 0; b < NBP; ++b) acc[b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     const u32x4_t* arow = reinterpret_cast<const u32x4_t*>(&a_lds[cur.spair][cur.half * KH]);
+    const uint8_t* xs = xsl + wave * XREG + lane;  // X4T: this unit's decoded bytes
 #pragma unroll
     for (int s = 0; s < STEPS; ++s) {
       if (s + P < STEPS) load_w(cur, s + P, wb[(s + P) % NBUF]);
-      else if (un < units) load_w(nxt, s + P - STEPS, wb[(s + P) % NBUF]);
+      else load_w(nxt, s + P - STEPS, wb[(s + P) % NBUF]);
+      // X4T: the next unit's first exception words, once its range has landed
+      if (X4T && s == STEPS / 2) x4t_fetch(nxt);
       __builtin_amdgcn_sched_barrier(0);
       const WBuf& W = wb[s % NBUF];
+      uint32_t ws[NBP];
+#pragma unroll
+      for (int b = 0; b < NBP; ++b) ws[b] = X4T ? (uint32_t)xs[(b * STEPS + s) * 64] : W.ws[b];
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         const bf16x8_t fa = __builtin_bit_cast(bf16x8_t, arow[16 * s + 4 * g + t]);
 #pragma unroll
         for (int b = 0; b < NBP; ++b) {
-          const bf16x8_t fb = gemm::dequant8<1>(u32x2_t{W.w[b][t], 0u}, W.ws[b]);
+          const bf16x8_t fb = gemm::dequant8<1>(u32x2_t{W.w[b][t], 0u}, ws[b]);
           acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa, fb, acc[b], 0, 0, 0);
         }
       }
       __builtin_amdgcn_sched_barrier(0);
     }
+    if constexpr (X4T)
+      if (un < units) x4t_write(nxt);
     // D layout: lane holds rows (slots) 4 g + j, column m
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -2556,10 +2646,10 @@ static int moe_forward_impl(const char* fn, int activation, float act_beta, floa
   // activations needs no routing launch: one gate/up workgroup per pair, and
   // the down projection with the combine in one launch.
   // decodes of at most DD_PAIRS pairs: per-pair gate/up + moe_decode_down_kernel;
-  // up to DW_PAIRS pairs with dense scales: per-pair gate/up + moe_decode_down_wide_kernel
+  // up to DW_PAIRS pairs: per-pair gate/up + moe_decode_down_wide_kernel
   const bool dd = L.pairs <= DD_PAIRS && (inter == 512 || inter == 1024 || inter == 2048 || inter == 4096) &&
                   (!xa || inter / 32 <= DD_X4T_COLS);
-  const bool dw = !dd && L.pairs <= DW_PAIRS && !xa && (inter == 1024 || inter == 2048) && tokens <= 64;
+  const bool dw = !dd && L.pairs <= DW_PAIRS && (inter == 1024 || inter == 2048) && tokens <= 64;
   const bool route_in_gemv = decode && act_fmt < 0 && hidden % 32 == 0 && (dd || dw);
   const DecodeRouteArgs dra{route_ids, experts, (int)L.pairs};
   if (decode && !route_in_gemv) {
@@ -2666,15 +2756,19 @@ static int moe_forward_impl(const char* fn, int activation, float act_beta, floa
   if (route_in_gemv && dw) {
     const dim3 grid((unsigned)(hidden / 32));
     const bool f32 = out_dtype == KQ_DT_F32;
-#define KQ_DW_LAUNCH(NS, OUTC)                                                                                 \
-    moe_decode_down_wide_kernel<NS, OUTC><<<grid, 1024, 0, st>>>((const uint16_t*)act, inter, route_ids, topk,   \
-                                                                 experts, (int)tokens, w2_t, w2_st, hidden,      \
-                                                                 route_weights, out)
+    const X4TGemv xg2 = x4t_gemv(xa, false);
+#define KQ_DW_LAUNCH(NS, OUTC, X)                                                                              \
+    moe_decode_down_wide_kernel<NS, OUTC, X><<<grid, 1024, 0, st>>>((const uint16_t*)act, inter, route_ids,     \
+                                                                    topk, experts, (int)tokens, w2_t, w2_st,     \
+                                                                    hidden, route_weights, out, xg2)
+#define KQ_DW_CASE(NS, X) \
+    if (f32) KQ_DW_LAUNCH(NS, 2, X); else KQ_DW_LAUNCH(NS, 0, X);
     if (inter == 1024) {
-      if (f32) KQ_DW_LAUNCH(4, 2); else KQ_DW_LAUNCH(4, 0);
+      if (xa) { KQ_DW_CASE(4, true) } else { KQ_DW_CASE(4, false) }
     } else {
-      if (f32) KQ_DW_LAUNCH(8, 2); else KQ_DW_LAUNCH(8, 0);
+      if (xa) { KQ_DW_CASE(8, true) } else { KQ_DW_CASE(8, false) }
     }
+#undef KQ_DW_CASE
 #undef KQ_DW_LAUNCH
     return kq_check_launch(hipGetLastError(), "kq_moe_forward/decode_down_wide");
   }

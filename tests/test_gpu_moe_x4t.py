@@ -185,10 +185,12 @@ def test_x4t_graph_replay(gpu):
         assert torch.equal(s_out, want), f"replay {rep}"
 
 
-@pytest.mark.parametrize("tokens", [1, 16])
+@pytest.mark.parametrize("tokens", [1, 4, 16])
 def test_x4t_decode_real_shapes(gpu, tokens):
     """Configuration 5 shapes (hidden 7168, intermediate 2048, 384 experts,
-    top-8): X4T planes w1 / w3 [2048, 224], w2 [7168, 64]."""
+    top-8): X4T planes w1 / w3 [2048, 224], w2 [7168, 64].  One token takes
+    the fused decode of at most 8 pairs, four tokens (32 pairs) the wide
+    decode kernel, 16 tokens the routed-list path."""
     ids, w = workloads.random_routing(tokens, seed=100 + tokens)
     x = torch.randn(tokens, 7168, generator=torch.Generator().manual_seed(7)).to(torch.bfloat16)
     weights = workloads.quantized_experts(ids.flatten().tolist(), device=gpu)
@@ -196,6 +198,28 @@ def test_x4t_decode_real_shapes(gpu, tokens):
     coded = moe.prepare_expert_weights(*weights, scale_format="x4t")
     args = (x.to(gpu), ids.to(gpu), w.to(gpu))
     assert torch.equal(moe.grouped_expert_forward(*args, coded), moe.grouped_expert_forward(*args, dense))
+
+
+@pytest.mark.parametrize("T", [2, 3, 4])
+def test_x4t_wide_decode_exception_heavy(gpu, T):
+    """9 to 32 pairs at intermediate 2048 (the wide decode kernel decodes
+    each unit's half of two scale tiles in the workgroup), three experts
+    with exception-heavy planes (more than 64 exceptions per pair of tiles,
+    which the kernel loads past its prefetched words): bitwise the
+    dense-scale forward, bf16 and fp32 outputs."""
+    k, E, H, I = 8, 12, 512, 2048
+    g = torch.Generator().manual_seed(70 + T)
+    ids = torch.stack([torch.randperm(E, generator=g)[:k] for _ in range(T)]).to(torch.int32)
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    w = torch.softmax(torch.randn(T, k, generator=g), -1)
+    weights = _weights(E, H, I, 71, gpu, spread=(0, 4, 9))
+    dense = moe.prepare_expert_weights(*weights)
+    coded = moe.prepare_expert_weights(*weights, scale_format="x4t")
+    args = (x.to(gpu), ids.to(gpu), w.to(gpu))
+    for out_dtype in (torch.bfloat16, torch.float32):
+        want = moe.grouped_expert_forward(*args, dense, out_dtype=out_dtype)
+        got = moe.grouped_expert_forward(*args, coded, out_dtype=out_dtype)
+        assert torch.equal(got, want), out_dtype
 
 
 @pytest.mark.parametrize("T", [4, 600])
