@@ -497,16 +497,22 @@ __global__ __launch_bounds__(256) void chol_panel_kernel(float* __restrict__ l, 
 // factors it as panel b0's diagonal block.
 __global__ __launch_bounds__(256, 4) void chol_update_kernel(float* __restrict__ l, int64_t n, int64_t ldl, int64_t sl,
                                                           int b0, int q0, int q1, float* __restrict__ winv,
-                                                          int* __restrict__ info, int* __restrict__ diag_done) {
+                                                          int* __restrict__ info, int* __restrict__ diag_done,
+                                                          int column_only) {
   __shared__ float xi[NB][LD];
   __shared__ float xj[NB][LD];
   const int64_t b = blockIdx.y;
   float* L = l + b * sl;
   const int64_t t = blockIdx.x;
-  int64_t i = (int64_t)((sqrt(8.0 * (double)t + 1.0) - 1.0) * 0.5);
-  while ((i + 1) * (i + 2) / 2 <= t) ++i;
-  while (i * (i + 1) / 2 > t) --i;
-  const int64_t j = t - i * (i + 1) / 2;
+  // tile t: (i, j) of the trailing lower triangle, or (t, 0) of its first
+  // block column only
+  int64_t i = t, j = 0;
+  if (!column_only) {
+    i = (int64_t)((sqrt(8.0 * (double)t + 1.0) - 1.0) * 0.5);
+    while ((i + 1) * (i + 2) / 2 <= t) ++i;
+    while (i * (i + 1) / 2 > t) --i;
+    j = t - i * (i + 1) / 2;
+  }
   const int64_t ri = (int64_t)(b0 + i) * NB, rj = (int64_t)(b0 + j) * NB;
   // this lane's A entries, loaded first: their latency hides behind the products
   float av[2][2][4];
@@ -707,6 +713,9 @@ extern "C" int64_t kq_cholesky_workspace_size(int64_t n, int64_t batch) {
   return batch * 2 * NB * NB * (int64_t)sizeof(float) + (batch * (int64_t)sizeof(int) + 255) / 256 * 256;
 }
 
+#ifndef KQ_CHOL_R
+#define KQ_CHOL_R 2
+#endif
 extern "C" int kq_cholesky(const float* a, int64_t lda, int64_t stride_a, float* l, int64_t ldl, int64_t stride_l,
                            int64_t n, int64_t batch, int32_t* info, void* workspace, int64_t workspace_bytes,
                            void* stream) {
@@ -732,13 +741,15 @@ extern "C" int kq_cholesky(const float* a, int64_t lda, int64_t stride_a, float*
   chol_diag_kernel<<<(unsigned)batch, 256, 0, st>>>(l, n, ldl, stride_l, winv, info);
   if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_cholesky/diag");
   if (batch < 8) {
-    // Right-looking, one launch per panel after the first: update launch s
-    // applies panel s - 1 to the trailing matrix, factors diagonal block s
-    // (its first workgroup) and, in the workgroups of the tiles below that
-    // block, once it is factored, computes panel s itself (measured on
-    // MI355X: one n = 7168 matrix 4.93 ms, against 5.21 with separate panel
-    // launches and two-panel super-panels, 5.29 with one panel each; four
-    // matrices of n = 2048: 1.18 against 1.23 ms).
+    // One launch per panel after the first, in super-panels of R panels:
+    // the launch of a super-panel's first panel S applies the previous
+    // super-panel's panels to the whole trailing matrix (rank 64 R, so the
+    // trailing matrix is read and written once per super-panel), the launch
+    // of panel s inside it applies panels S .. s - 1 to block column s only.
+    // Each launch then factors diagonal block s (its first workgroup) and,
+    // in the workgroups of the tiles below that block, once it is factored,
+    // computes panel s itself.
+    constexpr int R = KQ_CHOL_R;
     if (m > 1) {
       chol_panel_kernel<<<dim3((unsigned)(m - 1), (unsigned)batch), 256, 0, st>>>(l, n, ldl, stride_l, 0, 0, 1,
                                                                                  winv, info);
@@ -746,8 +757,13 @@ extern "C" int kq_cholesky(const float* a, int64_t lda, int64_t stride_a, float*
     }
     for (int s = 1; s < m; ++s) {
       const int64_t q = m - s;
-      chol_update_kernel<<<dim3((unsigned)(q * (q + 1) / 2), (unsigned)batch), 256, 0, st>>>(
-          l, n, ldl, stride_l, s, s - 1, s, winv, info, diag_done);
+      const int S = s / R * R;  // this super-panel's first panel
+      if (s == S)
+        chol_update_kernel<<<dim3((unsigned)(q * (q + 1) / 2), (unsigned)batch), 256, 0, st>>>(
+            l, n, ldl, stride_l, s, s - R, s, winv, info, diag_done, 0);
+      else
+        chol_update_kernel<<<dim3((unsigned)q, (unsigned)batch), 256, 0, st>>>(
+            l, n, ldl, stride_l, s, S, s, winv, info, diag_done, 1);
       if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_cholesky/update");
     }
     return KQ_OK;
@@ -769,7 +785,7 @@ extern "C" int kq_cholesky(const float* a, int64_t lda, int64_t stride_a, float*
     if (s1 < m) {
       const int64_t q = m - s1;
       chol_update_kernel<<<dim3((unsigned)(q * (q + 1) / 2), (unsigned)batch), 256, 0, st>>>(
-          l, n, ldl, stride_l, s1, s0, s1, winv, info, nullptr);
+          l, n, ldl, stride_l, s1, s0, s1, winv, info, nullptr, 0);
       if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_cholesky/update");
     }
   }
