@@ -495,12 +495,29 @@ __global__ __launch_bounds__(256) void chol_panel_kernel(float* __restrict__ l, 
 // enumerates them row by row; the panels' products are summed in registers,
 // so A is read and written once).  The workgroup of tile (b0, b0) then
 // factors it as panel b0's diagonal block.
-__global__ __launch_bounds__(256, 4) void chol_update_kernel(float* __restrict__ l, int64_t n, int64_t ldl, int64_t sl,
-                                                          int b0, int q0, int q1, float* __restrict__ winv,
-                                                          int* __restrict__ info, int* __restrict__ diag_done,
-                                                          int column_only) {
-  __shared__ float xi[NB][LD];
-  __shared__ float xj[NB][LD];
+// DMA (n and ldl multiples of 64 and 4, l 16-byte aligned): the panel
+// tiles of two panels in flight at once, by direct loads into a two-slot LDS
+// ring (32 KiB a slot: the two 64 x 64 tiles, 256-byte rows with 16-byte
+// chunk c of row r at chunk c ^ (r % 16)), read as 128-bit fragments: lane
+// (i, k) of a 16-wide k block reads floats 4k .. 4k + 3 of its row, and
+// MFMA e of the block takes the lane's float e, so a 16 x 16 x 4 product
+// sums k values k0 + 4 lk + e (any order of k sums the same products).  Two
+// workgroups per CU; the other form keeps four with padded tiles loaded
+// through registers.
+namespace dup {
+constexpr int SLOT = 2 * NB * NB * 4;  // bytes: xi and xj
+constexpr int LOADS = 8;               // direct loads per wave per slot
+}  // namespace dup
+
+template <bool DMA>
+__global__ __launch_bounds__(256, DMA ? 2 : 4) void chol_update_kernel(float* __restrict__ l, int64_t n, int64_t ldl,
+                                                                     int64_t sl, int b0, int q0, int q1,
+                                                                     float* __restrict__ winv, int* __restrict__ info,
+                                                                     int* __restrict__ diag_done, int column_only) {
+  __shared__ __attribute__((aligned(16))) float ring[DMA ? 2 * dup::SLOT / 4 : 2 * NB * LD];
+  static_assert(2 * NB * LD * 4 <= (DMA ? 2 * dup::SLOT : 2 * NB * LD * 4), "padded tiles alias the ring");
+  float (*xi)[LD] = reinterpret_cast<float (*)[LD]>(ring);
+  float (*xj)[LD] = reinterpret_cast<float (*)[LD]>(ring + NB * LD);
   const int64_t b = blockIdx.y;
   float* L = l + b * sl;
   const int64_t t = blockIdx.x;
@@ -528,16 +545,68 @@ __global__ __launch_bounds__(256, 4) void chol_update_kernel(float* __restrict__
         av[bi][bj][q] = r < n && c < n ? L[r * ldl + c] : 0.f;
       }
   f32x4_t acc[2][2] = {};
-  for (int q = q0; q < q1; ++q) {
-    if (q > q0) __syncthreads();  // every wave is done reading the previous panel's tiles
-    load_tile(xi, L, ldl, n, ri, (int64_t)q * NB);
-    load_tile(xj, L, ldl, n, rj, (int64_t)q * NB);
-    __syncthreads();
-    mm_nt(xi, xj, acc);
+  if constexpr (DMA) {
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const uint32_t lds0 = dma::lds_offset_of(ring);
+    // the rows of tiles xi and xj (zero past n: out-of-range offsets)
+    const dma::i32x4_t rs_i = dma::make_rsrc(L + ri * ldl, (uint32_t)((n - ri < NB ? n - ri : NB) * ldl * 4));
+    const dma::i32x4_t rs_j = dma::make_rsrc(L + rj * ldl, (uint32_t)((n - rj < NB ? n - rj : NB) * ldl * 4));
+    // instruction u of this wave: tile u / 4, rows 4 g .. 4 g + 3 with
+    // g = 4 (u % 4) + wave; lane: row 4 g + lane / 16, LDS chunk lane % 16
+    auto issue = [&](int q, int slot) {
+#pragma unroll
+      for (int u = 0; u < dup::LOADS; ++u) {
+        const int g = 4 * (u % 4) + wave, row = 4 * g + (lane >> 4);
+        const int c = (lane & 15) ^ (row & 15);
+        const uint32_t off = (uint32_t)(row * ldl * 4 + q * NB * 4 + c * 16);
+        dma::load_to_lds16(u < 4 ? rs_i : rs_j, off,
+                           lds0 + (uint32_t)(slot * dup::SLOT + (u / 4) * NB * NB * 4 + g * 1024));
+      }
+    };
+    issue(q0, 0);
+    if (q0 + 1 < q1) issue(q0 + 1, 1);
+    const int li = lane & 15, lk = lane >> 4;
+    const int rb = 32 * (wave >> 1), cb = 32 * (wave & 1);
+    for (int q = q0; q < q1; ++q) {
+      const int slot = (q - q0) & 1;
+      // this wave's loads of slot q have landed (q + 1's may be in flight), then everyone's
+      if (q + 1 < q1) __builtin_amdgcn_s_waitcnt(dma::waitcnt_vm(dup::LOADS));
+      else __builtin_amdgcn_s_waitcnt(dma::waitcnt_vm(0));
+      __syncthreads();
+      const unsigned char* X = reinterpret_cast<const unsigned char*>(ring) + slot * dup::SLOT;
+      const unsigned char* Y = X + NB * NB * 4;
+#pragma unroll
+      for (int k0 = 0; k0 < NB; k0 += 16) {
+        const int cl = k0 / 4 + lk;  // logical chunk
+        const f32x4_t a0 = *reinterpret_cast<const f32x4_t*>(X + (rb + li) * 256 + ((cl ^ li) * 16));
+        const f32x4_t a1 = *reinterpret_cast<const f32x4_t*>(X + (rb + 16 + li) * 256 + ((cl ^ li) * 16));
+        const f32x4_t b0v = *reinterpret_cast<const f32x4_t*>(Y + (cb + li) * 256 + ((cl ^ li) * 16));
+        const f32x4_t b1v = *reinterpret_cast<const f32x4_t*>(Y + (cb + 16 + li) * 256 + ((cl ^ li) * 16));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          acc[0][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0[e], b0v[e], acc[0][0], 0, 0, 0);
+          acc[0][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0[e], b1v[e], acc[0][1], 0, 0, 0);
+          acc[1][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1[e], b0v[e], acc[1][0], 0, 0, 0);
+          acc[1][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1[e], b1v[e], acc[1][1], 0, 0, 0);
+        }
+      }
+      if (q + 2 < q1) {
+        __syncthreads();  // every wave is done reading the slot
+        issue(q + 2, slot);
+      }
+    }
+  } else {
+    for (int q = q0; q < q1; ++q) {
+      if (q > q0) __syncthreads();  // every wave is done reading the previous panel's tiles
+      load_tile(xi, L, ldl, n, ri, (int64_t)q * NB);
+      load_tile(xj, L, ldl, n, rj, (int64_t)q * NB);
+      __syncthreads();
+      mm_nt(xi, xj, acc);
+    }
   }
   const bool next_diag = t == 0;  // tile (b0, b0): panel b0's diagonal block
   const bool panel = diag_done != nullptr && j == 0 && i > 0;  // fused: a tile of panel b0 below it
-  if (next_diag || panel) __syncthreads();  // every wave is done reading xi / xj
+  if (next_diag || panel) __syncthreads();  // every wave is done reading the tiles xi / xj alias
 #pragma unroll
   for (int bi = 0; bi < 2; ++bi)
 #pragma unroll
@@ -738,6 +807,10 @@ extern "C" int kq_cholesky(const float* a, int64_t lda, int64_t stride_a, float*
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return kq_check_launch(e, "kq_cholesky/init");
   const int m = (int)((n + NB - 1) / NB);
+  // the update launches' direct-load form: whole 64-column tiles, 16-byte
+  // aligned rows, and a 64-row tile's bytes within one 32-bit range
+  const bool dma_ok = n % NB == 0 && ldl % 4 == 0 && (reinterpret_cast<uintptr_t>(l) & 15) == 0 &&
+                      (batch == 1 || stride_l % 4 == 0) && (uint64_t)NB * ldl * 4 <= kq::dma::MAX_RANGE;
   chol_diag_kernel<<<(unsigned)batch, 256, 0, st>>>(l, n, ldl, stride_l, winv, info);
   if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_cholesky/diag");
   if (batch < 8) {
@@ -758,12 +831,10 @@ extern "C" int kq_cholesky(const float* a, int64_t lda, int64_t stride_a, float*
     for (int s = 1; s < m; ++s) {
       const int64_t q = m - s;
       const int S = s / R * R;  // this super-panel's first panel
-      if (s == S)
-        chol_update_kernel<<<dim3((unsigned)(q * (q + 1) / 2), (unsigned)batch), 256, 0, st>>>(
-            l, n, ldl, stride_l, s, s - R, s, winv, info, diag_done, 0);
-      else
-        chol_update_kernel<<<dim3((unsigned)q, (unsigned)batch), 256, 0, st>>>(
-            l, n, ldl, stride_l, s, S, s, winv, info, diag_done, 1);
+      const dim3 grid((unsigned)(s == S ? q * (q + 1) / 2 : q), (unsigned)batch);
+      const int qa = s == S ? s - R : S, col = s == S ? 0 : 1;
+      if (dma_ok) chol_update_kernel<true><<<grid, 256, 0, st>>>(l, n, ldl, stride_l, s, qa, s, winv, info, diag_done, col);
+      else chol_update_kernel<false><<<grid, 256, 0, st>>>(l, n, ldl, stride_l, s, qa, s, winv, info, diag_done, col);
       if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_cholesky/update");
     }
     return KQ_OK;
@@ -784,8 +855,9 @@ extern "C" int kq_cholesky(const float* a, int64_t lda, int64_t stride_a, float*
     }
     if (s1 < m) {
       const int64_t q = m - s1;
-      chol_update_kernel<<<dim3((unsigned)(q * (q + 1) / 2), (unsigned)batch), 256, 0, st>>>(
-          l, n, ldl, stride_l, s1, s0, s1, winv, info, nullptr, 0);
+      const dim3 grid((unsigned)(q * (q + 1) / 2), (unsigned)batch);
+      if (dma_ok) chol_update_kernel<true><<<grid, 256, 0, st>>>(l, n, ldl, stride_l, s1, s0, s1, winv, info, nullptr, 0);
+      else chol_update_kernel<false><<<grid, 256, 0, st>>>(l, n, ldl, stride_l, s1, s0, s1, winv, info, nullptr, 0);
       if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_cholesky/update");
     }
   }
