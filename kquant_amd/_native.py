@@ -26,6 +26,7 @@ FMT_MXFP4_E2M1 = 1
 DT_BF16 = 0
 DT_F16 = 1
 DT_F32 = 2
+QSRT_OUT_E4M3 = 3  # kq_qsrt_decode_weight's E4M3 label-byte output (KQ_QSRT_OUT_E4M3)
 FLAG_SOFTWARE_CVT = 1
 TABLE_E8M0 = 0
 TABLE_E2M1 = 1

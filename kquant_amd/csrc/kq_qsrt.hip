@@ -637,6 +637,9 @@ struct DecArgs {
   void* out;
   int64_t ldo;
   int k_tiles, n_tiles, rate_n, kbw, transposed, out_dtype;
+  // E4M3 output with 4-byte aligned rows: the label bytes go to a byte tile
+  // in the output's orientation and leave as 4-byte stores
+  int bytes;
 };
 
 template <bool ROT>
@@ -644,7 +647,9 @@ __global__ __launch_bounds__(LIN_THREADS) void decode_fast_kernel(DecArgs a, Lin
   __shared__ __attribute__((aligned(16))) uint8_t lut[65536];
   constexpr int ST = 3;  // ring stages (the fp32 tile takes the fourth's LDS)
   __shared__ __attribute__((aligned(16))) uint32_t ring[ST][2048];  // 16 waves x 512 bytes
-  __shared__ float t[128][129];
+  __shared__ __attribute__((aligned(16))) float t[128][129];
+  constexpr int TBL = 132;  // byte tile row (bytes: 33 dwords, rows on distinct banks)
+  uint8_t* tb = reinterpret_cast<uint8_t*>(&t[0][0]);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int half = wave >> 3, ntl = wave & 7;
@@ -696,10 +701,20 @@ __global__ __launch_bounds__(LIN_THREADS) void decode_fast_kernel(DecArgs a, Lin
         const uint64_t v = (((uint64_t)w[d0] << 32) | w[d1]) << off;
         const uint32_t win = (uint32_t)(v >> sh);
         const int row = (half * 4 + i) * 16 + r0;
-        t[row][col] = e4m3_scaled(lut[(win >> (3 * bits)) & 0xffffu]);
-        t[row + 1][col] = e4m3_scaled(lut[(win >> (2 * bits)) & 0xffffu]);
-        t[row + 8][col] = e4m3_scaled(lut[(win >> bits) & 0xffffu]);
-        t[row + 9][col] = e4m3_scaled(lut[win & 0xffffu]);
+        const uint8_t l0 = lut[(win >> (3 * bits)) & 0xffffu], l1 = lut[(win >> (2 * bits)) & 0xffffu];
+        const uint8_t l2 = lut[(win >> bits) & 0xffffu], l3 = lut[win & 0xffffu];
+        if (!ROT && a.bytes) {  // byte tile [output row][128 + 4]
+          const int rs = a.transposed ? 1 : TBL, cs = a.transposed ? TBL : 1;
+          tb[row * rs + col * cs] = l0;
+          tb[(row + 1) * rs + col * cs] = l1;
+          tb[(row + 8) * rs + col * cs] = l2;
+          tb[(row + 9) * rs + col * cs] = l3;
+        } else {
+          t[row][col] = e4m3_scaled(l0);
+          t[row + 1][col] = e4m3_scaled(l1);
+          t[row + 8][col] = e4m3_scaled(l2);
+          t[row + 9][col] = e4m3_scaled(l3);
+        }
       }
     }
     if (kbi + ST < kbn) stage(kb + ST, ring[kbi % ST]);
@@ -726,7 +741,15 @@ __global__ __launch_bounds__(LIN_THREADS) void decode_fast_kernel(DecArgs a, Lin
       }
       __syncthreads();
     }
-    if (a.transposed) {  // out [N, K]: one output row (a column of the block) per wave pass
+    if (!ROT && a.bytes) {  // 128 output rows of 128 bytes: two per wave pass, 4 bytes a lane
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        const int orow = 8 * wave + 2 * h + (lane >> 5), ob = 4 * (lane & 31);
+        const uint32_t v = *reinterpret_cast<const uint32_t*>(tb + orow * TBL + ob);
+        const int64_t o = a.transposed ? (col0 + orow) * a.ldo + row0 + ob : (row0 + orow) * a.ldo + col0 + ob;
+        *reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(a.out) + o) = v;
+      }
+    } else if (a.transposed) {  // out [N, K]: one output row (a column of the block) per wave pass
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const int c = wave + 16 * i;
@@ -1113,7 +1136,8 @@ extern "C" int kq_qsrt_decode_weight(const int16_t* payload, int64_t payload_wor
     kbw = kbw < 1 ? 1 : kbw > k_blocks ? k_blocks : kbw;
     const int64_t chunks = (k_blocks + kbw - 1) / kbw;
     DecArgs da{reinterpret_cast<const uint32_t*>(payload), labels, suh, svh, out, ldo, (int)k_tiles, (int)n_tiles,
-               rate_axis, (int)kbw, tr ? 1 : 0, out_dtype};
+               rate_axis, (int)kbw, tr ? 1 : 0, out_dtype,
+               out_dtype == OUT_E4M3 && ldo % 4 == 0 && !kq_misaligned(out, 4) ? 1 : 0};
     const dim3 grid((unsigned)(n_blocks * chunks));
     if (suh) decode_fast_kernel<true><<<grid, LIN_THREADS, 0, (hipStream_t)stream>>>(da, lr);
     else decode_fast_kernel<false><<<grid, LIN_THREADS, 0, (hipStream_t)stream>>>(da, lr);

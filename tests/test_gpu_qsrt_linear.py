@@ -220,6 +220,35 @@ def test_every_finite_e4m3_label_converts_exactly(gpu):
     assert np.array_equal(out.cpu().numpy(), want)
 
 
+@pytest.mark.parametrize("transposed", [False, True])
+@pytest.mark.parametrize("pad", [0, 4, 3])
+def test_e4m3_label_bytes_every_code(gpu, transposed, pad):
+    """kq_qsrt_decode_weight to KQ_QSRT_OUT_E4M3 (the prefill's weight):
+    every finite code's byte, [K, N] and [N, K], with 4-byte aligned output
+    rows (the byte tile and 4-byte stores) and with a row stride that is not
+    (one byte per store); the bytes past each row stay untouched."""
+    from kquant_amd import _native as N
+
+    k_tiles, n_tiles, bits = 16, 24, (3, 2, 4)
+    payload = _random_matrix(k_tiles, n_tiles, "n", bits, 41)
+    table = (np.arange(65536) & 0xFF).astype(np.uint8)
+    table[(table & 0x7F) == 0x7F] = 0
+    labels = torch.from_numpy(np.stack([table] * 3)).to(gpu)
+    want = oq.decode_qsrt_weight(payload, k_tiles, n_tiles, bits, "n", {2: table, 3: table, 4: table})
+    if transposed:
+        want = want.T
+    want8 = torch.from_numpy(np.ascontiguousarray(want)).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    rows, cols = want.shape
+    ldo = cols + pad
+    out = torch.full((rows, ldo), 0xA5, dtype=torch.uint8, device=gpu)
+    p = torch.from_numpy(payload).to(gpu)
+    N.call("kq_qsrt_decode_weight", N.ptr(p), p.numel(), k_tiles, n_tiles, 1, bytes(bits), N.ptr(labels), None,
+           None, N.QSRT_OUT_E4M3, N.ptr(out), ldo, 1 if transposed else 0, N.stream(gpu))
+    got = out.cpu().numpy()
+    assert np.array_equal(got[:, :cols], want8)
+    assert (got[:, cols:] == 0xA5).all()
+
+
 @pytest.mark.parametrize("rate_axis,m,shape,record_bits", [
     ("n", qsrt.FUSED_MAX_ROWS + 1, (32, 16), (3, 4)),
     ("k", 100, (24, 40), (2, 4, 3)),
