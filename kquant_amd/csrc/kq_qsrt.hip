@@ -736,8 +736,20 @@ __global__ __launch_bounds__(LIN_THREADS) void decode_fast_kernel(DecArgs a, Lin
         const int c = wave + 16 * i;
         float v0 = t[lane][c], v1 = t[lane + 64][c];
         fwht128(v0, v1, lane);
-        t[lane][c] = v0 * su0;
-        t[lane + 64][c] = v1 * su1;
+        v0 *= su0;
+        v1 *= su1;
+        if (a.transposed) {  // out [N, K]: the column is an output row, stored from registers
+          const int64_t o = (col0 + c) * a.ldo + row0;
+          store_out(a.out, a.out_dtype, o + lane, v0);
+          store_out(a.out, a.out_dtype, o + lane + 64, v1);
+        } else {
+          t[lane][c] = v0;
+          t[lane + 64][c] = v1;
+        }
+      }
+      if (a.transposed) {
+        __syncthreads();  // the tile is rewritten by the next block
+        continue;
       }
       __syncthreads();
     }
