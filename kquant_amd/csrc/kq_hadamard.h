@@ -47,32 +47,40 @@ __device__ __forceinline__ void fwht_lines(float (*t)[HLD]) {
   __syncthreads();
 }
 
-// v of lane ^ S: quad permutes (DPP) for 1 and 2, a bit-mask swizzle for 4
-// and 8, and the gfx950 row swaps for 16 and 32 (lanes 0-31 receive the
-// upper half's values in the second result of permlane32_swap, lanes 32-63
-// the lower half's in the first; likewise per 16-lane row pair for
-// permlane16_swap) - none of them go through LDS addressing.
+// v of lane ^ S for S = 1, 2 (DPP quad permutes) and 4, 8 (bit-mask
+// swizzles), which go through no LDS addressing.
 template <int S>
-__device__ __forceinline__ float lane_xor(float v, int lane) {
+__device__ __forceinline__ float lane_xor(float v) {
   const int x = __float_as_int(v);
   if constexpr (S == 1) return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, false));
   else if constexpr (S == 2) return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, false));
-  else if constexpr (S == 4 || S == 8) return __int_as_float(__builtin_amdgcn_ds_swizzle(x, 0x1F | (S << 10)));
-  else if constexpr (S == 16) {
-    const auto r = __builtin_amdgcn_permlane16_swap((unsigned)x, (unsigned)x, false, false);
-    return __uint_as_float((lane & 16) ? r[0] : r[1]);
-  } else {
-    const auto r = __builtin_amdgcn_permlane32_swap((unsigned)x, (unsigned)x, false, false);
-    return __uint_as_float((lane & 32) ? r[0] : r[1]);
-  }
+  else return __int_as_float(__builtin_amdgcn_ds_swizzle(x, 0x1F | (S << 10)));
 }
 
+// Butterfly across lanes l and l ^ S (S < 16): the lower lane keeps
+// v + v', the upper v' - v, as one FMA with the lane's sign (exact products
+// by +-1, so the sums round as the plain adds would).
 template <int S>
 __device__ __forceinline__ void fwht_stage(float& v0, float& v1, int lane) {
-  const float p0 = lane_xor<S>(v0, lane), p1 = lane_xor<S>(v1, lane);
-  const bool up = lane & S;
-  v0 = up ? p0 - v0 : v0 + p0;
-  v1 = up ? p1 - v1 : v1 + p1;
+  const float s = (lane & S) ? -1.f : 1.f;
+  const float p0 = lane_xor<S>(v0), p1 = lane_xor<S>(v1);
+  v0 = fmaf(s, v0, p0);
+  v1 = fmaf(s, v1, p1);
+}
+
+// Butterfly across elements e and e + S for S = 16, 32 with the gfx950 row
+// swaps: exchanging the upper rows of v0 with the lower rows of v1 leaves
+// every lane holding one (e, e + S) pair, which it combines in place; the
+// same exchange restores the layout.
+template <int S>
+__device__ __forceinline__ void fwht_stage_swap(float& v0, float& v1) {
+  const auto r = S == 16 ? __builtin_amdgcn_permlane16_swap(__float_as_uint(v0), __float_as_uint(v1), false, false)
+                         : __builtin_amdgcn_permlane32_swap(__float_as_uint(v0), __float_as_uint(v1), false, false);
+  const float a = __uint_as_float(r[0]), b = __uint_as_float(r[1]);
+  const auto q = S == 16 ? __builtin_amdgcn_permlane16_swap(__float_as_uint(a + b), __float_as_uint(a - b), false, false)
+                         : __builtin_amdgcn_permlane32_swap(__float_as_uint(a + b), __float_as_uint(a - b), false, false);
+  v0 = __uint_as_float(q[0]);
+  v1 = __uint_as_float(q[1]);
 }
 
 // 128-point Sylvester transform (unnormalized) of the line held as
@@ -85,8 +93,8 @@ __device__ __forceinline__ void fwht128(float& v0, float& v1, int lane) {
   fwht_stage<2>(v0, v1, lane);
   fwht_stage<4>(v0, v1, lane);
   fwht_stage<8>(v0, v1, lane);
-  fwht_stage<16>(v0, v1, lane);
-  fwht_stage<32>(v0, v1, lane);
+  fwht_stage_swap<16>(v0, v1);
+  fwht_stage_swap<32>(v0, v1);
 }
 
 }  // namespace had
