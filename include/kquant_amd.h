@@ -488,7 +488,11 @@ int kq_qsrt_decode_states(const int16_t* states, int64_t k_tiles, int64_t n_tile
  * counters, and for one or two rows the K chunks' partial sums, which the
  * last chunk's workgroup polls), so it serves repeated calls of the same
  * sizes (zero it again before other sizes, and after a prefill-sized call,
- * which uses it as scratch).  Calls sharing a workspace must not overlap. */
+ * which uses it as scratch).  Calls sharing a workspace must not overlap.
+ * With one or two rows the workgroup of the last K chunk waits for the
+ * other chunks' partials (workgroups that precede it in dispatch order and
+ * wait on nothing); the wait is bounded, and a partial still missing after
+ * it reads as NaN in the output. */
 int64_t kq_qsrt_linear_workspace_size(int64_t rows, int64_t k_tiles, int64_t n_tiles);
 int kq_qsrt_linear(const void* x, int x_dtype, int64_t rows, int64_t ldx, const int16_t* payload,
                    int64_t payload_words, int64_t k_tiles, int64_t n_tiles, int rate_axis,
