@@ -425,6 +425,52 @@ __device__ __forceinline__ void poll_partials(const float* p, int64_t stride, in
     if (!stored(v[u])) v[u] = __builtin_nanf("");
 }
 
+typedef float qf32x4_t __attribute__((ext_vector_type(4)));
+
+// Four or more rows: the block's products on v_mfma_f32_16x16x4f32, one
+// 16 x 16 output (rows m, columns of the wave's n tile) per wave.  The four
+// k values of MFMA j are tile rows 4 kq + j for lane group kq, so lane
+// (n, kq) decodes the symbols at rows 4 kq .. 4 kq + 3 of column n -- in
+// the tensor-core order symbols b, b + 1, b + 8, b + 9 with b = (n % 8) << 5
+// | (kq % 2) << 4 | (n / 8) << 2 | (kq / 2) << 1, two windows of 16 + K
+// stream bits -- and reads x[n][4 kq .. 4 kq + 3] of the tile's k as one
+// 128-bit fragment (rows n >= M give zeros).  acc: rows 4 kq + r, column n.
+template <int M>
+__device__ __forceinline__ void accumulate_block_mfma(const uint32_t* slot, int bits, const uint8_t* lut,
+                                                      const float* xs, int xs_stride, int half, int lane,
+                                                      qf32x4_t& acc) {
+  const int n = lane & 15, kq = lane >> 4;
+  const int b = ((n & 7) << 5) | ((kq & 1) << 4) | ((n >> 3) << 2) | ((kq >> 1) << 1);
+  const int sh = 64 - (16 + bits);
+  int d0[2], d1[2], off[2];
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {  // symbols b + 8 p and b + 8 p + 1: the window ending at the second
+    int sb = (b + 8 * p + 1) * bits - 16;
+    if (sb < 0) sb += 256 * bits;
+    d0[p] = sb >> 5;
+    d1[p] = d0[p] + 1 == 8 * bits ? 0 : d0[p] + 1;
+    off[p] = sb & 31;
+  }
+  const bool live = n < M;
+  const float* xr = xs + (live ? n : 0) * xs_stride + half * 64 + 4 * kq;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t* t = slot + i * 8 * bits;
+    float w[4];
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const uint64_t v = (((uint64_t)t[d0[p]] << 32) | t[d1[p]]) << off[p];
+      const uint32_t win = (uint32_t)(v >> sh);
+      w[2 * p] = e4m3_scaled(lut[(win >> bits) & 0xffffu]);
+      w[2 * p + 1] = e4m3_scaled(lut[win & 0xffffu]);
+    }
+    qf32x4_t xa = *reinterpret_cast<const qf32x4_t*>(xr + i * 16);
+    if (!live) xa = qf32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[j], w[j], acc, 0, 0, 0);
+  }
+}
+
 // Stage this wave's tiles of k block kb of the kernel-argument matrix.
 __device__ __forceinline__ void stage_block(const LinArgs& a, const LinRecords& rec, int nb, int kb,
                                             uint32_t* stage, int wave, int lane) {
@@ -438,7 +484,10 @@ template <int M, bool ROT>
 __global__ __launch_bounds__(LIN_THREADS) void linear_kernel(LinArgs a, LinRecords rec) {
   __shared__ __attribute__((aligned(16))) uint8_t lut[65536];
   __shared__ __attribute__((aligned(16))) uint32_t ring[LIN_STAGES][2048];  // 16 waves x 512 bytes
-  __shared__ __attribute__((aligned(16))) float xs[M][lin_max_kb(M) * 128];
+  // rows padded by 16 bytes: the 128-bit fragment reads of 16 rows hit distinct bank groups
+  constexpr int XS = lin_max_kb(M) * 128 + 4;
+  constexpr bool MF = M >= 4;  // products on MFMA
+  __shared__ __attribute__((aligned(16))) float xs[M][XS];
   __shared__ float yb[2][M][128];
   __shared__ int s_last;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -485,9 +534,10 @@ __global__ __launch_bounds__(LIN_THREADS) void linear_kernel(LinArgs a, LinRecor
     sv0 = a.svh[(int64_t)nb * 128 + lane] * (1.f / 128.f);
     sv1 = a.svh[(int64_t)nb * 128 + lane + 64] * (1.f / 128.f);
   }
-  float acc[M];
+  float acc[MF ? 1 : M];
 #pragma unroll
-  for (int m = 0; m < M; ++m) acc[m] = 0.f;
+  for (int m = 0; m < (MF ? 1 : M); ++m) acc[m] = 0.f;
+  qf32x4_t macc = {0.f, 0.f, 0.f, 0.f};
   // every wave's labels (older than its stage loads) and activation rows
   wait_own_stage(min(LIN_STAGES, kbn));
   __syncthreads();
@@ -503,17 +553,28 @@ __global__ __launch_bounds__(LIN_THREADS) void linear_kernel(LinArgs a, LinRecor
     }
     // this wave's block kbi has landed once only its younger stages are in flight
     wait_own_stage(min(LIN_STAGES - 1, kbn - 1 - kbi));
-    accumulate_block<M>(ring[kbi % LIN_STAGES] + wave * 128, bits, lut, &xs[0][kbi * 128], lin_max_kb(M) * 128,
-                        half, lane, acc);
+    if constexpr (MF)
+      accumulate_block_mfma<M>(ring[kbi % LIN_STAGES] + wave * 128, bits, lut, &xs[0][kbi * 128], XS, half, lane,
+                               macc);
+    else
+      accumulate_block<M>(ring[kbi % LIN_STAGES] + wave * 128, bits, lut, &xs[0][kbi * 128], XS, half, lane, acc);
     // the wave has consumed its slot: refill it with block kbi + stages
     if (kbi + LIN_STAGES < kbn)
       stage_block(a, rec, nb, kb0 + kbi + LIN_STAGES, ring[kbi % LIN_STAGES], wave, lane);
   }
-  column_sums<M>(acc);
-  if ((lane & 6) == 0) {
-    const int c = ntl * 16 + (lane >> 3) + 8 * (lane & 1);
+  if constexpr (MF) {
 #pragma unroll
-    for (int m = 0; m < M; ++m) yb[half][m][c] = acc[m];
+    for (int r = 0; r < 4; ++r) {
+      const int m = 4 * (lane >> 4) + r;
+      if (m < M) yb[half][m][ntl * 16 + (lane & 15)] = macc[r];
+    }
+  } else {
+    column_sums<M>(acc);
+    if ((lane & 6) == 0) {
+      const int c = ntl * 16 + (lane >> 3) + 8 * (lane & 1);
+#pragma unroll
+      for (int m = 0; m < M; ++m) yb[half][m][c] = acc[m];
+    }
   }
   __syncthreads();
 
