@@ -169,23 +169,27 @@ __global__ __launch_bounds__(512, 1) void mx_linear_kernel(
 }
 
 // ------------------------------------------------ direct-to-LDS variant --
-// Same tile (256 x 256, 8 waves of 64 x 128, K step 64) and result as
-// mx_linear_kernel, with every operand moved HBM -> LDS by
-// buffer_load ... lds through a ring of three stages issued two steps ahead,
-// continuing across tile boundaries: the kernel is persistent (one workgroup
-// per CU, tiles t = worker, worker + G, ... in groups of LIN_GROUP_M row
-// tiles with N fastest inside a group, workers of one XCD numbered
-// consecutively so the 32 tiles they run together share 4 A row tiles and
-// 8 weight column tiles in its L2).
-//  * two wave groups in ping-pong: waves 0-3 and 4-7 put one wave on each
-//    SIMD, and group 1 runs half a step behind group 0.  A step of a group is
-//    a memory phase (every LDS read of the step into registers) and a compute
-//    phase (expansion and the 32 MFMAs, registers only), separated by
-//    workgroup barriers, so on every SIMD one wave streams MFMAs while the
-//    other reads LDS.  Group 0 also issues all of a stage's direct loads
-//    (13 E4M3 / 11 E2M1 per wave, one fewer with unit scales) and waits for
-//    them; group 1 starts with one extra
-//    barrier and group 0 ends with one, so both cross the same number.
+// Same tile (256 x 256, K step 64) and result as mx_linear_kernel, with every
+// operand moved HBM -> LDS by buffer_load ... lds through a ring of three
+// stages, continuing across tile boundaries: the kernel is persistent (one
+// workgroup per CU, tiles t = worker, worker + G, ... in groups of
+// LIN_GROUP_M row tiles with N fastest inside a group, workers of one XCD
+// numbered consecutively so the 32 tiles they run together share 4 A row
+// tiles and 8 weight column tiles in its L2).
+//  * four waves of 128 x 128, one per SIMD: each keeps 16 32x32 accumulators
+//    (256 registers, AGPRs) and runs 64 MFMAs per step, so every fragment
+//    read from LDS feeds four MFMAs.  One wave per SIMD issues in order, so
+//    every other instruction of a step has a fixed place between two MFMAs
+//    (sched_barrier pins the order, empty asm keeps the expansions where they
+//    are placed): nothing else runs while the matrix core waits.
+//  * a step: k16 block 0 of the step's MFMAs (the rest of the stage in flight
+//    is issued between them), the one barrier of the step (stage s + 1 has
+//    landed and every wave holds all of slot s in registers, so slot s is
+//    free), then blocks 1-3, between whose 48 MFMAs go the LDS reads of step
+//    s + 1 (at most one per MFMA, so they do not crowd the LDS), the first
+//    direct loads of stage s + 3 (into slot s) and the expansions.  A stage's
+//    13 direct loads per wave (E4M3; 11 E2M1; one fewer with unit scales)
+//    thus spread over two steps and are waited for one step after the last.
 //  * k order: in a 64-k step, lane half f of MFMA q (0..3) takes
 //    k = 32 f + 8 q + [0, 8) on both operands, so a lane's weights for the
 //    step are one 16-byte chunk (E2M1) or two (E4M3) of its row, read with
@@ -223,13 +227,13 @@ __device__ __forceinline__ void tile_mn(int tl, int mtiles, int ntiles, int& mt,
 __shared__ __attribute__((aligned(16))) unsigned char lin3_lds[lin3::NSTAGE * lin3::stage<0>()];
 
 template <int FMT, int OUT, bool UNIT = false>
-__global__ __launch_bounds__(512, 1) void mx_linear_dma_kernel(
+__global__ __launch_bounds__(256, 1) void mx_linear_dma_kernel(
     const uint16_t* __restrict__ a, int64_t lda, uint32_t a_bytes, const uint8_t* __restrict__ wq,
     const uint8_t* __restrict__ ws, uint32_t w_bytes, uint32_t s_bytes, void* __restrict__ c,
     int64_t ldc, int M, int N, int K, int KB, int slices, int64_t plane) {
   using namespace lin3;
   using dma::i32x4_t;
-  constexpr int WQ = FMT == 0 ? 4 : 2;  // weight loads per loading wave per stage
+  constexpr int WQ = FMT == 0 ? 4 : 2;  // weight loads per wave per stage
   constexpr int H = FMT == 0 ? 2 : 1;   // 16-byte weight chunks per row and step
   constexpr int WROW = w_row<FMT>(), STAGE = stage<FMT>(), LOADS = 8 + WQ + (UNIT ? 0 : 1);
   constexpr int BM = lin::BM, BN = lin::BN, BK = lin::BK;
@@ -239,9 +243,7 @@ __global__ __launch_bounds__(512, 1) void mx_linear_dma_kernel(
   const int worker = (int)(blockIdx.x % 8) * (G / 8) + (int)(blockIdx.x / 8);
   if (worker >= total) return;
   const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const bool g0 = wave < 4;  // group 0 (waves 0-3) loads and leads; group 1 trails by half a step
-  const int lw = wave & 3;
+  const int lw = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t kw = FMT == 0 ? KB : KB / 2;
   const int64_t ks = KB / 32;
   const int steps = K / BK;
@@ -251,8 +253,6 @@ __global__ __launch_bounds__(512, 1) void mx_linear_dma_kernel(
   const i32x4_t s_rsrc = dma::make_rsrc(ws, s_bytes);
 
   int lt = worker, ls = 0, ls_end = steps;
-  // loading lane's first A row and weight row of the tile, and how many of
-  // the rows 32 q (A) / 64 q (E4M3) or 128 q (E2M1) past them are in range
   uint32_t a_base = 0, w_base = 0, s_off = 0;
   int a_lim = 0, w_lim = 0;
   const uint32_t a_qstep = (uint32_t)(32 * lda * 2);
@@ -267,13 +267,13 @@ __global__ __launch_bounds__(512, 1) void mx_linear_dma_kernel(
     if (live) tile_mn(tl, mtiles, ntiles, mt, nt);
     const int m0 = mt * BM, n0 = nt * BN;
     {
-      const int row = 8 * lw + (lane >> 3);  // + 32 q; the swizzle does not depend on q
+      const int row = 8 * lw + (lane >> 3);
       const int ch = (lane & 7) ^ ((row >> 1) & 7);
       a_lim = live ? M - m0 - row : 0;
       a_base = a_lim > 0 ? (uint32_t)((int64_t)(m0 + row) * lda * 2 + ch * 16) : 0u;
     }
     {
-      const int row = FMT == 0 ? 16 * lw + (lane >> 2) : 32 * lw + (lane >> 1);  // + WSTEP q
+      const int row = FMT == 0 ? 16 * lw + (lane >> 2) : 32 * lw + (lane >> 1);
       const int ch = FMT == 0 ? (lane & 3) ^ ((row >> 2) & 3) : (lane & 1) ^ ((row >> 3) & 1);
       w_lim = live ? N - n0 - row : 0;
       w_base = w_lim > 0 ? (uint32_t)((int64_t)(n0 + row) * kw + ch * 16) : 0u;
@@ -283,21 +283,26 @@ __global__ __launch_bounds__(512, 1) void mx_linear_dma_kernel(
       s_off = live && n0 + row < N ? (uint32_t)((int64_t)(n0 + row) * ks) : s_bytes;
     }
   };
-  auto issue = [&](int slot) {
+  // load u (0-7 A, then WQ weight loads, then the scale load) of the stage at ls into slot
+  auto issue_one = [&](int slot, int u) {
     const uint32_t base = lds0 + (uint32_t)(slot * STAGE);
     const int k0 = ls * BK, kb0 = k0 % KB;
-#pragma unroll
-    for (int q = 0; q < 8; ++q)
-      dma::load_to_lds16(a_rsrc, 32 * q < a_lim ? a_base + q * a_qstep + 2 * (uint32_t)k0 : a_bytes,
-                         base + (uint32_t)((4 * q + lw) * 1024));
-    const uint32_t wk = FMT == 0 ? (uint32_t)kb0 : (uint32_t)kb0 / 2;
-#pragma unroll
-    for (int q = 0; q < WQ; ++q)
+    if (u < 8) {
+      dma::load_to_lds16(a_rsrc, 32 * u < a_lim ? a_base + u * a_qstep + 2 * (uint32_t)k0 : a_bytes,
+                         base + (uint32_t)((4 * u + lw) * 1024));
+    } else if (u < 8 + WQ) {
+      const int q = u - 8;
+      const uint32_t wk = FMT == 0 ? (uint32_t)kb0 : (uint32_t)kb0 / 2;
       dma::load_to_lds16(w_rsrc, WSTEP * q < w_lim ? w_base + q * w_qstep + wk : w_bytes,
                          base + (uint32_t)(A_BYTES + (4 * q + lw) * 1024));
-    if (!UNIT)
+    } else if (!UNIT) {
       dma::load_to_lds4(s_rsrc, s_off >= s_bytes ? s_bytes : s_off + (uint32_t)((kb0 / 32) & ~3),
                         base + (uint32_t)(A_BYTES + b_bytes<FMT>() + lw * 256));
+    }
+  };
+  auto issue = [&](int slot) {
+#pragma unroll
+    for (int u = 0; u < LOADS; ++u) issue_one(slot, u);
   };
   auto advance = [&]() {
     if (++ls == ls_end) {
@@ -306,11 +311,11 @@ __global__ __launch_bounds__(512, 1) void mx_linear_dma_kernel(
     }
   };
 
-  const int wm = (wave >> 1) * 64, wn = (wave & 1) * 128;
+  const int wm = (lw >> 1) * 128, wn = (lw & 1) * 128;
   const int frow = lane & 31, f = lane >> 5;
-  int arow[2], axor[2], woff[4][H], soff[4];
+  int arow[4], axor[4], woff[4][H], soff[4];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+  for (int i = 0; i < 4; ++i) {
     const int row = wm + i * 32 + frow;
     arow[i] = row * (BK * 2);
     axor[i] = (4 * f) ^ ((row >> 1) & 7);
@@ -324,17 +329,72 @@ __global__ __launch_bounds__(512, 1) void mx_linear_dma_kernel(
     } else {
       woff[j][0] = A_BYTES + row * WROW + 16 * (f ^ ((row >> 3) & 1));
     }
-    soff[j] = A_BYTES + b_bytes<FMT>() + row * 4 + f;
+    soff[j] = A_BYTES + b_bytes<FMT>() + row * 4;  // the row's scale dword
   }
 
-  if (g0) {
-    set_load_tile();
-    issue(0);
+  // one step's fragments: weight chunks, scale dwords (four blocks of the
+  // row; this lane's byte is picked when the step runs) and A fragments
+  constexpr int NR = 4 * H + (UNIT ? 0 : 4) + 16;  // LDS reads per step
+  u32x4_t wv[4][H];
+  uint32_t scw[4];
+  bf16x8_t fa[4][4];
+  // read r of a step from slot st: weight chunks, then scale dwords, then A fragments
+  auto read_one = [&](const unsigned char* st, int r, u32x4_t (&w)[4][H], uint32_t (&sw)[4], bf16x8_t (&a)[4][4]) {
+    if (r < 4 * H) {
+      w[r / H][r % H] = *reinterpret_cast<const u32x4_t*>(st + woff[r / H][r % H]);
+    } else if (!UNIT && r < 4 * H + 4) {
+      sw[r - 4 * H] = *reinterpret_cast<const uint32_t*>(st + soff[r - 4 * H]);
+    } else {
+      const int e = r - (NR - 16), q = e >> 2, i = e & 3;
+      a[q][i] = *reinterpret_cast<const bf16x8_t*>(st + arow[i] + 16 * (q ^ axor[i]));
+    }
+  };
+  auto expand1 = [&](const u32x4_t (&w4)[4][H], int q, int j, const uint32_t (&sc)[4]) -> bf16x8_t {
+    u32x2_t w;
+    if (FMT == 0) w = u32x2_t{w4[j][q >> 1][2 * (q & 1)], w4[j][q >> 1][2 * (q & 1) + 1]};
+    else w = u32x2_t{w4[j][0][q], 0u};
+    return gemm::dequant8<FMT>(w, sc[j]);
+  };
+  auto scale_bytes = [&](const uint32_t (&sw)[4], int kb, uint32_t (&sc)[4]) {
+    const int sh = 8 * ((kb >> 5) & 3) + 8 * f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      sc[j] = UNIT ? 127u : (sw[j] >> sh) & 0xffu;
+      asm volatile("" : "+v"(sc[j]));  // computed here, not sunk to its first use
+    }
+  };
+  // an expansion computed where it is placed, not sunk to its first use
+  auto pinned = [](bf16x8_t v) -> bf16x8_t {
+    asm volatile("" : "+v"(v));
+    return v;
+  };
+  // The loads of a stage are split: LA of them among the MFMAs of k16 block
+  // 3 of one step, the rest among those of block 0 of the next, so the four
+  // waves' direct loads spread over the whole step.
+  constexpr int LA = LOADS > 7 ? 7 : LOADS;
+  int lslot = 0;  // ring slot of the stage at ls
+  auto next_stage = [&]() {
     advance();
-    issue(1);
-    advance();
-  } else {
-    __builtin_amdgcn_s_barrier();  // group 1 starts half a step behind
+    lslot = lslot == 2 ? 0 : lslot + 1;
+  };
+
+  set_load_tile();
+  issue(0);
+  next_stage();
+  issue(1);
+  next_stage();
+  dma::wait_and_barrier<LOADS>();  // stage 0 landed
+#pragma unroll
+  for (int r = 0; r < NR; ++r) read_one(lin3_lds, r, wv, scw, fa);
+#pragma unroll
+  for (int u = 0; u < LA; ++u) issue_one(lslot, u);
+  uint32_t sc[4];
+  bf16x8_t fb0[4];
+  {
+    const int s0 = worker < total ? (int)((int64_t)(worker / tiles) * steps / slices) : 0;
+    scale_bytes(scw, (int)((int64_t)s0 * BK % KB), sc);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) fb0[j] = expand1(wv, 0, j, sc);
   }
   int cslot = 0;
   for (int t = worker; t < total; t += G) {
@@ -344,78 +404,91 @@ __global__ __launch_bounds__(512, 1) void mx_linear_dma_kernel(
     const int s_begin = (int)((int64_t)sl * steps / slices), s_end = (int)((int64_t)(sl + 1) * steps / slices);
     const int m0 = mt * BM, n0 = nt * BN;
     const bool active = m0 + wm < M && n0 + wn < N;
-    float16_t acc[2][4];
+    // k of the first step of the next work item (its scale bytes are picked at this item's last step)
+    const int kb_next_item = t + G < total ? (int)((int64_t)((t + G) / tiles) * steps / slices * BK % KB) : 0;
+    float16_t acc[4][4];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int j = 0; j < 4; ++j)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
+    int kb = (int)((int64_t)s_begin * BK % KB);  // k of the step within its scale row
+    // One wave per SIMD issues in order, so every load, LDS read and expansion
+    // has a fixed place between two MFMAs (sched_barrier pins the order): the
+    // matrix core never waits behind a run of other instructions, and the
+    // LDS reads of the next step (at most one per MFMA) spread over the 48
+    // MFMAs after the barrier instead of crowding the LDS.
     for (int s = s_begin; s < s_end; ++s) {
-      const int kb0 = (s * BK) % KB;
-      if (g0) {
-        dma::wait_and_barrier<LOADS>();  // stage s landed; group 1 is done reading slot s - 1
-        issue(cslot == 0 ? 2 : cslot - 1);
-        advance();
-      } else {
-        asm volatile("" ::: "memory");
-        __builtin_amdgcn_s_barrier();
-        asm volatile("" ::: "memory");
+      kb = kb + BK == KB ? 0 : kb + BK;
+      bf16x8_t fb1[4], fb2[4], fb3[4];
+      // k16 block 0 (expanded at the end of the previous step); the rest of
+      // the stage in flight; expansion of block 1
+#pragma unroll
+      for (int m = 0; m < 16; ++m) {
+        acc[m >> 2][m & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[0][m >> 2], fb0[m & 3], acc[m >> 2][m & 3], 0, 0, 0);
+        if (!(m & 1) && m / 2 < LOADS - LA) issue_one(lslot, LA + m / 2);
+        if ((m & 1) && m / 2 < 4) fb1[m / 2] = pinned(expand1(wv, 1, m / 2, sc));
+        __builtin_amdgcn_sched_barrier(0);
       }
-      // memory phase: this step's weight chunks, scales and activation fragments into registers
-      u32x4_t wv[4][H];
-      uint32_t sc[4];
-      bf16x8_t fa[4][2];
-      if (active) {
-        const unsigned char* st = lin3_lds + cslot * STAGE;
-        const int sbyte = (kb0 / 32) & 3;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-#pragma unroll
-          for (int h = 0; h < H; ++h) wv[j][h] = *reinterpret_cast<const u32x4_t*>(st + woff[j][h]);
-          sc[j] = UNIT ? 127u : st[soff[j] + sbyte];
-        }
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-#pragma unroll
-          for (int i = 0; i < 2; ++i)
-            fa[q][i] = *reinterpret_cast<const bf16x8_t*>(st + arow[i] + 16 * (q ^ axor[i]));
-      }
-      // every LDS read of the slot stays above the barrier and has returned
-      // (the barrier builtin alone does not order memory accesses), and no
-      // MFMA is scheduled into the memory phase
-      asm volatile("" ::: "memory");
+      next_stage();
+      // stage s + 1 landed; every wave has every fragment of slot s in registers
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): no read of slot s is still in flight
+      dma::wait_and_barrier<LOADS>();
       __builtin_amdgcn_sched_barrier(0);
-      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
-      __builtin_amdgcn_s_barrier();
-      asm volatile("" ::: "memory");
-      __builtin_amdgcn_sched_barrier(0);
-      // compute phase
-      if (active) {
+      const int nslot = cslot == 2 ? 0 : cslot + 1;
+      const unsigned char* nst = lin3_lds + nslot * STAGE;
+      const int kb_next = s + 1 < s_end ? kb : kb_next_item;
+      u32x4_t wvn[4][H];
+      uint32_t scwn[4], scn[4];
+      bf16x8_t fan[4][4];
+      // slot m (0-47) of the MFMAs of blocks 1-3: reads of step s + 1 (this
+      // item's or the next one's), expansions of blocks 2 and 3, the first
+      // loads of stage s + 3 (into slot s, free since the barrier), then the
+      // scale bytes and block-0 expansion of step s + 1
+      auto slot_work = [&](int m) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          bf16x8_t fb[4];
+        for (int r = 0; r < NR; ++r)
+          if (m == r * 40 / NR) read_one(nst, r, wvn, scwn, fan);
+        if (m < 8 && (m & 1)) fb2[m / 2] = pinned(expand1(wv, 2, m / 2, sc));
+        if (m >= 16 && m < 24 && (m & 1)) fb3[(m - 16) / 2] = pinned(expand1(wv, 3, (m - 16) / 2, sc));
+        if (m >= 32 && !(m & 1) && (m - 32) / 2 < LA) issue_one(lslot, (m - 32) / 2);
+        if (m == 43) scale_bytes(scwn, kb_next, scn);
+        if (m >= 44) fb0[m - 44] = pinned(expand1(wvn, 0, m - 44, scn));
+      };
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            u32x2_t w;
-            if (FMT == 0) w = u32x2_t{wv[j][q >> 1][2 * (q & 1)], wv[j][q >> 1][2 * (q & 1) + 1]};
-            else w = u32x2_t{wv[j][0][q], 0u};
-            fb[j] = gemm::dequant8<FMT>(w, sc[j]);
-          }
-#pragma unroll
-          for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[q][i], fb[j], acc[i][j], 0, 0, 0);
-        }
+      for (int m = 0; m < 16; ++m) {
+        acc[m >> 2][m & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[1][m >> 2], fb1[m & 3], acc[m >> 2][m & 3], 0, 0, 0);
+        slot_work(m);
+        __builtin_amdgcn_sched_barrier(0);
       }
-      cslot = cslot == 2 ? 0 : cslot + 1;
+#pragma unroll
+      for (int m = 0; m < 16; ++m) {
+        acc[m >> 2][m & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[2][m >> 2], fb2[m & 3], acc[m >> 2][m & 3], 0, 0, 0);
+        slot_work(16 + m);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int m = 0; m < 16; ++m) {
+        acc[m >> 2][m & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[3][m >> 2], fb3[m & 3], acc[m >> 2][m & 3], 0, 0, 0);
+        slot_work(32 + m);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      cslot = nslot;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+#pragma unroll
+        for (int h = 0; h < H; ++h) wv[j][h] = wvn[j][h];
+        sc[j] = scn[j];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) fa[q][j] = fan[q][j];
+      }
     }
 
     if (active) {
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -429,7 +502,6 @@ __global__ __launch_bounds__(512, 1) void mx_linear_dma_kernel(
           }
     }
   }
-  if (g0) __builtin_amdgcn_s_barrier();  // matches group 1's first barrier
   __builtin_amdgcn_s_waitcnt(dma::waitcnt_vm(0));  // no load may land after the workgroup ends
 }
 
@@ -751,7 +823,7 @@ static hipError_t launch_linear_dma(const uint16_t* a, int64_t lda, const uint8_
       if (grid > (tiles + 7) / 8 * 8) grid = (tiles + 7) / 8 * 8;
       void* cp = OUT == 2 ? (void*)(static_cast<float*>(c) + m0 * ldc + n0)
                           : (void*)(static_cast<uint16_t*>(c) + m0 * ldc + n0);
-      mx_linear_dma_kernel<FMT, OUT, UNIT><<<grid, lin::THREADS, 0, st>>>(
+      mx_linear_dma_kernel<FMT, OUT, UNIT><<<grid, 256, 0, st>>>(
           a + m0 * lda, lda, (uint32_t)(mc * lda * 2), wq + n0 * kw, ws + n0 * ks,
           (uint32_t)(nc * kw), (uint32_t)(nc * ks), cp, ldc, mc, nc, K, KB, slices, plane);
       if ((e = hipGetLastError()) != hipSuccess) return e;
