@@ -1145,7 +1145,7 @@ __device__ __forceinline__ void grouped_tile(int t, int col_tiles, int nblk, con
 // The bf16-activation grouped GEMM (W4A16), organised around direct HBM ->
 // LDS loads:
 //  * tiles of 128 gathered token rows x 512 weight rows (gate/up: 256 gate
-//    and the matching 256 up channels), 8 waves of 64 x 128 (2 x 4).  The
+//    and the matching 256 up channels), 4 waves of 128 x 128 (1 x 4).  The
 //    bf16 activations are four fifths of a 256 x 256 tile's operand bytes;
 //    this shape moves 33 KiB per 64-k step instead of 41 for the same MFMA
 //    work, and four stages fit in LDS, so three steps are in flight.
@@ -1166,7 +1166,16 @@ __device__ __forceinline__ void grouped_tile(int t, int col_tiles, int nblk, con
 //    step are the one 16-byte tile unit (row, block f) -- one 128-bit LDS
 //    read, the 16 lanes of a row group reading 256 contiguous bytes -- under
 //    the one scale byte of block f.
-//  * waves whose 64 rows are all past the expert's count skip their MFMAs.
+//  * one wave per SIMD (16 32x32 accumulators in AGPRs, 64 MFMAs per step),
+//    issuing in order, so every other instruction of a step has a fixed
+//    place between two MFMAs: k16 block 0 (the rest of the stage in flight
+//    issued between its MFMAs), the step's one barrier (stage s + 1 landed,
+//    slot s in registers everywhere, hence free), then blocks 1-3 with the
+//    LDS reads of step s + 1 (at most one per MFMA), the first direct loads
+//    of stage s + 4 (into slot s) and the expansions.  Each wave loads 4
+//    activation blocks, 4 weight row-group pairs and (16 lanes) one scale
+//    block per stage; stages are waited for three steps after their first
+//    loads.
 namespace dma_gemm {
 constexpr int NSTAGE = 4;
 constexpr int DA_BYTES = DMA_BM * BK * 2;    // 16 KiB, unpadded 128-byte rows
@@ -1179,7 +1188,7 @@ constexpr int LOADS_PER_STAGE = 5;           // per wave: 2 activation, 2 weight
 __shared__ __attribute__((aligned(16))) unsigned char moe_dma_lds[dma_gemm::NSTAGE * dma_gemm::DSTAGE];
 
 template <bool GATEUP>
-__global__ __launch_bounds__(512, 1) void moe_large_dma_kernel(
+__global__ __launch_bounds__(256, 1) void moe_large_dma_kernel(
     const uint16_t* __restrict__ a, int64_t lda, uint32_t a_bytes, int topk,
     const int* __restrict__ offsets, const int* __restrict__ sorted, const int* __restrict__ tiles,
     const int* __restrict__ meta, const uint8_t* __restrict__ wt, const uint8_t* __restrict__ wst,
@@ -1188,6 +1197,7 @@ __global__ __launch_bounds__(512, 1) void moe_large_dma_kernel(
     float* __restrict__ y_out, int64_t hidden) {
   using namespace dma_gemm;
   using dma::i32x4_t;
+  constexpr int LOADS = 9, LA = 5;  // direct loads per wave per stage; of them issued in the step after the barrier
   const int G = gridDim.x;
   const int worker = (int)(blockIdx.x % 8) * (G / 8) + (int)(blockIdx.x / 8);
   const int total = meta[1] * col_tiles;
@@ -1203,7 +1213,6 @@ __global__ __launch_bounds__(512, 1) void moe_large_dma_kernel(
   while (col_tiles % nblk != 0) --nblk;
   const i32x4_t a_rsrc = dma::make_rsrc(a, a_bytes);
 
-  // global row group of local group lrg (32 per tile) for column tile c0
   auto grow_group = [&](int64_t c0, int lrg) -> int64_t {
     if (GATEUP) return lrg < 16 ? c0 / 16 + lrg : inter / 16 + c0 / 16 + (lrg - 16);
     return c0 / 16 + lrg;
@@ -1211,12 +1220,15 @@ __global__ __launch_bounds__(512, 1) void moe_large_dma_kernel(
 
   // ---- load side: tile lt, step ls; per-lane byte offsets (invalid -> past the range)
   int lt = worker, ls = 0;
-  uint32_t a_off[2], b_off[2], s_off = 0;
+  uint32_t a_off[4], b_off[4], s_off = 0;
   i32x4_t b_rsrc = dma::make_rsrc(wt, 0), s_rsrc = dma::make_rsrc(wst, 0);
   auto set_load_tile = [&]() {
     if (lt >= total) {
-      a_off[0] = a_off[1] = a_bytes;
-      b_off[0] = b_off[1] = b_bytes;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        a_off[q] = a_bytes;
+        b_off[q] = b_bytes;
+      }
       s_off = s_bytes;
       return;
     }
@@ -1225,16 +1237,15 @@ __global__ __launch_bounds__(512, 1) void moe_large_dma_kernel(
     const int e = tiles[2 * mt], m0 = tiles[2 * mt + 1];
     const int beg = offsets[e], n = offsets[e + 1] - beg;
     const int64_t c0 = (int64_t)nt * (GATEUP ? DMA_BN / 2 : DMA_BN);
-    // both row lookups are issued before the first is used (one wait)
-    int src[2];
+    int src[4];
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const int slot = m0 + 8 * (8 * q + wave) + (lane >> 3);
+    for (int q = 0; q < 4; ++q) {
+      const int slot = m0 + 8 * (4 * q + wave) + (lane >> 3);
       src[q] = GATEUP ? sorted[beg + (slot < n ? slot : n - 1)] : beg + slot;
     }
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const int row = 8 * (8 * q + wave) + (lane >> 3);
+    for (int q = 0; q < 4; ++q) {
+      const int row = 8 * (4 * q + wave) + (lane >> 3);
       const int c = (lane & 7) ^ ((row >> 1) & 7);
       const int64_t r = GATEUP ? src[q] / topk : src[q];
       a_off[q] = m0 + row < n ? (uint32_t)(r * lda * 2 + c * 16) : a_bytes;
@@ -1242,47 +1253,50 @@ __global__ __launch_bounds__(512, 1) void moe_large_dma_kernel(
     b_rsrc = dma::make_rsrc(wt + (int64_t)e * rgs * nchunk * 1024, b_bytes);
     s_rsrc = dma::make_rsrc(wst + (int64_t)(sslot ? sslot[e] : e) * rgs * nchunk * 64, s_bytes);
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const int64_t rg = grow_group(c0, 4 * wave + 2 * q + (lane >> 5));
+    for (int q = 0; q < 4; ++q) {
+      const int64_t rg = grow_group(c0, 2 * (4 * wave + q) + (lane >> 5));
       b_off[q] = 16 * rg < nrows ? (uint32_t)(rg * nchunk * 1024 + (lane & 31) * 16) : b_bytes;
     }
     {
-      const int64_t rg = grow_group(c0, 4 * wave + ((lane >> 1) & 3));
+      const int64_t rg = grow_group(c0, 8 * wave + ((lane >> 1) & 7));
       s_off = 16 * rg < nrows ? (uint32_t)(rg * nchunk * 64 + (lane & 1) * 16) : s_bytes;
     }
   };
-  auto issue = [&](int slot) {
+  // load u of the stage at ls into ring slot `slot`: 0-3 activation blocks,
+  // 4-7 weight row-group pairs, 8 the scale block (lanes 0-15)
+  auto issue_one = [&](int slot, int u) {
     const uint32_t base = lds0 + (uint32_t)(slot * DSTAGE);
     const uint32_t k0 = (uint32_t)(ls * BK);
     const uint32_t chunk = k0 / 128, h = (k0 / 64) & 1;
-#pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const uint32_t off = a_off[q] >= a_bytes ? a_bytes : a_off[q] + 2 * k0;
-      dma::load_to_lds16(a_rsrc, off, base + (uint32_t)((8 * q + wave) * 1024));
-    }
-#pragma unroll
-    for (int q = 0; q < 2; ++q)
+    if (u < 4) {
+      const uint32_t off = a_off[u] >= a_bytes ? a_bytes : a_off[u] + 2 * k0;
+      dma::load_to_lds16(a_rsrc, off, base + (uint32_t)((4 * u + wave) * 1024));
+    } else if (u < 8) {
+      const int q = u - 4;
       dma::load_to_lds16(b_rsrc, b_off[q] >= b_bytes ? b_bytes : b_off[q] + chunk * 1024 + h * 512,
-                         base + (uint32_t)(DA_BYTES + (2 * wave + q) * 1024));
-    if (lane < 8)
+                         base + (uint32_t)(DA_BYTES + (4 * wave + q) * 1024));
+    } else if (lane < 16) {
       dma::load_to_lds16(s_rsrc, s_off >= s_bytes ? s_bytes : s_off + chunk * 64 + h * 32,
-                         base + (uint32_t)(DA_BYTES + DB_BYTES + wave * 128));
+                         base + (uint32_t)(DA_BYTES + DB_BYTES + wave * 256));
+    }
   };
-  auto advance = [&]() {
+  int lslot = 0;  // ring slot of the stage at ls
+  auto next_stage = [&]() {
     if (++ls == steps) {
       ls = 0;
       lt += G;
       set_load_tile();
     }
+    lslot = lslot == NSTAGE - 1 ? 0 : lslot + 1;
   };
 
   // ---- compute side: per-lane LDS read offsets (fixed for the whole kernel)
-  const int wm = (wave >> 2) * 64, wn = (wave & 3) * 64;
+  const int wn = wave * 64;
   const int frow = lane & 31, fk = lane >> 5;
-  int arow[2], axor[2], boff[4], soff[4];
+  int arow[4], axor[4], boff[4], soff[4];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int row = wm + i * 32 + frow;
+  for (int i = 0; i < 4; ++i) {
+    const int row = i * 32 + frow;
     arow[i] = row * (BK * 2);
     axor[i] = (4 * fk) ^ ((row >> 1) & 7);
   }
@@ -1292,13 +1306,43 @@ __global__ __launch_bounds__(512, 1) void moe_large_dma_kernel(
     boff[j] = DA_BYTES + (r >> 4) * 512 + (fk * 16 + (r & 15)) * 16;
     soff[j] = DA_BYTES + DB_BYTES + (r >> 4) * 32 + fk * 16 + (r & 15);
   }
+  // read r of a step: 0-3 weight chunks, 4-7 scale bytes, 8-23 A fragments
+  constexpr int NR = 24;
+  auto read_one = [&](const unsigned char* st, int r, u32x4_t (&w)[4], uint32_t (&sc)[4], bf16x8_t (&fa)[4][4]) {
+    if (r < 4) {
+      w[r] = *reinterpret_cast<const u32x4_t*>(st + boff[r]);
+    } else if (r < 8) {
+      sc[r - 4] = st[soff[r - 4]];
+    } else {
+      const int e = r - 8, q = e >> 2, i = e & 3;
+      fa[q][i] = *reinterpret_cast<const bf16x8_t*>(st + arow[i] + 16 * (q ^ axor[i]));
+    }
+  };
+  auto pinned = [](bf16x8_t v) -> bf16x8_t {
+    asm volatile("" : "+v"(v));  // computed where it is placed, not sunk to its first use
+    return v;
+  };
+  auto expand1 = [&](const u32x4_t (&w)[4], int q, int j, const uint32_t (&sc)[4]) -> bf16x8_t {
+    return gemm::dequant8<1>(u32x2_t{w[j][q], 0u}, sc[j]);
+  };
 
+  u32x4_t wv[4];
+  uint32_t sc[4];
+  bf16x8_t fa[4][4], fb0[4];
   set_load_tile();
 #pragma unroll
   for (int p = 0; p < NSTAGE - 1; ++p) {
-    issue(p);
-    advance();
+#pragma unroll
+    for (int u = 0; u < LOADS; ++u) issue_one(lslot, u);
+    next_stage();
   }
+  dma::wait_and_barrier<(NSTAGE - 2) * LOADS>();  // stage 0 landed
+#pragma unroll
+  for (int r = 0; r < NR; ++r) read_one(moe_dma_lds, r, wv, sc, fa);
+#pragma unroll
+  for (int u = 0; u < LA; ++u) issue_one(lslot, u);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) fb0[j] = expand1(wv, 0, j, sc);
   int cslot = 0;
   for (int t = worker; t < total; t += G) {
     int mt, nt;
@@ -1306,73 +1350,94 @@ __global__ __launch_bounds__(512, 1) void moe_large_dma_kernel(
     const int e = tiles[2 * mt], m0 = tiles[2 * mt + 1];
     const int beg = offsets[e], n = offsets[e + 1] - beg;
     const int64_t c0 = (int64_t)nt * (GATEUP ? DMA_BN / 2 : DMA_BN);
-    const bool active = m0 + wm < n;
 
-    float16_t acc[2][4];
+    float16_t acc[4][4];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int j = 0; j < 4; ++j)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
     for (int s = 0; s < steps; ++s) {
-      // this step's loads landed (the next steps' may be in flight); every
-      // wave is done with the slot the next issue overwrites
-      dma::wait_and_barrier<(NSTAGE - 2) * LOADS_PER_STAGE>();
-      issue(cslot == 0 ? NSTAGE - 1 : cslot - 1);
-      advance();
-      if (active) {
-        const unsigned char* st = moe_dma_lds + cslot * DSTAGE;
-        u32x4_t raw[4];
-        uint32_t sc[4];
+      bf16x8_t fb1[4], fb2[4], fb3[4];
+      // k16 block 0; the rest of the stage in flight; expansion of block 1
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          raw[j] = *reinterpret_cast<const u32x4_t*>(st + boff[j]);
-          sc[j] = st[soff[j]];
-        }
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          bf16x8_t fa[2], fb[4];
-#pragma unroll
-          for (int i = 0; i < 2; ++i)
-            fa[i] = *reinterpret_cast<const bf16x8_t*>(st + arow[i] + 16 * (q ^ axor[i]));
-#pragma unroll
-          for (int j = 0; j < 4; ++j) fb[j] = gemm::dequant8<1>(u32x2_t{raw[j][q], 0u}, sc[j]);
-#pragma unroll
-          for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
-        }
+      for (int m = 0; m < 16; ++m) {
+        acc[m >> 2][m & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[0][m >> 2], fb0[m & 3], acc[m >> 2][m & 3], 0, 0, 0);
+        if (!(m & 1) && m / 2 < LOADS - LA) issue_one(lslot, LA + m / 2);
+        if ((m & 1) && m / 2 < 4) fb1[m / 2] = pinned(expand1(wv, 1, m / 2, sc));
+        __builtin_amdgcn_sched_barrier(0);
       }
-      cslot = cslot == NSTAGE - 1 ? 0 : cslot + 1;
+      next_stage();
+      // stage s + 1 landed; every wave has every fragment of slot s in registers
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): no read of slot s is still in flight
+      dma::wait_and_barrier<(NSTAGE - 2) * LOADS>();
+      __builtin_amdgcn_sched_barrier(0);
+      const int nslot = cslot == NSTAGE - 1 ? 0 : cslot + 1;
+      const unsigned char* nst = moe_dma_lds + nslot * DSTAGE;
+      u32x4_t wvn[4];
+      uint32_t scn[4];
+      bf16x8_t fan[4][4];
+      auto slot_work = [&](int m) {
+#pragma unroll
+        for (int r = 0; r < NR; ++r)
+          if (m == r * 40 / NR) read_one(nst, r, wvn, scn, fan);
+        if (m < 8 && (m & 1)) fb2[m / 2] = pinned(expand1(wv, 2, m / 2, sc));
+        if (m >= 16 && m < 24 && (m & 1)) fb3[(m - 16) / 2] = pinned(expand1(wv, 3, (m - 16) / 2, sc));
+        if (m >= 32 && !(m & 1) && (m - 32) / 2 < LA) issue_one(lslot, (m - 32) / 2);
+        if (m >= 44) fb0[m - 44] = pinned(expand1(wvn, 0, m - 44, scn));
+      };
+#pragma unroll
+      for (int m = 0; m < 16; ++m) {
+        acc[m >> 2][m & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[1][m >> 2], fb1[m & 3], acc[m >> 2][m & 3], 0, 0, 0);
+        slot_work(m);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int m = 0; m < 16; ++m) {
+        acc[m >> 2][m & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[2][m >> 2], fb2[m & 3], acc[m >> 2][m & 3], 0, 0, 0);
+        slot_work(16 + m);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int m = 0; m < 16; ++m) {
+        acc[m >> 2][m & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[3][m >> 2], fb3[m & 3], acc[m >> 2][m & 3], 0, 0, 0);
+        slot_work(32 + m);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        wv[j] = wvn[j];
+        sc[j] = scn[j];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) fa[q][j] = fan[q][j];
+      }
+      cslot = nslot;
     }
 
-    if (active) {
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int row = wm + i * 32 + 8 * (r >> 2) + 4 * fk + (r & 3);
-          const int slot = m0 + row;
-          if (slot >= n) continue;
-          if (GATEUP) {
+      for (int r = 0; r < 16; ++r) {
+        const int row = i * 32 + 8 * (r >> 2) + 4 * fk + (r & 3);
+        const int slot = m0 + row;
+        if (slot >= n) continue;
+        if (GATEUP) {
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-              const float v = activate(act, acc[i][j][r], acc[i][j + 2][r]);
-              const int64_t ch = c0 + wn + j * 32 + frow;
-              reinterpret_cast<__bf16*>(act_out)[(int64_t)(beg + slot) * inter + ch] = (__bf16)v;
-            }
-          } else {
+          for (int j = 0; j < 2; ++j) {
+            const float v = activate(act, acc[i][j][r], acc[i][j + 2][r]);
+            const int64_t ch = c0 + wn + j * 32 + frow;
+            reinterpret_cast<__bf16*>(act_out)[(int64_t)(beg + slot) * inter + ch] = (__bf16)v;
+          }
+        } else {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              const int64_t h = c0 + 2 * wn + j * 32 + frow;
-              y_out[(int64_t)(beg + slot) * hidden + h] = acc[i][j][r];
-            }
+          for (int j = 0; j < 4; ++j) {
+            const int64_t h = c0 + 2 * wn + j * 32 + frow;
+            y_out[(int64_t)(beg + slot) * hidden + h] = acc[i][j][r];
           }
         }
-    }
+      }
   }
   __builtin_amdgcn_s_waitcnt(dma::waitcnt_vm(0));  // no load may land after the workgroup ends
 }
@@ -2736,7 +2801,7 @@ static int moe_forward_impl(const char* fn, int activation, float act_beta, floa
     if (e != hipSuccess) return kq_check_launch(e, "kq_moe_forward/device");
     grid_dma = cus / 8 * 8 > 0 ? cus / 8 * 8 : 8;
     const int col_tiles = (int)(inter / (DMA_BN / 2));
-    moe_large_dma_kernel<true><<<grid_dma, THREADS, 0, st>>>(
+    moe_large_dma_kernel<true><<<grid_dma, 256, 0, st>>>(
         xb, ldx, (uint32_t)x_bytes, topk, offsets, sorted, large_tiles, meta, w13_t, w13_st, sslot,
         2 * inter, hidden, inter, col_tiles, ap, route_weights, act, y, hidden);
     if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_moe_forward/gateup_large");
@@ -2804,7 +2869,7 @@ static int moe_forward_impl(const char* fn, int activation, float act_beta, floa
   }
   if (any_large && dma_path) {
     const int col_tiles = (int)(hidden / DMA_BN);
-    moe_large_dma_kernel<false><<<grid_dma, THREADS, 0, st>>>(
+    moe_large_dma_kernel<false><<<grid_dma, 256, 0, st>>>(
         act, inter, (uint32_t)act_bytes, topk, offsets, sorted, large_tiles, meta, w2_t, w2_st, sslot,
         hidden, inter, inter, col_tiles, ap, route_weights, act, y, hidden);
     if ((e = hipGetLastError()) != hipSuccess) return kq_check_launch(e, "kq_moe_forward/down_large");
