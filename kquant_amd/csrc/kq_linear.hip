@@ -186,8 +186,10 @@ __global__ __launch_bounds__(512, 1) void mx_linear_kernel(
 //    is issued between them), the one barrier of the step (stage s + 1 has
 //    landed and every wave holds all of slot s in registers, so slot s is
 //    free), then blocks 1-3, between whose 48 MFMAs go the LDS reads of step
-//    s + 1 (at most one per MFMA, so they do not crowd the LDS), the first
-//    direct loads of stage s + 3 (into slot s) and the expansions.  A stage's
+//    s + 1 (at most one per MFMA, so they do not crowd the LDS; each writes
+//    its registers in place once their old value is dead, block 3's from
+//    the current slot during the next step's block 0), the first direct
+//    loads of stage s + 3 (into slot s) and the expansions.  A stage's
 //    13 direct loads per wave (E4M3; 11 E2M1; one fewer with unit scales)
 //    thus spread over two steps and are waited for one step after the last.
 //  * k order: in a 64-k step, lane half f of MFMA q (0..3) takes
@@ -422,6 +424,7 @@ __global__ __launch_bounds__(256, 1) void mx_linear_dma_kernel(
     // MFMAs after the barrier instead of crowding the LDS.
     for (int s = s_begin; s < s_end; ++s) {
       kb = kb + BK == KB ? 0 : kb + BK;
+      const unsigned char* cst = lin3_lds + cslot * STAGE;
       bf16x8_t fb1[4], fb2[4], fb3[4];
       // k16 block 0 (expanded at the end of the previous step); the rest of
       // the stage in flight; expansion of block 1
@@ -430,6 +433,7 @@ __global__ __launch_bounds__(256, 1) void mx_linear_dma_kernel(
         acc[m >> 2][m & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[0][m >> 2], fb0[m & 3], acc[m >> 2][m & 3], 0, 0, 0);
         if (!(m & 1) && m / 2 < LOADS - LA) issue_one(lslot, LA + m / 2);
         if ((m & 1) && m / 2 < 4) fb1[m / 2] = pinned(expand1(wv, 1, m / 2, sc));
+        if ((m & 1) && m >= 9) read_one(cst, NR - 16 + 12 + (m - 9) / 2, wv, scw, fa);  // A block 3
         __builtin_amdgcn_sched_barrier(0);
       }
       next_stage();
@@ -440,22 +444,26 @@ __global__ __launch_bounds__(256, 1) void mx_linear_dma_kernel(
       const int nslot = cslot == 2 ? 0 : cslot + 1;
       const unsigned char* nst = lin3_lds + nslot * STAGE;
       const int kb_next = s + 1 < s_end ? kb : kb_next_item;
-      u32x4_t wvn[4][H];
-      uint32_t scwn[4], scn[4];
-      bf16x8_t fan[4][4];
-      // slot m (0-47) of the MFMAs of blocks 1-3: reads of step s + 1 (this
-      // item's or the next one's), expansions of blocks 2 and 3, the first
-      // loads of stage s + 3 (into slot s, free since the barrier), then the
-      // scale bytes and block-0 expansion of step s + 1
+      // slot m (0-47) of the MFMAs of blocks 1-3.  The reads of step s + 1
+      // (this item's or the next one's) write the registers in place, each
+      // once its old value is dead: A block 0 at once, block 1 after its
+      // MFMAs (m >= 16), the weight chunks and scale dwords after the last
+      // expansion (m >= 24), block 2 after its MFMAs (m >= 32); block 3 is
+      // read from this slot during the next step's block 0.  Between them the
+      // expansions of blocks 2 and 3, the first loads of stage s + 3 (into
+      // slot s, free since the barrier), then the scale bytes and block-0
+      // expansion of step s + 1.
       auto slot_work = [&](int m) {
-#pragma unroll
-        for (int r = 0; r < NR; ++r)
-          if (m == r * 40 / NR) read_one(nst, r, wvn, scwn, fan);
+        if (m < 8 && !(m & 1)) read_one(nst, NR - 16 + m / 2, wv, scw, fa);
+        if (m >= 16 && m < 24 && !(m & 1)) read_one(nst, NR - 16 + 4 + (m - 16) / 2, wv, scw, fa);
+        if (m >= 24 && m < 24 + 4 * H) read_one(nst, m - 24, wv, scw, fa);
+        if (!UNIT && m >= 32 && m < 36) read_one(nst, 4 * H + (m - 32), wv, scw, fa);
+        if (m >= 36 && m < 40) read_one(nst, NR - 16 + 8 + (m - 36), wv, scw, fa);
         if (m < 8 && (m & 1)) fb2[m / 2] = pinned(expand1(wv, 2, m / 2, sc));
         if (m >= 16 && m < 24 && (m & 1)) fb3[(m - 16) / 2] = pinned(expand1(wv, 3, (m - 16) / 2, sc));
         if (m >= 32 && !(m & 1) && (m - 32) / 2 < LA) issue_one(lslot, (m - 32) / 2);
-        if (m == 43) scale_bytes(scwn, kb_next, scn);
-        if (m >= 44) fb0[m - 44] = pinned(expand1(wvn, 0, m - 44, scn));
+        if (m == 43) scale_bytes(scw, kb_next, sc);
+        if (m >= 44) fb0[m - 44] = pinned(expand1(wv, 0, m - 44, sc));
       };
 #pragma unroll
       for (int m = 0; m < 16; ++m) {
@@ -476,14 +484,6 @@ __global__ __launch_bounds__(256, 1) void mx_linear_dma_kernel(
         __builtin_amdgcn_sched_barrier(0);
       }
       cslot = nslot;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-#pragma unroll
-        for (int h = 0; h < H; ++h) wv[j][h] = wvn[j][h];
-        sc[j] = scn[j];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) fa[q][j] = fan[q][j];
-      }
     }
 
     if (active) {
