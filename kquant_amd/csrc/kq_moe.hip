@@ -1171,8 +1171,10 @@ __device__ __forceinline__ void grouped_tile(int t, int col_tiles, int nblk, con
 //    place between two MFMAs: k16 block 0 (the rest of the stage in flight
 //    issued between its MFMAs), the step's one barrier (stage s + 1 landed,
 //    slot s in registers everywhere, hence free), then blocks 1-3 with the
-//    LDS reads of step s + 1 (at most one per MFMA), the first direct loads
-//    of stage s + 4 (into slot s) and the expansions.  Each wave loads 4
+//    LDS reads of step s + 1 (at most one per MFMA, each into its registers
+//    once their old value is dead; A block 3 from the current slot during
+//    the next step's block 0), the first direct loads of stage s + 4 (into
+//    slot s) and the expansions.  Each wave loads 4
 //    activation blocks, 4 weight row-group pairs and (16 lanes) one scale
 //    block per stage; stages are waited for three steps after their first
 //    loads.
@@ -1360,6 +1362,7 @@ __global__ __launch_bounds__(256, 1) void moe_large_dma_kernel(
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
     for (int s = 0; s < steps; ++s) {
+      const unsigned char* cst = moe_dma_lds + cslot * DSTAGE;
       bf16x8_t fb1[4], fb2[4], fb3[4];
       // k16 block 0; the rest of the stage in flight; expansion of block 1
 #pragma unroll
@@ -1367,6 +1370,7 @@ __global__ __launch_bounds__(256, 1) void moe_large_dma_kernel(
         acc[m >> 2][m & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[0][m >> 2], fb0[m & 3], acc[m >> 2][m & 3], 0, 0, 0);
         if (!(m & 1) && m / 2 < LOADS - LA) issue_one(lslot, LA + m / 2);
         if ((m & 1) && m / 2 < 4) fb1[m / 2] = pinned(expand1(wv, 1, m / 2, sc));
+        if ((m & 1) && m >= 9) read_one(cst, 20 + (m - 9) / 2, wv, sc, fa);  // A block 3
         __builtin_amdgcn_sched_barrier(0);
       }
       next_stage();
@@ -1376,17 +1380,17 @@ __global__ __launch_bounds__(256, 1) void moe_large_dma_kernel(
       __builtin_amdgcn_sched_barrier(0);
       const int nslot = cslot == NSTAGE - 1 ? 0 : cslot + 1;
       const unsigned char* nst = moe_dma_lds + nslot * DSTAGE;
-      u32x4_t wvn[4];
-      uint32_t scn[4];
-      bf16x8_t fan[4][4];
+      // reads of step s + 1 in place, each once its register is dead (A block 3
+      // is read from this slot during the next step's block 0)
       auto slot_work = [&](int m) {
-#pragma unroll
-        for (int r = 0; r < NR; ++r)
-          if (m == r * 40 / NR) read_one(nst, r, wvn, scn, fan);
+        if (m < 8 && !(m & 1)) read_one(nst, 8 + m / 2, wv, sc, fa);
+        if (m >= 16 && m < 24 && !(m & 1)) read_one(nst, 12 + (m - 16) / 2, wv, sc, fa);
+        if (m >= 24 && m < 32) read_one(nst, m - 24, wv, sc, fa);
+        if (m >= 36 && m < 40) read_one(nst, 16 + (m - 36), wv, sc, fa);
         if (m < 8 && (m & 1)) fb2[m / 2] = pinned(expand1(wv, 2, m / 2, sc));
         if (m >= 16 && m < 24 && (m & 1)) fb3[(m - 16) / 2] = pinned(expand1(wv, 3, (m - 16) / 2, sc));
         if (m >= 32 && !(m & 1) && (m - 32) / 2 < LA) issue_one(lslot, (m - 32) / 2);
-        if (m >= 44) fb0[m - 44] = pinned(expand1(wvn, 0, m - 44, scn));
+        if (m >= 44) fb0[m - 44] = pinned(expand1(wv, 0, m - 44, sc));
       };
 #pragma unroll
       for (int m = 0; m < 16; ++m) {
@@ -1405,13 +1409,6 @@ __global__ __launch_bounds__(256, 1) void moe_large_dma_kernel(
         acc[m >> 2][m & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[3][m >> 2], fb3[m & 3], acc[m >> 2][m & 3], 0, 0, 0);
         slot_work(32 + m);
         __builtin_amdgcn_sched_barrier(0);
-      }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        wv[j] = wvn[j];
-        sc[j] = scn[j];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) fa[q][j] = fan[q][j];
       }
       cslot = nslot;
     }
